@@ -1,0 +1,116 @@
+/*
+ * rec_amd — C ABI of the MI355X (gfx950) quantized-KV attention library.
+ *
+ * Every pointer is a caller-owned device buffer unless stated otherwise; the
+ * library allocates nothing.  Calls are asynchronous on `stream` (a
+ * hipStream_t, NULL for the default stream) and return 0 on success or a
+ * negative REC_E* code, with a message for the calling thread available from
+ * rec_last_error().  Nothing throws across this boundary.
+ *
+ * Cache layout per layer (bh = b*Hkv + h, C = capacity, a multiple of 64,
+ * head_dim D = 128, scales and zero-points are IEEE fp16 bit patterns):
+ *   int8 K codes  int8  [B][Hkv][C][128]          row-major
+ *   int8 V codes  int8  [B][Hkv][C/64][128][64]   token-blocked
+ *   int8 scales   fp16  [B][Hkv][C]               one per (token, head)
+ *   int4 K codes  uint8 [B][Hkv][C][64]           low nibble = even dim
+ *   int4 V codes  uint8 [B][Hkv][C/64][128][32]   token-blocked, low nibble = even token
+ *   int4 scale/zp fp16  [B][Hkv][C/64][4][64]     per 32-dim group
+ * Quantizers: int8 symmetric s = fp16(amax/127), q = clamp(rint(x/s), ±127);
+ * uint4 asymmetric over [min(0, x), max(0, x)], s = fp16(range/15),
+ * z = clamp(rint(-min/s), 0, 15), q = clamp(rint(x/s) + z, 0, 15).
+ */
+#ifndef REC_AMD_H
+#define REC_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  REC_OK = 0,
+  REC_EINVAL = -1,       /* bad shape, dtype or argument */
+  REC_EALIGN = -2,       /* a buffer is not 16-byte aligned */
+  REC_ECAPACITY = -3,    /* tokens beyond the cache capacity */
+  REC_EWORKSPACE = -4,   /* workspace missing or too small */
+  REC_ELAUNCH = -5,      /* the HIP runtime rejected a launch */
+  REC_EUNSUPPORTED = -6  /* a valid request this build does not implement */
+};
+
+/* Element types of the float inputs (queries, new keys/values). */
+enum { REC_F16 = 0, REC_BF16 = 1, REC_F32 = 2 };
+
+/* Library version, e.g. "rec_amd 0.1.0 gfx950". */
+const char* rec_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* rec_last_error(void);
+
+/*
+ * Quantize-on-append: quantize rows [0, L) of k_new / v_new (B, Hkv, L, D),
+ * element strides (sb, sh, st) with unit dim stride, and store them at cache
+ * positions [offset, offset + L).  k_bits / v_bits are 8 or 4; zeros are used
+ * (and required) for 4-bit only.
+ * Replaces the quantize-and-write step of MixedQuantizedKVCache.update_and_fetch,
+ * engine/src/rec_mlx/model.py:76-81 (mx.quantize at :77-78, slice writes at :79-81).
+ */
+int rec_kv_append(const void* k_new, const void* v_new, int in_dtype,
+                  int64_t k_sb, int64_t k_sh, int64_t k_st,
+                  int64_t v_sb, int64_t v_sh, int64_t v_st,
+                  int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros,
+                  int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
+                  int B, int Hkv, int L, int D, int64_t offset, int64_t capacity, void* stream);
+
+/* Split count the library would pick for a decode over T tokens. */
+int rec_decode_default_splits(int B, int Hkv, int64_t T);
+
+/* Bytes of workspace a decode with up to `splits` splits needs. */
+size_t rec_decode_workspace_bytes(int B, int Hkv, int splits);
+
+/*
+ * Make a fresh workspace usable (zeroes its counters with a kernel, so it can
+ * be captured in a HIP graph).  Decode calls leave the counters zeroed again.
+ * One workspace serves one stream at a time.
+ */
+int rec_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GQA decode attention over the first T cached tokens for one query token per
+ * sequence: q (B, Hq, D) with element strides (q_sb, q_sh), q-head h reads
+ * kv-head h / (Hq/Hkv), Hq/Hkv <= 8.  scores = scale * q·k̂; `sinks` (Hq fp32
+ * logits, or NULL) join the softmax denominator; out (B, Hq, D) fp32.
+ * splits <= 0 picks rec_decode_default_splits().
+ * Replaces quantized_attention_with_sinks, engine/src/rec_mlx/model.py:108-139
+ * (split-K structure of engine/src/rec_mlx/kernels/megakernel.py:619-693 and
+ * merge :276-318).
+ */
+int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                    int k_bits, const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros,
+                    int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
+                    const float* sinks, float scale,
+                    int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
+                    void* workspace, size_t workspace_bytes, float* out, void* stream);
+
+/*
+ * One decode step in one launch: quantize-append the single new token
+ * k_new / v_new (B, Hkv, 1, D) at cache position T-1, then attend over all T
+ * tokens, the new one included, as Attention.__call__ does
+ * (engine/src/rec_mlx/model.py:177-190: update_and_fetch, then
+ * quantized_attention_with_sinks).
+ */
+int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                           const void* k_new, const void* v_new, int new_dtype,
+                           int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
+                           int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros,
+                           int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
+                           const float* sinks, float scale,
+                           int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
+                           void* workspace, size_t workspace_bytes, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REC_AMD_H */

@@ -1,0 +1,273 @@
+"""CPU restatement of rec's quantized-KV attention path — TEST INFRASTRUCTURE.
+
+This module is the oracle the HIP kernels in ``rec_amd`` are checked against.
+It is not part of the product: ``rec_amd`` never imports it, and only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg use it.  Everything is NumPy on logical layouts ``(B, H, T, D)``.
+
+Reference semantics restated here (paths relative to the rec repository):
+
+* quantize-on-append: ``engine/src/rec_mlx/model.py:45-82``
+  (``MixedQuantizedKVCache.update_and_fetch``: quantize the new rows, write them
+  at ``[prev:offset]``, attend over the cache *including* them).
+* decode attention with sinks: ``engine/src/rec_mlx/model.py:108-139``
+  (``quantized_attention_with_sinks``: scores = (q*scale)·k̂, optional mask,
+  the per-head sink logit joins the softmax and is then dropped, out = P·v̂).
+* masks: ``engine/src/rec_mlx/model.py:122-128`` ("causal" string →
+  ``arange(kL-L, kL)[:, None] >= arange(kL)``; bool → where; float → add).
+* split-K flash decode and merge: ``engine/src/rec_mlx/kernels/megakernel.py``
+  ``:619-693`` (per-part (max, sum, acc) with the sink seeded once) and
+  ``:276-318`` (merge: top = max m_p, z = Σ e^{m_p-top} l_p,
+  out = Σ e^{m_p-top} acc_p / z, or acc when z == 0).
+* chunked prefill over the quantized cache: ``engine/src/rec_mlx/model.py:191-203``.
+
+KV formats.  The reference's own cache uses MLX affine group-64 quantization
+(``model.py:77-78``); MLX is third-party (mlx==0.32.0) and cannot run here, so
+byte parity with that layout is *not* claimed.  The formats below are this
+project's specification, restated exactly so the GPU quantizer can be
+compared bit-for-bit:
+
+int8, symmetric, one fp16 scale per (token, head) row ``x[D]``::
+
+    amax = max|x|                          (float32, exact)
+    s16  = fp16_rn(amax / 127)             (IEEE float32 divide; overflow saturates to 65504)
+    q    = clamp(rint(x / float(s16)), -127, 127)   (float32 divide, round-half-even)
+    q    = 0 where s16 == 0
+    x̂    = q * float(s16)
+
+uint4, asymmetric, fp16 scale and integer-valued fp16 zero-point per group of
+32 along D (two codes per byte, the low nibble holds the even element)::
+
+    mn = min(0, min x), mx = max(0, max x)  (the range always contains 0)
+    s16 = fp16_rn((mx - mn) / 15)          (saturating)
+    z   = clamp(rint(-mn / float(s16)), 0, 15)   (stored as +0.0 when zero)
+    q   = clamp(rint(x / float(s16)) + z, 0, 15)
+    q = z = 0 where s16 == 0
+    x̂   = (q - z) * float(s16)
+
+Pinning (see ``tests/test_oracle.py``): the quantizers are checked against a
+brute-force nearest-code search on small rows, closed forms (all-zero rows,
+constant rows, the max element mapping to ±127) and invariants (symmetry,
+|x̂ - x| ≤ s/2 inside the range); the attention functions against
+``torch.nn.functional.scaled_dot_product_attention`` in float64 (sinks as an
+extra zero key with an additive mask), the T = 1 closed form, identical-key and
+permutation invariants, and split-merge over arbitrary partitions.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "FP16_MAX",
+    "LOG2E",
+    "fp16_rn_saturate",
+    "quantize_int8",
+    "dequantize_int8",
+    "quantize_int4",
+    "dequantize_int4",
+    "pack_int4",
+    "unpack_int4",
+    "attention",
+    "split_k_decode",
+    "split_k_decode_quantized",
+    "causal_mask",
+]
+
+FP16_MAX = np.float32(65504.0)
+LOG2E = 1.4426950408889634
+
+
+def fp16_rn_saturate(x):
+    """Round float32 to fp16 (round-half-even); |overflow| saturates to 65504."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        h = x.astype(np.float16)
+    return np.where(np.isinf(h) & ~np.isinf(x), np.copysign(np.float16(65504), x).astype(np.float16), h)
+
+
+def quantize_int8(x):
+    """Symmetric int8 per row of the last axis.
+
+    Restates the append-time quantization of ``model.py:77`` for this
+    project's int8 format (module docstring).  Returns ``(codes int8 [..., D],
+    scale fp16 [...])``.
+    """
+    xf = np.asarray(x, dtype=np.float32)
+    amax = np.max(np.abs(xf), axis=-1)
+    s16 = fp16_rn_saturate(amax / np.float32(127.0))
+    sf = s16.astype(np.float32)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.rint(xf / sf)
+    q = np.clip(q, -127, 127)
+    q = np.where(sf == 0, 0, q)
+    return q.astype(np.int8), s16
+
+
+def dequantize_int8(codes, scale):
+    """x̂ = q · s in float32 (exact: 8-bit × 11-bit significands)."""
+    return np.asarray(codes, np.float32) * np.asarray(scale, np.float16).astype(np.float32)[..., None]
+
+
+def pack_int4(q):
+    """Pack uint4 codes ``[..., D]`` two per byte; the low nibble is the even index."""
+    q = np.asarray(q, dtype=np.uint8)
+    return (q[..., 0::2] | (q[..., 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_int4(packed):
+    p = np.asarray(packed, dtype=np.uint8)
+    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), dtype=np.uint8)
+    out[..., 0::2] = p & 0xF
+    out[..., 1::2] = p >> 4
+    return out
+
+
+def quantize_int4(x, group=32):
+    """Asymmetric uint4 with an fp16 scale and zero-point per ``group`` elements.
+
+    Returns ``(codes uint8 [..., D/2], scale fp16 [..., D/group], zero fp16 [..., D/group])``.
+    """
+    xf = np.asarray(x, dtype=np.float32)
+    D = xf.shape[-1]
+    assert D % group == 0
+    g = xf.reshape(xf.shape[:-1] + (D // group, group))
+    mn = np.minimum(g.min(axis=-1), np.float32(0))
+    mx = np.maximum(g.max(axis=-1), np.float32(0))
+    s16 = fp16_rn_saturate((mx - mn) / np.float32(15.0))
+    sf = s16.astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        z = np.clip(np.rint(-mn / sf), 0, 15) + np.float32(0.0)  # +0, never -0
+        q = np.clip(np.rint(g / sf[..., None]) + z[..., None], 0, 15)
+    z = np.where(sf == 0, 0, z)
+    q = np.where(sf[..., None] == 0, 0, q)
+    q = q.reshape(xf.shape).astype(np.uint8)
+    return pack_int4(q), s16, z.astype(np.float16)
+
+
+def dequantize_int4(packed, scale, zero, group=32):
+    q = unpack_int4(packed).astype(np.float32)
+    D = q.shape[-1]
+    g = q.reshape(q.shape[:-1] + (D // group, group))
+    s = np.asarray(scale, np.float16).astype(np.float32)[..., None]
+    z = np.asarray(zero, np.float16).astype(np.float32)[..., None]
+    return ((g - z) * s).reshape(q.shape)
+
+
+def causal_mask(L, T):
+    """The "causal" string mask of ``model.py:124-125``: query i sits at T-L+i."""
+    return np.arange(T - L, T)[:, None] >= np.arange(T)[None, :]
+
+
+def _expand_mask(mask, L, T):
+    if mask is None:
+        return None
+    if isinstance(mask, str):
+        if mask != "causal":
+            raise ValueError(f"unknown mask {mask!r}")
+        return causal_mask(L, T)
+    m = np.asarray(mask)
+    if m.ndim > 3:  # (B, X, L, T) -> (B, X, 1, L, T), model.py:126-127
+        m = np.expand_dims(m, -3)
+    return m
+
+
+def attention(q, k_hat, v_hat, scale, sinks=None, mask=None):
+    """Textbook GQA attention with sinks in float64.
+
+    ``q`` is ``(B, Hq, L, D)``, ``k_hat``/``v_hat`` are dequantized
+    ``(B, Hkv, T, D)``; q-head h reads kv-head ``h // (Hq // Hkv)``
+    (``model.py:111-116``).  Returns ``(B, Hq, L, D)`` float64.  A row whose
+    denominator is zero (every key masked and no sink) returns zeros, like the
+    merge's ``z == 0`` branch (``megakernel.py:302-316``).
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k_hat, np.float64)
+    v = np.asarray(v_hat, np.float64)
+    B, Hq, L, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    qh = (q * scale).reshape(B, Hkv, G, L, D)
+    s = np.einsum("bhgld,bhtd->bhglt", qh, k)
+    m = _expand_mask(mask, L, T)
+    if m is not None:
+        s = np.where(m, s, -np.inf) if m.dtype == np.bool_ else s + m
+    if sinks is None:
+        sink = np.full((1, Hkv, G, 1, 1), -np.inf)
+    else:
+        sink = np.asarray(sinks, np.float64).reshape(1, Hkv, G, 1, 1)
+    top = np.maximum(s.max(axis=-1, keepdims=True, initial=-np.inf), sink)
+    top = np.where(np.isfinite(top), top, 0.0)
+    p = np.exp(s - top)
+    den = p.sum(axis=-1, keepdims=True) + np.exp(sink - top)
+    num = np.einsum("bhglt,bhtd->bhgld", p, v)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        out = np.where(den > 0, num / np.where(den > 0, den, 1.0), 0.0)
+    return out.reshape(B, Hq, L, D)
+
+
+def split_k_decode(q, k_hat_fn, v_hat_fn, T, scale, sinks=None, parts=None, chunk=4096):
+    """Split-K flash decode in float32 with a second merge pass.
+
+    Follows ``megakernel.py:619-693`` (each part keeps a running max, a sum
+    and an fp32 accumulator) and ``megakernel.py:276-318`` (the merge).  The
+    sink enters the merge once, which equals seeding part 0 with
+    ``hi = sink, z = 1`` as the reference kernel does.  ``k_hat_fn(a, b)`` and
+    ``v_hat_fn(a, b)`` dequantize tokens ``[a, b)`` to float32
+    ``(B, Hkv, b-a, D)``, so the whole cache is never materialised.
+    Parts are contiguous token ranges of ``chunk`` tokens (the CPU analogue of
+    the GPU's splits).  Returns ``(B, Hq, D)`` float32.
+    """
+    q = np.asarray(q, np.float32)
+    B, Hq, D = q.shape
+    kb = k_hat_fn(0, min(T, 1))
+    Hkv = kb.shape[1]
+    G = Hq // Hkv
+    qh = (q * np.float32(scale)).reshape(B, Hkv, G, D)
+    bounds = list(range(0, T, chunk)) if parts is None else list(parts)
+    bounds = [b for b in bounds if b < T] + [T]
+    ms, ls, accs = [], [], []
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        k = k_hat_fn(a, b)
+        v = v_hat_fn(a, b)
+        s = np.matmul(qh, k.transpose(0, 1, 3, 2))  # (B, Hkv, G, n)
+        m = s.max(axis=-1, keepdims=True)
+        p = np.exp(s - m)
+        ms.append(m[..., 0])
+        ls.append(p.sum(axis=-1))
+        accs.append(np.matmul(p, v))  # (B, Hkv, G, D)
+    m = np.stack(ms, 0)
+    l = np.stack(ls, 0)
+    acc = np.stack(accs, 0)
+    top = m.max(axis=0)
+    if sinks is not None:
+        sink = np.asarray(sinks, np.float32).reshape(1, Hkv, G)
+        top = np.maximum(top, sink)
+    w = np.exp(m - top[None])
+    z = (w * l).sum(axis=0)
+    if sinks is not None:
+        z = z + np.exp(sink - top)
+    num = (w[..., None] * acc).sum(axis=0)
+    out = np.where(z[..., None] == 0, num, num / np.where(z == 0, 1, z)[..., None])
+    return out.reshape(B, Hq, D).astype(np.float32)
+
+
+def split_k_decode_quantized(q, cache, T, scale, sinks=None, chunk=4096):
+    """``split_k_decode`` over a logical quantized cache dict.
+
+    ``cache`` holds ``k_bits``/``v_bits`` and logical arrays ``kq, ks[, kz]``
+    and ``vq, vs[, vz]`` of shape ``(B, Hkv, T, ...)``; dequantization happens
+    per chunk, as the CPU baseline does.
+    """
+
+    def deq(prefix, bits):
+        def fn(a, b):
+            if bits == 8:
+                return dequantize_int8(cache[prefix + "q"][:, :, a:b], cache[prefix + "s"][:, :, a:b])
+            return dequantize_int4(
+                cache[prefix + "q"][:, :, a:b], cache[prefix + "s"][:, :, a:b], cache[prefix + "z"][:, :, a:b]
+            )
+
+        return fn
+
+    return split_k_decode(q, deq("k", cache["k_bits"]), deq("v", cache["v_bits"]), T, scale, sinks, chunk=chunk)

@@ -1,0 +1,14 @@
+"""rec_amd — MI355X (gfx950) GQA decode attention over a quantized KV cache.
+
+Drop-in for the quantized-KV attention path of rec's engine
+(engine/src/rec_mlx/model.py:40-139,165-203): a quantize-on-append cache with
+the reference's cache surface and ``quantized_attention_with_sinks`` with its
+signature, running hand-written HIP kernels through the C ABI in
+``include/rec_amd.h``.
+"""
+
+from ._lib import RecError, load as library  # noqa: F401
+from .attention import attend, quantized_attention_with_sinks  # noqa: F401
+from .cache import MixedQuantizedKVCache, QuantizedKV, QuantizedKVCache, to_logical  # noqa: F401
+
+__version__ = "0.1.0"

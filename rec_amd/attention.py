@@ -1,0 +1,171 @@
+"""Attention over the quantized cache, with the reference's call surface.
+
+* :func:`quantized_attention_with_sinks` keeps the signature of
+  engine/src/rec_mlx/model.py:108-110 and runs the gfx950 split-K decode kernel
+  (``rec_decode_attn``) for one query token.
+* :func:`attend` mirrors the cache/attention part of ``Attention.__call__``
+  (model.py:177-203): append first, then attend, decode for ``L == 1``.  For a
+  single decode token it issues ONE launch (``rec_decode_append_attn``) that
+  quantizes the new token into the cache and attends over it.
+
+There is no CPU path: without the built HIP library every call raises.
+"""
+
+from __future__ import annotations
+
+import threading
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .cache import _DTYPES, HEAD_DIM, QuantizedKV, QuantizedKVCache
+
+_ws_lock = threading.Lock()
+_workspaces = {}
+
+
+def workspace(device: torch.device, B: int, Hkv: int, splits: int, stream: int) -> torch.Tensor:
+    """A zero-initialised decode workspace for (device, stream), grown on demand.
+
+    Decode launches leave its counters at zero, so it is reused as is.  One
+    workspace per stream: launches on one stream are ordered.
+    """
+    lib = _lib.load()
+    need = lib.rec_decode_workspace_bytes(B, Hkv, splits)
+    key = (device.index, stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.zeros(need, dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+        return ws
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _sinks(sinks, Hq, device):
+    if sinks is None:
+        return None
+    s = torch.as_tensor(sinks, device=device).to(torch.float32).reshape(-1).contiguous()
+    if s.numel() != Hq:
+        raise ValueError(f"sinks has {s.numel()} entries, expected {Hq}")
+    return s
+
+
+def _check_query(queries):
+    if queries.dim() != 4:
+        raise ValueError(f"queries must be (B, n_heads, L, head_dim), got {tuple(queries.shape)}")
+    if queries.dtype not in _DTYPES:
+        raise ValueError(f"queries dtype {queries.dtype} is not float16/bfloat16/float32")
+    if not queries.is_cuda:
+        raise ValueError("queries must be a GPU tensor")
+    if queries.shape[-1] != HEAD_DIM:
+        raise NotImplementedError(f"head_dim {queries.shape[-1]} is not supported (128 only)")
+
+
+def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, splits, out,
+                   k_new=None, v_new=None, T=None, capacity=None):
+    lib = _lib.load()
+    B, Hq, L, D = queries.shape
+    Hkv = keys.n_kv_heads
+    T = keys.length if T is None else T
+    capacity = keys.capacity if capacity is None else capacity
+    q = queries[:, :, 0]
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    dev = queries.device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if splits is None or splits <= 0:
+        splits = lib.rec_decode_default_splits(B, Hkv, T)
+    ws = workspace(dev, B, Hkv, splits, stream)
+    sk = _sinks(sinks, Hq, dev)
+    common_tail = (
+        _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity), int(splits),
+        ws.data_ptr(), ws.numel(), out.data_ptr(), stream,
+    )
+    if k_new is None:
+        rc = lib.rec_decode_attn(
+            q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1),
+            keys.bits, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
+            values.bits, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
+            *common_tail,
+        )
+        _lib.check(rc, "rec_decode_attn")
+    else:
+        rc = lib.rec_decode_append_attn(
+            q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1),
+            k_new.data_ptr(), v_new.data_ptr(), _DTYPES[k_new.dtype],
+            k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
+            keys.bits, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
+            values.bits, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
+            *common_tail,
+        )
+        _lib.check(rc, "rec_decode_append_attn")
+
+
+def quantized_attention_with_sinks(
+    queries, keys, values, scale, mask, sinks, group_size, key_bits, value_bits, *, out_dtype=None, splits=None
+):
+    """GQA attention of ``queries`` ``(B, n_q, L, 128)`` over a quantized cache.
+
+    ``keys``/``values`` are what :meth:`QuantizedKVCache.update_and_fetch`
+    returns; ``sinks`` (``n_q`` logits or None) join the softmax denominator;
+    ``mask`` is None or "causal" (for ``L == 1`` both mean "every cached
+    token").  Returns ``(B, n_q, L, 128)`` in ``out_dtype`` (default: the
+    query dtype, as the reference returns, model.py:132-139).
+    """
+    _check_query(queries)
+    B, Hq, L, D = queries.shape
+    if not isinstance(keys, QuantizedKV) or not isinstance(values, QuantizedKV):
+        raise TypeError("keys/values must come from QuantizedKVCache.update_and_fetch")
+    if (keys.bits, values.bits) != (key_bits, value_bits):
+        raise ValueError(f"cache holds {keys.bits}/{values.bits}-bit K/V, call asked for {key_bits}/{value_bits}")
+    if 4 in (key_bits, value_bits) and group_size != 32:
+        raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
+    if mask is not None and not (isinstance(mask, str) and mask == "causal"):
+        raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
+    if L != 1:
+        raise NotImplementedError("multi-token queries go through the chunked prefill kernel")
+    out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+    _decode_launch(queries, keys, values, scale, sinks, splits, out)
+    out = out.view(B, Hq, 1, D)
+    return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+
+
+def attend(queries, keys, values, cache: QuantizedKVCache, scale, mask=None, sinks=None, *, out_dtype=None,
+           splits=None, fused=True):
+    """The cache + attention part of ``Attention.__call__`` (model.py:177-203).
+
+    New ``keys``/``values`` ``(B, Hkv, L, 128)`` are quantized into ``cache``
+    first, then ``queries`` attend over the whole cache, the new tokens
+    included.  A single decode token takes one fused launch.
+    """
+    _check_query(queries)
+    B, Hq, L, D = queries.shape
+    if fused and L == 1:
+        cache._check_usable()
+        if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
+            raise ValueError("a fused decode step takes one new K/V token of a float dtype")
+        if mask is not None and not (isinstance(mask, str) and mask == "causal"):
+            raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
+        Bk, H = keys.shape[:2]
+        cache._reserve(Bk, H, cache.offset + 1, keys.device)
+        k_kv, v_kv = cache._view()
+        kn = keys if keys.stride(-1) == 1 else keys.contiguous()
+        vn = values if values.stride(-1) == 1 else values.contiguous()
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+        try:
+            _decode_launch(queries, k_kv, v_kv, scale, sinks, splits, out, kn, vn, T=cache.offset + 1,
+                           capacity=cache.capacity)
+        except _lib.RecError:
+            cache._usable = False
+            raise
+        cache.offset += 1
+        out = out.view(B, Hq, 1, D)
+        return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+    k, v = cache.update_and_fetch(keys, values)
+    return quantized_attention_with_sinks(queries, k, v, scale, mask, sinks, cache.group_size, cache.key_bits,
+                                          cache.value_bits, out_dtype=out_dtype, splits=splits)

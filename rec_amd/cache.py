@@ -1,0 +1,265 @@
+"""Quantized KV cache with the reference's cache call surface.
+
+Mirrors ``MixedQuantizedKVCache`` (engine/src/rec_mlx/model.py:40-105) and the
+mlx-lm ``QuantizedKVCache`` methods it inherits (mlx-lm 0.31.3, third-party:
+``step``, ``offset``, ``keys_and_values``, ``make_mask``, ``size``,
+``empty``, ``is_trimmable``, ``trim``, ``meta_state``, ``nbytes``), with
+torch tensors in HBM instead of MLX arrays and the quantize-on-append done by
+the gfx950 kernel behind ``rec_kv_append``.
+
+Formats (bits per K and V independently):
+
+* 8-bit: symmetric int8, one fp16 scale per (token, head).
+* 4-bit: asymmetric uint4, fp16 scale and zero-point per 32 dims.
+
+V codes (and 4-bit scales) are stored token-blocked in 64-token blocks, so
+the capacity is always a multiple of 64; :func:`to_logical` turns any cache
+tensor back into the plain ``(B, Hkv, T, ...)`` layout.
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple, Optional
+
+import torch
+
+from . import _lib
+
+BLOCK = 64
+HEAD_DIM = 128
+GROUP4 = 32
+
+_DTYPES = {torch.float16: _lib.REC_F16, torch.bfloat16: _lib.REC_BF16, torch.float32: _lib.REC_F32}
+
+
+class QuantizedKV(NamedTuple):
+    """Quantized K or V of one layer: what ``update_and_fetch`` returns.
+
+    ``codes``/``scales``/``zeros`` span the full capacity; ``length`` tokens
+    are valid.  ``zeros`` is None for 8-bit.  ``blocked`` marks the
+    token-blocked layout used for V.
+    """
+
+    codes: torch.Tensor
+    scales: torch.Tensor
+    zeros: Optional[torch.Tensor]
+    bits: int
+    length: int
+    blocked: bool
+
+    @property
+    def n_kv_heads(self) -> int:
+        return self.codes.shape[1]
+
+    @property
+    def capacity(self) -> int:
+        return self.scales.shape[2] if self.bits == 8 else self.scales.shape[2] * BLOCK
+
+
+def _alloc(B, H, cap, bits, blocked, device):
+    nb = cap // BLOCK
+    if bits == 8:
+        codes = torch.zeros((B, H, nb, HEAD_DIM * BLOCK) if blocked else (B, H, cap, HEAD_DIM), dtype=torch.int8, device=device)
+        scales = torch.zeros((B, H, cap), dtype=torch.float16, device=device)
+        zeros = None
+    else:
+        codes = torch.zeros(
+            (B, H, nb, HEAD_DIM * BLOCK // 2) if blocked else (B, H, cap, HEAD_DIM // 2), dtype=torch.uint8, device=device
+        )
+        scales = torch.zeros((B, H, nb, HEAD_DIM // GROUP4, BLOCK), dtype=torch.float16, device=device)
+        zeros = torch.zeros_like(scales)
+    return codes, scales, zeros
+
+
+def _grow_tensor(old, new):
+    if old is None:
+        return new
+    idx = tuple(slice(0, s) for s in old.shape)
+    new[idx] = old
+    return new
+
+
+def to_logical(kv: QuantizedKV, length: Optional[int] = None):
+    """Return ``(codes, scales, zeros)`` in the plain layout, first ``length`` tokens.
+
+    8-bit: codes int8 ``(B, H, T, 128)``, scales fp16 ``(B, H, T)``.
+    4-bit: codes uint8 ``(B, H, T, 64)`` (low nibble = even dim), scales and
+    zeros fp16 ``(B, H, T, 4)``.
+    """
+    T = kv.length if length is None else length
+    B, H = kv.codes.shape[:2]
+    if kv.bits == 8:
+        codes = kv.codes
+        if kv.blocked:
+            codes = codes.view(B, H, -1, HEAD_DIM, BLOCK).permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
+        return codes[:, :, :T].contiguous(), kv.scales[:, :, :T].contiguous(), None
+    if kv.blocked:
+        packed = kv.codes.view(B, H, -1, HEAD_DIM, BLOCK // 2)
+        lo, hi = packed & 0xF, packed >> 4
+        tok = torch.stack([lo, hi], -1).reshape(B, H, -1, HEAD_DIM, BLOCK)  # token-major within block
+        q = tok.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
+        codes = (q[..., 0::2] | (q[..., 1::2] << 4)).to(torch.uint8)
+    else:
+        codes = kv.codes
+    sc = kv.scales.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
+    zp = kv.zeros.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
+    return codes[:, :, :T].contiguous(), sc[:, :, :T].contiguous(), zp[:, :, :T].contiguous()
+
+
+def _stride3(x):
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x, x.stride(0), x.stride(1), x.stride(2)
+
+
+class QuantizedKVCache:
+    """Quantize-on-append KV cache of one attention layer (GPU resident).
+
+    ``group_size`` is the 4-bit group (32); 8-bit uses one scale per row.
+    ``max_tokens`` preallocates the whole context once (no growth copies);
+    appending beyond it raises ``ValueError("Decode context limit
+    exhausted")`` like the reference (engine/src/rec_mlx/kernels/megakernel.py:1330-1331).
+    Without it the capacity grows in multiples of ``step``, preserving the
+    contents, as ``update_and_fetch`` does in the reference (model.py:49-75).
+    """
+
+    step = 256
+
+    def __init__(self, group_size: int = GROUP4, key_bits: int = 8, value_bits: int = 8, *, max_tokens=None):
+        for name, bits in (("key_bits", key_bits), ("value_bits", value_bits)):
+            if bits not in (4, 8):
+                raise ValueError(f"{name} must be 4 or 8, got {bits}")
+        if 4 in (key_bits, value_bits) and group_size != GROUP4:
+            raise ValueError(f"4-bit caches use groups of {GROUP4}, got group_size={group_size}")
+        self.group_size = group_size
+        self.key_bits, self.value_bits = key_bits, value_bits
+        self.bits = key_bits
+        self.max_tokens = max_tokens
+        self.keys = None  # (codes, scales, zeros)
+        self.values = None
+        self.offset = 0
+        self.capacity = 0
+        self._usable = True
+
+    # ------------------------------------------------------------ helpers --
+    def _check_usable(self):
+        if not self._usable:
+            raise RuntimeError("Quantized KV cache was invalidated by a failed GPU call")
+
+    def _reserve(self, B, H, needed, device):
+        if self.max_tokens is not None and needed > self.max_tokens:
+            raise ValueError("Decode context limit exhausted")
+        if self.keys is not None and needed <= self.capacity:
+            return
+        if self.max_tokens is not None:
+            cap = -(-self.max_tokens // BLOCK) * BLOCK
+        else:
+            cap = -(-needed // self.step) * self.step
+        k = _alloc(B, H, cap, self.key_bits, False, device)
+        v = _alloc(B, H, cap, self.value_bits, True, device)
+        if self.keys is not None:
+            k = tuple(_grow_tensor(o, n) if n is not None else None for o, n in zip(self.keys, k))
+            v = tuple(_grow_tensor(o, n) if n is not None else None for o, n in zip(self.values, v))
+        self.keys, self.values, self.capacity = k, v, cap
+
+    def _view(self):
+        k = QuantizedKV(*self.keys, self.key_bits, self.offset, False)
+        v = QuantizedKV(*self.values, self.value_bits, self.offset, True)
+        return k, v
+
+    # ------------------------------------------------------ reference API --
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        """Quantize ``keys``/``values`` ``(B, Hkv, L, 128)`` into positions
+        ``[offset, offset+L)`` and return the quantized K and V covering
+        ``[0, offset+L)`` (model.py:45-82)."""
+        self._check_usable()
+        B, H, L, D = keys.shape
+        if values.shape != keys.shape:
+            raise ValueError(f"keys {tuple(keys.shape)} and values {tuple(values.shape)} differ in shape")
+        if D != HEAD_DIM:
+            raise NotImplementedError(f"head_dim {D} is not supported (128 only)")
+        if keys.dtype not in _DTYPES or values.dtype != keys.dtype:
+            raise ValueError(f"keys/values must share a float16/bfloat16/float32 dtype, got {keys.dtype}/{values.dtype}")
+        if not keys.is_cuda:
+            raise ValueError("keys/values must be GPU tensors")
+        if self.keys is not None and (self.keys[0].shape[0], self.keys[0].shape[1]) != (B, H):
+            raise ValueError("batch/head shape differs from the cached one")
+        prev = self.offset
+        self._reserve(B, H, prev + L, keys.device)
+        k, ksb, ksh, kst = _stride3(keys)
+        v, vsb, vsh, vst = _stride3(values)
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(keys.device).cuda_stream
+        kc, ks, kz = self.keys
+        vc, vs, vz = self.values
+        rc = lib.rec_kv_append(
+            k.data_ptr(), v.data_ptr(), _DTYPES[keys.dtype], ksb, ksh, kst, vsb, vsh, vst,
+            self.key_bits, kc.data_ptr(), ks.data_ptr(), kz.data_ptr() if kz is not None else None,
+            self.value_bits, vc.data_ptr(), vs.data_ptr(), vz.data_ptr() if vz is not None else None,
+            B, H, L, D, prev, self.capacity, stream,
+        )
+        if rc == _lib.REC_ELAUNCH:
+            self._usable = False
+        _lib.check(rc, "rec_kv_append")
+        self.offset = prev + L
+        return self.keys_and_values()
+
+    def keys_and_values(self):
+        return self._view()
+
+    @property
+    def state(self):
+        return (self.keys, self.values, self.offset, self.group_size, self.key_bits, self.value_bits)
+
+    @state.setter
+    def state(self, v):
+        (self.keys, self.values, self.offset, self.group_size, self.key_bits, self.value_bits) = v
+        self.bits = self.key_bits
+        self.capacity = 0 if self.keys is None else QuantizedKV(*self.keys, self.key_bits, 0, False).capacity
+        self._usable = True
+
+    @property
+    def meta_state(self):
+        return tuple(map(str, (self.step, self.offset, self.group_size, self.key_bits, self.value_bits)))
+
+    def size(self) -> int:
+        return self.offset
+
+    def empty(self) -> bool:
+        return self.keys is None
+
+    def is_trimmable(self) -> bool:
+        return True
+
+    def trim(self, n: int) -> int:
+        n = min(self.offset, n)
+        self.offset -= n
+        return n
+
+    def make_mask(self, n_tokens: int, window_size=None, return_array: bool = False):
+        """None for a single decode token (engine/src/rec_mlx/cache.py:140-143),
+        else "causal", or the boolean array when asked for one."""
+        if window_size is not None:
+            raise NotImplementedError("sliding-window masks are not supported by this cache")
+        if n_tokens == 1 and not return_array:
+            return None
+        if not return_array:
+            return "causal"
+        T = self.offset + n_tokens
+        q = torch.arange(T - n_tokens, T)
+        return q[:, None] >= torch.arange(T)[None]
+
+    @property
+    def nbytes(self) -> int:
+        if self.keys is None:
+            return 0
+        return sum(t.numel() * t.element_size() for t in (*self.keys, *self.values) if t is not None)
+
+
+class MixedQuantizedKVCache(QuantizedKVCache):
+    """8-bit keys and 4-bit values by default, like the reference's
+    ``MixedQuantizedKVCache(group_size=64, key_bits=8, value_bits=4)``
+    (model.py:40-43); 4-bit groups here are 32 wide."""
+
+    def __init__(self, group_size: int = GROUP4, key_bits: int = 8, value_bits: int = 4, **kw):
+        super().__init__(group_size, key_bits, value_bits, **kw)

@@ -1,0 +1,235 @@
+// C ABI of the library: argument validation, workspace layout and launches.
+// Declarations and the reference interface each entry point replaces are in
+// include/rec_amd.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <cmath>
+
+#include "../../include/rec_amd.h"
+#include "kernels.h"
+
+using namespace rec;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = 0;
+  return REC_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(REC_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct WorkspaceLayout {
+  size_t counters, stat, acc, total;
+};
+
+WorkspaceLayout ws_layout(int B, int Hkv, int splits) {
+  WorkspaceLayout w;
+  const size_t bh = (size_t)B * Hkv;
+  w.counters = 0;
+  w.stat = round256(bh * sizeof(int));
+  w.acc = w.stat + round256(bh * splits * 8 * 2 * sizeof(float));
+  w.total = w.acc + bh * splits * 8 * HEAD_DIM * sizeof(float);
+  return w;
+}
+
+int check_bits(int bits, const char* name) {
+  if (bits != 8 && bits != 4) return fail(REC_EINVAL, "%s must be 8 or 4, got %d", name, bits);
+  return REC_OK;
+}
+
+int check_cache(int bits, const void* codes, const void* scales, const void* zeros, const char* name) {
+  if (!codes || !scales) return fail(REC_EINVAL, "%s codes/scales pointer is null", name);
+  if (bits == 4 && !zeros) return fail(REC_EINVAL, "%s zero-points are required for 4-bit", name);
+  if (!aligned16(codes) || !aligned16(scales) || (bits == 4 && !aligned16(zeros)))
+    return fail(REC_EALIGN, "%s cache buffers must be 16-byte aligned", name);
+  return REC_OK;
+}
+
+int check_dtype(int dt, const char* name) {
+  if (dt != REC_F16 && dt != REC_BF16 && dt != REC_F32) return fail(REC_EINVAL, "%s dtype %d is not f16/bf16/f32", name, dt);
+  return REC_OK;
+}
+
+// Splits actually launched for a request: chunk-aligned spans, no empty split.
+void effective_splits(int64_t T, int req, int* S, int* span) {
+  const int64_t chunks = (T + BLOCK_T - 1) / BLOCK_T;
+  int64_t s = req < 1 ? 1 : req;
+  if (s > chunks) s = chunks;
+  const int64_t span_chunks = (chunks + s - 1) / s;
+  *span = (int)(span_chunks * BLOCK_T);
+  *S = (int)((chunks + span_chunks - 1) / span_chunks);
+}
+
+int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_bits, const void* kq,
+                  const uint16_t* ks, const uint16_t* kz, int v_bits, const void* vq, const uint16_t* vs,
+                  const uint16_t* vz, const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
+                  int64_t cap, int splits, void* ws, size_t ws_bytes, float* out, const RowSrc* knew,
+                  const RowSrc* vnew, void* stream) {
+  int e;
+  if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
+  if ((e = check_dtype(q_dtype, "query"))) return e;
+  if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
+  if (B < 1 || Hkv < 1 || Hq < 1) return fail(REC_EINVAL, "B, Hq and Hkv must be positive");
+  if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
+  if (Hq / Hkv > 8) return fail(REC_EUNSUPPORTED, "GQA ratio %d exceeds 8", Hq / Hkv);
+  if (T < 1) return fail(REC_EINVAL, "decode needs at least one cached token (T=%lld)", (long long)T);
+  if (cap % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 64", (long long)cap);
+  if (T > cap) return fail(REC_ECAPACITY, "T=%lld exceeds the cache capacity %lld", (long long)T, (long long)cap);
+  if (!q || !out) return fail(REC_EINVAL, "query/output pointer is null");
+  if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
+  if ((e = check_cache(k_bits, kq, ks, kz, "key")) || (e = check_cache(v_bits, vq, vs, vz, "value"))) return e;
+  if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
+  if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
+  if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
+  int S, span;
+  effective_splits(T, splits, &S, &span);
+  const WorkspaceLayout w = ws_layout(B, Hkv, S);
+  if (!ws || ws_bytes < w.total)
+    return fail(REC_EWORKSPACE, "workspace of %zu bytes is too small (%zu needed for %d splits)", ws_bytes, w.total, S);
+  if (!aligned16(ws)) return fail(REC_EALIGN, "workspace must be 16-byte aligned");
+  DecodeArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.kq = kq;
+  a.ks = ks;
+  a.kz = kz;
+  a.vq = vq;
+  a.vs = vs;
+  a.vz = vz;
+  a.sinks = sinks;
+  a.out = out;
+  a.counters = (int*)((char*)ws + w.counters);
+  a.ws_stat = (float*)((char*)ws + w.stat);
+  a.ws_acc = (float*)((char*)ws + w.acc);
+  if (knew) {
+    a.knew = *knew;
+    a.vnew = *vnew;
+  }
+  a.q_mul = scale * LOG2E;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.T = T;
+  a.cap = cap;
+  a.S = S;
+  a.span = span;
+  return launched(launch_decode(k_bits, v_bits, a, (hipStream_t)stream), "decode launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rec_version(void) { return "rec_amd 0.1.0 gfx950"; }
+
+const char* rec_last_error(void) { return g_err; }
+
+int rec_kv_append(const void* k_new, const void* v_new, int in_dtype, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                  int64_t v_sb, int64_t v_sh, int64_t v_st, int k_bits, void* k_codes, uint16_t* k_scales,
+                  uint16_t* k_zeros, int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros, int B,
+                  int Hkv, int L, int D, int64_t offset, int64_t capacity, void* stream) {
+  int e;
+  if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
+  if ((e = check_dtype(in_dtype, "input"))) return e;
+  if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
+  if (B < 1 || Hkv < 1 || L < 0) return fail(REC_EINVAL, "bad shape B=%d Hkv=%d L=%d", B, Hkv, L);
+  if (offset < 0) return fail(REC_EINVAL, "negative offset");
+  if (capacity % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 64", (long long)capacity);
+  if (offset + L > capacity)
+    return fail(REC_ECAPACITY, "appending %d tokens at %lld exceeds the capacity %lld", L, (long long)offset,
+                (long long)capacity);
+  if (L == 0) return ok();
+  if (!k_new || !v_new) return fail(REC_EINVAL, "new keys/values pointer is null");
+  if ((e = check_cache(k_bits, k_codes, k_scales, k_zeros, "key")) ||
+      (e = check_cache(v_bits, v_codes, v_scales, v_zeros, "value")))
+    return e;
+  AppendArgs a{};
+  a.k = RowSrc{k_new, in_dtype, k_sb, k_sh, k_st};
+  a.v = RowSrc{v_new, in_dtype, v_sb, v_sh, v_st};
+  a.kq = k_codes;
+  a.ks = k_scales;
+  a.kz = k_zeros;
+  a.vq = v_codes;
+  a.vs = v_scales;
+  a.vz = v_zeros;
+  a.B = B;
+  a.Hkv = Hkv;
+  a.L = L;
+  a.offset = offset;
+  a.cap = capacity;
+  a.v_units = v_bits == 4 ? ((offset + L - 1) >> 1) - (offset >> 1) + 1 : L;
+  return launched(launch_append(k_bits, v_bits, a, (hipStream_t)stream), "append launch");
+}
+
+int rec_decode_default_splits(int B, int Hkv, int64_t T) {
+  // Aim for about two workgroups per CU (256 CUs), at least one 64-token chunk
+  // per split.
+  const int64_t target = 512;
+  const int64_t bh = (int64_t)(B < 1 ? 1 : B) * (Hkv < 1 ? 1 : Hkv);
+  int64_t s = (target + bh - 1) / bh;
+  const int64_t chunks = (T + BLOCK_T - 1) / BLOCK_T;
+  if (s > chunks) s = chunks;
+  if (s > DECODE_MAX_SPLITS) s = DECODE_MAX_SPLITS;
+  return (int)(s < 1 ? 1 : s);
+}
+
+size_t rec_decode_workspace_bytes(int B, int Hkv, int splits) {
+  if (splits <= 0 || splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
+  return ws_layout(B, Hkv, splits).total;
+}
+
+int rec_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return fail(REC_EWORKSPACE, "workspace is null");
+  if (!aligned16(workspace)) return fail(REC_EALIGN, "workspace must be 16-byte aligned");
+  return launched(launch_fill_zero((uint32_t*)workspace, (int64_t)(workspace_bytes / 4), (hipStream_t)stream),
+                  "workspace init");
+}
+
+int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_bits, const void* k_codes,
+                    const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits, const void* v_codes,
+                    const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks, float scale, int B,
+                    int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
+                    size_t workspace_bytes, float* out, void* stream) {
+  return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
+                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out, nullptr,
+                       nullptr, stream);
+}
+
+int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new,
+                           const void* v_new, int new_dtype, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
+                           int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros, int v_bits,
+                           void* v_codes, uint16_t* v_scales, uint16_t* v_zeros, const float* sinks, float scale,
+                           int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
+                           size_t workspace_bytes, float* out, void* stream) {
+  int e;
+  if ((e = check_dtype(new_dtype, "new keys/values"))) return e;
+  if (!k_new || !v_new) return fail(REC_EINVAL, "new keys/values pointer is null");
+  const RowSrc kn{k_new, new_dtype, k_sb, k_sh, 0}, vn{v_new, new_dtype, v_sb, v_sh, 0};
+  return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
+                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out, &kn, &vn,
+                       stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+// Shared device helpers for the gfx950 quantized-KV attention kernels.
+//
+// Cache formats (per layer; bh = b * Hkv + h; C = capacity, a multiple of 64):
+//   int8 K codes   int8  [B][Hkv][C][128]            row-major per token
+//   int8 V codes   int8  [B][Hkv][C/64][128][64]     token-blocked: per 64-token
+//                                                    block, dim-major, tokens contiguous
+//   int8 scales    fp16  [B][Hkv][C]                 one per (token, head), K and V
+//   int4 K codes   uint8 [B][Hkv][C][64]             row-major, low nibble = even dim
+//   int4 V codes   uint8 [B][Hkv][C/64][128][32]     token-blocked, byte j of a dim
+//                                                    holds tokens 2j (low), 2j+1 (high)
+//   int4 scale/zp  fp16  [B][Hkv][C/64][4][64]       per 32-dim group, token-blocked
+// The blocked layouts let one 16-byte load hand a lane the 16 consecutive
+// tokens of one dim that the P·V matrix-core operand needs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rec {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+constexpr int HEAD_DIM = 128;
+constexpr int BLOCK_T = 64;      // tokens per V block and per wave iteration
+constexpr int GROUP4 = 32;       // int4 group size along head_dim
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+enum InDtype { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+  return (float)h;
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round-to-nearest-even
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Load element i of a half/bfloat16/float array as float (exact).
+__device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dt) {
+  if (dt == DT_F16) {
+    return (float)((const _Float16*)p)[i];
+  } else if (dt == DT_BF16) {
+    uint32_t b = ((const uint16_t*)p)[i];
+    return __builtin_bit_cast(float, b << 16);
+  }
+  return ((const float*)p)[i];
+}
+
+// fp16 round-to-nearest-even of a non-negative float, saturating at 65504.
+__device__ __forceinline__ uint16_t half_bits_saturate(float f) {
+  uint16_t b = float_to_half_bits(f);
+  if ((b & 0x7fff) == 0x7c00) b = (b & 0x8000) | 0x7bff;
+  return b;
+}
+
+// Exchange with the lane 8 positions away inside each row of 16 (DPP row_ror:8).
+__device__ __forceinline__ int dpp_ror8(int x) {
+  return __builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float dpp_ror8f(float x) {
+  return __builtin_bit_cast(float, dpp_ror8(__builtin_bit_cast(int, x)));
+}
+
+__device__ __forceinline__ float shfl_xor_f(float x, int m) {
+  return __shfl_xor(x, m, 64);
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
+// Four signed int8 codes -> two packed fp16 pairs, exactly.
+// The code is biased to unsigned (xor 0x80), glued under the fp16 exponent of
+// 1024 with v_perm, then 1024 + 128 is subtracted: (1024 + 128 + q) - 1152 = q.
+__device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, v2h& lo, v2h& hi) {
+  const uint32_t u = w ^ 0x80808080u;
+  const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+  const v2h bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  lo = __builtin_bit_cast(v2h, a) + bias;
+  hi = __builtin_bit_cast(v2h, b) + bias;
+}
+
+// Eight int8 codes in two dwords -> eight fp16 values in order.
+__device__ __forceinline__ v8h i8x8_to_h8(uint32_t w0, uint32_t w1) {
+  v2h a, b, c, d;
+  i8x4_to_h2x2(w0, a, b);
+  i8x4_to_h2x2(w1, c, d);
+  v8h r;
+  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+  return r;
+}
+
+// Eight uint4 codes in one dword (byte j = elements 2j | 2j+1 << 4) -> eight
+// fp16 values in the order [e0, e4, e1, e5, e2, e6, e3, e7].
+__device__ __forceinline__ v8h u4x8_to_h8_interleaved(uint32_t w) {
+  const v2h bias = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  v8h r;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    uint32_t t = ((w >> (4 * s)) & 0x000f000fu) | 0x64006400u;
+    v2h h = __builtin_bit_cast(v2h, t) + bias;
+    r[2 * s] = h[0];
+    r[2 * s + 1] = h[1];
+  }
+  return r;
+}
+
+}  // namespace rec

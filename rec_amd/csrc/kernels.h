@@ -1,0 +1,51 @@
+// Argument blocks and host-side launchers of the device kernels.
+#pragma once
+
+#include "common.h"
+#include "quant.h"
+
+namespace rec {
+
+struct AppendArgs {
+  RowSrc k, v;
+  void* kq;
+  uint16_t* ks;
+  uint16_t* kz;
+  void* vq;
+  uint16_t* vs;
+  uint16_t* vz;
+  int B, Hkv, L;
+  int64_t offset, cap;
+  int64_t v_units;  // per (b, h): L rows, or byte pairs for uint4 V
+};
+
+struct DecodeArgs {
+  const void* q;
+  int q_dtype;
+  int64_t q_sb, q_sh;  // element strides of q (batch, head); dims contiguous
+  const void* kq;
+  const uint16_t* ks;
+  const uint16_t* kz;
+  const void* vq;
+  const uint16_t* vs;
+  const uint16_t* vz;
+  const float* sinks;  // [Hq] or null
+  float* out;          // [B][Hq][128] fp32
+  float* ws_acc;       // [B*Hkv][S][8][128]
+  float* ws_stat;      // [B*Hkv][S][8][2]
+  int* counters;       // [B*Hkv], zero between launches
+  RowSrc knew, vnew;   // fused single-token append (knew.p null: none)
+  float q_mul;         // softmax scale * log2(e)
+  int B, Hq, Hkv, G;
+  int64_t T, cap;
+  int S;     // number of splits
+  int span;  // tokens per split (multiple of 64)
+};
+
+constexpr int DECODE_MAX_SPLITS = 256;
+
+hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream);
+hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream);
+hipError_t launch_decode(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
+
+}  // namespace rec

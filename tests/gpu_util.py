@@ -1,0 +1,52 @@
+"""Helpers shared by the GPU parity tests (oracle on the CPU, kernels on the GPU)."""
+
+import numpy as np
+import torch
+
+import oracle as O
+from rec_amd import to_logical
+
+SCALE = 1.0 / np.sqrt(128.0)
+ATOL, RTOL = 2e-3, 1e-3  # output tolerance of the decode path (fp32 accumulation)
+
+
+def f32(x: torch.Tensor) -> np.ndarray:
+    return x.detach().float().cpu().numpy()
+
+
+def oracle_quantize(x: np.ndarray, bits: int):
+    """Logical (codes, scales, zeros) of the oracle quantizer; zeros None for 8-bit."""
+    if bits == 8:
+        c, s = O.quantize_int8(x)
+        return c, s, None
+    return O.quantize_int4(x, 32)
+
+
+def dequant(bits, codes, scales, zeros):
+    if bits == 8:
+        return O.dequantize_int8(codes, scales)
+    return O.dequantize_int4(codes, scales, zeros, 32)
+
+
+def gpu_logical(kv):
+    c, s, z = to_logical(kv)
+    return (c.cpu().numpy(), s.cpu().numpy(), None if z is None else z.cpu().numpy())
+
+
+def assert_cache_equal(kv, ref):
+    got = gpu_logical(kv)
+    np.testing.assert_array_equal(got[0], ref[0], err_msg="codes differ")
+    np.testing.assert_array_equal(got[1].view(np.uint16), np.asarray(ref[1]).view(np.uint16), err_msg="scales differ")
+    if ref[2] is not None:
+        np.testing.assert_array_equal(got[2].view(np.uint16), np.asarray(ref[2]).view(np.uint16), err_msg="zeros differ")
+
+
+def assert_close(got: np.ndarray, ref: np.ndarray, what=""):
+    got = np.asarray(got, np.float64)
+    err = np.abs(got - ref)
+    bound = ATOL + RTOL * np.abs(ref)
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert np.all(err <= bound), (
+        f"{what}: max |err| {err.max():.3e} (at {worst}: got {got[worst]:.6f} ref {ref[worst]:.6f})"
+    )

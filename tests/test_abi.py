@@ -1,0 +1,100 @@
+"""The C-ABI library loads and exports every symbol include/rec_amd.h declares.
+
+No kernel is launched: argument validation runs on the host before any HIP
+call, so these tests run without a GPU.
+"""
+
+import os
+import re
+
+import pytest
+
+import rec_amd
+from rec_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rec_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rec_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("librec_amd.so is not built (run python -m rec_amd.build)")
+    return rec_amd.library()
+
+
+def test_header_symbols_exported(lib):
+    syms = declared_symbols()
+    assert len(syms) >= 7
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in rec_amd.h but not exported"
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_version_and_sizes(lib):
+    assert lib.rec_version().startswith(b"rec_amd")
+    assert lib.rec_decode_default_splits(1, 4, 32768) >= 64
+    assert lib.rec_decode_default_splits(1, 1, 10) == 1
+    assert lib.rec_decode_default_splits(1, 4, 258048) <= 256
+    small = lib.rec_decode_workspace_bytes(1, 4, 16)
+    big = lib.rec_decode_workspace_bytes(1, 4, 256)
+    assert 0 < small < big
+    # counters + stats + acc for 4 heads x 256 splits x 8 rows x 128 floats
+    assert big >= 4 * 256 * 8 * 128 * 4
+
+
+def _append(lib, **kw):
+    a = dict(k=None, v=None, dt=0, kb=8, vb=8, B=1, H=1, L=1, D=128, off=0, cap=64)
+    a.update(kw)
+    return lib.rec_kv_append(
+        a["k"], a["v"], a["dt"], 0, 0, 0, 0, 0, 0, a["kb"], 16, 16, 16, a["vb"], 16, 16, 16,
+        a["B"], a["H"], a["L"], a["D"], a["off"], a["cap"], None,
+    )
+
+
+def test_append_validation(lib):
+    assert _append(lib, kb=5) == _lib.REC_EINVAL
+    assert "k_bits" in _lib.last_error()
+    assert _append(lib, D=64) == _lib.REC_EUNSUPPORTED
+    assert _append(lib, cap=100) == _lib.REC_EINVAL
+    assert _append(lib, off=64, L=1, cap=64) == _lib.REC_ECAPACITY
+    assert "capacity" in _lib.last_error()
+    assert _append(lib, L=0) == _lib.REC_OK  # nothing to do, nothing launched
+    assert _append(lib, dt=7) == _lib.REC_EINVAL
+
+
+def _decode(lib, **kw):
+    a = dict(q=16, dt=0, kb=8, vb=8, B=1, Hq=8, Hkv=1, D=128, T=10, cap=64, splits=0, ws=16, wsb=1 << 30, out=16)
+    a.update(kw)
+    return lib.rec_decode_attn(
+        a["q"], a["dt"], 0, 0, a["kb"], 16, 16, 16, a["vb"], 16, 16, 16, None, 0.088,
+        a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["out"], None,
+    )
+
+
+def test_decode_validation(lib):
+    assert _decode(lib, Hq=12, Hkv=8) == _lib.REC_EINVAL
+    assert _decode(lib, Hq=16, Hkv=1) == _lib.REC_EUNSUPPORTED
+    assert "GQA" in _lib.last_error()
+    assert _decode(lib, T=0) == _lib.REC_EINVAL
+    assert _decode(lib, T=65) == _lib.REC_ECAPACITY
+    assert _decode(lib, wsb=16) == _lib.REC_EWORKSPACE
+    assert _decode(lib, ws=8) == _lib.REC_EALIGN
+    assert _decode(lib, out=4) == _lib.REC_EALIGN
+    assert _decode(lib, D=96) == _lib.REC_EUNSUPPORTED
+
+
+def test_error_mapping():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.REC_ECAPACITY, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.REC_EUNSUPPORTED, "x")
+    with pytest.raises(_lib.RecError):
+        _lib.check(_lib.REC_ELAUNCH, "x")
+    _lib.check(_lib.REC_OK, "x")

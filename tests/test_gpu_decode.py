@@ -1,0 +1,149 @@
+"""Parity of the gfx950 append and decode kernels with the CPU oracle.
+
+Cache bytes and scales must be bit-identical; attention outputs within
+2e-3 absolute + 1e-3 relative of the float64 oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from rec_amd import QuantizedKVCache, attend, quantized_attention_with_sinks, synthetic
+from tests.gpu_util import SCALE, assert_cache_equal, assert_close, dequant, f32, oracle_quantize
+
+pytestmark = pytest.mark.gpu
+
+BITS = [(8, 8), (8, 4), (4, 8), (4, 4)]
+
+
+def fill(cache, B, H, T, seed, kind="outliers", frac=0.01, dtype=torch.float16, chunks=None):
+    """Append T tokens in chunks; return the float32 K/V that went in."""
+    k = synthetic.kv((B, H, T, 128), seed, kind=kind, frac=frac, dtype=dtype)
+    v = synthetic.kv((B, H, T, 128), seed + 1, kind=kind, frac=frac, dtype=dtype)
+    pos = 0
+    for L in chunks or [T]:
+        cache.update_and_fetch(k[:, :, pos : pos + L], v[:, :, pos : pos + L])
+        pos += L
+    assert pos == T
+    return f32(k), f32(v)
+
+
+@pytest.mark.parametrize("bits", BITS)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_append_bit_exact(gpu, bits, dtype):
+    B, H = 2, 3
+    cache = QuantizedKVCache(32, *bits)
+    chunks = [5, 64, 1, 1, 70, 3, 200]
+    k, v = fill(cache, B, H, sum(chunks), 11, kind="heavy", frac=0.05, dtype=dtype, chunks=chunks)
+    kv_k, kv_v = cache.keys_and_values()
+    assert cache.offset == sum(chunks) and cache.capacity % 64 == 0
+    assert_cache_equal(kv_k, oracle_quantize(k, bits[0]))
+    assert_cache_equal(kv_v, oracle_quantize(v, bits[1]))
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_append_strided_and_special_rows(gpu, bits):
+    B, H, L = 1, 2, 9
+    x = torch.randn(B, L, H, 128, device="cuda", dtype=torch.float16)
+    x[:, 0] = 0  # all-zero rows
+    x[:, 1] = 1.5  # constant rows
+    x[:, 2, :, 7] = 300.0  # one large element
+    k = x.transpose(1, 2)  # (B, H, L, D) view, non-contiguous
+    v = (-x).transpose(1, 2)
+    cache = QuantizedKVCache(32, *bits)
+    cache.update_and_fetch(k, v)
+    kv_k, kv_v = cache.keys_and_values()
+    assert_cache_equal(kv_k, oracle_quantize(f32(k), bits[0]))
+    assert_cache_equal(kv_v, oracle_quantize(f32(v), bits[1]))
+
+
+DECODE_CASES = [
+    # B, Hq, Hkv, T, k_bits, v_bits, sinks, splits
+    (1, 8, 1, 1024, 8, 8, False, None),  # the tiny CPU-sized workload
+    (1, 8, 1, 1024, 8, 8, True, None),
+    (1, 32, 4, 4096, 8, 8, True, None),
+    (1, 32, 4, 1000, 8, 8, False, 3),
+    (2, 16, 2, 777, 8, 8, True, 256),
+    (1, 4, 1, 1, 8, 8, True, None),
+    (1, 4, 1, 1, 8, 8, False, None),
+    (1, 8, 4, 130, 8, 8, False, 1),
+    (1, 32, 4, 2048, 4, 4, True, None),
+    (1, 32, 4, 2048, 8, 4, True, None),
+    (1, 32, 4, 2048, 4, 8, False, 7),
+    (1, 8, 8, 333, 4, 4, True, 2),
+    (3, 24, 4, 65, 8, 4, True, None),
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_T{}_k{}v{}_s{}_sp{}".format(*c))
+def test_decode_matches_oracle(gpu, case):
+    B, Hq, Hkv, T, kb, vb, with_sinks, splits = case
+    cache = QuantizedKVCache(32, kb, vb)
+    k, v = fill(cache, B, Hkv, T, seed=100 + T, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, 1, seed=7 + Hq)
+    sinks = torch.randn(Hq, device="cuda") if with_sinks else None
+    kq, vq = cache.keys_and_values()
+    out = quantized_attention_with_sinks(q, kq, vq, SCALE, None, sinks, 32, kb, vb, out_dtype=torch.float32,
+                                         splits=splits)
+    rk, rv = oracle_quantize(k, kb), oracle_quantize(v, vb)
+    assert_cache_equal(kq, rk)
+    assert_cache_equal(vq, rv)
+    ref = O.attention(f32(q), dequant(kb, *rk), dequant(vb, *rv), SCALE, None if sinks is None else f32(sinks))
+    assert_close(f32(out), ref, f"case {case}")
+
+
+@pytest.mark.parametrize("bits", BITS)
+def test_fused_decode_steps(gpu, bits):
+    """append-then-attend in one launch, several steps, vs the oracle."""
+    B, Hq, Hkv, T0 = 1, 32, 4, 511
+    cache = QuantizedKVCache(32, *bits)
+    k0, v0 = fill(cache, B, Hkv, T0, seed=5)
+    ks, vs = [k0], [v0]
+    sinks = torch.randn(Hq, device="cuda")
+    for step in range(4):  # crosses the 512-token boundary and an odd/even pair
+        q = synthetic.query(B, Hq, 1, seed=50 + step)
+        kn = synthetic.kv((B, Hkv, 1, 128), 60 + step)
+        vn = synthetic.kv((B, Hkv, 1, 128), 70 + step)
+        out = attend(q, kn, vn, cache, SCALE, None, sinks, out_dtype=torch.float32)
+        ks.append(f32(kn))
+        vs.append(f32(vn))
+        K, V = np.concatenate(ks, 2), np.concatenate(vs, 2)
+        rk, rv = oracle_quantize(K, bits[0]), oracle_quantize(V, bits[1])
+        ref = O.attention(f32(q), dequant(bits[0], *rk), dequant(bits[1], *rv), SCALE, f32(sinks))
+        assert_close(f32(out), ref, f"step {step}")
+    kq, vq = cache.keys_and_values()
+    assert cache.offset == T0 + 4
+    assert_cache_equal(kq, rk)
+    assert_cache_equal(vq, rv)
+
+
+def test_unfused_equals_fused(gpu):
+    B, Hq, Hkv = 1, 32, 4
+    c1, c2 = QuantizedKVCache(32, 8, 8), QuantizedKVCache(32, 8, 8)
+    fill(c1, B, Hkv, 300, seed=9)
+    fill(c2, B, Hkv, 300, seed=9)
+    q = synthetic.query(B, Hq, 1, seed=1)
+    kn, vn = synthetic.kv((B, Hkv, 1, 128), 2), synthetic.kv((B, Hkv, 1, 128), 3)
+    a = attend(q, kn, vn, c1, SCALE, None, None, out_dtype=torch.float32, fused=True)
+    b = attend(q, kn, vn, c2, SCALE, None, None, out_dtype=torch.float32, fused=False)
+    torch.testing.assert_close(a, b, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("T", [32768, 258048])
+def test_long_context_int8(gpu, T):
+    """Full-size 32K / 252K int8 decode against the chunked CPU oracle."""
+    B, Hq, Hkv = 1, 32, 4
+    cache = QuantizedKVCache(32, 8, 8, max_tokens=T)
+    fill(cache, B, Hkv, T, seed=3, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, 1, seed=4)
+    sinks = torch.randn(Hq, device="cuda")
+    kq, vq = cache.keys_and_values()
+    out = quantized_attention_with_sinks(q, kq, vq, SCALE, None, sinks, 32, 8, 8, out_dtype=torch.float32)
+    from rec_amd import to_logical
+
+    kc, ksc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(kq))
+    vc, vsc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(vq))
+    cache_np = dict(k_bits=8, v_bits=8, kq=kc, ks=ksc, vq=vc, vs=vsc)
+    ref = O.split_k_decode_quantized(f32(q)[:, :, 0], cache_np, T, SCALE, f32(sinks), chunk=8192)
+    assert_close(f32(out)[:, :, 0], ref.astype(np.float64), f"T={T}")

@@ -1,0 +1,299 @@
+"""Pins the CPU oracle with checks that do not restate its formulas.
+
+Quantizers: brute-force nearest-code search, closed forms and invariants.
+Attention: torch's scaled_dot_product_attention in float64 (an independent
+library routine), the T = 1 closed form, permutation / identical-key / GQA
+invariants, and split-K merge over arbitrary partitions.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+def _fp16_rows(rng, n, d, scale=1.0):
+    return (rng.standard_normal((n, d)) * scale).astype(np.float16)
+
+
+# ---------------------------------------------------------------- int8 ----
+
+
+def _nearest_even(r):
+    """Round-half-even in float64 without numpy.rint (brute force over k)."""
+    fl = np.floor(r)
+    cands = np.stack([fl - 1, fl, fl + 1, fl + 2], -1)
+    dist = np.abs(cands - r[..., None])
+    best = dist.min(-1, keepdims=True)
+    ok = np.isclose(dist, best, rtol=0, atol=0)
+    # among equidistant candidates prefer the even one
+    even = (np.mod(cands, 2) == 0) & ok
+    pick = np.where(even.any(-1, keepdims=True), even, ok)
+    return (cands * pick).sum(-1) / pick.sum(-1)
+
+
+def test_int8_codes_are_the_nearest_representable_code():
+    rng = np.random.default_rng(1)
+    x = _fp16_rows(rng, 64, 128, 3.0)
+    codes, s16 = O.quantize_int8(x)
+    s = s16.astype(np.float64)[:, None]
+    # brute force: every code in [-127, 127], pick the closest q*s (ties -> even)
+    ks = np.arange(-127, 128, dtype=np.float64)
+    err = np.abs(x.astype(np.float64)[..., None] - ks * s[..., None])
+    best = err.min(-1, keepdims=True)
+    tie = err == best
+    even_pref = np.where((tie & (np.mod(ks, 2) == 0)).any(-1, keepdims=True), tie & (np.mod(ks, 2) == 0), tie)
+    brute = (ks * even_pref).sum(-1) / even_pref.sum(-1)
+    np.testing.assert_array_equal(codes.astype(np.float64), brute)
+
+
+def test_int8_scale_is_nearest_fp16_to_amax_over_127():
+    rng = np.random.default_rng(2)
+    x = _fp16_rows(rng, 256, 128, 2.0)
+    _, s16 = O.quantize_int8(x)
+    exact = np.abs(x.astype(np.float64)).max(-1) / 127.0
+    # neighbours of s16 in fp16 are no closer to the exact ratio
+    up = np.nextafter(s16, np.float16(np.inf)).astype(np.float64)
+    dn = np.nextafter(s16, np.float16(-np.inf)).astype(np.float64)
+    d0 = np.abs(s16.astype(np.float64) - exact)
+    assert np.all(d0 <= np.abs(up - exact)) and np.all(d0 <= np.abs(dn - exact))
+
+
+def test_int8_closed_forms_and_invariants():
+    rng = np.random.default_rng(3)
+    zero = np.zeros((3, 128), np.float16)
+    c, s = O.quantize_int8(zero)
+    assert not c.any() and not s.astype(np.float32).any()
+    one = np.zeros((1, 128), np.float16)
+    one[0, 17] = -5.5
+    c, s = O.quantize_int8(one)
+    assert c[0, 17] == -127 and np.count_nonzero(c) == 1
+    assert s[0] == np.float16(5.5 / 127)
+    x = _fp16_rows(rng, 128, 128, 4.0)
+    c, s = O.quantize_int8(x)
+    # the element of largest magnitude lands on +-127
+    i = np.abs(x.astype(np.float32)).argmax(-1)
+    np.testing.assert_array_equal(np.abs(c[np.arange(128), i]), 127)
+    # symmetric: q(-x) = -q(x), same scale
+    c2, s2 = O.quantize_int8(-x)
+    np.testing.assert_array_equal(c2, -c)
+    np.testing.assert_array_equal(s2, s)
+    # reconstruction error within half a step (tiny slack for the clamp at 127)
+    xh = O.dequantize_int8(c, s)
+    sf = s.astype(np.float32)[:, None]
+    assert np.all(np.abs(xh - x.astype(np.float32)) <= 0.5 * sf * 1.001 + 1e-12)
+    assert np.abs(c.astype(np.int32)).max() <= 127
+
+
+def test_int8_saturating_scale_for_huge_bf16_inputs():
+    x = np.zeros((1, 128), np.float32)
+    x[0, 0] = 1e30
+    c, s = O.quantize_int8(x)
+    assert s[0] == np.float16(65504) and c[0, 0] == 127
+
+
+# ---------------------------------------------------------------- int4 ----
+
+
+def test_int4_pack_order_low_nibble_even():
+    q = np.array([[1, 2, 15, 0]], np.uint8)
+    p = O.pack_int4(q)
+    np.testing.assert_array_equal(p, np.array([[0x21, 0x0F]], np.uint8))
+    np.testing.assert_array_equal(O.unpack_int4(p), q)
+
+
+def test_int4_codes_nearest_given_scale_and_zero():
+    rng = np.random.default_rng(4)
+    x = _fp16_rows(rng, 64, 128, 1.5)
+    x[:, 5] = (rng.standard_t(3, 64) * 2).astype(np.float16)
+    p, s16, z16 = O.quantize_int4(x, 32)
+    q = O.unpack_int4(p).astype(np.float64).reshape(64, 4, 32)
+    s = s16.astype(np.float64)[..., None]
+    z = z16.astype(np.float64)
+    xg = x.astype(np.float64).reshape(64, 4, 32)
+    # zero-point: nearest integer to -mn/s, inside [0, 15]
+    mn = np.minimum(xg.min(-1), 0)
+    np.testing.assert_array_equal(z, np.clip(_nearest_even(-mn / s[..., 0]), 0, 15))
+    # codes: brute force over 0..15 of |x - (k - z) s|
+    ks = np.arange(16, dtype=np.float64)
+    err = np.abs(xg[..., None] - (ks - z[..., None, None]) * s[..., None])
+    best = err.min(-1, keepdims=True)
+    tie = err == best
+    ev = tie & (np.mod(ks - z[..., None, None], 2) == 0)
+    pick = np.where(ev.any(-1, keepdims=True), ev, tie)
+    brute = (ks * pick).sum(-1) / pick.sum(-1)
+    np.testing.assert_array_equal(q, brute)
+
+
+def test_int4_closed_forms():
+    # all-zero group -> zero scale, zero codes, exact zero
+    z = np.zeros((2, 128), np.float16)
+    p, s, zz = O.quantize_int4(z)
+    assert not p.any() and not s.astype(np.float32).any() and not zz.astype(np.float32).any()
+    # a constant positive group keeps its value (range contains 0)
+    c = np.full((1, 128), 1.25, np.float16)
+    p, s, zz = O.quantize_int4(c)
+    xh = O.dequantize_int4(p, s, zz)
+    assert np.all(zz.astype(np.float32) == 0)
+    assert np.allclose(xh, 1.25, rtol=2e-3)
+    # exact zeros stay exact zeros
+    rng = np.random.default_rng(5)
+    x = _fp16_rows(rng, 32, 128)
+    x[:, ::7] = 0
+    p, s, zz = O.quantize_int4(x)
+    xh = O.dequantize_int4(p, s, zz)
+    assert np.all(xh[:, ::7] == 0)
+    sf = np.repeat(s.astype(np.float32), 32, axis=-1)
+    assert np.all(np.abs(xh - x.astype(np.float32)) <= 0.5 * sf * 1.01 + 1e-12)
+
+
+# ----------------------------------------------------------- attention ----
+
+
+def _torch_reference(q, k, v, scale, sinks=None, mask=None):
+    """Independent check: torch SDPA in float64; sinks become an extra zero key
+    whose additive mask equals the sink logit."""
+    q = torch.from_numpy(np.asarray(q, np.float64))
+    k = torch.from_numpy(np.asarray(k, np.float64))
+    v = torch.from_numpy(np.asarray(v, np.float64))
+    B, Hq, L, D = q.shape
+    Hkv, T = k.shape[1], k.shape[2]
+    k = k.repeat_interleave(Hq // Hkv, dim=1)
+    v = v.repeat_interleave(Hq // Hkv, dim=1)
+    bias = torch.zeros(B, Hq, L, T, dtype=torch.float64)
+    if mask is not None:
+        m = torch.from_numpy(np.asarray(O.causal_mask(L, T) if isinstance(mask, str) else mask))
+        bias = bias.masked_fill(~m, float("-inf")) if m.dtype == torch.bool else bias + m
+    if sinks is not None:
+        k = torch.cat([k, torch.zeros(B, Hq, 1, D, dtype=torch.float64)], 2)
+        v = torch.cat([v, torch.zeros(B, Hq, 1, D, dtype=torch.float64)], 2)
+        sb = torch.from_numpy(np.asarray(sinks, np.float64)).view(1, Hq, 1, 1).expand(B, Hq, L, 1)
+        bias = torch.cat([bias, sb], -1)
+    out = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=bias, scale=scale)
+    return out.numpy()
+
+
+def _cache(rng, B, Hkv, T, D=128):
+    k = rng.standard_normal((B, Hkv, T, D)).astype(np.float16)
+    v = rng.standard_normal((B, Hkv, T, D)).astype(np.float16)
+    kc, ks = O.quantize_int8(k)
+    vc, vs = O.quantize_int8(v)
+    return O.dequantize_int8(kc, ks), O.dequantize_int8(vc, vs)
+
+
+@pytest.mark.parametrize("with_sinks", [False, True])
+def test_attention_matches_torch_sdpa(with_sinks):
+    rng = np.random.default_rng(6)
+    B, Hq, Hkv, T = 2, 8, 2, 200
+    kh, vh = _cache(rng, B, Hkv, T)
+    q = rng.standard_normal((B, Hq, 1, 128)).astype(np.float16)
+    sinks = rng.standard_normal(Hq) if with_sinks else None
+    scale = 1 / np.sqrt(128)
+    ours = O.attention(q, kh, vh, scale, sinks)
+    ref = _torch_reference(q, kh, vh, scale, sinks)
+    np.testing.assert_allclose(ours, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_causal_and_bool_mask_match_torch():
+    rng = np.random.default_rng(7)
+    B, Hq, Hkv, T, L = 1, 4, 1, 96, 16
+    kh, vh = _cache(rng, B, Hkv, T)
+    q = rng.standard_normal((B, Hq, L, 128))
+    sinks = rng.standard_normal(Hq)
+    scale = 0.0883883
+    np.testing.assert_allclose(
+        O.attention(q, kh, vh, scale, sinks, "causal"), _torch_reference(q, kh, vh, scale, sinks, "causal"), atol=1e-12
+    )
+    m = rng.random((L, T)) > 0.3
+    np.testing.assert_allclose(O.attention(q, kh, vh, scale, sinks, m), _torch_reference(q, kh, vh, scale, sinks, m), atol=1e-12)
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(8)
+    # T = 1: out = v0 * e^{s0} / (e^{s0} + e^{sink})
+    k = rng.standard_normal((1, 1, 1, 128))
+    v = rng.standard_normal((1, 1, 1, 128))
+    q = rng.standard_normal((1, 2, 1, 128))
+    sinks = np.array([0.3, -1.2])
+    out = O.attention(q, k, v, 0.1, sinks)
+    for h in range(2):
+        s0 = 0.1 * float(q[0, h, 0] @ k[0, 0, 0])
+        w = 1.0 / (1.0 + np.exp(sinks[h] - s0))
+        np.testing.assert_allclose(out[0, h, 0], w * v[0, 0, 0], rtol=1e-13)
+    # identical keys: uniform weights -> mean of values, scaled by the sink share
+    T = 37
+    k = np.repeat(rng.standard_normal((1, 1, 1, 128)), T, axis=2)
+    v = rng.standard_normal((1, 1, T, 128))
+    out = O.attention(q, k, v, 0.1, sinks)
+    for h in range(2):
+        s0 = 0.1 * float(q[0, h, 0] @ k[0, 0, 0])
+        share = T / (T + np.exp(sinks[h] - s0))
+        np.testing.assert_allclose(out[0, h, 0], share * v[0, 0].mean(0), rtol=1e-12)
+
+
+def test_attention_invariants():
+    rng = np.random.default_rng(9)
+    kh, vh = _cache(rng, 1, 2, 120)
+    q = rng.standard_normal((1, 16, 1, 128))
+    q[:, 8:12] = q[:, 8:9]  # equal queries in one GQA group
+    out = O.attention(q, kh, vh, 0.088, None)
+    for h in range(9, 12):
+        np.testing.assert_allclose(out[0, h], out[0, 8], rtol=1e-14)
+    perm = rng.permutation(120)
+    out2 = O.attention(q, kh[:, :, perm], vh[:, :, perm], 0.088, None)
+    np.testing.assert_allclose(out, out2, rtol=1e-12, atol=1e-14)
+    # all keys masked, no sink -> zeros (the merge's z == 0 branch)
+    m = np.zeros((1, 120), bool)
+    assert not O.attention(q, kh, vh, 0.088, None, m).any()
+
+
+def test_prefill_rows_equal_decode_over_prefix():
+    rng = np.random.default_rng(10)
+    P, L = 50, 12
+    kh, vh = _cache(rng, 1, 1, P + L)
+    q = rng.standard_normal((1, 8, L, 128))
+    sinks = rng.standard_normal(8)
+    full = O.attention(q, kh, vh, 0.088, sinks, "causal")
+    for i in range(L):
+        row = O.attention(q[:, :, i : i + 1], kh[:, :, : P + i + 1], vh[:, :, : P + i + 1], 0.088, sinks)
+        np.testing.assert_allclose(full[:, :, i : i + 1], row, rtol=1e-12, atol=1e-15)
+
+
+@pytest.mark.parametrize("parts", [None, [0, 1, 7, 100, 101], [0, 64, 128, 192, 256, 300]])
+def test_split_k_merge_equals_single_pass(parts):
+    rng = np.random.default_rng(11)
+    T = 333
+    kh, vh = _cache(rng, 1, 4, T)
+    q = rng.standard_normal((1, 32, 128)).astype(np.float32)
+    sinks = rng.standard_normal(32)
+    ref = O.attention(q[:, :, None], kh, vh, 0.088, sinks)[:, :, 0]
+    got = O.split_k_decode(
+        q, lambda a, b: kh[:, :, a:b], lambda a, b: vh[:, :, a:b], T, 0.088, sinks, parts=parts, chunk=64
+    )
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-6)
+
+
+def test_split_k_quantized_int4_and_mixed():
+    rng = np.random.default_rng(12)
+    T = 130
+    k = rng.standard_normal((1, 2, T, 128)).astype(np.float16)
+    v = rng.standard_normal((1, 2, T, 128)).astype(np.float16)
+    kq, ks = O.quantize_int8(k)
+    vq, vs, vz = O.quantize_int4(v)
+    cache = dict(k_bits=8, v_bits=4, kq=kq, ks=ks, vq=vq, vs=vs, vz=vz)
+    q = rng.standard_normal((1, 16, 128)).astype(np.float32)
+    got = O.split_k_decode_quantized(q, cache, T, 0.088, None, chunk=48)
+    ref = O.attention(q[:, :, None], O.dequantize_int8(kq, ks), O.dequantize_int4(vq, vs, vz), 0.088)[:, :, 0]
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-6)
+
+
+def test_mutation_in_oracle_is_caught():
+    """A planted mistake (dropped sink term) must fail the torch pin."""
+    rng = np.random.default_rng(13)
+    kh, vh = _cache(rng, 1, 1, 20)
+    q = rng.standard_normal((1, 2, 1, 128))
+    sinks = np.array([1.0, 2.0])
+    wrong = O.attention(q, kh, vh, 0.088, None)  # sink dropped
+    ref = _torch_reference(q, kh, vh, 0.088, sinks)
+    assert not np.allclose(wrong, ref, rtol=1e-6, atol=1e-9)
