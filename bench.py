@@ -1,0 +1,349 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X.
+
+A step is one decode step of one attention layer: quantize-append one new K/V
+token into the int8 cache and attend 32 query heads (GQA 8:1 over 4 KV heads,
+head_dim 128) over every cached token, in one fused launch
+(``rec_decode_append_attn``).  The headline workload is a 32K-token context;
+the same run measures a 252K (258,048-token) context.
+
+Inputs are resident in HBM before timing starts.  To keep the 256 MB
+Infinity Cache (MALL) from serving the KV cache, consecutive steps rotate over
+independent cache instances totalling more than 1 GB (32 x 34 MB at 32K,
+4 x 268 MB at 252K).  Each instance starts ``n`` tokens short of the context
+and grows by one token per step it serves.
+
+Timing: W eager warm-up steps, then K steps captured in one HIP graph and
+replayed once between synchronisations (HIP events on the launch stream).
+Per-launch kernel time for the roofline comes from a separate pass with an
+event pair around every launch.  Algorithmic bytes per step are the K/V codes
+and scales of all T tokens read once, the query read, the fp32 output written
+and the appended token read and written.
+
+The CPU baseline times the oracle's split-K restatement (chunked
+dequantization, float32 attention with sinks, merge) on the host over a
+bounded sample of the same 32K workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode-attn HBM GB/s (% of peak) and µs/step per layer at 32K and 252K ctx"
+HQ, HKV, D = 32, 4, 128
+SCALE = 1.0 / np.sqrt(D)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_i8_32k_traffic.json")
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def row_bytes(bits):
+    return D + 2 if bits == 8 else D // 2 + 16  # codes + fp16 scale (+ zero-points)
+
+
+def step_bytes(T, B=1, k_bits=8, v_bits=8):
+    kv = B * T * HKV * (row_bytes(k_bits) + row_bytes(v_bits))
+    q = B * HQ * D * 2
+    out = B * HQ * D * 4
+    append = B * HKV * (2 * D * 2 + row_bytes(k_bits) + row_bytes(v_bits))
+    return kv + q + out + append
+
+
+class DecodeWorkload:
+    """R cache instances of one context length plus a pool of new tokens."""
+
+    def __init__(self, T, R, total_steps, seed, splits=0):
+        import torch
+
+        import rec_amd
+        from rec_amd import synthetic
+
+        self.torch, self.lib = torch, rec_amd.library()
+        self.T, self.R, self.splits = T, R, splits
+        counts = [len(range(i, total_steps, R)) for i in range(R)]
+        self.caches = []
+        for i in range(R):
+            T0 = T - counts[i]
+            c = rec_amd.QuantizedKVCache(32, 8, 8, max_tokens=T)
+            k = synthetic.kv((1, HKV, T0, D), seed + 2 * i, kind="outliers", frac=0.01)
+            v = synthetic.kv((1, HKV, T0, D), seed + 2 * i + 1, kind="outliers", frac=0.01)
+            c.update_and_fetch(k, v)
+            del k, v
+            self.caches.append(c)
+        P = 16
+        self.pool = [
+            (
+                synthetic.query(1, HQ, 1, seed + 1000 + j)[:, :, 0].contiguous(),
+                synthetic.kv((1, HKV, 1, D), seed + 2000 + j),
+                synthetic.kv((1, HKV, 1, D), seed + 3000 + j),
+            )
+            for j in range(P)
+        ]
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.sinks = torch.randn(HQ, generator=g, device="cuda")
+        self.out = torch.empty((1, HQ, D), dtype=torch.float32, device="cuda")
+        self.ws = torch.zeros(self.lib.rec_decode_workspace_bytes(1, HKV, 256), dtype=torch.uint8, device="cuda")
+        self.step_T = []
+        torch.cuda.synchronize()
+
+    def step(self, s):
+        """Launch one fused append+attend step on the current stream."""
+        from rec_amd import _lib
+
+        c = self.caches[s % self.R]
+        q, kn, vn = self.pool[s % len(self.pool)]
+        T = c.offset + 1
+        kc, ks, _ = c.keys
+        vc, vs, _ = c.values
+        stream = self.torch.cuda.current_stream().cuda_stream
+        rc = self.lib.rec_decode_append_attn(
+            q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
+            kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1),
+            8, kc.data_ptr(), ks.data_ptr(), None, 8, vc.data_ptr(), vs.data_ptr(), None,
+            self.sinks.data_ptr(), SCALE, 1, HQ, HKV, D, T, c.capacity, self.splits,
+            self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), stream,
+        )
+        _lib.check(rc, "rec_decode_append_attn")
+        c.offset = T
+        return T
+
+
+def run_decode(T, R, steps, warmup, kernel_steps, seed):
+    import torch
+
+    total = warmup + steps + kernel_steps
+    log(f"T={T}: building {R} cache instances")
+    w = DecodeWorkload(T, R, total, seed)
+    log(f"T={T}: warm-up {warmup} steps")
+    for s in range(warmup):
+        w.step(s)
+    torch.cuda.synchronize()
+    # K timed steps in one graph, replayed once
+    graph = torch.cuda.CUDAGraph()
+    timed_T = []
+    with torch.cuda.graph(graph):
+        for s in range(warmup, warmup + steps):
+            timed_T.append(w.step(s))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = e0.elapsed_time(e1) / steps
+    log(f"T={T}: {steps} steps in {ms_per_step * steps:.3f} ms (host wall {wall * 1e3:.3f} ms)")
+    # per-launch kernel time
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(kernel_steps)]
+    kT = []
+    for i, s in enumerate(range(warmup + steps, total)):
+        evs[i][0].record()
+        kT.append(w.step(s))
+        evs[i][1].record()
+    torch.cuda.synchronize()
+    kms = np.array([a.elapsed_time(b) for a, b in evs])
+    bytes_step = float(np.mean([step_bytes(t) for t in timed_T]))
+    bytes_kernel = float(np.mean([step_bytes(t) for t in kT]))
+    res = dict(
+        T=T,
+        instances=R,
+        ms_per_step=ms_per_step,
+        us_per_step=ms_per_step * 1e3,
+        bytes_per_step=bytes_step,
+        gbs=bytes_step / (ms_per_step * 1e-3) / 1e9,
+        kernel_us_mean=float(kms.mean() * 1e3),
+        kernel_us_median=float(np.median(kms) * 1e3),
+        kernel_gbs=bytes_kernel / (float(kms.mean()) * 1e-3) / 1e9,
+        bytes_per_launch=bytes_kernel,
+        cache_bytes=sum(c.nbytes for c in w.caches),
+    )
+    del graph, w
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(T, seed, budget_s=10.0):
+    """The oracle's split-K decode over one 32K instance on the host cores."""
+    import torch
+
+    import oracle as O
+    import rec_amd
+    from rec_amd import synthetic
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    c = rec_amd.QuantizedKVCache(32, 8, 8, max_tokens=T)
+    k = synthetic.kv((1, HKV, T - 1, D), seed, kind="outliers", frac=0.01)
+    v = synthetic.kv((1, HKV, T - 1, D), seed + 1, kind="outliers", frac=0.01)
+    kq, vq = c.update_and_fetch(k, v)
+    kc, ksc = (x.cpu().numpy() for x in rec_amd.to_logical(kq)[:2])
+    vc, vsc = (x.cpu().numpy() for x in rec_amd.to_logical(vq)[:2])
+    del k, v, c
+    torch.cuda.empty_cache()
+    rng = np.random.default_rng(seed)
+    kbuf = np.zeros((1, HKV, T, D), np.int8)
+    vbuf = np.zeros((1, HKV, T, D), np.int8)
+    ksb = np.zeros((1, HKV, T), np.float16)
+    vsb = np.zeros((1, HKV, T), np.float16)
+    kbuf[:, :, : T - 1], vbuf[:, :, : T - 1], ksb[:, :, : T - 1], vsb[:, :, : T - 1] = kc, vc, ksc, vsc
+    sinks = rng.standard_normal(HQ).astype(np.float32)
+    times = []
+    limiter = threadpool_limits(1) if threadpool_limits else None
+    try:
+        start = time.perf_counter()
+        while True:
+            q = rng.standard_normal((1, HQ, D)).astype(np.float16).astype(np.float32)
+            kn = rng.standard_normal((1, HKV, 1, D)).astype(np.float16)
+            vn = rng.standard_normal((1, HKV, 1, D)).astype(np.float16)
+            t0 = time.perf_counter()
+            a, b = O.quantize_int8(kn)
+            kbuf[:, :, T - 1 :], ksb[:, :, T - 1 :] = a, b
+            a, b = O.quantize_int8(vn)
+            vbuf[:, :, T - 1 :], vsb[:, :, T - 1 :] = a, b
+            cache = dict(k_bits=8, v_bits=8, kq=kbuf, ks=ksb, vq=vbuf, vs=vsb)
+            O.split_k_decode_quantized(q, cache, T, SCALE, sinks, chunk=4096, workers=cores)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - start > budget_s and len(times) >= 3:
+                break
+    finally:
+        if limiter is not None:
+            limiter.unregister()
+    sec = float(np.median(times))
+    return dict(
+        value=step_bytes(T) / sec / 1e9,
+        unit="GB/s",
+        cores=cores,
+        kind="port",
+        us_per_step=sec * 1e6,
+        sample=f"{len(times)} decode steps (1-token int8 append + attention) of the 32K workload, one cache "
+        f"instance, NumPy float32 split-K over 4096-token chunks on {cores} threads; median step time",
+    )
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--kernel-steps", type=int, default=64)
+    ap.add_argument("--long-steps", type=int, default=0, help="timed steps at 252K (default steps/8)")
+    ap.add_argument("--no-long", action="store_true", help="skip the 252K measurement")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+            "the decode path shards by KV head or by context with no per-step collective beyond a "
+            "16.6 KB merge, which this single-GPU build does not run",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    import rec_amd
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    rec_amd.library()
+    torch.cuda.set_device(0)
+
+    r32 = run_decode(32768, 32, args.steps, args.warmup, args.kernel_steps, args.seed)
+    log(f"32K: {r32['us_per_step']:.2f} us/step, {r32['gbs']:.0f} GB/s; kernel {r32['kernel_us_mean']:.2f} us")
+    r252 = None
+    if not args.no_long:
+        ls = args.long_steps or max(16, args.steps // 8)
+        r252 = run_decode(258048, 4, ls, max(4, args.warmup // 4), max(16, args.kernel_steps // 2), args.seed + 99)
+        log(f"252K: {r252['us_per_step']:.2f} us/step, {r252['gbs']:.0f} GB/s; kernel {r252['kernel_us_mean']:.2f} us")
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        traffic = t.get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline")
+        cpu = cpu_baseline(32768, args.seed + 7, args.cpu_budget)
+
+    result = {
+        "metric": METRIC,
+        "value": round(r32["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r32["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode step at 32K context: 1-token int8 quantize-append + GQA attention, 32 q heads / "
+            "4 kv heads, head_dim 128, batch 1, one layer",
+            "context": 32768,
+            "q_heads": HQ,
+            "kv_heads": HKV,
+            "head_dim": D,
+            "batch": 1,
+            "kv_format": "int8 symmetric, fp16 scale per (token, head); 1% outlier channels x8",
+            "cache_instances": r32["instances"],
+            "cache_bytes_total": r32["cache_bytes"],
+            "timing": "K steps in one HIP graph replay, HIP events",
+        },
+        "us_per_step": round(r32["us_per_step"], 3),
+        "frac_of_peak": round(r32["gbs"] / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(r32["kernel_gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(r32["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "rec::decode_kernel<8, 8> (fused append + split-K decode + merge)",
+            "kernel_us_mean": round(r32["kernel_us_mean"], 3),
+            "kernel_us_median": round(r32["kernel_us_median"], 3),
+            "algorithmic_bytes_per_launch": r32["bytes_per_launch"],
+        },
+        "cpu_baseline": cpu,
+    }
+    if r252 is not None:
+        result["context_252k"] = {
+            "context": 258048,
+            "us_per_step": round(r252["us_per_step"], 3),
+            "gbs": round(r252["gbs"], 2),
+            "frac_of_peak": round(r252["gbs"] / HBM_PEAK_GBS, 4),
+            "kernel_us_mean": round(r252["kernel_us_mean"], 3),
+            "kernel_gbs": round(r252["kernel_gbs"], 2),
+            "bytes_per_step": r252["bytes_per_step"],
+            "cache_instances": r252["instances"],
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

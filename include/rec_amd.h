@@ -70,9 +70,9 @@ int rec_decode_default_splits(int B, int Hkv, int64_t T);
 size_t rec_decode_workspace_bytes(int B, int Hkv, int splits);
 
 /*
- * Make a fresh workspace usable (zeroes its counters with a kernel, so it can
- * be captured in a HIP graph).  Decode calls leave the counters zeroed again.
- * One workspace serves one stream at a time.
+ * Zero a workspace with a kernel (capturable in a HIP graph).  Decode calls
+ * need no particular workspace contents; this is for callers that want a
+ * deterministic buffer.  One workspace serves one stream at a time.
  */
 int rec_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 

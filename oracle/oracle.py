@@ -206,7 +206,7 @@ def attention(q, k_hat, v_hat, scale, sinks=None, mask=None):
     return out.reshape(B, Hq, L, D)
 
 
-def split_k_decode(q, k_hat_fn, v_hat_fn, T, scale, sinks=None, parts=None, chunk=4096):
+def split_k_decode(q, k_hat_fn, v_hat_fn, T, scale, sinks=None, parts=None, chunk=4096, workers=None):
     """Split-K flash decode in float32 with a second merge pass.
 
     Follows ``megakernel.py:619-693`` (each part keeps a running max, a sum
@@ -216,7 +216,8 @@ def split_k_decode(q, k_hat_fn, v_hat_fn, T, scale, sinks=None, parts=None, chun
     ``v_hat_fn(a, b)`` dequantize tokens ``[a, b)`` to float32
     ``(B, Hkv, b-a, D)``, so the whole cache is never materialised.
     Parts are contiguous token ranges of ``chunk`` tokens (the CPU analogue of
-    the GPU's splits).  Returns ``(B, Hq, D)`` float32.
+    the GPU's splits), computed on ``workers`` threads when given.  Returns
+    ``(B, Hq, D)`` float32.
     """
     q = np.asarray(q, np.float32)
     B, Hq, D = q.shape
@@ -226,19 +227,27 @@ def split_k_decode(q, k_hat_fn, v_hat_fn, T, scale, sinks=None, parts=None, chun
     qh = (q * np.float32(scale)).reshape(B, Hkv, G, D)
     bounds = list(range(0, T, chunk)) if parts is None else list(parts)
     bounds = [b for b in bounds if b < T] + [T]
-    ms, ls, accs = [], [], []
-    for a, b in zip(bounds[:-1], bounds[1:]):
+
+    def part(ab):
+        a, b = ab
         k = k_hat_fn(a, b)
         v = v_hat_fn(a, b)
         s = np.matmul(qh, k.transpose(0, 1, 3, 2))  # (B, Hkv, G, n)
         m = s.max(axis=-1, keepdims=True)
         p = np.exp(s - m)
-        ms.append(m[..., 0])
-        ls.append(p.sum(axis=-1))
-        accs.append(np.matmul(p, v))  # (B, Hkv, G, D)
-    m = np.stack(ms, 0)
-    l = np.stack(ls, 0)
-    acc = np.stack(accs, 0)
+        return m[..., 0], p.sum(axis=-1), np.matmul(p, v)  # acc (B, Hkv, G, D)
+
+    ranges = list(zip(bounds[:-1], bounds[1:]))
+    if workers and workers > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(workers) as ex:
+            parts_out = list(ex.map(part, ranges))
+    else:
+        parts_out = [part(r) for r in ranges]
+    m = np.stack([x[0] for x in parts_out], 0)
+    l = np.stack([x[1] for x in parts_out], 0)
+    acc = np.stack([x[2] for x in parts_out], 0)
     top = m.max(axis=0)
     if sinks is not None:
         sink = np.asarray(sinks, np.float32).reshape(1, Hkv, G)
@@ -252,7 +261,7 @@ def split_k_decode(q, k_hat_fn, v_hat_fn, T, scale, sinks=None, parts=None, chun
     return out.reshape(B, Hq, D).astype(np.float32)
 
 
-def split_k_decode_quantized(q, cache, T, scale, sinks=None, chunk=4096):
+def split_k_decode_quantized(q, cache, T, scale, sinks=None, chunk=4096, workers=None):
     """``split_k_decode`` over a logical quantized cache dict.
 
     ``cache`` holds ``k_bits``/``v_bits`` and logical arrays ``kq, ks[, kz]``
@@ -270,4 +279,6 @@ def split_k_decode_quantized(q, cache, T, scale, sinks=None, chunk=4096):
 
         return fn
 
-    return split_k_decode(q, deq("k", cache["k_bits"]), deq("v", cache["v_bits"]), T, scale, sinks, chunk=chunk)
+    return split_k_decode(
+        q, deq("k", cache["k_bits"]), deq("v", cache["v_bits"]), T, scale, sinks, chunk=chunk, workers=workers
+    )

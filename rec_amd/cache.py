@@ -12,9 +12,10 @@ Formats (bits per K and V independently):
 * 8-bit: symmetric int8, one fp16 scale per (token, head).
 * 4-bit: asymmetric uint4, fp16 scale and zero-point per 32 dims.
 
-V codes (and 4-bit scales) are stored token-blocked in 64-token blocks, so
-the capacity is always a multiple of 64; :func:`to_logical` turns any cache
-tensor back into the plain ``(B, Hkv, T, ...)`` layout.
+Codes and scales are stored in 32-token blocks laid out for the matrix-core
+operands of the decode kernel (table in ``rec_amd/csrc/common.h``), so the
+capacity is a multiple of 32; :func:`to_logical` turns any cache tensor back
+into the plain ``(B, Hkv, T, ...)`` layout.
 """
 
 from __future__ import annotations
@@ -25,7 +26,7 @@ import torch
 
 from . import _lib
 
-BLOCK = 64
+BLOCK = 32
 HEAD_DIM = 128
 GROUP4 = 32
 
@@ -35,9 +36,9 @@ _DTYPES = {torch.float16: _lib.REC_F16, torch.bfloat16: _lib.REC_BF16, torch.flo
 class QuantizedKV(NamedTuple):
     """Quantized K or V of one layer: what ``update_and_fetch`` returns.
 
-    ``codes``/``scales``/``zeros`` span the full capacity; ``length`` tokens
-    are valid.  ``zeros`` is None for 8-bit.  ``blocked`` marks the
-    token-blocked layout used for V.
+    ``codes``/``scales``/``zeros`` span the full capacity in 32-token blocks;
+    ``length`` tokens are valid.  ``zeros`` is None for 8-bit.  ``blocked``
+    marks the dim-major V layout (K blocks are token-major).
     """
 
     codes: torch.Tensor
@@ -53,19 +54,18 @@ class QuantizedKV(NamedTuple):
 
     @property
     def capacity(self) -> int:
-        return self.scales.shape[2] if self.bits == 8 else self.scales.shape[2] * BLOCK
+        return self.codes.shape[2] * BLOCK
 
 
-def _alloc(B, H, cap, bits, blocked, device):
+def _alloc(B, H, cap, bits, is_v, device):
+    """Zeroed codes/scales/zeros of one cache tensor (layout table in rec_amd/csrc/common.h)."""
     nb = cap // BLOCK
     if bits == 8:
-        codes = torch.zeros((B, H, nb, HEAD_DIM * BLOCK) if blocked else (B, H, cap, HEAD_DIM), dtype=torch.int8, device=device)
-        scales = torch.zeros((B, H, cap), dtype=torch.float16, device=device)
+        codes = torch.zeros((B, H, nb, BLOCK * HEAD_DIM), dtype=torch.int8, device=device)
+        scales = torch.zeros((B, H, nb, BLOCK), dtype=torch.float16, device=device)
         zeros = None
     else:
-        codes = torch.zeros(
-            (B, H, nb, HEAD_DIM * BLOCK // 2) if blocked else (B, H, cap, HEAD_DIM // 2), dtype=torch.uint8, device=device
-        )
+        codes = torch.zeros((B, H, nb, BLOCK * HEAD_DIM // 2), dtype=torch.uint8, device=device)
         scales = torch.zeros((B, H, nb, HEAD_DIM // GROUP4, BLOCK), dtype=torch.float16, device=device)
         zeros = torch.zeros_like(scales)
     return codes, scales, zeros
@@ -79,6 +79,14 @@ def _grow_tensor(old, new):
     return new
 
 
+def block_pos(t):
+    """Position of token t (0..31) inside its 32-token cache block."""
+    return ((t >> 2) & 3) * 8 + (t >> 4) * 4 + (t & 3)
+
+
+_POS = [block_pos(t) for t in range(BLOCK)]
+
+
 def to_logical(kv: QuantizedKV, length: Optional[int] = None):
     """Return ``(codes, scales, zeros)`` in the plain layout, first ``length`` tokens.
 
@@ -87,23 +95,29 @@ def to_logical(kv: QuantizedKV, length: Optional[int] = None):
     zeros fp16 ``(B, H, T, 4)``.
     """
     T = kv.length if length is None else length
-    B, H = kv.codes.shape[:2]
-    if kv.bits == 8:
-        codes = kv.codes
-        if kv.blocked:
-            codes = codes.view(B, H, -1, HEAD_DIM, BLOCK).permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
-        return codes[:, :, :T].contiguous(), kv.scales[:, :, :T].contiguous(), None
-    if kv.blocked:
-        packed = kv.codes.view(B, H, -1, HEAD_DIM, BLOCK // 2)
-        lo, hi = packed & 0xF, packed >> 4
-        tok = torch.stack([lo, hi], -1).reshape(B, H, -1, HEAD_DIM, BLOCK)  # token-major within block
-        q = tok.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
+    B, H, nb = kv.codes.shape[:3]
+    pos = torch.tensor(_POS, device=kv.codes.device)
+    if not kv.blocked:  # K: [nb][2 halves][32 tokens][64 or 32 bytes]
+        w = HEAD_DIM // 2 if kv.bits == 8 else HEAD_DIM // 4
+        codes = kv.codes.view(B, H, nb, 2, BLOCK, w).permute(0, 1, 2, 4, 3, 5).reshape(B, H, nb * BLOCK, 2 * w)
+    elif kv.bits == 8:  # V: [nb][128 dims][32 positions]
+        codes = kv.codes.view(B, H, nb, HEAD_DIM, BLOCK)[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
+    else:  # V: [nb][128 dims][16 bytes], position p in byte p // 2
+        packed = kv.codes.view(B, H, nb, HEAD_DIM, BLOCK // 2)
+        q = torch.stack([packed & 0xF, packed >> 4], -1).reshape(B, H, nb, HEAD_DIM, BLOCK)[..., pos]
+        q = q.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
         codes = (q[..., 0::2] | (q[..., 1::2] << 4)).to(torch.uint8)
+    if kv.bits == 8:
+        sc = kv.scales[..., pos].reshape(B, H, -1)
+        zp = None
     else:
-        codes = kv.codes
-    sc = kv.scales.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
-    zp = kv.zeros.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
-    return codes[:, :, :T].contiguous(), sc[:, :, :T].contiguous(), zp[:, :, :T].contiguous()
+        sc = kv.scales[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
+        zp = kv.zeros[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
+    return (
+        codes[:, :, :T].contiguous(),
+        sc[:, :, :T].contiguous(),
+        None if zp is None else zp[:, :, :T].contiguous(),
+    )
 
 
 def _stride3(x):

@@ -38,15 +38,15 @@ int launched(hipError_t e, const char* what) {
 size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WorkspaceLayout {
-  size_t counters, stat, acc, total;
+  size_t stat, acc, total;
 };
 
+// Split partials: stats (m, l) then accumulators, per (b, h, split, head-in-group).
 WorkspaceLayout ws_layout(int B, int Hkv, int splits) {
   WorkspaceLayout w;
   const size_t bh = (size_t)B * Hkv;
-  w.counters = 0;
-  w.stat = round256(bh * sizeof(int));
-  w.acc = w.stat + round256(bh * splits * 8 * 2 * sizeof(float));
+  w.stat = 0;
+  w.acc = round256(bh * splits * 8 * 2 * sizeof(float));
   w.total = w.acc + bh * splits * 8 * HEAD_DIM * sizeof(float);
   return w;
 }
@@ -69,14 +69,26 @@ int check_dtype(int dt, const char* name) {
   return REC_OK;
 }
 
-// Splits actually launched for a request: chunk-aligned spans, no empty split.
-void effective_splits(int64_t T, int req, int* S, int* span) {
-  const int64_t chunks = (T + BLOCK_T - 1) / BLOCK_T;
-  int64_t s = req < 1 ? 1 : req;
-  if (s > chunks) s = chunks;
-  const int64_t span_chunks = (chunks + s - 1) / s;
-  *span = (int)(span_chunks * BLOCK_T);
-  *S = (int)((chunks + span_chunks - 1) / span_chunks);
+// Splits actually launched for a request.  Regular splits cover
+// [0, t_split_end) in spans of whole 32-token chunks; with a fused append the
+// newest token's chunk [t_split_end, T) is one more split of its own, so the
+// append's latency is not added to a full-size split.
+constexpr int CHUNK = BLOCK_T;
+void effective_splits(int64_t T, int req, bool fused, int* S, int* span, int* t_split_end) {
+  const int64_t R = fused ? ((T - 1) / CHUNK) * CHUNK : T;
+  int S_reg = 0, sp = CHUNK;
+  if (R > 0) {
+    const int64_t chunks = (R + CHUNK - 1) / CHUNK;
+    int64_t s = req - (fused ? 1 : 0);
+    if (s < 1) s = 1;
+    if (s > chunks) s = chunks;
+    const int64_t span_chunks = (chunks + s - 1) / s;
+    sp = (int)(span_chunks * CHUNK);
+    S_reg = (int)((chunks + span_chunks - 1) / span_chunks);
+  }
+  *S = S_reg + (fused ? 1 : 0);
+  *span = sp;
+  *t_split_end = (int)R;
 }
 
 int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_bits, const void* kq,
@@ -92,16 +104,17 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
   if (Hq / Hkv > 8) return fail(REC_EUNSUPPORTED, "GQA ratio %d exceeds 8", Hq / Hkv);
   if (T < 1) return fail(REC_EINVAL, "decode needs at least one cached token (T=%lld)", (long long)T);
-  if (cap % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 64", (long long)cap);
+  if (cap % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 32", (long long)cap);
   if (T > cap) return fail(REC_ECAPACITY, "T=%lld exceeds the cache capacity %lld", (long long)T, (long long)cap);
+  if (cap > ((int64_t)1 << 24)) return fail(REC_EUNSUPPORTED, "capacity above 16M tokens per head");
   if (!q || !out) return fail(REC_EINVAL, "query/output pointer is null");
   if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
   if ((e = check_cache(k_bits, kq, ks, kz, "key")) || (e = check_cache(v_bits, vq, vs, vz, "value"))) return e;
   if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
   if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
   if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
-  int S, span;
-  effective_splits(T, splits, &S, &span);
+  int S, span, t_split_end;
+  effective_splits(T, splits, knew != nullptr, &S, &span, &t_split_end);
   const WorkspaceLayout w = ws_layout(B, Hkv, S);
   if (!ws || ws_bytes < w.total)
     return fail(REC_EWORKSPACE, "workspace of %zu bytes is too small (%zu needed for %d splits)", ws_bytes, w.total, S);
@@ -119,7 +132,6 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   a.vz = vz;
   a.sinks = sinks;
   a.out = out;
-  a.counters = (int*)((char*)ws + w.counters);
   a.ws_stat = (float*)((char*)ws + w.stat);
   a.ws_acc = (float*)((char*)ws + w.acc);
   if (knew) {
@@ -135,6 +147,7 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   a.cap = cap;
   a.S = S;
   a.span = span;
+  a.t_split_end = t_split_end;
   return launched(launch_decode(k_bits, v_bits, a, (hipStream_t)stream), "decode launch");
 }
 
@@ -156,7 +169,7 @@ int rec_kv_append(const void* k_new, const void* v_new, int in_dtype, int64_t k_
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
   if (B < 1 || Hkv < 1 || L < 0) return fail(REC_EINVAL, "bad shape B=%d Hkv=%d L=%d", B, Hkv, L);
   if (offset < 0) return fail(REC_EINVAL, "negative offset");
-  if (capacity % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 64", (long long)capacity);
+  if (capacity % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 32", (long long)capacity);
   if (offset + L > capacity)
     return fail(REC_ECAPACITY, "appending %d tokens at %lld exceeds the capacity %lld", L, (long long)offset,
                 (long long)capacity);
@@ -189,7 +202,7 @@ int rec_decode_default_splits(int B, int Hkv, int64_t T) {
   const int64_t target = 512;
   const int64_t bh = (int64_t)(B < 1 ? 1 : B) * (Hkv < 1 ? 1 : Hkv);
   int64_t s = (target + bh - 1) / bh;
-  const int64_t chunks = (T + BLOCK_T - 1) / BLOCK_T;
+  const int64_t chunks = (T + CHUNK - 1) / CHUNK;
   if (s > chunks) s = chunks;
   if (s > DECODE_MAX_SPLITS) s = DECODE_MAX_SPLITS;
   return (int)(s < 1 ? 1 : s);

@@ -1,16 +1,17 @@
 // Shared device helpers for the gfx950 quantized-KV attention kernels.
 //
-// Cache formats (per layer; bh = b * Hkv + h; C = capacity, a multiple of 64):
-//   int8 K codes   int8  [B][Hkv][C][128]            row-major per token
-//   int8 V codes   int8  [B][Hkv][C/64][128][64]     token-blocked: per 64-token
-//                                                    block, dim-major, tokens contiguous
-//   int8 scales    fp16  [B][Hkv][C]                 one per (token, head), K and V
-//   int4 K codes   uint8 [B][Hkv][C][64]             row-major, low nibble = even dim
-//   int4 V codes   uint8 [B][Hkv][C/64][128][32]     token-blocked, byte j of a dim
-//                                                    holds tokens 2j (low), 2j+1 (high)
-//   int4 scale/zp  fp16  [B][Hkv][C/64][4][64]       per 32-dim group, token-blocked
-// The blocked layouts let one 16-byte load hand a lane the 16 consecutive
-// tokens of one dim that the P·V matrix-core operand needs.
+// Cache layout per layer, in 32-token blocks (bh = b * Hkv + h, C = capacity,
+// a multiple of 32, blk = t / 32, t' = t % 32, p = pi(t') the position of
+// token t' inside its block, see block_pos()):
+//   int8 K codes   int8  [B][Hkv][C/32][2][32][64]   half m holds dims 64m..64m+63 of token t'
+//   int4 K codes   uint8 [B][Hkv][C/32][2][32][32]   half m packed, low nibble = even dim
+//   int8 V codes   int8  [B][Hkv][C/32][128][32]     dim-major, token t' at position p
+//   int4 V codes   uint8 [B][Hkv][C/32][128][16]     position p in byte p/2, low nibble = even p
+//   int8 scales    fp16  [B][Hkv][C/32][32]          one per (token, head), K and V, position p
+//   int4 scale/zp  fp16  [B][Hkv][C/32][4][32]       per 32-dim group, position p
+// Every load of the decode kernel reads one contiguous span: a Q·Kᵀ operand
+// is 16 tokens x 64 bytes of one K half, a P·V operand 16 dims x 32 tokens,
+// and a lane's eight scales are 16 adjacent bytes.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -28,12 +29,19 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int HEAD_DIM = 128;
-constexpr int BLOCK_T = 64;      // tokens per V block and per wave iteration
+constexpr int BLOCK_T = 32;      // tokens per cache block and per wave iteration
 constexpr int GROUP4 = 32;       // int4 group size along head_dim
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float NEG_INF = -__builtin_huge_valf();
 
 enum InDtype { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
+
+// Position of token t (0..31) inside its 32-token block.  The Q·Kᵀ MFMA
+// leaves lane group kg (0..3) holding the scores of tokens 16j + 4kg + i
+// (j = 0..1, i = 0..3); storing those eight at positions 8kg .. 8kg+7 lets the
+// lane read its V codes and scales with one load each.  Tokens t and t^1 stay
+// neighbours (positions p and p^1), so a uint4 byte never straddles blocks.
+__host__ __device__ constexpr int block_pos(int t) { return ((t >> 2) & 3) * 8 + (t >> 4) * 4 + (t & 3); }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
   _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);

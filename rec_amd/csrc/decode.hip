@@ -10,9 +10,12 @@
 //   * the append-then-attend order of Attention.__call__ (model.py:177-190),
 //     fused here: the split that owns the newest token quantizes it first.
 //
+// Each workgroup writes one partial (m, l, acc) per query head; a second
+// kernel merges the splits, one workgroup per query head.
+//
 // Work decomposition.  Grid (splits, Hkv, B), 256 threads = 4 wavefronts.  A
 // workgroup owns one KV head and a contiguous token range; its waves take
-// 64-token chunks in turn.  All G <= 8 query heads of the KV head share every
+// 64-token chunks in turn, loading chunk i+1 while computing chunk i.  All G <= 8 query heads of the KV head share every
 // K/V byte loaded (GQA), so a K/V byte is read from HBM exactly once.
 //
 // Q·Kᵀ runs on v_mfma_i32_16x16x64_i8: the A operand is 16 cache rows of int8
@@ -43,15 +46,12 @@ constexpr int WAVES = 4;
 constexpr float Q16 = 32512.0f;  // int16 query range: hi, lo stay inside int8
 
 // LDS layout (bytes)
-constexpr int LDS_QOP = 0;                         // up to 4 operands x 64 lanes x 16 B
-constexpr int LDS_QSC = 4096;                      // 8 floats: per-head query scale
-constexpr int LDS_QSUM = LDS_QSC + 32;             // 8 x 4 ints: per-group query sums (int4 K)
-constexpr int LDS_FLAG = LDS_QSUM + 128;           // last-workgroup flag
-constexpr int LDS_PART = 4352;                     // wave partials: 4 x 8 x 128 floats
+constexpr int LDS_QOP = 0;                                 // up to 4 operands x 64 lanes x 16 B
+constexpr int LDS_QSC = 4096;                              // 8 floats: per-head query scale
+constexpr int LDS_QSUM = LDS_QSC + 32;                     // 8 x 4 ints: per-group query sums (int4 K)
+constexpr int LDS_PART = 4352;                             // wave partials: 4 x 8 x 128 floats
 constexpr int LDS_PSTAT = LDS_PART + WAVES * 8 * 128 * 4;  // 4 x 8 x (m, l)
-constexpr int LDS_FSTAT = LDS_PART;                // final merge: S x 8 x (w, l), reuses partials
 constexpr int LDS_BYTES = LDS_PSTAT + WAVES * 8 * 8;
-static_assert(MAX_SPLITS * 8 * 8 <= WAVES * 8 * 128 * 4 + WAVES * 8 * 8, "final stats must fit");
 
 // Order in which widen_u4() lays out 16 packed nibbles (8 bytes): unpacked byte
 // j holds element perm16(j) of the 16.
@@ -118,6 +118,200 @@ __device__ void prepare_query(const DecodeArgs& a, int b, int h, char* smem, int
   if ((tid & 31) == 0) qsc[hh] = amax / Q16;
 }
 
+// Tokens per compute chunk of one wave: one 32-token cache block.
+constexpr int CH = BLOCK_T;
+
+// Registers of one 32-token chunk as it arrives from HBM.  Members a format
+// does not use are never touched and vanish.
+struct Chunk {
+  v4i k8[2][2];   // int8 K: tile j, MFMA half m (16 bytes each)
+  v2i k4[2][2];   // int4 K: tile j, group pair (8 packed bytes each)
+  v4i ks;         // int8 K: scales of this lane's 8 tokens
+  v4i ks4[2];     // int4 K: scales, this lane's two groups
+  v4i kz4[2];     // int4 K: zero-points
+  v2i v8[8];      // int8 V: dim block n, this lane's 8 tokens
+  uint32_t v4[8]; // int4 V: dim block n, this lane's 8 tokens packed
+  v4i vs;         // int8 V: scales of this lane's 8 tokens
+  v4i vs4[4];     // int4 V: scales, all four groups
+  v4i vz4[4];     // int4 V: zero-points
+};
+
+struct Bases {
+  const int8_t* k;     // this (b, h) slice of the K codes
+  const int8_t* v;     // this (b, h) slice of the V codes
+  const uint16_t* ks;  // K scales (int8: per token; int4: blocked per group)
+  const uint16_t* kz;
+  const uint16_t* vs;
+  const uint16_t* vz;
+};
+
+__device__ __forceinline__ float half_at(const v4i& w, int idx) {
+  const uint32_t x = (uint32_t)w[idx >> 1];
+  return half_bits_to_float((idx & 1) ? (x >> 16) : (x & 0xffff));
+}
+
+template <class T>
+__device__ __forceinline__ T ld_nt(const void* p) {
+  return __builtin_nontemporal_load((const T*)p);
+}
+
+// Issue every load of the chunk (cache block) starting at token t0, a
+// multiple of 32.  The KV cache is streamed once, so the loads are nontemporal.
+template <int KB, int VB>
+__device__ __forceinline__ void load_chunk(Chunk& R, const Bases& B, int t0, int lane) {
+  const int c = lane & 15, kg = lane >> 4;
+  const int blk = t0 >> 5;
+  // Q·Kᵀ tile j, row r is token 16j + r of the block; the MFMA leaves lane
+  // (c, kg) holding the scores of tokens 16j + 4kg + i, i.e. block positions
+  // 8kg .. 8kg+7 in the order idx = 4j + i.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if constexpr (KB == 8) {
+      const int8_t* p = B.k + blk * 4096 + (16 * j + c) * 64 + 16 * kg;
+      R.k8[j][0] = ld_nt<v4i>(p);
+      R.k8[j][1] = ld_nt<v4i>(p + 2048);
+    } else {
+      const int8_t* p = B.k + blk * 2048 + (16 * j + c) * 32 + 8 * kg;
+      R.k4[j][0] = ld_nt<v2i>(p);
+      R.k4[j][1] = ld_nt<v2i>(p + 1024);
+    }
+  }
+  if constexpr (KB == 8) {
+    R.ks = ld_nt<v4i>(B.ks + blk * 32 + 8 * kg);
+  } else {
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int off = blk * 128 + (2 * gi + (c >> 3)) * 32 + 8 * kg;
+      R.ks4[gi] = ld_nt<v4i>(B.ks + off);
+      R.kz4[gi] = ld_nt<v4i>(B.kz + off);
+    }
+  }
+  // V block n: lane (c, kg) gets dim 16n+c at block positions 8kg .. 8kg+7
+  if constexpr (VB == 8) {
+    const int8_t* p = B.v + blk * 4096 + c * 32 + 8 * kg;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) R.v8[n] = ld_nt<v2i>(p + n * 512);
+    R.vs = ld_nt<v4i>(B.vs + blk * 32 + 8 * kg);
+  } else {
+    const int8_t* p = B.v + blk * 2048 + c * 16 + 4 * kg;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) R.v4[n] = ld_nt<uint32_t>(p + n * 256);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int off = blk * 128 + g * 32 + 8 * kg;
+      R.vs4[g] = ld_nt<v4i>(B.vs + off);
+      R.vz4[g] = ld_nt<v4i>(B.vz + off);
+    }
+  }
+}
+
+struct State {
+  float m, l;     // running max (log2 domain) and sum of this lane's head
+  v4f acc[8];     // P·V accumulators: dims 16n + 4kg + i of head c
+  float corr[4];  // int4 V: Σ P'·z per group
+};
+
+template <int KB, int VB>
+__device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, int qsum_a,
+                                              int qsum_b, int valid, int lane) {
+  const int c = lane & 15, kg = lane >> 4;
+  // ---------------- scores (log2 domain) ----------------
+  float s[8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if constexpr (KB == 8) {
+      v4i d = {0, 0, 0, 0};
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(R.k8[j][0], qop[0], d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(R.k8[j][1], qop[1], d, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mine = d[i], partner = dpp_ror8(mine);
+        const int full = c < 8 ? mine * 256 + partner : partner * 256 + mine;
+        s[4 * j + i] = (float)full * (half_at(R.ks, 4 * j + i) * qsc);
+      }
+    } else {
+      const v4i ka = widen_u4(R.k4[j][0]), kb = widen_u4(R.k4[j][1]);
+      v4i dah = {0, 0, 0, 0}, dal = {0, 0, 0, 0}, dbh = {0, 0, 0, 0}, dbl = {0, 0, 0, 0};
+      dah = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qop[0], dah, 0, 0, 0);
+      dal = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qop[1], dal, 0, 0, 0);
+      dbh = __builtin_amdgcn_mfma_i32_16x16x64_i8(kb, qop[2], dbh, 0, 0, 0);
+      dbl = __builtin_amdgcn_mfma_i32_16x16x64_i8(kb, qop[3], dbl, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int idx = 4 * j + i;
+        const int ta = dah[i] * 256 + dal[i] - (int)half_at(R.kz4[0], idx) * qsum_a;
+        const int tb = dbh[i] * 256 + dbl[i] - (int)half_at(R.kz4[1], idx) * qsum_b;
+        const float part = half_at(R.ks4[0], idx) * (float)ta + half_at(R.ks4[1], idx) * (float)tb;
+        s[idx] = (part + dpp_ror8f(part)) * qsc;
+      }
+    }
+  }
+  if (valid < CH) {  // tail chunk: tokens past the split end
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx)
+      if (16 * (idx >> 2) + 4 * kg + (idx & 3) >= valid) s[idx] = NEG_INF;
+  }
+
+  // ---------------- online softmax ----------------
+  float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
+  cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
+  const float m_new = fmaxf(st.m, cmax);
+  if (__ballot(m_new > st.m)) {  // some head's max moved: rescale (rare after warm-up)
+    const float factor = __builtin_amdgcn_exp2f(st.m - m_new);
+    st.l *= factor;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) st.acc[n] *= factor;
+    if constexpr (VB == 4) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) st.corr[g] *= factor;
+    }
+    st.m = m_new;
+  }
+  float p[8];
+#pragma unroll
+  for (int idx = 0; idx < 8; ++idx) {
+    p[idx] = __builtin_amdgcn_exp2f(s[idx] - st.m);
+    st.l += p[idx];
+  }
+
+  // ---------------- P·V ----------------
+  if constexpr (VB == 8) {
+    v8h pb;
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) pb[idx] = (_Float16)(p[idx] * half_at(R.vs, idx));
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const v8h a0 = i8x8_to_h8((uint32_t)R.v8[n][0], (uint32_t)R.v8[n][1]);
+      st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb, st.acc[n], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      v8h pb;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int idx = (k >> 1) + 4 * (k & 1);  // order of u4x8_to_h8_interleaved
+        const _Float16 ph = (_Float16)(p[idx] * half_at(R.vs4[g], idx));
+        pb[k] = ph;
+        st.corr[g] += (float)ph * half_at(R.vz4[g], idx);
+      }
+#pragma unroll
+      for (int nn = 0; nn < 2; ++nn) {
+        const int n = 2 * g + nn;
+        st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u4x8_to_h8_interleaved(R.v4[n]), pb, st.acc[n], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Chunks in flight per wave: three for the int8 formats, two when int4
+// scale/zero-point registers make a chunk larger.
+template <int KB, int VB>
+struct Depth {
+  static constexpr int value = (KB == 8 && VB == 8) ? 3 : 2;
+};
+
 template <int KB, int VB>
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
@@ -126,11 +320,27 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * a.Hkv + h;
   const int64_t cap = a.cap;
-  const int64_t t_begin = (int64_t)split * a.span;
-  const int64_t t_end = t_begin + a.span < a.T ? t_begin + a.span : a.T;
+  const bool fused = a.knew.p != nullptr;
+  const bool tail = fused && split == a.S - 1;  // the split that owns the newest token
+  int t_begin, t_end;
+  if (tail) {
+    t_begin = a.t_split_end;
+    t_end = (int)a.T;
+  } else {
+    t_begin = split * a.span;
+    t_end = t_begin + a.span < a.t_split_end ? t_begin + a.span : a.t_split_end;
+  }
 
-  // Fused append of the newest token (position T-1) by the split that owns it.
-  if (a.knew.p != nullptr && split == a.S - 1) {
+  Bases B;
+  B.k = (const int8_t*)a.kq + bh * cap * (KB == 8 ? HEAD_DIM : HEAD_DIM / 2);
+  B.v = (const int8_t*)a.vq + bh * cap * (VB == 8 ? HEAD_DIM : HEAD_DIM / 2);
+  B.ks = a.ks + bh * cap * (KB == 8 ? 1 : 4);
+  B.kz = KB == 4 ? a.kz + bh * cap * 4 : nullptr;
+  B.vs = a.vs + bh * cap * (VB == 8 ? 1 : 4);
+  B.vz = VB == 4 ? a.vz + bh * cap * 4 : nullptr;
+
+  // Fused append of the newest token (position T-1), before this split reads it.
+  if (tail) {
     const int64_t pos = a.T - 1;
     if (wave == 0) {
       append_row<KB>(a.knew, b, h, 0, 0, (void*)a.kq, (uint16_t*)a.ks, (uint16_t*)a.kz, bh, cap, pos, lane);
@@ -144,12 +354,22 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       }
     }
     __threadfence_block();
+    __syncthreads();
   }
+
+  // Start streaming before the query is prepared: the first chunks' loads
+  // overlap the query load and quantization.
+  constexpr int NBUF = Depth<KB, VB>::value;
+  constexpr int STEP = WAVES * CH;
+  Chunk buf[NBUF];
+  int t = t_begin + wave * CH;
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i)
+    if (t + i * STEP < t_end) load_chunk<KB, VB>(buf[i], B, t + i * STEP, lane);
 
   prepare_query<KB>(a, b, h, smem, tid);
   __syncthreads();
 
-  // Per-lane query operands and constants.
   constexpr int NOP = KB == 8 ? 2 : 4;
   v4i qop[NOP];
 #pragma unroll
@@ -162,206 +382,40 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     qsum_b = qsum[(c & 7) * 4 + 2 + (c >> 3)];
   }
 
-  float m_run = NEG_INF, l_run = 0.f;
-  v4f acc[8];
+  State st;
+  st.m = NEG_INF;
+  st.l = 0.f;
 #pragma unroll
-  for (int n = 0; n < 8; ++n) acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
-  float corr[4] = {0.f, 0.f, 0.f, 0.f};  // int4 V: Σ P'·z per group
+  for (int n = 0; n < 8; ++n) st.acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int g = 0; g < 4; ++g) st.corr[g] = 0.f;
 
-  const int r = lane & 15;  // A-operand row of the Q·Kᵀ tiles
-  for (int64_t t0 = t_begin + (int64_t)wave * BLOCK_T; t0 < t_end; t0 += WAVES * BLOCK_T) {
-    // ---------------- loads ----------------
-    // Q·Kᵀ tile j, row r holds token 16*(r>>2) + 4*j + (r&3) of the chunk, so
-    // after four tiles lane (c, kg) holds the scores of tokens 16*kg .. 16*kg+15.
-    v4i ka[4][2];
-    if constexpr (KB == 8) {
-      const int8_t* kbase = (const int8_t*)a.kq + (bh * cap + t0) * HEAD_DIM + 16 * kg;
+  // Ring of NBUF chunk buffers, unrolled so every buffer index is static:
+  // while buffer i is consumed, the loads of the chunk NBUF-1 ahead are in flight.
+  bool more = t < t_end;
+  while (more) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tok = 16 * (r >> 2) + 4 * j + (r & 3);
-        ka[j][0] = *(const v4i*)(kbase + tok * HEAD_DIM);
-        ka[j][1] = *(const v4i*)(kbase + tok * HEAD_DIM + 64);
-      }
-    } else {
-      const uint8_t* kbase = (const uint8_t*)a.kq + (bh * cap + t0) * (HEAD_DIM / 2) + 8 * kg;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tok = 16 * (r >> 2) + 4 * j + (r & 3);
-        ka[j][0] = widen_u4(*(const v2i*)(kbase + tok * (HEAD_DIM / 2)));
-        ka[j][1] = widen_u4(*(const v2i*)(kbase + tok * (HEAD_DIM / 2) + 32));
-      }
-    }
-    // row scales of this lane's 16 tokens
-    v4i ksr[2], kzr[2][2], ksr4[2][2];
-    if constexpr (KB == 8) {
-      const v4i* p = (const v4i*)(a.ks + bh * cap + t0 + 16 * kg);
-      ksr[0] = p[0];
-      ksr[1] = p[1];
-    } else {
-#pragma unroll
-      for (int gi = 0; gi < 2; ++gi) {
-        const int g = 2 * gi + (c >> 3);
-        const int64_t off = bh * cap * 4 + (t0 >> 6) * (4 * BLOCK_T) + g * BLOCK_T + 16 * kg;
-        ksr4[gi][0] = ((const v4i*)(a.ks + off))[0];
-        ksr4[gi][1] = ((const v4i*)(a.ks + off))[1];
-        kzr[gi][0] = ((const v4i*)(a.kz + off))[0];
-        kzr[gi][1] = ((const v4i*)(a.kz + off))[1];
-      }
-    }
-    // V: block n covers dims 16n..16n+15; lane (c, kg) gets dim 16n+c, tokens 16kg..16kg+15
-    v4i va[8];
-    v2i va4[8];
-    if constexpr (VB == 8) {
-      const int8_t* vbase = (const int8_t*)a.vq + bh * cap * HEAD_DIM + (t0 >> 6) * (BLOCK_T * HEAD_DIM) + c * BLOCK_T + 16 * kg;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) va[n] = *(const v4i*)(vbase + n * 16 * BLOCK_T);
-    } else {
-      const uint8_t* vbase = (const uint8_t*)a.vq + bh * cap * (HEAD_DIM / 2) + (t0 >> 6) * (BLOCK_T * HEAD_DIM / 2) +
-                             c * (BLOCK_T / 2) + 8 * kg;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) va4[n] = *(const v2i*)(vbase + n * 16 * (BLOCK_T / 2));
-    }
-    v4i vsr[2], vsr4[4][2], vzr4[4][2];
-    if constexpr (VB == 8) {
-      const v4i* p = (const v4i*)(a.vs + bh * cap + t0 + 16 * kg);
-      vsr[0] = p[0];
-      vsr[1] = p[1];
-    } else {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t off = bh * cap * 4 + (t0 >> 6) * (4 * BLOCK_T) + g * BLOCK_T + 16 * kg;
-        vsr4[g][0] = ((const v4i*)(a.vs + off))[0];
-        vsr4[g][1] = ((const v4i*)(a.vs + off))[1];
-        vzr4[g][0] = ((const v4i*)(a.vz + off))[0];
-        vzr4[g][1] = ((const v4i*)(a.vz + off))[1];
-      }
-    }
-
-    // ---------------- scores ----------------
-    float s[16];
-    if constexpr (KB == 8) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v4i d = {0, 0, 0, 0};
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[j][0], qop[0], d, 0, 0, 0);
-        d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[j][1], qop[1], d, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int mine = d[i], partner = dpp_ror8(mine);
-          const int full = c < 8 ? mine * 256 + partner : partner * 256 + mine;
-          const int idx = 4 * j + i;
-          const uint32_t sw = (uint32_t)ksr[idx >> 3][(idx & 7) >> 1];
-          const float ksf = half_bits_to_float((idx & 1) ? (sw >> 16) : (sw & 0xffff));
-          s[idx] = (float)full * (ksf * qsc);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v4i dah = {0, 0, 0, 0}, dal = {0, 0, 0, 0}, dbh = {0, 0, 0, 0}, dbl = {0, 0, 0, 0};
-        dah = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[j][0], qop[0], dah, 0, 0, 0);
-        dal = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[j][0], qop[1], dal, 0, 0, 0);
-        dbh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[j][1], qop[2], dbh, 0, 0, 0);
-        dbl = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[j][1], qop[3], dbl, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int idx = 4 * j + i;
-          const int sh = (idx & 1) ? 16 : 0;
-          const float sa = half_bits_to_float(((uint32_t)ksr4[0][idx >> 3][(idx & 7) >> 1] >> sh) & 0xffff);
-          const float za = half_bits_to_float(((uint32_t)kzr[0][idx >> 3][(idx & 7) >> 1] >> sh) & 0xffff);
-          const float sb = half_bits_to_float(((uint32_t)ksr4[1][idx >> 3][(idx & 7) >> 1] >> sh) & 0xffff);
-          const float zb = half_bits_to_float(((uint32_t)kzr[1][idx >> 3][(idx & 7) >> 1] >> sh) & 0xffff);
-          const int ta = dah[i] * 256 + dal[i] - (int)za * qsum_a;
-          const int tb = dbh[i] * 256 + dbl[i] - (int)zb * qsum_b;
-          const float part = sa * (float)ta + sb * (float)tb;
-          s[idx] = (part + dpp_ror8f(part)) * qsc;
-        }
-      }
-    }
-    // tokens past the split end
-#pragma unroll
-    for (int idx = 0; idx < 16; ++idx)
-      if (t0 + 16 * kg + idx >= t_end) s[idx] = NEG_INF;
-
-    // ---------------- online softmax ----------------
-    float cmax = s[0];
-#pragma unroll
-    for (int idx = 1; idx < 16; ++idx) cmax = fmaxf(cmax, s[idx]);
-    cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
-    cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
-    const float m_new = fmaxf(m_run, cmax);
-    const float m_use = m_new == NEG_INF ? 0.f : m_new;
-    const float factor = exp2f(m_run - m_use);
-    float p[16], psum = 0.f;
-#pragma unroll
-    for (int idx = 0; idx < 16; ++idx) {
-      p[idx] = exp2f(s[idx] - m_use);
-      psum += p[idx];
-    }
-    l_run = l_run * factor + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) acc[n] *= factor;
-
-    // ---------------- P·V ----------------
-    if constexpr (VB == 8) {
-      v8h pb[2];
-#pragma unroll
-      for (int idx = 0; idx < 16; ++idx) {
-        const uint32_t sw = (uint32_t)vsr[idx >> 3][(idx & 7) >> 1];
-        const float vsf = half_bits_to_float((idx & 1) ? (sw >> 16) : (sw & 0xffff));
-        pb[idx >> 3][idx & 7] = (_Float16)(p[idx] * vsf);
-      }
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const v8h a0 = i8x8_to_h8((uint32_t)va[n][0], (uint32_t)va[n][1]);
-        const v8h a1 = i8x8_to_h8((uint32_t)va[n][2], (uint32_t)va[n][3]);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb[0], acc[n], 0, 0, 0);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pb[1], acc[n], 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) corr[g] *= factor;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        v8h pb[2];
-#pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const int e = (k >> 1) + 4 * (k & 1);  // interleaved order of u4x8_to_h8_interleaved
-            const int idx = 8 * qq + e;
-            const int sh = (idx & 1) ? 16 : 0;
-            const float vsf = half_bits_to_float(((uint32_t)vsr4[g][idx >> 3][(idx & 7) >> 1] >> sh) & 0xffff);
-            const float vzf = half_bits_to_float(((uint32_t)vzr4[g][idx >> 3][(idx & 7) >> 1] >> sh) & 0xffff);
-            const _Float16 ph = (_Float16)(p[idx] * vsf);
-            pb[qq][k] = ph;
-            corr[g] += (float)ph * vzf;
-          }
-        }
-#pragma unroll
-        for (int nn = 0; nn < 2; ++nn) {
-          const int n = 2 * g + nn;
-          const v8h a0 = u4x8_to_h8_interleaved((uint32_t)va4[n][0]);
-          const v8h a1 = u4x8_to_h8_interleaved((uint32_t)va4[n][1]);
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb[0], acc[n], 0, 0, 0);
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pb[1], acc[n], 0, 0, 0);
-        }
+    for (int i = 0; i < NBUF; ++i) {
+      if (more) {
+        const int ahead = t + (NBUF - 1) * STEP;
+        if (ahead < t_end) load_chunk<KB, VB>(buf[(i + NBUF - 1) % NBUF], B, ahead, lane);
+        process_chunk<KB, VB>(buf[i], st, qop, qsc, qsum_a, qsum_b, t_end - t, lane);
+        t += STEP;
+        more = t < t_end;
       }
     }
   }
 
   // ---------------- wave partial -> LDS ----------------
-  l_run += shfl_xor_f(l_run, 16);
-  l_run += shfl_xor_f(l_run, 32);
+  st.l += shfl_xor_f(st.l, 16);
+  st.l += shfl_xor_f(st.l, 32);
   if constexpr (VB == 4) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      corr[g] += shfl_xor_f(corr[g], 16);
-      corr[g] += shfl_xor_f(corr[g], 32);
+      st.corr[g] += shfl_xor_f(st.corr[g], 16);
+      st.corr[g] += shfl_xor_f(st.corr[g], 32);
     }
   }
-  __syncthreads();  // query operands are no longer read; partial region is free
   float* part = (float*)(smem + LDS_PART);
   float* pstat = (float*)(smem + LDS_PSTAT);
   if (c < 8 && c < a.G) {
@@ -369,18 +423,18 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     for (int n = 0; n < 8; ++n)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v = acc[n][i];
-        if constexpr (VB == 4) v -= corr[n >> 1];
+        float v = st.acc[n][i];
+        if constexpr (VB == 4) v -= st.corr[n >> 1];
         part[(wave * 8 + c) * HEAD_DIM + 16 * n + 4 * kg + i] = v;
       }
     if (kg == 0) {
-      pstat[(wave * 8 + c) * 2 + 0] = m_run;
-      pstat[(wave * 8 + c) * 2 + 1] = l_run;
+      pstat[(wave * 8 + c) * 2 + 0] = st.m;
+      pstat[(wave * 8 + c) * 2 + 1] = st.l;
     }
   }
   __syncthreads();
 
-  // ---------------- workgroup partial -> workspace ----------------
+  // ---------------- workgroup partial (or the output when S == 1) ----------------
   const int hh = tid >> 5, d0 = (tid & 31) * 4;
   if (hh < a.G) {
     float mw[WAVES], M = NEG_INF;
@@ -389,70 +443,90 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       mw[w] = pstat[(w * 8 + hh) * 2];
       M = fmaxf(M, mw[w]);
     }
+    float sink = NEG_INF;
+    if (a.S == 1 && a.sinks != nullptr) {
+      sink = a.sinks[h * a.G + hh] * LOG2E;
+      M = fmaxf(M, sink);
+    }
     v4f acc4 = {0.f, 0.f, 0.f, 0.f};
     float l = 0.f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
-      const float f = mw[w] == NEG_INF ? 0.f : exp2f(mw[w] - M);
+      const float f = (mw[w] == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
       acc4 += f * *(const v4f*)(part + (w * 8 + hh) * HEAD_DIM + d0);
       l += f * pstat[(w * 8 + hh) * 2 + 1];
     }
-    const int64_t row = (bh * a.S + split) * 8 + hh;
-    *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = acc4;
-    if ((tid & 31) == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){M, l};
+    if (a.S == 1) {
+      if (sink != NEG_INF) l += __builtin_amdgcn_exp2f(sink - M);
+      const v4f o = l > 0.f ? acc4 / l : acc4;
+      *(v4f*)(a.out + ((int64_t)b * a.Hq + h * a.G + hh) * HEAD_DIM + d0) = o;
+    } else {
+      const int64_t row = (bh * a.S + split) * 8 + hh;
+      *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = acc4;
+      if ((tid & 31) == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){M, l};
+    }
   }
+}
 
-  // ---------------- last workgroup of this KV head merges ----------------
-  __threadfence();
-  __syncthreads();
-  int* flag = (int*)(smem + LDS_FLAG);
-  if (tid == 0) flag[0] = atomicAdd(a.counters + bh, 1) == a.S - 1;
-  __syncthreads();
-  if (!flag[0]) return;
-  __threadfence();
-
-  float* fst = (float*)(smem + LDS_FSTAT);  // [S][8][2]: (m, l), then (weight, l)
-  for (int i = tid; i < a.S * 8; i += 256) *(v2f*)(fst + 2 * i) = ((const v2f*)(a.ws_stat + bh * a.S * 16))[i];
-  __syncthreads();
-  const int sub = tid & 31;
-  float lsum = 0.f;
-  if (hh < a.G) {
-    float M = NEG_INF;
-    for (int sp = sub; sp < a.S; sp += 32) M = fmaxf(M, fst[(sp * 8 + hh) * 2]);
+// Cross-split merge (megakernel.py:276-318): one workgroup per (query head,
+// batch).  Thread (sg, d4) sums splits sg, sg+8, ... for dims 4*d4..4*d4+3;
+// every partial load is issued before the first is used.
+__global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
+  __shared__ float red[8];
+  __shared__ float wts[MAX_SPLITS];
+  __shared__ v4f acc_part[8][32];
+  const int tid = threadIdx.x, d4 = tid & 31, sg = tid >> 5;
+  const int hq = blockIdx.x, b = blockIdx.y;
+  const int h = hq / a.G, hh = hq % a.G;
+  const int64_t bh = (int64_t)b * a.Hkv + h;
+  const int S = a.S;
+  constexpr int PER = MAX_SPLITS / 8;
+  v4f v[PER];
+  const float* src = a.ws_acc + ((bh * S) * 8 + hh) * HEAD_DIM + 4 * d4;
 #pragma unroll
-    for (int m = 1; m < 32; m <<= 1) M = fmaxf(M, __shfl_xor(M, m, 64));
-    float sink = NEG_INF;
-    if (a.sinks != nullptr) {
-      sink = a.sinks[h * a.G + hh] * LOG2E;
-      M = fmaxf(M, sink);
-    }
-    for (int sp = sub; sp < a.S; sp += 32) {
-      const float ms = fst[(sp * 8 + hh) * 2];
-      const float w = (ms == NEG_INF || M == NEG_INF) ? 0.f : exp2f(ms - M);
-      fst[(sp * 8 + hh) * 2] = w;
-      lsum += w * fst[(sp * 8 + hh) * 2 + 1];
-    }
-#pragma unroll
-    for (int m = 1; m < 32; m <<= 1) lsum += __shfl_xor(lsum, m, 64);
-    if (sink != NEG_INF) lsum += exp2f(sink - M);
+  for (int i = 0; i < PER; ++i) {
+    const int sp = sg + 8 * i;
+    v[i] = sp < S ? *(const v4f*)(src + (int64_t)sp * 8 * HEAD_DIM) : (v4f){0.f, 0.f, 0.f, 0.f};
   }
-  __syncthreads();
-  if (hh < a.G) {
-    v4f acc4 = {0.f, 0.f, 0.f, 0.f};
-    const float* src = a.ws_acc + (bh * a.S * 8 + hh) * HEAD_DIM + d0;
-    int sp = 0;
-    for (; sp + 8 <= a.S; sp += 8) {
-      v4f v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = *(const v4f*)(src + (int64_t)(sp + u) * 8 * HEAD_DIM);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc4 += fst[((sp + u) * 8 + hh) * 2] * v[u];
-    }
-    for (; sp < a.S; ++sp) acc4 += fst[(sp * 8 + hh) * 2] * *(const v4f*)(src + (int64_t)sp * 8 * HEAD_DIM);
-    const v4f o = lsum > 0.f ? acc4 / lsum : acc4;
-    *(v4f*)(a.out + ((int64_t)b * a.Hq + h * a.G + hh) * HEAD_DIM + d0) = o;
+  float ms = NEG_INF, ls = 0.f;
+  if (tid < S) {
+    const v2f st = *(const v2f*)(a.ws_stat + ((bh * S + tid) * 8 + hh) * 2);
+    ms = st[0];
+    ls = st[1];
   }
-  if (tid == 0) a.counters[bh] = 0;
+  float M = wave_max(ms);
+  if ((tid & 63) == 0) red[tid >> 6] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float sink = NEG_INF;
+  if (a.sinks != nullptr) {
+    sink = a.sinks[hq] * LOG2E;
+    M = fmaxf(M, sink);
+  }
+  const float w = (ms == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+  if (tid < MAX_SPLITS) wts[tid] = w;
+  float lw = w * ls;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) lw += __shfl_xor(lw, m, 64);
+  __syncthreads();
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = lw;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int sp = sg + 8 * i;
+    if (sp < S) acc += wts[sp] * v[i];
+  }
+  acc_part[sg][d4] = acc;
+  __syncthreads();
+  if (sg == 0) {
+    float L = red[4] + red[5] + red[6] + red[7];
+    if (sink != NEG_INF) L += __builtin_amdgcn_exp2f(sink - M);
+    v4f t = acc_part[0][d4];
+#pragma unroll
+    for (int g = 1; g < 8; ++g) t += acc_part[g][d4];
+    const v4f o = L > 0.f ? t / L : t;
+    *(v4f*)(a.out + ((int64_t)b * a.Hq + hq) * HEAD_DIM + 4 * d4) = o;
+  }
 }
 
 hipError_t launch_decode(int kb, int vb, const DecodeArgs& a, hipStream_t stream) {
@@ -461,6 +535,9 @@ hipError_t launch_decode(int kb, int vb, const DecodeArgs& a, hipStream_t stream
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((decode_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((decode_kernel<4, 8>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((decode_kernel<4, 4>), grid, block, 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.S == 1) return e;
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.Hq, a.B), block, 0, stream, a);
   return hipGetLastError();
 }
 

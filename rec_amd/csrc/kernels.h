@@ -33,13 +33,13 @@ struct DecodeArgs {
   float* out;          // [B][Hq][128] fp32
   float* ws_acc;       // [B*Hkv][S][8][128]
   float* ws_stat;      // [B*Hkv][S][8][2]
-  int* counters;       // [B*Hkv], zero between launches
   RowSrc knew, vnew;   // fused single-token append (knew.p null: none)
   float q_mul;         // softmax scale * log2(e)
   int B, Hq, Hkv, G;
   int64_t T, cap;
   int S;     // number of splits
-  int span;  // tokens per split (multiple of 64)
+  int span;         // tokens per regular split (multiple of 32)
+  int t_split_end;  // end of the regular splits; a fused append adds one split [t_split_end, T)
 };
 
 constexpr int DECODE_MAX_SPLITS = 256;

@@ -58,17 +58,33 @@ __device__ __forceinline__ void quantize_u4_pair(float x0, float x1, int& q0, in
   zbits = float_to_half_bits(z);
 }
 
-// Cache addressing (element offsets), see the layout table in common.h.
-__device__ __forceinline__ int64_t i8_row_off(int64_t bh, int64_t cap, int64_t t) { return (bh * cap + t) * HEAD_DIM; }
-__device__ __forceinline__ int64_t i8_blk_off(int64_t bh, int64_t cap, int64_t t, int d) {
-  return bh * cap * HEAD_DIM + (t >> 6) * (BLOCK_T * HEAD_DIM) + (int64_t)d * BLOCK_T + (t & 63);
+// Cache addressing in elements (bytes for codes), see the layout table in common.h.
+__device__ __forceinline__ int64_t blk_base(int64_t bh, int64_t cap, int64_t t, int block_elems) {
+  return (bh * (cap / BLOCK_T) + (t >> 5)) * block_elems;
 }
-__device__ __forceinline__ int64_t u4_row_off(int64_t bh, int64_t cap, int64_t t) { return (bh * cap + t) * (HEAD_DIM / 2); }
-__device__ __forceinline__ int64_t u4_blk_byte(int64_t bh, int64_t cap, int64_t t, int d) {
-  return bh * cap * (HEAD_DIM / 2) + (t >> 6) * (BLOCK_T * HEAD_DIM / 2) + (int64_t)d * (BLOCK_T / 2) + ((t & 63) >> 1);
+// int8 K: byte of dim d
+__device__ __forceinline__ int64_t k8_off(int64_t bh, int64_t cap, int64_t t, int d) {
+  return blk_base(bh, cap, t, 4096) + (d >> 6) * 2048 + (t & 31) * 64 + (d & 63);
 }
-__device__ __forceinline__ int64_t u4_scale_off(int64_t bh, int64_t cap, int64_t t, int g) {
-  return bh * cap * 4 + (t >> 6) * (4 * BLOCK_T) + g * BLOCK_T + (t & 63);
+// int4 K: byte holding dims d, d+1 (d even)
+__device__ __forceinline__ int64_t k4_off(int64_t bh, int64_t cap, int64_t t, int d) {
+  return blk_base(bh, cap, t, 2048) + (d >> 6) * 1024 + (t & 31) * 32 + ((d & 63) >> 1);
+}
+// int8 V: byte of dim d
+__device__ __forceinline__ int64_t v8_off(int64_t bh, int64_t cap, int64_t t, int d) {
+  return blk_base(bh, cap, t, 4096) + d * 32 + block_pos((int)(t & 31));
+}
+// int4 V: byte holding token t (and its neighbour t^1) of dim d
+__device__ __forceinline__ int64_t v4_off(int64_t bh, int64_t cap, int64_t t, int d) {
+  return blk_base(bh, cap, t, 2048) + d * 16 + (block_pos((int)(t & 31)) >> 1);
+}
+// per-token scale (int8)
+__device__ __forceinline__ int64_t s8_off(int64_t bh, int64_t cap, int64_t t) {
+  return blk_base(bh, cap, t, 32) + block_pos((int)(t & 31));
+}
+// per-(token, group) scale / zero-point (int4)
+__device__ __forceinline__ int64_t s4_off(int64_t bh, int64_t cap, int64_t t, int g) {
+  return blk_base(bh, cap, t, 128) + g * 32 + block_pos((int)(t & 31));
 }
 
 // Quantize row (b, h, t_src) of `src` and store it at cache position `pos`.
@@ -87,28 +103,28 @@ __device__ __forceinline__ void append_row(const RowSrc& src, int b, int h, int 
     quantize_i8_pair(x0, x1, q0, q1, sb);
     int8_t* c = (int8_t*)codes;
     if (kind == 0) {
-      uint16_t packed = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
-      ((uint16_t*)(c + i8_row_off(bh, cap, pos)))[lane] = packed;
+      *(uint16_t*)(c + k8_off(bh, cap, pos, 2 * lane)) = (uint16_t)((q0 & 0xff) | ((q1 & 0xff) << 8));
     } else {
-      c[i8_blk_off(bh, cap, pos, 2 * lane)] = (int8_t)q0;
-      c[i8_blk_off(bh, cap, pos, 2 * lane + 1)] = (int8_t)q1;
+      c[v8_off(bh, cap, pos, 2 * lane)] = (int8_t)q0;
+      c[v8_off(bh, cap, pos, 2 * lane + 1)] = (int8_t)q1;
     }
-    if (lane == 0) scales[bh * cap + pos] = sb;
+    if (lane == 0) scales[s8_off(bh, cap, pos)] = sb;
   } else {
     int q0, q1;
     uint16_t sb, zb;
     quantize_u4_pair(x0, x1, q0, q1, sb, zb);
-    ((uint8_t*)codes)[u4_row_off(bh, cap, pos) + lane] = (uint8_t)(q0 | (q1 << 4));
+    ((uint8_t*)codes)[k4_off(bh, cap, pos, 2 * lane)] = (uint8_t)(q0 | (q1 << 4));
     if ((lane & 15) == 0) {
       const int g = lane >> 4;
-      scales[u4_scale_off(bh, cap, pos, g)] = sb;
-      zeros[u4_scale_off(bh, cap, pos, g)] = zb;
+      scales[s4_off(bh, cap, pos, g)] = sb;
+      zeros[s4_off(bh, cap, pos, g)] = zb;
     }
   }
 }
 
-// uint4 V: the byte pair of cache positions (2p, 2p+1).  Rows whose flag is
-// false keep the nibble already in the cache; each byte is written once.
+// uint4 V: the byte shared by tokens (2p, 2p+1) (block positions p', p'^1 with
+// the even token in the low nibble).  Rows whose flag is false keep the nibble
+// already in the cache; each byte is written once.
 __device__ __forceinline__ void append_v4_pair(const RowSrc& src, int b, int h, int t_even, bool has_even,
                                                bool has_odd, uint8_t* codes, uint16_t* scales, uint16_t* zeros,
                                                int64_t bh, int64_t cap, int64_t pos_even, int lane) {
@@ -126,12 +142,12 @@ __device__ __forceinline__ void append_v4_pair(const RowSrc& src, int b, int h, 
     if (r == 0) { qe0 = q0; qe1 = q1; } else { qo0 = q0; qo1 = q1; }
     if ((lane & 15) == 0) {
       const int g = lane >> 4;
-      scales[u4_scale_off(bh, cap, pos_even + r, g)] = sb;
-      zeros[u4_scale_off(bh, cap, pos_even + r, g)] = zb;
+      scales[s4_off(bh, cap, pos_even + r, g)] = sb;
+      zeros[s4_off(bh, cap, pos_even + r, g)] = zb;
     }
   }
-  const int64_t a0 = u4_blk_byte(bh, cap, pos_even, 2 * lane);
-  const int64_t a1 = u4_blk_byte(bh, cap, pos_even, 2 * lane + 1);
+  const int64_t a0 = v4_off(bh, cap, pos_even, 2 * lane);
+  const int64_t a1 = v4_off(bh, cap, pos_even, 2 * lane + 1);
   uint8_t o0 = 0, o1 = 0;
   if (!(has_even && has_odd)) { o0 = codes[a0]; o1 = codes[a1]; }
   const int lo0 = has_even ? qe0 : (o0 & 15), hi0 = has_odd ? qo0 : (o0 >> 4);

@@ -10,57 +10,106 @@ import pytest
 import torch
 
 from rec_amd import MixedQuantizedKVCache, QuantizedKV, QuantizedKVCache, to_logical
-from rec_amd.cache import BLOCK, _alloc
+from rec_amd.cache import _alloc
 
 
-def _block_v8(codes_logical):
-    """Independent blocked layout for int8 V: [B][H][T/64][128][64]."""
-    B, H, T, D = codes_logical.shape
-    x = codes_logical.reshape(B, H, T // 64, 64, D).transpose(0, 1, 2, 4, 3)
-    return np.ascontiguousarray(x).reshape(B, H, T // 64, D * 64)
+def _pos(t):
+    # tokens 16j + 4kg + i of a 32-token block sit at positions 8kg + 4j + i
+    j, kg, i = t // 16, (t // 4) % 4, t % 4
+    return 8 * kg + 4 * j + i
 
 
-def _block_v4(q):
-    """uint4 V codes q[B][H][T][128] (0..15) -> [B][H][T/64][128][32] bytes."""
+def _store_k(logical, bits):
+    """Independent loop construction of the K code layout [nb][2][32][w]."""
+    B, H, T, W = logical.shape  # W = 128 (int8) or 64 packed bytes (int4)
+    w = W // 2
+    out = np.zeros((B, H, T // 32, 2 * 32 * w), logical.dtype)
+    for t in range(T):
+        for m in range(2):
+            out[:, :, t // 32, m * 32 * w + (t % 32) * w : m * 32 * w + (t % 32) * w + w] = logical[:, :, t, m * w : (m + 1) * w]
+    return out
+
+
+def _store_v8(logical):
+    B, H, T, D = logical.shape
+    out = np.zeros((B, H, T // 32, D * 32), np.int8)
+    for t in range(T):
+        for d in range(D):
+            out[:, :, t // 32, d * 32 + _pos(t % 32)] = logical[:, :, t, d]
+    return out
+
+
+def _store_v4(q):
+    """uint4 V codes q[B][H][T][128] (0..15) -> [nb][128][16] bytes."""
     B, H, T, D = q.shape
-    x = q.reshape(B, H, T // 64, 64, D).transpose(0, 1, 2, 4, 3)  # [.., d, t]
-    packed = x[..., 0::2] | (x[..., 1::2] << 4)
-    return np.ascontiguousarray(packed).reshape(B, H, T // 64, D * 32).astype(np.uint8)
+    out = np.zeros((B, H, T // 32, D * 16), np.uint8)
+    for t in range(T):
+        p = _pos(t % 32)
+        for d in range(D):
+            out[:, :, t // 32, d * 16 + p // 2] |= (q[:, :, t, d] << (4 * (p % 2))).astype(np.uint8)
+    return out
 
 
-def test_to_logical_int8_blocked_roundtrip():
+def _store_scales(logical, groups=None):
+    if groups is None:  # (B, H, T) -> (B, H, nb, 32)
+        B, H, T = logical.shape
+        out = np.zeros((B, H, T // 32, 32), logical.dtype)
+        for t in range(T):
+            out[:, :, t // 32, _pos(t % 32)] = logical[:, :, t]
+        return out
+    B, H, T, G = logical.shape
+    out = np.zeros((B, H, T // 32, G, 32), logical.dtype)
+    for t in range(T):
+        out[:, :, t // 32, :, _pos(t % 32)] = logical[:, :, t, :]
+    return out
+
+
+def test_block_pos_is_a_permutation_keeping_pairs():
+    from rec_amd.cache import block_pos
+
+    ps = [block_pos(t) for t in range(32)]
+    assert sorted(ps) == list(range(32))
+    assert all(ps[t] == _pos(t) for t in range(32))
+    assert all(block_pos(t ^ 1) == ps[t] ^ 1 for t in range(32))
+
+
+def test_to_logical_int8_roundtrip():
     rng = np.random.default_rng(0)
-    logical = rng.integers(-127, 128, size=(2, 3, 128, 128), dtype=np.int8)
-    blocked = torch.from_numpy(_block_v8(logical))
-    scales = torch.from_numpy(rng.standard_normal((2, 3, 128)).astype(np.float16))
-    kv = QuantizedKV(blocked, scales, None, 8, 100, True)
-    c, s, z = to_logical(kv)
-    np.testing.assert_array_equal(c.numpy(), logical[:, :, :100])
-    np.testing.assert_array_equal(s.numpy(), scales.numpy()[:, :, :100])
+    kl = rng.integers(-127, 128, size=(2, 3, 96, 128), dtype=np.int8)
+    vl = rng.integers(-127, 128, size=(2, 3, 96, 128), dtype=np.int8)
+    sl = rng.standard_normal((2, 3, 96)).astype(np.float16)
+    k = QuantizedKV(torch.from_numpy(_store_k(kl, 8)), torch.from_numpy(_store_scales(sl)), None, 8, 70, False)
+    v = QuantizedKV(torch.from_numpy(_store_v8(vl)), torch.from_numpy(_store_scales(sl)), None, 8, 70, True)
+    c, s, z = to_logical(k)
+    np.testing.assert_array_equal(c.numpy(), kl[:, :, :70])
+    np.testing.assert_array_equal(s.numpy(), sl[:, :, :70])
     assert z is None
+    c, s, _ = to_logical(v)
+    np.testing.assert_array_equal(c.numpy(), vl[:, :, :70])
 
 
-def test_to_logical_int4_blocked_roundtrip():
+def test_to_logical_int4_roundtrip():
     rng = np.random.default_rng(1)
-    q = rng.integers(0, 16, size=(1, 2, 192, 128), dtype=np.uint8)
-    blocked = torch.from_numpy(_block_v4(q))
-    sc = rng.standard_normal((1, 2, 3, 4, 64)).astype(np.float16)
-    zp = rng.integers(0, 16, size=(1, 2, 3, 4, 64)).astype(np.float16)
-    kv = QuantizedKV(blocked, torch.from_numpy(sc), torch.from_numpy(zp), 4, 150, True)
-    c, s, z = to_logical(kv)
-    expect = q[..., 0::2] | (q[..., 1::2] << 4)
-    np.testing.assert_array_equal(c.numpy(), expect[:, :, :150])
-    # scale of token t, group g lives at [t // 64][g][t % 64]
-    t, g = 130, 3
-    assert s.numpy()[0, 1, t, g] == sc[0, 1, t // 64, g, t % 64]
-    assert z.numpy()[0, 0, t, g] == zp[0, 0, t // 64, g, t % 64]
+    q = rng.integers(0, 16, size=(1, 2, 64, 128), dtype=np.uint8)
+    packed = q[..., 0::2] | (q[..., 1::2] << 4)
+    sc = rng.standard_normal((1, 2, 64, 4)).astype(np.float16)
+    zp = rng.integers(0, 16, size=(1, 2, 64, 4)).astype(np.float16)
+    k = QuantizedKV(torch.from_numpy(_store_k(packed, 4)), torch.from_numpy(_store_scales(sc, 4)),
+                    torch.from_numpy(_store_scales(zp, 4)), 4, 50, False)
+    v = QuantizedKV(torch.from_numpy(_store_v4(q)), torch.from_numpy(_store_scales(sc, 4)),
+                    torch.from_numpy(_store_scales(zp, 4)), 4, 50, True)
+    for kv in (k, v):
+        c, s, z = to_logical(kv)
+        np.testing.assert_array_equal(c.numpy(), packed[:, :, :50])
+        np.testing.assert_array_equal(s.numpy(), sc[:, :, :50])
+        np.testing.assert_array_equal(z.numpy(), zp[:, :, :50])
 
 
 def test_alloc_shapes():
     k = _alloc(1, 4, 256, 8, False, "cpu")
     v = _alloc(1, 4, 256, 4, True, "cpu")
-    assert k[0].shape == (1, 4, 256, 128) and k[1].shape == (1, 4, 256) and k[2] is None
-    assert v[0].shape == (1, 4, 4, 128 * 32) and v[1].shape == (1, 4, 4, 4, 64) and v[2].shape == v[1].shape
+    assert k[0].shape == (1, 4, 8, 32 * 128) and k[1].shape == (1, 4, 8, 32) and k[2] is None
+    assert v[0].shape == (1, 4, 8, 32 * 64) and v[1].shape == (1, 4, 8, 4, 32) and v[2].shape == v[1].shape
     assert QuantizedKV(*v, 4, 0, True).capacity == 256
     assert QuantizedKV(*k, 8, 0, False).capacity == 256
 
@@ -69,11 +118,11 @@ def test_growth_keeps_contents_and_step_rounding():
     c = QuantizedKVCache(32, 8, 4)
     c._reserve(1, 2, 5, "cpu")
     assert c.capacity == 256
-    c.keys[0][0, 1, 3] = 7
+    c.keys[0][0, 1, 3, 5] = 7
     c.values[1][0, 0, 0, 2, 5] = 1.5
     c._reserve(1, 2, 300, "cpu")
     assert c.capacity == 512
-    assert c.keys[0][0, 1, 3, 0] == 7
+    assert c.keys[0][0, 1, 3, 5] == 7
     assert c.values[1][0, 0, 0, 2, 5] == 1.5
     c._reserve(1, 2, 512, "cpu")
     assert c.capacity == 512
@@ -82,7 +131,7 @@ def test_growth_keeps_contents_and_step_rounding():
 def test_limits_and_invalidation():
     c = QuantizedKVCache(32, 8, 8, max_tokens=100)
     c._reserve(1, 1, 10, "cpu")
-    assert c.capacity == 128  # one allocation, rounded to 64-token blocks
+    assert c.capacity == 128  # one allocation, rounded to 32-token blocks
     with pytest.raises(ValueError, match="Decode context limit exhausted"):
         c._reserve(1, 1, 101, "cpu")
     c._usable = False
