@@ -14,11 +14,12 @@ independent cache instances totalling more than 1 GB (32 x 34 MB at 32K,
 and grows by one token per step it serves.
 
 Timing: W eager warm-up steps, then K steps captured in one HIP graph and
-replayed once between synchronisations (HIP events on the launch stream).
-Per-launch kernel time for the roofline comes from a separate pass with an
-event pair around every launch.  Algorithmic bytes per step are the K/V codes
-and scales of all T tokens read once, the query read, the fp32 output written
-and the appended token read and written.
+replayed once between synchronisations (HIP events on the launch stream).  A
+step is two launches: the fused append + attention kernel and the split
+merge.  For the roofline, K launches of the attention kernel alone
+(``rec_decode_partial``) are captured and timed the same way.  Algorithmic
+bytes per step are the K/V codes and scales of all T tokens read once, the
+query read, the fp32 output written and the appended token read and written.
 
 The CPU baseline times the oracle's split-K restatement (chunked
 dequantization, float32 attention with sinks, merge) on the host over a
@@ -44,6 +45,7 @@ METRIC = "decode-attn HBM GB/s (% of peak) and µs/step per layer at 32K and 252
 HQ, HKV, D = 32, 4, 128
 SCALE = 1.0 / np.sqrt(D)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_i8_32k_traffic.json")
+CALIB_BYTES = 256 << 20
 
 
 def log(msg):
@@ -54,10 +56,13 @@ def row_bytes(bits):
     return D + 2 if bits == 8 else D // 2 + 16  # codes + fp16 scale (+ zero-points)
 
 
-def step_bytes(T, B=1, k_bits=8, v_bits=8):
+def step_bytes(T, B=1, k_bits=8, v_bits=8, output=True):
+    """Algorithmic HBM bytes of one decode step over T tokens: K/V codes and
+    scales read once, query read, appended token read (fp16) and written
+    (codes + scale), fp32 output written (by the merge when output=False)."""
     kv = B * T * HKV * (row_bytes(k_bits) + row_bytes(v_bits))
     q = B * HQ * D * 2
-    out = B * HQ * D * 4
+    out = B * HQ * D * 4 if output else 0
     append = B * HKV * (2 * D * 2 + row_bytes(k_bits) + row_bytes(v_bits))
     return kv + q + out + append
 
@@ -100,8 +105,10 @@ class DecodeWorkload:
         self.step_T = []
         torch.cuda.synchronize()
 
-    def step(self, s):
-        """Launch one fused append+attend step on the current stream."""
+    def step(self, s, partial_only=False):
+        """Launch one decode step on the current stream: the fused
+        append+attention kernel and the split merge, or (partial_only) the
+        append+attention kernel alone, for timing that kernel by itself."""
         from rec_amd import _lib
 
         c = self.caches[s % self.R]
@@ -110,55 +117,55 @@ class DecodeWorkload:
         kc, ks, _ = c.keys
         vc, vs, _ = c.values
         stream = self.torch.cuda.current_stream().cuda_stream
-        rc = self.lib.rec_decode_append_attn(
+        fn = self.lib.rec_decode_partial if partial_only else self.lib.rec_decode_append_attn
+        rc = fn(
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1),
             8, kc.data_ptr(), ks.data_ptr(), None, 8, vc.data_ptr(), vs.data_ptr(), None,
             self.sinks.data_ptr(), SCALE, 1, HQ, HKV, D, T, c.capacity, self.splits,
             self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), stream,
         )
-        _lib.check(rc, "rec_decode_append_attn")
+        _lib.check(rc, "decode step")
         c.offset = T
         return T
 
 
-def run_decode(T, R, steps, warmup, kernel_steps, seed):
+def _replay_timed(torch, graph, n):
+    """Replay a captured graph once between synchronisations; ms per launch."""
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def run_decode(T, R, steps, warmup, seed):
     import torch
 
-    total = warmup + steps + kernel_steps
+    total = warmup + 2 * steps
     log(f"T={T}: building {R} cache instances")
     w = DecodeWorkload(T, R, total, seed)
     log(f"T={T}: warm-up {warmup} steps")
     for s in range(warmup):
         w.step(s)
     torch.cuda.synchronize()
-    # K timed steps in one graph, replayed once
-    graph = torch.cuda.CUDAGraph()
-    timed_T = []
-    with torch.cuda.graph(graph):
+    # K whole steps (attention kernel + merge kernel) in one graph
+    g_step, step_T = torch.cuda.CUDAGraph(), []
+    with torch.cuda.graph(g_step):
         for s in range(warmup, warmup + steps):
-            timed_T.append(w.step(s))
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = e0.elapsed_time(e1) / steps
-    log(f"T={T}: {steps} steps in {ms_per_step * steps:.3f} ms (host wall {wall * 1e3:.3f} ms)")
-    # per-launch kernel time
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(kernel_steps)]
-    kT = []
-    for i, s in enumerate(range(warmup + steps, total)):
-        evs[i][0].record()
-        kT.append(w.step(s))
-        evs[i][1].record()
-    torch.cuda.synchronize()
-    kms = np.array([a.elapsed_time(b) for a, b in evs])
-    bytes_step = float(np.mean([step_bytes(t) for t in timed_T]))
-    bytes_kernel = float(np.mean([step_bytes(t) for t in kT]))
+            step_T.append(w.step(s))
+    # K launches of the attention kernel alone, the dominant kernel
+    g_kern, kern_T = torch.cuda.CUDAGraph(), []
+    with torch.cuda.graph(g_kern):
+        for s in range(warmup + steps, total):
+            kern_T.append(w.step(s, partial_only=True))
+    ms_per_step = _replay_timed(torch, g_step, steps)
+    kernel_ms = _replay_timed(torch, g_kern, steps)
+    log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step; attention kernel {kernel_ms * 1e3:.2f} us")
+    bytes_step = float(np.mean([step_bytes(t) for t in step_T]))
+    bytes_kernel = float(np.mean([step_bytes(t, output=False) for t in kern_T]))
     res = dict(
         T=T,
         instances=R,
@@ -166,13 +173,12 @@ def run_decode(T, R, steps, warmup, kernel_steps, seed):
         us_per_step=ms_per_step * 1e3,
         bytes_per_step=bytes_step,
         gbs=bytes_step / (ms_per_step * 1e-3) / 1e9,
-        kernel_us_mean=float(kms.mean() * 1e3),
-        kernel_us_median=float(np.median(kms) * 1e3),
-        kernel_gbs=bytes_kernel / (float(kms.mean()) * 1e-3) / 1e9,
+        kernel_us=kernel_ms * 1e3,
+        kernel_gbs=bytes_kernel / (kernel_ms * 1e-3) / 1e9,
         bytes_per_launch=bytes_kernel,
         cache_bytes=sum(c.nbytes for c in w.caches),
     )
-    del graph, w
+    del g_step, g_kern, w
     torch.cuda.empty_cache()
     return res
 
@@ -243,12 +249,16 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--kernel-steps", type=int, default=64)
     ap.add_argument("--long-steps", type=int, default=0, help="timed steps at 252K (default steps/8)")
     ap.add_argument("--no-long", action="store_true", help="skip the 252K measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument(
+        "--calibrate",
+        action="store_true",
+        help="first run two plain 256 MiB device copies (a known-size kernel for hardware-counter scaling)",
+    )
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -268,14 +278,22 @@ def main(argv=None):
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     rec_amd.library()
     torch.cuda.set_device(0)
+    if args.calibrate:
+        src = torch.ones(CALIB_BYTES, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"calibration: 2 copies of {CALIB_BYTES} bytes")
 
-    r32 = run_decode(32768, 32, args.steps, args.warmup, args.kernel_steps, args.seed)
-    log(f"32K: {r32['us_per_step']:.2f} us/step, {r32['gbs']:.0f} GB/s; kernel {r32['kernel_us_mean']:.2f} us")
+    r32 = run_decode(32768, 32, args.steps, args.warmup, args.seed)
+    log(f"32K: {r32['us_per_step']:.2f} us/step, {r32['gbs']:.0f} GB/s; kernel {r32['kernel_us']:.2f} us")
     r252 = None
     if not args.no_long:
         ls = args.long_steps or max(16, args.steps // 8)
-        r252 = run_decode(258048, 4, ls, max(4, args.warmup // 4), max(16, args.kernel_steps // 2), args.seed + 99)
-        log(f"252K: {r252['us_per_step']:.2f} us/step, {r252['gbs']:.0f} GB/s; kernel {r252['kernel_us_mean']:.2f} us")
+        r252 = run_decode(258048, 4, ls, max(4, args.warmup // 4), args.seed + 99)
+        log(f"252K: {r252['us_per_step']:.2f} us/step, {r252['gbs']:.0f} GB/s; kernel {r252['kernel_us']:.2f} us")
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -323,10 +341,10 @@ def main(argv=None):
             "unit": "GB/s",
             "frac": round(r32["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "rec::decode_kernel<8, 8> (fused append + split-K decode + merge)",
-            "kernel_us_mean": round(r32["kernel_us_mean"], 3),
-            "kernel_us_median": round(r32["kernel_us_median"], 3),
+            "kernel": "rec::decode_kernel<8, 8> (fused append + split-K attention partials)",
+            "kernel_us": round(r32["kernel_us"], 3),
             "algorithmic_bytes_per_launch": r32["bytes_per_launch"],
+            "timing": "HIP events around one graph replay of K launches of the kernel",
         },
         "cpu_baseline": cpu,
     }
@@ -336,8 +354,9 @@ def main(argv=None):
             "us_per_step": round(r252["us_per_step"], 3),
             "gbs": round(r252["gbs"], 2),
             "frac_of_peak": round(r252["gbs"] / HBM_PEAK_GBS, 4),
-            "kernel_us_mean": round(r252["kernel_us_mean"], 3),
+            "kernel_us": round(r252["kernel_us"], 3),
             "kernel_gbs": round(r252["kernel_gbs"], 2),
+            "kernel_frac_of_peak": round(r252["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_step": r252["bytes_per_step"],
             "cache_instances": r252["instances"],
         }

@@ -94,9 +94,10 @@ int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
- * One decode step in one launch: quantize-append the single new token
- * k_new / v_new (B, Hkv, 1, D) at cache position T-1, then attend over all T
- * tokens, the new one included, as Attention.__call__ does
+ * One decode step: quantize-append the single new token k_new / v_new
+ * (B, Hkv, 1, D) at cache position T-1 and attend over all T tokens, the new
+ * one included, in one attention launch (plus the split merge), as
+ * Attention.__call__ does
  * (engine/src/rec_mlx/model.py:177-190: update_and_fetch, then
  * quantized_attention_with_sinks).
  */
@@ -108,6 +109,30 @@ int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                            const float* sinks, float scale,
                            int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
                            void* workspace, size_t workspace_bytes, float* out, void* stream);
+
+/*
+ * The two launches of a decode step, for callers that schedule them apart
+ * (for instance to time or overlap them).  rec_decode_partial takes the
+ * arguments of rec_decode_append_attn; k_new/v_new NULL means no append.  It
+ * writes `out` directly when the request resolves to a single split, else the
+ * split partials into the workspace.  rec_decode_merge then combines those
+ * partials into `out` (nothing to do for a single split); it must be given the
+ * B, Hq, Hkv, T, splits, sinks and workspace of the partial call, and
+ * appended = 1 if that call appended a token.
+ * Together they are rec_decode_append_attn: the split-K partial of
+ * engine/src/rec_mlx/kernels/megakernel.py:619-693 and its merge :276-318.
+ */
+int rec_decode_partial(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                       const void* k_new, const void* v_new, int new_dtype,
+                       int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
+                       int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros,
+                       int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
+                       const float* sinks, float scale,
+                       int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
+                       void* workspace, size_t workspace_bytes, float* out, void* stream);
+
+int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int splits, int appended,
+                     void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -51,6 +51,8 @@ SIGNATURES = {
         ],
     ),
 }
+SIGNATURES["rec_decode_partial"] = SIGNATURES["rec_decode_append_attn"]
+SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _p, _p])
 
 _lock = threading.Lock()
 _lib = None

@@ -95,7 +95,7 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
                   const uint16_t* ks, const uint16_t* kz, int v_bits, const void* vq, const uint16_t* vs,
                   const uint16_t* vz, const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
                   int64_t cap, int splits, void* ws, size_t ws_bytes, float* out, const RowSrc* knew,
-                  const RowSrc* vnew, void* stream) {
+                  const RowSrc* vnew, int phases, void* stream) {
   int e;
   if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
   if ((e = check_dtype(q_dtype, "query"))) return e;
@@ -148,7 +148,12 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   a.S = S;
   a.span = span;
   a.t_split_end = t_split_end;
-  return launched(launch_decode(k_bits, v_bits, a, (hipStream_t)stream), "decode launch");
+  if (phases & 1) {
+    const int e1 = launched(launch_decode_partial(k_bits, v_bits, a, (hipStream_t)stream), "decode launch");
+    if (e1 != REC_OK) return e1;
+  }
+  if (phases & 2) return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
+  return ok();
 }
 
 }  // namespace
@@ -227,7 +232,25 @@ int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int 
                     size_t workspace_bytes, float* out, void* stream) {
   return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
                        sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out, nullptr,
-                       nullptr, stream);
+                       nullptr, 3, stream);
+}
+
+static int append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
+                       int new_dtype, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh, int k_bits,
+                       void* k_codes, uint16_t* k_scales, uint16_t* k_zeros, int v_bits, void* v_codes,
+                       uint16_t* v_scales, uint16_t* v_zeros, const float* sinks, float scale, int B, int Hq, int Hkv,
+                       int D, int64_t T, int64_t capacity, int splits, void* workspace, size_t workspace_bytes,
+                       float* out, int phases, void* stream) {
+  const bool append = k_new != nullptr || v_new != nullptr;
+  if (append) {
+    int e;
+    if ((e = check_dtype(new_dtype, "new keys/values"))) return e;
+    if (!k_new || !v_new) return fail(REC_EINVAL, "new keys and values must both be given");
+  }
+  const RowSrc kn{k_new, new_dtype, k_sb, k_sh, 0}, vn{v_new, new_dtype, v_sb, v_sh, 0};
+  return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
+                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out,
+                       append ? &kn : nullptr, append ? &vn : nullptr, phases, stream);
 }
 
 int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new,
@@ -236,13 +259,46 @@ int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                            void* v_codes, uint16_t* v_scales, uint16_t* v_zeros, const float* sinks, float scale,
                            int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
                            size_t workspace_bytes, float* out, void* stream) {
-  int e;
-  if ((e = check_dtype(new_dtype, "new keys/values"))) return e;
   if (!k_new || !v_new) return fail(REC_EINVAL, "new keys/values pointer is null");
-  const RowSrc kn{k_new, new_dtype, k_sb, k_sh, 0}, vn{v_new, new_dtype, v_sb, v_sh, 0};
-  return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
-                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out, &kn, &vn,
-                       stream);
+  return append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
+                     k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
+                     splits, workspace, workspace_bytes, out, 3, stream);
+}
+
+int rec_decode_partial(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
+                       int new_dtype, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh, int k_bits,
+                       void* k_codes, uint16_t* k_scales, uint16_t* k_zeros, int v_bits, void* v_codes,
+                       uint16_t* v_scales, uint16_t* v_zeros, const float* sinks, float scale, int B, int Hq, int Hkv,
+                       int D, int64_t T, int64_t capacity, int splits, void* workspace, size_t workspace_bytes,
+                       float* out, void* stream) {
+  return append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
+                     k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
+                     splits, workspace, workspace_bytes, out, 1, stream);
+}
+
+int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int splits, int appended, void* workspace,
+                     size_t workspace_bytes, float* out, void* stream) {
+  if (B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv != 0 || Hq / Hkv > 8 || T < 1)
+    return fail(REC_EINVAL, "bad shape B=%d Hq=%d Hkv=%d T=%lld", B, Hq, Hkv, (long long)T);
+  if (!out || !aligned16(out)) return fail(REC_EALIGN, "output must be a 16-byte aligned buffer");
+  if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
+  if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
+  int S, span, t_split_end;
+  effective_splits(T, splits, appended != 0, &S, &span, &t_split_end);
+  const WorkspaceLayout w = ws_layout(B, Hkv, S);
+  if (!workspace || workspace_bytes < w.total) return fail(REC_EWORKSPACE, "workspace too small");
+  DecodeArgs a{};
+  a.sinks = sinks;
+  a.out = out;
+  a.ws_stat = (float*)((char*)workspace + w.stat);
+  a.ws_acc = (float*)((char*)workspace + w.acc);
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.T = T;
+  a.S = S;
+  return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
 }
 
 }  // extern "C"

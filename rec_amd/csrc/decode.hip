@@ -529,15 +529,18 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
   }
 }
 
-hipError_t launch_decode(int kb, int vb, const DecodeArgs& a, hipStream_t stream) {
+hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.S, a.Hkv, a.B), block(256);
   if (kb == 8 && vb == 8) hipLaunchKernelGGL((decode_kernel<8, 8>), grid, block, 0, stream, a);
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((decode_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((decode_kernel<4, 8>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((decode_kernel<4, 4>), grid, block, 0, stream, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.S == 1) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.Hq, a.B), block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream) {
+  if (a.S == 1) return hipSuccess;  // the partial kernel wrote the output
+  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.Hq, a.B), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -46,6 +46,7 @@ constexpr int DECODE_MAX_SPLITS = 256;
 
 hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream);
 hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream);
-hipError_t launch_decode(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 
 }  // namespace rec

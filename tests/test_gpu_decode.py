@@ -147,3 +147,60 @@ def test_long_context_int8(gpu, T):
     cache_np = dict(k_bits=8, v_bits=8, kq=kc, ks=ksc, vq=vc, vs=vsc)
     ref = O.split_k_decode_quantized(f32(q)[:, :, 0], cache_np, T, SCALE, f32(sinks), chunk=8192)
     assert_close(f32(out)[:, :, 0], ref.astype(np.float64), f"T={T}")
+
+
+def test_repeated_launches_share_workspace(gpu):
+    """Many launches on one workspace with changing split counts: the merge
+    counters must re-arm and no stale partial may leak between launches."""
+    B, Hq, Hkv = 1, 32, 4
+    caches, refs = [], []
+    for i, T in enumerate([700, 2048, 96]):
+        c = QuantizedKVCache(32, 8, 8)
+        k, v = fill(c, B, Hkv, T, seed=300 + i)
+        caches.append(c)
+        rk, rv = oracle_quantize(k, 8), oracle_quantize(v, 8)
+        refs.append((dequant(8, *rk), dequant(8, *rv)))
+    qs = [synthetic.query(B, Hq, 1, seed=400 + i) for i in range(4)]
+    for it in range(24):
+        i = it % 3
+        q = qs[it % 4]
+        kq, vq = caches[i].keys_and_values()
+        splits = [2, 5, 8, 64, 200, 3][it % 6]
+        out = quantized_attention_with_sinks(q, kq, vq, SCALE, None, None, 32, 8, 8, out_dtype=torch.float32,
+                                             splits=splits)
+        ref = O.attention(f32(q), *refs[i], SCALE)
+        assert_close(f32(out), ref, f"iteration {it} cache {i} splits {splits}")
+
+
+def test_partial_then_merge_equals_one_call(gpu):
+    """rec_decode_partial + rec_decode_merge give the same bytes as rec_decode_append_attn."""
+    import rec_amd
+    from rec_amd import _lib
+    from rec_amd.attention import workspace
+
+    lib = rec_amd.library()
+    B, Hq, Hkv, T0 = 1, 32, 4, 3000
+    outs = []
+    for phased in (False, True):
+        c = QuantizedKVCache(32, 8, 8)
+        fill(c, B, Hkv, T0, seed=21)
+        c._reserve(B, Hkv, T0 + 1, "cuda")
+        q = synthetic.query(B, Hq, 1, seed=22)[:, :, 0].contiguous()
+        kn, vn = synthetic.kv((B, Hkv, 1, 128), 23), synthetic.kv((B, Hkv, 1, 128), 24)
+        sinks = torch.randn(Hq, device="cuda", generator=torch.Generator("cuda").manual_seed(5))
+        out = torch.empty((B, Hq, 128), dtype=torch.float32, device="cuda")
+        stream = torch.cuda.current_stream().cuda_stream
+        ws = workspace(q.device, B, Hkv, 256, stream)
+        (kc, ks, _), (vc, vs, _) = c.keys, c.values
+        args = (q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1), kn.data_ptr(), vn.data_ptr(), _lib.REC_F16,
+                kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1), 8, kc.data_ptr(), ks.data_ptr(), None,
+                8, vc.data_ptr(), vs.data_ptr(), None, sinks.data_ptr(), SCALE, B, Hq, Hkv, 128, T0 + 1,
+                c.capacity, 0, ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
+        if phased:
+            _lib.check(lib.rec_decode_partial(*args), "partial")
+            _lib.check(lib.rec_decode_merge(sinks.data_ptr(), B, Hq, Hkv, T0 + 1, 0, 1, ws.data_ptr(), ws.numel(),
+                                            out.data_ptr(), stream), "merge")
+        else:
+            _lib.check(lib.rec_decode_append_attn(*args), "append_attn")
+        outs.append(out.clone())
+    torch.testing.assert_close(outs[0], outs[1], rtol=0, atol=0)
