@@ -183,6 +183,84 @@ def run_decode(T, R, steps, warmup, seed):
     return res
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def run_prefill(P, L, steps, warmup, seed):
+    """Chunked prefill: quantize-append L new tokens after a P-token int8 prefix,
+    then L causal bf16 queries attend over all P + L tokens.  Each step rewrites
+    the same L positions, so every step does identical work."""
+    import torch
+
+    import rec_amd
+    from rec_amd import _lib, synthetic
+
+    lib = rec_amd.library()
+    T = P + L
+    log(f"prefill: building a {P}-token prefix")
+    c = rec_amd.QuantizedKVCache(32, 8, 8, max_tokens=T)
+    k = synthetic.kv((1, HKV, P, D), seed, kind="outliers", frac=0.01)
+    v = synthetic.kv((1, HKV, P, D), seed + 1, kind="outliers", frac=0.01)
+    c.update_and_fetch(k, v)
+    del k, v
+    kn = synthetic.kv((1, HKV, L, D), seed + 2, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    vn = synthetic.kv((1, HKV, L, D), seed + 3, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    q = synthetic.query(1, HQ, L, seed + 4, dtype=torch.bfloat16)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    sinks = torch.randn(HQ, generator=g, device="cuda")
+    out = torch.empty((1, HQ, L, D), dtype=torch.float32, device="cuda")
+    c._reserve(1, HKV, T, "cuda")
+    (kc, ks, _), (vc, vs, _) = c.keys, c.values
+
+    def append():
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.rec_kv_append(kn.data_ptr(), vn.data_ptr(), _lib.REC_BF16, *kn.stride()[:3], *vn.stride()[:3],
+                               8, kc.data_ptr(), ks.data_ptr(), None, 8, vc.data_ptr(), vs.data_ptr(), None,
+                               1, HKV, L, D, P, c.capacity, st)
+        _lib.check(rc, "rec_kv_append")
+
+    def attention():
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3], 8, kc.data_ptr(), ks.data_ptr(),
+                                  None, 8, vc.data_ptr(), vs.data_ptr(), None, sinks.data_ptr(), SCALE, 1,
+                                  1, HQ, HKV, D, L, T, c.capacity, out.data_ptr(), st)
+        _lib.check(rc, "rec_prefill_attn")
+
+    for _ in range(warmup):
+        append()
+        attention()
+    torch.cuda.synchronize()
+    g_step, g_att = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_step):
+        for _ in range(steps):
+            append()
+            attention()
+    with torch.cuda.graph(g_att):
+        for _ in range(steps):
+            attention()
+    ms_step = _replay_timed(torch, g_step, steps)
+    ms_att = _replay_timed(torch, g_att, steps)
+    pairs = L * P + L * (L + 1) // 2
+    flops = 4.0 * D * HQ * pairs
+    tflops = flops / (ms_att * 1e-3) / 1e12
+    log(f"prefill: {ms_step:.3f} ms/step, attention {ms_att:.3f} ms = {tflops:.0f} TFLOP/s")
+    del g_step, g_att, c
+    torch.cuda.empty_cache()
+    return dict(
+        prefix=P,
+        new_tokens=L,
+        ms_per_step=round(ms_step, 4),
+        append_ms=round(ms_step - ms_att, 4),
+        attention_ms=round(ms_att, 4),
+        attention_flops=flops,
+        attention_tflops=round(tflops, 1),
+        frac_of_mfma_peak=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        mfma_peak_tflops=MFMA_BF16_PEAK_TFLOPS,
+        note="Q.K^T on bf16 MFMA, P.V on fp16 MFMA; peak is the dense bf16 figure",
+    )
+
+
 def cpu_baseline(T, seed, budget_s=10.0):
     """The oracle's split-K decode over one 32K instance on the host cores."""
     import torch
@@ -251,6 +329,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--long-steps", type=int, default=0, help="timed steps at 252K (default steps/8)")
     ap.add_argument("--no-long", action="store_true", help="skip the 252K measurement")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the chunked-prefill measurement")
+    ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--seed", type=int, default=1234)
@@ -294,6 +374,10 @@ def main(argv=None):
         ls = args.long_steps or max(16, args.steps // 8)
         r252 = run_decode(258048, 4, ls, max(4, args.warmup // 4), args.seed + 99)
         log(f"252K: {r252['us_per_step']:.2f} us/step, {r252['gbs']:.0f} GB/s; kernel {r252['kernel_us']:.2f} us")
+
+    rpf = None
+    if not args.no_prefill:
+        rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -360,6 +444,8 @@ def main(argv=None):
             "bytes_per_step": r252["bytes_per_step"],
             "cache_instances": r252["instances"],
         }
+    if rpf is not None:
+        result["prefill_65536_plus_2048"] = rpf
     print(json.dumps(result), flush=True)
     return 0
 

@@ -134,6 +134,22 @@ int rec_decode_partial(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
 int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int splits, int appended,
                      void* workspace, size_t workspace_bytes, float* out, void* stream);
 
+/*
+ * Chunked prefill: the last L of the T cached tokens are new (already
+ * quantize-appended with rec_kv_append); their queries q (B, Hq, L, D), element
+ * strides (q_sb, q_sh, q_st), bf16 or f16, attend over all T tokens — with
+ * causal != 0, query i sees tokens [0, T-L+i] — with optional sink logits.
+ * out (B, Hq, L, D) fp32.  int8 K and V.
+ * Replaces the prefill branch of Attention.__call__,
+ * engine/src/rec_mlx/model.py:191-203 (mask rule :122-125).
+ */
+int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                     int k_bits, const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros,
+                     int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
+                     const float* sinks, float scale, int causal,
+                     int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
+                     float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

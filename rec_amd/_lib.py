@@ -53,6 +53,10 @@ SIGNATURES = {
 }
 SIGNATURES["rec_decode_partial"] = SIGNATURES["rec_decode_append_attn"]
 SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _p, _p])
+SIGNATURES["rec_prefill_attn"] = (
+    _i,
+    [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i64, _i64, _p, _p],
+)
 
 _lock = threading.Lock()
 _lib = None

@@ -2,9 +2,11 @@
 
 * :func:`quantized_attention_with_sinks` keeps the signature of
   engine/src/rec_mlx/model.py:108-110 and runs the gfx950 split-K decode kernel
-  (``rec_decode_attn``) for one query token.
+  (``rec_decode_attn``) for one query token, the chunked prefill kernel
+  (``rec_prefill_attn``, model.py:191-203) for several.
 * :func:`attend` mirrors the cache/attention part of ``Attention.__call__``
-  (model.py:177-203): append first, then attend, decode for ``L == 1``.  For a
+  (model.py:177-203): append first, then attend, decode for ``L == 1`` and
+  chunked prefill for ``L > 1``.  For a
   single decode token it issues ONE launch (``rec_decode_append_attn``) that
   quantizes the new token into the cache and attends over it.
 
@@ -106,6 +108,22 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
         _lib.check(rc, "rec_decode_append_attn")
 
 
+def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out):
+    lib = _lib.load()
+    B, Hq, L, D = queries.shape
+    q = queries if queries.stride(-1) == 1 else queries.contiguous()
+    dev = queries.device
+    sk = _sinks(sinks, Hq, dev)
+    rc = lib.rec_prefill_attn(
+        q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), q.stride(2),
+        keys.bits, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
+        values.bits, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
+        _ptr(sk), float(scale), int(causal), B, Hq, keys.n_kv_heads, D, L, int(keys.length), int(keys.capacity),
+        out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream,
+    )
+    _lib.check(rc, "rec_prefill_attn")
+
+
 def quantized_attention_with_sinks(
     queries, keys, values, scale, mask, sinks, group_size, key_bits, value_bits, *, out_dtype=None, splits=None
 ):
@@ -114,8 +132,10 @@ def quantized_attention_with_sinks(
     ``keys``/``values`` are what :meth:`QuantizedKVCache.update_and_fetch`
     returns; ``sinks`` (``n_q`` logits or None) join the softmax denominator;
     ``mask`` is None or "causal" (for ``L == 1`` both mean "every cached
-    token").  Returns ``(B, n_q, L, 128)`` in ``out_dtype`` (default: the
-    query dtype, as the reference returns, model.py:132-139).
+    token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` the chunked
+    prefill kernel (int8 cache, bf16/f16 queries), the queries being the newest
+    ``L`` cached tokens.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
+    (default: the query dtype, as the reference returns, model.py:132-139).
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
@@ -127,11 +147,16 @@ def quantized_attention_with_sinks(
         raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
     if mask is not None and not (isinstance(mask, str) and mask == "causal"):
         raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
-    if L != 1:
-        raise NotImplementedError("multi-token queries go through the chunked prefill kernel")
-    out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
-    _decode_launch(queries, keys, values, scale, sinks, splits, out)
-    out = out.view(B, Hq, 1, D)
+    if L == 1:
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+        _decode_launch(queries, keys, values, scale, sinks, splits, out)
+        out = out.view(B, Hq, 1, D)
+    else:
+        # the L queries are the newest L cached tokens (model.py:122-125)
+        if L > keys.length:
+            raise ValueError(f"{L} queries but only {keys.length} cached tokens")
+        out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
+        _prefill_launch(queries, keys, values, scale, sinks, mask == "causal", out)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 

@@ -301,4 +301,51 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
   return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
 }
 
+int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int k_bits,
+                     const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits,
+                     const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks,
+                     float scale, int causal, int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
+                     float* out, void* stream) {
+  int e;
+  if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
+  if (k_bits != 8 || v_bits != 8) return fail(REC_EUNSUPPORTED, "prefill supports int8 K and V only");
+  if (q_dtype != REC_BF16 && q_dtype != REC_F16)
+    return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
+  if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
+  if (B < 1 || Hkv < 1 || Hq < 1 || L < 1) return fail(REC_EINVAL, "bad shape B=%d Hq=%d Hkv=%d L=%d", B, Hq, Hkv, L);
+  if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
+  if (Hq / Hkv > 8) return fail(REC_EUNSUPPORTED, "GQA ratio %d exceeds 8", Hq / Hkv);
+  if (T < L) return fail(REC_EINVAL, "T=%lld is smaller than L=%d (the new tokens are cached first)", (long long)T, L);
+  if (capacity % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 32", (long long)capacity);
+  if (T > capacity) return fail(REC_ECAPACITY, "T=%lld exceeds the cache capacity %lld", (long long)T, (long long)capacity);
+  if (capacity > ((int64_t)1 << 24)) return fail(REC_EUNSUPPORTED, "capacity above 16M tokens per head");
+  if (!q || !out) return fail(REC_EINVAL, "query/output pointer is null");
+  if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
+  if ((e = check_cache(8, k_codes, k_scales, k_zeros, "key")) || (e = check_cache(8, v_codes, v_scales, v_zeros, "value")))
+    return e;
+  if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
+  PrefillArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_st = q_st;
+  a.kq = k_codes;
+  a.ks = k_scales;
+  a.vq = v_codes;
+  a.vs = v_scales;
+  a.sinks = sinks;
+  a.out = out;
+  a.q_mul = scale * LOG2E;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.L = L;
+  a.T = T;
+  a.cap = capacity;
+  a.causal = causal != 0;
+  return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
+}
+
 }  // extern "C"

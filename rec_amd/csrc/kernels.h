@@ -42,11 +42,28 @@ struct DecodeArgs {
   int t_split_end;  // end of the regular splits; a fused append adds one split [t_split_end, T)
 };
 
+struct PrefillArgs {
+  const void* q;
+  int q_dtype;                 // DT_BF16 (bf16 MFMA) or DT_F16 (fp16 MFMA)
+  int64_t q_sb, q_sh, q_st;    // element strides of q (batch, head, position)
+  const void* kq;              // int8 K codes (cache layout)
+  const uint16_t* ks;
+  const void* vq;              // int8 V codes
+  const uint16_t* vs;
+  const float* sinks;          // [Hq] or null
+  float* out;                  // [B][Hq][L][128] fp32
+  float q_mul;                 // softmax scale * log2(e)
+  int B, Hq, Hkv, G, L;
+  int64_t T, cap;              // cached tokens including the L new ones; capacity
+  int causal;
+};
+
 constexpr int DECODE_MAX_SPLITS = 256;
 
 hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream);
 hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream);
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
 
 }  // namespace rec

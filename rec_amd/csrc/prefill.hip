@@ -1,0 +1,270 @@
+// Chunked prefill attention over the int8 KV cache on bf16 / fp16 matrix cores
+// (gfx950).
+//
+// Restates the prefill branch of Attention.__call__
+// (engine/src/rec_mlx/model.py:191-203): the new tokens were quantize-appended
+// first (model.py:177-178), then the L new queries attend over the whole
+// cache, the new tokens included, with the causal "string" mask of
+// model.py:122-125 (query i sits at position T-L+i) and the per-head sink
+// logit in the softmax denominator.  The reference dequantizes the cache to the
+// query dtype; here K/V codes are converted to bf16/fp16 exactly (|q| <= 127)
+// and the row scales are applied outside the matrix products: the K scale to
+// the scores, the V scale folded into the probabilities before their one
+// rounding.  Q·K^T runs on bf16 MFMAs for bf16 queries (fp16 for fp16
+// queries); P·V always on fp16 MFMAs, whose 11-bit significand keeps the
+// rounded probabilities within 2^-12 (bf16 would allow 2^-9, more than the
+// 1e-3 output tolerance when one token dominates).
+//
+// Work decomposition.  Grid (ceil(L/32), Hkv, B), 512 threads = 8 wavefronts;
+// wave w owns query head w of the KV head's GQA group and 32 query positions.
+// Each 64-token K/V tile is loaded once per workgroup, converted into
+// double-buffered LDS and shared by the 8 waves.
+//
+// S^T = K Q^T on 16x16x32 MFMAs (A = 16 tokens x 32 dims from LDS, B = Q^T held
+// in registers), which leaves lane (c, g) with the scores of query row c for
+// tokens 16j + 4g + i -- the order the cache keeps V in inside a 32-token
+// block.  P·V then takes A = V^T straight from LDS (dims x tokens, cache
+// order) and B = P'^T from the lane's own registers.
+#include "kernels.h"
+
+namespace rec {
+
+constexpr int PF_QB = 32;           // query positions per workgroup
+constexpr int PF_KT = 64;           // tokens per K/V tile
+constexpr int PF_KROW = 136;        // LDS row pitch of K (elements): 128 + 8 pad
+constexpr int PF_VROW = 72;         // LDS row pitch of V (elements): 64 + 8 pad
+constexpr int PF_K_ELEMS = PF_KT * PF_KROW;
+constexpr int PF_V_ELEMS = HEAD_DIM * PF_VROW;
+
+template <bool BF16>
+struct MT;
+template <>
+struct MT<true> {
+  typedef v8bf vec;
+  typedef __bf16 elem;
+  static __device__ __forceinline__ v4f mfma(vec a, vec b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // exact for integers |x| <= 256 and for bf16 inputs; round-to-nearest-even otherwise
+  static __device__ __forceinline__ elem from_float(float x) { return (__bf16)x; }
+};
+template <>
+struct MT<false> {
+  typedef v8h vec;
+  typedef _Float16 elem;
+  static __device__ __forceinline__ v4f mfma(vec a, vec b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ elem from_float(float x) { return (_Float16)x; }
+};
+
+// One thread's share of a 64-token tile as loaded from HBM.
+struct TileRegs {
+  v4i k, v;    // 16 int8 codes of K and of V
+  uint32_t s;  // one fp16 scale (threads 0..127: K then V)
+};
+
+__device__ __forceinline__ void load_tile(TileRegs& R, const PrefillArgs& a, int64_t bh, int t0, int tid, int t_end) {
+  const int bk = tid >> 8, o = (tid & 255) * 16;  // cache block within the tile, byte in block
+  const int blk = (t0 >> 5) + bk;
+  const bool live = t0 + 32 * bk < t_end;
+  const int8_t* kb = (const int8_t*)a.kq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
+  const int8_t* vb = (const int8_t*)a.vq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
+  R.k = live ? __builtin_nontemporal_load((const v4i*)(kb + o)) : (v4i){0, 0, 0, 0};
+  R.v = live ? __builtin_nontemporal_load((const v4i*)(vb + o)) : (v4i){0, 0, 0, 0};
+  R.s = 0;
+  if (tid < 128) {
+    const int which = tid >> 6, tt = tid & 63;  // 0 = K scale, 1 = V scale
+    const uint16_t* sp = which == 0 ? a.ks : a.vs;
+    if (t0 + tt < t_end) R.s = sp[(bh * (a.cap / BLOCK_T) + (t0 >> 5) + (tt >> 5)) * 32 + block_pos(tt & 31)];
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void store_tile(const TileRegs& R, typename MT<BF16>::elem* Kl, _Float16* Vl, float* KS,
+                                           float* VS, int tid) {
+  typedef typename MT<BF16>::elem E;
+  const int bk = tid >> 8, o = (tid & 255) * 16;
+  // K block: [2 halves][32 tokens][64 B] -> LDS [token][dim]
+  {
+    const int m = o >> 11, r = (o & 2047) >> 6, e0 = o & 63;
+    E* dst = Kl + (32 * bk + r) * PF_KROW + 64 * m + e0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) dst[4 * w + b] = MT<BF16>::from_float((float)(int8_t)((uint32_t)R.k[w] >> (8 * b)));
+  }
+  // V block: [128 dims][32 positions] -> LDS [dim][64 positions of the tile]
+  {
+    const int d = o >> 5, p0 = o & 31;
+    _Float16* dst = Vl + d * PF_VROW + 32 * bk + p0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) dst[4 * w + b] = (_Float16)(float)(int8_t)((uint32_t)R.v[w] >> (8 * b));
+  }
+  if (tid < 128) (tid < 64 ? KS : VS)[tid & 63] = half_bits_to_float(R.s);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
+  typedef typename MT<BF16>::elem E;
+  typedef typename MT<BF16>::vec V8;
+  __shared__ __attribute__((aligned(16))) E Kl[2][PF_K_ELEMS];
+  __shared__ __attribute__((aligned(16))) _Float16 Vl[2][PF_V_ELEMS];
+  __shared__ __attribute__((aligned(16))) float KS[2][PF_KT];
+  __shared__ __attribute__((aligned(16))) float VS[2][PF_KT];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int q0 = blockIdx.x * PF_QB, h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * a.Hkv + h;
+  const int P = (int)(a.T - a.L);  // cached tokens before the new ones
+  const int t_end = a.causal ? min((int)a.T, P + q0 + PF_QB) : (int)a.T;
+  const bool active = w < a.G;
+  const int hq = h * a.G + (active ? w : 0);
+
+  // Q^T operands: column tile rt holds query rows q0+16rt .. +15, k-step ks dims 32ks..32ks+31.
+  V8 qop[2][4];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int qr = min(q0 + 16 * rt + c, a.L - 1);
+    const int64_t base = (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)qr * a.q_st;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qop[rt][ks][e] = MT<BF16>::from_float(load_as_float(a.q, base + 32 * ks + 8 * g + e, a.q_dtype));
+  }
+
+  float m_run[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
+  v4f acc[8][2];
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) acc[n][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  TileRegs R;
+  load_tile(R, a, bh, 0, tid, t_end);
+  store_tile<BF16>(R, Kl[0], Vl[0], KS[0], VS[0], tid);
+  __syncthreads();
+  int buf = 0;
+  for (int t0 = 0; t0 < t_end; t0 += PF_KT) {
+    const bool more = t0 + PF_KT < t_end;
+    if (more) load_tile(R, a, bh, t0 + PF_KT, tid, t_end);  // in flight during this tile
+    if (active) {
+      const E* K = Kl[buf];
+      const _Float16* Vv = Vl[buf];
+      // ---------------- S^T = K Q^T ----------------
+      v4f s4[2][4];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s4[rt][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const V8 ka = *(const V8*)(K + (16 * j + c) * PF_KROW + 32 * ks + 8 * g);
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) s4[rt][j] = MT<BF16>::mfma(ka, qop[rt][ks], s4[rt][j]);
+        }
+      // scale, mask, online softmax per query row (lane column c of tile rt)
+      const bool diag = t0 + PF_KT > P + q0 || t0 + PF_KT > t_end;
+      v8h pb[2][2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        float s[16];
+        const int qabs = P + q0 + 16 * rt + c;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v4f ksc = *(const v4f*)(&KS[buf][16 * j + 4 * g]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float v = s4[rt][j][i] * (ksc[i] * a.q_mul);
+            if (diag) {
+              const int tok = t0 + 16 * j + 4 * g + i;
+              if (tok >= t_end || (a.causal && tok > qabs)) v = NEG_INF;
+            }
+            s[4 * j + i] = v;
+          }
+        }
+        float cmax = s[0];
+#pragma unroll
+        for (int k = 1; k < 16; ++k) cmax = fmaxf(cmax, s[k]);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+        const float m_new = fmaxf(m_run[rt], cmax);
+        const float m_use = m_new == NEG_INF ? 0.f : m_new;
+        if (__ballot(m_new > m_run[rt])) {
+          const float factor = __builtin_amdgcn_exp2f(m_run[rt] - m_use);
+          l_run[rt] *= factor;
+#pragma unroll
+          for (int n = 0; n < 8; ++n) acc[n][rt] *= factor;
+          m_run[rt] = m_new;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v4f vsc = *(const v4f*)(&VS[buf][16 * j + 4 * g]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(s[4 * j + i] - m_use);
+            l_run[rt] += p;
+            // B operand of P·V for token half qq = j/2: k order (j&1, i)
+            pb[rt][j >> 1][4 * (j & 1) + i] = (_Float16)(p * vsc[i]);
+          }
+        }
+      }
+      // ---------------- O^T += V^T P'^T ----------------
+#pragma unroll
+      for (int n = 0; n < 8; ++n)
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          const v8h va = *(const v8h*)(Vv + (16 * n + c) * PF_VROW + 32 * qq + 8 * g);
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+            acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][qq], acc[n][rt], 0, 0, 0);
+        }
+    }
+    if (more) {
+      // The other buffer was last read in the previous tile, before the barrier
+      // that ended it, so it can be refilled without waiting.
+      store_tile<BF16>(R, Kl[buf ^ 1], Vl[buf ^ 1], KS[buf ^ 1], VS[buf ^ 1], tid);
+      __syncthreads();
+      buf ^= 1;
+    }
+  }
+
+  if (!active) return;
+  // ---------------- normalise and write ----------------
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float l = l_run[rt];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    float M = m_run[rt];
+    if (a.sinks != nullptr) {
+      const float sink = a.sinks[hq] * LOG2E;
+      const float Mn = fmaxf(M, sink);
+      const float f = M == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+      l = l * f + __builtin_amdgcn_exp2f(sink - Mn);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) acc[n][rt] *= f;
+    }
+    const float inv = l > 0.f ? 1.f / l : 1.f;
+    const int qr = q0 + 16 * rt + c;
+    if (qr < a.L) {
+      float* o = a.out + (((int64_t)b * a.Hq + hq) * a.L + qr) * HEAD_DIM + 4 * g;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt] * inv;
+    }
+  }
+}
+
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.L + PF_QB - 1) / PF_QB), a.Hkv, a.B), block(512);
+  if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((prefill_kernel<false>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace rec

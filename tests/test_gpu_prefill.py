@@ -1,0 +1,115 @@
+"""Parity of the chunked prefill kernel with the CPU oracle.
+
+The L queries are the newest L cached tokens (appended first, as
+Attention.__call__ does, model.py:177-203); with the "causal" mask query i
+sees tokens [0, T-L+i].  Outputs within 2e-3 absolute + 1e-3 relative.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from rec_amd import QuantizedKVCache, attend, quantized_attention_with_sinks, synthetic, to_logical
+from tests.gpu_util import SCALE, assert_close, f32, oracle_quantize, dequant
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # B, Hq, Hkv, P, L, causal, sinks, dtype
+    (1, 8, 1, 192, 64, True, True, torch.float16),
+    (1, 8, 1, 0, 100, True, False, torch.bfloat16),
+    (1, 32, 4, 1000, 257, True, True, torch.bfloat16),
+    (2, 16, 2, 300, 64, False, True, torch.float16),
+    (1, 8, 2, 33, 31, True, True, torch.bfloat16),
+    (1, 6, 3, 64, 96, True, False, torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_causal{}_s{}_{}".format(*c[:7], str(c[7])[6:]))
+def test_prefill_matches_oracle(gpu, case):
+    B, Hq, Hkv, P, L, causal, with_sinks, dtype = case
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 11 + T, kind="outliers", frac=0.01)
+    v = synthetic.kv((B, Hkv, T, 128), 12 + T, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, L, 13 + L, dtype=dtype)
+    sinks = torch.randn(Hq, device="cuda") if with_sinks else None
+    cache = QuantizedKVCache(32, 8, 8)
+    if P:
+        cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, "causal" if causal else None, sinks,
+                 out_dtype=torch.float32)
+    rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
+    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None if sinks is None else f32(sinks),
+                      "causal" if causal else None)
+    assert_close(f32(out), ref, f"case {case}")
+
+
+def test_prefill_golden(gpu):
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "prefill_causal.npz")
+    with np.load(path, allow_pickle=False) as f:
+        g = {k: f[k] for k in f.files}
+    P = int(g["prefix"])
+    dev = torch.device("cuda")
+    k, v = torch.from_numpy(g["k"]).to(dev), torch.from_numpy(g["v"]).to(dev)
+    cache = QuantizedKVCache(32, 8, 8)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    q = torch.from_numpy(g["q"]).to(dev)
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, "causal", torch.from_numpy(g["sinks"]).to(dev),
+                 out_dtype=torch.float32)
+    kq, vq = cache.keys_and_values()
+    for kv, p in ((kq, "k"), (vq, "v")):
+        c, s, _ = (None if t is None else t.cpu().numpy() for t in to_logical(kv))
+        np.testing.assert_array_equal(c, g[p + "_codes"])
+        np.testing.assert_array_equal(s.view(np.uint16), g[p + "_scales"].view(np.uint16))
+    assert_close(f32(out), g["out_sinks"].astype(np.float64), "golden prefill")
+
+
+def test_chunked_prefill_then_decode(gpu):
+    """The QATSession loop (quantized.py:122-136): prefill in chunks, then decode."""
+    B, Hq, Hkv, chunk = 1, 32, 4, 96
+    T = 3 * chunk + 17
+    k = synthetic.kv((B, Hkv, T + 3, 128), 40)
+    v = synthetic.kv((B, Hkv, T + 3, 128), 41)
+    q = synthetic.query(B, Hq, T + 3, 42, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    cache = QuantizedKVCache(32, 8, 8)
+    rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
+    kh, vh = dequant(8, *rk), dequant(8, *rv)
+    for a in range(0, T, chunk):
+        b = min(T, a + chunk)
+        out = attend(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], cache, SCALE, "causal", sinks, out_dtype=torch.float32)
+        ref = O.attention(f32(q[:, :, a:b]), kh[:, :, :b], vh[:, :, :b], SCALE, f32(sinks), "causal")
+        assert_close(f32(out), ref, f"chunk {a}:{b}")
+    for t in range(T, T + 3):
+        out = attend(q[:, :, t : t + 1], k[:, :, t : t + 1], v[:, :, t : t + 1], cache, SCALE, None, sinks,
+                     out_dtype=torch.float32)
+        ref = O.attention(f32(q[:, :, t : t + 1]), kh[:, :, : t + 1], vh[:, :, : t + 1], SCALE, f32(sinks))
+        assert_close(f32(out), ref, f"decode {t}")
+
+
+def test_prefill_full_size_rows(gpu):
+    """2048 causal queries over a 65536-token prefix: sampled rows equal a
+    decode over their prefix (a size-independent property), checked against the
+    chunked CPU oracle."""
+    B, Hq, Hkv, P, L = 1, 32, 4, 65536, 2048
+    T = P + L
+    cache = QuantizedKVCache(32, 8, 8, max_tokens=T)
+    k = synthetic.kv((B, Hkv, T, 128), 7, kind="outliers", frac=0.01)
+    v = synthetic.kv((B, Hkv, T, 128), 8, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, L, 9, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, "causal", sinks, out_dtype=torch.float32)
+    kq, vq = cache.keys_and_values()
+    kc, ksc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(kq))
+    vc, vsc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(vq))
+    del k, v
+    qf, of, sf = f32(q), f32(out), f32(sinks)
+    for i in [0, 1, 777, 1500, 2047]:
+        Ti = P + i + 1
+        cache_np = dict(k_bits=8, v_bits=8, kq=kc[:, :, :Ti], ks=ksc[:, :, :Ti], vq=vc[:, :, :Ti], vs=vsc[:, :, :Ti])
+        ref = O.split_k_decode_quantized(qf[:, :, i], cache_np, Ti, SCALE, sf, chunk=8192)
+        assert_close(of[:, :, i], ref.astype(np.float64), f"row {i}")
