@@ -70,21 +70,21 @@ def step_bytes(T, B=1, k_bits=8, v_bits=8, output=True):
 class DecodeWorkload:
     """R cache instances of one context length plus a pool of new tokens."""
 
-    def __init__(self, T, R, total_steps, seed, splits=0):
+    def __init__(self, T, R, total_steps, seed, splits=0, bits=8, kind="outliers", frac=0.01):
         import torch
 
         import rec_amd
         from rec_amd import synthetic
 
         self.torch, self.lib = torch, rec_amd.library()
-        self.T, self.R, self.splits = T, R, splits
+        self.T, self.R, self.splits, self.bits = T, R, splits, bits
         counts = [len(range(i, total_steps, R)) for i in range(R)]
         self.caches = []
         for i in range(R):
             T0 = T - counts[i]
-            c = rec_amd.QuantizedKVCache(32, 8, 8, max_tokens=T)
-            k = synthetic.kv((1, HKV, T0, D), seed + 2 * i, kind="outliers", frac=0.01)
-            v = synthetic.kv((1, HKV, T0, D), seed + 2 * i + 1, kind="outliers", frac=0.01)
+            c = rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T)
+            k = synthetic.kv((1, HKV, T0, D), seed + 2 * i, kind=kind, frac=frac)
+            v = synthetic.kv((1, HKV, T0, D), seed + 2 * i + 1, kind=kind, frac=frac)
             c.update_and_fetch(k, v)
             del k, v
             self.caches.append(c)
@@ -114,14 +114,15 @@ class DecodeWorkload:
         c = self.caches[s % self.R]
         q, kn, vn = self.pool[s % len(self.pool)]
         T = c.offset + 1
-        kc, ks, _ = c.keys
-        vc, vs, _ = c.values
+        kc, ks, kz = c.keys
+        vc, vs, vz = c.values
         stream = self.torch.cuda.current_stream().cuda_stream
         fn = self.lib.rec_decode_partial if partial_only else self.lib.rec_decode_append_attn
         rc = fn(
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1),
-            8, kc.data_ptr(), ks.data_ptr(), None, 8, vc.data_ptr(), vs.data_ptr(), None,
+            self.bits, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
+            self.bits, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
             self.sinks.data_ptr(), SCALE, 1, HQ, HKV, D, T, c.capacity, self.splits,
             self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), stream,
         )
@@ -141,12 +142,12 @@ def _replay_timed(torch, graph, n):
     return e0.elapsed_time(e1) / n
 
 
-def run_decode(T, R, steps, warmup, seed):
+def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01):
     import torch
 
     total = warmup + 2 * steps
     log(f"T={T}: building {R} cache instances")
-    w = DecodeWorkload(T, R, total, seed)
+    w = DecodeWorkload(T, R, total, seed, bits=bits, kind=kind, frac=frac)
     log(f"T={T}: warm-up {warmup} steps")
     for s in range(warmup):
         w.step(s)
@@ -164,8 +165,8 @@ def run_decode(T, R, steps, warmup, seed):
     ms_per_step = _replay_timed(torch, g_step, steps)
     kernel_ms = _replay_timed(torch, g_kern, steps)
     log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step; attention kernel {kernel_ms * 1e3:.2f} us")
-    bytes_step = float(np.mean([step_bytes(t) for t in step_T]))
-    bytes_kernel = float(np.mean([step_bytes(t, output=False) for t in kern_T]))
+    bytes_step = float(np.mean([step_bytes(t, k_bits=bits, v_bits=bits) for t in step_T]))
+    bytes_kernel = float(np.mean([step_bytes(t, k_bits=bits, v_bits=bits, output=False) for t in kern_T]))
     res = dict(
         T=T,
         instances=R,
@@ -330,6 +331,7 @@ def main(argv=None):
     ap.add_argument("--long-steps", type=int, default=0, help="timed steps at 252K (default steps/8)")
     ap.add_argument("--no-long", action="store_true", help="skip the 252K measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the chunked-prefill measurement")
+    ap.add_argument("--no-int4", action="store_true", help="skip the 131K uint4 measurement")
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -374,6 +376,12 @@ def main(argv=None):
         ls = args.long_steps or max(16, args.steps // 8)
         r252 = run_decode(258048, 4, ls, max(4, args.warmup // 4), args.seed + 99)
         log(f"252K: {r252['us_per_step']:.2f} us/step, {r252['gbs']:.0f} GB/s; kernel {r252['kernel_us']:.2f} us")
+
+    r4 = None
+    if not args.no_int4:
+        ls = args.long_steps or max(16, args.steps // 8)
+        r4 = run_decode(131072, 12, ls, max(4, args.warmup // 4), args.seed + 77, bits=4, kind="heavy", frac=0.05)
+        log(f"131K int4: {r4['us_per_step']:.2f} us/step, {r4['gbs']:.0f} GB/s; kernel {r4['kernel_us']:.2f} us")
 
     rpf = None
     if not args.no_prefill:
@@ -443,6 +451,19 @@ def main(argv=None):
             "kernel_frac_of_peak": round(r252["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_step": r252["bytes_per_step"],
             "cache_instances": r252["instances"],
+        }
+    if r4 is not None:
+        result["context_131k_int4"] = {
+            "context": 131072,
+            "kv_format": "uint4 asymmetric, fp16 scale + zero-point per 32 dims; 5% Student-t(3) channels",
+            "us_per_step": round(r4["us_per_step"], 3),
+            "gbs": round(r4["gbs"], 2),
+            "frac_of_peak": round(r4["gbs"] / HBM_PEAK_GBS, 4),
+            "kernel_us": round(r4["kernel_us"], 3),
+            "kernel_gbs": round(r4["kernel_gbs"], 2),
+            "kernel_frac_of_peak": round(r4["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_step": r4["bytes_per_step"],
+            "cache_instances": r4["instances"],
         }
     if rpf is not None:
         result["prefill_65536_plus_2048"] = rpf
