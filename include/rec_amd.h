@@ -7,14 +7,15 @@
  * negative REC_E* code, with a message for the calling thread available from
  * rec_last_error().  Nothing throws across this boundary.
  *
- * Cache layout per layer (bh = b*Hkv + h, C = capacity, a multiple of 64,
- * head_dim D = 128, scales and zero-points are IEEE fp16 bit patterns):
- *   int8 K codes  int8  [B][Hkv][C][128]          row-major
- *   int8 V codes  int8  [B][Hkv][C/64][128][64]   token-blocked
- *   int8 scales   fp16  [B][Hkv][C]               one per (token, head)
- *   int4 K codes  uint8 [B][Hkv][C][64]           low nibble = even dim
- *   int4 V codes  uint8 [B][Hkv][C/64][128][32]   token-blocked, low nibble = even token
- *   int4 scale/zp fp16  [B][Hkv][C/64][4][64]     per 32-dim group
+ * Cache layout per layer, in 32-token blocks (bh = b*Hkv + h, C = capacity, a
+ * multiple of 32, head_dim D = 128, scales and zero-points are IEEE fp16 bit
+ * patterns; token t of a block sits at position p = 8*((t>>2)&3) + 4*(t>>4) + (t&3)):
+ *   int8 K codes  int8  [B][Hkv][C/32][2][32][64]   half m = dims 64m..64m+63, row = token t
+ *   int4 K codes  uint8 [B][Hkv][C/32][2][32][32]   same, low nibble = even dim
+ *   int8 V codes  int8  [B][Hkv][C/32][128][32]     dim-major, column = position p
+ *   int4 V codes  uint8 [B][Hkv][C/32][128][16]     byte p/2, low nibble = even p
+ *   int8 scales   fp16  [B][Hkv][C/32][32]          one per (token, head), position p
+ *   int4 scale/zp fp16  [B][Hkv][C/32][4][32]       per 32-dim group, position p
  * Quantizers: int8 symmetric s = fp16(amax/127), q = clamp(rint(x/s), ±127);
  * uint4 asymmetric over [min(0, x), max(0, x)], s = fp16(range/15),
  * z = clamp(rint(-min/s), 0, 15), q = clamp(rint(x/s) + z, 0, 15).
@@ -79,7 +80,8 @@ int rec_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 /*
  * GQA decode attention over the first T cached tokens for one query token per
  * sequence: q (B, Hq, D) with element strides (q_sb, q_sh), q-head h reads
- * kv-head h / (Hq/Hkv), Hq/Hkv <= 8.  scores = scale * q·k̂; `sinks` (Hq fp32
+ * kv-head h / (Hq/Hkv), Hq/Hkv <= 8; q rows start 16-byte aligned with strides
+ * that are multiples of 4 elements (else REC_EALIGN).  scores = scale * q·k̂; `sinks` (Hq fp32
  * logits, or NULL) join the softmax denominator; out (B, Hq, D) fp32.
  * splits <= 0 picks rec_decode_default_splits().
  * Replaces quantized_attention_with_sinks, engine/src/rec_mlx/model.py:108-139

@@ -44,6 +44,16 @@ def workspace(device: torch.device, B: int, Hkv: int, splits: int, stream: int) 
         return ws
 
 
+def _rows_aligned(t: torch.Tensor) -> bool:
+    """Rows the kernels read with vector loads: unit dim stride, 16-byte
+    aligned start, other strides multiples of 4 elements."""
+    return (
+        t.stride(-1) == 1
+        and t.data_ptr() % 16 == 0
+        and all(s % 4 == 0 for s in t.stride()[:-1])
+    )
+
+
 def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
@@ -76,7 +86,7 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
     T = keys.length if T is None else T
     capacity = keys.capacity if capacity is None else capacity
     q = queries[:, :, 0]
-    if q.stride(-1) != 1:
+    if not _rows_aligned(q):
         q = q.contiguous()
     dev = queries.device
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -179,8 +189,8 @@ def attend(queries, keys, values, cache: QuantizedKVCache, scale, mask=None, sin
         Bk, H = keys.shape[:2]
         cache._reserve(Bk, H, cache.offset + 1, keys.device)
         k_kv, v_kv = cache._view()
-        kn = keys if keys.stride(-1) == 1 else keys.contiguous()
-        vn = values if values.stride(-1) == 1 else values.contiguous()
+        kn = keys if _rows_aligned(keys) else keys.contiguous()
+        vn = values if _rows_aligned(values) else values.contiguous()
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
         try:
             _decode_launch(queries, k_kv, v_kv, scale, sinks, splits, out, kn, vn, T=cache.offset + 1,

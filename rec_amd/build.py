@@ -29,6 +29,10 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the decode loop rescales them on the
+    # VALU, and AGPR accumulators cost a copy out and back per chunk
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -30,6 +30,12 @@ int ok() {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Rows of p can be read with vector loads: 16-byte aligned base, strides that
+// keep every row start 16-byte aligned for 4-byte elements (8 for 2-byte).
+int vec_rows(const void* p, int64_t s0, int64_t s1, int64_t s2) {
+  return aligned16(p) && s0 % 4 == 0 && s1 % 4 == 0 && s2 % 4 == 0;
+}
+
 int launched(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(REC_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
   return ok();
@@ -109,6 +115,8 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   if (cap > ((int64_t)1 << 24)) return fail(REC_EUNSUPPORTED, "capacity above 16M tokens per head");
   if (!q || !out) return fail(REC_EINVAL, "query/output pointer is null");
   if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
+  if (!vec_rows(q, q_sb, q_sh, 0))
+    return fail(REC_EALIGN, "query rows must start 16-byte aligned (strides multiples of 4 elements)");
   if ((e = check_cache(k_bits, kq, ks, kz, "key")) || (e = check_cache(v_bits, vq, vs, vz, "value"))) return e;
   if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
   if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
@@ -184,8 +192,8 @@ int rec_kv_append(const void* k_new, const void* v_new, int in_dtype, int64_t k_
       (e = check_cache(v_bits, v_codes, v_scales, v_zeros, "value")))
     return e;
   AppendArgs a{};
-  a.k = RowSrc{k_new, in_dtype, k_sb, k_sh, k_st};
-  a.v = RowSrc{v_new, in_dtype, v_sb, v_sh, v_st};
+  a.k = RowSrc{k_new, in_dtype, k_sb, k_sh, k_st, vec_rows(k_new, k_sb, k_sh, k_st)};
+  a.v = RowSrc{v_new, in_dtype, v_sb, v_sh, v_st, vec_rows(v_new, v_sb, v_sh, v_st)};
   a.kq = k_codes;
   a.ks = k_scales;
   a.kz = k_zeros;
@@ -202,9 +210,10 @@ int rec_kv_append(const void* k_new, const void* v_new, int in_dtype, int64_t k_
 }
 
 int rec_decode_default_splits(int B, int Hkv, int64_t T) {
-  // Aim for about two workgroups per CU (256 CUs), at least one 64-token chunk
-  // per split.
-  const int64_t target = 512;
+  // One workgroup per CU (256 CUs) across all (b, h) pairs: measured best at
+  // 32K-252K tokens (two per CU, or uneven counts, leave some CUs a second
+  // round); at least one 32-token chunk per split.
+  const int64_t target = 256;
   const int64_t bh = (int64_t)(B < 1 ? 1 : B) * (Hkv < 1 ? 1 : Hkv);
   int64_t s = (target + bh - 1) / bh;
   const int64_t chunks = (T + CHUNK - 1) / CHUNK;
@@ -247,7 +256,8 @@ static int append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
     if ((e = check_dtype(new_dtype, "new keys/values"))) return e;
     if (!k_new || !v_new) return fail(REC_EINVAL, "new keys and values must both be given");
   }
-  const RowSrc kn{k_new, new_dtype, k_sb, k_sh, 0}, vn{v_new, new_dtype, v_sb, v_sh, 0};
+  const RowSrc kn{k_new, new_dtype, k_sb, k_sh, 0, vec_rows(k_new, k_sb, k_sh, 0)},
+      vn{v_new, new_dtype, v_sb, v_sh, 0, vec_rows(v_new, v_sb, v_sh, 0)};
   return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
                        sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out,
                        append ? &kn : nullptr, append ? &vn : nullptr, phases, stream);

@@ -67,10 +67,35 @@ __device__ __forceinline__ v4i widen_u4(v2i w) {
   return r;
 }
 
+// Raw bits of query elements i .. i+3 of a row whose dims are contiguous and
+// whose start is 16-byte aligned (the host checks).  Two 8-byte loads, the
+// second one only meaningful for fp32; no branch, so the compiler can leave the
+// load in flight while the cache loads are issued behind it.
+__device__ __forceinline__ v4i load_q_raw(const void* p, int64_t i, int dt) {
+  const int es = dt == DT_F32 ? 4 : 2;
+  const char* base = (const char*)p + i * es;
+  const v2i w0 = *(const v2i*)base;
+  const v2i w1 = *(const v2i*)(base + (es == 4 ? 8 : 0));
+  return (v4i){w0[0], w0[1], w1[0], w1[1]};
+}
+
+__device__ __forceinline__ void q_raw_to_float(const v4i& r, int dt, float x[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t w = (uint32_t)r[k >> 1];
+    const uint32_t bits = (k & 1) ? (w >> 16) : (w & 0xffffu);
+    const float h16 = half_bits_to_float(bits), b16 = __builtin_bit_cast(float, bits << 16);
+    const int rk = r[k];  // copy first: bit_cast of a vector subscript reads lane 0 in this clang
+    const float f32 = __builtin_bit_cast(float, rk);
+    x[k] = dt == DT_F32 ? f32 : (dt == DT_F16 ? h16 : b16);
+  }
+}
+
 // Quantize this workgroup's G query rows to int16 (hi/lo int8) and lay them out
-// as the B operands of the Q·Kᵀ MFMAs.
+// as the B operands of the Q·Kᵀ MFMAs.  Thread (hh, d0) brings dims d0..d0+3 of
+// head hh, already scaled (zero for hh >= G).
 template <int KB>
-__device__ void prepare_query(const DecodeArgs& a, int b, int h, char* smem, int tid) {
+__device__ void prepare_query(const float x[4], char* smem, int tid) {
   int8_t* qop = (int8_t*)(smem + LDS_QOP);
   float* qsc = (float*)(smem + LDS_QSC);
   int* qsum = (int*)(smem + LDS_QSUM);
@@ -79,12 +104,6 @@ __device__ void prepare_query(const DecodeArgs& a, int b, int h, char* smem, int
     __syncthreads();
   }
   const int hh = tid >> 5, d0 = (tid & 31) * 4;
-  float x[4] = {0.f, 0.f, 0.f, 0.f};
-  if (hh < a.G) {
-    const int64_t base = (int64_t)b * a.q_sb + (int64_t)(h * a.G + hh) * a.q_sh + d0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = load_as_float(a.q, base + i, a.q_dtype) * a.q_mul;
-  }
   float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
 #pragma unroll
   for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
@@ -136,71 +155,110 @@ struct Chunk {
   v4i vz4[4];     // int4 V: zero-points
 };
 
-struct Bases {
-  const int8_t* k;     // this (b, h) slice of the K codes
-  const int8_t* v;     // this (b, h) slice of the V codes
-  const uint16_t* ks;  // K scales (int8: per token; int4: blocked per group)
-  const uint16_t* kz;
-  const uint16_t* vs;
-  const uint16_t* vz;
+// Buffer resources of one (b, h) slice of the cache, plus an empty one.  Every
+// chunk load goes through them: a chunk slot a wave does not own loads through
+// the empty resource (zeros, no memory access) but is issued all the same, which
+// keeps every load unconditional and lets the compiler count the loads in
+// flight exactly (a load under a branch makes it drain them all).  Block
+// offsets travel in the scalar soffset operand and the per-lane offsets are
+// loop-invariant registers.  Range checks need not cover soffset: the empty
+// resource has no records, so any lane offset is out of range and reads zero,
+// and real loads stay inside their slice.
+struct Res {
+  __amdgpu_buffer_rsrc_t k, v, ks, kz, vs, vz, none;
 };
+
+constexpr int BUF_NT = 2;  // cache policy: nontemporal (the KV is streamed once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  // gfx9 buffer descriptor word 3 for raw (stride 0) dword access
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
 
 __device__ __forceinline__ float half_at(const v4i& w, int idx) {
   const uint32_t x = (uint32_t)w[idx >> 1];
   return half_bits_to_float((idx & 1) ? (x >> 16) : (x & 0xffff));
 }
 
-template <class T>
-__device__ __forceinline__ T ld_nt(const void* p) {
-  return __builtin_nontemporal_load((const T*)p);
+// The builtins return unsigned vectors; convert with bit_cast only (an
+// implicit conversion to a signed vector type can turn into a splat of lane 0).
+template <int POL = BUF_NT>
+__device__ __forceinline__ v4i ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL));
+}
+template <int POL = BUF_NT>
+__device__ __forceinline__ v2i ld64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL));
+}
+template <int POL = BUF_NT>
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL);
 }
 
-// Issue every load of the chunk (cache block) starting at token t0, a
-// multiple of 32.  The KV cache is streamed once, so the loads are nontemporal.
+// Per-lane byte offsets inside a cache block (fixed for the whole kernel).
+struct LaneOff {
+  uint32_t k[2];  // K codes, tile j (the second MFMA half is +2048 / +1024)
+  uint32_t ks;    // int8 K scales
+  uint32_t ks4;   // int4 K scale / zero-point, first group (second: +128)
+  uint32_t v;     // V codes, dim block 0 (block n: +512 n / +256 n)
+  uint32_t vs;    // int8 V scales
+  uint32_t vs4;   // int4 V scale / zero-point, group 0 (group g: +64 g)
+};
+
 template <int KB, int VB>
-__device__ __forceinline__ void load_chunk(Chunk& R, const Bases& B, int t0, int lane) {
+__device__ __forceinline__ LaneOff lane_offsets(int lane) {
   const int c = lane & 15, kg = lane >> 4;
-  const int blk = t0 >> 5;
+  LaneOff o;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) o.k[j] = KB == 8 ? (16 * j + c) * 64 + 16 * kg : (16 * j + c) * 32 + 8 * kg;
+  o.ks = 16 * kg;
+  o.ks4 = ((c >> 3) * 32 + 8 * kg) * 2;
+  o.v = VB == 8 ? c * 32 + 8 * kg : c * 16 + 4 * kg;
+  o.vs = 16 * kg;
+  o.vs4 = 8 * kg * 2;
+  return o;
+}
+
+// Issue every load of cache block `blk` of the slice, or (ok false) the same
+// loads through the empty resource.
+template <int KB, int VB>
+__device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff& o, bool ok, uint32_t blk) {
+  const __amdgpu_buffer_rsrc_t rk = ok ? S.k : S.none, rks = ok ? S.ks : S.none, rkz = ok ? S.kz : S.none;
+  const __amdgpu_buffer_rsrc_t rv = ok ? S.v : S.none, rvs = ok ? S.vs : S.none, rvz = ok ? S.vz : S.none;
   // Q·Kᵀ tile j, row r is token 16j + r of the block; the MFMA leaves lane
   // (c, kg) holding the scores of tokens 16j + 4kg + i, i.e. block positions
   // 8kg .. 8kg+7 in the order idx = 4j + i.
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     if constexpr (KB == 8) {
-      const int8_t* p = B.k + blk * 4096 + (16 * j + c) * 64 + 16 * kg;
-      R.k8[j][0] = ld_nt<v4i>(p);
-      R.k8[j][1] = ld_nt<v4i>(p + 2048);
+      R.k8[j][0] = ld128(rk, o.k[j], blk * 4096);
+      R.k8[j][1] = ld128(rk, o.k[j] + 2048, blk * 4096);
     } else {
-      const int8_t* p = B.k + blk * 2048 + (16 * j + c) * 32 + 8 * kg;
-      R.k4[j][0] = ld_nt<v2i>(p);
-      R.k4[j][1] = ld_nt<v2i>(p + 1024);
+      R.k4[j][0] = ld64(rk, o.k[j], blk * 2048);
+      R.k4[j][1] = ld64(rk, o.k[j] + 1024, blk * 2048);
     }
   }
   if constexpr (KB == 8) {
-    R.ks = ld_nt<v4i>(B.ks + blk * 32 + 8 * kg);
+    R.ks = ld128(rks, o.ks, blk * 64);
   } else {
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
-      const int off = blk * 128 + (2 * gi + (c >> 3)) * 32 + 8 * kg;
-      R.ks4[gi] = ld_nt<v4i>(B.ks + off);
-      R.kz4[gi] = ld_nt<v4i>(B.kz + off);
+      R.ks4[gi] = ld128(rks, o.ks4 + 128 * gi, blk * 256);
+      R.kz4[gi] = ld128(rkz, o.ks4 + 128 * gi, blk * 256);
     }
   }
   // V block n: lane (c, kg) gets dim 16n+c at block positions 8kg .. 8kg+7
   if constexpr (VB == 8) {
-    const int8_t* p = B.v + blk * 4096 + c * 32 + 8 * kg;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) R.v8[n] = ld_nt<v2i>(p + n * 512);
-    R.vs = ld_nt<v4i>(B.vs + blk * 32 + 8 * kg);
+    for (int n = 0; n < 8; ++n) R.v8[n] = ld64(rv, o.v + n * 512, blk * 4096);
+    R.vs = ld128(rvs, o.vs, blk * 64);
   } else {
-    const int8_t* p = B.v + blk * 2048 + c * 16 + 4 * kg;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) R.v4[n] = ld_nt<uint32_t>(p + n * 256);
+    for (int n = 0; n < 8; ++n) R.v4[n] = ld32(rv, o.v + n * 256, blk * 2048);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int off = blk * 128 + g * 32 + 8 * kg;
-      R.vs4[g] = ld_nt<v4i>(B.vs + off);
-      R.vz4[g] = ld_nt<v4i>(B.vz + off);
+      R.vs4[g] = ld128(rvs, o.vs4 + 64 * g, blk * 256);
+      R.vz4[g] = ld128(rvz, o.vs4 + 64 * g, blk * 256);
     }
   }
 }
@@ -315,7 +373,8 @@ struct Depth {
 template <int KB, int VB>
 __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, kg = lane >> 4;
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * a.Hkv + h;
@@ -331,13 +390,18 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     t_end = t_begin + a.span < a.t_split_end ? t_begin + a.span : a.t_split_end;
   }
 
-  Bases B;
-  B.k = (const int8_t*)a.kq + bh * cap * (KB == 8 ? HEAD_DIM : HEAD_DIM / 2);
-  B.v = (const int8_t*)a.vq + bh * cap * (VB == 8 ? HEAD_DIM : HEAD_DIM / 2);
-  B.ks = a.ks + bh * cap * (KB == 8 ? 1 : 4);
-  B.kz = KB == 4 ? a.kz + bh * cap * 4 : nullptr;
-  B.vs = a.vs + bh * cap * (VB == 8 ? 1 : 4);
-  B.vz = VB == 4 ? a.vz + bh * cap * 4 : nullptr;
+  constexpr int64_t KROW = KB == 8 ? HEAD_DIM : HEAD_DIM / 2;  // code bytes per token
+  constexpr int64_t VROW = VB == 8 ? HEAD_DIM : HEAD_DIM / 2;
+  constexpr int64_t KSROW = KB == 8 ? 1 : 4;                   // fp16 scales per token
+  constexpr int64_t VSROW = VB == 8 ? 1 : 4;
+  Res R;
+  R.k = make_rsrc((const int8_t*)a.kq + bh * cap * KROW, cap * KROW);
+  R.v = make_rsrc((const int8_t*)a.vq + bh * cap * VROW, cap * VROW);
+  R.ks = make_rsrc(a.ks + bh * cap * KSROW, cap * KSROW * 2);
+  R.vs = make_rsrc(a.vs + bh * cap * VSROW, cap * VSROW * 2);
+  R.kz = KB == 4 ? make_rsrc(a.kz + bh * cap * 4, cap * 8) : R.ks;
+  R.vz = VB == 4 ? make_rsrc(a.vz + bh * cap * 4, cap * 8) : R.vs;
+  R.none = make_rsrc(a.ks, 0);
 
   // Fused append of the newest token (position T-1), before this split reads it.
   if (tail) {
@@ -357,17 +421,32 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     __syncthreads();
   }
 
-  // Start streaming before the query is prepared: the first chunks' loads
-  // overlap the query load and quantization.
-  constexpr int NBUF = Depth<KB, VB>::value;
-  constexpr int STEP = WAVES * CH;
-  Chunk buf[NBUF];
-  int t = t_begin + wave * CH;
-#pragma unroll
-  for (int i = 0; i < NBUF - 1; ++i)
-    if (t + i * STEP < t_end) load_chunk<KB, VB>(buf[i], B, t + i * STEP, lane);
+  // The query rows are loaded first: everything below overlaps their latency.
+  const int hh = tid >> 5, d0 = (tid & 31) * 4;
+  const int hq_ld = h * a.G + (hh < a.G ? hh : 0);
+  const v4i qraw = load_q_raw(a.q, (int64_t)b * a.q_sb + (int64_t)hq_ld * a.q_sh + d0, a.q_dtype);
 
-  prepare_query<KB>(a, b, h, smem, tid);
+  // Wave w takes chunks w, w+4, ... of the split; a ring of NBUF chunk buffers
+  // keeps NBUF-1 chunks in flight while one is computed.  Slots past the
+  // wave's last chunk load nothing (NO_CHUNK) but are still issued.
+  constexpr int NBUF = Depth<KB, VB>::value;
+  const int n_split = (t_end - t_begin + CH - 1) / CH;
+  const int n_w = n_split > wave ? (n_split - wave + WAVES - 1) / WAVES : 0;
+  const int blk0 = t_begin / CH + wave;
+  const LaneOff lo = lane_offsets<KB, VB>(lane);
+  Chunk buf[NBUF];
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i) load_chunk<KB, VB>(buf[i], R, lo, i < n_w, blk0 + WAVES * i);
+
+  // Quantize the query into MFMA operands while the chunks stream in.
+  {
+    float x[4];
+    q_raw_to_float(qraw, a.q_dtype, x);
+    const float mul = hh < a.G ? a.q_mul : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] *= mul;
+    prepare_query<KB>(x, smem, tid);
+  }
   __syncthreads();
 
   constexpr int NOP = KB == 8 ? 2 : 4;
@@ -390,19 +469,20 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) st.corr[g] = 0.f;
 
-  // Ring of NBUF chunk buffers, unrolled so every buffer index is static:
-  // while buffer i is consumed, the loads of the chunk NBUF-1 ahead are in flight.
-  bool more = t < t_end;
-  while (more) {
+  // Step i loads chunk i+NBUF-1 into the buffer freed by step i-1, then
+  // computes chunk i.  The ring is unrolled so buffer indices are static, and
+  // the step count is padded to a whole number of revolutions: every step
+  // issues its loads (padding steps through the empty resource), only the
+  // compute of padding steps is skipped, and the loop has a single back edge.
+  // The compiler then counts the loads in flight exactly on every path.
+  const int n_pad = (n_w + NBUF - 1) / NBUF * NBUF;
+  for (int i0 = 0; i0 < n_pad; i0 += NBUF) {
 #pragma unroll
-    for (int i = 0; i < NBUF; ++i) {
-      if (more) {
-        const int ahead = t + (NBUF - 1) * STEP;
-        if (ahead < t_end) load_chunk<KB, VB>(buf[(i + NBUF - 1) % NBUF], B, ahead, lane);
-        process_chunk<KB, VB>(buf[i], st, qop, qsc, qsum_a, qsum_b, t_end - t, lane);
-        t += STEP;
-        more = t < t_end;
-      }
+    for (int j = 0; j < NBUF; ++j) {
+      const int i = i0 + j;
+      load_chunk<KB, VB>(buf[(j + NBUF - 1) % NBUF], R, lo, i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1));
+      if (i < n_w)
+        process_chunk<KB, VB>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane);
     }
   }
 
@@ -435,7 +515,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   __syncthreads();
 
   // ---------------- workgroup partial (or the output when S == 1) ----------------
-  const int hh = tid >> 5, d0 = (tid & 31) * 4;
   if (hh < a.G) {
     float mw[WAVES], M = NEG_INF;
 #pragma unroll
@@ -469,8 +548,10 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 }
 
 // Cross-split merge (megakernel.py:276-318): one workgroup per (query head,
-// batch).  Thread (sg, d4) sums splits sg, sg+8, ... for dims 4*d4..4*d4+3;
-// every partial load is issued before the first is used.
+// batch).  Thread (sg, d4) sums splits sg, sg+8, ... for dims 4*d4..4*d4+3.
+// Every load is an unconditional buffer load issued before the first result is
+// used (slots past the last split read zeros), so the kernel waits for memory
+// once.
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
   __shared__ float red[8];
   __shared__ float wts[MAX_SPLITS];
@@ -481,19 +562,21 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
   const int64_t bh = (int64_t)b * a.Hkv + h;
   const int S = a.S;
   constexpr int PER = MAX_SPLITS / 8;
+  // partials of this (b, h): [S][8][128] floats and [S][8][2] stats
+  const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.ws_acc + bh * S * 8 * HEAD_DIM, (int64_t)S * 8 * HEAD_DIM * 4);
+  const __amdgpu_buffer_rsrc_t rst = make_rsrc(a.ws_stat + bh * S * 8 * 2, (int64_t)S * 8 * 2 * 4);
   v4f v[PER];
-  const float* src = a.ws_acc + ((bh * S) * 8 + hh) * HEAD_DIM + 4 * d4;
+  const uint32_t voff = (uint32_t)((hh * HEAD_DIM + 4 * d4) * 4);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const int sp = sg + 8 * i;
-    v[i] = sp < S ? *(const v4f*)(src + (int64_t)sp * 8 * HEAD_DIM) : (v4f){0.f, 0.f, 0.f, 0.f};
+    const uint32_t sp = (uint32_t)(sg + 8 * i);
+    // the whole offset in voffset: it is range-checked (soffset may not be)
+    v[i] = __builtin_bit_cast(v4f, ld128<0>(racc, voff + sp * 8 * HEAD_DIM * 4, 0));
   }
-  float ms = NEG_INF, ls = 0.f;
-  if (tid < S) {
-    const v2f st = *(const v2f*)(a.ws_stat + ((bh * S + tid) * 8 + hh) * 2);
-    ms = st[0];
-    ls = st[1];
-  }
+  const v2i stw = ld64<0>(rst, (uint32_t)((tid * 8 + hh) * 8), 0);
+  const int m_bits = stw[0], l_bits = stw[1];  // copies: bit_cast of a vector subscript reads lane 0
+  const float ms = tid < S ? __builtin_bit_cast(float, m_bits) : NEG_INF;
+  const float ls = tid < S ? __builtin_bit_cast(float, l_bits) : 0.f;
   float M = wave_max(ms);
   if ((tid & 63) == 0) red[tid >> 6] = M;
   __syncthreads();
@@ -512,10 +595,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
   if ((tid & 63) == 0) red[4 + (tid >> 6)] = lw;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int sp = sg + 8 * i;
-    if (sp < S) acc += wts[sp] * v[i];
-  }
+  for (int i = 0; i < PER; ++i) acc += wts[sg + 8 * i] * v[i];
   acc_part[sg][d4] = acc;
   __syncthreads();
   if (sg == 0) {

@@ -14,7 +14,31 @@ struct RowSrc {
   const void* p;
   int dtype;
   int64_t sb, sh, st;  // element strides for batch, head, token (dim stride 1)
+  int vec;             // p is 16-byte aligned and every stride a multiple of 4 elements
 };
+
+// Elements i, i+1 (i even) of a row as floats: one load when src.vec.
+__device__ __forceinline__ void load2_as_float(const RowSrc& s, int64_t i, float& x0, float& x1) {
+  if (s.vec) {
+    if (s.dtype == DT_F32) {
+      const v2f v = *(const v2f*)((const float*)s.p + i);
+      x0 = v[0];
+      x1 = v[1];
+    } else {
+      const uint32_t w = *(const uint32_t*)((const uint16_t*)s.p + i);
+      if (s.dtype == DT_F16) {
+        x0 = half_bits_to_float(w & 0xffffu);
+        x1 = half_bits_to_float(w >> 16);
+      } else {
+        x0 = __builtin_bit_cast(float, w << 16);
+        x1 = __builtin_bit_cast(float, w & 0xffff0000u);
+      }
+    }
+  } else {
+    x0 = load_as_float(s.p, i, s.dtype);
+    x1 = load_as_float(s.p, i + 1, s.dtype);
+  }
+}
 
 __device__ __forceinline__ int64_t row_base(const RowSrc& s, int b, int h, int t) {
   return (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st;
@@ -95,8 +119,8 @@ __device__ __forceinline__ void append_row(const RowSrc& src, int b, int h, int 
                                            uint16_t* scales, uint16_t* zeros, int64_t bh, int64_t cap,
                                            int64_t pos, int lane) {
   const int64_t base = row_base(src, b, h, t_src);
-  const float x0 = load_as_float(src.p, base + 2 * lane, src.dtype);
-  const float x1 = load_as_float(src.p, base + 2 * lane + 1, src.dtype);
+  float x0, x1;
+  load2_as_float(src, base + 2 * lane, x0, x1);
   if constexpr (BITS == 8) {
     int q0, q1;
     uint16_t sb;
@@ -134,8 +158,8 @@ __device__ __forceinline__ void append_v4_pair(const RowSrc& src, int b, int h, 
     const bool has = r == 0 ? has_even : has_odd;
     if (!has) continue;  // wave-uniform
     const int64_t base = row_base(src, b, h, t_even + r);
-    const float x0 = load_as_float(src.p, base + 2 * lane, src.dtype);
-    const float x1 = load_as_float(src.p, base + 2 * lane + 1, src.dtype);
+    float x0, x1;
+    load2_as_float(src, base + 2 * lane, x0, x1);
     int q0, q1;
     uint16_t sb, zb;
     quantize_u4_pair(x0, x1, q0, q1, sb, zb);
