@@ -547,65 +547,71 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   }
 }
 
-// Cross-split merge (megakernel.py:276-318): one workgroup per (query head,
-// batch).  Thread (sg, d4) sums splits sg, sg+8, ... for dims 4*d4..4*d4+3.
-// Every load is an unconditional buffer load issued before the first result is
-// used (slots past the last split read zeros), so the kernel waits for memory
-// once.
-__global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeArgs a) {
-  __shared__ float red[8];
-  __shared__ float wts[MAX_SPLITS];
-  __shared__ v4f acc_part[8][32];
-  const int tid = threadIdx.x, d4 = tid & 31, sg = tid >> 5;
-  const int hq = blockIdx.x, b = blockIdx.y;
-  const int h = hq / a.G, hh = hq % a.G;
+// Cross-split merge (megakernel.py:276-318).  One wavefront per (query head,
+// quarter of the dims, batch): lane (sg, d4) sums splits sg, sg+8, ... for
+// dims 32*quarter + 4*d4 .. +3, and lane l also owns the (m, l) statistics of
+// splits l, l+64, ...  Every load (partials, statistics, sink) is issued at
+// entry as an unconditional buffer load (slots past the last split read zeros)
+// and the reductions stay inside the wavefront, so the kernel makes a single
+// trip to memory.
+template <int PER>  // splits per lane group: S <= 8 * PER
+__global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
+  __shared__ float wts[8 * PER];
+  constexpr int SPL = (8 * PER + 63) / 64;  // statistics slots per lane
+  const int lane = threadIdx.x, d4 = lane & 7, sg = lane >> 3;
+  const int hq = blockIdx.x >> 2, qd = blockIdx.x & 3, b = blockIdx.y;
+  const int h = hq / a.G, hh = hq - h * a.G;
   const int64_t bh = (int64_t)b * a.Hkv + h;
   const int S = a.S;
-  constexpr int PER = MAX_SPLITS / 8;
-  // partials of this (b, h): [S][8][128] floats and [S][8][2] stats
+  // partials of this (b, h): [S][8][128] floats and [S][8][2] statistics
   const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.ws_acc + bh * S * 8 * HEAD_DIM, (int64_t)S * 8 * HEAD_DIM * 4);
   const __amdgpu_buffer_rsrc_t rst = make_rsrc(a.ws_stat + bh * S * 8 * 2, (int64_t)S * 8 * 2 * 4);
+  const uint32_t voff = (uint32_t)((hh * HEAD_DIM + 32 * qd + 4 * d4) * 4);
   v4f v[PER];
-  const uint32_t voff = (uint32_t)((hh * HEAD_DIM + 4 * d4) * 4);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const uint32_t sp = (uint32_t)(sg + 8 * i);
-    // the whole offset in voffset: it is range-checked (soffset may not be)
-    v[i] = __builtin_bit_cast(v4f, ld128<0>(racc, voff + sp * 8 * HEAD_DIM * 4, 0));
+  for (int i = 0; i < PER; ++i)  // whole offset in voffset: it is range-checked (soffset may not be)
+    v[i] = __builtin_bit_cast(v4f, ld128<0>(racc, voff + (uint32_t)(sg + 8 * i) * 8 * HEAD_DIM * 4, 0));
+  v2i stw[SPL];
+#pragma unroll
+  for (int k = 0; k < SPL; ++k) stw[k] = ld64<0>(rst, (uint32_t)(((lane + 64 * k) * 8 + hh) * 8), 0);
+  // the sink logit through a buffer too (no sinks: an empty resource reads 0),
+  // so it joins the same batch of loads instead of a scalar load waited on first
+  const bool has_sink = a.sinks != nullptr;
+  const __amdgpu_buffer_rsrc_t rsk = make_rsrc(has_sink ? a.sinks : a.ws_stat, has_sink ? a.Hq * 4 : 0);
+  const uint32_t sink_bits = ld32<0>(rsk, (uint32_t)hq * 4, 0);
+
+  float ms[SPL], ls[SPL], M = NEG_INF;
+#pragma unroll
+  for (int k = 0; k < SPL; ++k) {
+    const int m_bits = stw[k][0], l_bits = stw[k][1];  // copies: bit_cast of a vector subscript reads lane 0
+    const bool ok = lane + 64 * k < S;
+    ms[k] = ok ? __builtin_bit_cast(float, m_bits) : NEG_INF;
+    ls[k] = ok ? __builtin_bit_cast(float, l_bits) : 0.f;
+    M = fmaxf(M, ms[k]);
   }
-  const v2i stw = ld64<0>(rst, (uint32_t)((tid * 8 + hh) * 8), 0);
-  const int m_bits = stw[0], l_bits = stw[1];  // copies: bit_cast of a vector subscript reads lane 0
-  const float ms = tid < S ? __builtin_bit_cast(float, m_bits) : NEG_INF;
-  const float ls = tid < S ? __builtin_bit_cast(float, l_bits) : 0.f;
-  float M = wave_max(ms);
-  if ((tid & 63) == 0) red[tid >> 6] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float sink = NEG_INF;
-  if (a.sinks != nullptr) {
-    sink = a.sinks[hq] * LOG2E;
-    M = fmaxf(M, sink);
+  const float sink = has_sink ? __builtin_bit_cast(float, sink_bits) * LOG2E : NEG_INF;
+  M = fmaxf(wave_max(M), sink);
+  float lw = 0.f;
+#pragma unroll
+  for (int k = 0; k < SPL; ++k) {
+    const float w = (ms[k] == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(ms[k] - M);
+    lw += w * ls[k];
+    if (lane + 64 * k < 8 * PER) wts[lane + 64 * k] = w;
   }
-  const float w = (ms == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-  if (tid < MAX_SPLITS) wts[tid] = w;
-  float lw = w * ls;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) lw += __shfl_xor(lw, m, 64);
   __syncthreads();
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = lw;
   v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < PER; ++i) acc += wts[sg + 8 * i] * v[i];
-  acc_part[sg][d4] = acc;
-  __syncthreads();
-  if (sg == 0) {
-    float L = red[4] + red[5] + red[6] + red[7];
-    if (sink != NEG_INF) L += __builtin_amdgcn_exp2f(sink - M);
-    v4f t = acc_part[0][d4];
 #pragma unroll
-    for (int g = 1; g < 8; ++g) t += acc_part[g][d4];
-    const v4f o = L > 0.f ? t / L : t;
-    *(v4f*)(a.out + ((int64_t)b * a.Hq + hq) * HEAD_DIM + 4 * d4) = o;
+  for (int m = 8; m < 64; m <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], m, 64);
+  if (sg == 0) {
+    const float L = sink != NEG_INF ? lw + __builtin_amdgcn_exp2f(sink - M) : lw;
+    const v4f o = L > 0.f ? acc / L : acc;
+    *(v4f*)(a.out + ((int64_t)b * a.Hq + hq) * HEAD_DIM + 32 * qd + 4 * d4) = o;
   }
 }
 
@@ -620,7 +626,13 @@ hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_
 
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream) {
   if (a.S == 1) return hipSuccess;  // the partial kernel wrote the output
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(a.Hq, a.B), dim3(256), 0, stream, a);
+  const dim3 grid(a.Hq * 4, a.B), block(64);
+  if (a.S <= 8) hipLaunchKernelGGL(decode_merge_kernel<1>, grid, block, 0, stream, a);
+  else if (a.S <= 16) hipLaunchKernelGGL(decode_merge_kernel<2>, grid, block, 0, stream, a);
+  else if (a.S <= 32) hipLaunchKernelGGL(decode_merge_kernel<4>, grid, block, 0, stream, a);
+  else if (a.S <= 64) hipLaunchKernelGGL(decode_merge_kernel<8>, grid, block, 0, stream, a);
+  else if (a.S <= 128) hipLaunchKernelGGL(decode_merge_kernel<16>, grid, block, 0, stream, a);
+  else hipLaunchKernelGGL(decode_merge_kernel<32>, grid, block, 0, stream, a);
   return hipGetLastError();
 }
 
