@@ -11,9 +11,11 @@
  * multiple of 32, head_dim D = 128, scales and zero-points are IEEE fp16 bit
  * patterns; token t of a block sits at position p = 8*((t>>2)&3) + 4*(t>>4) + (t&3)):
  *   int8 K codes  int8  [B][Hkv][C/32][2][32][64]   half m = dims 64m..64m+63, row = token t
- *   int4 K codes  uint8 [B][Hkv][C/32][2][32][32]   same, low nibble = even dim
+ *   int4 K codes  uint8 [B][Hkv][C/32][32][4][2][8]  row = token t, [byte run r][half m][8 bytes]:
+ *                                                   byte 8r+i of half m holds dims 64m+16r+2i, +1 (low nibble even)
  *   int8 V codes  int8  [B][Hkv][C/32][128][32]     dim-major, column = position p
- *   int4 V codes  uint8 [B][Hkv][C/32][128][16]     byte p/2, low nibble = even p
+ *   int4 V codes  uint8 [B][Hkv][C/32][2][16][4][4][4]  dim 16n+c, position p = 8g+e at
+ *                                                   [n/4][c][g][n%4][e/2], low nibble = even e
  *   int8 scales   fp16  [B][Hkv][C/32][32]          one per (token, head), position p
  *   int4 scale/zp fp16  [B][Hkv][C/32][4][32]       per 32-dim group, position p
  * Quantizers: int8 symmetric s = fp16(amax/127), q = clamp(rint(x/s), ±127);

@@ -97,13 +97,16 @@ def to_logical(kv: QuantizedKV, length: Optional[int] = None):
     T = kv.length if length is None else length
     B, H, nb = kv.codes.shape[:3]
     pos = torch.tensor(_POS, device=kv.codes.device)
-    if not kv.blocked:  # K: [nb][2 halves][32 tokens][64 or 32 bytes]
-        w = HEAD_DIM // 2 if kv.bits == 8 else HEAD_DIM // 4
+    if not kv.blocked and kv.bits == 8:  # K: [nb][2 halves][32 tokens][64 bytes]
+        w = HEAD_DIM // 2
         codes = kv.codes.view(B, H, nb, 2, BLOCK, w).permute(0, 1, 2, 4, 3, 5).reshape(B, H, nb * BLOCK, 2 * w)
+    elif not kv.blocked:  # K: [nb][32 tokens][4 byte groups][2 halves][8 bytes]
+        codes = kv.codes.view(B, H, nb, BLOCK, 4, 2, 8).permute(0, 1, 2, 3, 5, 4, 6).reshape(B, H, nb * BLOCK, 64)
     elif kv.bits == 8:  # V: [nb][128 dims][32 positions]
         codes = kv.codes.view(B, H, nb, HEAD_DIM, BLOCK)[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
-    else:  # V: [nb][128 dims][16 bytes], position p in byte p // 2
-        packed = kv.codes.view(B, H, nb, HEAD_DIM, BLOCK // 2)
+    else:  # V: [nb][n / 4][c][position group][n % 4][4 bytes], dim 16 n + c, position p in byte p // 2
+        packed = kv.codes.view(B, H, nb, 2, 16, 4, 4, 4)  # (h, c, pg, n4, byte)
+        packed = packed.permute(0, 1, 2, 3, 6, 4, 5, 7).reshape(B, H, nb, HEAD_DIM, BLOCK // 2)  # (n, c) -> dim
         q = torch.stack([packed & 0xF, packed >> 4], -1).reshape(B, H, nb, HEAD_DIM, BLOCK)[..., pos]
         q = q.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
         codes = (q[..., 0::2] | (q[..., 1::2] << 4)).to(torch.uint8)

@@ -4,14 +4,18 @@
 // a multiple of 32, blk = t / 32, t' = t % 32, p = pi(t') the position of
 // token t' inside its block, see block_pos()):
 //   int8 K codes   int8  [B][Hkv][C/32][2][32][64]   half m holds dims 64m..64m+63 of token t'
-//   int4 K codes   uint8 [B][Hkv][C/32][2][32][32]   half m packed, low nibble = even dim
+//   int4 K codes   uint8 [B][Hkv][C/32][32][4][2][8] row t', [byte run r][half m][8 bytes]: byte
+//                                                   8r+i of half m = dims 64m+16r+2i, +1 (low nibble even)
 //   int8 V codes   int8  [B][Hkv][C/32][128][32]     dim-major, token t' at position p
-//   int4 V codes   uint8 [B][Hkv][C/32][128][16]     position p in byte p/2, low nibble = even p
+//   int4 V codes   uint8 [B][Hkv][C/32][2][16][4][4][4]  dim 16n+c, position p = 8g+e at
+//                                                   [n/4][c][g][n%4][e/2], low nibble = even e
 //   int8 scales    fp16  [B][Hkv][C/32][32]          one per (token, head), K and V, position p
 //   int4 scale/zp  fp16  [B][Hkv][C/32][4][32]       per 32-dim group, position p
-// Every load of the decode kernel reads one contiguous span: a Q·Kᵀ operand
-// is 16 tokens x 64 bytes of one K half, a P·V operand 16 dims x 32 tokens,
-// and a lane's eight scales are 16 adjacent bytes.
+// Every load of the decode kernel reads one contiguous span: an int8 Q·Kᵀ
+// operand is 16 tokens x 64 bytes of one K half, an int8 P·V operand 16 dims x
+// 32 tokens, an int4 lane's K bytes (both halves) and V bytes (four dim
+// blocks) are 16 adjacent bytes, and int4 scales / zero-points are read one
+// dword per lane and handed out through LDS.
 #pragma once
 
 #include <hip/hip_runtime.h>

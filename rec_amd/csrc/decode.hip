@@ -28,12 +28,12 @@
 // of the query per head (relative error < 2^-16 of the head's largest
 // element), well inside the 1e-3 output tolerance.
 //
-// P·V runs on v_mfma_f32_16x16x32_f16 with A = Vᵀ (16 dims × 32 tokens, exact
-// small integers in fp16) and B = P'ᵀ where P' = p · v_scale is rounded to fp16
-// once, as the reference rounds probabilities to the query dtype
-// (model.py:132-133).  The token-blocked V layout makes each A operand one
-// 16-byte load.  int4 V: P' carries each group's scale, the zero-point enters
-// as a per-group correction Σ P'·z computed from the same rounded P'.
+// P·V runs on v_mfma_f32_16x16x32_f16.  int8 V: A = Vᵀ (16 dims × 32 tokens,
+// exact small integers in fp16) and B = P'ᵀ where P' = p · v_scale is rounded
+// to fp16 once, as the reference rounds probabilities to the query dtype
+// (model.py:132-133).  uint4 V: A = the dequantized (q - z) · s in fp16 (one
+// rounding) and B = p in fp16.  The token-blocked V layout makes each A operand
+// one load per lane.
 //
 // Softmax runs in the log2 domain (log2(e) folded into the query scale).
 #include "kernels.h"
@@ -42,7 +42,8 @@ namespace rec {
 
 
 constexpr int MAX_SPLITS = DECODE_MAX_SPLITS;
-constexpr int WAVES = 4;
+constexpr int WAVES = 4;  // wavefronts per workgroup
+constexpr int THREADS = 64 * WAVES;
 constexpr float Q16 = 32512.0f;  // int16 query range: hi, lo stay inside int8
 
 // LDS layout (bytes)
@@ -51,11 +52,20 @@ constexpr int LDS_QSC = 4096;                              // 8 floats: per-head
 constexpr int LDS_QSUM = LDS_QSC + 32;                     // 8 x 4 ints: per-group query sums (int4 K)
 constexpr int LDS_PART = 4352;                             // wave partials: 4 x 8 x 128 floats
 constexpr int LDS_PSTAT = LDS_PART + WAVES * 8 * 128 * 4;  // 4 x 8 x (m, l)
-constexpr int LDS_BYTES = LDS_PSTAT + WAVES * 8 * 8;
+constexpr int LDS_META = LDS_PSTAT + WAVES * 8 * 8;       // int4: per wave [4 arrays][256 B] of one block
+constexpr int LDS_BYTES = LDS_META + WAVES * 1024;
 
 // Order in which widen_u4() lays out 16 packed nibbles (8 bytes): unpacked byte
 // j holds element perm16(j) of the 16.
 __device__ __forceinline__ int u4_unpacked_pos(int o) { return (o & 8) + 4 * (o & 1) + ((o & 7) >> 1); }
+
+// (x & m) | o in one v_and_or_b32 (the compiler splits it when both constants
+// would need the single scalar operand slot).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+  return r;
+}
 
 __device__ __forceinline__ v4i widen_u4(v2i w) {
   const uint32_t w0 = (uint32_t)w[0], w1 = (uint32_t)w[1];
@@ -100,9 +110,10 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
   float* qsc = (float*)(smem + LDS_QSC);
   int* qsum = (int*)(smem + LDS_QSUM);
   if constexpr (KB == 4) {
-    for (int i = tid; i < 1024; i += 256) ((int*)qop)[i] = 0;
+    for (int i = tid; i < 1024; i += THREADS) ((int*)qop)[i] = 0;
     __syncthreads();
   }
+  if (tid >= 256) return;  // threads (hh, d0) cover 8 heads x 128 dims
   const int hh = tid >> 5, d0 = (tid & 31) * 4;
   float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
 #pragma unroll
@@ -144,15 +155,12 @@ constexpr int CH = BLOCK_T;
 // does not use are never touched and vanish.
 struct Chunk {
   v4i k8[2][2];   // int8 K: tile j, MFMA half m (16 bytes each)
-  v2i k4[2][2];   // int4 K: tile j, group pair (8 packed bytes each)
+  v4i k4[2];      // int4 K: tile j, both halves (8 packed bytes each)
   v4i ks;         // int8 K: scales of this lane's 8 tokens
-  v4i ks4[2];     // int4 K: scales, this lane's two groups
-  v4i kz4[2];     // int4 K: zero-points
   v2i v8[8];      // int8 V: dim block n, this lane's 8 tokens
-  uint32_t v4[8]; // int4 V: dim block n, this lane's 8 tokens packed
+  v4i v4[2];      // int4 V: dim blocks 4h..4h+3, this lane's 8 tokens packed
   v4i vs;         // int8 V: scales of this lane's 8 tokens
-  v4i vs4[4];     // int4 V: scales, all four groups
-  v4i vz4[4];     // int4 V: zero-points
+  uint32_t m4[4]; // int4: one dword per lane of the block's K scales, K zeros, V scales, V zeros
 };
 
 // Buffer resources of one (b, h) slice of the cache, plus an empty one.  Every
@@ -197,12 +205,11 @@ __device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff
 
 // Per-lane byte offsets inside a cache block (fixed for the whole kernel).
 struct LaneOff {
-  uint32_t k[2];  // K codes, tile j (the second MFMA half is +2048 / +1024)
+  uint32_t k[2];  // K codes, tile j (int8: the second MFMA half is +2048)
   uint32_t ks;    // int8 K scales
-  uint32_t ks4;   // int4 K scale / zero-point, first group (second: +128)
-  uint32_t v;     // V codes, dim block 0 (block n: +512 n / +256 n)
+  uint32_t v;     // V codes (int8: dim block n at +512 n; int4: dim blocks 4h.. at +1024 h)
   uint32_t vs;    // int8 V scales
-  uint32_t vs4;   // int4 V scale / zero-point, group 0 (group g: +64 g)
+  uint32_t m4;    // int4 scale / zero-point dword of this lane
 };
 
 template <int KB, int VB>
@@ -210,12 +217,11 @@ __device__ __forceinline__ LaneOff lane_offsets(int lane) {
   const int c = lane & 15, kg = lane >> 4;
   LaneOff o;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) o.k[j] = KB == 8 ? (16 * j + c) * 64 + 16 * kg : (16 * j + c) * 32 + 8 * kg;
+  for (int j = 0; j < 2; ++j) o.k[j] = (16 * j + c) * 64 + 16 * kg;
   o.ks = 16 * kg;
-  o.ks4 = ((c >> 3) * 32 + 8 * kg) * 2;
-  o.v = VB == 8 ? c * 32 + 8 * kg : c * 16 + 4 * kg;
+  o.v = VB == 8 ? c * 32 + 8 * kg : (c * 4 + kg) * 16;
   o.vs = 16 * kg;
-  o.vs4 = 8 * kg * 2;
+  o.m4 = 4 * lane;
   return o;
 }
 
@@ -234,18 +240,14 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
       R.k8[j][0] = ld128(rk, o.k[j], blk * 4096);
       R.k8[j][1] = ld128(rk, o.k[j] + 2048, blk * 4096);
     } else {
-      R.k4[j][0] = ld64(rk, o.k[j], blk * 2048);
-      R.k4[j][1] = ld64(rk, o.k[j] + 1024, blk * 2048);
+      R.k4[j] = ld128(rk, o.k[j], blk * 2048);
     }
   }
   if constexpr (KB == 8) {
     R.ks = ld128(rks, o.ks, blk * 64);
   } else {
-#pragma unroll
-    for (int gi = 0; gi < 2; ++gi) {
-      R.ks4[gi] = ld128(rks, o.ks4 + 128 * gi, blk * 256);
-      R.kz4[gi] = ld128(rkz, o.ks4 + 128 * gi, blk * 256);
-    }
+    R.m4[0] = ld32(rks, o.m4, blk * 256);
+    R.m4[1] = ld32(rkz, o.m4, blk * 256);
   }
   // V block n: lane (c, kg) gets dim 16n+c at block positions 8kg .. 8kg+7
   if constexpr (VB == 8) {
@@ -253,26 +255,56 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
     for (int n = 0; n < 8; ++n) R.v8[n] = ld64(rv, o.v + n * 512, blk * 4096);
     R.vs = ld128(rvs, o.vs, blk * 64);
   } else {
-#pragma unroll
-    for (int n = 0; n < 8; ++n) R.v4[n] = ld32(rv, o.v + n * 256, blk * 2048);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      R.vs4[g] = ld128(rvs, o.vs4 + 64 * g, blk * 256);
-      R.vz4[g] = ld128(rvz, o.vs4 + 64 * g, blk * 256);
-    }
+    R.v4[0] = ld128(rv, o.v, blk * 2048);
+    R.v4[1] = ld128(rv, o.v + 1024, blk * 2048);
+    R.m4[2] = ld32(rvs, o.m4, blk * 256);
+    R.m4[3] = ld32(rvz, o.m4, blk * 256);
   }
 }
 
 struct State {
   float m, l;     // running max (log2 domain) and sum of this lane's head
   v4f acc[8];     // P·V accumulators: dims 16n + 4kg + i of head c
-  float corr[4];  // int4 V: Σ P'·z per group
 };
 
 template <int KB, int VB>
-__device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, int qsum_a,
-                                              int qsum_b, int valid, int lane) {
+__device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, float qsum_a,
+                                              float qsum_b, int valid, int lane, char* meta) {
   const int c = lane & 15, kg = lane >> 4;
+  // int4 scales / zero-points: the block's arrays arrive one dword per lane;
+  // this wavefront's LDS region [K scales][K zeros][V scales][V zeros] (256 B
+  // each, [4 groups][32 positions] fp16) hands each lane the 16-byte runs it
+  // needs (positions 8kg .. 8kg+7 of a group).
+  v4i ks4[2], kz4[2], vs4[4], vz4[4];
+  if constexpr (KB == 4 || VB == 4) {
+    uint32_t* mw = (uint32_t*)meta;
+    if constexpr (KB == 4) {
+      mw[lane] = R.m4[0];
+      mw[64 + lane] = R.m4[1];
+    }
+    if constexpr (VB == 4) {
+      mw[128 + lane] = R.m4[2];
+      mw[192 + lane] = R.m4[3];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if constexpr (KB == 4) {
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi) {
+        const int off = (2 * gi + (c >> 3)) * 64 + 16 * kg;  // this lane's groups: 2gi + (c >= 8)
+        ks4[gi] = *(const v4i*)(meta + off);
+        kz4[gi] = *(const v4i*)(meta + 256 + off);
+      }
+    }
+    if constexpr (VB == 4) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        vs4[g] = *(const v4i*)(meta + 512 + g * 64 + 16 * kg);
+        vz4[g] = *(const v4i*)(meta + 768 + g * 64 + 16 * kg);
+      }
+    }
+  }
   // ---------------- scores (log2 domain) ----------------
   float s[8];
 #pragma unroll
@@ -288,7 +320,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         s[4 * j + i] = (float)full * (half_at(R.ks, 4 * j + i) * qsc);
       }
     } else {
-      const v4i ka = widen_u4(R.k4[j][0]), kb = widen_u4(R.k4[j][1]);
+      const v4i ka = widen_u4((v2i){R.k4[j][0], R.k4[j][1]}), kb = widen_u4((v2i){R.k4[j][2], R.k4[j][3]});
       v4i dah = {0, 0, 0, 0}, dal = {0, 0, 0, 0}, dbh = {0, 0, 0, 0}, dbl = {0, 0, 0, 0};
       dah = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qop[0], dah, 0, 0, 0);
       dal = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qop[1], dal, 0, 0, 0);
@@ -297,9 +329,11 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int idx = 4 * j + i;
-        const int ta = dah[i] * 256 + dal[i] - (int)half_at(R.kz4[0], idx) * qsum_a;
-        const int tb = dbh[i] * 256 + dbl[i] - (int)half_at(R.kz4[1], idx) * qsum_b;
-        const float part = half_at(R.ks4[0], idx) * (float)ta + half_at(R.ks4[1], idx) * (float)tb;
+        // Σ (k - z) q over one 32-dim group, in float: |k - z| <= 15 and
+        // |q| <= 32512 keep every intermediate an integer below 2^24, so exact
+        const float ta = fmaf(-half_at(kz4[0], idx), qsum_a, fmaf((float)dah[i], 256.f, (float)dal[i]));
+        const float tb = fmaf(-half_at(kz4[1], idx), qsum_b, fmaf((float)dbh[i], 256.f, (float)dbl[i]));
+        const float part = half_at(ks4[0], idx) * ta + half_at(ks4[1], idx) * tb;
         s[idx] = (part + dpp_ror8f(part)) * qsc;
       }
     }
@@ -320,10 +354,6 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     st.l *= factor;
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.acc[n] *= factor;
-    if constexpr (VB == 4) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) st.corr[g] *= factor;
-    }
     st.m = m_new;
   }
   float p[8];
@@ -344,34 +374,61 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb, st.acc[n], 0, 0, 0);
     }
   } else {
+    // uint4 V is dequantized in the A operand: (q - z) * s per element in
+    // packed fp16 (q - z is exact, one rounding in the product), so the B
+    // operand is the fp16 probabilities alone.  The nibble unpack yields token
+    // pairs (t, t+4) of the lane's eight; scales and zero-points are paired
+    // the same way with byte permutes.
+    v8h pb;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pb[k] = (_Float16)p[(k >> 1) + 4 * (k & 1)];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      v8h pb;
+      // pairs q4 = 0, 2 unpack to 1024 + q: subtract 1024 + z;
+      // pairs q4 = 1, 3 unpack to 1024 + 16 q: (t / 16) - (64 + z), exact
+      v2h sp[4], zq[4];
+      const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int idx = (k >> 1) + 4 * (k & 1);  // order of u4x8_to_h8_interleaved
-        const _Float16 ph = (_Float16)(p[idx] * half_at(R.vs4[g], idx));
-        pb[k] = ph;
-        st.corr[g] += (float)ph * half_at(R.vz4[g], idx);
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const uint32_t s_lo = (uint32_t)vs4[g][h2], s_hi = (uint32_t)vs4[g][h2 + 2];
+        const uint32_t z_lo = (uint32_t)vz4[g][h2], z_hi = (uint32_t)vz4[g][h2 + 2];
+        // word h2 holds tokens (2h2, 2h2+1), word h2+2 tokens (2h2+4, 2h2+5)
+        sp[2 * h2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(s_hi, s_lo, 0x05040100u));
+        sp[2 * h2 + 1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(s_hi, s_lo, 0x07060302u));
+        zq[2 * h2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(z_hi, z_lo, 0x05040100u)) + k1024;
+        zq[2 * h2 + 1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(z_hi, z_lo, 0x07060302u)) + k64;
       }
+      const v2h k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
 #pragma unroll
       for (int nn = 0; nn < 2; ++nn) {
         const int n = 2 * g + nn;
-        st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(u4x8_to_h8_interleaved(R.v4[n]), pb, st.acc[n], 0, 0, 0);
+        const uint32_t w = (uint32_t)R.v4[n >> 2][n & 3], w8 = w >> 8;
+        v8h a;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          // 1024 + q (q4 even) or 1024 + 16 q (q4 odd) for tokens (q4, q4 + 4)
+          const uint32_t src = q4 < 2 ? w : w8;
+          const uint32_t t = and_or(src, (q4 & 1) ? 0x00f000f0u : 0x000f000fu, 0x64006400u);
+          const v2h th = __builtin_bit_cast(v2h, t);
+          const v2h d = (q4 & 1) ? th * k16th - zq[q4] : th - zq[q4];
+          const v2h v = d * sp[q4];
+          a[2 * q4] = v[0];
+          a[2 * q4 + 1] = v[1];
+        }
+        st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, st.acc[n], 0, 0, 0);
       }
     }
   }
 }
 
-// Chunks in flight per wave: three for the int8 formats, two when int4
-// scale/zero-point registers make a chunk larger.
+// Chunk buffers per wave: three (two chunks in flight while one is computed).
 template <int KB, int VB>
 struct Depth {
-  static constexpr int value = (KB == 8 && VB == 8) ? 3 : 2;
+  static constexpr int value = 3;
 };
 
 template <int KB, int VB>
-__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -454,11 +511,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
   for (int o = 0; o < NOP; ++o) qop[o] = ((const v4i*)(smem + LDS_QOP))[o * 64 + lane];
   const float qsc = ((const float*)(smem + LDS_QSC))[c & 7];
-  int qsum_a = 0, qsum_b = 0;  // int4 K: per-group query sums of this lane's two groups
+  float qsum_a = 0.f, qsum_b = 0.f;  // int4 K: per-group query sums of this lane's two groups (exact)
   if constexpr (KB == 4) {
     const int* qsum = (const int*)(smem + LDS_QSUM);
-    qsum_a = qsum[(c & 7) * 4 + (c >> 3)];
-    qsum_b = qsum[(c & 7) * 4 + 2 + (c >> 3)];
+    qsum_a = (float)qsum[(c & 7) * 4 + (c >> 3)];
+    qsum_b = (float)qsum[(c & 7) * 4 + 2 + (c >> 3)];
   }
 
   State st;
@@ -466,8 +523,6 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   st.l = 0.f;
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int g = 0; g < 4; ++g) st.corr[g] = 0.f;
 
   // Step i loads chunk i+NBUF-1 into the buffer freed by step i-1, then
   // computes chunk i.  The ring is unrolled so buffer indices are static, and
@@ -482,20 +537,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       const int i = i0 + j;
       load_chunk<KB, VB>(buf[(j + NBUF - 1) % NBUF], R, lo, i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1));
       if (i < n_w)
-        process_chunk<KB, VB>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane);
+        process_chunk<KB, VB>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane,
+                              smem + LDS_META + wave * 1024);
     }
   }
 
   // ---------------- wave partial -> LDS ----------------
   st.l += shfl_xor_f(st.l, 16);
   st.l += shfl_xor_f(st.l, 32);
-  if constexpr (VB == 4) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      st.corr[g] += shfl_xor_f(st.corr[g], 16);
-      st.corr[g] += shfl_xor_f(st.corr[g], 32);
-    }
-  }
   float* part = (float*)(smem + LDS_PART);
   float* pstat = (float*)(smem + LDS_PSTAT);
   if (c < 8 && c < a.G) {
@@ -503,9 +552,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     for (int n = 0; n < 8; ++n)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float v = st.acc[n][i];
-        if constexpr (VB == 4) v -= st.corr[n >> 1];
-        part[(wave * 8 + c) * HEAD_DIM + 16 * n + 4 * kg + i] = v;
+        part[(wave * 8 + c) * HEAD_DIM + 16 * n + 4 * kg + i] = st.acc[n][i];
       }
     if (kg == 0) {
       pstat[(wave * 8 + c) * 2 + 0] = st.m;
@@ -616,7 +663,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
 }
 
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream) {
-  const dim3 grid(a.S, a.Hkv, a.B), block(256);
+  const dim3 grid(a.S, a.Hkv, a.B), block(THREADS);
   if (kb == 8 && vb == 8) hipLaunchKernelGGL((decode_kernel<8, 8>), grid, block, 0, stream, a);
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((decode_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((decode_kernel<4, 8>), grid, block, 0, stream, a);

@@ -90,17 +90,24 @@ __device__ __forceinline__ int64_t blk_base(int64_t bh, int64_t cap, int64_t t, 
 __device__ __forceinline__ int64_t k8_off(int64_t bh, int64_t cap, int64_t t, int d) {
   return blk_base(bh, cap, t, 4096) + (d >> 6) * 2048 + (t & 31) * 64 + (d & 63);
 }
-// int4 K: byte holding dims d, d+1 (d even)
+// int4 K: byte holding dims d, d+1 (d even).  Row t of the block is 64 bytes:
+// [4 dim-groups of 16 per half][half m][8 bytes], so the 16 bytes a lane reads
+// (dims 16g..16g+15 of both halves) are contiguous.
 __device__ __forceinline__ int64_t k4_off(int64_t bh, int64_t cap, int64_t t, int d) {
-  return blk_base(bh, cap, t, 2048) + (d >> 6) * 1024 + (t & 31) * 32 + ((d & 63) >> 1);
+  const int b = (d & 63) >> 1;  // byte inside the half
+  return blk_base(bh, cap, t, 2048) + (t & 31) * 64 + (b >> 3) * 16 + (d >> 6) * 8 + (b & 7);
 }
 // int8 V: byte of dim d
 __device__ __forceinline__ int64_t v8_off(int64_t bh, int64_t cap, int64_t t, int d) {
   return blk_base(bh, cap, t, 4096) + d * 32 + block_pos((int)(t & 31));
 }
-// int4 V: byte holding token t (and its neighbour t^1) of dim d
+// int4 V: byte holding token t (and its neighbour t^1) of dim d.  For dim
+// d = 16n + c and position p = 8kg + e the byte sits at
+// [n/4][c][kg][n%4][e/2]: the 4 bytes of (d, kg) for n = 4h..4h+3 are one
+// 16-byte run, so a lane reads its 32 bytes with two 16-byte loads.
 __device__ __forceinline__ int64_t v4_off(int64_t bh, int64_t cap, int64_t t, int d) {
-  return blk_base(bh, cap, t, 2048) + d * 16 + (block_pos((int)(t & 31)) >> 1);
+  const int p = block_pos((int)(t & 31)), n = d >> 4, c = d & 15;
+  return blk_base(bh, cap, t, 2048) + (n >> 2) * 1024 + (c * 4 + (p >> 3)) * 16 + (n & 3) * 4 + ((p & 7) >> 1);
 }
 // per-token scale (int8)
 __device__ __forceinline__ int64_t s8_off(int64_t bh, int64_t cap, int64_t t) {

@@ -20,13 +20,23 @@ def _pos(t):
 
 
 def _store_k(logical, bits):
-    """Independent loop construction of the K code layout [nb][2][32][w]."""
+    """Independent loop construction of the K code layouts.
+
+    int8: [nb][2 halves][32 tokens][64 bytes].  int4 (64 packed bytes per
+    token, byte L = half L // 32, byte b = L % 32 of the half):
+    [nb][32 tokens][4 runs of 8 bytes][2 halves][8 bytes].
+    """
     B, H, T, W = logical.shape  # W = 128 (int8) or 64 packed bytes (int4)
     w = W // 2
     out = np.zeros((B, H, T // 32, 2 * 32 * w), logical.dtype)
     for t in range(T):
-        for m in range(2):
-            out[:, :, t // 32, m * 32 * w + (t % 32) * w : m * 32 * w + (t % 32) * w + w] = logical[:, :, t, m * w : (m + 1) * w]
+        if bits == 8:
+            for m in range(2):
+                out[:, :, t // 32, m * 32 * w + (t % 32) * w : m * 32 * w + (t % 32) * w + w] = logical[:, :, t, m * w : (m + 1) * w]
+        else:
+            for L in range(64):
+                m, b = L // 32, L % 32
+                out[:, :, t // 32, (t % 32) * 64 + (b // 8) * 16 + m * 8 + b % 8] = logical[:, :, t, L]
     return out
 
 
@@ -40,13 +50,19 @@ def _store_v8(logical):
 
 
 def _store_v4(q):
-    """uint4 V codes q[B][H][T][128] (0..15) -> [nb][128][16] bytes."""
+    """uint4 V codes q[B][H][T][128] (0..15) -> 2048-byte blocks.
+
+    Dim d = 16 n + c at position p = 8 kg + e sits in byte
+    [n // 4][c][kg][n % 4][e // 2], low nibble = even e.
+    """
     B, H, T, D = q.shape
     out = np.zeros((B, H, T // 32, D * 16), np.uint8)
     for t in range(T):
         p = _pos(t % 32)
         for d in range(D):
-            out[:, :, t // 32, d * 16 + p // 2] |= (q[:, :, t, d] << (4 * (p % 2))).astype(np.uint8)
+            n, c = d // 16, d % 16
+            byte = (n // 4) * 1024 + (c * 4 + p // 8) * 16 + (n % 4) * 4 + (p % 8) // 2
+            out[:, :, t // 32, byte] |= (q[:, :, t, d] << (4 * (p % 2))).astype(np.uint8)
     return out
 
 
