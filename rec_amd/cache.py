@@ -102,8 +102,10 @@ def to_logical(kv: QuantizedKV, length: Optional[int] = None):
         codes = kv.codes.view(B, H, nb, 2, BLOCK, w).permute(0, 1, 2, 4, 3, 5).reshape(B, H, nb * BLOCK, 2 * w)
     elif not kv.blocked:  # K: [nb][32 tokens][4 byte groups][2 halves][8 bytes]
         codes = kv.codes.view(B, H, nb, BLOCK, 4, 2, 8).permute(0, 1, 2, 3, 5, 4, 6).reshape(B, H, nb * BLOCK, 64)
-    elif kv.bits == 8:  # V: [nb][128 dims][32 positions]
-        codes = kv.codes.view(B, H, nb, HEAD_DIM, BLOCK)[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
+    elif kv.bits == 8:  # V: [nb][n / 2][c][position group][n % 2][8 bytes], dim 16 n + c
+        blocked = kv.codes.view(B, H, nb, 4, 16, 4, 2, 8)  # (h, c, pg, n2, e)
+        blocked = blocked.permute(0, 1, 2, 3, 6, 4, 5, 7).reshape(B, H, nb, HEAD_DIM, BLOCK)  # (n, c) -> dim
+        codes = blocked[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
     else:  # V: [nb][n / 4][c][position group][n % 4][4 bytes], dim 16 n + c, position p in byte p // 2
         packed = kv.codes.view(B, H, nb, 2, 16, 4, 4, 4)  # (h, c, pg, n4, byte)
         packed = packed.permute(0, 1, 2, 3, 6, 4, 5, 7).reshape(B, H, nb, HEAD_DIM, BLOCK // 2)  # (n, c) -> dim

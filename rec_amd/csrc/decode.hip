@@ -156,11 +156,11 @@ constexpr int CH = BLOCK_T;
 struct Chunk {
   v4i k8[2][2];   // int8 K: tile j, MFMA half m (16 bytes each)
   v4i k4[2];      // int4 K: tile j, both halves (8 packed bytes each)
-  v4i ks;         // int8 K: scales of this lane's 8 tokens
-  v2i v8[8];      // int8 V: dim block n, this lane's 8 tokens
+  v4i v8[4];      // int8 V: dim blocks 2h, 2h+1 (8 bytes each), this lane's 8 tokens
   v4i v4[2];      // int4 V: dim blocks 4h..4h+3, this lane's 8 tokens packed
-  v4i vs;         // int8 V: scales of this lane's 8 tokens
-  uint32_t m4[4]; // int4: one dword per lane of the block's K scales, K zeros, V scales, V zeros
+  uint32_t m[4];  // scales (and int4 zero-points) of the block, one dword per lane:
+                  // [0] K scales, [1] int4 K zeros, [2] V scales, [3] int4 V zeros (int8
+                  // scales on lanes 0-15 only); handed out through LDS
 };
 
 // Buffer resources of one (b, h) slice of the cache, plus an empty one.  Every
@@ -206,9 +206,8 @@ __device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff
 // Per-lane byte offsets inside a cache block (fixed for the whole kernel).
 struct LaneOff {
   uint32_t k[2];  // K codes, tile j (int8: the second MFMA half is +2048)
-  uint32_t ks;    // int8 K scales
-  uint32_t v;     // V codes (int8: dim block n at +512 n; int4: dim blocks 4h.. at +1024 h)
-  uint32_t vs;    // int8 V scales
+  uint32_t v;     // V codes, run h at +1024 h
+  uint32_t m8;    // int8 scale dword of this lane (out of range past lane 15: reads zero)
   uint32_t m4;    // int4 scale / zero-point dword of this lane
 };
 
@@ -218,9 +217,8 @@ __device__ __forceinline__ LaneOff lane_offsets(int lane) {
   LaneOff o;
 #pragma unroll
   for (int j = 0; j < 2; ++j) o.k[j] = (16 * j + c) * 64 + 16 * kg;
-  o.ks = 16 * kg;
-  o.v = VB == 8 ? c * 32 + 8 * kg : (c * 4 + kg) * 16;
-  o.vs = 16 * kg;
+  o.v = (c * 4 + kg) * 16;
+  o.m8 = lane < 16 ? 4 * lane : 0x40000000u;
   o.m4 = 4 * lane;
   return o;
 }
@@ -244,21 +242,21 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
     }
   }
   if constexpr (KB == 8) {
-    R.ks = ld128(rks, o.ks, blk * 64);
+    R.m[0] = ld32(rks, o.m8, blk * 64);
   } else {
-    R.m4[0] = ld32(rks, o.m4, blk * 256);
-    R.m4[1] = ld32(rkz, o.m4, blk * 256);
+    R.m[0] = ld32(rks, o.m4, blk * 256);
+    R.m[1] = ld32(rkz, o.m4, blk * 256);
   }
-  // V block n: lane (c, kg) gets dim 16n+c at block positions 8kg .. 8kg+7
+  // V: lane (c, kg) gets dims 16n+c at block positions 8kg .. 8kg+7
   if constexpr (VB == 8) {
 #pragma unroll
-    for (int n = 0; n < 8; ++n) R.v8[n] = ld64(rv, o.v + n * 512, blk * 4096);
-    R.vs = ld128(rvs, o.vs, blk * 64);
+    for (int h = 0; h < 4; ++h) R.v8[h] = ld128(rv, o.v + h * 1024, blk * 4096);
+    R.m[2] = ld32(rvs, o.m8, blk * 64);
   } else {
     R.v4[0] = ld128(rv, o.v, blk * 2048);
     R.v4[1] = ld128(rv, o.v + 1024, blk * 2048);
-    R.m4[2] = ld32(rvs, o.m4, blk * 256);
-    R.m4[3] = ld32(rvz, o.m4, blk * 256);
+    R.m[2] = ld32(rvs, o.m4, blk * 256);
+    R.m[3] = ld32(rvz, o.m4, blk * 256);
   }
 }
 
@@ -271,25 +269,31 @@ template <int KB, int VB>
 __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, float qsum_a,
                                               float qsum_b, int valid, int lane, char* meta) {
   const int c = lane & 15, kg = lane >> 4;
-  // int4 scales / zero-points: the block's arrays arrive one dword per lane;
-  // this wavefront's LDS region [K scales][K zeros][V scales][V zeros] (256 B
-  // each, [4 groups][32 positions] fp16) hands each lane the 16-byte runs it
-  // needs (positions 8kg .. 8kg+7 of a group).
-  v4i ks4[2], kz4[2], vs4[4], vz4[4];
-  if constexpr (KB == 4 || VB == 4) {
+  // Scales (and int4 zero-points) arrive one dword per lane; this wavefront's
+  // LDS region hands each lane the 16-byte runs it needs (positions
+  // 8kg .. 8kg+7).  int8: [K scales 64 B][V scales 64 B]; int4:
+  // [K scales][K zeros][V scales][V zeros], 256 B each ([4 groups][32 positions]).
+  v4i ks, vs, ks4[2], kz4[2], vs4[4], vz4[4];
+  {
     uint32_t* mw = (uint32_t*)meta;
-    if constexpr (KB == 4) {
-      mw[lane] = R.m4[0];
-      mw[64 + lane] = R.m4[1];
+    if constexpr (KB == 8) {
+      if (lane < 16) mw[lane] = R.m[0];
+    } else {
+      mw[lane] = R.m[0];
+      mw[64 + lane] = R.m[1];
     }
-    if constexpr (VB == 4) {
-      mw[128 + lane] = R.m4[2];
-      mw[192 + lane] = R.m4[3];
+    if constexpr (VB == 8) {
+      if (lane < 16) mw[(KB == 8 ? 16 : 128) + lane] = R.m[2];
+    } else {
+      mw[128 + lane] = R.m[2];
+      mw[192 + lane] = R.m[3];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if constexpr (KB == 4) {
+    if constexpr (KB == 8) {
+      ks = *(const v4i*)(meta + 16 * kg);
+    } else {
 #pragma unroll
       for (int gi = 0; gi < 2; ++gi) {
         const int off = (2 * gi + (c >> 3)) * 64 + 16 * kg;  // this lane's groups: 2gi + (c >= 8)
@@ -297,7 +301,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         kz4[gi] = *(const v4i*)(meta + 256 + off);
       }
     }
-    if constexpr (VB == 4) {
+    if constexpr (VB == 8) {
+      vs = *(const v4i*)(meta + (KB == 8 ? 64 : 512) + 16 * kg);
+    } else {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         vs4[g] = *(const v4i*)(meta + 512 + g * 64 + 16 * kg);
@@ -317,7 +323,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       for (int i = 0; i < 4; ++i) {
         const int mine = d[i], partner = dpp_ror8(mine);
         const int full = c < 8 ? mine * 256 + partner : partner * 256 + mine;
-        s[4 * j + i] = (float)full * (half_at(R.ks, 4 * j + i) * qsc);
+        s[4 * j + i] = (float)full * (half_at(ks, 4 * j + i) * qsc);
       }
     } else {
       const v4i ka = widen_u4((v2i){R.k4[j][0], R.k4[j][1]}), kb = widen_u4((v2i){R.k4[j][2], R.k4[j][3]});
@@ -367,10 +373,10 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   if constexpr (VB == 8) {
     v8h pb;
 #pragma unroll
-    for (int idx = 0; idx < 8; ++idx) pb[idx] = (_Float16)(p[idx] * half_at(R.vs, idx));
+    for (int idx = 0; idx < 8; ++idx) pb[idx] = (_Float16)(p[idx] * half_at(vs, idx));
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      const v8h a0 = i8x8_to_h8((uint32_t)R.v8[n][0], (uint32_t)R.v8[n][1]);
+      const v8h a0 = i8x8_to_h8((uint32_t)R.v8[n >> 1][2 * (n & 1)], (uint32_t)R.v8[n >> 1][2 * (n & 1) + 1]);
       st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb, st.acc[n], 0, 0, 0);
     }
   } else {

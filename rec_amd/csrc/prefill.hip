@@ -94,14 +94,20 @@ __device__ __forceinline__ void store_tile(const TileRegs& R, typename MT<BF16>:
 #pragma unroll
       for (int b = 0; b < 4; ++b) dst[4 * w + b] = MT<BF16>::from_float((float)(int8_t)((uint32_t)R.k[w] >> (8 * b)));
   }
-  // V block: [128 dims][32 positions] -> LDS [dim][64 positions of the tile]
+  // V block: 16-byte run o = [n/2][c][position group pg] holds positions
+  // 8pg .. 8pg+7 of dims 16n + c for n = 2(o/1024) and that + 1 -> LDS
+  // [dim][64 positions of the tile]
   {
-    const int d = o >> 5, p0 = o & 31;
-    _Float16* dst = Vl + d * PF_VROW + 32 * bk + p0;
+    const int n0 = 2 * (o >> 10), cc = (o >> 6) & 15, pg = (o >> 4) & 3;
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+    for (int half = 0; half < 2; ++half) {
+      _Float16* dst = Vl + (16 * (n0 + half) + cc) * PF_VROW + 32 * bk + 8 * pg;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) dst[4 * w + b] = (_Float16)(float)(int8_t)((uint32_t)R.v[w] >> (8 * b));
+      for (int w = 0; w < 2; ++w)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          dst[4 * w + b] = (_Float16)(float)(int8_t)((uint32_t)R.v[2 * half + w] >> (8 * b));
+    }
   }
   if (tid < 128) (tid < 64 ? KS : VS)[tid & 63] = half_bits_to_float(R.s);
 }

@@ -97,9 +97,12 @@ __device__ __forceinline__ int64_t k4_off(int64_t bh, int64_t cap, int64_t t, in
   const int b = (d & 63) >> 1;  // byte inside the half
   return blk_base(bh, cap, t, 2048) + (t & 31) * 64 + (b >> 3) * 16 + (d >> 6) * 8 + (b & 7);
 }
-// int8 V: byte of dim d
+// int8 V: byte of dim d.  For d = 16n + c and position p = 8kg + e the byte
+// sits at [n/2][c][kg][n%2][e]: the 8 bytes of (d, kg) for n = 2h, 2h+1 are
+// one 16-byte run, so a lane reads its 64 bytes with four 16-byte loads.
 __device__ __forceinline__ int64_t v8_off(int64_t bh, int64_t cap, int64_t t, int d) {
-  return blk_base(bh, cap, t, 4096) + d * 32 + block_pos((int)(t & 31));
+  const int p = block_pos((int)(t & 31)), n = d >> 4, c = d & 15;
+  return blk_base(bh, cap, t, 4096) + (n >> 1) * 1024 + (c * 4 + (p >> 3)) * 16 + (n & 1) * 8 + (p & 7);
 }
 // int4 V: byte holding token t (and its neighbour t^1) of dim d.  For dim
 // d = 16n + c and position p = 8kg + e the byte sits at

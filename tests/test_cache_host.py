@@ -41,11 +41,15 @@ def _store_k(logical, bits):
 
 
 def _store_v8(logical):
+    """int8 V codes: dim d = 16 n + c at position p = 8 kg + e sits in byte
+    [n // 2][c][kg][n % 2][e] of its 4096-byte block."""
     B, H, T, D = logical.shape
     out = np.zeros((B, H, T // 32, D * 32), np.int8)
     for t in range(T):
+        p = _pos(t % 32)
         for d in range(D):
-            out[:, :, t // 32, d * 32 + _pos(t % 32)] = logical[:, :, t, d]
+            n, c = d // 16, d % 16
+            out[:, :, t // 32, (n // 2) * 1024 + (c * 4 + p // 8) * 16 + (n % 2) * 8 + p % 8] = logical[:, :, t, d]
     return out
 
 
