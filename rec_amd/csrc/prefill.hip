@@ -17,8 +17,9 @@
 //
 // Work decomposition.  Grid (ceil(L/32), Hkv, B), 512 threads = 8 wavefronts;
 // wave w owns query head w of the KV head's GQA group and 32 query positions.
-// Each 64-token K/V tile is loaded once per workgroup, converted into
-// double-buffered LDS and shared by the 8 waves.
+// Each 128-token K/V tile is loaded once per workgroup, converted into
+// double-buffered LDS (141 KB) and shared by the 8 waves, which compute it in
+// two 64-token steps between barriers.
 //
 // S^T = K Q^T on 16x16x32 MFMAs (A = 16 tokens x 32 dims from LDS, B = Q^T held
 // in registers), which leaves lane (c, g) with the scores of query row c for
@@ -30,9 +31,10 @@
 namespace rec {
 
 constexpr int PF_QB = 32;           // query positions per workgroup
-constexpr int PF_KT = 64;           // tokens per K/V tile
+constexpr int PF_KT = 128;          // tokens per K/V tile in LDS (one barrier per tile)
+constexpr int PF_ST = 64;           // tokens per compute step (two steps per tile)
 constexpr int PF_KROW = 136;        // LDS row pitch of K (elements): 128 + 8 pad
-constexpr int PF_VROW = 72;         // LDS row pitch of V (elements): 64 + 8 pad
+constexpr int PF_VROW = 136;        // LDS row pitch of V (elements): 128 + 8 pad
 constexpr int PF_K_ELEMS = PF_KT * PF_KROW;
 constexpr int PF_V_ELEMS = HEAD_DIM * PF_VROW;
 
@@ -58,23 +60,29 @@ struct MT<false> {
   static __device__ __forceinline__ elem from_float(float x) { return (_Float16)x; }
 };
 
-// One thread's share of a 64-token tile as loaded from HBM.
+// One thread's share of a 128-token tile as loaded from HBM: 16 bytes of K
+// and of V from each of two cache blocks, and one fp16 scale (threads 0..255:
+// 128 K scales then 128 V scales).
 struct TileRegs {
-  v4i k, v;    // 16 int8 codes of K and of V
-  uint32_t s;  // one fp16 scale (threads 0..127: K then V)
+  v4i k[2], v[2];
+  uint32_t s;
 };
 
 __device__ __forceinline__ void load_tile(TileRegs& R, const PrefillArgs& a, int64_t bh, int t0, int tid, int t_end) {
-  const int bk = tid >> 8, o = (tid & 255) * 16;  // cache block within the tile, byte in block
-  const int blk = (t0 >> 5) + bk;
-  const bool live = t0 + 32 * bk < t_end;
-  const int8_t* kb = (const int8_t*)a.kq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
-  const int8_t* vb = (const int8_t*)a.vq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
-  R.k = live ? __builtin_nontemporal_load((const v4i*)(kb + o)) : (v4i){0, 0, 0, 0};
-  R.v = live ? __builtin_nontemporal_load((const v4i*)(vb + o)) : (v4i){0, 0, 0, 0};
+  const int o = (tid & 255) * 16;  // byte in block
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const int bk = 2 * part + (tid >> 8);  // cache block within the tile
+    const int blk = (t0 >> 5) + bk;
+    const bool live = t0 + 32 * bk < t_end;
+    const int8_t* kb = (const int8_t*)a.kq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
+    const int8_t* vb = (const int8_t*)a.vq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
+    R.k[part] = live ? __builtin_nontemporal_load((const v4i*)(kb + o)) : (v4i){0, 0, 0, 0};
+    R.v[part] = live ? __builtin_nontemporal_load((const v4i*)(vb + o)) : (v4i){0, 0, 0, 0};
+  }
   R.s = 0;
-  if (tid < 128) {
-    const int which = tid >> 6, tt = tid & 63;  // 0 = K scale, 1 = V scale
+  if (tid < 256) {
+    const int which = tid >> 7, tt = tid & 127;  // 0 = K scale, 1 = V scale
     const uint16_t* sp = which == 0 ? a.ks : a.vs;
     if (t0 + tt < t_end) R.s = sp[(bh * (a.cap / BLOCK_T) + (t0 >> 5) + (tt >> 5)) * 32 + block_pos(tt & 31)];
   }
@@ -82,34 +90,129 @@ __device__ __forceinline__ void load_tile(TileRegs& R, const PrefillArgs& a, int
 
 template <bool BF16>
 __device__ __forceinline__ void store_tile(const TileRegs& R, typename MT<BF16>::elem* Kl, _Float16* Vl, float* KS,
-                                           float* VS, int tid) {
+                                           float* VS, int tid, float q_mul) {
   typedef typename MT<BF16>::elem E;
-  const int bk = tid >> 8, o = (tid & 255) * 16;
-  // K block: [2 halves][32 tokens][64 B] -> LDS [token][dim]
-  {
-    const int m = o >> 11, r = (o & 2047) >> 6, e0 = o & 63;
-    E* dst = Kl + (32 * bk + r) * PF_KROW + 64 * m + e0;
+  const int o = (tid & 255) * 16;
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+  for (int part = 0; part < 2; ++part) {
+    const int bk = 2 * part + (tid >> 8);
+    // K block: [2 halves][32 tokens][64 B] -> LDS [token][dim]
+    {
+      const int m = o >> 11, r = (o & 2047) >> 6, e0 = o & 63;
+      E* dst = Kl + (32 * bk + r) * PF_KROW + 64 * m + e0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) dst[4 * w + b] = MT<BF16>::from_float((float)(int8_t)((uint32_t)R.k[w] >> (8 * b)));
-  }
-  // V block: 16-byte run o = [n/2][c][position group pg] holds positions
-  // 8pg .. 8pg+7 of dims 16n + c for n = 2(o/1024) and that + 1 -> LDS
-  // [dim][64 positions of the tile]
-  {
-    const int n0 = 2 * (o >> 10), cc = (o >> 6) & 15, pg = (o >> 4) & 3;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      _Float16* dst = Vl + (16 * (n0 + half) + cc) * PF_VROW + 32 * bk + 8 * pg;
-#pragma unroll
-      for (int w = 0; w < 2; ++w)
+      for (int w = 0; w < 4; ++w)
 #pragma unroll
         for (int b = 0; b < 4; ++b)
-          dst[4 * w + b] = (_Float16)(float)(int8_t)((uint32_t)R.v[2 * half + w] >> (8 * b));
+          dst[4 * w + b] = MT<BF16>::from_float((float)(int8_t)((uint32_t)R.k[part][w] >> (8 * b)));
+    }
+    // V block: 16-byte run o = [n/2][c][position group pg] holds positions
+    // 8pg .. 8pg+7 of dims 16n + c for n = 2(o/1024) and that + 1 -> LDS
+    // [dim][128 positions of the tile]
+    {
+      const int n0 = 2 * (o >> 10), cc = (o >> 6) & 15, pg = (o >> 4) & 3;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        _Float16* dst = Vl + (16 * (n0 + half) + cc) * PF_VROW + 32 * bk + 8 * pg;
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            dst[4 * w + b] = (_Float16)(float)(int8_t)((uint32_t)R.v[part][2 * half + w] >> (8 * b));
+      }
     }
   }
-  if (tid < 128) (tid < 64 ? KS : VS)[tid & 63] = half_bits_to_float(R.s);
+  // K scales carry the softmax scale (log2 domain)
+  if (tid < 256) (tid < 128 ? KS : VS)[tid & 127] = half_bits_to_float(R.s) * (tid < 128 ? q_mul : 1.f);
+}
+
+// One 64-token step for one wave: 32 query rows (two column tiles of 16) of
+// one head.  mask: some token of the tile lies past the cache end or past a
+// query's causal diagonal (only the tiles that reach a query block's diagonal);
+// masking is one loop under one uniform branch.
+template <bool BF16>
+__device__ __forceinline__ void tile_step(const typename MT<BF16>::elem* K, const _Float16* Vv, const float* KS,
+                                          const float* VS, const typename MT<BF16>::vec (&qop)[2][4], float (&m_run)[2],
+                                          float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end, int qabs0, int causal,
+                                          bool mask, int c, int g) {
+  typedef typename MT<BF16>::vec V8;
+  // ---------------- S^T = K Q^T ----------------
+  // Matrix-core phases run at raised wave priority, so the SIMD's other wave
+  // tends to be in its softmax (VALU) phase meanwhile instead of in lockstep.
+  __builtin_amdgcn_s_setprio(1);
+  v4f s4[2][4];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s4[rt][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const V8 ka = *(const V8*)(K + (16 * j + c) * PF_KROW + 32 * ks + 8 * g);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) s4[rt][j] = MT<BF16>::mfma(ka, qop[rt][ks], s4[rt][j]);
+    }
+  __builtin_amdgcn_s_setprio(0);
+  // scale (K scale x softmax scale, one multiply), mask, online softmax per
+  // query row (lane column c of tile rt)
+  v8h pb[2][2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float s[16];
+    const int qabs = qabs0 + 16 * rt + c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4f ksc = *(const v4f*)(&KS[16 * j + 4 * g]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[4 * j + i] = s4[rt][j][i] * ksc[i];
+    }
+    if (mask) {
+      // last visible token of this row, relative to the lane's first token t0 + 4g
+      const int last = (causal ? min(qabs, t_end - 1) : t_end - 1) - t0 - 4 * g;
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (16 * (k >> 2) + (k & 3) > last) s[k] = NEG_INF;
+    }
+    float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+#pragma unroll
+    for (int k = 4; k < 16; k += 4) cmax = fmaxf(cmax, fmaxf(fmaxf(s[k], s[k + 1]), fmaxf(s[k + 2], s[k + 3])));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    const float m_new = fmaxf(m_run[rt], cmax);
+    const float m_use = m_new == NEG_INF ? 0.f : m_new;
+    if (__ballot(m_new > m_run[rt])) {
+      const float factor = __builtin_amdgcn_exp2f(m_run[rt] - m_use);
+      l_run[rt] *= factor;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) acc[n][rt] *= factor;
+      m_run[rt] = m_new;
+    }
+    float lsum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4f vsc = *(const v4f*)(&VS[16 * j + 4 * g]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(s[4 * j + i] - m_use);
+        lsum += p;
+        // B operand of P·V for token half qq = j/2: k order (j&1, i)
+        pb[rt][j >> 1][4 * (j & 1) + i] = (_Float16)(p * vsc[i]);
+      }
+    }
+    l_run[rt] += lsum;
+  }
+  // ---------------- O^T += V^T P'^T ----------------
+  __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq) {
+      const v8h va = *(const v8h*)(Vv + (16 * n + c) * PF_VROW + 32 * qq + 8 * g);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][qq], acc[n][rt], 0, 0, 0);
+    }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 template <bool BF16>
@@ -151,90 +254,28 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 
   TileRegs R;
   load_tile(R, a, bh, 0, tid, t_end);
-  store_tile<BF16>(R, Kl[0], Vl[0], KS[0], VS[0], tid);
+  store_tile<BF16>(R, Kl[0], Vl[0], KS[0], VS[0], tid, a.q_mul);
   __syncthreads();
   int buf = 0;
   for (int t0 = 0; t0 < t_end; t0 += PF_KT) {
     const bool more = t0 + PF_KT < t_end;
     if (more) load_tile(R, a, bh, t0 + PF_KT, tid, t_end);  // in flight during this tile
     if (active) {
-      const E* K = Kl[buf];
-      const _Float16* Vv = Vl[buf];
-      // ---------------- S^T = K Q^T ----------------
-      v4f s4[2][4];
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) s4[rt][j] = (v4f){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const V8 ka = *(const V8*)(K + (16 * j + c) * PF_KROW + 32 * ks + 8 * g);
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt) s4[rt][j] = MT<BF16>::mfma(ka, qop[rt][ks], s4[rt][j]);
-        }
-      // scale, mask, online softmax per query row (lane column c of tile rt)
-      const bool diag = t0 + PF_KT > P + q0 || t0 + PF_KT > t_end;
-      v8h pb[2][2];
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        float s[16];
-        const int qabs = P + q0 + 16 * rt + c;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v4f ksc = *(const v4f*)(&KS[buf][16 * j + 4 * g]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = s4[rt][j][i] * (ksc[i] * a.q_mul);
-            if (diag) {
-              const int tok = t0 + 16 * j + 4 * g + i;
-              if (tok >= t_end || (a.causal && tok > qabs)) v = NEG_INF;
-            }
-            s[4 * j + i] = v;
-          }
-        }
-        float cmax = s[0];
-#pragma unroll
-        for (int k = 1; k < 16; ++k) cmax = fmaxf(cmax, s[k]);
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-        const float m_new = fmaxf(m_run[rt], cmax);
-        const float m_use = m_new == NEG_INF ? 0.f : m_new;
-        if (__ballot(m_new > m_run[rt])) {
-          const float factor = __builtin_amdgcn_exp2f(m_run[rt] - m_use);
-          l_run[rt] *= factor;
-#pragma unroll
-          for (int n = 0; n < 8; ++n) acc[n][rt] *= factor;
-          m_run[rt] = m_new;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v4f vsc = *(const v4f*)(&VS[buf][16 * j + 4 * g]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = __builtin_amdgcn_exp2f(s[4 * j + i] - m_use);
-            l_run[rt] += p;
-            // B operand of P·V for token half qq = j/2: k order (j&1, i)
-            pb[rt][j >> 1][4 * (j & 1) + i] = (_Float16)(p * vsc[i]);
-          }
+      for (int s0 = 0; s0 < PF_KT; s0 += PF_ST) {
+        const int ts = t0 + s0;
+        if (ts < t_end) {
+          // steps that reach a query block's diagonal or the end of the cache are masked
+          const bool mask = ts + PF_ST > P + q0 || ts + PF_ST > t_end;
+          tile_step<BF16>(Kl[buf] + s0 * PF_KROW, Vl[buf] + s0, KS[buf] + s0, VS[buf] + s0, qop, m_run, l_run, acc,
+                          ts, t_end, P + q0, a.causal, mask, c, g);
         }
       }
-      // ---------------- O^T += V^T P'^T ----------------
-#pragma unroll
-      for (int n = 0; n < 8; ++n)
-#pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-          const v8h va = *(const v8h*)(Vv + (16 * n + c) * PF_VROW + 32 * qq + 8 * g);
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt)
-            acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][qq], acc[n][rt], 0, 0, 0);
-        }
     }
     if (more) {
       // The other buffer was last read in the previous tile, before the barrier
       // that ended it, so it can be refilled without waiting.
-      store_tile<BF16>(R, Kl[buf ^ 1], Vl[buf ^ 1], KS[buf ^ 1], VS[buf ^ 1], tid);
+      store_tile<BF16>(R, Kl[buf ^ 1], Vl[buf ^ 1], KS[buf ^ 1], VS[buf ^ 1], tid, a.q_mul);
       __syncthreads();
       buf ^= 1;
     }
