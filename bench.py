@@ -184,6 +184,70 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01):
     return res
 
 
+def bf16_step_bytes(T, B=1):
+    """Algorithmic HBM bytes of one bf16-cache decode step: K/V rows of T tokens
+    (2 x 256 B per token and head), query, fp32 output, new token read + written."""
+    return B * (T * HKV * 2 * D * 2 + HQ * D * 2 + HQ * D * 4 + 2 * HKV * 2 * D * 2)
+
+
+def run_decode_bf16(T, R, steps, warmup, seed):
+    """Decode steps over the reference's production bf16 cache (KVStorage /
+    FixedKVCache): fused write of the new token + attention + merge, rotating
+    R single-layer storages."""
+    import torch
+
+    import rec_amd
+    from rec_amd import synthetic
+    from rec_amd.attention import _bf16_decode_launch
+
+    log(f"bf16 T={T}: building {R} storages")
+    caches = []
+    for i in range(R):
+        c = rec_amd.FixedKVCache(rec_amd.KVStorage(1, T, HKV), 0)
+        k = synthetic.kv((1, HKV, T - 1, D), seed + 2 * i, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+        v = synthetic.kv((1, HKV, T - 1, D), seed + 2 * i + 1, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+        c.update_and_fetch(k, v)
+        del k, v
+        caches.append(c)
+    q = synthetic.query(1, HQ, 1, seed + 100, dtype=torch.bfloat16)
+    kn = synthetic.kv((1, HKV, 1, D), seed + 101, dtype=torch.bfloat16)
+    vn = synthetic.kv((1, HKV, 1, D), seed + 102, dtype=torch.bfloat16)
+    g0 = torch.Generator(device="cuda")
+    g0.manual_seed(seed)
+    sinks = torch.randn(HQ, generator=g0, device="cuda")
+    out = torch.empty((1, HQ, D), dtype=torch.float32, device="cuda")
+
+    def step(s):
+        c = caches[s % R]
+        data = c.storage.layer(0)
+        _bf16_decode_launch(q, data[:, 0], data[:, 1], SCALE, sinks, None, out, kn, vn, T=T,
+                            capacity=c.storage.capacity)
+
+    for s in range(warmup):
+        step(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for s in range(steps):
+            step(s)
+    ms = _replay_timed(torch, g, steps)
+    gbs = bf16_step_bytes(T) / (ms * 1e-3) / 1e9
+    log(f"bf16 T={T}: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+    res = dict(
+        context=T,
+        kv_format="bf16 token-major [2][Hkv][cap][128] (KVStorage)",
+        us_per_step=round(ms * 1e3, 3),
+        gbs=round(gbs, 2),
+        frac_of_peak=round(gbs / HBM_PEAK_GBS, 4),
+        bytes_per_step=bf16_step_bytes(T),
+        storages=R,
+        note="fused write of the new token + attention + merge per step",
+    )
+    del g, caches
+    torch.cuda.empty_cache()
+    return res
+
+
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -332,6 +396,7 @@ def main(argv=None):
     ap.add_argument("--no-long", action="store_true", help="skip the 252K measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the chunked-prefill measurement")
     ap.add_argument("--no-int4", action="store_true", help="skip the 131K uint4 measurement")
+    ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-cache measurements")
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -382,6 +447,12 @@ def main(argv=None):
         ls = args.long_steps or max(16, args.steps // 8)
         r4 = run_decode(131072, 12, ls, max(4, args.warmup // 4), args.seed + 77, bits=4, kind="heavy", frac=0.05)
         log(f"131K int4: {r4['us_per_step']:.2f} us/step, {r4['gbs']:.0f} GB/s; kernel {r4['kernel_us']:.2f} us")
+
+    rbf = {}
+    if not args.no_bf16:
+        ls = args.long_steps or max(16, args.steps // 8)
+        rbf["context_32k_bf16"] = run_decode_bf16(32768, 8, max(16, args.steps // 4), 8, args.seed + 61)
+        rbf["context_252k_bf16"] = run_decode_bf16(258048, 2, ls, 4, args.seed + 63)
 
     rpf = None
     if not args.no_prefill:
@@ -465,6 +536,7 @@ def main(argv=None):
             "bytes_per_step": r4["bytes_per_step"],
             "cache_instances": r4["instances"],
         }
+    result.update(rbf)
     if rpf is not None:
         result["prefill_65536_plus_2048"] = rpf
     print(json.dumps(result), flush=True)

@@ -154,6 +154,43 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
                      float* out, void* stream);
 
+/*
+ * bf16 KV cache (the reference's production format): K and V are (B, Hkv,
+ * capacity, 128) bf16 tensors with unit dim stride, token stride 128 and
+ * element strides (sb, sh) for batch and head — the [2][Hkv][cap][128] layer
+ * region of KVStorage (engine/src/rec_mlx/cache.py:48-95) is K = region[0],
+ * V = region[1].  Storage must be 16-byte aligned, strides multiples of 8.
+ *
+ * rec_kv_write_bf16: store rows [0, L) of k_new / v_new (any float dtype,
+ * rounded to bf16) at positions [offset, offset + L).
+ * Replaces KVStorage.write and its flint_write_kv kernel,
+ * engine/src/rec_mlx/cache.py:30-45, :97-119.
+ */
+int rec_kv_write_bf16(const void* k_new, const void* v_new, int in_dtype,
+                      int64_t k_sb, int64_t k_sh, int64_t k_st,
+                      int64_t v_sb, int64_t v_sh, int64_t v_st,
+                      void* k, int64_t kc_sb, int64_t kc_sh, void* v, int64_t vc_sb, int64_t vc_sh,
+                      int B, int Hkv, int L, int D, int64_t offset, int64_t capacity, void* stream);
+
+/*
+ * GQA decode attention over the first T tokens of a bf16 K/V cache, with an
+ * optional fused write of the newest token (k_new / v_new (B, Hkv, 1, D), any
+ * float dtype, stored at position T-1 first; NULL: no write).  Query, sinks,
+ * scale, splits, workspace and output as rec_decode_attn; the split-K partial
+ * and the merge are both launched.
+ * Replaces the attention of Attention.__call__ over a FixedKVCache,
+ * engine/src/rec_mlx/model.py:204-211 (FixedKVCache.update_and_fetch first,
+ * cache.py:145-150), whose fused-decoder form is the bf16 split-K partial of
+ * engine/src/rec_mlx/kernels/megakernel.py:619-693 and merge :276-318.
+ */
+int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                    const void* k_new, const void* v_new, int new_dtype,
+                    int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh,
+                    void* k, int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh,
+                    const float* sinks, float scale,
+                    int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
+                    void* workspace, size_t workspace_bytes, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,14 +1,16 @@
 """rec_amd — MI355X (gfx950) GQA decode attention over a quantized KV cache.
 
 Drop-in for the quantized-KV attention path of rec's engine
-(engine/src/rec_mlx/model.py:40-139,165-203): a quantize-on-append cache with
+(engine/src/rec_mlx/model.py:40-139,165-211): a quantize-on-append cache with
 the reference's cache surface and ``quantized_attention_with_sinks`` with its
-signature, running hand-written HIP kernels through the C ABI in
-``include/rec_amd.h``.
+signature, and the bf16 ``KVStorage`` / ``FixedKVCache`` path
+(engine/src/rec_mlx/cache.py:48-150) with its decode attention, running
+hand-written HIP kernels through the C ABI in ``include/rec_amd.h``.
 """
 
 from ._lib import RecError, load as library  # noqa: F401
-from .attention import attend, quantized_attention_with_sinks  # noqa: F401
+from .attention import attend, quantized_attention_with_sinks, scaled_dot_product_attention  # noqa: F401
 from .cache import MixedQuantizedKVCache, QuantizedKV, QuantizedKVCache, to_logical  # noqa: F401
+from .kvstorage import FixedKVCache, KVStorage  # noqa: F401
 
 __version__ = "0.1.0"

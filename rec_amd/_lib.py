@@ -58,6 +58,20 @@ SIGNATURES["rec_prefill_attn"] = (
     [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i64, _i64, _p, _p],
 )
 
+SIGNATURES["rec_kv_write_bf16"] = (
+    _i,
+    [_p, _p, _i, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i, _i, _i, _i, _i64, _i64, _p],
+)
+SIGNATURES["rec_decode_bf16"] = (
+    _i,
+    [
+        _p, _i, _i64, _i64,  # q
+        _p, _p, _i, _i64, _i64, _i64, _i64,  # new k/v
+        _p, _i64, _i64, _p, _i64, _i64,  # bf16 K, V
+        _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _p, _p,
+    ],
+)
+
 _lock = threading.Lock()
 _lib = None
 

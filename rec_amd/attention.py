@@ -22,6 +22,7 @@ import torch
 
 from . import _lib
 from .cache import _DTYPES, HEAD_DIM, QuantizedKV, QuantizedKVCache
+from .kvstorage import FixedKVCache
 
 _ws_lock = threading.Lock()
 _workspaces = {}
@@ -170,16 +171,92 @@ def quantized_attention_with_sinks(
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 
-def attend(queries, keys, values, cache: QuantizedKVCache, scale, mask=None, sinks=None, *, out_dtype=None,
-           splits=None, fused=True):
-    """The cache + attention part of ``Attention.__call__`` (model.py:177-203).
+def _bf16_kv_ok(t: torch.Tensor) -> bool:
+    return t.dtype == torch.bfloat16 and t.is_cuda and t.stride(-1) == 1 and t.stride(-2) == HEAD_DIM
 
-    New ``keys``/``values`` ``(B, Hkv, L, 128)`` are quantized into ``cache``
-    first, then ``queries`` attend over the whole cache, the new tokens
-    included.  A single decode token takes one fused launch.
+
+def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=None, v_new=None, T=None,
+                        capacity=None):
+    lib = _lib.load()
+    B, Hq, L, D = queries.shape
+    Hkv = keys.shape[1]
+    T = keys.shape[2] if T is None else T
+    capacity = T if capacity is None else capacity
+    q = queries[:, :, 0]
+    if not _rows_aligned(q):
+        q = q.contiguous()
+    dev = queries.device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    if splits is None or splits <= 0:
+        splits = lib.rec_decode_default_splits(B, Hkv, T)
+    ws = workspace(dev, B, Hkv, splits, stream)
+    sk = _sinks(sinks, Hq, dev)
+    if k_new is None:
+        new = (None, None, _lib.REC_BF16, 0, 0, 0, 0)
+    else:
+        new = (k_new.data_ptr(), v_new.data_ptr(), _DTYPES[k_new.dtype], k_new.stride(0), k_new.stride(1),
+               v_new.stride(0), v_new.stride(1))
+    rc = lib.rec_decode_bf16(
+        q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), *new,
+        keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
+        _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity), int(splits), ws.data_ptr(), ws.numel(),
+        out.data_ptr(), stream,
+    )
+    _lib.check(rc, "rec_decode_bf16")
+
+
+def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=None, *, out_dtype=None,
+                                 splits=None):
+    """Attention of ``queries`` ``(B, n_q, 1, 128)`` over bf16 ``keys``/``values``
+    ``(B, Hkv, T, 128)`` with token stride 128 (a :class:`FixedKVCache`'s views),
+    the per-head ``sinks`` in the softmax denominator: the call
+    Attention.__call__ makes for a FixedKVCache (model.py:204-211, the fused
+    SDPA's sinks argument).  One query token (decode) only.
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
+    if L != 1:
+        raise NotImplementedError("attention over a bf16 cache runs for one query token (decode) only")
+    if not (_bf16_kv_ok(keys) and _bf16_kv_ok(values)):
+        raise ValueError("keys/values must be bf16 GPU tensors (B, Hkv, T, 128) with token stride 128")
+    if keys.shape != values.shape or keys.shape[0] != B or keys.shape[-1] != D:
+        raise ValueError(f"keys {tuple(keys.shape)} / values {tuple(values.shape)} do not match queries")
+    if mask is not None and not (isinstance(mask, str) and mask == "causal"):
+        raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
+    out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+    _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out)
+    out = out.view(B, Hq, 1, D)
+    return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+
+
+def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dtype=None,
+           splits=None, fused=True):
+    """The cache + attention part of ``Attention.__call__`` (model.py:177-211).
+
+    New ``keys``/``values`` ``(B, Hkv, L, 128)`` go into ``cache`` first
+    (quantized for a :class:`QuantizedKVCache`, stored as bf16 for a
+    :class:`FixedKVCache`), then ``queries`` attend over the whole cache, the
+    new tokens included.  A single decode token takes one fused launch.
+    """
+    _check_query(queries)
+    B, Hq, L, D = queries.shape
+    if isinstance(cache, FixedKVCache):
+        if fused and L == 1:
+            if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
+                raise ValueError("a fused decode step takes one new K/V token of a float dtype")
+            T = cache.offset + 1
+            cache._reserve(T)
+            data = cache.storage.layer(cache.index)
+            kn = keys if _rows_aligned(keys) else keys.contiguous()
+            vn = values if _rows_aligned(values) else values.contiguous()
+            out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+            _bf16_decode_launch(queries, data[:, 0], data[:, 1], scale, sinks, splits, out, kn, vn, T=T,
+                                capacity=cache.storage.capacity)
+            cache.offset = T
+            out = out.view(B, Hq, 1, D)
+            return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+        k, v = cache.update_and_fetch(keys, values)
+        return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits)
     if fused and L == 1:
         cache._check_usable()
         if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:

@@ -358,4 +358,104 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
 }
 
+int rec_kv_write_bf16(const void* k_new, const void* v_new, int in_dtype, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                      int64_t v_sb, int64_t v_sh, int64_t v_st, void* k, int64_t kc_sb, int64_t kc_sh, void* v,
+                      int64_t vc_sb, int64_t vc_sh, int B, int Hkv, int L, int D, int64_t offset, int64_t capacity,
+                      void* stream) {
+  int e;
+  if ((e = check_dtype(in_dtype, "input"))) return e;
+  if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
+  if (B < 1 || Hkv < 1 || L < 0) return fail(REC_EINVAL, "bad shape B=%d Hkv=%d L=%d", B, Hkv, L);
+  if (offset < 0) return fail(REC_EINVAL, "negative offset");
+  if (offset + L > capacity)
+    return fail(REC_ECAPACITY, "writing %d tokens at %lld exceeds the capacity %lld", L, (long long)offset,
+                (long long)capacity);
+  if (L == 0) return ok();
+  if (!k_new || !v_new || !k || !v) return fail(REC_EINVAL, "null key/value pointer");
+  if (!vec_rows(k, kc_sb, kc_sh, 0) || !vec_rows(v, vc_sb, vc_sh, 0))
+    return fail(REC_EALIGN, "bf16 K/V storage must be 16-byte aligned with strides that are multiples of 8 elements");
+  if (kc_sb % 8 || kc_sh % 8 || vc_sb % 8 || vc_sh % 8)
+    return fail(REC_EALIGN, "bf16 K/V storage strides must be multiples of 8 elements");
+  AppendArgs a{};
+  a.k = RowSrc{k_new, in_dtype, k_sb, k_sh, k_st, vec_rows(k_new, k_sb, k_sh, k_st)};
+  a.v = RowSrc{v_new, in_dtype, v_sb, v_sh, v_st, vec_rows(v_new, v_sb, v_sh, v_st)};
+  a.kq = k;
+  a.vq = v;
+  a.B = B;
+  a.Hkv = Hkv;
+  a.L = L;
+  a.offset = offset;
+  a.cap = capacity;
+  return launched(launch_write_bf16(a, kc_sb, kc_sh, vc_sb, vc_sh, (hipStream_t)stream), "bf16 write launch");
+}
+
+int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
+                    int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k, int64_t k_sb,
+                    int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale, int B, int Hq,
+                    int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
+                    size_t workspace_bytes, float* out, void* stream) {
+  int e;
+  if ((e = check_dtype(q_dtype, "query"))) return e;
+  if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
+  if (B < 1 || Hkv < 1 || Hq < 1) return fail(REC_EINVAL, "B, Hq and Hkv must be positive");
+  if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
+  if (Hq / Hkv > 8) return fail(REC_EUNSUPPORTED, "GQA ratio %d exceeds 8", Hq / Hkv);
+  if (T < 1) return fail(REC_EINVAL, "decode needs at least one cached token (T=%lld)", (long long)T);
+  if (T > capacity) return fail(REC_ECAPACITY, "T=%lld exceeds the cache capacity %lld", (long long)T, (long long)capacity);
+  if (T > ((int64_t)1 << 23)) return fail(REC_EUNSUPPORTED, "more than 8M tokens per head");
+  if (!q || !out || !k || !v) return fail(REC_EINVAL, "null query/output/key/value pointer");
+  if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
+  if (!vec_rows(q, q_sb, q_sh, 0))
+    return fail(REC_EALIGN, "query rows must start 16-byte aligned (strides multiples of 4 elements)");
+  if (!aligned16(k) || !aligned16(v) || k_sb % 8 || k_sh % 8 || v_sb % 8 || v_sh % 8)
+    return fail(REC_EALIGN, "bf16 K/V must be 16-byte aligned with strides that are multiples of 8 elements");
+  if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
+  const bool append = k_new != nullptr || v_new != nullptr;
+  if (append) {
+    if ((e = check_dtype(new_dtype, "new keys/values"))) return e;
+    if (!k_new || !v_new) return fail(REC_EINVAL, "new keys and values must both be given");
+  }
+  if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
+  if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
+  int S, span, t_split_end;
+  effective_splits(T, splits, append, &S, &span, &t_split_end);
+  const WorkspaceLayout w = ws_layout(B, Hkv, S);
+  if (!workspace || workspace_bytes < w.total)
+    return fail(REC_EWORKSPACE, "workspace of %zu bytes is too small (%zu needed for %d splits)", workspace_bytes,
+                w.total, S);
+  if (!aligned16(workspace)) return fail(REC_EALIGN, "workspace must be 16-byte aligned");
+  DecodeArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.kq = k;
+  a.vq = v;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.sinks = sinks;
+  a.out = out;
+  a.ws_stat = (float*)((char*)workspace + w.stat);
+  a.ws_acc = (float*)((char*)workspace + w.acc);
+  if (append) {
+    a.knew = RowSrc{k_new, new_dtype, kn_sb, kn_sh, 0, vec_rows(k_new, kn_sb, kn_sh, 0)};
+    a.vnew = RowSrc{v_new, new_dtype, vn_sb, vn_sh, 0, vec_rows(v_new, vn_sb, vn_sh, 0)};
+  }
+  a.q_mul = scale * LOG2E;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.T = T;
+  a.cap = capacity;
+  a.S = S;
+  a.span = span;
+  a.t_split_end = t_split_end;
+  const int e1 = launched(launch_decode_bf16(a, (hipStream_t)stream), "bf16 decode launch");
+  if (e1 != REC_OK) return e1;
+  return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
+}
+
 }  // extern "C"

@@ -131,4 +131,42 @@ __device__ __forceinline__ v8h u4x8_to_h8_interleaved(uint32_t w) {
   return r;
 }
 
+// ---- raw buffer loads ----------------------------------------------------
+// A buffer resource bounds every load: offsets past its records read zero
+// without touching memory, so loads of absent data are issued unconditionally.
+constexpr int BUF_NT = 2;  // cache policy: nontemporal (the KV is streamed once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  // gfx9 buffer descriptor word 3 for raw (stride 0) dword access
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ float half_at(const v4i& w, int idx) {
+  const uint32_t x = (uint32_t)w[idx >> 1];
+  return half_bits_to_float((idx & 1) ? (x >> 16) : (x & 0xffff));
+}
+
+// The builtins return unsigned vectors; convert with bit_cast only (an
+// implicit conversion to a signed vector type can turn into a splat of lane 0).
+template <int POL = BUF_NT>
+__device__ __forceinline__ v4i ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL));
+}
+template <int POL = BUF_NT>
+__device__ __forceinline__ v2i ld64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL));
+}
+template <int POL = BUF_NT>
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL);
+}
+
+// Ordering of LDS accesses between the lanes of one wavefront (no hardware
+// barrier: a wavefront's LDS operations execute in order).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace rec

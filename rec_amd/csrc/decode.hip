@@ -176,33 +176,6 @@ struct Res {
   __amdgpu_buffer_rsrc_t k, v, ks, kz, vs, vz, none;
 };
 
-constexpr int BUF_NT = 2;  // cache policy: nontemporal (the KV is streamed once)
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
-  // gfx9 buffer descriptor word 3 for raw (stride 0) dword access
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ float half_at(const v4i& w, int idx) {
-  const uint32_t x = (uint32_t)w[idx >> 1];
-  return half_bits_to_float((idx & 1) ? (x >> 16) : (x & 0xffff));
-}
-
-// The builtins return unsigned vectors; convert with bit_cast only (an
-// implicit conversion to a signed vector type can turn into a splat of lane 0).
-template <int POL = BUF_NT>
-__device__ __forceinline__ v4i ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL));
-}
-template <int POL = BUF_NT>
-__device__ __forceinline__ v2i ld64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL));
-}
-template <int POL = BUF_NT>
-__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL);
-}
-
 // Per-lane byte offsets inside a cache block (fixed for the whole kernel).
 struct LaneOff {
   uint32_t k[2];  // K codes, tile j (int8: the second MFMA half is +2048)

@@ -1,0 +1,325 @@
+// Split-K flash decode over a bf16 KV cache (gfx950): the reference's
+// production cache format.
+//
+// Restates, for bf16 K/V held token-major ([token][128] rows, the layout of
+// KVStorage / FixedKVCache, engine/src/rec_mlx/cache.py:30-150):
+//   * the attention of Attention.__call__ over a FixedKVCache
+//     (engine/src/rec_mlx/model.py:204-211, scaled_dot_product_attention with the
+//     per-head sink logit), which the reference's fused decoder runs as the
+//     bf16 split-K partial of engine/src/rec_mlx/kernels/megakernel.py:619-693;
+//   * the write of the new token into the storage (cache.py:30-45, :97-119),
+//     fused: the split that owns the newest token writes it first.
+// Partials use the layout of the quantized decode, and rec_decode_merge /
+// the merge kernel combine them.
+//
+// Work decomposition: as the quantized decode — grid (splits, Hkv, B), 4
+// wavefronts, wave w takes 32-token chunks w, w+4, ..., a 2-deep ring of raw
+// buffer loads (chunks past the wave's last one load through an empty
+// resource and only their compute is skipped).
+//
+// Q·Kᵀ on v_mfma_f32_16x16x32_bf16: A = 16 K rows x 32 dims straight from
+// HBM (16 bytes per lane), B = the scaled query split into bf16 high and low
+// parts that fill the 16 columns (columns 0-7 = high parts of heads 0-7, 8-15 =
+// low parts: 16 significant bits), recombined with one DPP row rotation.
+//
+// P·V on the same MFMA.  The A operand is Vᵀ (16 dims x 32 tokens) while the
+// cache holds V token-major, so each wave stages its chunk's V rows in LDS (at
+// the block positions of the quantized layout, which puts lane group g's
+// tokens at rows 8g .. 8g+7) and reads the operand back with
+// ds_read_b64_tr_b16: in a group of 16 lanes, lane 4a+b receives element b of
+// the 8-byte rows addressed by lanes 4k+a (k = 0..3), so lanes addressing rows
+// 8g+k, dims 16n+4a hand lane c dim 16n+c of four consecutive rows.  The
+// probabilities split the same way (columns 0-7 bf16(p), 8-15 the bf16
+// remainder), and the two column halves of the result are added at the end.
+#include "kernels.h"
+
+namespace rec {
+namespace {
+
+constexpr int BW = 4;          // wavefronts per workgroup
+constexpr int BCH = 32;        // tokens per chunk
+constexpr int ROWB = 256;      // bytes per K/V row (128 bf16)
+constexpr int VPITCH = 288;    // LDS bytes per staged V row: 256 + 32 keeps the transposed reads conflict-free
+constexpr int BL_QOP = 0;                             // 4 k-steps x 64 lanes x 16 B
+constexpr int BL_PART = 4096;                         // wave partials: 4 x 8 x 128 floats
+constexpr int BL_PSTAT = BL_PART + BW * 8 * 128 * 4;  // 4 x 8 x (m, l)
+constexpr int BL_V = BL_PSTAT + BW * 8 * 8;           // per wave: 32 rows x VPITCH
+constexpr int BL_BYTES = BL_V + BW * BCH * VPITCH;
+
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+
+// One chunk as it arrives from HBM: tile j (tokens 16j..16j+15), k-step ks
+// (dims 32ks..32ks+31); lane (c, kg) holds token 16j + c, dims 32ks + 8kg ..+7.
+struct BChunk {
+  v4i k[2][4];
+  v4i v[2][4];
+};
+
+struct BState {
+  float m, l;
+  v4f acc[8];  // columns 0-7: P_hi · V, columns 8-15: P_lo · V
+};
+
+__device__ __forceinline__ void load_bchunk(BChunk& R, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                            __amdgpu_buffer_rsrc_t none, bool ok, uint32_t blk, uint32_t loff) {
+  const __amdgpu_buffer_rsrc_t a = ok ? rk : none, b = ok ? rv : none;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) R.k[j][ks] = ld128(a, loff + j * 16 * ROWB + ks * 64, blk * BCH * ROWB);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) R.v[j][ks] = ld128(b, loff + j * 16 * ROWB + ks * 64, blk * BCH * ROWB);
+}
+
+__device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, const v8bf* qop, int valid, int lane,
+                                               char* vl) {
+  const int c = lane & 15, kg = lane >> 4;
+  // stage V: token 16j + c goes to row block_pos(16j + c)
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) *(v4i*)(vl + block_pos(16 * j + c) * VPITCH + ks * 64 + kg * 16) = R.v[j][ks];
+
+  // ---------------- scores (log2 domain: the query carries scale * log2 e) ----------------
+  float s[8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    v4f d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, R.k[j][ks]),
+                                                                               qop[ks], d, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[4 * j + i] = d[i] + dpp_ror8f(d[i]);  // high part + low part
+  }
+  if (valid < BCH) {  // tail chunk: tokens past the split end
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx)
+      if (16 * (idx >> 2) + 4 * kg + (idx & 3) >= valid) s[idx] = NEG_INF;
+  }
+
+  // ---------------- online softmax ----------------
+  float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
+  cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
+  const float m_new = fmaxf(st.m, cmax);
+  if (__ballot(m_new > st.m)) {
+    const float factor = __builtin_amdgcn_exp2f(st.m - m_new);
+    st.l *= factor;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) st.acc[n] *= factor;
+    st.m = m_new;
+  }
+  // P split into bf16 high (columns 0-7) and low (8-15) parts, position order
+  v8bf pb;
+#pragma unroll
+  for (int idx = 0; idx < 8; ++idx) {
+    const float p = __builtin_amdgcn_exp2f(s[idx] - st.m);
+    st.l += p;
+    const __bf16 hi = (__bf16)p;
+    pb[idx] = c < 8 ? hi : (__bf16)(p - (float)hi);
+  }
+
+  // ---------------- P·V: Vᵀ operands by transposed LDS reads ----------------
+  wave_lds_sync();
+  const int sk = (lane & 15) >> 2, sa = lane & 3;  // this lane addresses row 8kg + sk (+4), dims 16n + 4sa
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    typedef __attribute__((address_space(3))) v4bf lds_v4bf;
+    char* base = vl + (8 * kg + sk) * VPITCH + (16 * n + 4 * sa) * 2;
+    const v4bf r0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base));
+    const v4bf r1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base + 4 * VPITCH));
+    const v8bf a = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+    st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, st.acc[n], 0, 0, 0);
+  }
+  wave_lds_sync();  // the next chunk's staging overwrites these rows
+}
+
+__device__ __forceinline__ void store_bf16_row_pair(const RowSrc& src, int b, int h, void* dst_base, int64_t sb,
+                                                    int64_t sh, int64_t pos, int lane) {
+  float x0, x1;
+  load2_as_float(src, row_base(src, b, h, 0) + 2 * lane, x0, x1);
+  const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+  const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+  *(uint32_t*)((__bf16*)dst_base + (int64_t)b * sb + (int64_t)h * sh + pos * HEAD_DIM + 2 * lane) = w;
+}
+
+__global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[BL_BYTES];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, kg = lane >> 4;
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * a.Hkv + h;
+  const bool fused = a.knew.p != nullptr;
+  const bool tail = fused && split == a.S - 1;
+  int t_begin, t_end;
+  if (tail) {
+    t_begin = a.t_split_end;
+    t_end = (int)a.T;
+  } else {
+    t_begin = split * a.span;
+    t_end = t_begin + a.span < a.t_split_end ? t_begin + a.span : a.t_split_end;
+  }
+
+  const __bf16* kbase = (const __bf16*)a.kq + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh;
+  const __bf16* vbase = (const __bf16*)a.vq + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, a.T * ROWB), rv = make_rsrc(vbase, a.T * ROWB);
+  const __amdgpu_buffer_rsrc_t none = make_rsrc(kbase, 0);
+
+  // Fused write of the newest token (position T-1), before this split reads it.
+  if (tail) {
+    if (wave == 0) store_bf16_row_pair(a.knew, b, h, (void*)a.kq, a.k_sb, a.k_sh, a.T - 1, lane);
+    else if (wave == 1) store_bf16_row_pair(a.vnew, b, h, (void*)a.vq, a.v_sb, a.v_sh, a.T - 1, lane);
+    __threadfence_block();
+    __syncthreads();
+  }
+
+  // Query first, then the first chunk; the query is split while it streams.
+  const int hh = tid >> 5, d0 = (tid & 31) * 4;
+  const int hq_ld = h * a.G + (hh < a.G ? hh : 0);
+  const int64_t qi = (int64_t)b * a.q_sb + (int64_t)hq_ld * a.q_sh + d0;
+  const int es = a.q_dtype == DT_F32 ? 4 : 2;
+  const char* qp = (const char*)a.q + qi * es;
+  const v2i qw0 = *(const v2i*)qp;
+  const v2i qw1 = *(const v2i*)(qp + (es == 4 ? 8 : 0));
+
+  constexpr int NBUF = 2;
+  const int n_split = (t_end - t_begin + BCH - 1) / BCH;
+  const int n_w = n_split > wave ? (n_split - wave + BW - 1) / BW : 0;
+  const int blk0 = t_begin / BCH + wave;
+  const uint32_t loff = (uint32_t)(c * ROWB + kg * 16);
+  BChunk buf[NBUF];
+  load_bchunk(buf[0], rk, rv, none, 0 < n_w, blk0, loff);
+
+  {
+    __bf16* qop = (__bf16*)(smem + BL_QOP);
+    if (tid < 256) {
+      const v4i raw = {qw0[0], qw0[1], qw1[0], qw1[1]};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rk_ = raw[i];  // copy first: bit_cast of a vector subscript reads lane 0 in this clang
+        const uint32_t w = (uint32_t)raw[i >> 1];
+        const uint32_t bits = (i & 1) ? (w >> 16) : (w & 0xffffu);
+        float x = a.q_dtype == DT_F32 ? __builtin_bit_cast(float, rk_)
+                                      : (a.q_dtype == DT_F16 ? half_bits_to_float(bits)
+                                                             : __builtin_bit_cast(float, bits << 16));
+        x *= hh < a.G ? a.q_mul : 0.f;
+        const __bf16 hi = (__bf16)x, lo = (__bf16)(x - (float)hi);
+        const int d = d0 + i, ks = d >> 5, g = (d >> 3) & 3, jj = d & 7;
+        qop[(ks * 64 + g * 16 + hh) * 8 + jj] = hi;
+        qop[(ks * 64 + g * 16 + hh + 8) * 8 + jj] = lo;
+      }
+    }
+  }
+  __syncthreads();
+  v8bf qop[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qop[ks] = ((const v8bf*)(smem + BL_QOP))[ks * 64 + lane];
+
+  BState st;
+  st.m = NEG_INF;
+  st.l = 0.f;
+#pragma unroll
+  for (int n = 0; n < 8; ++n) st.acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
+  char* vl = smem + BL_V + wave * BCH * VPITCH;
+
+  // Ring as in the quantized decode: step i loads chunk i+1, computes chunk i;
+  // padded to whole revolutions, only the padding's compute is skipped.
+  const int n_pad = (n_w + NBUF - 1) / NBUF * NBUF;
+  for (int i0 = 0; i0 < n_pad; i0 += NBUF) {
+#pragma unroll
+    for (int j = 0; j < NBUF; ++j) {
+      const int i = i0 + j;
+      load_bchunk(buf[(j + 1) % NBUF], rk, rv, none, i + 1 < n_w, blk0 + BW * (i + 1), loff);
+      if (i < n_w) process_bchunk(buf[j], st, qop, t_end - (blk0 + BW * i) * BCH, lane, vl);
+    }
+  }
+
+  // ---------------- wave partial -> LDS (columns c and c+8 summed) ----------------
+  st.l += shfl_xor_f(st.l, 16);
+  st.l += shfl_xor_f(st.l, 32);
+  float* part = (float*)(smem + BL_PART);
+  float* pstat = (float*)(smem + BL_PSTAT);
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = st.acc[n][i] + dpp_ror8f(st.acc[n][i]);
+      if (c < 8 && c < a.G) part[(wave * 8 + c) * HEAD_DIM + 16 * n + 4 * kg + i] = v;
+    }
+  if (c < 8 && c < a.G && kg == 0) {
+    pstat[(wave * 8 + c) * 2 + 0] = st.m;
+    pstat[(wave * 8 + c) * 2 + 1] = st.l;
+  }
+  __syncthreads();
+
+  // ---------------- workgroup partial (or the output when S == 1) ----------------
+  if (hh < a.G) {
+    float mw[BW], M = NEG_INF;
+#pragma unroll
+    for (int w = 0; w < BW; ++w) {
+      mw[w] = pstat[(w * 8 + hh) * 2];
+      M = fmaxf(M, mw[w]);
+    }
+    float sink = NEG_INF;
+    if (a.S == 1 && a.sinks != nullptr) {
+      sink = a.sinks[h * a.G + hh] * LOG2E;
+      M = fmaxf(M, sink);
+    }
+    v4f acc4 = {0.f, 0.f, 0.f, 0.f};
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < BW; ++w) {
+      const float f = (mw[w] == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
+      acc4 += f * *(const v4f*)(part + (w * 8 + hh) * HEAD_DIM + d0);
+      l += f * pstat[(w * 8 + hh) * 2 + 1];
+    }
+    if (a.S == 1) {
+      if (sink != NEG_INF) l += __builtin_amdgcn_exp2f(sink - M);
+      const v4f o = l > 0.f ? acc4 / l : acc4;
+      *(v4f*)(a.out + ((int64_t)b * a.Hq + h * a.G + hh) * HEAD_DIM + d0) = o;
+    } else {
+      const int64_t row = (bh * a.S + split) * 8 + hh;
+      *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = acc4;
+      if ((tid & 31) == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){M, l};
+    }
+  }
+}
+
+// Bulk write of L new rows into bf16 K/V storage (FixedKVCache.update_and_fetch's
+// write, cache.py:97-119): one wavefront per (row, K or V), two elements per lane.
+__global__ __launch_bounds__(256) void write_bf16_kernel(const AppendArgs a, int64_t k_sb, int64_t k_sh,
+                                                         int64_t v_sb, int64_t v_sh) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= (int64_t)a.B * a.Hkv * a.L) return;
+  const int64_t bh = unit / a.L, u = unit % a.L;
+  const int b = (int)(bh / a.Hkv), h = (int)(bh % a.Hkv);
+  const bool isv = blockIdx.y == 1;
+  const RowSrc& src = isv ? a.v : a.k;
+  float x0, x1;
+  load2_as_float(src, row_base(src, b, h, (int)u) + 2 * lane, x0, x1);
+  const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+  const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+  __bf16* dst = (__bf16*)(isv ? a.vq : a.kq) + (int64_t)b * (isv ? v_sb : k_sb) + (int64_t)h * (isv ? v_sh : k_sh);
+  *(uint32_t*)(dst + (a.offset + u) * HEAD_DIM + 2 * lane) = w;
+}
+
+}  // namespace
+
+hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(decode_bf16_kernel, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_write_bf16(const AppendArgs& a, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
+                             hipStream_t stream) {
+  const int64_t rows = (int64_t)a.B * a.Hkv * a.L;
+  hipLaunchKernelGGL(write_bf16_kernel, dim3((unsigned)((rows + 3) / 4), 2), dim3(256), 0, stream, a, k_sb, k_sh, v_sb,
+                     v_sh);
+  return hipGetLastError();
+}
+
+}  // namespace rec

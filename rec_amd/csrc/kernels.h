@@ -33,6 +33,7 @@ struct DecodeArgs {
   float* out;          // [B][Hq][128] fp32
   float* ws_acc;       // [B*Hkv][S][8][128]
   float* ws_stat;      // [B*Hkv][S][8][2]
+  int64_t k_sb, k_sh, v_sb, v_sh;  // bf16 K/V (B, Hkv, T, 128) element strides (token stride 128)
   RowSrc knew, vnew;   // fused single-token append (knew.p null: none)
   float q_mul;         // softmax scale * log2(e)
   int B, Hq, Hkv, G;
@@ -65,5 +66,8 @@ hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream);
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
+hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_write_bf16(const AppendArgs& a, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
+                             hipStream_t stream);
 
 }  // namespace rec

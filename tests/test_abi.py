@@ -98,3 +98,45 @@ def test_error_mapping():
     with pytest.raises(_lib.RecError):
         _lib.check(_lib.REC_ELAUNCH, "x")
     _lib.check(_lib.REC_OK, "x")
+
+
+def _decode_bf16(lib, **kw):
+    a = dict(q=16, dt=1, kn=None, vn=None, k=16, sb=0, sh=0, v=16, B=1, Hq=8, Hkv=1, D=128, T=10, cap=64,
+             splits=0, ws=16, wsb=1 << 30, out=16)
+    a.update(kw)
+    return lib.rec_decode_bf16(
+        a["q"], a["dt"], 0, 0, a["kn"], a["vn"], 1, 0, 0, 0, 0, a["k"], a["sb"], a["sh"], a["v"], a["sb"], a["sh"],
+        None, 0.088, a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["out"],
+        None,
+    )
+
+
+def test_decode_bf16_validation(lib):
+    assert _decode_bf16(lib, T=65) == _lib.REC_ECAPACITY
+    assert _decode_bf16(lib, T=0) == _lib.REC_EINVAL
+    assert _decode_bf16(lib, k=8) == _lib.REC_EALIGN
+    assert _decode_bf16(lib, sh=4) == _lib.REC_EALIGN
+    assert "multiples of 8" in _lib.last_error()
+    assert _decode_bf16(lib, Hq=16, Hkv=1) == _lib.REC_EUNSUPPORTED
+    assert _decode_bf16(lib, wsb=16) == _lib.REC_EWORKSPACE
+    assert _decode_bf16(lib, kn=16) == _lib.REC_EINVAL  # new keys without new values
+    assert _decode_bf16(lib, D=64) == _lib.REC_EUNSUPPORTED
+    assert _decode_bf16(lib, q=8) == _lib.REC_EALIGN
+
+
+def _write_bf16(lib, **kw):
+    a = dict(k=16, v=16, dt=1, s=16, B=1, H=4, L=1, D=128, off=0, cap=64)
+    a.update(kw)
+    return lib.rec_kv_write_bf16(
+        16, 16, a["dt"], 0, 0, 0, 0, 0, 0, a["k"], 0, a["s"], a["v"], 0, a["s"],
+        a["B"], a["H"], a["L"], a["D"], a["off"], a["cap"], None,
+    )
+
+
+def test_write_bf16_validation(lib):
+    assert _write_bf16(lib, off=64) == _lib.REC_ECAPACITY
+    assert _write_bf16(lib, L=0) == _lib.REC_OK
+    assert _write_bf16(lib, D=64) == _lib.REC_EUNSUPPORTED
+    assert _write_bf16(lib, k=8) == _lib.REC_EALIGN
+    assert _write_bf16(lib, s=12) == _lib.REC_EALIGN
+    assert _write_bf16(lib, dt=9) == _lib.REC_EINVAL

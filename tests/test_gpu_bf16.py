@@ -1,0 +1,156 @@
+"""Parity of the bf16 KV-cache path (KVStorage / FixedKVCache and its decode
+kernel) with the CPU oracle.
+
+Stored K/V must be the bf16 rounding of the inputs, bit for bit; attention
+outputs within 2e-3 absolute + 1e-3 relative of the float64 oracle computed
+on the stored bf16 values (the reference's cache holds bf16,
+engine/src/rec_mlx/cache.py:30-45).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from rec_amd import FixedKVCache, KVStorage, attend, scaled_dot_product_attention, synthetic
+from tests.gpu_util import SCALE, assert_close, f32
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_np(x: torch.Tensor) -> np.ndarray:
+    return x.to(torch.bfloat16).float().cpu().numpy()
+
+
+CASES = [
+    # B, Hq, Hkv, T, q dtype, sinks, splits
+    (1, 8, 1, 1024, torch.bfloat16, False, None),
+    (1, 32, 4, 4096, torch.bfloat16, True, None),
+    (1, 32, 4, 777, torch.float16, True, 5),
+    (2, 16, 2, 300, torch.float32, False, 256),
+    (1, 4, 1, 1, torch.bfloat16, True, None),
+    (3, 24, 4, 65, torch.bfloat16, True, 1),
+    (1, 8, 8, 2049, torch.float16, False, 3),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"B{c[0]}_Hq{c[1]}_Hkv{c[2]}_T{c[3]}_{str(c[4])[6:]}_s{c[5]}_sp{c[6]}")
+def test_bf16_decode_matches_oracle(gpu, case):
+    B, Hq, Hkv, T, qdt, use_sinks, splits = case
+    k = synthetic.kv((B, Hkv, T, 128), 21, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, T, 128), 22, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    q = synthetic.query(B, Hq, 1, 23, dtype=qdt)
+    sinks = torch.randn(Hq, device="cuda") if use_sinks else None
+    out = scaled_dot_product_attention(q, k, v, SCALE, None, sinks, out_dtype=torch.float32, splits=splits)
+    torch.cuda.synchronize()
+    ref = O.attention(f32(q), f32(k), f32(v), SCALE, sinks=None if sinks is None else f32(sinks))
+    assert_close(f32(out), ref, f"case {case}")
+
+
+def test_fixed_kv_cache_prefill_then_fused_decode(gpu):
+    """update_and_fetch stores bf16(x) bit for bit; fused decode steps (write the
+    new token, then attend) match the oracle at every step."""
+    B, Hq, Hkv, P = 1, 32, 4, 1000
+    store = KVStorage(2, 2048, Hkv)
+    cache = FixedKVCache(store, 1)
+    assert cache.empty() and cache.make_mask(1) is None and cache.make_mask(5) == "causal"
+    k = synthetic.kv((B, Hkv, P + 6, 128), 31, kind="outliers", frac=0.01, dtype=torch.float16)
+    v = synthetic.kv((B, Hkv, P + 6, 128), 32, kind="outliers", frac=0.01, dtype=torch.float16)
+    kk, vv = cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    assert kk.shape == (B, Hkv, P, 128) and cache.offset == P
+    np.testing.assert_array_equal(kk.float().cpu().numpy(), bf16_np(k[:, :, :P]))
+    np.testing.assert_array_equal(vv.float().cpu().numpy(), bf16_np(v[:, :, :P]))
+    sinks = torch.randn(Hq, device="cuda")
+    for step in range(6):
+        T = P + step + 1
+        q = synthetic.query(B, Hq, 1, 40 + step, dtype=torch.bfloat16)
+        out = attend(q, k[:, :, T - 1 : T], v[:, :, T - 1 : T], cache, SCALE, None, sinks, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert cache.offset == T
+        ref = O.attention(f32(q), bf16_np(k[:, :, :T]), bf16_np(v[:, :, :T]), SCALE, sinks=f32(sinks))
+        assert_close(f32(out), ref, f"step {step}")
+    data = store.layer(1, cache.offset)
+    np.testing.assert_array_equal(data[:, 0].float().cpu().numpy(), bf16_np(k))
+    np.testing.assert_array_equal(data[:, 1].float().cpu().numpy(), bf16_np(v))
+    assert torch.count_nonzero(store.layer(0)) == 0  # the other layer is untouched
+
+
+def test_fused_equals_write_then_attend(gpu):
+    B, Hq, Hkv, P = 2, 16, 2, 333
+    outs = []
+    for fused in (True, False):
+        store = KVStorage(1, 1024, Hkv, batch=B)
+        cache = FixedKVCache(store, 0)
+        k = synthetic.kv((B, Hkv, P + 1, 128), 51, dtype=torch.bfloat16)
+        v = synthetic.kv((B, Hkv, P + 1, 128), 52, dtype=torch.bfloat16)
+        cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+        q = synthetic.query(B, Hq, 1, 53, dtype=torch.bfloat16)
+        outs.append(attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, None, None, out_dtype=torch.float32,
+                           fused=fused))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(outs[0], outs[1], rtol=0, atol=0)
+
+
+def test_long_context_bf16(gpu):
+    """32K tokens: the default split schedule over a long cache."""
+    B, Hq, Hkv, T = 1, 32, 4, 32768
+    k = synthetic.kv((B, Hkv, T, 128), 61, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, T, 128), 62, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    q = synthetic.query(B, Hq, 1, 63, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    out = scaled_dot_product_attention(q, k, v, SCALE, None, sinks, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.attention(f32(q), f32(k), f32(v), SCALE, sinks=f32(sinks))
+    assert_close(f32(out), ref, "32K bf16")
+
+
+def test_fused_decode_in_hip_graph(gpu):
+    """Fused bf16 decode steps captured in a HIP graph and replayed several
+    times, with eager work between replays, match eager steps every time."""
+    B, Hq, Hkv, P, steps = 1, 32, 4, 700, 4
+    k = synthetic.kv((B, Hkv, P + steps, 128), 71, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, P + steps, 128), 72, dtype=torch.bfloat16)
+    qs = [synthetic.query(B, Hq, 1, 80 + i, dtype=torch.bfloat16) for i in range(steps)]
+    sinks = torch.randn(Hq, device="cuda")
+
+    def run(cache, outs):
+        for i in range(steps):
+            T = P + i + 1
+            outs[i].copy_(attend(qs[i], k[:, :, T - 1 : T], v[:, :, T - 1 : T], cache, SCALE, None, sinks,
+                                 out_dtype=torch.float32))
+
+    store = KVStorage(1, 1024, Hkv)
+    cache = FixedKVCache(store, 0)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    eager = [torch.empty((B, Hq, 1, 128), device="cuda") for _ in range(steps)]
+    run(cache, eager)
+    torch.cuda.synchronize()
+
+    cache.offset = P
+    graph_out = [torch.empty_like(e) for e in eager]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(cache, graph_out)
+    for rep in range(3):
+        for o in graph_out:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(steps):
+            torch.testing.assert_close(graph_out[i], eager[i], rtol=0, atol=0, msg=f"replay {rep} step {i}")
+
+
+def test_bf16_rejects_bad_inputs(gpu):
+    k = torch.zeros((1, 4, 64, 128), dtype=torch.float16, device="cuda")
+    q = torch.zeros((1, 32, 1, 128), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        scaled_dot_product_attention(q, k, k, SCALE)
+    kb = k.to(torch.bfloat16)
+    with pytest.raises(NotImplementedError):
+        scaled_dot_product_attention(q.expand(1, 32, 2, 128), kb, kb, SCALE)
+    store = KVStorage(1, 100, 4)
+    cache = FixedKVCache(store, 0)
+    with pytest.raises(ValueError, match="Decode context limit exhausted"):
+        cache.update_and_fetch(torch.zeros((1, 4, 262145, 128), dtype=torch.bfloat16, device="cuda"),
+                               torch.zeros((1, 4, 262145, 128), dtype=torch.bfloat16, device="cuda"))
