@@ -22,7 +22,7 @@ import torch
 
 from . import _lib
 from .cache import _DTYPES, HEAD_DIM, QuantizedKV, QuantizedKVCache
-from .kvstorage import FixedKVCache
+from .kvstorage import FixedKVCache, FixedSlidingKVCache
 
 _ws_lock = threading.Lock()
 _workspaces = {}
@@ -240,6 +240,10 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
+    if isinstance(cache, FixedSlidingKVCache):
+        # the new token goes to its ring slot; decode attends over the valid slots (order-free)
+        k, v = cache.update_and_fetch(keys, values)
+        return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits)
     if isinstance(cache, FixedKVCache):
         if fused and L == 1:
             if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:

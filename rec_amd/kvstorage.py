@@ -7,8 +7,8 @@ the bf16 decode kernel (``rec_decode_bf16``).  The reference grows its
 storage in banks of 65,536 tokens up to four banks (cache.py:46-78); here a
 layer's region is one allocation whose capacity grows in the same 65,536-token
 steps to the same 262,144-token limit, the earlier contents copied over.
-Sliding-window layers (``FixedSlidingKVCache``, cache.py:153-258) are not
-covered.
+Sliding-window layers keep a ring of window slots, ``FixedSlidingKVCache``
+(cache.py:153-258); decode attends over its valid slots with the same kernel.
 """
 
 from __future__ import annotations
@@ -141,3 +141,123 @@ class FixedKVCache:
         self.offset = stop
         data = self.storage.layer(self.index, stop)
         return data[:, 0], data[:, 1]
+
+
+class FixedSlidingKVCache:
+    """Sliding-window bf16 cache (engine/src/rec_mlx/cache.py:153-258).
+
+    Two slots of ``(B, Hkv, capacity, 128)`` bf16 buffers, ``capacity =
+    min(window_size, max_sequence_tokens)``.  A single new token is written at
+    the next free slot, then round the ring; a multi-token update returns the
+    ring's tokens in order followed by the new ones (the keys a windowed
+    prefill chunk attends to) and keeps the last ``capacity`` of them in the
+    other slot.  Decode attention over the ring is order-free (softmax over a
+    set of keys), so it reads the ``size()`` valid slots in place.
+    """
+
+    def __init__(self, *, max_sequence_tokens: int, num_kv_heads: int, head_dim: int, window_size: int,
+                 dtype=torch.bfloat16, batch: int = 1, device=None):
+        if head_dim != HEAD_DIM:
+            raise NotImplementedError(f"head_dim {head_dim} is not supported (128 only)")
+        if dtype != torch.bfloat16:
+            raise NotImplementedError("the sliding cache holds bf16")
+        self.window_size = window_size
+        self.capacity = min(window_size, max_sequence_tokens)
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        shape = (batch, num_kv_heads, self.capacity, head_dim)
+        self.key_buffers = [torch.zeros(shape, dtype=dtype, device=self.device) for _ in range(2)]
+        self.value_buffers = [torch.zeros(shape, dtype=dtype, device=self.device) for _ in range(2)]
+        self.offset = 0
+        self._valid = 0
+        self._slot = 0
+        self._ring_index = 0
+
+    def grow(self, capacity: int):
+        capacity = min(self.window_size, capacity)
+        if capacity > self.capacity:
+            pad = capacity - self.capacity
+            grow = lambda t: torch.nn.functional.pad(t, (0, 0, 0, pad))  # noqa: E731
+            self.key_buffers = [grow(t) for t in self.key_buffers]
+            self.value_buffers = [grow(t) for t in self.value_buffers]
+            self.capacity = capacity
+
+    @property
+    def state(self):
+        return tuple(self.key_buffers), tuple(self.value_buffers)
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (*self.key_buffers, *self.value_buffers))
+
+    def empty(self) -> bool:
+        return self.offset == 0
+
+    def size(self) -> int:
+        return self._valid
+
+    def is_trimmable(self) -> bool:
+        return False
+
+    def make_mask(self, n_tokens: int, window_size=None, return_array: bool = False):
+        """None for one decode token, "causal" for a first chunk within the
+        window, else the windowed causal boolean array (cache.py:199-205)."""
+        window = self.window_size if window_size is None else window_size
+        if n_tokens == 1 and not return_array:
+            return None
+        if self._valid == 0 and n_tokens <= window and not return_array:
+            return "causal"
+        T = self._valid + n_tokens
+        q = torch.arange(T - n_tokens, T)[:, None]
+        k = torch.arange(T)[None]
+        return (q >= k) & (q < k + window)
+
+    def _next_index(self) -> int:
+        """Slot the next single token goes to; advances the ring."""
+        if self._valid < self.capacity:
+            index = self._valid
+            self._valid += 1
+        else:
+            index = self._ring_index
+            self._ring_index = (self._ring_index + 1) % self.capacity
+        return index
+
+    def _write(self, index: int, keys: torch.Tensor, values: torch.Tensor):
+        kb, vb = self.key_buffers[self._slot], self.value_buffers[self._slot]
+        B, H, L, D = keys.shape
+        k, ksb, ksh, kst = _stride3(keys)
+        v, vsb, vsh, vst = _stride3(values)
+        rc = _lib.load().rec_kv_write_bf16(
+            k.data_ptr(), v.data_ptr(), _DTYPES[keys.dtype], ksb, ksh, kst, vsb, vsh, vst,
+            kb.data_ptr(), kb.stride(0), kb.stride(1), vb.data_ptr(), vb.stride(0), vb.stride(1),
+            B, H, L, D, index, self.capacity, torch.cuda.current_stream(self.device).cuda_stream,
+        )
+        _lib.check(rc, "rec_kv_write_bf16")
+
+    def _prior(self):
+        keys, values = self.key_buffers[self._slot], self.value_buffers[self._slot]
+        if self._valid == self.capacity and self._ring_index:
+            r = self._ring_index
+            return (torch.cat((keys[:, :, r:], keys[:, :, :r]), dim=2),
+                    torch.cat((values[:, :, r:], values[:, :, :r]), dim=2))
+        return keys[:, :, : self._valid], values[:, :, : self._valid]
+
+    def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
+        if keys.shape != values.shape or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
+            raise ValueError("keys/values must share a shape and a float dtype")
+        if keys.shape[-2] == 1:
+            self._write(self._next_index(), keys, values)
+            self.offset += 1
+            return (self.key_buffers[self._slot][:, :, : self._valid],
+                    self.value_buffers[self._slot][:, :, : self._valid])
+        prior_keys, prior_values = self._prior()
+        attention_keys = torch.cat((prior_keys, keys.to(torch.bfloat16)), dim=2)
+        attention_values = torch.cat((prior_values, values.to(torch.bfloat16)), dim=2)
+        retained = min(self.capacity, attention_keys.shape[2])
+        nxt = 1 - self._slot
+        self.key_buffers[nxt][:, :, :retained] = attention_keys[:, :, -retained:]
+        self.value_buffers[nxt][:, :, :retained] = attention_values[:, :, -retained:]
+        self._slot = nxt
+        self._valid = retained
+        self._ring_index = 0
+        self.offset += keys.shape[2]
+        return attention_keys, attention_values

@@ -154,3 +154,39 @@ def test_bf16_rejects_bad_inputs(gpu):
     with pytest.raises(ValueError, match="Decode context limit exhausted"):
         cache.update_and_fetch(torch.zeros((1, 4, 262145, 128), dtype=torch.bfloat16, device="cuda"),
                                torch.zeros((1, 4, 262145, 128), dtype=torch.bfloat16, device="cuda"))
+
+
+def test_sliding_window_ring_decode(gpu):
+    """A window-40 ring fed 1-token steps well past the window (and one
+    multi-token chunk): every decode step attends exactly the last
+    min(window, offset) tokens (cache.py:153-258)."""
+    from rec_amd import FixedSlidingKVCache
+
+    B, Hq, Hkv, W = 1, 16, 2, 40
+    cache = FixedSlidingKVCache(max_sequence_tokens=4096, num_kv_heads=Hkv, head_dim=128, window_size=W)
+    n = 130
+    k = synthetic.kv((B, Hkv, n, 128), 91, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, n, 128), 92, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    pos = 0
+    for step in range(n):
+        if step == 60:  # one multi-token chunk: returns ring order + new tokens, keeps the last W
+            kk, vv = cache.update_and_fetch(k[:, :, pos : pos + 7], v[:, :, pos : pos + 7])
+            np.testing.assert_array_equal(kk.float().cpu().numpy(), bf16_np(k[:, :, max(0, pos + 7 - W - 7) : pos + 7])[:, :, -kk.shape[2]:])
+            pos += 7
+            assert cache.size() == W and cache.offset == pos
+            continue
+        if pos >= n:
+            break
+        q = synthetic.query(B, Hq, 1, 100 + step, dtype=torch.bfloat16)
+        out = attend(q, k[:, :, pos : pos + 1], v[:, :, pos : pos + 1], cache, SCALE, None, sinks,
+                     out_dtype=torch.float32)
+        pos += 1
+        lo = max(0, pos - W)
+        torch.cuda.synchronize()
+        assert cache.size() == pos - lo
+        ref = O.attention(f32(q), bf16_np(k[:, :, lo:pos]), bf16_np(v[:, :, lo:pos]), SCALE, sinks=f32(sinks))
+        assert_close(f32(out), ref, f"step {step}")
+    assert cache.make_mask(1) is None
+    m = cache.make_mask(3, return_array=True)
+    assert m.shape == (3, W + 3) and bool(m[0, 0]) is False and bool(m[2, -1]) is True
