@@ -17,7 +17,8 @@
  *   int4 V codes  uint8 [B][Hkv][C/32][2][16][4][4][4]  dim 16n+c, position p = 8g+e at
  *                                                   [n/4][c][g][n%4][e/2], low nibble = even e
  *   int8 scales   fp16  [B][Hkv][C/32][32]          one per (token, head), position p
- *   int4 scale/zp fp16  [B][Hkv][C/32][4][32]       per 32-dim group, position p
+ *   int4 scale/zp fp16  [B][Hkv][C/32][4][32]       per 32-dim group, at slot
+ *                                                    (p & ~7) | 2*(p & 3) | ((p >> 2) & 1)
  * Quantizers: int8 symmetric s = fp16(amax/127), q = clamp(rint(x/s), ±127);
  * uint4 asymmetric over [min(0, x), max(0, x)], s = fp16(range/15),
  * z = clamp(rint(-min/s), 0, 15), q = clamp(rint(x/s) + z, 0, 15).

@@ -87,6 +87,15 @@ def block_pos(t):
 _POS = [block_pos(t) for t in range(BLOCK)]
 
 
+def s4_slot(p):
+    """Slot of block position ``p`` in a 4-bit scale / zero-point row: each run
+    of 8 positions is stored in the order 0,4,1,5,2,6,3,7."""
+    return (p & ~7) | (2 * (p & 3)) | ((p >> 2) & 1)
+
+
+_SLOT4 = [s4_slot(p) for p in _POS]
+
+
 def to_logical(kv: QuantizedKV, length: Optional[int] = None):
     """Return ``(codes, scales, zeros)`` in the plain layout, first ``length`` tokens.
 
@@ -116,8 +125,9 @@ def to_logical(kv: QuantizedKV, length: Optional[int] = None):
         sc = kv.scales[..., pos].reshape(B, H, -1)
         zp = None
     else:
-        sc = kv.scales[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
-        zp = kv.zeros[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
+        slot = torch.tensor(_SLOT4, device=kv.codes.device)
+        sc = kv.scales[..., slot].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
+        zp = kv.zeros[..., slot].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
     return (
         codes[:, :, :T].contiguous(),
         sc[:, :, :T].contiguous(),

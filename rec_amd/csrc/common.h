@@ -10,7 +10,7 @@
 //   int4 V codes   uint8 [B][Hkv][C/32][2][16][4][4][4]  dim 16n+c, position p = 8g+e at
 //                                                   [n/4][c][g][n%4][e/2], low nibble = even e
 //   int8 scales    fp16  [B][Hkv][C/32][32]          one per (token, head), K and V, position p
-//   int4 scale/zp  fp16  [B][Hkv][C/32][4][32]       per 32-dim group, position p
+//   int4 scale/zp  fp16  [B][Hkv][C/32][4][32]       per 32-dim group, slot s4_slot(p)
 // Every load of the decode kernel reads one contiguous span: an int8 Q·Kᵀ
 // operand is 16 tokens x 64 bytes of one K half, an int8 P·V operand 16 dims x
 // 32 tokens, an int4 lane's K bytes (both halves) and V bytes (four dim
@@ -46,6 +46,12 @@ enum InDtype { DT_F16 = 0, DT_BF16 = 1, DT_F32 = 2 };
 // lane read its V codes and scales with one load each.  Tokens t and t^1 stay
 // neighbours (positions p and p^1), so a uint4 byte never straddles blocks.
 __host__ __device__ constexpr int block_pos(int t) { return ((t >> 2) & 3) * 8 + (t >> 4) * 4 + (t & 3); }
+
+// Slot of block position p in a 4-bit scale / zero-point row.  Inside each run
+// of 8 positions the slots hold positions 0,4,1,5,2,6,3,7: a uint4 V nibble
+// unpack yields the codes of positions (e, e+4) as one fp16 pair, and their
+// scales (zero-points) then sit in one dword.
+__host__ __device__ constexpr int s4_slot(int p) { return (p & ~7) | (2 * (p & 3)) | ((p >> 2) & 1); }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
   _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);

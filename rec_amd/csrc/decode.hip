@@ -284,7 +284,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       }
     }
   }
-  // ---------------- scores (log2 domain) ----------------
+  // ---------------- scores ----------------
+  // In units of the query quantization step: the step (qsc) is applied in the
+  // exponent below, where it costs an fma instead of a multiply per score.
   float s[8];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -292,11 +294,14 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       v4i d = {0, 0, 0, 0};
       d = __builtin_amdgcn_mfma_i32_16x16x64_i8(R.k8[j][0], qop[0], d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_i32_16x16x64_i8(R.k8[j][1], qop[1], d, 0, 0, 0);
+      // columns c < 8 hold the high query byte, c + 8 the low one: the lane
+      // weights its own sum and its partner's by 256 and 1 (or 1 and 256)
+      const int sh_mine = c < 8 ? 8 : 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int mine = d[i], partner = dpp_ror8(mine);
-        const int full = c < 8 ? mine * 256 + partner : partner * 256 + mine;
-        s[4 * j + i] = (float)full * (half_at(ks, 4 * j + i) * qsc);
+        const int full = (mine << sh_mine) + (partner << (8 - sh_mine));
+        s[4 * j + i] = (float)full * half_at(ks, 4 * j + i);
       }
     } else {
       const v4i ka = widen_u4((v2i){R.k4[j][0], R.k4[j][1]}), kb = widen_u4((v2i){R.k4[j][2], R.k4[j][3]});
@@ -307,13 +312,14 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       dbl = __builtin_amdgcn_mfma_i32_16x16x64_i8(kb, qop[3], dbl, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int idx = 4 * j + i;
-        // Σ (k - z) q over one 32-dim group, in float: |k - z| <= 15 and
-        // |q| <= 32512 keep every intermediate an integer below 2^24, so exact
-        const float ta = fmaf(-half_at(kz4[0], idx), qsum_a, fmaf((float)dah[i], 256.f, (float)dal[i]));
-        const float tb = fmaf(-half_at(kz4[1], idx), qsum_b, fmaf((float)dbh[i], 256.f, (float)dbl[i]));
-        const float part = half_at(ks4[0], idx) * ta + half_at(ks4[1], idx) * tb;
-        s[idx] = (part + dpp_ror8f(part)) * qsc;
+        const int idx = 4 * j + i, sl = 2 * i + j;  // position idx of the lane's run sits at slot sl
+        // Σ (k - z) q over one 32-dim group: the high/low byte sums combine
+        // exactly in int32; |k - z| <= 15 and |q| <= 32512 keep every float
+        // intermediate an integer below 2^24, so the fma is exact too
+        const float ta = fmaf(-half_at(kz4[0], sl), qsum_a, (float)((dah[i] << 8) + dal[i]));
+        const float tb = fmaf(-half_at(kz4[1], sl), qsum_b, (float)((dbh[i] << 8) + dbl[i]));
+        const float part = fmaf(half_at(ks4[0], sl), ta, half_at(ks4[1], sl) * tb);
+        s[idx] = part + dpp_ror8f(part);
       }
     }
   }
@@ -323,11 +329,11 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       if (16 * (idx >> 2) + 4 * kg + (idx & 3) >= valid) s[idx] = NEG_INF;
   }
 
-  // ---------------- online softmax ----------------
+  // ---------------- online softmax (log2 domain: score * qsc) ----------------
   float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
   cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
   cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
-  const float m_new = fmaxf(st.m, cmax);
+  const float m_new = fmaxf(st.m, cmax * qsc);  // qsc > 0
   if (__ballot(m_new > st.m)) {  // some head's max moved: rescale (rare after warm-up)
     const float factor = __builtin_amdgcn_exp2f(st.m - m_new);
     st.l *= factor;
@@ -338,7 +344,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   float p[8];
 #pragma unroll
   for (int idx = 0; idx < 8; ++idx) {
-    p[idx] = __builtin_amdgcn_exp2f(s[idx] - st.m);
+    p[idx] = __builtin_amdgcn_exp2f(fmaf(s[idx], qsc, -st.m));
     st.l += p[idx];
   }
 
@@ -353,46 +359,42 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb, st.acc[n], 0, 0, 0);
     }
   } else {
-    // uint4 V is dequantized in the A operand: (q - z) * s per element in
-    // packed fp16 (q - z is exact, one rounding in the product), so the B
-    // operand is the fp16 probabilities alone.  The nibble unpack yields token
-    // pairs (t, t+4) of the lane's eight; scales and zero-points are paired
-    // the same way with byte permutes.
-    v8h pb;
+    // uint4 V: the A operand is q - z, exact in fp16, and the scale of the
+    // (token, group) goes into the B operand, fp16(p) * s, one B operand per
+    // 32-dim group.  The nibble unpack yields positions (e, e+4) of the lane's
+    // run as one fp16 pair: low nibbles under the fp16 exponent of 1024 read
+    // 1024 + q, high nibbles under that of 64 read 64 + q.  Scales and
+    // zero-points are stored in that pair order (s4_slot), so dword e of a
+    // run is the pair for unpack step e.
+    v2h pp[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) pb[k] = (_Float16)p[(k >> 1) + 4 * (k & 1)];
+    for (int e = 0; e < 4; ++e) pp[e] = (v2h){(_Float16)p[e], (_Float16)p[e + 4]};
+    const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      // pairs q4 = 0, 2 unpack to 1024 + q: subtract 1024 + z;
-      // pairs q4 = 1, 3 unpack to 1024 + 16 q: (t / 16) - (64 + z), exact
-      v2h sp[4], zq[4];
-      const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+      v8h pb;
+      v2h zq[4];
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const uint32_t s_lo = (uint32_t)vs4[g][h2], s_hi = (uint32_t)vs4[g][h2 + 2];
-        const uint32_t z_lo = (uint32_t)vz4[g][h2], z_hi = (uint32_t)vz4[g][h2 + 2];
-        // word h2 holds tokens (2h2, 2h2+1), word h2+2 tokens (2h2+4, 2h2+5)
-        sp[2 * h2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(s_hi, s_lo, 0x05040100u));
-        sp[2 * h2 + 1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(s_hi, s_lo, 0x07060302u));
-        zq[2 * h2] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(z_hi, z_lo, 0x05040100u)) + k1024;
-        zq[2 * h2 + 1] = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(z_hi, z_lo, 0x07060302u)) + k64;
+      for (int e = 0; e < 4; ++e) {
+        // copies first: a bit_cast of a vector subscript reads element 0
+        const uint32_t sw = (uint32_t)vs4[g][e], zw = (uint32_t)vz4[g][e];
+        const v2h t = pp[e] * __builtin_bit_cast(v2h, sw);
+        pb[2 * e] = t[0];
+        pb[2 * e + 1] = t[1];
+        zq[e] = __builtin_bit_cast(v2h, zw) + ((e & 1) ? k64 : k1024);
       }
-      const v2h k16th = {(_Float16)0.0625f, (_Float16)0.0625f};
 #pragma unroll
       for (int nn = 0; nn < 2; ++nn) {
         const int n = 2 * g + nn;
         const uint32_t w = (uint32_t)R.v4[n >> 2][n & 3], w8 = w >> 8;
         v8h a;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          // 1024 + q (q4 even) or 1024 + 16 q (q4 odd) for tokens (q4, q4 + 4)
-          const uint32_t src = q4 < 2 ? w : w8;
-          const uint32_t t = and_or(src, (q4 & 1) ? 0x00f000f0u : 0x000f000fu, 0x64006400u);
-          const v2h th = __builtin_bit_cast(v2h, t);
-          const v2h d = (q4 & 1) ? th * k16th - zq[q4] : th - zq[q4];
-          const v2h v = d * sp[q4];
-          a[2 * q4] = v[0];
-          a[2 * q4 + 1] = v[1];
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t t = (e & 1) ? and_or(e < 2 ? w : w8, 0x00f000f0u, 0x54005400u)
+                                     : and_or(e < 2 ? w : w8, 0x000f000fu, 0x64006400u);
+          const v2h d = __builtin_bit_cast(v2h, t) - zq[e];
+          a[2 * e] = d[0];
+          a[2 * e + 1] = d[1];
         }
         st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, st.acc[n], 0, 0, 0);
       }
@@ -489,7 +491,10 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
   v4i qop[NOP];
 #pragma unroll
   for (int o = 0; o < NOP; ++o) qop[o] = ((const v4i*)(smem + LDS_QOP))[o * 64 + lane];
-  const float qsc = ((const float*)(smem + LDS_QSC))[c & 7];
+  // query quantization step of this lane's head; an all-zero query has step 0
+  // and all-zero scores, for which any positive step is exact
+  const float qsc_h = ((const float*)(smem + LDS_QSC))[c & 7];
+  const float qsc = qsc_h > 0.f ? qsc_h : 1.f;
   float qsum_a = 0.f, qsum_b = 0.f;  // int4 K: per-group query sums of this lane's two groups (exact)
   if constexpr (KB == 4) {
     const int* qsum = (const int*)(smem + LDS_QSUM);

@@ -116,9 +116,9 @@ __device__ __forceinline__ int64_t v4_off(int64_t bh, int64_t cap, int64_t t, in
 __device__ __forceinline__ int64_t s8_off(int64_t bh, int64_t cap, int64_t t) {
   return blk_base(bh, cap, t, 32) + block_pos((int)(t & 31));
 }
-// per-(token, group) scale / zero-point (int4)
+// per-(token, group) scale / zero-point (int4), at slot s4_slot(position)
 __device__ __forceinline__ int64_t s4_off(int64_t bh, int64_t cap, int64_t t, int g) {
-  return blk_base(bh, cap, t, 128) + g * 32 + block_pos((int)(t & 31));
+  return blk_base(bh, cap, t, 128) + g * 32 + s4_slot(block_pos((int)(t & 31)));
 }
 
 // Quantize row (b, h, t_src) of `src` and store it at cache position `pos`.

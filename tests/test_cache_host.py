@@ -79,8 +79,11 @@ def _store_scales(logical, groups=None):
         return out
     B, H, T, G = logical.shape
     out = np.zeros((B, H, T // 32, G, 32), logical.dtype)
+    order = [0, 4, 1, 5, 2, 6, 3, 7]  # positions held by the 8 slots of each run
     for t in range(T):
-        out[:, :, t // 32, :, _pos(t % 32)] = logical[:, :, t, :]
+        p = _pos(t % 32)
+        slot = (p // 8) * 8 + order.index(p % 8)
+        out[:, :, t // 32, :, slot] = logical[:, :, t, :]
     return out
 
 
