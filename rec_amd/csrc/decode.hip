@@ -158,9 +158,10 @@ struct Chunk {
   v4i k4[2];      // int4 K: tile j, both halves (8 packed bytes each)
   v4i v8[4];      // int8 V: dim blocks 2h, 2h+1 (8 bytes each), this lane's 8 tokens
   v4i v4[2];      // int4 V: dim blocks 4h..4h+3, this lane's 8 tokens packed
-  uint32_t m[4];  // scales (and int4 zero-points) of the block, one dword per lane:
-                  // [0] K scales, [1] int4 K zeros, [2] V scales, [3] int4 V zeros (int8
-                  // scales on lanes 0-15 only); handed out through LDS
+  v4i s8[2];      // int8 scales of this lane's 8 positions: [0] K, [1] V
+  uint32_t m[4];  // int4 scales and zero-points of the block, one dword per lane:
+                  // [0] K scales, [1] K zeros, [2] V scales, [3] V zeros; handed out
+                  // through LDS
 };
 
 // Buffer resources of one (b, h) slice of the cache, plus an empty one.  Every
@@ -180,7 +181,7 @@ struct Res {
 struct LaneOff {
   uint32_t k[2];  // K codes, tile j (int8: the second MFMA half is +2048)
   uint32_t v;     // V codes, run h at +1024 h
-  uint32_t m8;    // int8 scale dword of this lane (out of range past lane 15: reads zero)
+  uint32_t s8;    // int8 scales of this lane's positions 8kg .. 8kg+7
   uint32_t m4;    // int4 scale / zero-point dword of this lane
 };
 
@@ -191,7 +192,7 @@ __device__ __forceinline__ LaneOff lane_offsets(int lane) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) o.k[j] = (16 * j + c) * 64 + 16 * kg;
   o.v = (c * 4 + kg) * 16;
-  o.m8 = lane < 16 ? 4 * lane : 0x40000000u;
+  o.s8 = 16 * kg;
   o.m4 = 4 * lane;
   return o;
 }
@@ -215,7 +216,7 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
     }
   }
   if constexpr (KB == 8) {
-    R.m[0] = ld32(rks, o.m8, blk * 64);
+    R.s8[0] = ld128(rks, o.s8, blk * 64);
   } else {
     R.m[0] = ld32(rks, o.m4, blk * 256);
     R.m[1] = ld32(rkz, o.m4, blk * 256);
@@ -224,7 +225,7 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
   if constexpr (VB == 8) {
 #pragma unroll
     for (int h = 0; h < 4; ++h) R.v8[h] = ld128(rv, o.v + h * 1024, blk * 4096);
-    R.m[2] = ld32(rvs, o.m8, blk * 64);
+    R.s8[1] = ld128(rvs, o.s8, blk * 64);
   } else {
     R.v4[0] = ld128(rv, o.v, blk * 2048);
     R.v4[1] = ld128(rv, o.v + 1024, blk * 2048);
@@ -242,31 +243,25 @@ template <int KB, int VB>
 __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, float qsum_a,
                                               float qsum_b, int valid, int lane, char* meta) {
   const int c = lane & 15, kg = lane >> 4;
-  // Scales (and int4 zero-points) arrive one dword per lane; this wavefront's
-  // LDS region hands each lane the 16-byte runs it needs (positions
-  // 8kg .. 8kg+7).  int8: [K scales 64 B][V scales 64 B]; int4:
-  // [K scales][K zeros][V scales][V zeros], 256 B each ([4 groups][32 positions]).
+  // int8 scales arrive as the lane's own 16-byte run (positions 8kg ..
+  // 8kg+7).  int4 scales and zero-points arrive one dword per lane; this
+  // wavefront's LDS region ([K scales][K zeros][V scales][V zeros], 256 B
+  // each, [4 groups][32 slots]) hands each lane the 16-byte runs it needs.
   v4i ks, vs, ks4[2], kz4[2], vs4[4], vz4[4];
-  {
+  if constexpr (KB == 8) ks = R.s8[0];
+  if constexpr (VB == 8) vs = R.s8[1];
+  if constexpr (KB == 4 || VB == 4) {
     uint32_t* mw = (uint32_t*)meta;
-    if constexpr (KB == 8) {
-      if (lane < 16) mw[lane] = R.m[0];
-    } else {
+    if constexpr (KB == 4) {
       mw[lane] = R.m[0];
       mw[64 + lane] = R.m[1];
     }
-    if constexpr (VB == 8) {
-      if (lane < 16) mw[(KB == 8 ? 16 : 128) + lane] = R.m[2];
-    } else {
+    if constexpr (VB == 4) {
       mw[128 + lane] = R.m[2];
       mw[192 + lane] = R.m[3];
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if constexpr (KB == 8) {
-      ks = *(const v4i*)(meta + 16 * kg);
-    } else {
+    wave_lds_sync();
+    if constexpr (KB == 4) {
 #pragma unroll
       for (int gi = 0; gi < 2; ++gi) {
         const int off = (2 * gi + (c >> 3)) * 64 + 16 * kg;  // this lane's groups: 2gi + (c >= 8)
@@ -274,9 +269,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         kz4[gi] = *(const v4i*)(meta + 256 + off);
       }
     }
-    if constexpr (VB == 8) {
-      vs = *(const v4i*)(meta + (KB == 8 ? 64 : 512) + 16 * kg);
-    } else {
+    if constexpr (VB == 4) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         vs4[g] = *(const v4i*)(meta + 512 + g * 64 + 16 * kg);
@@ -330,12 +323,16 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   }
 
   // ---------------- online softmax (log2 domain: score * qsc) ----------------
+  // A head's max over the chunk exceeds its running max iff one of its four
+  // lanes' own maxima does, so the cross-lane reduction and the rescale run
+  // only then (rare after the first chunks).
   float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-  cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
-  cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
-  const float m_new = fmaxf(st.m, cmax * qsc);  // qsc > 0
-  if (__ballot(m_new > st.m)) {  // some head's max moved: rescale (rare after warm-up)
-    const float factor = __builtin_amdgcn_exp2f(st.m - m_new);
+  cmax *= qsc;  // qsc > 0
+  if (__ballot(cmax > st.m)) {
+    cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
+    cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
+    const float m_new = fmaxf(st.m, cmax);
+    const float factor = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first chunk, 1 if unchanged
     st.l *= factor;
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.acc[n] *= factor;
