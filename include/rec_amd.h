@@ -192,6 +192,32 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
                     void* workspace, size_t workspace_bytes, float* out, void* stream);
 
+/*
+ * int4 group-64 GEMV (MLX affine 4-bit, the format of the decoder's
+ * projections, experts and lm head): y[m] = x[m] · Wᵀ for an (N, K) matrix
+ * given as MLX words w (N, K/8) uint32 (code e of a word at bits 4e), bf16
+ * scales and biases (N, K/64), element (r, k) = s·q + b.
+ *
+ * rec_q4_packed_bytes: bytes of the repacked matrix (0 if N < 1 or K is not a
+ * positive multiple of 128).  Row tiles are 16 rows: the rows [16t, N) of a
+ * packed matrix start at byte t · (K/128) · 1152.
+ * rec_q4_pack: repack w / scales / biases (contiguous, 16-byte aligned w) into
+ * `packed` (16-byte aligned, at least rec_q4_packed_bytes).  Once per matrix,
+ * as the reference packs its weight banks, megakernel.py:1017-1040.
+ * rec_q4_gemv: M (1..8) bf16 vectors x (row stride x_stride elements, a
+ * multiple of 8; 16-byte aligned) to out (out_dtype REC_BF16, rounded to
+ * nearest even as the reference stores bfloat16_t, or REC_F32; row stride
+ * out_stride elements).
+ * Replaces q4 / dot16 (and q4_local) of
+ * engine/src/rec_mlx/kernels/megakernel.py:161-232, the projections of
+ * model.py:151-154 quantized by quantized.py:27-36 (group 64, 4 bits, affine).
+ */
+size_t rec_q4_packed_bytes(int64_t N, int64_t K);
+int rec_q4_pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int64_t N, int64_t K,
+                void* packed, size_t packed_bytes, void* stream);
+int rec_q4_gemv(const void* packed, int64_t N, int64_t K, const uint16_t* x, int64_t x_stride, int M,
+                void* out, int out_dtype, int64_t out_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

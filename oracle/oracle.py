@@ -20,6 +20,10 @@ Reference semantics restated here (paths relative to the rec repository):
   ``:276-318`` (merge: top = max m_p, z = Σ e^{m_p-top} l_p,
   out = Σ e^{m_p-top} acc_p / z, or acc when z == 0).
 * chunked prefill over the quantized cache: ``engine/src/rec_mlx/model.py:191-203``.
+* int4 group-64 GEMV of the decoder's projections:
+  ``engine/src/rec_mlx/kernels/megakernel.py:161-232`` (``q4`` / ``dot16``:
+  per run of 16 elements ``s·Σ q x + b·Σ x``, summed over the row) on MLX
+  affine 4-bit matrices (``quantized.py:27-36``: group 64, bits 4).
 
 KV formats.  The reference's own cache uses MLX affine group-64 quantization
 (``model.py:77-78``); MLX is third-party (mlx==0.32.0) and cannot run here, so
@@ -72,6 +76,9 @@ __all__ = [
     "split_k_decode",
     "split_k_decode_quantized",
     "causal_mask",
+    "q4_unpack",
+    "q4_dequantize",
+    "q4_gemv",
 ]
 
 FP16_MAX = np.float32(65504.0)
@@ -282,3 +289,38 @@ def split_k_decode_quantized(q, cache, T, scale, sinks=None, chunk=4096, workers
     return split_k_decode(
         q, deq("k", cache["k_bits"]), deq("v", cache["v_bits"]), T, scale, sinks, chunk=chunk, workers=workers
     )
+
+
+# ---------------------------------------------------------------------------
+# int4 group-64 GEMV (engine/src/rec_mlx/kernels/megakernel.py:161-232)
+
+
+def q4_unpack(w):
+    """MLX 4-bit words ``(N, K/8)`` uint32 -> codes ``(N, K)`` uint8.
+
+    Code ``e`` of a word sits at bits ``4e``: ``dot16`` reads the same order
+    through little-endian ushorts, element ``4j + t`` of a 16-element run at
+    bits ``4t`` of ushort ``j`` (``megakernel.py:189-195``).
+    """
+    w = np.asarray(w).astype(np.uint32)
+    shifts = np.arange(8, dtype=np.uint32) * np.uint32(4)
+    return ((w[..., None] >> shifts) & np.uint32(15)).astype(np.uint8).reshape(w.shape[0], -1)
+
+
+def q4_dequantize(w, scales, biases, group=64):
+    """Element ``(r, k)`` of the matrix: ``s[r, k // 64] * q + b[r, k // 64]`` in float64."""
+    q = q4_unpack(w).astype(np.float64)
+    s = np.repeat(np.asarray(scales, np.float64), group, axis=1)
+    b = np.repeat(np.asarray(biases, np.float64), group, axis=1)
+    return s * q + b
+
+
+def q4_gemv(x, w, scales, biases, group=64):
+    """``y[m, r] = Σ_g s[r, g] Σ_{k∈g} q[r, k] x[m, k] + b[r, g] Σ_{k∈g} x[m, k]``.
+
+    ``x`` is ``(M, K)`` (bf16 values), ``w`` ``(N, K/8)`` uint32, ``scales`` and
+    ``biases`` ``(N, K/64)`` (bf16 values).  Float64; the reference sums the
+    same terms in float32 and stores bfloat16 (``megakernel.py:198-214``).
+    """
+    x = np.asarray(x, np.float64)
+    return x @ q4_dequantize(w, scales, biases, group).T

@@ -458,4 +458,56 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, cons
   return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
 }
 
+size_t rec_q4_packed_bytes(int64_t N, int64_t K) {
+  if (N < 1 || K < 128 || K % 128 != 0) return 0;
+  return (size_t)((N + 15) / 16) * (size_t)(K / 128) * 1152;
+}
+
+int rec_q4_pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int64_t N, int64_t K,
+                void* packed, size_t packed_bytes, void* stream) {
+  const size_t need = rec_q4_packed_bytes(N, K);
+  if (need == 0) return fail(REC_EINVAL, "q4 matrix must have N >= 1 and K a positive multiple of 128 (N=%lld K=%lld)",
+                             (long long)N, (long long)K);
+  if (!w || !scales || !biases || !packed) return fail(REC_EINVAL, "q4 pack: null pointer");
+  if (!aligned16(w) || !aligned16(packed)) return fail(REC_EALIGN, "q4 pack: w and packed must be 16-byte aligned");
+  if (packed_bytes < need) return fail(REC_EWORKSPACE, "q4 pack: packed buffer has %zu bytes, needs %zu", packed_bytes, need);
+  if ((N + 15) / 16 > 65535) return fail(REC_EUNSUPPORTED, "q4 pack: N=%lld exceeds 1048560 rows", (long long)N);
+  Q4PackArgs a;
+  a.w = w;
+  a.scales = scales;
+  a.biases = biases;
+  a.N = N;
+  a.K = K;
+  a.packed = (uint8_t*)packed;
+  return launched(launch_q4_pack(a, (hipStream_t)stream), "q4 pack launch");
+}
+
+int rec_q4_gemv(const void* packed, int64_t N, int64_t K, const uint16_t* x, int64_t x_stride, int M, void* out,
+                int out_dtype, int64_t out_stride, void* stream) {
+  if (rec_q4_packed_bytes(N, K) == 0)
+    return fail(REC_EINVAL, "q4 matrix must have N >= 1 and K a positive multiple of 128 (N=%lld K=%lld)",
+                (long long)N, (long long)K);
+  if (M < 1 || M > Q4_MAX_M) return fail(REC_EINVAL, "q4 gemv: M=%d vectors, 1..%d supported", M, Q4_MAX_M);
+  if (!packed || !x || !out) return fail(REC_EINVAL, "q4 gemv: null pointer");
+  if (out_dtype != REC_BF16 && out_dtype != REC_F32) return fail(REC_EINVAL, "q4 gemv: out dtype must be bf16 or f32");
+  if (M > 1 && (x_stride < K || out_stride < N))
+    return fail(REC_EINVAL, "q4 gemv: row strides (%lld, %lld) shorter than rows (%lld, %lld)", (long long)x_stride,
+                (long long)out_stride, (long long)K, (long long)N);
+  if (!aligned16(packed) || !aligned16(x) || (M > 1 && x_stride % 8 != 0))
+    return fail(REC_EALIGN, "q4 gemv: packed and x must be 16-byte aligned, x_stride a multiple of 8");
+  if (q4_gemv_lds_bytes(M, K) > 160 * 1024)
+    return fail(REC_EUNSUPPORTED, "q4 gemv: M=%d vectors of K=%lld exceed the LDS staging", M, (long long)K);
+  Q4GemvArgs a;
+  a.packed = (const uint8_t*)packed;
+  a.N = N;
+  a.K = K;
+  a.x = x;
+  a.x_stride = x_stride;
+  a.M = M;
+  a.out = out;
+  a.out_dtype = out_dtype == REC_F32 ? DT_F32 : DT_BF16;
+  a.out_stride = out_stride;
+  return launched(launch_q4_gemv(a, (hipStream_t)stream), "q4 gemv launch");
+}
+
 }  // extern "C"

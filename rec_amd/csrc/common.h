@@ -89,6 +89,14 @@ __device__ __forceinline__ float dpp_ror8f(float x) {
   return __builtin_bit_cast(float, dpp_ror8(__builtin_bit_cast(int, x)));
 }
 
+// (x & m) | o in one v_and_or_b32 (the compiler splits it when both constants
+// would need the single scalar operand slot).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+  return r;
+}
+
 __device__ __forceinline__ float shfl_xor_f(float x, int m) {
   return __shfl_xor(x, m, 64);
 }

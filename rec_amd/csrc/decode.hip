@@ -59,14 +59,6 @@ constexpr int LDS_BYTES = LDS_META + WAVES * 1024;
 // j holds element perm16(j) of the 16.
 __device__ __forceinline__ int u4_unpacked_pos(int o) { return (o & 8) + 4 * (o & 1) + ((o & 7) >> 1); }
 
-// (x & m) | o in one v_and_or_b32 (the compiler splits it when both constants
-// would need the single scalar operand slot).
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
-  return r;
-}
-
 __device__ __forceinline__ v4i widen_u4(v2i w) {
   const uint32_t w0 = (uint32_t)w[0], w1 = (uint32_t)w[1];
   v4i r;

@@ -1,0 +1,237 @@
+// int4 group-64 GEMV of the decoder's projections on bf16 MFMA.
+//
+// Restates q4 / dot16 of engine/src/rec_mlx/kernels/megakernel.py:161-232:
+// y[m][r] = Σ_g ( s[r][g] · Σ_{k∈g} q[r][k] x[m][k] + b[r][g] · Σ_{k∈g} x[m][k] )
+// for an MLX affine 4-bit matrix (group 64: uint32 words of 8 codes, code e
+// at bits 4e; bf16 scales and biases per (row, group)), bf16 x and a bf16 (or
+// fp32) result.  The weights are repacked once (q4_pack_kernel) into records
+// that one wavefront streams linearly.
+//
+// Packed layout: per 16-row tile and 128-element span, one 1152-byte record
+//   [64 lanes][16 B]  codes: lane (r, kq) holds row r, elements 32kq .. 32kq+31
+//                     of the span (four MLX words, unchanged)
+//   [4 rg][2 gs][16 B] row group rg, group 2·span+gs: scales of rows 4rg..4rg+3
+//                     (4 x bf16), then their biases (4 x bf16)
+// Records are ordered [tile][span]; rows past N are zero.
+//
+// Arithmetic: the codes enter a bf16 MFMA 16x16x32 as 128 + q (exact: the
+// nibble under the bf16 exponent of 128), x as bf16, products exact in fp32.
+// The B operand's 16 columns are (vector m, group half gs): a column only
+// holds x for the elements of its group, so one MFMA yields separate sums
+// D = Σ (128 + q) x for the two groups of a span, and
+// y += s·D + (b − 128 s)·X with X = Σ x over the group.
+#include "kernels.h"
+
+namespace rec {
+
+namespace {
+
+constexpr int GV_WAVES = 4;
+constexpr int GV_SPAN = 128;         // elements per span
+constexpr int GV_REC = 1024 + 128;   // bytes per (tile, span) record
+constexpr int GV_ZERO = 256;         // zero bytes read by B lanes without data
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// bf16 round-to-nearest-even of a finite or infinite float (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+}  // namespace
+
+// One workgroup of 64 threads per (tile, span) record.
+__global__ __launch_bounds__(64) void q4_pack_kernel(const Q4PackArgs a) {
+  const int l = threadIdx.x;
+  const int64_t tile = blockIdx.y, span = blockIdx.x;
+  const int64_t S = a.K / GV_SPAN, words = a.K / 8, groups = a.K / 64;
+  uint8_t* rec = a.packed + (tile * S + span) * GV_REC;
+  {
+    const int64_t row = tile * 16 + (l & 15);
+    v4i w = {0, 0, 0, 0};
+    if (row < a.N) {
+      const uint32_t* src = a.w + row * words + span * 16 + 4 * (l >> 4);
+      w = (v4i){(int)src[0], (int)src[1], (int)src[2], (int)src[3]};
+    }
+    *(v4i*)(rec + 16 * l) = w;
+  }
+  if (l < 8) {
+    const int rg = l >> 1, gs = l & 1;
+    const int64_t g = 2 * span + gs;
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = tile * 16 + 4 * rg + i;
+      v[i] = row < a.N ? a.scales[row * groups + g] : 0;
+      v[4 + i] = row < a.N ? a.biases[row * groups + g] : 0;
+    }
+    v4i o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (int)(v[2 * i] | ((uint32_t)v[2 * i + 1] << 16));
+    *(v4i*)(rec + 1024 + 16 * l) = o;
+  }
+}
+
+// LDS: [M][S][4 slabs][4 kq][8 bf16] permuted x, a zero block, [M][K/64] group sums.
+size_t q4_gemv_lds_bytes(int M, int64_t K) {
+  return (size_t)M * K * 2 + GV_ZERO + (size_t)M * (K / 64) * 4;
+}
+
+__global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int S = (int)(a.K / GV_SPAN), G = (int)(a.K / 64), M = a.M;
+  char* xp = smem;
+  char* zero = smem + (size_t)M * a.K * 2;
+  float* xs = (float*)(zero + GV_ZERO);
+
+  // ---- stage x: records of 8 elements in the MFMA's k order, and group sums ----
+  // Thread order (m, span, gs, slab, kq & 1) puts the 8 records of one group
+  // on 8 consecutive lanes.
+  for (int t = tid; t < GV_ZERO / 4; t += 64 * GV_WAVES) ((uint32_t*)zero)[t] = 0;
+  const int nrec = M * S * 16;
+  for (int t0 = 0; t0 < nrec; t0 += 64 * GV_WAVES) {
+    const int t = t0 + tid;
+    float sum = 0.f;
+    if (t < nrec) {
+      const int k1 = t & 1, slab = (t >> 1) & 3, gs = (t >> 3) & 1, rest = t >> 4;
+      const int span = rest % S, m = rest / S;
+      const int kq = 2 * gs + k1;
+      const int64_t e0 = (int64_t)span * GV_SPAN + 32 * kq + 8 * slab;
+      const v4i in = *(const v4i*)(a.x + (int64_t)m * a.x_stride + e0);
+      const uint32_t d0 = in[0], d1 = in[1], d2 = in[2], d3 = in[3];
+      // element order of the A operand's unpack: 0, 4, 1, 5, 2, 6, 3, 7
+      v4i o;
+      o[0] = (int)__builtin_amdgcn_perm(d2, d0, 0x05040100u);
+      o[1] = (int)__builtin_amdgcn_perm(d2, d0, 0x07060302u);
+      o[2] = (int)__builtin_amdgcn_perm(d3, d1, 0x05040100u);
+      o[3] = (int)__builtin_amdgcn_perm(d3, d1, 0x07060302u);
+      *(v4i*)(xp + ((((size_t)m * S + span) * 4 + slab) * 4 + kq) * 16) = o;
+      sum = ((bf16_lo(d0) + bf16_hi(d0)) + (bf16_lo(d1) + bf16_hi(d1))) +
+            ((bf16_lo(d2) + bf16_hi(d2)) + (bf16_lo(d3) + bf16_hi(d3)));
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    if (t < nrec && (t & 7) == 0) {
+      const int gs = (t >> 3) & 1, rest = t >> 4;
+      xs[(rest / S) * G + 2 * (rest % S) + gs] = sum;
+    }
+  }
+  __syncthreads();
+
+  const int tile = blockIdx.x * GV_WAVES + wave;
+  if (tile * 16 >= a.N) return;  // wave-uniform; no barrier follows
+
+  const int c = lane & 15, q4 = lane >> 4;  // output column / row group, A-operand row / k quarter
+  const int m = c >> 1, gs = c & 1;
+  // B lanes of absent vectors, or of the other group of a span, read zeros
+  const bool bval = m < M && (q4 >> 1) == gs;
+  const char* bbase = bval ? xp + (((size_t)m * S) * 16 + q4) * 16 : zero + 16 * q4;
+  const int bstride = bval ? 256 : 0;
+  const bool xval = m < M;
+  const float* xsum = xs + (xval ? m : 0) * G + gs;
+
+  // Every span slot of the ring loads; slots past the last span load through
+  // an empty resource (zeros, no memory access), so no load sits under a branch.
+  const __amdgpu_buffer_rsrc_t R = make_rsrc(a.packed + (int64_t)tile * S * GV_REC, (int64_t)S * GV_REC);
+  const __amdgpu_buffer_rsrc_t R0 = make_rsrc(a.packed, 0);
+  const uint32_t wl = 16 * lane, sl = 1024 + 16 * (2 * q4 + gs);
+
+  v4f y = {0.f, 0.f, 0.f, 0.f};
+  constexpr int NB = 4;  // spans in flight
+  v4i wbuf[NB], sbuf[NB];
+#pragma unroll
+  for (int i = 0; i < NB - 1; ++i) {
+    const __amdgpu_buffer_rsrc_t r = i < S ? R : R0;
+    wbuf[i] = ld128(r, wl, i * GV_REC);
+    sbuf[i] = ld128(r, sl, i * GV_REC);
+  }
+  const int s_pad = (S + NB - 1) / NB * NB;
+  for (int s0 = 0; s0 < s_pad; s0 += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int span = s0 + j;
+      const __amdgpu_buffer_rsrc_t r = span + NB - 1 < S ? R : R0;
+      wbuf[(j + NB - 1) % NB] = ld128(r, wl, (span + NB - 1) * GV_REC);
+      sbuf[(j + NB - 1) % NB] = ld128(r, sl, (span + NB - 1) * GV_REC);
+      if (span < S) {
+        const v4i w4 = wbuf[j], sb = sbuf[j];
+        const char* bp = bbase + span * bstride;
+        v4f d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int slab = 0; slab < 4; ++slab) {
+          const uint32_t w = (uint32_t)w4[slab];
+          v4i av;
+          av[0] = (int)and_or(w, 0x000f000fu, 0x43004300u);
+          av[1] = (int)and_or(w >> 4, 0x000f000fu, 0x43004300u);
+          av[2] = (int)and_or(w >> 8, 0x000f000fu, 0x43004300u);
+          av[3] = (int)and_or(w >> 12, 0x000f000fu, 0x43004300u);
+          const v4i bv = *(const v4i*)(bp + 64 * slab);
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, av), __builtin_bit_cast(v8bf, bv), d,
+                                                      0, 0, 0);
+        }
+        const float X = xval ? xsum[2 * span] : 0.f;
+        const uint32_t s01 = (uint32_t)sb[0], s23 = (uint32_t)sb[1], b01 = (uint32_t)sb[2], b23 = (uint32_t)sb[3];
+        const float sc[4] = {bf16_lo(s01), bf16_hi(s01), bf16_lo(s23), bf16_hi(s23)};
+        const float bi[4] = {bf16_lo(b01), bf16_hi(b01), bf16_lo(b23), bf16_hi(b23)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = fmaf(fmaf(-128.f, sc[i], bi[i]), X, fmaf(sc[i], d[i], y[i]));
+      }
+    }
+  }
+
+  // the two group halves of a vector sit in lanes c, c ^ 1
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float mine = y[i];  // a copy: a bit_cast of a vector subscript reads element 0
+    const int other = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mine), 0xb1, 0xf, 0xf, false);  // quad_perm 1,0,3,2
+    y[i] = mine + __builtin_bit_cast(float, other);
+  }
+  if (gs == 0 && m < M) {
+    const int64_t r0 = (int64_t)tile * 16 + 4 * q4;
+    if (a.out_dtype == DT_F32) {
+      float* o = (float*)a.out + (int64_t)m * a.out_stride + r0;
+      if (r0 + 3 < a.N) {
+        *(v4f*)o = y;
+      } else {
+        for (int i = 0; i < 4; ++i)
+          if (r0 + i < a.N) o[i] = y[i];
+      }
+    } else {
+      uint16_t* o = (uint16_t*)a.out + (int64_t)m * a.out_stride + r0;
+      const uint16_t h[4] = {f32_to_bf16(y[0]), f32_to_bf16(y[1]), f32_to_bf16(y[2]), f32_to_bf16(y[3])};
+      if (r0 + 3 < a.N) {
+        *(v2i*)o = (v2i){(int)(h[0] | ((uint32_t)h[1] << 16)), (int)(h[2] | ((uint32_t)h[3] << 16))};
+      } else {
+        for (int i = 0; i < 4; ++i)
+          if (r0 + i < a.N) o[i] = h[i];
+      }
+    }
+  }
+}
+
+hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)(a.K / GV_SPAN), (unsigned)((a.N + 15) / 16));
+  hipLaunchKernelGGL(q4_pack_kernel, grid, dim3(64), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream) {
+  const int64_t tiles = (a.N + 15) / 16;
+  const dim3 grid((unsigned)((tiles + GV_WAVES - 1) / GV_WAVES));
+  const size_t lds = q4_gemv_lds_bytes(a.M, a.K);
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute((const void*)q4_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(q4_gemv_kernel, grid, dim3(64 * GV_WAVES), lds, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace rec

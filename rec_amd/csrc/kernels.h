@@ -59,7 +59,28 @@ struct PrefillArgs {
   int causal;
 };
 
+// int4 group-64 GEMV: repack of an MLX affine matrix, then y = x Wᵀ.
+struct Q4PackArgs {
+  const uint32_t* w;        // [N][K/8] MLX words
+  const uint16_t* scales;   // [N][K/64] bf16
+  const uint16_t* biases;   // [N][K/64] bf16
+  int64_t N, K;
+  uint8_t* packed;          // [ceil(N/16)][K/128][1152 B]
+};
+
+struct Q4GemvArgs {
+  const uint8_t* packed;
+  int64_t N, K;
+  const uint16_t* x;        // [M][x_stride] bf16
+  int64_t x_stride;
+  int M;                    // 1..8 vectors
+  void* out;                // [M][out_stride] bf16 or fp32
+  int out_dtype;            // DT_BF16 or DT_F32
+  int64_t out_stride;
+};
+
 constexpr int DECODE_MAX_SPLITS = 256;
+constexpr int Q4_MAX_M = 8;
 
 hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream);
 hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream);
@@ -67,6 +88,9 @@ hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream);
+hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream);
+size_t q4_gemv_lds_bytes(int M, int64_t K);
 hipError_t launch_write_bf16(const AppendArgs& a, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
                              hipStream_t stream);
 

@@ -1,0 +1,108 @@
+"""int4 group-64 GEMV of the decoder's projections (MLX affine 4-bit weights).
+
+The reference decodes with 4-bit affine weights (group 64, bf16 scales and
+biases: engine/src/rec_mlx/quantized.py:27-36) and multiplies them by the
+bf16 activations with ``q4`` / ``dot16`` (engine/src/rec_mlx/kernels/
+megakernel.py:161-232) after packing its weight banks once
+(megakernel.py:1017-1040).  Here a :class:`Q4Matrix` packs an MLX-layout
+matrix once (``rec_q4_pack``) and :func:`q4_gemv` runs ``rec_q4_gemv``.
+:func:`quantized_matmul` keeps the call shape of ``mx.quantized_matmul`` for
+the one configuration the reference uses (``transpose=True``, group 64, 4 bits).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+GROUP = 64
+MAX_VECTORS = 8  # rows of x per launch
+
+
+def _words(w: torch.Tensor) -> torch.Tensor:
+    if w.dtype not in (torch.int32, torch.uint32):
+        raise ValueError(f"packed weights must be 32-bit words (int32/uint32), got {w.dtype}")
+    return w.contiguous()
+
+
+class Q4Matrix:
+    """An ``(N, K)`` MLX affine 4-bit matrix repacked for ``rec_q4_gemv``.
+
+    ``w`` is ``(N, K/8)`` 32-bit words (code ``e`` of a word at bits ``4e``),
+    ``scales`` and ``biases`` ``(N, K/64)`` bfloat16, all on the GPU.
+    """
+
+    def __init__(self, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor):
+        if w.dim() != 2 or scales.dim() != 2 or biases.dim() != 2:
+            raise ValueError("w, scales and biases must be 2-D")
+        N, K = w.shape[0], w.shape[1] * 8
+        if scales.shape != (N, K // GROUP) or biases.shape != scales.shape:
+            raise ValueError(
+                f"scales/biases {tuple(scales.shape)}/{tuple(biases.shape)} do not match w {tuple(w.shape)} "
+                f"at group {GROUP}"
+            )
+        if scales.dtype != torch.bfloat16 or biases.dtype != torch.bfloat16:
+            raise ValueError("scales and biases must be bfloat16")
+        lib = _lib.load()
+        nbytes = lib.rec_q4_packed_bytes(N, K)
+        if nbytes == 0:
+            raise NotImplementedError(f"K={K} is not a positive multiple of 128")
+        self.N, self.K = N, K
+        self.device = w.device
+        w = _words(w)
+        scales, biases = scales.contiguous(), biases.contiguous()
+        self.packed = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+        rc = lib.rec_q4_pack(
+            w.data_ptr(), scales.data_ptr(), biases.data_ptr(), N, K, self.packed.data_ptr(), nbytes,
+            torch.cuda.current_stream(w.device).cuda_stream,
+        )
+        _lib.check(rc, "rec_q4_pack")
+
+    @property
+    def shape(self):
+        return (self.N, self.K)
+
+    @property
+    def nbytes(self) -> int:
+        return self.packed.numel()
+
+
+def q4_gemv(x: torch.Tensor, m: Q4Matrix, out_dtype=None) -> torch.Tensor:
+    """``x @ Wᵀ`` for bf16 ``x`` of shape ``(..., K)``; returns ``(..., N)``
+    in bfloat16 (rounded to nearest even, as the reference stores it) or in
+    ``out_dtype=torch.float32``."""
+    if x.shape[-1] != m.K:
+        raise ValueError(f"x has {x.shape[-1]} features, the matrix {m.K}")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"x must be bfloat16, got {x.dtype}")
+    out_dtype = torch.bfloat16 if out_dtype is None else out_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"out_dtype must be bfloat16 or float32, got {out_dtype}")
+    lead = x.shape[:-1]
+    xs = x.reshape(-1, m.K)
+    if xs.stride(-1) != 1 or xs.data_ptr() % 16 or (xs.shape[0] > 1 and xs.stride(0) % 8):
+        xs = xs.contiguous()
+    rows = xs.shape[0]
+    out = torch.empty((rows, m.N), dtype=out_dtype, device=x.device)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    code = _lib.REC_F32 if out_dtype == torch.float32 else _lib.REC_BF16
+    for r0 in range(0, rows, MAX_VECTORS):
+        M = min(MAX_VECTORS, rows - r0)
+        xr, orow = xs[r0 : r0 + M], out[r0 : r0 + M]
+        rc = lib.rec_q4_gemv(
+            m.packed.data_ptr(), m.N, m.K, xr.data_ptr(), xs.stride(0), M, orow.data_ptr(), code, out.stride(0),
+            stream,
+        )
+        _lib.check(rc, "rec_q4_gemv")
+    return out.reshape(*lead, m.N)
+
+
+def quantized_matmul(x, w, scales, biases, transpose=True, group_size=GROUP, bits=4, mode="affine"):
+    """``mx.quantized_matmul`` for 4-bit affine group-64 weights with
+    ``transpose=True`` (``x @ Wᵀ``), the configuration of the reference's
+    projections.  Packs ``w`` on every call; keep a :class:`Q4Matrix` to pack once."""
+    if not transpose or group_size != GROUP or bits != 4 or mode != "affine":
+        raise NotImplementedError("only transpose=True, group_size=64, bits=4, mode='affine' is implemented")
+    return q4_gemv(x, Q4Matrix(w, scales, biases))

@@ -140,3 +140,27 @@ def test_write_bf16_validation(lib):
     assert _write_bf16(lib, k=8) == _lib.REC_EALIGN
     assert _write_bf16(lib, s=12) == _lib.REC_EALIGN
     assert _write_bf16(lib, dt=9) == _lib.REC_EINVAL
+
+
+def _q4_gemv(lib, **kw):
+    a = dict(p=16, N=64, K=256, x=16, xs=256, M=1, o=16, dt=1, os=64)
+    a.update(kw)
+    return lib.rec_q4_gemv(a["p"], a["N"], a["K"], a["x"], a["xs"], a["M"], a["o"], a["dt"], a["os"], None)
+
+
+def test_q4_validation(lib):
+    assert lib.rec_q4_packed_bytes(16, 256) == 2 * 1152
+    assert lib.rec_q4_packed_bytes(17, 256) == 2 * 2 * 1152
+    assert lib.rec_q4_packed_bytes(16, 192) == 0
+    assert lib.rec_q4_packed_bytes(0, 256) == 0
+    assert lib.rec_q4_pack(16, 16, 16, 16, 256, 16, 2303, None) == _lib.REC_EWORKSPACE
+    assert lib.rec_q4_pack(16, 16, 16, 16, 200, 16, 9999, None) == _lib.REC_EINVAL
+    assert lib.rec_q4_pack(8, 16, 16, 16, 256, 16, 2304, None) == _lib.REC_EALIGN
+    assert _q4_gemv(lib, K=192) == _lib.REC_EINVAL
+    assert _q4_gemv(lib, M=0) == _lib.REC_EINVAL
+    assert _q4_gemv(lib, M=9) == _lib.REC_EINVAL
+    assert _q4_gemv(lib, dt=0) == _lib.REC_EINVAL
+    assert _q4_gemv(lib, x=8) == _lib.REC_EALIGN
+    assert _q4_gemv(lib, M=2, xs=260) == _lib.REC_EALIGN
+    assert _q4_gemv(lib, M=2, xs=128) == _lib.REC_EINVAL
+    assert _q4_gemv(lib, M=8, K=12288, xs=12288) == _lib.REC_EUNSUPPORTED

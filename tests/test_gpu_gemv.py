@@ -1,0 +1,135 @@
+"""Parity of the int4 group-64 GEMV (rec_q4_pack + rec_q4_gemv) with the CPU oracle.
+
+The products inside the kernel are exact and the sums run in fp32, so the fp32
+output must lie within 1e-5 · (|x| · |W|ᵀ) + 1e-6 of the float64 oracle
+(far inside the decode path's 2e-3 abs + 1e-3 rel); the bf16 output must be
+the round-to-nearest-even of the fp32 output, bit for bit.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from rec_amd import Q4Matrix, q4_gemv, quantized_matmul
+
+pytestmark = pytest.mark.gpu
+
+
+def problem(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randint(-(2**31), 2**31, (N, K // 8), dtype=torch.int64, generator=g).to(torch.int32)
+    s = (torch.rand((N, K // 64), generator=g) * 0.049 + 0.001).to(torch.bfloat16)
+    b = (torch.rand((N, K // 64), generator=g) * 0.4 - 0.3).to(torch.bfloat16)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16)
+    return x.cuda(), w.cuda(), s.cuda(), b.cuda()
+
+
+def oracle_rows(x, w, s, b, rows=None):
+    wn = w.cpu().numpy().view(np.uint32)
+    sn, bn = s.float().cpu().numpy(), b.float().cpu().numpy()
+    if rows is not None:
+        wn, sn, bn = wn[rows], sn[rows], bn[rows]
+    xn = x.float().cpu().numpy()
+    ref = O.q4_gemv(xn, wn, sn, bn)
+    mag = np.abs(xn.astype(np.float64)) @ np.abs(O.q4_dequantize(wn, sn, bn)).T
+    return ref, mag
+
+
+def check(got, ref, mag, what):
+    got = got.double().cpu().numpy()
+    err = np.abs(got - ref)
+    bound = 1e-5 * mag + 1e-6
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert np.all(err <= bound), f"{what}: max err {err.max():.3e}, max err/bound {(err / bound).max():.2f}"
+
+
+CASES = [
+    # M, N, K
+    (1, 4096, 2048),   # q_proj
+    (1, 512, 2048),    # k_proj / v_proj
+    (1, 2048, 4096),   # o_proj
+    (1, 2048, 6144),   # dense MLP down
+    (1, 6144, 2048),   # dense MLP gate / up
+    (3, 1000, 512),    # ragged rows, expert down (K = 512)
+    (8, 100, 2048),
+    (5, 16, 128),
+    (1, 1, 128),
+    (2, 33, 384),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"M{c[0]}_N{c[1]}_K{c[2]}")
+def test_q4_gemv_matches_oracle(gpu, case):
+    M, N, K = case
+    x, w, s, b = problem(M, N, K, seed=N + K + M)
+    m = Q4Matrix(w, s, b)
+    y32 = q4_gemv(x, m, out_dtype=torch.float32)
+    y16 = q4_gemv(x, m)
+    torch.cuda.synchronize()
+    ref, mag = oracle_rows(x, w, s, b)
+    check(y32, ref, mag, f"case {case}")
+    assert y16.dtype == torch.bfloat16 and y16.shape == (M, N)
+    assert torch.equal(y16.view(torch.int16), y32.to(torch.bfloat16).view(torch.int16)), "bf16 output is not RNE(fp32)"
+
+
+def test_lm_head_size(gpu):
+    """The lm head (150,144 x 2048): sampled rows against the oracle, every row
+    against a float32 torch reference of the dequantized matrix."""
+    N, K = 150144, 2048
+    x, w, s, b = problem(1, N, K, seed=5)
+    y = q4_gemv(x, Q4Matrix(w, s, b), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(5).choice(N, 384, replace=False))
+    rows = np.concatenate([rows, [0, N - 1]])
+    ref, mag = oracle_rows(x, w, s, b, rows)
+    check(y[:, rows], ref, mag, "lm head sampled rows")
+    # full-size torch reference, dequantized on the GPU in float32
+    shifts = torch.arange(0, 32, 4, device="cuda", dtype=torch.int32)
+    q = ((w.unsqueeze(-1) >> shifts) & 15).reshape(N, K).float()
+    deq = q * s.float().repeat_interleave(64, 1) + b.float().repeat_interleave(64, 1)
+    full = (x.float() @ deq.T).double()
+    mag_full = (x.float().abs() @ deq.abs().T).double()
+    err = (y.double() - full).abs()
+    assert bool((err <= 2e-5 * mag_full + 1e-5).all()), f"max err {err.max().item():.3e}"
+
+
+def test_strided_rows_and_many_vectors(gpu):
+    """x with a row stride larger than K and more than 8 vectors (two launches),
+    leading dims kept; quantized_matmul has mx.quantized_matmul's call shape."""
+    N, K = 300, 1024
+    _, w, s, b = problem(1, N, K, seed=9)
+    big = torch.randn((11, K + 64), device="cuda").to(torch.bfloat16)
+    x = big[:, :K]
+    m = Q4Matrix(w, s, b)
+    y = q4_gemv(x.reshape(11, 1, K), m, out_dtype=torch.float32)
+    assert y.shape == (11, 1, N)
+    ref, mag = oracle_rows(x, w, s, b)
+    check(y.reshape(11, N), ref, mag, "strided")
+    y2 = quantized_matmul(x, w, s, b, transpose=True, group_size=64, bits=4)
+    torch.cuda.synchronize()
+    assert torch.equal(y2.view(torch.int16), y.reshape(11, N).to(torch.bfloat16).view(torch.int16))
+    with pytest.raises(NotImplementedError):
+        quantized_matmul(x, w, s, b, transpose=False)
+    with pytest.raises(ValueError):
+        q4_gemv(x.float(), m)
+
+
+def test_q4_gemv_in_hip_graph(gpu):
+    """Captured launches replayed several times, with eager work between the
+    replays, match the eager result every time."""
+    N, K = 2048, 4096
+    x, w, s, b = problem(2, N, K, seed=13)
+    m = Q4Matrix(w, s, b)
+    eager = q4_gemv(x, m, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    out = torch.empty_like(eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out.copy_(q4_gemv(x, m, out_dtype=torch.float32))
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, rtol=0, atol=0, msg=f"replay {rep}")

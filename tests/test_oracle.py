@@ -297,3 +297,78 @@ def test_mutation_in_oracle_is_caught():
     wrong = O.attention(q, kh, vh, 0.088, None)  # sink dropped
     ref = _torch_reference(q, kh, vh, 0.088, sinks)
     assert not np.allclose(wrong, ref, rtol=1e-6, atol=1e-9)
+
+
+# ---------------------------------------------------------------------------
+# int4 group-64 GEMV
+
+
+def _bf16_values(a):
+    """float32 array rounded to bf16 values (kept as float32)."""
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def _q4_problem(rng, M, N, K):
+    w = rng.integers(0, 2**32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = _bf16_values(rng.uniform(0.001, 0.05, size=(N, K // 64)))
+    b = _bf16_values(rng.uniform(-0.3, 0.1, size=(N, K // 64)))
+    x = _bf16_values(rng.standard_normal((M, K)))
+    return x, w, s, b
+
+
+def _dot16_form(x, w, s, b):
+    """q4 / load16 / dot16 of engine/src/rec_mlx/kernels/megakernel.py:170-214
+    taken literally: x divided by 1, 16, 256, 4096 by its place in each group
+    of four, codes read with the masks 15, 240, 3840, 61440 from little-endian
+    ushorts, s·a + sum·b per 16-element run (float64 here)."""
+    M, K = x.shape
+    N = w.shape[0]
+    u16 = np.ascontiguousarray(w.astype("<u4")).view("<u2").reshape(N, K // 4).astype(np.int64)
+    masks = np.array([15, 240, 3840, 61440], np.int64)
+    div = np.tile(np.array([1.0, 16.0, 256.0, 4096.0]), 4)
+    y = np.zeros((M, N))
+    for run in range(K // 16):
+        xs = x[:, 16 * run : 16 * run + 16].astype(np.float64)
+        v = xs / div
+        total = xs.sum(axis=1)
+        a = np.zeros((M, N))
+        for j in range(4):
+            p = u16[:, 4 * run + j]
+            for t in range(4):
+                a += v[:, 4 * j + t][:, None] * (p & masks[t]).astype(np.float64)[None]
+        gi = 16 * run // 64
+        y += s[:, gi][None] * a + total[:, None] * b[:, gi][None]
+    return y
+
+
+def test_q4_unpack_order():
+    w = np.array([[0x76543210, 0xFEDCBA98]], np.uint32)
+    np.testing.assert_array_equal(O.q4_unpack(w)[0], np.arange(16))
+
+
+def test_q4_gemv_matches_the_reference_dot16_form():
+    rng = np.random.default_rng(21)
+    x, w, s, b = _q4_problem(rng, 3, 40, 256)
+    np.testing.assert_allclose(O.q4_gemv(x, w, s, b), _dot16_form(x, w, s, b), rtol=1e-12, atol=1e-12)
+
+
+def test_q4_gemv_closed_forms():
+    """One-hot x picks a column s·q + b; x = 1 gives Σ_g (s Σq + 64 b)."""
+    rng = np.random.default_rng(22)
+    _, w, s, b = _q4_problem(rng, 1, 24, 128)
+    q = O.q4_unpack(w).astype(np.float64)
+    for k in (0, 1, 63, 64, 127):
+        x = np.zeros((1, 128))
+        x[0, k] = 1.0
+        np.testing.assert_array_equal(O.q4_gemv(x, w, s, b)[0], s[:, k // 64] * q[:, k] + b[:, k // 64])
+    ones = O.q4_gemv(np.ones((1, 128)), w, s, b)[0]
+    want = (s * q.reshape(24, 2, 64).sum(-1) + 64 * b).sum(-1)
+    np.testing.assert_allclose(ones, want, rtol=1e-13)
+
+
+def test_q4_planted_nibble_swap_is_caught():
+    """A planted mistake (high/low nibble swapped) fails the dot16 pin."""
+    rng = np.random.default_rng(23)
+    x, w, s, b = _q4_problem(rng, 1, 16, 128)
+    swapped = ((w & np.uint32(0x0F0F0F0F)) << np.uint32(4)) | ((w >> np.uint32(4)) & np.uint32(0x0F0F0F0F))
+    assert not np.allclose(O.q4_gemv(x, swapped, s, b), _dot16_form(x, w, s, b), rtol=1e-6)
