@@ -75,11 +75,18 @@ __global__ __launch_bounds__(64) void q4_pack_kernel(const Q4PackArgs a) {
   }
 }
 
-// LDS: [M][S][4 slabs][4 kq][8 bf16] permuted x, a zero block, [M][K/64] group sums.
-size_t q4_gemv_lds_bytes(int M, int64_t K) {
-  return (size_t)M * K * 2 + GV_ZERO + (size_t)M * (K / 64) * 4;
+// LDS: [M][S][4 slabs][4 kq][8 bf16] permuted x, a zero block, [M][K/64]
+// group sums, and the waves' partial results ([4 waves][64 lanes][4 floats]).
+__host__ __device__ size_t q4_gemv_red_offset(int M, int64_t K) {
+  return ((size_t)M * K * 2 + GV_ZERO + (size_t)M * (K / 64) * 4 + 15) & ~(size_t)15;
 }
 
+size_t q4_gemv_lds_bytes(int M, int64_t K) { return q4_gemv_red_offset(M, K) + GV_WAVES * 64 * 16; }
+
+// WPT waves share one 16-row tile, wave p taking spans p, p + WPT, ...: small
+// matrices (the attention projections, the experts) then still spread over
+// every SIMD.  A workgroup covers GV_WAVES / WPT tiles.
+template <int WPT>
 __global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -88,6 +95,37 @@ __global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs
   char* xp = smem;
   char* zero = smem + (size_t)M * a.K * 2;
   float* xs = (float*)(zero + GV_ZERO);
+  v4f* red = (v4f*)(smem + q4_gemv_red_offset(M, a.K));
+
+  const int tile = blockIdx.x * (GV_WAVES / WPT) + wave / WPT, part = wave % WPT;
+  const bool live = tile * 16 < a.N;  // wave-uniform
+  const int n_w = live && part < S ? (S - part + WPT - 1) / WPT : 0;  // spans of this wave
+
+  const int c = lane & 15, q4 = lane >> 4;  // output column / row group, A-operand row / k quarter
+  const int m = c >> 1, gs = c & 1;
+  // B lanes of absent vectors, or of the other group of a span, read zeros
+  const bool bval = m < M && (q4 >> 1) == gs;
+  const char* bbase = bval ? xp + (((size_t)m * S) * 16 + q4) * 16 : zero + 16 * q4;
+  const int bstride = bval ? 256 : 0;
+  const bool xval = m < M;
+  const float* xsum = xs + (xval ? m : 0) * G + gs;
+
+  // Every span slot of the ring loads; slots past the last span load through
+  // an empty resource (zeros, no memory access), so no load sits under a branch.
+  const __amdgpu_buffer_rsrc_t R =
+      make_rsrc(a.packed + (live ? (int64_t)tile * S * GV_REC : 0), live ? (int64_t)S * GV_REC : 0);
+  const __amdgpu_buffer_rsrc_t R0 = make_rsrc(a.packed, 0);
+  const uint32_t wl = 16 * lane, sl = 1024 + 16 * (2 * q4 + gs);
+
+  constexpr int NB = 4;  // spans in flight
+  v4i wbuf[NB], sbuf[NB];
+#pragma unroll
+  for (int i = 0; i < NB - 1; ++i) {
+    const __amdgpu_buffer_rsrc_t r = i < n_w ? R : R0;
+    wbuf[i] = ld128(r, wl, (part + WPT * i) * GV_REC);
+    sbuf[i] = ld128(r, sl, (part + WPT * i) * GV_REC);
+  }
+  // (the first spans' loads above are in flight while x is staged)
 
   // ---- stage x: records of 8 elements in the MFMA's k order, and group sums ----
   // Thread order (m, span, gs, slab, kq & 1) puts the 8 records of one group
@@ -124,42 +162,16 @@ __global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs
   }
   __syncthreads();
 
-  const int tile = blockIdx.x * GV_WAVES + wave;
-  if (tile * 16 >= a.N) return;  // wave-uniform; no barrier follows
-
-  const int c = lane & 15, q4 = lane >> 4;  // output column / row group, A-operand row / k quarter
-  const int m = c >> 1, gs = c & 1;
-  // B lanes of absent vectors, or of the other group of a span, read zeros
-  const bool bval = m < M && (q4 >> 1) == gs;
-  const char* bbase = bval ? xp + (((size_t)m * S) * 16 + q4) * 16 : zero + 16 * q4;
-  const int bstride = bval ? 256 : 0;
-  const bool xval = m < M;
-  const float* xsum = xs + (xval ? m : 0) * G + gs;
-
-  // Every span slot of the ring loads; slots past the last span load through
-  // an empty resource (zeros, no memory access), so no load sits under a branch.
-  const __amdgpu_buffer_rsrc_t R = make_rsrc(a.packed + (int64_t)tile * S * GV_REC, (int64_t)S * GV_REC);
-  const __amdgpu_buffer_rsrc_t R0 = make_rsrc(a.packed, 0);
-  const uint32_t wl = 16 * lane, sl = 1024 + 16 * (2 * q4 + gs);
-
   v4f y = {0.f, 0.f, 0.f, 0.f};
-  constexpr int NB = 4;  // spans in flight
-  v4i wbuf[NB], sbuf[NB];
-#pragma unroll
-  for (int i = 0; i < NB - 1; ++i) {
-    const __amdgpu_buffer_rsrc_t r = i < S ? R : R0;
-    wbuf[i] = ld128(r, wl, i * GV_REC);
-    sbuf[i] = ld128(r, sl, i * GV_REC);
-  }
-  const int s_pad = (S + NB - 1) / NB * NB;
-  for (int s0 = 0; s0 < s_pad; s0 += NB) {
+  const int n_pad = (n_w + NB - 1) / NB * NB;
+  for (int i0 = 0; i0 < n_pad; i0 += NB) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int span = s0 + j;
-      const __amdgpu_buffer_rsrc_t r = span + NB - 1 < S ? R : R0;
-      wbuf[(j + NB - 1) % NB] = ld128(r, wl, (span + NB - 1) * GV_REC);
-      sbuf[(j + NB - 1) % NB] = ld128(r, sl, (span + NB - 1) * GV_REC);
-      if (span < S) {
+      const int i = i0 + j, span = part + WPT * i;
+      const __amdgpu_buffer_rsrc_t r = i + NB - 1 < n_w ? R : R0;
+      wbuf[(j + NB - 1) % NB] = ld128(r, wl, (span + WPT * (NB - 1)) * GV_REC);
+      sbuf[(j + NB - 1) % NB] = ld128(r, sl, (span + WPT * (NB - 1)) * GV_REC);
+      if (i < n_w) {
         const v4i w4 = wbuf[j], sb = sbuf[j];
         const char* bp = bbase + span * bstride;
         v4f d = {0.f, 0.f, 0.f, 0.f};
@@ -180,10 +192,19 @@ __global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs
         const float sc[4] = {bf16_lo(s01), bf16_hi(s01), bf16_lo(s23), bf16_hi(s23)};
         const float bi[4] = {bf16_lo(b01), bf16_hi(b01), bf16_lo(b23), bf16_hi(b23)};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) y[i] = fmaf(fmaf(-128.f, sc[i], bi[i]), X, fmaf(sc[i], d[i], y[i]));
+        for (int r = 0; r < 4; ++r) y[r] = fmaf(fmaf(-128.f, sc[r], bi[r]), X, fmaf(sc[r], d[r], y[r]));
       }
     }
   }
+
+  if constexpr (WPT > 1) {  // sum the partial results of the tile's waves
+    red[wave * 64 + lane] = y;
+    __syncthreads();
+    if (part != 0) return;  // no barrier follows
+#pragma unroll
+    for (int p = 1; p < WPT; ++p) y += red[(wave + p) * 64 + lane];
+  }
+  if (!live) return;
 
   // the two group halves of a vector sit in lanes c, c ^ 1
 #pragma unroll
@@ -221,17 +242,26 @@ hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream) {
-  const int64_t tiles = (a.N + 15) / 16;
-  const dim3 grid((unsigned)((tiles + GV_WAVES - 1) / GV_WAVES));
-  const size_t lds = q4_gemv_lds_bytes(a.M, a.K);
+template <int WPT>
+hipError_t launch_q4_gemv_wpt(const Q4GemvArgs& a, int64_t tiles, size_t lds, hipStream_t stream) {
+  constexpr int TPG = GV_WAVES / WPT;  // tiles per workgroup
   if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute((const void*)q4_gemv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)lds);
+    const hipError_t e = hipFuncSetAttribute((const void*)q4_gemv_kernel<WPT>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(q4_gemv_kernel, grid, dim3(64 * GV_WAVES), lds, stream, a);
+  hipLaunchKernelGGL(q4_gemv_kernel<WPT>, dim3((unsigned)((tiles + TPG - 1) / TPG)), dim3(64 * GV_WAVES), lds, stream,
+                     a);
   return hipGetLastError();
+}
+
+hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream) {
+  const int64_t tiles = (a.N + 15) / 16;
+  const size_t lds = q4_gemv_lds_bytes(a.M, a.K);
+  // fewest waves per tile that still give every SIMD (1024) two waves
+  if (tiles >= 2048) return launch_q4_gemv_wpt<1>(a, tiles, lds, stream);
+  if (tiles >= 1024) return launch_q4_gemv_wpt<2>(a, tiles, lds, stream);
+  return launch_q4_gemv_wpt<4>(a, tiles, lds, stream);
 }
 
 }  // namespace rec

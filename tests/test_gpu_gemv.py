@@ -56,6 +56,8 @@ CASES = [
     (5, 16, 128),
     (1, 1, 128),
     (2, 33, 384),
+    (1, 24000, 256),   # 1500 row tiles: two waves per tile
+    (2, 40000, 128),   # 2500 row tiles: one wave per tile
 ]
 
 
