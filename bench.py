@@ -248,6 +248,66 @@ def run_decode_bf16(T, R, steps, warmup, seed):
     return res
 
 
+# (rows N, features K, name) of the int4 projections of one decode token
+Q4_SHAPES = [
+    (150144, 2048, "lm_head"),
+    (6144, 2048, "dense_gate_up"),
+    (2048, 6144, "dense_down"),
+    (4096, 2048, "q_proj"),
+    (2048, 4096, "o_proj"),
+    (512, 2048, "k_proj"),
+]
+
+
+def run_q4_gemv(steps, seed):
+    """int4 group-64 GEMV (one bf16 vector) at the decoder's projection
+    shapes; each launch reads a different copy of the packed matrix (about
+    600 MB of copies in rotation) so no launch finds its weights in cache."""
+    import torch
+
+    import rec_amd
+    from rec_amd import _lib
+
+    lib = rec_amd.library()
+    res = {}
+    for N, K, name in Q4_SHAPES:
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + N + K)
+        w = torch.randint(-(2**31), 2**31 - 1, (N, K // 8), dtype=torch.int32, device="cuda", generator=g)
+        s = (torch.rand((N, K // 64), device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+        b = (torch.rand((N, K // 64), device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+        base = rec_amd.Q4Matrix(w, s, b)
+        del w, s, b
+        nb = base.nbytes
+        copies = max(2, -(-600_000_000 // nb))
+        packs = [base.packed] + [base.packed.clone() for _ in range(copies - 1)]
+        x = torch.randn((1, K), device="cuda", generator=g).to(torch.bfloat16)
+        out = torch.empty((1, N), device="cuda", dtype=torch.bfloat16)
+
+        def step(i):
+            rc = lib.rec_q4_gemv(packs[i % copies].data_ptr(), N, K, x.data_ptr(), K, 1, out.data_ptr(),
+                                 _lib.REC_BF16, N, torch.cuda.current_stream().cuda_stream)
+            _lib.check(rc, "q4 gemv")
+
+        n = steps if nb > 50e6 else 4 * steps
+        for i in range(4):
+            step(i)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(n):
+                step(i)
+        ms = _replay_timed(torch, gr, n)
+        byts = nb + 2 * K + 2 * N
+        gbs = byts / (ms * 1e-3) / 1e9
+        log(f"q4 gemv {name} {N}x{K}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+        res[name] = dict(N=N, K=K, us=round(ms * 1e3, 3), gbs=round(gbs, 2), frac_of_peak=round(gbs / HBM_PEAK_GBS, 4),
+                         bytes_per_launch=byts, copies=copies)
+        del gr, packs, base
+        torch.cuda.empty_cache()
+    return res
+
+
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
@@ -397,6 +457,7 @@ def main(argv=None):
     ap.add_argument("--no-prefill", action="store_true", help="skip the chunked-prefill measurement")
     ap.add_argument("--no-int4", action="store_true", help="skip the 131K uint4 measurement")
     ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-cache measurements")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the int4 GEMV measurements")
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -453,6 +514,10 @@ def main(argv=None):
         ls = args.long_steps or max(16, args.steps // 8)
         rbf["context_32k_bf16"] = run_decode_bf16(32768, 8, max(16, args.steps // 4), 8, args.seed + 61)
         rbf["context_252k_bf16"] = run_decode_bf16(258048, 2, ls, 4, args.seed + 63)
+
+    rq4 = None
+    if not args.no_gemv:
+        rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
 
     rpf = None
     if not args.no_prefill:
@@ -537,6 +602,12 @@ def main(argv=None):
             "cache_instances": r4["instances"],
         }
     result.update(rbf)
+    if rq4 is not None:
+        result["q4_gemv"] = dict(
+            format="MLX affine 4-bit, group 64, bf16 scales and biases; one bf16 vector, bf16 out",
+            shapes=rq4,
+            kernel="rec::q4_gemv_kernel (bf16 MFMA 16x16x32)",
+        )
     if rpf is not None:
         result["prefill_65536_plus_2048"] = rpf
     print(json.dumps(result), flush=True)
