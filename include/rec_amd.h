@@ -13,7 +13,8 @@
  *   int8 K codes  int8  [B][Hkv][C/32][2][32][64]   half m = dims 64m..64m+63, row = token t
  *   int4 K codes  uint8 [B][Hkv][C/32][32][4][2][8]  row = token t, [byte run r][half m][8 bytes]:
  *                                                   byte 8r+i of half m holds dims 64m+16r+2i, +1 (low nibble even)
- *   int8 V codes  int8  [B][Hkv][C/32][128][32]     dim-major, column = position p
+ *   int8 V codes  int8  [B][Hkv][C/32][4][16][4][2][8]  dim 16n+c, position p = 8g+e at
+ *                                                   [n/2][c][g][n%2][e]
  *   int4 V codes  uint8 [B][Hkv][C/32][2][16][4][4][4]  dim 16n+c, position p = 8g+e at
  *                                                   [n/4][c][g][n%4][e/2], low nibble = even e
  *   int8 scales   fp16  [B][Hkv][C/32][32]          one per (token, head), position p
@@ -22,6 +23,17 @@
  * Quantizers: int8 symmetric s = fp16(amax/127), q = clamp(rint(x/s), ±127);
  * uint4 asymmetric over [min(0, x), max(0, x)], s = fp16(range/15),
  * z = clamp(rint(-min/s), 0, 15), q = clamp(rint(x/s) + z, 0, 15).
+ *
+ * MLX-style affine format (k_bits = REC_AFFINE8 with v_bits = REC_AFFINE4; the
+ * reference's MixedQuantizedKVCache, engine/src/rec_mlx/model.py:40-82, group
+ * 64): x = s*q + b with bf16 scale s and bias b per (token, 64-dim group).
+ * Key codes are uint8 in the int8 K layout, value codes uint4 in the int4 V
+ * layout; each "scales" buffer holds bf16 [B][Hkv][C/32][2 (scale, bias)][2
+ * groups][32] at the int4 slot order; the zeros pointers are unused (NULL).
+ * Quantizer: MLX's affine_quantize (w_max = max(0, max w), w_min = min w,
+ * step (w_max - w_min)/n_bins, the larger-magnitude extreme made exact, codes
+ * round-half-away((w - b)/s) clamped to [0, n_bins]), scale and bias rounded to
+ * bf16.
  */
 #ifndef REC_AMD_H
 #define REC_AMD_H
@@ -45,6 +57,9 @@ enum {
 
 /* Element types of the float inputs (queries, new keys/values). */
 enum { REC_F16 = 0, REC_BF16 = 1, REC_F32 = 2 };
+
+/* k_bits / v_bits: 8 (int8 symmetric), 4 (uint4 group 32), or the affine pair */
+enum { REC_AFFINE8 = 0x108, REC_AFFINE4 = 0x104 };
 
 /* Library version, e.g. "rec_amd 0.1.0 gfx950". */
 const char* rec_version(void);

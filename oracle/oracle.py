@@ -49,6 +49,20 @@ uint4, asymmetric, fp16 scale and integer-valued fp16 zero-point per group of
     q = z = 0 where s16 == 0
     x̂   = (q - z) * float(s16)
 
+MLX-style affine, group 64 (the reference's own KV format: ``mx.quantize``
+with ``group_size=64``, 8-bit keys and 4-bit values, ``model.py:40-82``),
+restated from MLX's published ``affine_quantize`` (mlx 0.32.0; MLX cannot run
+here, so byte parity with MLX is not pinned) per group ``w[64]``::
+
+    w_max = max(0, max w)      w_min = min w          (float32)
+    scale = max((w_max - w_min) / n_bins, 1e-7)       n_bins = 2^bits - 1
+    side  = |w_min| > |w_max|; scale = side ? scale : -scale
+    edge  = side ? w_min : w_max
+    q0    = round(edge / scale)                        (half away from zero)
+    scale = q0 == 0 ? scale : edge / q0;  bias = q0 == 0 ? 0 : edge
+    q     = min(round((w - bias) / scale), n_bins)     (codes 0 .. n_bins)
+    scale, bias stored as bf16 (round to nearest even); x̂ = q · s_bf16 + b_bf16
+
 Pinning (see ``tests/test_oracle.py``): the quantizers are checked against a
 brute-force nearest-code search on small rows, closed forms (all-zero rows,
 constant rows, the max element mapping to ±127) and invariants (symmetry,
@@ -76,6 +90,10 @@ __all__ = [
     "split_k_decode",
     "split_k_decode_quantized",
     "causal_mask",
+    "bf16_rn",
+    "round_half_away",
+    "quantize_affine",
+    "dequantize_affine",
     "q4_unpack",
     "q4_dequantize",
     "q4_gemv",
@@ -159,6 +177,56 @@ def dequantize_int4(packed, scale, zero, group=32):
     s = np.asarray(scale, np.float16).astype(np.float32)[..., None]
     z = np.asarray(zero, np.float16).astype(np.float32)[..., None]
     return ((g - z) * s).reshape(q.shape)
+
+
+def bf16_rn(x):
+    """float32 -> nearest bf16 value (ties to even), returned as float32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)) << np.uint64(16)
+    return r.astype(np.uint32).view(np.float32)
+
+
+def round_half_away(x):
+    """Round to the nearest integer, halves away from zero (exact in float32)."""
+    x = np.asarray(x, dtype=np.float32)
+    t = np.trunc(x)
+    frac = x - t  # exact
+    return (t + np.where(np.abs(frac) >= np.float32(0.5), np.sign(x), np.float32(0))).astype(np.float32)
+
+
+def quantize_affine(x, bits, group=64):
+    """MLX-style affine quantization of the last axis (module docstring).
+
+    Returns ``(codes uint8 [..., D] (unpacked), scale [..., D/group],
+    bias [..., D/group])``; scale and bias are bf16 values held in float32.
+    """
+    xf = np.asarray(x, dtype=np.float32)
+    D = xf.shape[-1]
+    g = xf.reshape(xf.shape[:-1] + (D // group, group))
+    n_bins = np.float32((1 << bits) - 1)
+    w_max = np.maximum(g.max(axis=-1), np.float32(0))
+    w_min = g.min(axis=-1)
+    scale = np.maximum((w_max - w_min) / n_bins, np.float32(1e-7))
+    side = np.abs(w_min) > np.abs(w_max)
+    scale = np.where(side, scale, -scale)
+    edge = np.where(side, w_min, w_max)
+    q0 = round_half_away(edge / scale)
+    at_zero = q0 == 0
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scale = np.where(at_zero, scale, edge / np.where(at_zero, np.float32(1), q0)).astype(np.float32)
+    bias = np.where(at_zero, np.float32(0), edge).astype(np.float32)
+    q = round_half_away((g - bias[..., None]) / scale[..., None])
+    q = np.minimum(np.maximum(q, 0), n_bins)
+    return q.reshape(xf.shape).astype(np.uint8), bf16_rn(scale), bf16_rn(bias)
+
+
+def dequantize_affine(codes, scale, bias, group=64):
+    """x̂ = q · s + b per group, float32 (one rounding: the fma-free product then sum)."""
+    q = np.asarray(codes, np.float32)
+    D = q.shape[-1]
+    s = np.repeat(np.asarray(scale, np.float32), group, axis=-1)
+    b = np.repeat(np.asarray(bias, np.float32), group, axis=-1)
+    return (q * s + b).reshape(q.shape[:-1] + (D,))
 
 
 def causal_mask(L, T):

@@ -102,8 +102,8 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
     if k_new is None:
         rc = lib.rec_decode_attn(
             q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1),
-            keys.bits, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
-            values.bits, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
+            keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
+            values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
             *common_tail,
         )
         _lib.check(rc, "rec_decode_attn")
@@ -112,8 +112,8 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
             q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1),
             k_new.data_ptr(), v_new.data_ptr(), _DTYPES[k_new.dtype],
             k_new.stride(0), k_new.stride(1), v_new.stride(0), v_new.stride(1),
-            keys.bits, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
-            values.bits, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
+            keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
+            values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
             *common_tail,
         )
         _lib.check(rc, "rec_decode_append_attn")
@@ -127,8 +127,8 @@ def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sink
     sk = _sinks(sinks, Hq, dev)
     rc = lib.rec_prefill_attn(
         q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), q.stride(2),
-        keys.bits, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
-        values.bits, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
+        keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
+        values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
         _ptr(sk), float(scale), int(causal), B, Hq, keys.n_kv_heads, D, L, int(keys.length), int(keys.capacity),
         out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream,
     )
@@ -154,7 +154,9 @@ def quantized_attention_with_sinks(
         raise TypeError("keys/values must come from QuantizedKVCache.update_and_fetch")
     if (keys.bits, values.bits) != (key_bits, value_bits):
         raise ValueError(f"cache holds {keys.bits}/{values.bits}-bit K/V, call asked for {key_bits}/{value_bits}")
-    if 4 in (key_bits, value_bits) and group_size != 32:
+    if keys.affine != values.affine or keys.affine != (group_size == 64):
+        raise ValueError(f"group_size={group_size} does not match the cache's format")
+    if not keys.affine and 4 in (key_bits, value_bits) and group_size != 32:
         raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
     if mask is not None and not (isinstance(mask, str) and mask == "causal"):
         raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")

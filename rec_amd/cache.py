@@ -7,10 +7,14 @@ mlx-lm ``QuantizedKVCache`` methods it inherits (mlx-lm 0.31.3, third-party:
 torch tensors in HBM instead of MLX arrays and the quantize-on-append done by
 the gfx950 kernel behind ``rec_kv_append``.
 
-Formats (bits per K and V independently):
+Formats (bits per K and V independently, ``group_size=32``):
 
 * 8-bit: symmetric int8, one fp16 scale per (token, head).
 * 4-bit: asymmetric uint4, fp16 scale and zero-point per 32 dims.
+
+With ``group_size=64`` (the reference's default) the cache holds MLX-style
+affine codes, 8-bit keys and 4-bit values with a bf16 scale and bias per 64
+dims (``mx.quantize``'s algorithm, restated by the kernel).
 
 Codes and scales are stored in 32-token blocks laid out for the matrix-core
 operands of the decode kernel (table in ``rec_amd/csrc/common.h``), so the
@@ -29,6 +33,7 @@ from . import _lib
 BLOCK = 32
 HEAD_DIM = 128
 GROUP4 = 32
+GROUP_AFFINE = 64
 
 _DTYPES = {torch.float16: _lib.REC_F16, torch.bfloat16: _lib.REC_BF16, torch.float32: _lib.REC_F32}
 
@@ -47,6 +52,14 @@ class QuantizedKV(NamedTuple):
     bits: int
     length: int
     blocked: bool
+    affine: bool = False  # MLX-style affine group 64: ``scales`` holds [scale, bias], ``zeros`` is None
+
+    @property
+    def code(self) -> int:
+        """Format code of the C ABI (8, 4, REC_AFFINE8 or REC_AFFINE4)."""
+        if self.affine:
+            return _lib.REC_AFFINE8 if self.bits == 8 else _lib.REC_AFFINE4
+        return self.bits
 
     @property
     def n_kv_heads(self) -> int:
@@ -57,9 +70,13 @@ class QuantizedKV(NamedTuple):
         return self.codes.shape[2] * BLOCK
 
 
-def _alloc(B, H, cap, bits, is_v, device):
+def _alloc(B, H, cap, bits, is_v, device, affine=False):
     """Zeroed codes/scales/zeros of one cache tensor (layout table in rec_amd/csrc/common.h)."""
     nb = cap // BLOCK
+    if affine:  # [scale, bias] x 2 groups x 32 slots of bf16 per block
+        codes = torch.zeros((B, H, nb, BLOCK * HEAD_DIM * bits // 8), dtype=torch.uint8, device=device)
+        scales = torch.zeros((B, H, nb, 2, HEAD_DIM // GROUP_AFFINE, BLOCK), dtype=torch.bfloat16, device=device)
+        return codes, scales, None
     if bits == 8:
         codes = torch.zeros((B, H, nb, BLOCK * HEAD_DIM), dtype=torch.int8, device=device)
         scales = torch.zeros((B, H, nb, BLOCK), dtype=torch.float16, device=device)
@@ -96,12 +113,24 @@ def s4_slot(p):
 _SLOT4 = [s4_slot(p) for p in _POS]
 
 
+def _unpack_v4(kv, B, H, nb, pos):
+    """4-bit V codes (blocked) -> (B, H, nb*32, 64) bytes, low nibble = even dim."""
+    packed = kv.codes.view(B, H, nb, 2, 16, 4, 4, 4)  # (h, c, pg, n4, byte)
+    packed = packed.permute(0, 1, 2, 3, 6, 4, 5, 7).reshape(B, H, nb, HEAD_DIM, BLOCK // 2)  # (n, c) -> dim
+    q = torch.stack([packed & 0xF, packed >> 4], -1).reshape(B, H, nb, HEAD_DIM, BLOCK)[..., pos]
+    q = q.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
+    return (q[..., 0::2] | (q[..., 1::2] << 4)).to(torch.uint8)
+
+
 def to_logical(kv: QuantizedKV, length: Optional[int] = None):
     """Return ``(codes, scales, zeros)`` in the plain layout, first ``length`` tokens.
 
     8-bit: codes int8 ``(B, H, T, 128)``, scales fp16 ``(B, H, T)``.
     4-bit: codes uint8 ``(B, H, T, 64)`` (low nibble = even dim), scales and
     zeros fp16 ``(B, H, T, 4)``.
+    Affine: codes uint8 ``(B, H, T, 128)`` (8-bit) or ``(B, H, T, 64)``
+    (4-bit, low nibble = even dim); scales and biases bf16 ``(B, H, T, 2)``
+    in place of scales and zeros.
     """
     T = kv.length if length is None else length
     B, H, nb = kv.codes.shape[:3]
@@ -116,16 +145,15 @@ def to_logical(kv: QuantizedKV, length: Optional[int] = None):
         blocked = blocked.permute(0, 1, 2, 3, 6, 4, 5, 7).reshape(B, H, nb, HEAD_DIM, BLOCK)  # (n, c) -> dim
         codes = blocked[..., pos].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
     else:  # V: [nb][n / 4][c][position group][n % 4][4 bytes], dim 16 n + c, position p in byte p // 2
-        packed = kv.codes.view(B, H, nb, 2, 16, 4, 4, 4)  # (h, c, pg, n4, byte)
-        packed = packed.permute(0, 1, 2, 3, 6, 4, 5, 7).reshape(B, H, nb, HEAD_DIM, BLOCK // 2)  # (n, c) -> dim
-        q = torch.stack([packed & 0xF, packed >> 4], -1).reshape(B, H, nb, HEAD_DIM, BLOCK)[..., pos]
-        q = q.permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM)
-        codes = (q[..., 0::2] | (q[..., 1::2] << 4)).to(torch.uint8)
-    if kv.bits == 8:
+        codes = _unpack_v4(kv, B, H, nb, pos)
+    slot = torch.tensor(_SLOT4, device=kv.codes.device)
+    if kv.affine:  # scales: [nb][scale, bias][2 groups][32 slots]
+        sb = kv.scales[..., slot].permute(0, 1, 3, 2, 5, 4).reshape(B, H, 2, -1, HEAD_DIM // GROUP_AFFINE)
+        sc, zp = sb[:, :, 0], sb[:, :, 1]
+    elif kv.bits == 8:
         sc = kv.scales[..., pos].reshape(B, H, -1)
         zp = None
     else:
-        slot = torch.tensor(_SLOT4, device=kv.codes.device)
         sc = kv.scales[..., slot].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
         zp = kv.zeros[..., slot].permute(0, 1, 2, 4, 3).reshape(B, H, -1, HEAD_DIM // GROUP4)
     return (
@@ -158,9 +186,13 @@ class QuantizedKVCache:
         for name, bits in (("key_bits", key_bits), ("value_bits", value_bits)):
             if bits not in (4, 8):
                 raise ValueError(f"{name} must be 4 or 8, got {bits}")
-        if 4 in (key_bits, value_bits) and group_size != GROUP4:
-            raise ValueError(f"4-bit caches use groups of {GROUP4}, got group_size={group_size}")
+        if group_size == GROUP_AFFINE:
+            if (key_bits, value_bits) != (8, 4):
+                raise NotImplementedError("the group-64 affine format is built for 8-bit keys with 4-bit values")
+        elif 4 in (key_bits, value_bits) and group_size != GROUP4:
+            raise ValueError(f"4-bit caches use groups of {GROUP4} (or 64 for the affine format), got {group_size}")
         self.group_size = group_size
+        self.affine = group_size == GROUP_AFFINE
         self.key_bits, self.value_bits = key_bits, value_bits
         self.bits = key_bits
         self.max_tokens = max_tokens
@@ -184,16 +216,16 @@ class QuantizedKVCache:
             cap = -(-self.max_tokens // BLOCK) * BLOCK
         else:
             cap = -(-needed // self.step) * self.step
-        k = _alloc(B, H, cap, self.key_bits, False, device)
-        v = _alloc(B, H, cap, self.value_bits, True, device)
+        k = _alloc(B, H, cap, self.key_bits, False, device, self.affine)
+        v = _alloc(B, H, cap, self.value_bits, True, device, self.affine)
         if self.keys is not None:
             k = tuple(_grow_tensor(o, n) if n is not None else None for o, n in zip(self.keys, k))
             v = tuple(_grow_tensor(o, n) if n is not None else None for o, n in zip(self.values, v))
         self.keys, self.values, self.capacity = k, v, cap
 
     def _view(self):
-        k = QuantizedKV(*self.keys, self.key_bits, self.offset, False)
-        v = QuantizedKV(*self.values, self.value_bits, self.offset, True)
+        k = QuantizedKV(*self.keys, self.key_bits, self.offset, False, self.affine)
+        v = QuantizedKV(*self.values, self.value_bits, self.offset, True, self.affine)
         return k, v
 
     # ------------------------------------------------------ reference API --
@@ -221,10 +253,11 @@ class QuantizedKVCache:
         stream = torch.cuda.current_stream(keys.device).cuda_stream
         kc, ks, kz = self.keys
         vc, vs, vz = self.values
+        kv_k, kv_v = self._view()
         rc = lib.rec_kv_append(
             k.data_ptr(), v.data_ptr(), _DTYPES[keys.dtype], ksb, ksh, kst, vsb, vsh, vst,
-            self.key_bits, kc.data_ptr(), ks.data_ptr(), kz.data_ptr() if kz is not None else None,
-            self.value_bits, vc.data_ptr(), vs.data_ptr(), vz.data_ptr() if vz is not None else None,
+            kv_k.code, kc.data_ptr(), ks.data_ptr(), kz.data_ptr() if kz is not None else None,
+            kv_v.code, vc.data_ptr(), vs.data_ptr(), vz.data_ptr() if vz is not None else None,
             B, H, L, D, prev, self.capacity, stream,
         )
         if rc == _lib.REC_ELAUNCH:
@@ -244,6 +277,7 @@ class QuantizedKVCache:
     def state(self, v):
         (self.keys, self.values, self.offset, self.group_size, self.key_bits, self.value_bits) = v
         self.bits = self.key_bits
+        self.affine = self.group_size == GROUP_AFFINE
         self.capacity = 0 if self.keys is None else QuantizedKV(*self.keys, self.key_bits, 0, False).capacity
         self._usable = True
 
@@ -286,9 +320,10 @@ class QuantizedKVCache:
 
 
 class MixedQuantizedKVCache(QuantizedKVCache):
-    """8-bit keys and 4-bit values by default, like the reference's
-    ``MixedQuantizedKVCache(group_size=64, key_bits=8, value_bits=4)``
-    (model.py:40-43); 4-bit groups here are 32 wide."""
+    """8-bit keys and 4-bit values in the group-64 affine format by default,
+    like the reference's ``MixedQuantizedKVCache(group_size=64, key_bits=8,
+    value_bits=4)`` (model.py:40-43); ``group_size=32`` selects this library's
+    int8 / uint4 formats."""
 
-    def __init__(self, group_size: int = GROUP4, key_bits: int = 8, value_bits: int = 4, **kw):
+    def __init__(self, group_size: int = GROUP_AFFINE, key_bits: int = 8, value_bits: int = 4, **kw):
         super().__init__(group_size, key_bits, value_bits, **kw)

@@ -62,6 +62,25 @@ int check_bits(int bits, const char* name) {
   return REC_OK;
 }
 
+// (k_bits, v_bits) -> kernel formats: this library's 8 / 4 in any mix, or
+// the MLX-style affine pair REC_AFFINE8 keys with REC_AFFINE4 values.
+int resolve_formats(int k_bits, int v_bits, int* kf, int* vf) {
+  const bool ka = k_bits == REC_AFFINE8 || k_bits == REC_AFFINE4, va = v_bits == REC_AFFINE8 || v_bits == REC_AFFINE4;
+  if (ka || va) {
+    if (k_bits != REC_AFFINE8 || v_bits != REC_AFFINE4)
+      return fail(REC_EUNSUPPORTED, "the affine format is REC_AFFINE8 keys with REC_AFFINE4 values (got %#x, %#x)",
+                  k_bits, v_bits);
+    *kf = FMT_A8;
+    *vf = FMT_A4;
+    return REC_OK;
+  }
+  int e;
+  if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
+  *kf = k_bits;
+  *vf = v_bits;
+  return REC_OK;
+}
+
 int check_cache(int bits, const void* codes, const void* scales, const void* zeros, const char* name) {
   if (!codes || !scales) return fail(REC_EINVAL, "%s codes/scales pointer is null", name);
   if (bits == 4 && !zeros) return fail(REC_EINVAL, "%s zero-points are required for 4-bit", name);
@@ -103,7 +122,7 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
                   int64_t cap, int splits, void* ws, size_t ws_bytes, float* out, const RowSrc* knew,
                   const RowSrc* vnew, int phases, void* stream) {
   int e;
-  if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
+  if ((e = resolve_formats(k_bits, v_bits, &k_bits, &v_bits))) return e;
   if ((e = check_dtype(q_dtype, "query"))) return e;
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
   if (B < 1 || Hkv < 1 || Hq < 1) return fail(REC_EINVAL, "B, Hq and Hkv must be positive");
@@ -177,7 +196,7 @@ int rec_kv_append(const void* k_new, const void* v_new, int in_dtype, int64_t k_
                   uint16_t* k_zeros, int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros, int B,
                   int Hkv, int L, int D, int64_t offset, int64_t capacity, void* stream) {
   int e;
-  if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
+  if ((e = resolve_formats(k_bits, v_bits, &k_bits, &v_bits))) return e;
   if ((e = check_dtype(in_dtype, "input"))) return e;
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
   if (B < 1 || Hkv < 1 || L < 0) return fail(REC_EINVAL, "bad shape B=%d Hkv=%d L=%d", B, Hkv, L);
@@ -205,7 +224,7 @@ int rec_kv_append(const void* k_new, const void* v_new, int in_dtype, int64_t k_
   a.L = L;
   a.offset = offset;
   a.cap = capacity;
-  a.v_units = v_bits == 4 ? ((offset + L - 1) >> 1) - (offset >> 1) + 1 : L;
+  a.v_units = v_bits == 4 || v_bits == FMT_A4 ? ((offset + L - 1) >> 1) - (offset >> 1) + 1 : L;
   return launched(launch_append(k_bits, v_bits, a, (hipStream_t)stream), "append launch");
 }
 
@@ -317,8 +336,9 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      float scale, int causal, int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
                      float* out, void* stream) {
   int e;
-  if ((e = check_bits(k_bits, "k_bits")) || (e = check_bits(v_bits, "v_bits"))) return e;
-  if (k_bits != 8 || v_bits != 8) return fail(REC_EUNSUPPORTED, "prefill supports int8 K and V only");
+  int kf, vf;
+  if ((e = resolve_formats(k_bits, v_bits, &kf, &vf))) return e;
+  if (kf != 8 || vf != 8) return fail(REC_EUNSUPPORTED, "prefill supports int8 K and V only");
   if (q_dtype != REC_BF16 && q_dtype != REC_F16)
     return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);

@@ -3,7 +3,8 @@
 // Restates MixedQuantizedKVCache.update_and_fetch's write step
 // (engine/src/rec_mlx/model.py:76-81): rows [0, L) of the new keys/values are
 // quantized and stored at cache positions [offset, offset + L).  One wavefront
-// per row (uint4 V: per byte pair of positions), four per workgroup.
+// per row (4-bit V: per byte pair of positions), four per workgroup.  Formats:
+// int8 / uint4 (this library's), and MLX-style affine 8-bit K with 4-bit V.
 #include "kernels.h"
 
 namespace rec {
@@ -27,8 +28,8 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
     const int64_t pos_even = ((a.offset >> 1) + u) * 2;
     const bool has_even = pos_even >= a.offset && pos_even < a.offset + a.L;
     const bool has_odd = pos_even + 1 >= a.offset && pos_even + 1 < a.offset + a.L;
-    append_v4_pair(a.v, b, h, (int)(pos_even - a.offset), has_even, has_odd, (uint8_t*)a.vq, a.vs, a.vz, bh, a.cap,
-                   pos_even, lane);
+    append_v4_pair<VB == FMT_A4>(a.v, b, h, (int)(pos_even - a.offset), has_even, has_odd, (uint8_t*)a.vq, a.vs,
+                                 a.vz, bh, a.cap, pos_even, lane);
   }
 }
 
@@ -44,6 +45,7 @@ hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream
   if (kb == 8 && vb == 8) hipLaunchKernelGGL((append_kernel<8, 8>), grid, block, 0, stream, a);
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((append_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((append_kernel<4, 8>), grid, block, 0, stream, a);
+  else if (kb == FMT_A8 && vb == FMT_A4) hipLaunchKernelGGL((append_kernel<FMT_A8, FMT_A4>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((append_kernel<4, 4>), grid, block, 0, stream, a);
   return hipGetLastError();
 }

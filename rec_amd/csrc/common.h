@@ -33,6 +33,12 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int HEAD_DIM = 128;
+// Cache formats (kernel template arguments): 8 = int8 symmetric, 4 = uint4
+// asymmetric group 32, FMT_A8 / FMT_A4 = MLX-style affine group 64 with bf16
+// scale and bias (8-bit keys / 4-bit values).
+constexpr int FMT_A8 = 18;
+constexpr int FMT_A4 = 14;
+constexpr int GROUP_A = 64;
 constexpr int BLOCK_T = 32;      // tokens per cache block and per wave iteration
 constexpr int GROUP4 = 32;       // int4 group size along head_dim
 constexpr float LOG2E = 1.4426950408889634f;
@@ -75,6 +81,12 @@ __device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dt)
 }
 
 // fp16 round-to-nearest-even of a non-negative float, saturating at 65504.
+// float -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
 __device__ __forceinline__ uint16_t half_bits_saturate(float f) {
   uint16_t b = float_to_half_bits(f);
   if ((b & 0x7fff) == 0x7c00) b = (b & 0x8000) | 0x7bff;

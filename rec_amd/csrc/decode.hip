@@ -120,7 +120,7 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
     const int lo = q16 - hi * 256;
     gsum += q16;
     const int d = d0 + i;
-    if constexpr (KB == 8) {
+    if constexpr (KB == 8 || KB == FMT_A8) {
       const int m = d >> 6, kg = (d >> 4) & 3, j = d & 15;
       qop[(m * 64 + kg * 16 + hh) * 16 + j] = (int8_t)hi;
       qop[(m * 64 + kg * 16 + hh + 8) * 16 + j] = (int8_t)lo;
@@ -131,7 +131,7 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
       qop[((pr * 2 + 1) * 64 + kg * 16 + c) * 16 + j] = (int8_t)lo;
     }
   }
-  if constexpr (KB == 4) {
+  if constexpr (KB == 4 || KB == FMT_A8) {
     // group of 32 dims = 8 consecutive threads
 #pragma unroll
     for (int m = 1; m < 8; m <<= 1) gsum += __shfl_xor(gsum, m, 64);
@@ -200,7 +200,7 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
   // 8kg .. 8kg+7 in the order idx = 4j + i.
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    if constexpr (KB == 8) {
+    if constexpr (KB == 8 || KB == FMT_A8) {
       R.k8[j][0] = ld128(rk, o.k[j], blk * 4096);
       R.k8[j][1] = ld128(rk, o.k[j] + 2048, blk * 4096);
     } else {
@@ -209,6 +209,8 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
   }
   if constexpr (KB == 8) {
     R.s8[0] = ld128(rks, o.s8, blk * 64);
+  } else if constexpr (KB == FMT_A8) {
+    R.m[0] = ld32(rks, o.m4, blk * 256);  // scales and biases
   } else {
     R.m[0] = ld32(rks, o.m4, blk * 256);
     R.m[1] = ld32(rkz, o.m4, blk * 256);
@@ -221,15 +223,22 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
   } else {
     R.v4[0] = ld128(rv, o.v, blk * 2048);
     R.v4[1] = ld128(rv, o.v + 1024, blk * 2048);
-    R.m[2] = ld32(rvs, o.m4, blk * 256);
-    R.m[3] = ld32(rvz, o.m4, blk * 256);
+    R.m[2] = ld32(rvs, o.m4, blk * 256);  // affine: scales and biases
+    if constexpr (VB == 4) R.m[3] = ld32(rvz, o.m4, blk * 256);
   }
 }
 
 struct State {
   float m, l;     // running max (log2 domain) and sum of this lane's head
   v4f acc[8];     // P·V accumulators: dims 16n + 4kg + i of head c
+  float vb[2];    // affine V: Σ p·bias over this lane's tokens, per 64-dim group
 };
+
+// bf16 element `slot` of 8 packed in a v4i, as float
+__device__ __forceinline__ float bf16_at(const v4i& w, int slot) {
+  const uint32_t x = (uint32_t)w[slot >> 1];
+  return __builtin_bit_cast(float, (slot & 1) ? (x & 0xffff0000u) : (x << 16));
+}
 
 template <int KB, int VB>
 __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, float qsum_a,
@@ -239,20 +248,37 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   // 8kg+7).  int4 scales and zero-points arrive one dword per lane; this
   // wavefront's LDS region ([K scales][K zeros][V scales][V zeros], 256 B
   // each, [4 groups][32 slots]) hands each lane the 16-byte runs it needs.
+  // Affine formats use the K and V halves of the region as [scales g0 g1][biases g0 g1].
   v4i ks, vs, ks4[2], kz4[2], vs4[4], vz4[4];
   if constexpr (KB == 8) ks = R.s8[0];
   if constexpr (VB == 8) vs = R.s8[1];
-  if constexpr (KB == 4 || VB == 4) {
+  if constexpr (KB == 4 || VB == 4 || KB == FMT_A8 || VB == FMT_A4) {
     uint32_t* mw = (uint32_t*)meta;
     if constexpr (KB == 4) {
       mw[lane] = R.m[0];
       mw[64 + lane] = R.m[1];
     }
+    if constexpr (KB == FMT_A8) mw[lane] = R.m[0];
     if constexpr (VB == 4) {
       mw[128 + lane] = R.m[2];
       mw[192 + lane] = R.m[3];
     }
+    if constexpr (VB == FMT_A4) mw[128 + lane] = R.m[2];
     wave_lds_sync();
+    if constexpr (KB == FMT_A8) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        ks4[g] = *(const v4i*)(meta + g * 64 + 16 * kg);        // scales, slots 8kg .. 8kg+7
+        kz4[g] = *(const v4i*)(meta + 128 + g * 64 + 16 * kg);  // biases
+      }
+    }
+    if constexpr (VB == FMT_A4) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        vs4[g] = *(const v4i*)(meta + 512 + g * 64 + 16 * kg);
+        vz4[g] = *(const v4i*)(meta + 640 + g * 64 + 16 * kg);
+      }
+    }
     if constexpr (KB == 4) {
 #pragma unroll
       for (int gi = 0; gi < 2; ++gi) {
@@ -287,6 +313,25 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         const int mine = d[i], partner = dpp_ror8(mine);
         const int full = (mine << sh_mine) + (partner << (8 - sh_mine));
         s[4 * j + i] = (float)full * half_at(ks, 4 * j + i);
+      }
+    } else if constexpr (KB == FMT_A8) {
+      // uint8 codes k enter as k - 128 (top bit flipped), one MFMA per 64-dim
+      // group: Σ q (s k + b) = s·Σ q (k - 128) + (128 s + b)·Q over the group,
+      // Q = the group's query sum (exact)
+      const v4i flip = {(int)0x80808080u, (int)0x80808080u, (int)0x80808080u, (int)0x80808080u};
+      v4i d0 = {0, 0, 0, 0}, d1 = {0, 0, 0, 0};
+      d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(R.k8[j][0] ^ flip, qop[0], d0, 0, 0, 0);
+      d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(R.k8[j][1] ^ flip, qop[1], d1, 0, 0, 0);
+      const int sh_mine = c < 8 ? 8 : 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sl = 2 * i + j;  // slot of position 4j + i
+        const int m0 = d0[i], p0 = dpp_ror8(m0), m1 = d1[i], p1 = dpp_ror8(m1);
+        const float f0 = (float)((m0 << sh_mine) + (p0 << (8 - sh_mine)));
+        const float f1 = (float)((m1 << sh_mine) + (p1 << (8 - sh_mine)));
+        const float s0 = bf16_at(ks4[0], sl), s1 = bf16_at(ks4[1], sl);
+        const float c0 = fmaf(128.f, s0, bf16_at(kz4[0], sl)), c1 = fmaf(128.f, s1, bf16_at(kz4[1], sl));
+        s[4 * j + i] = fmaf(s0, f0, fmaf(s1, f1, fmaf(c0, qsum_a, c1 * qsum_b)));
       }
     } else {
       const v4i ka = widen_u4((v2i){R.k4[j][0], R.k4[j][1]}), kb = widen_u4((v2i){R.k4[j][2], R.k4[j][3]});
@@ -326,6 +371,10 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     const float m_new = fmaxf(st.m, cmax);
     const float factor = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first chunk, 1 if unchanged
     st.l *= factor;
+    if constexpr (VB == FMT_A4) {
+      st.vb[0] *= factor;
+      st.vb[1] *= factor;
+    }
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.acc[n] *= factor;
     st.m = m_new;
@@ -346,6 +395,42 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     for (int n = 0; n < 8; ++n) {
       const v8h a0 = i8x8_to_h8((uint32_t)R.v8[n >> 1][2 * (n & 1)], (uint32_t)R.v8[n >> 1][2 * (n & 1) + 1]);
       st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb, st.acc[n], 0, 0, 0);
+    }
+  } else if constexpr (VB == FMT_A4) {
+    // affine 4-bit V, v = s q + b per 64-dim group: the A operand is q, exact
+    // in fp16 (nibble under the fp16 exponent of 1024 or 64, minus that
+    // offset), B = fp16(p·s) per group, and Σ p·b per group is kept aside and
+    // added to the group's dims at the end.  Scales and biases are stored in
+    // the nibble unpack's pair order (s4_slot): dword e of a run holds
+    // positions (e, e+4).
+    const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      v8h pb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t sw = (uint32_t)vs4[g][e], bw = (uint32_t)vz4[g][e];
+        const float slo = __builtin_bit_cast(float, sw << 16), shi = __builtin_bit_cast(float, sw & 0xffff0000u);
+        const float blo = __builtin_bit_cast(float, bw << 16), bhi = __builtin_bit_cast(float, bw & 0xffff0000u);
+        pb[2 * e] = (_Float16)(p[e] * slo);
+        pb[2 * e + 1] = (_Float16)(p[e + 4] * shi);
+        st.vb[g] = fmaf(p[e], blo, fmaf(p[e + 4], bhi, st.vb[g]));
+      }
+#pragma unroll
+      for (int nn = 0; nn < 4; ++nn) {
+        const int n = 4 * g + nn;
+        const uint32_t w = (uint32_t)R.v4[n >> 2][n & 3], w8 = w >> 8;
+        v8h a;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t t = (e & 1) ? and_or(e < 2 ? w : w8, 0x00f000f0u, 0x54005400u)
+                                     : and_or(e < 2 ? w : w8, 0x000f000fu, 0x64006400u);
+          const v2h d = __builtin_bit_cast(v2h, t) - ((e & 1) ? k64 : k1024);
+          a[2 * e] = d[0];
+          a[2 * e + 1] = d[1];
+        }
+        st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, st.acc[n], 0, 0, 0);
+      }
     }
   } else {
     // uint4 V: the A operand is q - z, exact in fp16, and the scale of the
@@ -417,7 +502,7 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
     t_end = t_begin + a.span < a.t_split_end ? t_begin + a.span : a.t_split_end;
   }
 
-  constexpr int64_t KROW = KB == 8 ? HEAD_DIM : HEAD_DIM / 2;  // code bytes per token
+  constexpr int64_t KROW = KB == 8 || KB == FMT_A8 ? HEAD_DIM : HEAD_DIM / 2;  // code bytes per token
   constexpr int64_t VROW = VB == 8 ? HEAD_DIM : HEAD_DIM / 2;
   constexpr int64_t KSROW = KB == 8 ? 1 : 4;                   // fp16 scales per token
   constexpr int64_t VSROW = VB == 8 ? 1 : 4;
@@ -440,8 +525,8 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
         append_row<8>(a.vnew, b, h, 0, 1, (void*)a.vq, (uint16_t*)a.vs, nullptr, bh, cap, pos, lane);
       } else {
         const bool odd = (pos & 1) != 0;
-        append_v4_pair(a.vnew, b, h, odd ? -1 : 0, !odd, odd, (uint8_t*)a.vq, (uint16_t*)a.vs, (uint16_t*)a.vz,
-                       bh, cap, pos & ~(int64_t)1, lane);
+        append_v4_pair<VB == FMT_A4>(a.vnew, b, h, odd ? -1 : 0, !odd, odd, (uint8_t*)a.vq, (uint16_t*)a.vs,
+                                     (uint16_t*)a.vz, bh, cap, pos & ~(int64_t)1, lane);
       }
     }
     __threadfence_block();
@@ -476,7 +561,7 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
   }
   __syncthreads();
 
-  constexpr int NOP = KB == 8 ? 2 : 4;
+  constexpr int NOP = KB == 8 || KB == FMT_A8 ? 2 : 4;
   v4i qop[NOP];
 #pragma unroll
   for (int o = 0; o < NOP; ++o) qop[o] = ((const v4i*)(smem + LDS_QOP))[o * 64 + lane];
@@ -484,11 +569,17 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
   // and all-zero scores, for which any positive step is exact
   const float qsc_h = ((const float*)(smem + LDS_QSC))[c & 7];
   const float qsc = qsc_h > 0.f ? qsc_h : 1.f;
-  float qsum_a = 0.f, qsum_b = 0.f;  // int4 K: per-group query sums of this lane's two groups (exact)
+  // query sums per group of this lane's head (exact integers): int4 K, the
+  // lane's two 32-dim groups; affine K, the two 64-dim groups
+  float qsum_a = 0.f, qsum_b = 0.f;
   if constexpr (KB == 4) {
     const int* qsum = (const int*)(smem + LDS_QSUM);
     qsum_a = (float)qsum[(c & 7) * 4 + (c >> 3)];
     qsum_b = (float)qsum[(c & 7) * 4 + 2 + (c >> 3)];
+  } else if constexpr (KB == FMT_A8) {
+    const int* qsum = (const int*)(smem + LDS_QSUM);
+    qsum_a = (float)(qsum[(c & 7) * 4] + qsum[(c & 7) * 4 + 1]);
+    qsum_b = (float)(qsum[(c & 7) * 4 + 2] + qsum[(c & 7) * 4 + 3]);
   }
 
   State st;
@@ -496,6 +587,7 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
   st.l = 0.f;
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
+  st.vb[0] = st.vb[1] = 0.f;
 
   // Step i loads chunk i+NBUF-1 into the buffer freed by step i-1, then
   // computes chunk i.  The ring is unrolled so buffer indices are static, and
@@ -518,6 +610,16 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
   // ---------------- wave partial -> LDS ----------------
   st.l += shfl_xor_f(st.l, 16);
   st.l += shfl_xor_f(st.l, 32);
+  if constexpr (VB == FMT_A4) {  // the bias terms join every dim of their group
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float vb = st.vb[g];
+      vb += shfl_xor_f(vb, 16);
+      vb += shfl_xor_f(vb, 32);
+#pragma unroll
+      for (int nn = 0; nn < 4; ++nn) st.acc[4 * g + nn] += vb;
+    }
+  }
   float* part = (float*)(smem + LDS_PART);
   float* pstat = (float*)(smem + LDS_PSTAT);
   if (c < 8 && c < a.G) {
@@ -640,6 +742,7 @@ hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_
   if (kb == 8 && vb == 8) hipLaunchKernelGGL((decode_kernel<8, 8>), grid, block, 0, stream, a);
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((decode_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((decode_kernel<4, 8>), grid, block, 0, stream, a);
+  else if (kb == FMT_A8 && vb == FMT_A4) hipLaunchKernelGGL((decode_kernel<FMT_A8, FMT_A4>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((decode_kernel<4, 4>), grid, block, 0, stream, a);
   return hipGetLastError();
 }

@@ -82,6 +82,38 @@ __device__ __forceinline__ void quantize_u4_pair(float x0, float x1, int& q0, in
   zbits = float_to_half_bits(z);
 }
 
+// MLX-style affine quantization of one group of 64 (32 lanes, 2 elements
+// each; restates mx.quantize's affine_quantize, mlx 0.32.0): the range is
+// [min w, max(0, max w)], the extreme of larger magnitude (the edge) is made
+// exact by stretching the step, codes are round((w - bias) / scale) clamped to
+// [0, 2^BITS - 1] (round = half away from zero), scale and bias are stored as
+// bf16.  Float32 arithmetic with correctly rounded division, so the codes and
+// bits match the CPU restatement exactly.
+template <int BITS>
+__device__ __forceinline__ void quantize_affine_pair(float x0, float x1, int& q0, int& q1, uint16_t& sbits,
+                                                     uint16_t& bbits) {
+  constexpr float n_bins = (float)((1 << BITS) - 1);
+  float mn = fminf(x0, x1), mx = fmaxf(x0, x1);
+#pragma unroll
+  for (int m = 1; m < 32; m <<= 1) {
+    mn = fminf(mn, __shfl_xor(mn, m, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+  }
+  mx = fmaxf(mx, 0.0f);
+  float scale = fmaxf((mx - mn) / n_bins, 1e-7f);
+  const bool side = fabsf(mn) > fabsf(mx);
+  scale = side ? scale : -scale;
+  const float edge = side ? mn : mx;
+  const float qe = __builtin_roundf(edge / scale);
+  const bool at_zero = qe == 0.0f;
+  scale = at_zero ? scale : edge / qe;
+  const float bias = at_zero ? 0.0f : edge;
+  q0 = (int)fminf(fmaxf(__builtin_roundf((x0 - bias) / scale), 0.0f), n_bins);
+  q1 = (int)fminf(fmaxf(__builtin_roundf((x1 - bias) / scale), 0.0f), n_bins);
+  sbits = float_to_bf16_bits(scale);
+  bbits = float_to_bf16_bits(bias);
+}
+
 // Cache addressing in elements (bytes for codes), see the layout table in common.h.
 __device__ __forceinline__ int64_t blk_base(int64_t bh, int64_t cap, int64_t t, int block_elems) {
   return (bh * (cap / BLOCK_T) + (t >> 5)) * block_elems;
@@ -121,6 +153,11 @@ __device__ __forceinline__ int64_t s4_off(int64_t bh, int64_t cap, int64_t t, in
   return blk_base(bh, cap, t, 128) + g * 32 + s4_slot(block_pos((int)(t & 31)));
 }
 
+// affine scale (which 0) or bias (which 1) of group g (0..1), at slot s4_slot(position)
+__device__ __forceinline__ int64_t sa_off(int64_t bh, int64_t cap, int64_t t, int which, int g) {
+  return blk_base(bh, cap, t, 128) + which * 64 + g * 32 + s4_slot(block_pos((int)(t & 31)));
+}
+
 // Quantize row (b, h, t_src) of `src` and store it at cache position `pos`.
 // kind 0 = K (row-major codes), kind 1 = V (token-blocked codes).  uint4 V
 // rows share bytes with their neighbour, so they go through append_v4_pair.
@@ -131,7 +168,16 @@ __device__ __forceinline__ void append_row(const RowSrc& src, int b, int h, int 
   const int64_t base = row_base(src, b, h, t_src);
   float x0, x1;
   load2_as_float(src, base + 2 * lane, x0, x1);
-  if constexpr (BITS == 8) {
+  if constexpr (BITS == FMT_A8) {  // affine 8-bit keys: uint8 codes in the int8 K layout
+    int q0, q1;
+    uint16_t sb, bb;
+    quantize_affine_pair<8>(x0, x1, q0, q1, sb, bb);
+    *(uint16_t*)((uint8_t*)codes + k8_off(bh, cap, pos, 2 * lane)) = (uint16_t)(q0 | (q1 << 8));
+    if ((lane & 31) == 0) {
+      scales[sa_off(bh, cap, pos, 0, lane >> 5)] = sb;
+      scales[sa_off(bh, cap, pos, 1, lane >> 5)] = bb;
+    }
+  } else if constexpr (BITS == 8) {
     int q0, q1;
     uint16_t sb;
     quantize_i8_pair(x0, x1, q0, q1, sb);
@@ -159,6 +205,8 @@ __device__ __forceinline__ void append_row(const RowSrc& src, int b, int h, int 
 // uint4 V: the byte shared by tokens (2p, 2p+1) (block positions p', p'^1 with
 // the even token in the low nibble).  Rows whose flag is false keep the nibble
 // already in the cache; each byte is written once.
+// AFFINE: MLX-style affine group 64 (scale and bias in `scales`, `zeros` unused).
+template <bool AFFINE = false>
 __device__ __forceinline__ void append_v4_pair(const RowSrc& src, int b, int h, int t_even, bool has_even,
                                                bool has_odd, uint8_t* codes, uint16_t* scales, uint16_t* zeros,
                                                int64_t bh, int64_t cap, int64_t pos_even, int lane) {
@@ -172,13 +220,21 @@ __device__ __forceinline__ void append_v4_pair(const RowSrc& src, int b, int h, 
     load2_as_float(src, base + 2 * lane, x0, x1);
     int q0, q1;
     uint16_t sb, zb;
-    quantize_u4_pair(x0, x1, q0, q1, sb, zb);
-    if (r == 0) { qe0 = q0; qe1 = q1; } else { qo0 = q0; qo1 = q1; }
-    if ((lane & 15) == 0) {
-      const int g = lane >> 4;
-      scales[s4_off(bh, cap, pos_even + r, g)] = sb;
-      zeros[s4_off(bh, cap, pos_even + r, g)] = zb;
+    if constexpr (AFFINE) {
+      quantize_affine_pair<4>(x0, x1, q0, q1, sb, zb);
+      if ((lane & 31) == 0) {
+        scales[sa_off(bh, cap, pos_even + r, 0, lane >> 5)] = sb;
+        scales[sa_off(bh, cap, pos_even + r, 1, lane >> 5)] = zb;
+      }
+    } else {
+      quantize_u4_pair(x0, x1, q0, q1, sb, zb);
+      if ((lane & 15) == 0) {
+        const int g = lane >> 4;
+        scales[s4_off(bh, cap, pos_even + r, g)] = sb;
+        zeros[s4_off(bh, cap, pos_even + r, g)] = zb;
+      }
     }
+    if (r == 0) { qe0 = q0; qe1 = q1; } else { qo0 = q0; qo1 = q1; }
   }
   const int64_t a0 = v4_off(bh, cap, pos_even, 2 * lane);
   const int64_t a1 = v4_off(bh, cap, pos_even, 2 * lane + 1);

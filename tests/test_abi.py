@@ -88,6 +88,12 @@ def test_decode_validation(lib):
     assert _decode(lib, ws=8) == _lib.REC_EALIGN
     assert _decode(lib, out=4) == _lib.REC_EALIGN
     assert _decode(lib, D=96) == _lib.REC_EUNSUPPORTED
+    # the affine format comes as REC_AFFINE8 keys with REC_AFFINE4 values only
+    assert _decode(lib, kb=_lib.REC_AFFINE8, vb=8) == _lib.REC_EUNSUPPORTED
+    assert _decode(lib, kb=_lib.REC_AFFINE4, vb=_lib.REC_AFFINE8) == _lib.REC_EUNSUPPORTED
+    assert "affine" in _lib.last_error()
+    assert _append(lib, kb=_lib.REC_AFFINE8, vb=4) == _lib.REC_EUNSUPPORTED
+    assert _append(lib, kb=_lib.REC_AFFINE8, vb=_lib.REC_AFFINE4, L=0) == _lib.REC_OK
 
 
 def test_error_mapping():

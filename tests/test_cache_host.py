@@ -163,12 +163,52 @@ def test_limits_and_invalidation():
 
 
 def test_constructor_validation_and_mixed_defaults():
-    m = MixedQuantizedKVCache()
-    assert (m.key_bits, m.value_bits, m.group_size, m.bits) == (8, 4, 32, 8)
+    m = MixedQuantizedKVCache()  # the reference's defaults: group 64 affine, 8-bit K, 4-bit V
+    assert (m.key_bits, m.value_bits, m.group_size, m.bits, m.affine) == (8, 4, 64, 8, True)
+    m32 = MixedQuantizedKVCache(32)
+    assert (m32.key_bits, m32.value_bits, m32.affine) == (8, 4, False)
+    with pytest.raises(NotImplementedError):
+        QuantizedKVCache(64, 8, 8)
     with pytest.raises(ValueError):
-        QuantizedKVCache(64, 8, 4)
+        QuantizedKVCache(48, 8, 4)
     with pytest.raises(ValueError):
         QuantizedKVCache(32, 3, 8)
+
+
+def _store_affine_scales(sc, bi):
+    """(B, H, T, 2) scales and biases -> [nb][scale, bias][2 groups][32 slots],
+    each run of 8 positions stored as 0, 4, 1, 5, 2, 6, 3, 7."""
+    B, H, T, G = sc.shape
+    out = np.zeros((B, H, T // 32, 2, G, 32), sc.dtype)
+    order = [0, 4, 1, 5, 2, 6, 3, 7]
+    for t in range(T):
+        p = _pos(t % 32)
+        slot = (p // 8) * 8 + order.index(p % 8)
+        out[:, :, t // 32, 0, :, slot] = sc[:, :, t]
+        out[:, :, t // 32, 1, :, slot] = bi[:, :, t]
+    return out
+
+
+def test_to_logical_affine_roundtrip():
+    rng = np.random.default_rng(2)
+    kq = rng.integers(0, 256, size=(1, 2, 64, 128), dtype=np.uint8)
+    vq = rng.integers(0, 16, size=(1, 2, 64, 128), dtype=np.uint8)
+    vpacked = vq[..., 0::2] | (vq[..., 1::2] << 4)
+    sc = torch.randn((1, 2, 64, 2)).to(torch.bfloat16)
+    bi = torch.randn((1, 2, 64, 2)).to(torch.bfloat16)
+    sb = torch.from_numpy(_store_affine_scales(sc.view(torch.int16).numpy(), bi.view(torch.int16).numpy()))
+    sb = sb.view(torch.bfloat16)
+    k = QuantizedKV(torch.from_numpy(_store_k(kq, 8)), sb, None, 8, 50, False, True)
+    v = QuantizedKV(torch.from_numpy(_store_v4(vq)), sb, None, 4, 50, True, True)
+    assert (k.code, v.code) == (0x108, 0x104)
+    for kv, codes in ((k, kq), (v, vpacked)):
+        c, s, b = to_logical(kv)
+        np.testing.assert_array_equal(c.numpy(), codes[:, :, :50])
+        assert torch.equal(s, sc[:, :, :50]) and torch.equal(b, bi[:, :, :50])
+    ka = _alloc(1, 4, 64, 8, False, "cpu", True)
+    va = _alloc(1, 4, 64, 4, True, "cpu", True)
+    assert ka[0].shape == (1, 4, 2, 4096) and ka[1].shape == (1, 4, 2, 2, 2, 32) and ka[2] is None
+    assert va[0].shape == (1, 4, 2, 2048) and va[1].dtype == torch.bfloat16
 
 
 def test_mask_trim_state():

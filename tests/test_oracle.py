@@ -372,3 +372,65 @@ def test_q4_planted_nibble_swap_is_caught():
     x, w, s, b = _q4_problem(rng, 1, 16, 128)
     swapped = ((w & np.uint32(0x0F0F0F0F)) << np.uint32(4)) | ((w >> np.uint32(4)) & np.uint32(0x0F0F0F0F))
     assert not np.allclose(O.q4_gemv(x, swapped, s, b), _dot16_form(x, w, s, b), rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# MLX-style affine group-64 quantizer
+
+
+def test_bf16_rn_and_round_half_away():
+    x = np.random.default_rng(31).standard_normal(10000).astype(np.float32) * 100
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.bf16_rn(x), want)
+    v = np.array([0.5, -0.5, 1.5, 2.5, -2.5, 0.49999997, -0.49999997, 3.0, -7.5], np.float32)
+    np.testing.assert_array_equal(O.round_half_away(v), [1, -1, 2, 3, -3, 0, -0, 3, -8])
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_affine_closed_forms(bits):
+    n = (1 << bits) - 1
+    k = np.arange(64) % (n + 1) if bits == 4 else np.round(np.linspace(0, n, 64)).astype(np.int64)
+    # levels 0 .. n of a step of 0.5, both ends present: codes n - k, scale -step, bias = max
+    q, s, b = O.quantize_affine((0.5 * k).astype(np.float32)[None], bits)
+    np.testing.assert_array_equal(q[0], n - k)
+    assert s[0, 0] == -0.5 and b[0, 0] == 0.5 * n
+    # the mirrored ramp: the negative edge wins, scale +step, bias = min
+    q, s, b = O.quantize_affine((-0.5 * k).astype(np.float32)[None], bits)
+    np.testing.assert_array_equal(q[0], n - k)
+    assert s[0, 0] == 0.5 and b[0, 0] == -0.5 * n
+    # constant and all-zero groups reconstruct to bf16 of the constant
+    for c in (0.0, 3.3, -1.7):
+        x = np.full((1, 64), c, np.float32)
+        q, s, b = O.quantize_affine(x, bits)
+        assert np.all(q == 0)
+        np.testing.assert_array_equal(O.dequantize_affine(q, s, b), O.bf16_rn(x))
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_affine_error_bound_and_edges(bits):
+    rng = np.random.default_rng(32 + bits)
+    x = (rng.standard_normal((50, 128)) * rng.uniform(0.1, 10, (50, 1))).astype(np.float32)
+    q, s, b = O.quantize_affine(x, bits)
+    assert q.max() <= (1 << bits) - 1
+    xh = O.dequantize_affine(q, s, b)
+    g = x.reshape(50, 2, 64)
+    # one step (the edge is made exact by stretching the step, so the far end
+    # can be clamped by up to one code), plus the bf16 rounding of scale and bias
+    slack = np.abs(s) * (1.0 + ((1 << bits) - 1) * 2.0**-8) + np.abs(b) * 2.0**-8
+    err = np.abs(xh - x).reshape(50, 2, 64)
+    assert np.all(err <= slack[..., None] * 1.001 + 1e-6)
+    # the edge element (the larger-magnitude extreme, or the max when zero wins) is code 0
+    w_min, w_max = g.min(-1), np.maximum(g.max(-1), 0)
+    edge = np.where(np.abs(w_min) > np.abs(w_max), w_min, w_max)
+    hit = (g == edge[..., None]) & (edge[..., None] != 0)
+    assert np.all(q.reshape(50, 2, 64)[hit] == 0)
+    # zero stays exact up to the bf16 rounding of scale and bias: the code of 0 is -q0
+    q0 = O.round_half_away(edge / np.where(np.abs(w_min) > np.abs(w_max), 1, -1) / np.maximum((w_max - w_min) / ((1 << bits) - 1), 1e-7))
+    assert np.all(np.abs(q0) <= (1 << bits) - 1)
+
+
+def test_affine_planted_bias_sign_is_caught():
+    x = (0.5 * (np.arange(64) % 16)).astype(np.float32)[None]
+    q, s, b = O.quantize_affine(x, 4)
+    assert not np.allclose(q * s.repeat(64, -1) - b.repeat(64, -1), x)  # wrong sign of the bias
+    np.testing.assert_array_equal(O.dequantize_affine(q, s, b), x)
