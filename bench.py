@@ -52,7 +52,13 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def row_bytes(bits):
+AFFINE = "affine"  # MLX-style affine group 64: 8-bit keys, 4-bit values, bf16 scale + bias
+
+
+def row_bytes(bits, is_v=False):
+    """Bytes per token per KV head: codes + scales (+ zero-points or biases)."""
+    if bits == AFFINE:
+        return (D // 2 if is_v else D) + 8  # codes + 2 groups x (bf16 scale + bf16 bias)
     return D + 2 if bits == 8 else D // 2 + 16  # codes + fp16 scale (+ zero-points)
 
 
@@ -60,10 +66,10 @@ def step_bytes(T, B=1, k_bits=8, v_bits=8, output=True):
     """Algorithmic HBM bytes of one decode step over T tokens: K/V codes and
     scales read once, query read, appended token read (fp16) and written
     (codes + scale), fp32 output written (by the merge when output=False)."""
-    kv = B * T * HKV * (row_bytes(k_bits) + row_bytes(v_bits))
+    kv = B * T * HKV * (row_bytes(k_bits) + row_bytes(v_bits, True))
     q = B * HQ * D * 2
     out = B * HQ * D * 4 if output else 0
-    append = B * HKV * (2 * D * 2 + row_bytes(k_bits) + row_bytes(v_bits))
+    append = B * HKV * (2 * D * 2 + row_bytes(k_bits) + row_bytes(v_bits, True))
     return kv + q + out + append
 
 
@@ -82,7 +88,8 @@ class DecodeWorkload:
         self.caches = []
         for i in range(R):
             T0 = T - counts[i]
-            c = rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T)
+            c = (rec_amd.QuantizedKVCache(64, 8, 4, max_tokens=T) if bits == AFFINE
+                 else rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T))
             k = synthetic.kv((1, HKV, T0, D), seed + 2 * i, kind=kind, frac=frac)
             v = synthetic.kv((1, HKV, T0, D), seed + 2 * i + 1, kind=kind, frac=frac)
             c.update_and_fetch(k, v)
@@ -118,11 +125,12 @@ class DecodeWorkload:
         vc, vs, vz = c.values
         stream = self.torch.cuda.current_stream().cuda_stream
         fn = self.lib.rec_decode_partial if partial_only else self.lib.rec_decode_append_attn
+        kcode, vcode = (_lib.REC_AFFINE8, _lib.REC_AFFINE4) if self.bits == AFFINE else (self.bits, self.bits)
         rc = fn(
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1),
-            self.bits, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
-            self.bits, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
+            kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
+            vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
             self.sinks.data_ptr(), SCALE, 1, HQ, HKV, D, T, c.capacity, self.splits,
             self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), stream,
         )
@@ -458,6 +466,7 @@ def main(argv=None):
     ap.add_argument("--no-int4", action="store_true", help="skip the 131K uint4 measurement")
     ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-cache measurements")
     ap.add_argument("--no-gemv", action="store_true", help="skip the int4 GEMV measurements")
+    ap.add_argument("--no-affine", action="store_true", help="skip the group-64 affine cache measurement")
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -508,6 +517,11 @@ def main(argv=None):
         ls = args.long_steps or max(16, args.steps // 8)
         r4 = run_decode(131072, 12, ls, max(4, args.warmup // 4), args.seed + 77, bits=4, kind="heavy", frac=0.05)
         log(f"131K int4: {r4['us_per_step']:.2f} us/step, {r4['gbs']:.0f} GB/s; kernel {r4['kernel_us']:.2f} us")
+
+    raf = None
+    if not args.no_affine:
+        raf = run_decode(32768, 40, max(16, args.steps // 4), max(4, args.warmup // 4), args.seed + 88, bits=AFFINE)
+        log(f"32K affine: {raf['us_per_step']:.2f} us/step, {raf['gbs']:.0f} GB/s; kernel {raf['kernel_us']:.2f} us")
 
     rbf = {}
     if not args.no_bf16:
@@ -600,6 +614,19 @@ def main(argv=None):
             "kernel_frac_of_peak": round(r4["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_step": r4["bytes_per_step"],
             "cache_instances": r4["instances"],
+        }
+    if raf is not None:
+        result["context_32k_affine"] = {
+            "context": 32768,
+            "kv_format": "MLX-style affine group 64: 8-bit K, 4-bit V, bf16 scale + bias (the reference's default)",
+            "us_per_step": round(raf["us_per_step"], 3),
+            "gbs": round(raf["gbs"], 2),
+            "frac_of_peak": round(raf["gbs"] / HBM_PEAK_GBS, 4),
+            "kernel_us": round(raf["kernel_us"], 3),
+            "kernel_gbs": round(raf["kernel_gbs"], 2),
+            "kernel_frac_of_peak": round(raf["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_step": raf["bytes_per_step"],
+            "cache_instances": raf["instances"],
         }
     result.update(rbf)
     if rq4 is not None:
