@@ -18,8 +18,9 @@
 // Work decomposition.  Grid (ceil(L/32), Hkv, B), 512 threads = 8 wavefronts;
 // wave w owns query head w of the KV head's GQA group and 32 query positions.
 // Each 128-token K/V tile is loaded once per workgroup, converted into
-// double-buffered LDS (141 KB) and shared by the 8 waves, which compute it in
-// two 64-token steps between barriers.
+// double-buffered LDS (149 KB) and shared by the 8 waves, which compute it in
+// four 32-token units, software-pipelined so that one unit's Q·Kᵀ runs on the
+// matrix cores while the previous unit's softmax runs on the VALU.
 //
 // S^T = K Q^T on 16x16x32 MFMAs (A = 16 tokens x 32 dims from LDS, B = Q^T held
 // in registers), which leaves lane (c, g) with the scores of query row c for
@@ -32,9 +33,8 @@ namespace rec {
 
 constexpr int PF_QB = 32;           // query positions per workgroup
 constexpr int PF_KT = 128;          // tokens per K/V tile in LDS (one barrier per tile)
-constexpr int PF_ST = 64;           // tokens per compute step (two steps per tile)
-constexpr int PF_KROW = 136;        // LDS row pitch of K (elements): 128 + 8 pad
-constexpr int PF_VROW = 136;        // LDS row pitch of V (elements): 128 + 8 pad
+constexpr int PF_KROW = 144;        // LDS row pitch of K (elements): 128 + 16 pad
+constexpr int PF_VROW = 144;        // LDS row pitch of V (elements): 128 + 16 pad
 constexpr int PF_K_ELEMS = PF_KT * PF_KROW;
 constexpr int PF_V_ELEMS = HEAD_DIM * PF_VROW;
 
@@ -126,43 +126,43 @@ __device__ __forceinline__ void store_tile(const TileRegs& R, typename MT<BF16>:
   if (tid < 256) (tid < 128 ? KS : VS)[tid & 127] = half_bits_to_float(R.s) * (tid < 128 ? q_mul : 1.f);
 }
 
-// One 64-token step for one wave: 32 query rows (two column tiles of 16) of
-// one head.  mask: some token of the tile lies past the cache end or past a
-// query's causal diagonal (only the tiles that reach a query block's diagonal);
-// masking is one loop under one uniform branch.
+// S^T = K Q^T for one 32-token unit of one wave: 32 query rows (two column
+// tiles of 16) of one head; lane (c, g) receives the scores of query row c for
+// tokens 16j + 4g + i of the unit.
 template <bool BF16>
-__device__ __forceinline__ void tile_step(const typename MT<BF16>::elem* K, const _Float16* Vv, const float* KS,
-                                          const float* VS, const typename MT<BF16>::vec (&qop)[2][4], float (&m_run)[2],
-                                          float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end, int qabs0, int causal,
-                                          bool mask, int c, int g) {
+__device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const typename MT<BF16>::vec (&qop)[2][4],
+                                        v4f (&s4)[2][2], int c, int g) {
   typedef typename MT<BF16>::vec V8;
-  // ---------------- S^T = K Q^T ----------------
-  // Matrix-core phases run at raised wave priority, so the SIMD's other wave
-  // tends to be in its softmax (VALU) phase meanwhile instead of in lockstep.
-  __builtin_amdgcn_s_setprio(1);
-  v4f s4[2][4];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s4[rt][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j) s4[rt][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const V8 ka = *(const V8*)(K + (16 * j + c) * PF_KROW + 32 * ks + 8 * g);
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) s4[rt][j] = MT<BF16>::mfma(ka, qop[rt][ks], s4[rt][j]);
     }
-  __builtin_amdgcn_s_setprio(0);
-  // scale (K scale x softmax scale, one multiply), mask, online softmax per
-  // query row (lane column c of tile rt)
-  v8h pb[2][2];
+}
+
+// Softmax of one unit's scores, then O^T += V^T P'^T.  mask: some token of the
+// unit lies past the cache end or past a query's causal diagonal (only units
+// that reach a query block's diagonal); one loop under one uniform branch.
+__device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
+                                                const float* VS, float (&m_run)[2], float (&l_run)[2],
+                                                v4f (&acc)[8][2], int t0, int t_end, int qabs0, int causal, bool mask,
+                                                int c, int g) {
+  v8h pb[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    float s[16];
+    // scale (K scale x softmax scale, one multiply), mask, online softmax per
+    // query row (lane column c of tile rt)
+    float s[8];
     const int qabs = qabs0 + 16 * rt + c;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const v4f ksc = *(const v4f*)(&KS[16 * j + 4 * g]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) s[4 * j + i] = s4[rt][j][i] * ksc[i];
@@ -171,48 +171,42 @@ __device__ __forceinline__ void tile_step(const typename MT<BF16>::elem* K, cons
       // last visible token of this row, relative to the lane's first token t0 + 4g
       const int last = (causal ? min(qabs, t_end - 1) : t_end - 1) - t0 - 4 * g;
 #pragma unroll
-      for (int k = 0; k < 16; ++k)
+      for (int k = 0; k < 8; ++k)
         if (16 * (k >> 2) + (k & 3) > last) s[k] = NEG_INF;
     }
-    float cmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-#pragma unroll
-    for (int k = 4; k < 16; k += 4) cmax = fmaxf(cmax, fmaxf(fmaxf(s[k], s[k + 1]), fmaxf(s[k + 2], s[k + 3])));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-    const float m_new = fmaxf(m_run[rt], cmax);
-    const float m_use = m_new == NEG_INF ? 0.f : m_new;
-    if (__ballot(m_new > m_run[rt])) {
-      const float factor = __builtin_amdgcn_exp2f(m_run[rt] - m_use);
+    float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    // a row's max moves iff one of its four lanes' maxima exceeds the running max
+    if (__ballot(cmax > m_run[rt])) {
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      const float m_new = fmaxf(m_run[rt], cmax);
+      const float factor = m_new == NEG_INF ? 1.f : __builtin_amdgcn_exp2f(m_run[rt] - m_new);
       l_run[rt] *= factor;
 #pragma unroll
       for (int n = 0; n < 8; ++n) acc[n][rt] *= factor;
       m_run[rt] = m_new;
     }
+    const float m_use = m_run[rt] == NEG_INF ? 0.f : m_run[rt];
     float lsum = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const v4f vsc = *(const v4f*)(&VS[16 * j + 4 * g]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = __builtin_amdgcn_exp2f(s[4 * j + i] - m_use);
         lsum += p;
-        // B operand of P·V for token half qq = j/2: k order (j&1, i)
-        pb[rt][j >> 1][4 * (j & 1) + i] = (_Float16)(p * vsc[i]);
+        // B operand of P·V: k index 8g + 4j + i = cache position of token 16j + 4g + i
+        pb[rt][4 * j + i] = (_Float16)(p * vsc[i]);
       }
     }
     l_run[rt] += lsum;
   }
-  // ---------------- O^T += V^T P'^T ----------------
-  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-  for (int n = 0; n < 8; ++n)
+  for (int n = 0; n < 8; ++n) {
+    const v8h va = *(const v8h*)(Vv + (16 * n + c) * PF_VROW + 8 * g);
 #pragma unroll
-    for (int qq = 0; qq < 2; ++qq) {
-      const v8h va = *(const v8h*)(Vv + (16 * n + c) * PF_VROW + 32 * qq + 8 * g);
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt][qq], acc[n][rt], 0, 0, 0);
-    }
-  __builtin_amdgcn_s_setprio(0);
+    for (int rt = 0; rt < 2; ++rt) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt], acc[n][rt], 0, 0, 0);
+  }
 }
 
 template <bool BF16>
@@ -256,30 +250,51 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   load_tile(R, a, bh, 0, tid, t_end);
   store_tile<BF16>(R, Kl[0], Vl[0], KS[0], VS[0], tid, a.q_mul);
   __syncthreads();
+
+  // Software pipeline over 32-token units (four per 128-token tile): the
+  // scores of unit k+1 are computed on the matrix cores while the VALU runs
+  // the softmax of unit k, so every unit's Q·Kᵀ overlaps another unit's
+  // softmax.  A tile's last unit is finished (softmax + P·V) in the next
+  // iteration, from the tile's buffer, which is refilled only after a barrier.
+  v4f sc[2][2][2];    // scores of two units in flight: [unit parity][rt][j]
+  bool pend = false;  // the previous unit awaits its softmax + P·V
+  int pend_t = 0;
   int buf = 0;
+  const int qabs0 = P + q0;
   for (int t0 = 0; t0 < t_end; t0 += PF_KT) {
     const bool more = t0 + PF_KT < t_end;
     if (more) load_tile(R, a, bh, t0 + PF_KT, tid, t_end);  // in flight during this tile
     if (active) {
 #pragma unroll
-      for (int s0 = 0; s0 < PF_KT; s0 += PF_ST) {
-        const int ts = t0 + s0;
-        if (ts < t_end) {
-          // steps that reach a query block's diagonal or the end of the cache are masked
-          const bool mask = ts + PF_ST > P + q0 || ts + PF_ST > t_end;
-          tile_step<BF16>(Kl[buf] + s0 * PF_KROW, Vl[buf] + s0, KS[buf] + s0, VS[buf] + s0, qop, m_run, l_run, acc,
-                          ts, t_end, P + q0, a.causal, mask, c, g);
+      for (int u = 0; u < PF_KT / 32; ++u) {
+        const int tu = t0 + 32 * u;
+        const bool live = tu < t_end;
+        if (live) qk_unit<BF16>(Kl[buf] + 32 * u * PF_KROW, qop, sc[u & 1], c, g);
+        if (pend) {
+          // the unit before: this tile's unit u - 1, or the previous tile's last
+          const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? PF_KT - 32 : 32 * (u - 1);
+          softmax_pv_unit(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_run, l_run, acc, pend_t,
+                          t_end, qabs0, a.causal, pend_t + 32 > qabs0 || pend_t + 32 > t_end, c, g);
         }
+        pend = live;
+        pend_t = tu;
       }
     }
     if (more) {
-      // The other buffer was last read in the previous tile, before the barrier
-      // that ended it, so it can be refilled without waiting.
+      // Other waves may still be finishing the previous tile's last unit,
+      // which reads the other buffer: all of them pass this barrier before it
+      // is refilled.
+      __syncthreads();
       store_tile<BF16>(R, Kl[buf ^ 1], Vl[buf ^ 1], KS[buf ^ 1], VS[buf ^ 1], tid, a.q_mul);
       __syncthreads();
       buf ^= 1;
     }
   }
+  // still pending: the last tile's last unit (every unit of a tile is visited,
+  // so a pending one here is unit 3, scores in sc[1])
+  if (active && pend)
+    softmax_pv_unit(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_run, l_run, acc,
+                    pend_t, t_end, qabs0, a.causal, pend_t + 32 > qabs0 || pend_t + 32 > t_end, c, g);
 
   if (!active) return;
   // ---------------- normalise and write ----------------
