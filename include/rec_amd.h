@@ -208,6 +208,23 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
+ * Prefill attention over a bf16 K/V cache (the FixedKVCache / FixedSlidingKVCache
+ * path): the L queries (B, Hq, L, D) bf16 or f16, element strides q_sb/q_sh/q_st,
+ * are the newest L of the T cached tokens (query i at position T-L+i); K and V
+ * are (B, Hkv, >=T, 128) bf16 with token stride 128 and 16-byte aligned rows.
+ * causal: query p sees keys <= p; window > 0 further limits it to keys
+ * > p - window (the sliding-window mask of cache.py:199-205).  Sinks, scale and
+ * the fp32 output (B, Hq, L, 128) as rec_prefill_attn.
+ * Replaces mx.fast.scaled_dot_product_attention over a FixedKVCache or
+ * FixedSlidingKVCache in Attention.__call__, engine/src/rec_mlx/model.py:204-211
+ * (the 512-query windowed form: engine/src/rec_mlx/m4_max_prefill.py:86-104).
+ */
+int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                     const void* k, int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh,
+                     const float* sinks, float scale, int causal, int window,
+                     int B, int Hq, int Hkv, int D, int L, int64_t T, float* out, void* stream);
+
+/*
  * int4 group-64 GEMV (MLX affine 4-bit, the format of the decoder's
  * projections, experts and lm head): y[m] = x[m] · Wᵀ for an (N, K) matrix
  * given as MLX words w (N, K/8) uint32 (code e of a word at bits 4e), bf16

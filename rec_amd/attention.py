@@ -207,27 +207,78 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
     _lib.check(rc, "rec_decode_bf16")
 
 
+def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out):
+    lib = _lib.load()
+    B, Hq, L, D = queries.shape
+    Hkv, T = keys.shape[1], keys.shape[2]
+    if queries.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
+    dev = queries.device
+    sk = _sinks(sinks, Hq, dev)
+    rc = lib.rec_prefill_bf16(
+        queries.data_ptr(), _DTYPES[queries.dtype], queries.stride(0), queries.stride(1), queries.stride(2),
+        keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
+        _ptr(sk), float(scale), int(causal), int(window), B, Hq, Hkv, D, L, T, out.data_ptr(),
+        torch.cuda.current_stream(dev).cuda_stream,
+    )
+    _lib.check(rc, "rec_prefill_bf16")
+
+
+def _mask_window(mask, L, T):
+    """(causal, window) of a mask: None, "causal", or a boolean (L, T) array
+    that must be the causal mask limited to the last ``window`` keys
+    (engine/src/rec_mlx/cache.py:199-205); anything else is not supported."""
+    if mask is None:
+        return False, 0
+    if isinstance(mask, str):
+        if mask != "causal":
+            raise NotImplementedError(f"mask {mask!r} is not supported")
+        return True, 0
+    if not isinstance(mask, torch.Tensor) or mask.dtype != torch.bool:
+        raise NotImplementedError("only boolean causal or sliding-window mask arrays are supported")
+    m = mask.reshape(mask.shape[-2:]) if mask.dim() > 2 and mask.numel() == L * T else mask
+    if tuple(m.shape) != (L, T):
+        raise NotImplementedError(f"mask of shape {tuple(mask.shape)} does not match ({L}, {T})")
+    window = int(m[-1].sum())
+    q = torch.arange(T - L, T, device=m.device)[:, None]
+    k = torch.arange(T, device=m.device)[None]
+    if torch.equal(m, (q >= k) & (q < k + window)):
+        return True, (0 if window >= T else window)
+    raise NotImplementedError("only causal or causal sliding-window mask arrays are supported")
+
+
 def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=None, *, out_dtype=None,
-                                 splits=None):
-    """Attention of ``queries`` ``(B, n_q, 1, 128)`` over bf16 ``keys``/``values``
-    ``(B, Hkv, T, 128)`` with token stride 128 (a :class:`FixedKVCache`'s views),
-    the per-head ``sinks`` in the softmax denominator: the call
-    Attention.__call__ makes for a FixedKVCache (model.py:204-211, the fused
-    SDPA's sinks argument).  One query token (decode) only.
+                                 splits=None, window=None):
+    """Attention of ``queries`` ``(B, n_q, L, 128)`` over bf16 ``keys``/``values``
+    ``(B, Hkv, T, 128)`` with token stride 128 (a :class:`FixedKVCache`'s views,
+    or the keys a :class:`FixedSlidingKVCache` returns), the per-head ``sinks``
+    in the softmax denominator: the call Attention.__call__ makes for those
+    caches (model.py:204-211, the fused SDPA's sinks argument).  One query
+    token decodes; ``L > 1`` queries are the newest ``L`` of the ``T`` keys,
+    under ``mask`` None, "causal" or a causal (sliding-window) boolean array;
+    ``window`` limits a causal mask to the last ``window`` keys.
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
-    if L != 1:
-        raise NotImplementedError("attention over a bf16 cache runs for one query token (decode) only")
     if not (_bf16_kv_ok(keys) and _bf16_kv_ok(values)):
         raise ValueError("keys/values must be bf16 GPU tensors (B, Hkv, T, 128) with token stride 128")
     if keys.shape != values.shape or keys.shape[0] != B or keys.shape[-1] != D:
         raise ValueError(f"keys {tuple(keys.shape)} / values {tuple(values.shape)} do not match queries")
-    if mask is not None and not (isinstance(mask, str) and mask == "causal"):
-        raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
-    out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
-    _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out)
-    out = out.view(B, Hq, 1, D)
+    if L == 1:
+        if mask is not None and not (isinstance(mask, str) and mask == "causal"):
+            raise NotImplementedError("explicit mask arrays are not supported for one query token; use None")
+        out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+        _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out)
+        out = out.view(B, Hq, 1, D)
+    else:
+        T = keys.shape[2]
+        if L > T:
+            raise ValueError(f"{L} queries but only {T} keys")
+        causal, win = _mask_window(mask, L, T)
+        if window is not None:
+            causal, win = True, (0 if window >= T else int(window))
+        out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
+        _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 
@@ -243,9 +294,14 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
     _check_query(queries)
     B, Hq, L, D = queries.shape
     if isinstance(cache, FixedSlidingKVCache):
-        # the new token goes to its ring slot; decode attends over the valid slots (order-free)
+        # a new token goes to its ring slot and decode attends over the valid
+        # slots (order-free); a chunk attends over the ring in order plus
+        # itself, causally within the window
         k, v = cache.update_and_fetch(keys, values)
-        return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits)
+        if L == 1:
+            return scaled_dot_product_attention(queries, k, v, scale, None, sinks, out_dtype=out_dtype, splits=splits)
+        return scaled_dot_product_attention(queries, k, v, scale, "causal", sinks, out_dtype=out_dtype,
+                                            window=cache.window_size)
     if isinstance(cache, FixedKVCache):
         if fused and L == 1:
             if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:

@@ -378,6 +378,52 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
 }
 
+int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
+                     int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale,
+                     int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T, float* out,
+                     void* stream) {
+  if (q_dtype != REC_BF16 && q_dtype != REC_F16)
+    return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
+  if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
+  if (B < 1 || Hkv < 1 || Hq < 1 || L < 1) return fail(REC_EINVAL, "bad shape B=%d Hq=%d Hkv=%d L=%d", B, Hq, Hkv, L);
+  if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
+  if (Hq / Hkv > 8) return fail(REC_EUNSUPPORTED, "GQA ratio %d exceeds 8", Hq / Hkv);
+  if (T < L) return fail(REC_EINVAL, "T=%lld is smaller than L=%d (the new tokens are cached first)", (long long)T, L);
+  if (T > ((int64_t)1 << 24)) return fail(REC_EUNSUPPORTED, "T above 16M tokens");
+  if (window < 0) return fail(REC_EINVAL, "negative window");
+  if (!q || !out || !k || !v) return fail(REC_EINVAL, "null pointer");
+  if (!aligned16(out) || !aligned16(k) || !aligned16(v)) return fail(REC_EALIGN, "K, V and output must be 16-byte aligned");
+  if (k_sb % 8 || k_sh % 8 || v_sb % 8 || v_sh % 8)
+    return fail(REC_EALIGN, "K/V batch and head strides must be multiples of 8 elements");
+  if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
+  PrefillArgs a{};
+  a.q = q;
+  a.q_dtype = q_dtype;
+  a.q_sb = q_sb;
+  a.q_sh = q_sh;
+  a.q_st = q_st;
+  a.kq = k;
+  a.vq = v;
+  a.k_sb = k_sb;
+  a.k_sh = k_sh;
+  a.v_sb = v_sb;
+  a.v_sh = v_sh;
+  a.kv_bf16 = 1;
+  a.sinks = sinks;
+  a.out = out;
+  a.q_mul = scale * LOG2E;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.L = L;
+  a.T = T;
+  a.cap = T;
+  a.causal = causal != 0;
+  a.window = window;
+  return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
+}
+
 int rec_kv_write_bf16(const void* k_new, const void* v_new, int in_dtype, int64_t k_sb, int64_t k_sh, int64_t k_st,
                       int64_t v_sb, int64_t v_sh, int64_t v_st, void* k, int64_t kc_sb, int64_t kc_sh, void* v,
                       int64_t vc_sb, int64_t vc_sh, int B, int Hkv, int L, int D, int64_t offset, int64_t capacity,

@@ -57,6 +57,9 @@ struct PrefillArgs {
   int B, Hq, Hkv, G, L;
   int64_t T, cap;              // cached tokens including the L new ones; capacity
   int causal;
+  int window;                  // > 0: query at position p sees keys (p - window, p] only
+  int kv_bf16;                 // K/V are bf16 (B, Hkv, T, 128) tensors, strides below
+  int64_t k_sb, k_sh, v_sb, v_sh;
 };
 
 // int4 group-64 GEMV: repack of an MLX affine matrix, then y = x Wᵀ.

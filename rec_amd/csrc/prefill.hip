@@ -32,11 +32,18 @@
 namespace rec {
 
 constexpr int PF_QB = 32;           // query positions per workgroup
-constexpr int PF_KT = 128;          // tokens per K/V tile in LDS (one barrier per tile)
 constexpr int PF_KROW = 144;        // LDS row pitch of K (elements): 128 + 16 pad
-constexpr int PF_VROW = 144;        // LDS row pitch of V (elements): 128 + 16 pad
-constexpr int PF_K_ELEMS = PF_KT * PF_KROW;
-constexpr int PF_V_ELEMS = HEAD_DIM * PF_VROW;
+
+// Tile geometry per cache format: tokens per K/V tile in LDS (one barrier per
+// tile) and the LDS row pitch of V (positions + 16 pad).  A bf16 cache moves
+// twice the bytes per token, so its tiles are half as long (same registers).
+template <bool KVB>
+struct PfTile {
+  static constexpr int KT = KVB ? 64 : 128;
+  static constexpr int VROW = KT + 16;
+  static constexpr int K_ELEMS = KT * PF_KROW;
+  static constexpr int V_ELEMS = HEAD_DIM * VROW;
+};
 
 template <bool BF16>
 struct MT;
@@ -113,7 +120,7 @@ __device__ __forceinline__ void store_tile(const TileRegs& R, typename MT<BF16>:
       const int n0 = 2 * (o >> 10), cc = (o >> 6) & 15, pg = (o >> 4) & 3;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        _Float16* dst = Vl + (16 * (n0 + half) + cc) * PF_VROW + 32 * bk + 8 * pg;
+        _Float16* dst = Vl + (16 * (n0 + half) + cc) * PfTile<false>::VROW + 32 * bk + 8 * pg;
 #pragma unroll
         for (int w = 0; w < 2; ++w)
 #pragma unroll
@@ -124,6 +131,56 @@ __device__ __forceinline__ void store_tile(const TileRegs& R, typename MT<BF16>:
   }
   // K scales carry the softmax scale (log2 domain)
   if (tid < 256) (tid < 128 ? KS : VS)[tid & 127] = half_bits_to_float(R.s) * (tid < 128 ? q_mul : 1.f);
+}
+
+// bf16 cache: a 64-token tile is 16 KB of K and of V; thread tid takes the
+// 16-byte chunks tid and tid + 512 of each, chunk = (token, 8 dims).
+__device__ __forceinline__ void load_tile_bf16(TileRegs& R, const PrefillArgs& a, int b, int h, int t0, int tid,
+                                               int t_end) {
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
+    const bool live = t0 + tok < t_end;
+    const int64_t row = (int64_t)(t0 + tok) * HEAD_DIM + d0;
+    const uint16_t* kp = (const uint16_t*)a.kq + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh + row;
+    const uint16_t* vp = (const uint16_t*)a.vq + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh + row;
+    R.k[part] = live ? __builtin_nontemporal_load((const v4i*)kp) : (v4i){0, 0, 0, 0};
+    R.v[part] = live ? __builtin_nontemporal_load((const v4i*)vp) : (v4i){0, 0, 0, 0};
+  }
+}
+
+// K rows as they are (bf16 queries) or in fp16; V transposed into [dim][cache
+// position] as fp16 (exact for bf16 values in fp16's normal range), the
+// position of token t of a 32-token unit being block_pos(t) as in the int8
+// layout; the "scales" are the softmax scale and 1.
+template <bool BF16>
+__device__ __forceinline__ void store_tile_bf16(const TileRegs& R, typename MT<BF16>::elem* Kl, _Float16* Vl,
+                                                float* KS, float* VS, int tid, float q_mul) {
+  constexpr int VROW = PfTile<true>::VROW;
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
+    if constexpr (BF16) {
+      *(v4i*)(Kl + tok * PF_KROW + d0) = R.k[part];
+    } else {
+      v8h kh;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = (uint32_t)R.k[part][e];
+        kh[2 * e] = (_Float16)__builtin_bit_cast(float, w << 16);
+        kh[2 * e + 1] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
+      }
+      *(v8h*)(Kl + tok * PF_KROW + d0) = kh;
+    }
+    const int col = (tok & ~31) + block_pos(tok & 31);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = (uint32_t)R.v[part][e];
+      Vl[(d0 + 2 * e) * VROW + col] = (_Float16)__builtin_bit_cast(float, w << 16);
+      Vl[(d0 + 2 * e + 1) * VROW + col] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
+    }
+  }
+  if (tid < 2 * PfTile<true>::KT) (tid < PfTile<true>::KT ? KS : VS)[tid & (PfTile<true>::KT - 1)] = tid < PfTile<true>::KT ? q_mul : 1.f;
 }
 
 // S^T = K Q^T for one 32-token unit of one wave: 32 query rows (two column
@@ -150,10 +207,11 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
 // Softmax of one unit's scores, then O^T += V^T P'^T.  mask: some token of the
 // unit lies past the cache end or past a query's causal diagonal (only units
 // that reach a query block's diagonal); one loop under one uniform branch.
+template <int VROW>
 __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
                                                 const float* VS, float (&m_run)[2], float (&l_run)[2],
-                                                v4f (&acc)[8][2], int t0, int t_end, int qabs0, int causal, bool mask,
-                                                int c, int g) {
+                                                v4f (&acc)[8][2], int t0, int t_end, int qabs0, int causal, int window,
+                                                bool mask, int c, int g) {
   v8h pb[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
@@ -168,11 +226,14 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
       for (int i = 0; i < 4; ++i) s[4 * j + i] = s4[rt][j][i] * ksc[i];
     }
     if (mask) {
-      // last visible token of this row, relative to the lane's first token t0 + 4g
+      // first and last visible token of this row, relative to the lane's first token t0 + 4g
       const int last = (causal ? min(qabs, t_end - 1) : t_end - 1) - t0 - 4 * g;
+      const int first = window > 0 ? qabs - window + 1 - t0 - 4 * g : INT32_MIN;
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (16 * (k >> 2) + (k & 3) > last) s[k] = NEG_INF;
+      for (int k = 0; k < 8; ++k) {
+        const int pos = 16 * (k >> 2) + (k & 3);
+        if (pos > last || pos < first) s[k] = NEG_INF;
+      }
     }
     float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
     // a row's max moves iff one of its four lanes' maxima exceeds the running max
@@ -203,18 +264,19 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
   }
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
-    const v8h va = *(const v8h*)(Vv + (16 * n + c) * PF_VROW + 8 * g);
+    const v8h va = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt], acc[n][rt], 0, 0, 0);
   }
 }
 
-template <bool BF16>
+template <bool BF16, bool KVB>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   typedef typename MT<BF16>::elem E;
   typedef typename MT<BF16>::vec V8;
-  __shared__ __attribute__((aligned(16))) E Kl[2][PF_K_ELEMS];
-  __shared__ __attribute__((aligned(16))) _Float16 Vl[2][PF_V_ELEMS];
+  constexpr int PF_KT = PfTile<KVB>::KT, VROW = PfTile<KVB>::VROW;
+  __shared__ __attribute__((aligned(16))) E Kl[2][PfTile<KVB>::K_ELEMS];
+  __shared__ __attribute__((aligned(16))) _Float16 Vl[2][PfTile<KVB>::V_ELEMS];
   __shared__ __attribute__((aligned(16))) float KS[2][PF_KT];
   __shared__ __attribute__((aligned(16))) float VS[2][PF_KT];
 
@@ -246,9 +308,20 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) acc[n][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
 
+  // a sliding window (bf16 caches only) starts the scan at the first query's first visible key
+  const int window = KVB ? a.window : 0;
+  const int t_first = window > 0 ? max(0, P + q0 - window + 1) / PF_KT * PF_KT : 0;
+  const auto fetch = [&](TileRegs& R, int t0) {
+    if constexpr (KVB) load_tile_bf16(R, a, b, h, t0, tid, t_end);
+    else load_tile(R, a, bh, t0, tid, t_end);
+  };
+  const auto put = [&](const TileRegs& R, int bf) {
+    if constexpr (KVB) store_tile_bf16<BF16>(R, Kl[bf], Vl[bf], KS[bf], VS[bf], tid, a.q_mul);
+    else store_tile<BF16>(R, Kl[bf], Vl[bf], KS[bf], VS[bf], tid, a.q_mul);
+  };
   TileRegs R;
-  load_tile(R, a, bh, 0, tid, t_end);
-  store_tile<BF16>(R, Kl[0], Vl[0], KS[0], VS[0], tid, a.q_mul);
+  fetch(R, t_first);
+  put(R, 0);
   __syncthreads();
 
   // Software pipeline over 32-token units (four per 128-token tile): the
@@ -261,9 +334,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   int pend_t = 0;
   int buf = 0;
   const int qabs0 = P + q0;
-  for (int t0 = 0; t0 < t_end; t0 += PF_KT) {
+  // a unit needs the mask loop if it reaches a query block's diagonal, the
+  // cache end, or (sliding window) lies before some query's window start
+  const auto needs_mask = [&](int tu) {
+    return tu + 32 > qabs0 || tu + 32 > t_end || (window > 0 && tu < qabs0 + PF_QB - window);
+  };
+  for (int t0 = t_first; t0 < t_end; t0 += PF_KT) {
     const bool more = t0 + PF_KT < t_end;
-    if (more) load_tile(R, a, bh, t0 + PF_KT, tid, t_end);  // in flight during this tile
+    if (more) fetch(R, t0 + PF_KT);  // in flight during this tile
     if (active) {
 #pragma unroll
       for (int u = 0; u < PF_KT / 32; ++u) {
@@ -273,8 +351,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
         if (pend) {
           // the unit before: this tile's unit u - 1, or the previous tile's last
           const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? PF_KT - 32 : 32 * (u - 1);
-          softmax_pv_unit(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_run, l_run, acc, pend_t,
-                          t_end, qabs0, a.causal, pend_t + 32 > qabs0 || pend_t + 32 > t_end, c, g);
+          softmax_pv_unit<VROW>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_run, l_run, acc,
+                                pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
         }
         pend = live;
         pend_t = tu;
@@ -285,16 +363,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       // which reads the other buffer: all of them pass this barrier before it
       // is refilled.
       __syncthreads();
-      store_tile<BF16>(R, Kl[buf ^ 1], Vl[buf ^ 1], KS[buf ^ 1], VS[buf ^ 1], tid, a.q_mul);
+      put(R, buf ^ 1);
       __syncthreads();
       buf ^= 1;
     }
   }
   // still pending: the last tile's last unit (every unit of a tile is visited,
-  // so a pending one here is unit 3, scores in sc[1])
+  // and a tile has an even number of units, so its scores are in sc[1])
   if (active && pend)
-    softmax_pv_unit(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_run, l_run, acc,
-                    pend_t, t_end, qabs0, a.causal, pend_t + 32 > qabs0 || pend_t + 32 > t_end, c, g);
+    softmax_pv_unit<VROW>(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_run, l_run,
+                          acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
 
   if (!active) return;
   // ---------------- normalise and write ----------------
@@ -324,8 +402,13 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)((a.L + PF_QB - 1) / PF_QB), a.Hkv, a.B), block(512);
-  if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((prefill_kernel<false>), grid, block, 0, stream, a);
+  if (a.kv_bf16) {
+    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((prefill_kernel<false, true>), grid, block, 0, stream, a);
+  } else {
+    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, block, 0, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -147,8 +147,8 @@ def test_bf16_rejects_bad_inputs(gpu):
     with pytest.raises(ValueError):
         scaled_dot_product_attention(q, k, k, SCALE)
     kb = k.to(torch.bfloat16)
-    with pytest.raises(NotImplementedError):
-        scaled_dot_product_attention(q.expand(1, 32, 2, 128), kb, kb, SCALE)
+    with pytest.raises(NotImplementedError):  # several float32 queries: no matrix-core input type
+        scaled_dot_product_attention(q.float().expand(1, 32, 2, 128), kb, kb, SCALE, "causal")
     store = KVStorage(1, 100, 4)
     cache = FixedKVCache(store, 0)
     with pytest.raises(ValueError, match="Decode context limit exhausted"):
@@ -190,3 +190,87 @@ def test_sliding_window_ring_decode(gpu):
     assert cache.make_mask(1) is None
     m = cache.make_mask(3, return_array=True)
     assert m.shape == (3, W + 3) and bool(m[0, 0]) is False and bool(m[2, -1]) is True
+
+
+# ---------------------------------------------------------------------------
+# prefill over the bf16 cache (L > 1 queries, the newest L of the T cached tokens)
+
+
+PREFILL_CASES = [
+    # B, Hq, Hkv, P (prefix), L (new), q dtype, sinks, causal
+    (1, 32, 4, 1000, 300, torch.bfloat16, True, True),
+    (1, 8, 1, 0, 77, torch.bfloat16, False, True),
+    (2, 16, 2, 130, 64, torch.float16, True, True),
+    (1, 32, 4, 500, 129, torch.bfloat16, True, False),
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_{}_s{}_c{}".format(
+    c[0], c[1], c[2], c[3], c[4], str(c[5])[6:], c[6], c[7]))
+def test_bf16_prefill_matches_oracle(gpu, case):
+    """FixedKVCache: the prefix goes in, then a chunk of L tokens is appended
+    and attends over everything (causal or full), as Attention.__call__ does."""
+    B, Hq, Hkv, P, L, qdt, use_sinks, causal = case
+    T = P + L
+    store = KVStorage(1, T, Hkv, batch=B)
+    cache = FixedKVCache(store, 0)
+    k = synthetic.kv((B, Hkv, T, 128), 111, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, T, 128), 112, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    if P:
+        cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    q = synthetic.query(B, Hq, L, 113, dtype=qdt)
+    sinks = torch.randn(Hq, device="cuda") if use_sinks else None
+    mask = "causal" if causal else None
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert cache.offset == T
+    ref = O.attention(f32(q), bf16_np(k), bf16_np(v), SCALE, sinks=None if sinks is None else f32(sinks), mask=mask)
+    assert_close(f32(out), ref, f"case {case}")
+
+
+def test_bf16_prefill_window_mask_array(gpu):
+    """A boolean sliding-window mask array (make_mask(..., return_array=True))
+    is recognised and gives the same result as the oracle with that mask."""
+    B, Hq, Hkv, T, L, W = 1, 16, 2, 400, 150, 97
+    k = synthetic.kv((B, Hkv, T, 128), 121, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, T, 128), 122, dtype=torch.bfloat16)
+    q = synthetic.query(B, Hq, L, 123, dtype=torch.bfloat16)
+    qi = torch.arange(T - L, T)[:, None]
+    ki = torch.arange(T)[None]
+    mask = ((qi >= ki) & (qi < ki + W)).cuda()
+    sinks = torch.randn(Hq, device="cuda")
+    out = scaled_dot_product_attention(q, k, v, SCALE, mask, sinks, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.attention(f32(q), bf16_np(k), bf16_np(v), SCALE, sinks=f32(sinks), mask=mask.cpu().numpy())
+    assert_close(f32(out), ref, "window mask array")
+    with pytest.raises(NotImplementedError):  # not a causal-window pattern
+        scaled_dot_product_attention(q, k, v, SCALE, ~mask, sinks)
+
+
+def test_sliding_window_prefill_chunks(gpu):
+    """FixedSlidingKVCache: chunks longer than the window, then decode steps;
+    each chunk attends over the ring (in order) plus itself within the window
+    (cache.py:153-258, the windowed prefill of m4_max_prefill.py:86-104)."""
+    from rec_amd import FixedSlidingKVCache
+
+    B, Hq, Hkv, W = 1, 32, 4, 100
+    cache = FixedSlidingKVCache(max_sequence_tokens=4096, num_kv_heads=Hkv, head_dim=128, window_size=W)
+    n = 400
+    k = synthetic.kv((B, Hkv, n, 128), 131, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, n, 128), 132, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    pos = 0
+    for L in (150, 1, 1, 70, 130, 1):
+        q = synthetic.query(B, Hq, L, 140 + pos, dtype=torch.bfloat16)
+        lo = max(0, pos - W) if L == 1 else max(0, pos - cache.size())
+        out = attend(q, k[:, :, pos : pos + L], v[:, :, pos : pos + L], cache, SCALE, "causal", sinks,
+                     out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        end = pos + L
+        Tk = end - lo if L > 1 else min(end, W)
+        kk, vv = bf16_np(k[:, :, end - Tk : end]), bf16_np(v[:, :, end - Tk : end])
+        qi = np.arange(Tk - L, Tk)[:, None]
+        ki = np.arange(Tk)[None]
+        ref = O.attention(f32(q), kk, vv, SCALE, sinks=f32(sinks), mask=(qi >= ki) & (qi < ki + W))
+        assert_close(f32(out), ref, f"chunk at {pos} of {L}")
+        pos = end
