@@ -208,6 +208,18 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
+ * Dequantize cache rows [0, T) of any format (k_bits / v_bits as rec_kv_append)
+ * into bf16 K and V tensors (B, Hkv, T, 128), contiguous and 16-byte aligned:
+ * x̂ formed in float32 (int8 q*s, uint4 (q - z)*s, affine q*s + b), rounded to
+ * bf16.  Replaces the dequantization of the prefill branch,
+ * engine/src/rec_mlx/model.py:194-195 (the attention then runs on the bf16
+ * tensors, rec_prefill_bf16).
+ */
+int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros,
+                        int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
+                        int B, int Hkv, int64_t T, int64_t capacity, void* k_out, void* v_out, void* stream);
+
+/*
  * Prefill attention over a bf16 K/V cache (the FixedKVCache / FixedSlidingKVCache
  * path): the L queries (B, Hq, L, D) bf16 or f16, element strides q_sb/q_sh/q_st,
  * are the newest L of the T cached tokens (query i at position T-L+i); K and V

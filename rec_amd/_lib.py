@@ -73,6 +73,7 @@ SIGNATURES["rec_decode_bf16"] = (
     ],
 )
 
+SIGNATURES["rec_kv_dequant_bf16"] = (_i, [_i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i64, _i64, _p, _p, _p])
 SIGNATURES["rec_prefill_bf16"] = (
     _i,
     [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64, _p, _p],

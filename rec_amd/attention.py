@@ -135,6 +135,25 @@ def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sink
     _lib.check(rc, "rec_prefill_attn")
 
 
+def dequantize_kv(keys: QuantizedKV, values: QuantizedKV):
+    """bf16 ``(B, Hkv, T, 128)`` copies of the ``T = keys.length`` valid cache
+    rows (x̂ in float32 from the stored codes, scales, zeros or biases, then
+    rounded to bf16), as the reference's prefill branch dequantizes its cache
+    before attention (engine/src/rec_mlx/model.py:194-195)."""
+    lib = _lib.load()
+    B, Hkv, T = keys.codes.shape[0], keys.n_kv_heads, int(keys.length)
+    dev = keys.codes.device
+    k = torch.empty((B, Hkv, T, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+    v = torch.empty_like(k)
+    rc = lib.rec_kv_dequant_bf16(
+        keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
+        values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
+        B, Hkv, T, int(keys.capacity), k.data_ptr(), v.data_ptr(), torch.cuda.current_stream(dev).cuda_stream,
+    )
+    _lib.check(rc, "rec_kv_dequant_bf16")
+    return k, v
+
+
 def quantized_attention_with_sinks(
     queries, keys, values, scale, mask, sinks, group_size, key_bits, value_bits, *, out_dtype=None, splits=None
 ):
@@ -143,9 +162,10 @@ def quantized_attention_with_sinks(
     ``keys``/``values`` are what :meth:`QuantizedKVCache.update_and_fetch`
     returns; ``sinks`` (``n_q`` logits or None) join the softmax denominator;
     ``mask`` is None or "causal" (for ``L == 1`` both mean "every cached
-    token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` the chunked
-    prefill kernel (int8 cache, bf16/f16 queries), the queries being the newest
-    ``L`` cached tokens.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
+    token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` (bf16/f16
+    queries, the newest ``L`` cached tokens) the chunked prefill kernel, which
+    reads an int8 cache directly; other formats are first dequantized to bf16
+    (:func:`dequantize_kv`) and run the bf16 prefill kernel.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
     (default: the query dtype, as the reference returns, model.py:132-139).
     """
     _check_query(queries)
@@ -168,8 +188,14 @@ def quantized_attention_with_sinks(
         # the L queries are the newest L cached tokens (model.py:122-125)
         if L > keys.length:
             raise ValueError(f"{L} queries but only {keys.length} cached tokens")
+        if queries.dtype not in (torch.bfloat16, torch.float16):
+            raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
-        _prefill_launch(queries, keys, values, scale, sinks, mask == "causal", out)
+        if keys.code == 8 and values.code == 8:
+            _prefill_launch(queries, keys, values, scale, sinks, mask == "causal", out)
+        else:
+            k, v = dequantize_kv(keys, values)
+            _bf16_prefill_launch(queries, k, v, scale, sinks, mask == "causal", 0, out)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 

@@ -378,6 +378,35 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
 }
 
+int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits,
+                        const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros, int B, int Hkv,
+                        int64_t T, int64_t capacity, void* k_out, void* v_out, void* stream) {
+  int e, kf, vf;
+  if ((e = resolve_formats(k_bits, v_bits, &kf, &vf))) return e;
+  if (B < 1 || Hkv < 1 || T < 0) return fail(REC_EINVAL, "bad shape B=%d Hkv=%d T=%lld", B, Hkv, (long long)T);
+  if (capacity % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 32", (long long)capacity);
+  if (T > capacity) return fail(REC_ECAPACITY, "T=%lld exceeds the cache capacity %lld", (long long)T, (long long)capacity);
+  if ((e = check_cache(kf, k_codes, k_scales, k_zeros, "key")) || (e = check_cache(vf, v_codes, v_scales, v_zeros, "value")))
+    return e;
+  if (!k_out || !v_out) return fail(REC_EINVAL, "output pointer is null");
+  if (!aligned16(k_out) || !aligned16(v_out)) return fail(REC_EALIGN, "outputs must be 16-byte aligned");
+  if (T == 0) return ok();
+  DequantArgs a{};
+  a.kq = k_codes;
+  a.ks = k_scales;
+  a.kz = k_zeros;
+  a.vq = v_codes;
+  a.vs = v_scales;
+  a.vz = v_zeros;
+  a.B = B;
+  a.Hkv = Hkv;
+  a.T = T;
+  a.cap = capacity;
+  a.k_out = (uint16_t*)k_out;
+  a.v_out = (uint16_t*)v_out;
+  return launched(launch_dequant(kf, vf, a, (hipStream_t)stream), "dequant launch");
+}
+
 int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
                      int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale,
                      int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T, float* out,

@@ -33,6 +33,87 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
   }
 }
 
+// Dequantize cache rows [0, T) to bf16 (B, Hkv, T, 128) tensors: the
+// reference's prefill branch dequantizes the cache to the query dtype before
+// its attention (engine/src/rec_mlx/model.py:194-195).  One wavefront per row,
+// lane l owns dims 2l, 2l+1; x̂ is formed in float32 exactly as the CPU
+// restatement does (int8 q·s, uint4 (q - z)·s, affine q·s + b), then rounded
+// to bf16.  blockIdx.y: 0 = K, 1 = V.
+template <int BITS>
+__device__ __forceinline__ void dequant_pair(const void* codes, const uint16_t* scales, const uint16_t* zeros,
+                                             bool is_v, int64_t bh, int64_t cap, int64_t t, int lane, float& x0,
+                                             float& x1) {
+  const int d = 2 * lane;
+  if constexpr (BITS == 8) {
+    const int8_t* c = (const int8_t*)codes;
+    const int q0 = is_v ? c[v8_off(bh, cap, t, d)] : c[k8_off(bh, cap, t, d)];
+    const int q1 = is_v ? c[v8_off(bh, cap, t, d + 1)] : c[k8_off(bh, cap, t, d + 1)];
+    const float s = half_bits_to_float(scales[s8_off(bh, cap, t)]);
+    x0 = (float)q0 * s;
+    x1 = (float)q1 * s;
+  } else if constexpr (BITS == 4) {
+    const uint8_t* c = (const uint8_t*)codes;
+    int q0, q1;
+    if (is_v) {
+      const int p = block_pos((int)(t & 31));
+      const uint8_t b0 = c[v4_off(bh, cap, t, d)], b1 = c[v4_off(bh, cap, t, d + 1)];
+      q0 = (p & 1) ? b0 >> 4 : b0 & 15;
+      q1 = (p & 1) ? b1 >> 4 : b1 & 15;
+    } else {
+      const uint8_t b = c[k4_off(bh, cap, t, d)];
+      q0 = b & 15;
+      q1 = b >> 4;
+    }
+    const int g = d >> 5;
+    const float s = half_bits_to_float(scales[s4_off(bh, cap, t, g)]);
+    const float z = half_bits_to_float(zeros[s4_off(bh, cap, t, g)]);
+    x0 = ((float)q0 - z) * s;
+    x1 = ((float)q1 - z) * s;
+  } else {  // affine: FMT_A8 keys (uint8 in the int8 K layout), FMT_A4 values (uint4 in the int4 V layout)
+    const uint8_t* c = (const uint8_t*)codes;
+    int q0, q1;
+    if constexpr (BITS == FMT_A8) {
+      q0 = c[k8_off(bh, cap, t, d)];
+      q1 = c[k8_off(bh, cap, t, d + 1)];
+    } else {
+      const int p = block_pos((int)(t & 31));
+      const uint8_t b0 = c[v4_off(bh, cap, t, d)], b1 = c[v4_off(bh, cap, t, d + 1)];
+      q0 = (p & 1) ? b0 >> 4 : b0 & 15;
+      q1 = (p & 1) ? b1 >> 4 : b1 & 15;
+    }
+    const int g = d >> 6;
+    const float s = __builtin_bit_cast(float, (uint32_t)scales[sa_off(bh, cap, t, 0, g)] << 16);
+    const float b = __builtin_bit_cast(float, (uint32_t)scales[sa_off(bh, cap, t, 1, g)] << 16);
+    x0 = (float)q0 * s + b;
+    x1 = (float)q1 * s + b;
+  }
+}
+
+template <int KB, int VB>
+__global__ __launch_bounds__(256) void dequant_kernel(const DequantArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (int64_t)a.B * a.Hkv * a.T) return;
+  const int64_t bh = row / a.T, t = row % a.T;
+  const bool is_v = blockIdx.y == 1;
+  float x0, x1;
+  if (!is_v) dequant_pair<KB>(a.kq, a.ks, a.kz, false, bh, a.cap, t, lane, x0, x1);
+  else dequant_pair<VB>(a.vq, a.vs, a.vz, true, bh, a.cap, t, lane, x0, x1);
+  uint16_t* o = (is_v ? a.v_out : a.k_out) + row * HEAD_DIM + 2 * lane;
+  *(uint32_t*)o = (uint32_t)float_to_bf16_bits(x0) | ((uint32_t)float_to_bf16_bits(x1) << 16);
+}
+
+hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stream) {
+  const int64_t rows = (int64_t)a.B * a.Hkv * a.T;
+  const dim3 grid((unsigned)((rows + 3) / 4), 2), block(256);
+  if (kb == 8 && vb == 8) hipLaunchKernelGGL((dequant_kernel<8, 8>), grid, block, 0, stream, a);
+  else if (kb == 8 && vb == 4) hipLaunchKernelGGL((dequant_kernel<8, 4>), grid, block, 0, stream, a);
+  else if (kb == 4 && vb == 8) hipLaunchKernelGGL((dequant_kernel<4, 8>), grid, block, 0, stream, a);
+  else if (kb == FMT_A8 && vb == FMT_A4) hipLaunchKernelGGL((dequant_kernel<FMT_A8, FMT_A4>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((dequant_kernel<4, 4>), grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
 // Zero a word range (graph-safe replacement for hipMemsetAsync).
 __global__ void fill_zero_kernel(uint32_t* p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

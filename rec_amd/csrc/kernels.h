@@ -62,6 +62,20 @@ struct PrefillArgs {
   int64_t k_sb, k_sh, v_sb, v_sh;
 };
 
+// Cache rows [0, T) dequantized to bf16 (B, Hkv, T, 128) tensors.
+struct DequantArgs {
+  const void* kq;
+  const uint16_t* ks;
+  const uint16_t* kz;
+  const void* vq;
+  const uint16_t* vs;
+  const uint16_t* vz;
+  int B, Hkv;
+  int64_t T, cap;
+  uint16_t* k_out;
+  uint16_t* v_out;
+};
+
 // int4 group-64 GEMV: repack of an MLX affine matrix, then y = x Wᵀ.
 struct Q4PackArgs {
   const uint32_t* w;        // [N][K/8] MLX words
@@ -91,6 +105,7 @@ hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stream);
 hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream);
 hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream);
 size_t q4_gemv_lds_bytes(int M, int64_t K);

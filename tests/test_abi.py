@@ -170,3 +170,23 @@ def test_q4_validation(lib):
     assert _q4_gemv(lib, M=2, xs=260) == _lib.REC_EALIGN
     assert _q4_gemv(lib, M=2, xs=128) == _lib.REC_EINVAL
     assert _q4_gemv(lib, M=8, K=12288, xs=12288) == _lib.REC_EUNSUPPORTED
+
+
+def _dequant(lib, **kw):
+    a = dict(kb=8, vb=8, B=1, H=2, T=10, cap=64, ko=16, vo=16)
+    a.update(kw)
+    return lib.rec_kv_dequant_bf16(a["kb"], 16, 16, 16, a["vb"], 16, 16, 16, a["B"], a["H"], a["T"], a["cap"],
+                                   a["ko"], a["vo"], None)
+
+
+def test_dequant_validation(lib):
+    assert _dequant(lib, kb=5) == _lib.REC_EINVAL
+    assert _dequant(lib, kb=_lib.REC_AFFINE8, vb=4) == _lib.REC_EUNSUPPORTED
+    assert _dequant(lib, cap=100) == _lib.REC_EINVAL
+    assert _dequant(lib, T=65) == _lib.REC_ECAPACITY
+    assert _dequant(lib, T=-1) == _lib.REC_EINVAL
+    assert _dequant(lib, H=0) == _lib.REC_EINVAL
+    assert _dequant(lib, ko=None) == _lib.REC_EINVAL
+    assert _dequant(lib, vo=8) == _lib.REC_EALIGN
+    assert _dequant(lib, T=0) == _lib.REC_OK  # nothing to do, nothing launched
+    assert _dequant(lib, kb=_lib.REC_AFFINE8, vb=_lib.REC_AFFINE4, T=0) == _lib.REC_OK
