@@ -13,7 +13,7 @@
 // Each workgroup writes one partial (m, l, acc) per query head; a second
 // kernel merges the splits, one workgroup per query head.
 //
-// Work decomposition.  Grid (splits, Hkv, B), 256 threads = 4 wavefronts.  A
+// Work decomposition.  Grid (splits, Hkv, B), 4 wavefronts (long uint4 splits: 8).  A
 // workgroup owns one KV head and a contiguous token range; its waves take
 // 32-token chunks in turn, loading chunk i+1 while computing chunk i.  All G <= 8 query heads of the KV head share every
 // K/V byte loaded (GQA), so a K/V byte is read from HBM exactly once.
@@ -42,18 +42,26 @@ namespace rec {
 
 
 constexpr int MAX_SPLITS = DECODE_MAX_SPLITS;
-constexpr int WAVES = 4;  // wavefronts per workgroup
-constexpr int THREADS = 64 * WAVES;
 constexpr float Q16 = 32512.0f;  // int16 query range: hi, lo stay inside int8
 
-// LDS layout (bytes)
-constexpr int LDS_QOP = 0;                                 // up to 4 operands x 64 lanes x 16 B
-constexpr int LDS_QSC = 4096;                              // 8 floats: per-head query scale
-constexpr int LDS_QSUM = LDS_QSC + 32;                     // 8 x 4 ints: per-group query sums (int4 K)
-constexpr int LDS_PART = 4352;                             // wave partials: 4 x 8 x 128 floats
-constexpr int LDS_PSTAT = LDS_PART + WAVES * 8 * 128 * 4;  // 4 x 8 x (m, l)
-constexpr int LDS_META = LDS_PSTAT + WAVES * 8 * 8;       // int4: per wave [4 arrays][256 B] of one block
-constexpr int LDS_BYTES = LDS_META + WAVES * 1024;
+// Wavefronts per workgroup: four; uint4 K/V with long splits (>= 32 chunks,
+// e.g. 131K tokens over 64 splits): eight, two per SIMD, because the nibble
+// unpacking makes a 32-token chunk twice the VALU work per byte of int8 and a
+// second wave per SIMD hides it (measured 3% faster at 131K tokens, slower
+// at 32K and for the other formats).
+constexpr int UINT4_WIDE_CHUNKS = 32;
+
+// LDS layout (bytes) for W wavefronts
+constexpr int LDS_QOP = 0;              // up to 4 operands x 64 lanes x 16 B
+constexpr int LDS_QSC = 4096;           // 8 floats: per-head query scale
+constexpr int LDS_QSUM = LDS_QSC + 32;  // 8 x 4 ints: per-group query sums (int4 K)
+template <int W>
+struct Lds {
+  static constexpr int part = 4352;                  // wave partials: W x 8 x 128 floats
+  static constexpr int pstat = part + W * 8 * 128 * 4;  // W x 8 x (m, l)
+  static constexpr int meta = pstat + W * 8 * 8;        // int4: per wave [4 arrays][256 B] of one block
+  static constexpr int bytes = meta + W * 1024;
+};
 
 // Order in which widen_u4() lays out 16 packed nibbles (8 bytes): unpacked byte
 // j holds element perm16(j) of the 16.
@@ -96,13 +104,13 @@ __device__ __forceinline__ void q_raw_to_float(const v4i& r, int dt, float x[4])
 // Quantize this workgroup's G query rows to int16 (hi/lo int8) and lay them out
 // as the B operands of the Q·Kᵀ MFMAs.  Thread (hh, d0) brings dims d0..d0+3 of
 // head hh, already scaled (zero for hh >= G).
-template <int KB>
+template <int KB, int NT>
 __device__ void prepare_query(const float x[4], char* smem, int tid) {
   int8_t* qop = (int8_t*)(smem + LDS_QOP);
   float* qsc = (float*)(smem + LDS_QSC);
   int* qsum = (int*)(smem + LDS_QSUM);
   if constexpr (KB == 4) {
-    for (int i = tid; i < 1024; i += THREADS) ((int*)qop)[i] = 0;
+    for (int i = tid; i < 1024; i += NT) ((int*)qop)[i] = 0;
     __syncthreads();
   }
   if (tid >= 256) return;  // threads (hh, d0) cover 8 heads x 128 dims
@@ -484,9 +492,10 @@ struct Depth {
   static constexpr int value = 2;
 };
 
-template <int KB, int VB>
-__global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[LDS_BYTES];
+template <int KB, int VB, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) {
+  using LD = Lds<WAVES>;
+  __shared__ __attribute__((aligned(16))) char smem[LD::bytes];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, kg = lane >> 4;
@@ -559,7 +568,7 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
     const float mul = hh < a.G ? a.q_mul : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] *= mul;
-    prepare_query<KB>(x, smem, tid);
+    prepare_query<KB, 64 * WAVES>(x, smem, tid);
   }
   __syncthreads();
 
@@ -605,7 +614,7 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
       load_chunk<KB, VB>(buf[(j + NBUF - 1) % NBUF], R, lo, i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1));
       if (i < n_w)
         process_chunk<KB, VB>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane,
-                              smem + LDS_META + wave * 1024);
+                              smem + LD::meta + wave * 1024);
     }
   }
 
@@ -622,8 +631,8 @@ __global__ __launch_bounds__(THREADS) void decode_kernel(const DecodeArgs a) {
       for (int nn = 0; nn < 4; ++nn) st.acc[4 * g + nn] += vb;
     }
   }
-  float* part = (float*)(smem + LDS_PART);
-  float* pstat = (float*)(smem + LDS_PSTAT);
+  float* part = (float*)(smem + LD::part);
+  float* pstat = (float*)(smem + LD::pstat);
   if (c < 8 && c < a.G) {
 #pragma unroll
     for (int n = 0; n < 8; ++n)
@@ -739,13 +748,18 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   }
 }
 
+template <int KB, int VB, int W>
+static void launch_partial(const DecodeArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_kernel<KB, VB, W>), dim3(a.S, a.Hkv, a.B), dim3(64 * W), 0, stream, a);
+}
+
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream) {
-  const dim3 grid(a.S, a.Hkv, a.B), block(THREADS);
-  if (kb == 8 && vb == 8) hipLaunchKernelGGL((decode_kernel<8, 8>), grid, block, 0, stream, a);
-  else if (kb == 8 && vb == 4) hipLaunchKernelGGL((decode_kernel<8, 4>), grid, block, 0, stream, a);
-  else if (kb == 4 && vb == 8) hipLaunchKernelGGL((decode_kernel<4, 8>), grid, block, 0, stream, a);
-  else if (kb == FMT_A8 && vb == FMT_A4) hipLaunchKernelGGL((decode_kernel<FMT_A8, FMT_A4>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((decode_kernel<4, 4>), grid, block, 0, stream, a);
+  if (kb == 8 && vb == 8) launch_partial<8, 8, 4>(a, stream);
+  else if (kb == 8 && vb == 4) launch_partial<8, 4, 4>(a, stream);
+  else if (kb == 4 && vb == 8) launch_partial<4, 8, 4>(a, stream);
+  else if (kb == FMT_A8 && vb == FMT_A4) launch_partial<FMT_A8, FMT_A4, 4>(a, stream);
+  else if (a.span / CH >= UINT4_WIDE_CHUNKS) launch_partial<4, 4, 8>(a, stream);
+  else launch_partial<4, 4, 4>(a, stream);
   return hipGetLastError();
 }
 

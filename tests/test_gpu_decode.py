@@ -73,6 +73,10 @@ DECODE_CASES = [
     (1, 32, 4, 2048, 4, 8, False, 7),
     (1, 8, 8, 333, 4, 4, True, 2),
     (3, 24, 4, 65, 8, 4, True, None),
+    # uint4 splits of >= 32 chunks run eight wavefronts per workgroup
+    (1, 32, 4, 5000, 4, 4, True, 2),
+    (2, 16, 2, 3000, 4, 4, False, 1),
+    (1, 8, 1, 1100, 4, 4, True, 1),
 ]
 
 
@@ -93,19 +97,21 @@ def test_decode_matches_oracle(gpu, case):
     assert_close(f32(out), ref, f"case {case}")
 
 
-@pytest.mark.parametrize("bits", BITS)
-def test_fused_decode_steps(gpu, bits):
-    """append-then-attend in one launch, several steps, vs the oracle."""
-    B, Hq, Hkv, T0 = 1, 32, 4, 511
+@pytest.mark.parametrize("bits,T0,splits", [(b, 511, None) for b in BITS] + [((4, 4), 2111, 2)],
+                         ids=lambda x: str(x))
+def test_fused_decode_steps(gpu, bits, T0, splits):
+    """append-then-attend in one launch, several steps, vs the oracle (the
+    last case: uint4 splits long enough for eight wavefronts)."""
+    B, Hq, Hkv = 1, 32, 4
     cache = QuantizedKVCache(32, *bits)
     k0, v0 = fill(cache, B, Hkv, T0, seed=5)
     ks, vs = [k0], [v0]
     sinks = torch.randn(Hq, device="cuda")
-    for step in range(4):  # crosses the 512-token boundary and an odd/even pair
+    for step in range(4):  # crosses a 32-token block boundary and an odd/even pair
         q = synthetic.query(B, Hq, 1, seed=50 + step)
         kn = synthetic.kv((B, Hkv, 1, 128), 60 + step)
         vn = synthetic.kv((B, Hkv, 1, 128), 70 + step)
-        out = attend(q, kn, vn, cache, SCALE, None, sinks, out_dtype=torch.float32)
+        out = attend(q, kn, vn, cache, SCALE, None, sinks, out_dtype=torch.float32, splits=splits)
         ks.append(f32(kn))
         vs.append(f32(vn))
         K, V = np.concatenate(ks, 2), np.concatenate(vs, 2)
