@@ -138,6 +138,44 @@ class DecodeWorkload:
         c.offset = T
         return T
 
+    def attend_only(self, s):
+        """rec_decode_attn over the cached tokens, no append (the attention half
+        of an unfused step); the offset does not move."""
+        from rec_amd import _lib
+
+        c = self.caches[s % self.R]
+        q = self.pool[s % len(self.pool)][0]
+        kc, ks, kz = c.keys
+        vc, vs, vz = c.values
+        kcode, vcode = (_lib.REC_AFFINE8, _lib.REC_AFFINE4) if self.bits == AFFINE else (self.bits, self.bits)
+        rc = self.lib.rec_decode_attn(
+            q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
+            kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
+            vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
+            self.sinks.data_ptr(), SCALE, 1, HQ, HKV, D, c.offset, c.capacity, self.splits,
+            self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), self.torch.cuda.current_stream().cuda_stream,
+        )
+        _lib.check(rc, "decode attention")
+
+    def append_only(self, s):
+        """rec_kv_append of one token at the last cached position (the append
+        half of an unfused step); the offset does not move."""
+        from rec_amd import _lib
+
+        c = self.caches[s % self.R]
+        _, kn, vn = self.pool[s % len(self.pool)]
+        kc, ks, kz = c.keys
+        vc, vs, vz = c.values
+        kcode, vcode = (_lib.REC_AFFINE8, _lib.REC_AFFINE4) if self.bits == AFFINE else (self.bits, self.bits)
+        rc = self.lib.rec_kv_append(
+            kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), kn.stride(2),
+            vn.stride(0), vn.stride(1), vn.stride(2),
+            kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
+            vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
+            1, HKV, 1, D, c.offset - 1, c.capacity, self.torch.cuda.current_stream().cuda_stream,
+        )
+        _lib.check(rc, "append")
+
 
 def _replay_timed(torch, graph, n):
     """Replay a captured graph once between synchronisations; ms per launch."""
@@ -150,7 +188,7 @@ def _replay_timed(torch, graph, n):
     return e0.elapsed_time(e1) / n
 
 
-def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01):
+def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, parts=10):
     import torch
 
     total = warmup + 2 * steps
@@ -160,19 +198,41 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01):
     for s in range(warmup):
         w.step(s)
     torch.cuda.synchronize()
-    # K whole steps (attention kernel + merge kernel) in one graph
-    g_step, step_T = torch.cuda.CUDAGraph(), []
-    with torch.cuda.graph(g_step):
-        for s in range(warmup, warmup + steps):
-            step_T.append(w.step(s))
+    # K whole steps (attention kernel + merge kernel) in `parts` graphs of
+    # about K / parts steps each, timed one replay apiece: the per-step time is
+    # the total over K, the spread that of the parts' per-step means
+    parts = max(1, min(parts, steps))
+    bounds = [warmup + steps * i // parts for i in range(parts + 1)]
+    g_steps, step_T = [], []
+    for i in range(parts):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for s in range(bounds[i], bounds[i + 1]):
+                step_T.append(w.step(s))
+        g_steps.append((g, bounds[i + 1] - bounds[i]))
     # K launches of the attention kernel alone, the dominant kernel
     g_kern, kern_T = torch.cuda.CUDAGraph(), []
     with torch.cuda.graph(g_kern):
         for s in range(warmup + steps, total):
             kern_T.append(w.step(s, partial_only=True))
-    ms_per_step = _replay_timed(torch, g_step, steps)
+    # the unfused halves of a step, each K times: attention over the cached
+    # tokens (two launches) and the append of one token (one launch)
+    g_att, g_app = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_att):
+        for s in range(steps):
+            w.attend_only(s)
+    with torch.cuda.graph(g_app):
+        for s in range(steps):
+            w.append_only(s)
+    part_ms = [_replay_timed(torch, g, n) for g, n in g_steps]
+    ms_per_step = sum(m * n for m, (_, n) in zip(part_ms, g_steps)) / steps
     kernel_ms = _replay_timed(torch, g_kern, steps)
-    log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step; attention kernel {kernel_ms * 1e3:.2f} us")
+    att_ms = _replay_timed(torch, g_att, steps)
+    app_ms = _replay_timed(torch, g_app, steps)
+    p10, p50, p90 = (float(np.percentile(part_ms, p)) for p in (10, 50, 90))
+    log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step (parts p10/p50/p90 {p10 * 1e3:.2f}/"
+        f"{p50 * 1e3:.2f}/{p90 * 1e3:.2f}); attention kernel {kernel_ms * 1e3:.2f} us; unfused: attention "
+        f"{att_ms * 1e3:.2f} us + append {app_ms * 1e3:.2f} us")
     bytes_step = float(np.mean([step_bytes(t, k_bits=bits, v_bits=bits) for t in step_T]))
     bytes_kernel = float(np.mean([step_bytes(t, k_bits=bits, v_bits=bits, output=False) for t in kern_T]))
     res = dict(
@@ -186,8 +246,11 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01):
         kernel_gbs=bytes_kernel / (kernel_ms * 1e-3) / 1e9,
         bytes_per_launch=bytes_kernel,
         cache_bytes=sum(c.nbytes for c in w.caches),
+        step_us_p10_p50_p90=[round(p10 * 1e3, 3), round(p50 * 1e3, 3), round(p90 * 1e3, 3)],
+        unfused_attention_us=att_ms * 1e3,
+        unfused_append_us=app_ms * 1e3,
     )
-    del g_step, g_kern, w
+    del g_steps, g_kern, g_att, g_app, w
     torch.cuda.empty_cache()
     return res
 
@@ -455,6 +518,17 @@ def cpu_baseline(T, seed, budget_s=10.0):
     )
 
 
+def _step_detail(r):
+    """Spread of the fused step over the timed graph parts, and the two halves
+    of an unfused step timed alone (attention = partial + merge launches;
+    append = one rec_kv_append launch)."""
+    return {
+        "us_per_step_p10_p50_p90": r["step_us_p10_p50_p90"],
+        "unfused_attention_us": round(r["unfused_attention_us"], 3),
+        "unfused_append_us": round(r["unfused_append_us"], 3),
+    }
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -572,9 +646,10 @@ def main(argv=None):
             "kv_format": "int8 symmetric, fp16 scale per (token, head); 1% outlier channels x8",
             "cache_instances": r32["instances"],
             "cache_bytes_total": r32["cache_bytes"],
-            "timing": "K steps in one HIP graph replay, HIP events",
+            "timing": "K steps as 10 HIP graphs of K/10 steps, one replay each between HIP events",
         },
         "us_per_step": round(r32["us_per_step"], 3),
+        **_step_detail(r32),
         "frac_of_peak": round(r32["gbs"] / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
@@ -594,6 +669,7 @@ def main(argv=None):
         result["context_252k"] = {
             "context": 258048,
             "us_per_step": round(r252["us_per_step"], 3),
+            **_step_detail(r252),
             "gbs": round(r252["gbs"], 2),
             "frac_of_peak": round(r252["gbs"] / HBM_PEAK_GBS, 4),
             "kernel_us": round(r252["kernel_us"], 3),
@@ -607,6 +683,7 @@ def main(argv=None):
             "context": 131072,
             "kv_format": "uint4 asymmetric, fp16 scale + zero-point per 32 dims; 5% Student-t(3) channels",
             "us_per_step": round(r4["us_per_step"], 3),
+            **_step_detail(r4),
             "gbs": round(r4["gbs"], 2),
             "frac_of_peak": round(r4["gbs"] / HBM_PEAK_GBS, 4),
             "kernel_us": round(r4["kernel_us"], 3),
@@ -620,6 +697,7 @@ def main(argv=None):
             "context": 32768,
             "kv_format": "MLX-style affine group 64: 8-bit K, 4-bit V, bf16 scale + bias (the reference's default)",
             "us_per_step": round(raf["us_per_step"], 3),
+            **_step_detail(raf),
             "gbs": round(raf["gbs"], 2),
             "frac_of_peak": round(raf["gbs"] / HBM_PEAK_GBS, 4),
             "kernel_us": round(raf["kernel_us"], 3),
