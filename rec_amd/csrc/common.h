@@ -109,14 +109,90 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
   return r;
 }
 
-__device__ __forceinline__ float shfl_xor_f(float x, int m) {
-  return __shfl_xor(x, m, 64);
+// ---- cross-lane combines without LDS round trips ----
+// DPP moves inside rows of 16 lanes; v_permlane16_swap / v_permlane32_swap
+// (gfx950) across rows and halves.  A swap of x with itself returns
+// {x[l & ~m], x[l | m]} (m = 16 or 32), so combining the pair gives every lane
+// the xor-m butterfly of x, the same value in both partners.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+constexpr int DPP_XOR1 = 0xb1;         // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4e;         // quad_perm [2, 3, 0, 1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <-> 7 - i in each 8
+constexpr int DPP_MIRROR = 0x140;       // lane i <-> 15 - i in each 16
+constexpr int DPP_ROR8 = 0x128;         // lane i <-> i ^ 8 in each 16
+
+__device__ __forceinline__ void pair16(float x, float& lo, float& hi) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t a = r[0], b = r[1];  // copies: a bit_cast of a vector subscript reads element 0
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ void pair32(float x, float& lo, float& hi) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t a = r[0], b = r[1];
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  float a, b;
+  pair16(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  float a, b;
+  pair32(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  float a, b;
+  pair16(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  float a, b;
+  pair32(x, a, b);
+  return fmaxf(a, b);
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
-  return x;
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
+}
+
+// max / min / sum over each group of 8 or 16 lanes (every lane receiving its
+// group's result), and over the 64 lanes
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_f<DPP_XOR1>(x));
+  x = fmaxf(x, dpp_f<DPP_XOR2>(x));
+  x = fmaxf(x, dpp_f<DPP_HALF_MIRROR>(x));
+  return fmaxf(x, dpp_f<DPP_MIRROR>(x));
+}
+__device__ __forceinline__ float row16_min(float x) {
+  x = fminf(x, dpp_f<DPP_XOR1>(x));
+  x = fminf(x, dpp_f<DPP_XOR2>(x));
+  x = fminf(x, dpp_f<DPP_HALF_MIRROR>(x));
+  return fminf(x, dpp_f<DPP_MIRROR>(x));
+}
+__device__ __forceinline__ int group8_sum(int x) {
+  x += dpp_i<DPP_XOR1>(x);
+  x += dpp_i<DPP_XOR2>(x);
+  return x + dpp_i<DPP_HALF_MIRROR>(x);
+}
+__device__ __forceinline__ float group8_sum(float x) {
+  x += dpp_f<DPP_XOR1>(x);
+  x += dpp_f<DPP_XOR2>(x);
+  return x + dpp_f<DPP_HALF_MIRROR>(x);
+}
+__device__ __forceinline__ float wave_max(float x) { return max_xor32(max_xor16(row16_max(x))); }
+__device__ __forceinline__ float wave_sum(float x) {
+  x = group8_sum(x);
+  x += dpp_f<DPP_MIRROR>(x);
+  return sum_xor32(sum_xor16(x));
 }
 
 // Four signed int8 codes -> two packed fp16 pairs, exactly.

@@ -116,8 +116,7 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
   if (tid >= 256) return;  // threads (hh, d0) cover 8 heads x 128 dims
   const int hh = tid >> 5, d0 = (tid & 31) * 4;
   float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-#pragma unroll
-  for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, 64));
+  amax = max_xor16(row16_max(amax));  // the 32 lanes of head hh
   const float inv = amax > 0.f ? Q16 / amax : 0.f;
   int gsum = 0;
 #pragma unroll
@@ -141,8 +140,7 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
   }
   if constexpr (KB == 4 || KB == FMT_A8) {
     // group of 32 dims = 8 consecutive threads
-#pragma unroll
-    for (int m = 1; m < 8; m <<= 1) gsum += __shfl_xor(gsum, m, 64);
+    gsum = group8_sum(gsum);
     if ((tid & 7) == 0) qsum[hh * 4 + ((tid & 31) >> 3)] = gsum;
   }
   if ((tid & 31) == 0) qsc[hh] = amax / Q16;
@@ -374,8 +372,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
   cmax *= qsc;  // qsc > 0
   if (__ballot(cmax > st.m)) {
-    cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
-    cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
+    cmax = max_xor32(max_xor16(cmax));
     const float m_new = fmaxf(st.m, cmax);
     const float factor = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first chunk, 1 if unchanged
     st.l *= factor;
@@ -619,14 +616,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
   }
 
   // ---------------- wave partial -> LDS ----------------
-  st.l += shfl_xor_f(st.l, 16);
-  st.l += shfl_xor_f(st.l, 32);
+  st.l = sum_xor32(sum_xor16(st.l));
   if constexpr (VB == FMT_A4) {  // the bias terms join every dim of their group
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       float vb = st.vb[g];
-      vb += shfl_xor_f(vb, 16);
-      vb += shfl_xor_f(vb, 32);
+      vb = sum_xor32(sum_xor16(vb));
 #pragma unroll
       for (int nn = 0; nn < 4; ++nn) st.acc[4 * g + nn] += vb;
     }
@@ -731,19 +726,21 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
     lw += w * ls[k];
     if (lane + 64 * k < 8 * PER) wts[lane + 64 * k] = w;
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) lw += __shfl_xor(lw, m, 64);
+  lw = wave_sum(lw);
   __syncthreads();
   v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < PER; ++i) acc += wts[sg + 8 * i] * v[i];
+  // sum over the eight split groups sg (lanes d4 + 8 sg): xor 8, 16, 32
 #pragma unroll
-  for (int m = 8; m < 64; m <<= 1)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], m, 64);
+  for (int e = 0; e < 4; ++e) {
+    float t = acc[e];
+    t += dpp_f<DPP_ROR8>(t);
+    acc[e] = sum_xor32(sum_xor16(t));
+  }
   if (sg == 0) {
     const float L = sink != NEG_INF ? lw + __builtin_amdgcn_exp2f(sink - M) : lw;
-    const v4f o = L > 0.f ? acc / L : acc;
+    const v4f o = L > 0.f ? acc * (1.f / L) : acc;
     *(v4f*)(a.out + ((int64_t)b * a.Hq + hq) * HEAD_DIM + 32 * qd + 4 * d4) = o;
   }
 }

@@ -101,8 +101,7 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
 
   // ---------------- online softmax ----------------
   float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-  cmax = fmaxf(cmax, shfl_xor_f(cmax, 16));
-  cmax = fmaxf(cmax, shfl_xor_f(cmax, 32));
+  cmax = max_xor32(max_xor16(cmax));
   const float m_new = fmaxf(st.m, cmax);
   if (__ballot(m_new > st.m)) {
     const float factor = __builtin_amdgcn_exp2f(st.m - m_new);
@@ -238,8 +237,7 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
   }
 
   // ---------------- wave partial -> LDS (columns c and c+8 summed) ----------------
-  st.l += shfl_xor_f(st.l, 16);
-  st.l += shfl_xor_f(st.l, 32);
+  st.l = sum_xor32(sum_xor16(st.l));
   float* part = (float*)(smem + BL_PART);
   float* pstat = (float*)(smem + BL_PSTAT);
 #pragma unroll

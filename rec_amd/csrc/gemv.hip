@@ -152,9 +152,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs
       sum = ((bf16_lo(d0) + bf16_hi(d0)) + (bf16_lo(d1) + bf16_hi(d1))) +
             ((bf16_lo(d2) + bf16_hi(d2)) + (bf16_lo(d3) + bf16_hi(d3)));
     }
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
+    sum = group8_sum(sum);
     if (t < nrec && (t & 7) == 0) {
       const int gs = (t >> 3) & 1, rest = t >> 4;
       xs[(rest / S) * G + 2 * (rest % S) + gs] = sum;

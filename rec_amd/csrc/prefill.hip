@@ -238,8 +238,7 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
     // a row's max moves iff one of its four lanes' maxima exceeds the running max
     if (__ballot(cmax > m_run[rt])) {
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      cmax = max_xor32(max_xor16(cmax));
       const float m_new = fmaxf(m_run[rt], cmax);
       const float factor = m_new == NEG_INF ? 1.f : __builtin_amdgcn_exp2f(m_run[rt] - m_new);
       l_run[rt] *= factor;
@@ -379,8 +378,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     float l = l_run[rt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = sum_xor32(sum_xor16(l));
     float M = m_run[rt];
     if (a.sinks != nullptr) {
       const float sink = a.sinks[hq] * LOG2E;

@@ -61,12 +61,7 @@ __device__ __forceinline__ void quantize_i8_pair(float x0, float x1, int& q0, in
 // uint4 asymmetric per 32-dim group (16 lanes).  Lane l owns dims 2l, 2l+1.
 __device__ __forceinline__ void quantize_u4_pair(float x0, float x1, int& q0, int& q1, uint16_t& sbits,
                                                  uint16_t& zbits) {
-  float mn = fminf(x0, x1), mx = fmaxf(x0, x1);
-#pragma unroll
-  for (int m = 1; m < 16; m <<= 1) {
-    mn = fminf(mn, __shfl_xor(mn, m, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-  }
+  float mn = row16_min(fminf(x0, x1)), mx = row16_max(fmaxf(x0, x1));
   mn = fminf(mn, 0.0f);
   mx = fmaxf(mx, 0.0f);
   sbits = half_bits_saturate((mx - mn) / 15.0f);
@@ -93,12 +88,11 @@ template <int BITS>
 __device__ __forceinline__ void quantize_affine_pair(float x0, float x1, int& q0, int& q1, uint16_t& sbits,
                                                      uint16_t& bbits) {
   constexpr float n_bins = (float)((1 << BITS) - 1);
-  float mn = fminf(x0, x1), mx = fmaxf(x0, x1);
-#pragma unroll
-  for (int m = 1; m < 32; m <<= 1) {
-    mn = fminf(mn, __shfl_xor(mn, m, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-  }
+  float a, b;
+  float mn = row16_min(fminf(x0, x1)), mx = row16_max(fmaxf(x0, x1));
+  pair16(mn, a, b);  // the two rows of the 32-lane group
+  mn = fminf(a, b);
+  mx = max_xor16(mx);
   mx = fmaxf(mx, 0.0f);
   float scale = fmaxf((mx - mn) / n_bins, 1e-7f);
   const bool side = fabsf(mn) > fabsf(mx);
