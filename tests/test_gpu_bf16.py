@@ -31,6 +31,9 @@ CASES = [
     (1, 4, 1, 1, torch.bfloat16, True, None),
     (3, 24, 4, 65, torch.bfloat16, True, 1),
     (1, 8, 8, 2049, torch.float16, False, 3),
+    # long splits (79 and 66 chunks)
+    (1, 32, 4, 5000, torch.bfloat16, True, 2),
+    (1, 8, 1, 2100, torch.float16, False, 1),
 ]
 
 
@@ -75,33 +78,40 @@ def test_fixed_kv_cache_prefill_then_fused_decode(gpu):
     assert torch.count_nonzero(store.layer(0)) == 0  # the other layer is untouched
 
 
-def test_fused_equals_write_then_attend(gpu):
-    B, Hq, Hkv, P = 2, 16, 2, 333
+@pytest.mark.parametrize("P,cap,splits", [(333, 1024, None), (2500, 4096, 1)])
+def test_fused_equals_write_then_attend(gpu, P, cap, splits):
+    """The fused write + attend launch equals a write then an attend: bit for
+    bit where both partition the tokens alike; the second case (one split of
+    78 chunks) partitions them differently, so it agrees to fp32 rounding."""
+    B, Hq, Hkv = 2, 16, 2
     outs = []
     for fused in (True, False):
-        store = KVStorage(1, 1024, Hkv, batch=B)
+        store = KVStorage(1, cap, Hkv, batch=B)
         cache = FixedKVCache(store, 0)
         k = synthetic.kv((B, Hkv, P + 1, 128), 51, dtype=torch.bfloat16)
         v = synthetic.kv((B, Hkv, P + 1, 128), 52, dtype=torch.bfloat16)
         cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
         q = synthetic.query(B, Hq, 1, 53, dtype=torch.bfloat16)
         outs.append(attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, None, None, out_dtype=torch.float32,
-                           fused=fused))
+                           fused=fused, splits=splits))
     torch.cuda.synchronize()
-    torch.testing.assert_close(outs[0], outs[1], rtol=0, atol=0)
+    tol = 0 if splits is None else 1e-5
+    torch.testing.assert_close(outs[0], outs[1], rtol=tol, atol=tol)
 
 
-def test_long_context_bf16(gpu):
-    """32K tokens: the default split schedule over a long cache."""
+@pytest.mark.parametrize("splits", [None, 8])
+def test_long_context_bf16(gpu, splits):
+    """32K tokens: the default split schedule over a long cache, and 8 splits
+    of 4096 tokens."""
     B, Hq, Hkv, T = 1, 32, 4, 32768
     k = synthetic.kv((B, Hkv, T, 128), 61, kind="outliers", frac=0.01, dtype=torch.bfloat16)
     v = synthetic.kv((B, Hkv, T, 128), 62, kind="outliers", frac=0.01, dtype=torch.bfloat16)
     q = synthetic.query(B, Hq, 1, 63, dtype=torch.bfloat16)
     sinks = torch.randn(Hq, device="cuda")
-    out = scaled_dot_product_attention(q, k, v, SCALE, None, sinks, out_dtype=torch.float32)
+    out = scaled_dot_product_attention(q, k, v, SCALE, None, sinks, out_dtype=torch.float32, splits=splits)
     torch.cuda.synchronize()
     ref = O.attention(f32(q), f32(k), f32(v), SCALE, sinks=f32(sinks))
-    assert_close(f32(out), ref, "32K bf16")
+    assert_close(f32(out), ref, f"32K bf16, splits {splits}")
 
 
 def test_fused_decode_in_hip_graph(gpu):
