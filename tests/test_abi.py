@@ -190,3 +190,9 @@ def test_dequant_validation(lib):
     assert _dequant(lib, vo=8) == _lib.REC_EALIGN
     assert _dequant(lib, T=0) == _lib.REC_OK  # nothing to do, nothing launched
     assert _dequant(lib, kb=_lib.REC_AFFINE8, vb=_lib.REC_AFFINE4, T=0) == _lib.REC_OK
+
+
+def test_capacity_bound(lib):
+    """2^24 tokens per KV head is the largest cache the decode accepts."""
+    assert _decode(lib, cap=(1 << 24) + 32, T=100) == _lib.REC_EUNSUPPORTED
+    assert "16M" in _lib.last_error()
