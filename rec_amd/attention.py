@@ -2,8 +2,10 @@
 
 * :func:`quantized_attention_with_sinks` keeps the signature of
   engine/src/rec_mlx/model.py:108-110 and runs the gfx950 split-K decode kernel
-  (``rec_decode_attn``) for one query token, the chunked prefill kernel
-  (``rec_prefill_attn``, model.py:191-203) for several.
+  (``rec_decode_attn``) for one query token, the chunked prefill kernel for
+  several (model.py:191-203: ``rec_prefill_attn`` reads an int8 cache
+  directly; other formats are dequantized to bf16 first, ``rec_kv_dequant_bf16``
+  then ``rec_prefill_bf16``).
 * :func:`attend` mirrors the cache/attention part of ``Attention.__call__``
   (model.py:177-203): append first, then attend, decode for ``L == 1`` and
   chunked prefill for ``L > 1``.  For a
@@ -29,10 +31,9 @@ _workspaces = {}
 
 
 def workspace(device: torch.device, B: int, Hkv: int, splits: int, stream: int) -> torch.Tensor:
-    """A zero-initialised decode workspace for (device, stream), grown on demand.
-
-    Decode launches leave its counters at zero, so it is reused as is.  One
-    workspace per stream: launches on one stream are ordered.
+    """The decode workspace (split partials) for (device, stream), grown on
+    demand.  One workspace per stream: launches on one stream are ordered, so
+    one step's partials are merged before the next step overwrites them.
     """
     lib = _lib.load()
     need = lib.rec_decode_workspace_bytes(B, Hkv, splits)
