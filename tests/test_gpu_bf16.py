@@ -212,6 +212,8 @@ PREFILL_CASES = [
     (1, 8, 1, 0, 77, torch.bfloat16, False, True),
     (2, 16, 2, 130, 64, torch.float16, True, True),
     (1, 32, 4, 500, 129, torch.bfloat16, True, False),
+    (3, 4, 4, 40, 33, torch.bfloat16, True, True),    # one query head per KV head
+    (1, 12, 4, 256, 96, torch.float16, False, True),  # three per KV head
 ]
 
 

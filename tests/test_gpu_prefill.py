@@ -25,6 +25,9 @@ CASES = [
     (2, 16, 2, 300, 64, False, True, torch.float16),
     (1, 8, 2, 33, 31, True, True, torch.bfloat16),
     (1, 6, 3, 64, 96, True, False, torch.float16),
+    (3, 4, 4, 40, 33, True, True, torch.bfloat16),    # one query head per KV head, three sequences
+    (1, 12, 4, 256, 96, True, True, torch.float16),   # three per KV head
+    (2, 8, 1, 31, 1, True, True, torch.bfloat16),     # a one-token chunk (attend takes the decode path)
 ]
 
 

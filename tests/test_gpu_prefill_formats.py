@@ -71,6 +71,7 @@ CASES = [
     ("u4_u4", 1, 32, 4, 300, 129, True, True, torch.bfloat16),
     ("i8_u4", 1, 8, 2, 33, 31, True, False, torch.float16),
     ("u4_i8", 2, 6, 3, 64, 96, False, True, torch.bfloat16),
+    ("affine", 3, 4, 4, 40, 33, True, True, torch.bfloat16),
 ]
 
 
