@@ -210,3 +210,50 @@ def test_partial_then_merge_equals_one_call(gpu):
             _lib.check(lib.rec_decode_append_attn(*args), "append_attn")
         outs.append(out.clone())
     torch.testing.assert_close(outs[0], outs[1], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "affine"])
+def test_fused_decode_steps_in_hip_graph(gpu, fmt):
+    """Four fused decode steps (append + attention + merge) captured in one HIP
+    graph and replayed three times, with eager work between the replays: every
+    replay's outputs and the cache bytes equal the eager run's, bit for bit."""
+    from rec_amd import MixedQuantizedKVCache, to_logical
+
+    B, Hq, Hkv, P, steps = 1, 32, 4, 700, 4
+
+    def make():
+        c = MixedQuantizedKVCache(max_tokens=1024) if fmt == "affine" else QuantizedKVCache(32, 8, 8, max_tokens=1024)
+        fill(c, B, Hkv, P, seed=501)
+        return c
+
+    qs = [synthetic.query(B, Hq, 1, seed=510 + i) for i in range(steps)]
+    kns = [synthetic.kv((B, Hkv, 1, 128), 520 + i) for i in range(steps)]
+    vns = [synthetic.kv((B, Hkv, 1, 128), 530 + i) for i in range(steps)]
+    sinks = torch.randn(Hq, device="cuda", generator=torch.Generator("cuda").manual_seed(7))
+
+    eager_cache = make()
+    eager = [attend(qs[i], kns[i], vns[i], eager_cache, SCALE, None, sinks, out_dtype=torch.float32)
+             for i in range(steps)]
+    torch.cuda.synchronize()
+    want_k, want_v = (to_logical(kv) for kv in eager_cache.keys_and_values())
+
+    cache = make()
+    outs = [torch.empty_like(e) for e in eager]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            outs[i].copy_(attend(qs[i], kns[i], vns[i], cache, SCALE, None, sinks, out_dtype=torch.float32))
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        x = torch.randn(256, 256, device="cuda")
+        (x @ x).sum().item()  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(steps):
+            assert torch.equal(outs[i], eager[i]), f"replay {rep} step {i}"
+        got_k, got_v = (to_logical(kv) for kv in cache.keys_and_values())
+        for got, want in ((got_k, want_k), (got_v, want_v)):
+            for a_, b_ in zip(got, want):
+                assert (a_ is None and b_ is None) or torch.equal(a_, b_), f"replay {rep}: cache differs"
