@@ -109,6 +109,12 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
   return r;
 }
 
+// Online softmax: the running max (log2 units) is moved only when a score
+// exceeds it by more than this, so probabilities stay below 2^8 — as exact in
+// fp16 / bf16 operands and fp32 sums as ones below 1 — and the rescale of the
+// accumulators runs rarely.
+constexpr float RESCALE_GAP = 8.f;
+
 // ---- cross-lane combines without LDS round trips ----
 // DPP moves inside rows of 16 lanes; v_permlane16_swap / v_permlane32_swap
 // (gfx950) across rows and halves.  A swap of x with itself returns

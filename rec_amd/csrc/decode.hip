@@ -366,12 +366,15 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   }
 
   // ---------------- online softmax (log2 domain: score * qsc) ----------------
-  // A head's max over the chunk exceeds its running max iff one of its four
-  // lanes' own maxima does, so the cross-lane reduction and the rescale run
-  // only then (rare after the first chunks).
+  // The running max moves only when a score exceeds it by more than
+  // RESCALE_GAP: probabilities up to 2^RESCALE_GAP are as exact in the fp16
+  // operands and fp32 sums as ones up to 1.  A head's max over the chunk
+  // exceeds the bound iff one of its four lanes' own maxima does, so the
+  // cross-lane reduction and the rescale run only then (after the first
+  // chunk, rarely).
   float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
   cmax *= qsc;  // qsc > 0
-  if (__ballot(cmax > st.m)) {
+  if (__ballot(cmax > st.m + RESCALE_GAP)) {
     cmax = max_xor32(max_xor16(cmax));
     const float m_new = fmaxf(st.m, cmax);
     const float factor = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first chunk, 1 if unchanged

@@ -99,11 +99,11 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
       if (16 * (idx >> 2) + 4 * kg + (idx & 3) >= valid) s[idx] = NEG_INF;
   }
 
-  // ---------------- online softmax ----------------
+  // ---------------- online softmax (lazy running max, RESCALE_GAP) ----------------
   float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-  cmax = max_xor32(max_xor16(cmax));
-  const float m_new = fmaxf(st.m, cmax);
-  if (__ballot(m_new > st.m)) {
+  if (__ballot(cmax > st.m + RESCALE_GAP)) {
+    cmax = max_xor32(max_xor16(cmax));
+    const float m_new = fmaxf(st.m, cmax);
     const float factor = __builtin_amdgcn_exp2f(st.m - m_new);
     st.l *= factor;
 #pragma unroll

@@ -32,7 +32,6 @@
 namespace rec {
 
 constexpr int PF_QB = 32;           // query positions per workgroup
-constexpr float RESCALE_GAP = 8.f;  // lazy running max, see softmax_pv_unit
 constexpr int PF_KROW = 144;        // LDS row pitch of K (elements): 128 + 16 pad
 
 // Tile geometry per cache format: tokens per K/V tile in LDS (one barrier per
