@@ -10,26 +10,36 @@
 namespace rec {
 
 
+// Workgroups per launch of the row kernels, at most: they stride over the
+// rows, so any row count stays inside the dispatch's 32-bit thread count.
+constexpr int64_t ROW_GRID_MAX = 1 << 20;
+
+__host__ __device__ inline unsigned row_grid(int64_t rows) {
+  const int64_t wgs = (rows + 3) / 4;
+  return (unsigned)(wgs < ROW_GRID_MAX ? (wgs > 0 ? wgs : 1) : ROW_GRID_MAX);
+}
+
 // blockIdx.y: 0 = K, 1 = V
 template <int KB, int VB>
 __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int kind = blockIdx.y;
   const int64_t per_bh = kind == 0 ? a.L : a.v_units;
-  if (unit >= (int64_t)a.B * a.Hkv * per_bh) return;
-  const int64_t bh = unit / per_bh, u = unit % per_bh;
-  const int b = (int)(bh / a.Hkv), h = (int)(bh % a.Hkv);
-  if (kind == 0) {
-    append_row<KB>(a.k, b, h, (int)u, 0, a.kq, a.ks, a.kz, bh, a.cap, a.offset + u, lane);
-  } else if constexpr (VB == 8) {
-    append_row<8>(a.v, b, h, (int)u, 1, a.vq, a.vs, nullptr, bh, a.cap, a.offset + u, lane);
-  } else {
-    const int64_t pos_even = ((a.offset >> 1) + u) * 2;
-    const bool has_even = pos_even >= a.offset && pos_even < a.offset + a.L;
-    const bool has_odd = pos_even + 1 >= a.offset && pos_even + 1 < a.offset + a.L;
-    append_v4_pair<VB == FMT_A4>(a.v, b, h, (int)(pos_even - a.offset), has_even, has_odd, (uint8_t*)a.vq, a.vs,
-                                 a.vz, bh, a.cap, pos_even, lane);
+  const int64_t total = (int64_t)a.B * a.Hkv * per_bh;
+  for (int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); unit < total; unit += (int64_t)gridDim.x * 4) {
+    const int64_t bh = unit / per_bh, u = unit % per_bh;
+    const int b = (int)(bh / a.Hkv), h = (int)(bh % a.Hkv);
+    if (kind == 0) {
+      append_row<KB>(a.k, b, h, (int)u, 0, a.kq, a.ks, a.kz, bh, a.cap, a.offset + u, lane);
+    } else if constexpr (VB == 8) {
+      append_row<8>(a.v, b, h, (int)u, 1, a.vq, a.vs, nullptr, bh, a.cap, a.offset + u, lane);
+    } else {
+      const int64_t pos_even = ((a.offset >> 1) + u) * 2;
+      const bool has_even = pos_even >= a.offset && pos_even < a.offset + a.L;
+      const bool has_odd = pos_even + 1 >= a.offset && pos_even + 1 < a.offset + a.L;
+      append_v4_pair<VB == FMT_A4>(a.v, b, h, (int)(pos_even - a.offset), has_even, has_odd, (uint8_t*)a.vq, a.vs,
+                                   a.vz, bh, a.cap, pos_even, lane);
+    }
   }
 }
 
@@ -92,20 +102,21 @@ __device__ __forceinline__ void dequant_pair(const void* codes, const uint16_t* 
 template <int KB, int VB>
 __global__ __launch_bounds__(256) void dequant_kernel(const DequantArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= (int64_t)a.B * a.Hkv * a.T) return;
-  const int64_t bh = row / a.T, t = row % a.T;
+  const int64_t total = (int64_t)a.B * a.Hkv * a.T;
   const bool is_v = blockIdx.y == 1;
-  float x0, x1;
-  if (!is_v) dequant_pair<KB>(a.kq, a.ks, a.kz, false, bh, a.cap, t, lane, x0, x1);
-  else dequant_pair<VB>(a.vq, a.vs, a.vz, true, bh, a.cap, t, lane, x0, x1);
-  uint16_t* o = (is_v ? a.v_out : a.k_out) + row * HEAD_DIM + 2 * lane;
-  *(uint32_t*)o = (uint32_t)float_to_bf16_bits(x0) | ((uint32_t)float_to_bf16_bits(x1) << 16);
+  for (int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); row < total; row += (int64_t)gridDim.x * 4) {
+    const int64_t bh = row / a.T, t = row % a.T;
+    float x0, x1;
+    if (!is_v) dequant_pair<KB>(a.kq, a.ks, a.kz, false, bh, a.cap, t, lane, x0, x1);
+    else dequant_pair<VB>(a.vq, a.vs, a.vz, true, bh, a.cap, t, lane, x0, x1);
+    uint16_t* o = (is_v ? a.v_out : a.k_out) + row * HEAD_DIM + 2 * lane;
+    *(uint32_t*)o = (uint32_t)float_to_bf16_bits(x0) | ((uint32_t)float_to_bf16_bits(x1) << 16);
+  }
 }
 
 hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stream) {
   const int64_t rows = (int64_t)a.B * a.Hkv * a.T;
-  const dim3 grid((unsigned)((rows + 3) / 4), 2), block(256);
+  const dim3 grid(row_grid(rows), 2), block(256);
   if (kb == 8 && vb == 8) hipLaunchKernelGGL((dequant_kernel<8, 8>), grid, block, 0, stream, a);
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((dequant_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((dequant_kernel<4, 8>), grid, block, 0, stream, a);
@@ -116,13 +127,13 @@ hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stre
 
 // Zero a word range (graph-safe replacement for hipMemsetAsync).
 __global__ void fill_zero_kernel(uint32_t* p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
 }
 
 hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream) {
   const int64_t rows = (int64_t)a.B * a.Hkv * (a.L > a.v_units ? a.L : a.v_units);
-  const dim3 grid((unsigned)((rows + 3) / 4), 2), block(256);
+  const dim3 grid(row_grid(rows), 2), block(256);
   if (kb == 8 && vb == 8) hipLaunchKernelGGL((append_kernel<8, 8>), grid, block, 0, stream, a);
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((append_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((append_kernel<4, 8>), grid, block, 0, stream, a);
@@ -133,7 +144,9 @@ hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream
 
 hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream) {
   if (words <= 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream, p, words);
+  const int64_t wgs = (words + 255) / 256;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)(wgs < ROW_GRID_MAX ? wgs : ROW_GRID_MAX)), dim3(256), 0, stream,
+                     p, words);
   return hipGetLastError();
 }
 

@@ -291,18 +291,19 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
 __global__ __launch_bounds__(256) void write_bf16_kernel(const AppendArgs a, int64_t k_sb, int64_t k_sh,
                                                          int64_t v_sb, int64_t v_sh) {
   const int lane = threadIdx.x & 63;
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (unit >= (int64_t)a.B * a.Hkv * a.L) return;
-  const int64_t bh = unit / a.L, u = unit % a.L;
-  const int b = (int)(bh / a.Hkv), h = (int)(bh % a.Hkv);
+  const int64_t total = (int64_t)a.B * a.Hkv * a.L;
   const bool isv = blockIdx.y == 1;
   const RowSrc& src = isv ? a.v : a.k;
-  float x0, x1;
-  load2_as_float(src, row_base(src, b, h, (int)u) + 2 * lane, x0, x1);
-  const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
-  const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-  __bf16* dst = (__bf16*)(isv ? a.vq : a.kq) + (int64_t)b * (isv ? v_sb : k_sb) + (int64_t)h * (isv ? v_sh : k_sh);
-  *(uint32_t*)(dst + (a.offset + u) * HEAD_DIM + 2 * lane) = w;
+  for (int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); unit < total; unit += (int64_t)gridDim.x * 4) {
+    const int64_t bh = unit / a.L, u = unit % a.L;
+    const int b = (int)(bh / a.Hkv), h = (int)(bh % a.Hkv);
+    float x0, x1;
+    load2_as_float(src, row_base(src, b, h, (int)u) + 2 * lane, x0, x1);
+    const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+    const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    __bf16* dst = (__bf16*)(isv ? a.vq : a.kq) + (int64_t)b * (isv ? v_sb : k_sb) + (int64_t)h * (isv ? v_sh : k_sh);
+    *(uint32_t*)(dst + (a.offset + u) * HEAD_DIM + 2 * lane) = w;
+  }
 }
 
 }  // namespace
@@ -315,7 +316,9 @@ hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream) {
 hipError_t launch_write_bf16(const AppendArgs& a, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
                              hipStream_t stream) {
   const int64_t rows = (int64_t)a.B * a.Hkv * a.L;
-  hipLaunchKernelGGL(write_bf16_kernel, dim3((unsigned)((rows + 3) / 4), 2), dim3(256), 0, stream, a, k_sb, k_sh, v_sb,
+  const int64_t wgs = (rows + 3) / 4;
+  const unsigned grid_x = (unsigned)(wgs < (1 << 20) ? (wgs > 0 ? wgs : 1) : (1 << 20));  // the kernel strides over rows
+  hipLaunchKernelGGL(write_bf16_kernel, dim3(grid_x, 2), dim3(256), 0, stream, a, k_sb, k_sh, v_sb,
                      v_sh);
   return hipGetLastError();
 }

@@ -64,3 +64,30 @@ def test_decode_at_max_capacity(gpu, fmt):
     del cache
     torch.cuda.empty_cache()
 
+
+
+def test_row_kernels_stride_past_their_grid(gpu):
+    """An append of 4.8M rows (600K tokens x 8 KV heads) needs more than the
+    2^20 workgroups the row kernels launch, so they stride; the rows written
+    last (and their bf16 dequantization) equal the oracle's, bit for bit."""
+    from rec_amd import dequantize_kv, to_logical
+
+    B, Hkv, L, tail = 1, 8, 600_000, 256
+    cache = QuantizedKVCache(32, 8, 8, max_tokens=L)
+    g = torch.Generator(device="cuda").manual_seed(77)
+    k = torch.randn((B, Hkv, L, 128), generator=g, device="cuda").to(torch.float16)
+    v = torch.randn((B, Hkv, L, 128), generator=g, device="cuda").to(torch.float16)
+    kq, vq = cache.update_and_fetch(k, v)
+    kd, vd = dequantize_kv(kq, vq)
+    torch.cuda.synchronize()
+    for kv, x, xd, name in ((kq, k, kd, "K"), (vq, v, vd, "V")):
+        codes, scales, _ = to_logical(kv)
+        want_c, want_s = O.quantize_int8(f32(x[:, :, L - tail :]))
+        np.testing.assert_array_equal(codes[:, :, L - tail : L].cpu().numpy(), want_c, err_msg=f"{name} codes")
+        np.testing.assert_array_equal(scales[:, :, L - tail : L].cpu().numpy().view(np.uint16),
+                                      np.asarray(want_s, np.float16).view(np.uint16), err_msg=f"{name} scales")
+        want_d = O.bf16_rn(O.dequantize_int8(want_c, want_s))
+        got_d = xd[:, :, L - tail :].float().cpu().numpy()
+        np.testing.assert_array_equal(got_d, want_d, err_msg=f"{name} dequantized")
+    del cache, k, v, kd, vd
+    torch.cuda.empty_cache()
