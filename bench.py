@@ -592,10 +592,15 @@ def main(argv=None):
         r4 = run_decode(131072, 12, ls, max(4, args.warmup // 4), args.seed + 77, bits=4, kind="heavy", frac=0.05)
         log(f"131K int4: {r4['us_per_step']:.2f} us/step, {r4['gbs']:.0f} GB/s; kernel {r4['kernel_us']:.2f} us")
 
-    raf = None
+    raf = raf252 = None
     if not args.no_affine:
         raf = run_decode(32768, 40, max(16, args.steps // 4), max(4, args.warmup // 4), args.seed + 88, bits=AFFINE)
         log(f"32K affine: {raf['us_per_step']:.2f} us/step, {raf['gbs']:.0f} GB/s; kernel {raf['kernel_us']:.2f} us")
+        if not args.no_long:
+            ls = args.long_steps or max(16, args.steps // 8)
+            raf252 = run_decode(258048, 5, ls, max(4, args.warmup // 4), args.seed + 89, bits=AFFINE)
+            log(f"252K affine: {raf252['us_per_step']:.2f} us/step, {raf252['gbs']:.0f} GB/s; "
+                f"kernel {raf252['kernel_us']:.2f} us")
 
     rbf = {}
     if not args.no_bf16:
@@ -705,6 +710,20 @@ def main(argv=None):
             "kernel_frac_of_peak": round(raf["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_step": raf["bytes_per_step"],
             "cache_instances": raf["instances"],
+        }
+    if raf252 is not None:
+        result["context_252k_affine"] = {
+            "context": 258048,
+            "kv_format": "MLX-style affine group 64: 8-bit K, 4-bit V, bf16 scale + bias (the reference's default)",
+            "us_per_step": round(raf252["us_per_step"], 3),
+            **_step_detail(raf252),
+            "gbs": round(raf252["gbs"], 2),
+            "frac_of_peak": round(raf252["gbs"] / HBM_PEAK_GBS, 4),
+            "kernel_us": round(raf252["kernel_us"], 3),
+            "kernel_gbs": round(raf252["kernel_gbs"], 2),
+            "kernel_frac_of_peak": round(raf252["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_step": raf252["bytes_per_step"],
+            "cache_instances": raf252["instances"],
         }
     result.update(rbf)
     if rq4 is not None:
