@@ -55,10 +55,13 @@ constexpr int UINT4_WIDE_CHUNKS = 32;
 constexpr int LDS_QOP = 0;              // up to 4 operands x 64 lanes x 16 B
 constexpr int LDS_QSC = 4096;           // 8 floats: per-head query scale
 constexpr int LDS_QSUM = LDS_QSC + 32;  // 8 x 4 ints: per-group query sums (int4 K)
+// A wave partial row holds 128 floats plus 4 of padding, so that the 8 query
+// heads' rows start 4 banks apart and their stores do not collide on one bank.
+constexpr int PART_ROW = HEAD_DIM + 4;
 template <int W>
 struct Lds {
-  static constexpr int part = 4352;                  // wave partials: W x 8 x 128 floats
-  static constexpr int pstat = part + W * 8 * 128 * 4;  // W x 8 x (m, l)
+  static constexpr int part = 4352;                  // wave partials: W x 8 rows of PART_ROW floats
+  static constexpr int pstat = part + W * 8 * PART_ROW * 4;  // W x 8 x (m, l)
   static constexpr int meta = pstat + W * 8 * 8;        // int4: per wave [4 arrays][256 B] of one block
   static constexpr int bytes = meta + W * 1024;
 };
@@ -119,6 +122,7 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
   amax = max_xor16(row16_max(amax));  // the 32 lanes of head hh
   const float inv = amax > 0.f ? Q16 / amax : 0.f;
   int gsum = 0;
+  uint32_t hi4 = 0, lo4 = 0;  // int8 K: the four dims' bytes, stored as one dword each
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     int q16 = (int)__builtin_rintf(x[i] * inv);
@@ -128,15 +132,20 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
     gsum += q16;
     const int d = d0 + i;
     if constexpr (KB == 8 || KB == FMT_A8) {
-      const int m = d >> 6, kg = (d >> 4) & 3, j = d & 15;
-      qop[(m * 64 + kg * 16 + hh) * 16 + j] = (int8_t)hi;
-      qop[(m * 64 + kg * 16 + hh + 8) * 16 + j] = (int8_t)lo;
+      hi4 |= (uint32_t)(hi & 0xff) << (8 * i);
+      lo4 |= (uint32_t)(lo & 0xff) << (8 * i);
     } else {
       const int gg = d >> 5, pr = gg >> 1, o = d & 31;
       const int kg = 2 * (gg & 1) + (o >> 4), c = hh + 8 * (gg & 1), j = u4_unpacked_pos(o & 15);
       qop[((pr * 2 + 0) * 64 + kg * 16 + c) * 16 + j] = (int8_t)hi;
       qop[((pr * 2 + 1) * 64 + kg * 16 + c) * 16 + j] = (int8_t)lo;
     }
+  }
+  if constexpr (KB == 8 || KB == FMT_A8) {
+    // dims d0 .. d0+3 share operand m and lane row kg*16 + hh; bytes j .. j+3
+    const int m = d0 >> 6, kg = (d0 >> 4) & 3, j = d0 & 15;
+    *(uint32_t*)(qop + (m * 64 + kg * 16 + hh) * 16 + j) = hi4;
+    *(uint32_t*)(qop + (m * 64 + kg * 16 + hh + 8) * 16 + j) = lo4;
   }
   if constexpr (KB == 4 || KB == FMT_A8) {
     // group of 32 dims = 8 consecutive threads
@@ -636,7 +645,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
     for (int n = 0; n < 8; ++n)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        part[(wave * 8 + c) * HEAD_DIM + 16 * n + 4 * kg + i] = st.acc[n][i];
+        part[(wave * 8 + c) * PART_ROW + 16 * n + 4 * kg + i] = st.acc[n][i];
       }
     if (kg == 0) {
       pstat[(wave * 8 + c) * 2 + 0] = st.m;
@@ -663,7 +672,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) {
       const float f = (mw[w] == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
-      acc4 += f * *(const v4f*)(part + (w * 8 + hh) * HEAD_DIM + d0);
+      acc4 += f * *(const v4f*)(part + (w * 8 + hh) * PART_ROW + d0);
       l += f * pstat[(w * 8 + hh) * 2 + 1];
     }
     if (a.S == 1) {
