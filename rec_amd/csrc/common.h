@@ -154,6 +154,13 @@ __device__ __forceinline__ float sum_xor32(float x) {
   pair32(x, a, b);
   return a + b;
 }
+// Maximum that propagates NaN (v_maximum3_f32 on gfx950).  fmaxf must quiet a
+// signaling NaN input, so the compiler puts a v_max_f32 x, x, x in front of
+// every operand it cannot prove canonical (matrix-core results among them);
+// this one needs none, and a chain of n operands costs ceil((n - 1) / 2)
+// instructions.
+__device__ __forceinline__ float maxp(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 __device__ __forceinline__ float max_xor16(float x) {
   float a, b;
   pair16(x, a, b);

@@ -207,23 +207,29 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
 // Softmax of one unit's scores, then O^T += V^T P'^T.  mask: some token of the
 // unit lies past the cache end or past a query's causal diagonal (only units
 // that reach a query block's diagonal); one loop under one uniform branch.
+//
+// Row state (per query row rt of the lane): m_use, the offset the
+// probabilities are taken against (log2 domain; 0 before the row's first
+// finite score), thr, the bound past which a score moves it (-inf until the
+// row has seen a finite score, then RESCALE_GAP), and l_run, the sum of
+// probabilities.  t = s * ksc - m_use is one fma per score.
 template <int VROW>
 __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
-                                                const float* VS, float (&m_run)[2], float (&l_run)[2],
-                                                v4f (&acc)[8][2], int t0, int t_end, int qabs0, int causal, int window,
-                                                bool mask, int c, int g) {
+                                                const float* VS, float (&m_use)[2], float (&thr)[2],
+                                                float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end, int qabs0,
+                                                int causal, int window, bool mask, int c, int g) {
   v8h pb[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    // scale (K scale x softmax scale, one multiply), mask, online softmax per
-    // query row (lane column c of tile rt)
-    float s[8];
+    // scale (K scale x softmax scale) and offset in one fma, mask, online
+    // softmax per query row (lane column c of tile rt)
+    float t[8];
     const int qabs = qabs0 + 16 * rt + c;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const v4f ksc = *(const v4f*)(&KS[16 * j + 4 * g]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[4 * j + i] = s4[rt][j][i] * ksc[i];
+      for (int i = 0; i < 4; ++i) t[4 * j + i] = __builtin_fmaf(s4[rt][j][i], ksc[i], -m_use[rt]);
     }
     if (mask) {
       // first and last visible token of this row, relative to the lane's first token t0 + 4g
@@ -232,33 +238,42 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int pos = 16 * (k >> 2) + (k & 3);
-        if (pos > last || pos < first) s[k] = NEG_INF;
+        if (pos > last || pos < first) t[k] = NEG_INF;
       }
     }
-    float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-    // The running max is moved only when a score exceeds it by more than
-    // RESCALE_GAP (log2 units): until then probabilities up to 2^RESCALE_GAP
-    // are as exact in fp16 P' and the fp32 sums as ones up to 1, and the
-    // rescale (a cross-lane max, an exp and 32 multiplies per row tile) runs
-    // far less often (measured 2% faster).  A row's max exceeds the bound iff
-    // one of its four lanes' maxima does.
-    if (__ballot(cmax > m_run[rt] + RESCALE_GAP)) {
-      cmax = max_xor32(max_xor16(cmax));
-      const float m_new = fmaxf(m_run[rt], cmax);
-      const float factor = m_new == NEG_INF ? 1.f : __builtin_amdgcn_exp2f(m_run[rt] - m_new);
+    float cmax = t[0];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) cmax = maxp(cmax, t[k]);
+    // The offset moves only when a score passes it by more than RESCALE_GAP
+    // (log2 units): until then probabilities up to 2^RESCALE_GAP are as exact
+    // in fp16 P' and the fp32 sums as ones up to 1, and the rescale (a
+    // cross-lane max, an exp and 32 multiplies per row tile) runs far less
+    // often (measured 2% faster).  A row's max passes the bound iff one of its
+    // four lanes' maxima does.
+    if (__ballot(cmax > thr[rt])) {
+      cmax = max_xor32(max_xor16(cmax));  // the row's max of t
+      // a row with finite scores so far moves to max(offset, row max); a new
+      // row takes its first finite max; an all-masked row stays
+      float delta = maxp(cmax, thr[rt] == NEG_INF ? cmax : 0.f);
+      delta = delta == NEG_INF ? 0.f : delta;
+      // a new row's sums are still zero; its delta may be far below zero, where
+      // exp2(-delta) would overflow
+      const float factor = thr[rt] == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(-delta);
       l_run[rt] *= factor;
 #pragma unroll
       for (int n = 0; n < 8; ++n) acc[n][rt] *= factor;
-      m_run[rt] = m_new;
+      m_use[rt] += delta;
+      thr[rt] = cmax == NEG_INF ? thr[rt] : RESCALE_GAP;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t[k] -= delta;
     }
-    const float m_use = m_run[rt] == NEG_INF ? 0.f : m_run[rt];
     float lsum = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const v4f vsc = *(const v4f*)(&VS[16 * j + 4 * g]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(s[4 * j + i] - m_use);
+        const float p = __builtin_amdgcn_exp2f(t[4 * j + i]);
         lsum += p;
         // B operand of P·V: k index 8g + 4j + i = cache position of token 16j + 4g + i
         pb[rt][4 * j + i] = (_Float16)(p * vsc[i]);
@@ -305,7 +320,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       for (int e = 0; e < 8; ++e) qop[rt][ks][e] = MT<BF16>::from_float(load_as_float(a.q, base + 32 * ks + 8 * g + e, a.q_dtype));
   }
 
-  float m_run[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
+  float m_use[2] = {0.f, 0.f}, thr[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
   v4f acc[8][2];
 #pragma unroll
   for (int n = 0; n < 8; ++n)
@@ -355,8 +370,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
         if (pend) {
           // the unit before: this tile's unit u - 1, or the previous tile's last
           const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? PF_KT - 32 : 32 * (u - 1);
-          softmax_pv_unit<VROW>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_run, l_run, acc,
-                                pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
+          softmax_pv_unit<VROW>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
+                                acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
         }
         pend = live;
         pend_t = tu;
@@ -375,8 +390,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   // still pending: the last tile's last unit (every unit of a tile is visited,
   // and a tile has an even number of units, so its scores are in sc[1])
   if (active && pend)
-    softmax_pv_unit<VROW>(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_run, l_run,
-                          acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
+    softmax_pv_unit<VROW>(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_use, thr,
+                          l_run, acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
 
   if (!active) return;
   // ---------------- normalise and write ----------------
@@ -384,7 +399,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   for (int rt = 0; rt < 2; ++rt) {
     float l = l_run[rt];
     l = sum_xor32(sum_xor16(l));
-    float M = m_run[rt];
+    float M = thr[rt] == NEG_INF ? NEG_INF : m_use[rt];  // -inf: no visible key
     if (a.sinks != nullptr) {
       const float sink = a.sinks[hq] * LOG2E;
       const float Mn = fmaxf(M, sink);
