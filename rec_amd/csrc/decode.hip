@@ -381,7 +381,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   // exceeds the bound iff one of its four lanes' own maxima does, so the
   // cross-lane reduction and the rescale run only then (after the first
   // chunk, rarely).
-  float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  float cmax = s[0];
+#pragma unroll
+  for (int idx = 1; idx < 8; ++idx) cmax = maxp(cmax, s[idx]);
   cmax *= qsc;  // qsc > 0
   if (__ballot(cmax > st.m + RESCALE_GAP)) {
     cmax = max_xor32(max_xor16(cmax));
@@ -727,7 +729,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
     const bool ok = lane + 64 * k < S;
     ms[k] = ok ? __builtin_bit_cast(float, m_bits) : NEG_INF;
     ls[k] = ok ? __builtin_bit_cast(float, l_bits) : 0.f;
-    M = fmaxf(M, ms[k]);
+    M = maxp(M, ms[k]);
   }
   const float sink = has_sink ? __builtin_bit_cast(float, sink_bits) * LOG2E : NEG_INF;
   M = fmaxf(wave_max(M), sink);

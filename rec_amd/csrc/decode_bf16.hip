@@ -100,7 +100,9 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
   }
 
   // ---------------- online softmax (lazy running max, RESCALE_GAP) ----------------
-  float cmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+  float cmax = s[0];
+#pragma unroll
+  for (int idx = 1; idx < 8; ++idx) cmax = maxp(cmax, s[idx]);
   if (__ballot(cmax > st.m + RESCALE_GAP)) {
     cmax = max_xor32(max_xor16(cmax));
     const float m_new = fmaxf(st.m, cmax);
