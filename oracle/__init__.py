@@ -1,6 +1,6 @@
 """CPU oracle for quantized-KV GQA attention (test infrastructure only).
 
-This package is the checker, never the product: only ``tests/``,
+This package checks the product and is never part of it: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  ``rec_amd`` never imports it and has no CPU fallback.
 """

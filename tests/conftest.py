@@ -14,7 +14,7 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def gpu():
-    """Return the rec_amd library handle on a GPU box; fail loudly if it is missing."""
+    """Return the rec_amd library handle on a machine with a GPU; fail loudly if it is missing."""
     import torch
 
     if not torch.cuda.is_available():
