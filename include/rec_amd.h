@@ -52,7 +52,7 @@ enum {
   REC_ECAPACITY = -3,    /* tokens beyond the cache capacity */
   REC_EWORKSPACE = -4,   /* workspace missing or too small */
   REC_ELAUNCH = -5,      /* the HIP runtime rejected a launch */
-  REC_EUNSUPPORTED = -6  /* a valid request this build does not implement */
+  REC_EUNSUPPORTED = -6  /* a valid request this library does not implement */
 };
 
 /* Element types of the float inputs (queries, new keys/values). */
