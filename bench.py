@@ -76,39 +76,40 @@ def step_bytes(T, B=1, k_bits=8, v_bits=8, output=True):
 class DecodeWorkload:
     """R cache instances of one context length plus a pool of new tokens."""
 
-    def __init__(self, T, R, total_steps, seed, splits=0, bits=8, kind="outliers", frac=0.01):
+    def __init__(self, T, R, total_steps, seed, splits=0, bits=8, kind="outliers", frac=0.01, batch=1):
         import torch
 
         import rec_amd
         from rec_amd import synthetic
 
         self.torch, self.lib = torch, rec_amd.library()
-        self.T, self.R, self.splits, self.bits = T, R, splits, bits
+        self.T, self.R, self.splits, self.bits, self.B = T, R, splits, bits, batch
+        B = batch
         counts = [len(range(i, total_steps, R)) for i in range(R)]
         self.caches = []
         for i in range(R):
             T0 = T - counts[i]
             c = (rec_amd.QuantizedKVCache(64, 8, 4, max_tokens=T) if bits == AFFINE
                  else rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T))
-            k = synthetic.kv((1, HKV, T0, D), seed + 2 * i, kind=kind, frac=frac)
-            v = synthetic.kv((1, HKV, T0, D), seed + 2 * i + 1, kind=kind, frac=frac)
+            k = synthetic.kv((B, HKV, T0, D), seed + 2 * i, kind=kind, frac=frac)
+            v = synthetic.kv((B, HKV, T0, D), seed + 2 * i + 1, kind=kind, frac=frac)
             c.update_and_fetch(k, v)
             del k, v
             self.caches.append(c)
         P = 16
         self.pool = [
             (
-                synthetic.query(1, HQ, 1, seed + 1000 + j)[:, :, 0].contiguous(),
-                synthetic.kv((1, HKV, 1, D), seed + 2000 + j),
-                synthetic.kv((1, HKV, 1, D), seed + 3000 + j),
+                synthetic.query(B, HQ, 1, seed + 1000 + j)[:, :, 0].contiguous(),
+                synthetic.kv((B, HKV, 1, D), seed + 2000 + j),
+                synthetic.kv((B, HKV, 1, D), seed + 3000 + j),
             )
             for j in range(P)
         ]
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
         self.sinks = torch.randn(HQ, generator=g, device="cuda")
-        self.out = torch.empty((1, HQ, D), dtype=torch.float32, device="cuda")
-        self.ws = torch.zeros(self.lib.rec_decode_workspace_bytes(1, HKV, 256), dtype=torch.uint8, device="cuda")
+        self.out = torch.empty((B, HQ, D), dtype=torch.float32, device="cuda")
+        self.ws = torch.zeros(self.lib.rec_decode_workspace_bytes(B, HKV, 256), dtype=torch.uint8, device="cuda")
         self.step_T = []
         torch.cuda.synchronize()
 
@@ -131,7 +132,7 @@ class DecodeWorkload:
             kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
-            self.sinks.data_ptr(), SCALE, 1, HQ, HKV, D, T, c.capacity, self.splits,
+            self.sinks.data_ptr(), SCALE, self.B, HQ, HKV, D, T, c.capacity, self.splits,
             self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), stream,
         )
         _lib.check(rc, "decode step")
@@ -152,7 +153,7 @@ class DecodeWorkload:
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
-            self.sinks.data_ptr(), SCALE, 1, HQ, HKV, D, c.offset, c.capacity, self.splits,
+            self.sinks.data_ptr(), SCALE, self.B, HQ, HKV, D, c.offset, c.capacity, self.splits,
             self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), self.torch.cuda.current_stream().cuda_stream,
         )
         _lib.check(rc, "decode attention")
@@ -172,7 +173,7 @@ class DecodeWorkload:
             vn.stride(0), vn.stride(1), vn.stride(2),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
-            1, HKV, 1, D, c.offset - 1, c.capacity, self.torch.cuda.current_stream().cuda_stream,
+            self.B, HKV, 1, D, c.offset - 1, c.capacity, self.torch.cuda.current_stream().cuda_stream,
         )
         _lib.check(rc, "append")
 
@@ -188,12 +189,12 @@ def _replay_timed(torch, graph, n):
     return e0.elapsed_time(e1) / n
 
 
-def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, parts=10):
+def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, parts=10, batch=1):
     import torch
 
     total = warmup + 2 * steps
     log(f"T={T}: building {R} cache instances")
-    w = DecodeWorkload(T, R, total, seed, bits=bits, kind=kind, frac=frac)
+    w = DecodeWorkload(T, R, total, seed, bits=bits, kind=kind, frac=frac, batch=batch)
     log(f"T={T}: warm-up {warmup} steps")
     for s in range(warmup):
         w.step(s)
@@ -233,8 +234,8 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, pa
     log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step (parts p10/p50/p90 {p10 * 1e3:.2f}/"
         f"{p50 * 1e3:.2f}/{p90 * 1e3:.2f}); attention kernel {kernel_ms * 1e3:.2f} us; unfused: attention "
         f"{att_ms * 1e3:.2f} us + append {app_ms * 1e3:.2f} us")
-    bytes_step = float(np.mean([step_bytes(t, k_bits=bits, v_bits=bits) for t in step_T]))
-    bytes_kernel = float(np.mean([step_bytes(t, k_bits=bits, v_bits=bits, output=False) for t in kern_T]))
+    bytes_step = float(np.mean([step_bytes(t, batch, k_bits=bits, v_bits=bits) for t in step_T]))
+    bytes_kernel = float(np.mean([step_bytes(t, batch, k_bits=bits, v_bits=bits, output=False) for t in kern_T]))
     res = dict(
         T=T,
         instances=R,
@@ -538,6 +539,7 @@ def main(argv=None):
     ap.add_argument("--no-long", action="store_true", help="skip the 252K measurement")
     ap.add_argument("--no-prefill", action="store_true", help="skip the chunked-prefill measurement")
     ap.add_argument("--no-int4", action="store_true", help="skip the 131K uint4 measurement")
+    ap.add_argument("--no-batch", action="store_true", help="skip the 32K batch-4 measurement")
     ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-cache measurements")
     ap.add_argument("--no-gemv", action="store_true", help="skip the int4 GEMV measurements")
     ap.add_argument("--no-affine", action="store_true", help="skip the group-64 affine cache measurement")
@@ -585,6 +587,14 @@ def main(argv=None):
         ls = args.long_steps or max(16, args.steps // 8)
         r252 = run_decode(258048, 4, ls, max(4, args.warmup // 4), args.seed + 99)
         log(f"252K: {r252['us_per_step']:.2f} us/step, {r252['gbs']:.0f} GB/s; kernel {r252['kernel_us']:.2f} us")
+
+    rb4 = None
+    if not args.no_batch:
+        # the 32K configuration for 4 sequences at once: the same two launches
+        # per step carry 4x the bytes, which separates the fixed per-step cost
+        # (launches, first-load latency) from the kernel's streaming rate
+        rb4 = run_decode(32768, 8, max(16, args.steps // 4), max(4, args.warmup // 4), args.seed + 55, batch=4)
+        log(f"32K batch 4: {rb4['us_per_step']:.2f} us/step, {rb4['gbs']:.0f} GB/s; kernel {rb4['kernel_us']:.2f} us")
 
     r4 = None
     if not args.no_int4:
@@ -682,6 +692,21 @@ def main(argv=None):
             "kernel_frac_of_peak": round(r252["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_step": r252["bytes_per_step"],
             "cache_instances": r252["instances"],
+        }
+    if rb4 is not None:
+        result["context_32k_batch4"] = {
+            "context": 32768,
+            "batch": 4,
+            "note": "informational: 4 sequences per step, the metric's configuration is batch 1",
+            "us_per_step": round(rb4["us_per_step"], 3),
+            **_step_detail(rb4),
+            "gbs": round(rb4["gbs"], 2),
+            "frac_of_peak": round(rb4["gbs"] / HBM_PEAK_GBS, 4),
+            "kernel_us": round(rb4["kernel_us"], 3),
+            "kernel_gbs": round(rb4["kernel_gbs"], 2),
+            "kernel_frac_of_peak": round(rb4["kernel_gbs"] / HBM_PEAK_GBS, 4),
+            "bytes_per_step": rb4["bytes_per_step"],
+            "cache_instances": rb4["instances"],
         }
     if r4 is not None:
         result["context_131k_int4"] = {
