@@ -421,7 +421,7 @@ def run_prefill(P, L, steps, warmup, seed):
         st = torch.cuda.current_stream().cuda_stream
         rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3], 8, kc.data_ptr(), ks.data_ptr(),
                                   None, 8, vc.data_ptr(), vs.data_ptr(), None, sinks.data_ptr(), SCALE, 1,
-                                  1, HQ, HKV, D, L, T, c.capacity, out.data_ptr(), st)
+                                  1, HQ, HKV, D, L, T, c.capacity, 0, None, 0, out.data_ptr(), st)
         _lib.check(rc, "rec_prefill_attn")
 
     for _ in range(warmup):

@@ -160,6 +160,12 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * strides (q_sb, q_sh, q_st), bf16 or f16, attend over all T tokens — with
  * causal != 0, query i sees tokens [0, T-L+i] — with optional sink logits.
  * out (B, Hq, L, D) fp32.  int8 K and V.
+ * splits: key splits (<= 0: automatic, 1: none, at most 64).  A short chunk
+ * over a long cache (few query blocks x KV heads x batch) splits the keys so
+ * that the launch fills the chip; the partials go to `workspace`
+ * (rec_prefill_workspace_bytes) and a second kernel merges them.  An automatic
+ * plan without a workspace (NULL or too small) runs unsplit; an explicit
+ * split count > 1 without one fails with REC_EWORKSPACE.
  * Replaces the prefill branch of Attention.__call__,
  * engine/src/rec_mlx/model.py:191-203 (mask rule :122-125).
  */
@@ -168,7 +174,13 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
                      const float* sinks, float scale, int causal,
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
-                     float* out, void* stream);
+                     int splits, void* workspace, size_t workspace_bytes, float* out, void* stream);
+
+/* Workspace bytes a prefill launch of L queries needs for `splits` key splits
+ * (<= 0: the most the automatic plan can use); 0 when it does not split.
+ * Serves rec_prefill_attn and rec_prefill_bf16; no counterpart in the
+ * reference, whose prefill is one library call. */
+size_t rec_prefill_workspace_bytes(int B, int Hkv, int L, int splits);
 
 /*
  * bf16 KV cache (the reference's production format): K and V are (B, Hkv,
@@ -226,7 +238,7 @@ int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scale
  * are (B, Hkv, >=T, 128) bf16 with token stride 128 and 16-byte aligned rows.
  * causal: query p sees keys <= p; window > 0 further limits it to keys
  * > p - window (the sliding-window mask of cache.py:199-205).  Sinks, scale and
- * the fp32 output (B, Hq, L, 128) as rec_prefill_attn.
+ * the fp32 output (B, Hq, L, 128), splits and workspace as rec_prefill_attn.
  * Replaces mx.fast.scaled_dot_product_attention over a FixedKVCache or
  * FixedSlidingKVCache in Attention.__call__, engine/src/rec_mlx/model.py:204-211
  * (the 512-query windowed form: engine/src/rec_mlx/m4_max_prefill.py:86-104).
@@ -234,7 +246,8 @@ int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scale
 int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
                      const void* k, int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh,
                      const float* sinks, float scale, int causal, int window,
-                     int B, int Hq, int Hkv, int D, int L, int64_t T, float* out, void* stream);
+                     int B, int Hq, int Hkv, int D, int L, int64_t T, int splits,
+                     void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
  * int4 group-64 GEMV (MLX affine 4-bit, the format of the decoder's

@@ -56,8 +56,10 @@ SIGNATURES["rec_decode_partial"] = SIGNATURES["rec_decode_append_attn"]
 SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _p, _p])
 SIGNATURES["rec_prefill_attn"] = (
     _i,
-    [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i64, _i64, _p, _p],
+    [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i64, _i64,
+     _i, _p, _sz, _p, _p],
 )
+SIGNATURES["rec_prefill_workspace_bytes"] = (_sz, [_i, _i, _i, _i])
 
 SIGNATURES["rec_kv_write_bf16"] = (
     _i,
@@ -76,7 +78,8 @@ SIGNATURES["rec_decode_bf16"] = (
 SIGNATURES["rec_kv_dequant_bf16"] = (_i, [_i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i64, _i64, _p, _p, _p])
 SIGNATURES["rec_prefill_bf16"] = (
     _i,
-    [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64, _p, _p],
+    [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64,
+     _i, _p, _sz, _p, _p],
 )
 SIGNATURES["rec_q4_packed_bytes"] = (_sz, [_i64, _i64])
 SIGNATURES["rec_q4_pack"] = (_i, [_p, _p, _p, _i64, _i64, _p, _sz, _p])

@@ -120,18 +120,36 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
         _lib.check(rc, "rec_decode_append_attn")
 
 
-def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out):
+def prefill_workspace(device: torch.device, B: int, Hkv: int, L: int, splits: int, stream: int) -> torch.Tensor:
+    """The prefill workspace (key-split partials) for (device, stream), grown on
+    demand; an empty tensor when the launch does not split.  Kept apart from the
+    decode workspace: a chunk's prefill and the decode steps after it may
+    interleave on one stream, but each launch pair (partials, merge) is ordered."""
+    lib = _lib.load()
+    need = lib.rec_prefill_workspace_bytes(B, Hkv, L, splits)
+    key = ("prefill", device.index, stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < need:
+            ws = torch.empty(max(need, 16), dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+        return ws
+
+
+def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out, splits=0):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     q = queries if queries.stride(-1) == 1 else queries.contiguous()
     dev = queries.device
     sk = _sinks(sinks, Hq, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = prefill_workspace(dev, B, keys.n_kv_heads, L, splits, stream)
     rc = lib.rec_prefill_attn(
         q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), q.stride(2),
         keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
         values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
         _ptr(sk), float(scale), int(causal), B, Hq, keys.n_kv_heads, D, L, int(keys.length), int(keys.capacity),
-        out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream,
+        int(splits), ws.data_ptr(), ws.numel(), out.data_ptr(), stream,
     )
     _lib.check(rc, "rec_prefill_attn")
 
@@ -193,10 +211,10 @@ def quantized_attention_with_sinks(
             raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
         if keys.code == 8 and values.code == 8:
-            _prefill_launch(queries, keys, values, scale, sinks, mask == "causal", out)
+            _prefill_launch(queries, keys, values, scale, sinks, mask == "causal", out, splits or 0)
         else:
             k, v = dequantize_kv(keys, values)
-            _bf16_prefill_launch(queries, k, v, scale, sinks, mask == "causal", 0, out)
+            _bf16_prefill_launch(queries, k, v, scale, sinks, mask == "causal", 0, out, splits or 0)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 
@@ -234,7 +252,7 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
     _lib.check(rc, "rec_decode_bf16")
 
 
-def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out):
+def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out, splits=0):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv, T = keys.shape[1], keys.shape[2]
@@ -242,11 +260,13 @@ def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, ou
         raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
     dev = queries.device
     sk = _sinks(sinks, Hq, dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    ws = prefill_workspace(dev, B, Hkv, L, splits, stream)
     rc = lib.rec_prefill_bf16(
         queries.data_ptr(), _DTYPES[queries.dtype], queries.stride(0), queries.stride(1), queries.stride(2),
         keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
-        _ptr(sk), float(scale), int(causal), int(window), B, Hq, Hkv, D, L, T, out.data_ptr(),
-        torch.cuda.current_stream(dev).cuda_stream,
+        _ptr(sk), float(scale), int(causal), int(window), B, Hq, Hkv, D, L, T, int(splits), ws.data_ptr(),
+        ws.numel(), out.data_ptr(), stream,
     )
     _lib.check(rc, "rec_prefill_bf16")
 
@@ -305,7 +325,7 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
         if window is not None:
             causal, win = True, (0 if window >= T else int(window))
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
-        _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out)
+        _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 

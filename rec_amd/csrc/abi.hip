@@ -330,11 +330,49 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
   return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
 }
 
+// Key splits of a prefill launch: the plan for `splits` (<= 0: automatic),
+// which needs a workspace when it splits; an automatic plan without one runs
+// unsplit, an explicit split count without one is an error.
+static int plan_prefill_splits(PrefillArgs& a, int splits, void* workspace, size_t workspace_bytes) {
+  if (splits > PREFILL_MAX_SPLITS) return fail(REC_EINVAL, "splits %d exceeds %d", splits, PREFILL_MAX_SPLITS);
+  PrefillPlan p = prefill_plan(a, splits);
+  size_t need = prefill_ws_bytes(a.B, a.Hkv, p.nqb, p.S);
+  if (need > 0 && (!workspace || workspace_bytes < need)) {
+    if (splits > 1)
+      return fail(REC_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu that %d splits need",
+                  workspace ? workspace_bytes : (size_t)0, need, splits);
+    p = prefill_plan(a, 1);
+    need = 0;
+  }
+  if (need > 0 && !aligned16(workspace)) return fail(REC_EALIGN, "workspace must be 16-byte aligned");
+  a.S = p.S;
+  a.nqb = p.nqb;
+  a.split_lo = p.split_lo;
+  a.split_len = p.split_len;
+  if (p.S > 1) {
+    const size_t rows = (size_t)a.B * a.Hkv * p.S * p.nqb * 8 * 32;
+    a.ws_acc = (float*)workspace;
+    a.ws_stat = (float*)((char*)workspace + rows * HEAD_DIM * 4);
+  }
+  return REC_OK;
+}
+
+size_t rec_prefill_workspace_bytes(int B, int Hkv, int L, int splits) {
+  if (B < 1 || Hkv < 1 || L < 1) return 0;
+  const int nqb = (L + 31) / 32;
+  int S = splits;
+  if (S <= 0) {
+    const int64_t nwg = (int64_t)nqb * Hkv * B;
+    S = nwg >= 128 ? 1 : (int)std::min<int64_t>(PREFILL_MAX_SPLITS, (256 + nwg - 1) / nwg);
+  }
+  return prefill_ws_bytes(B, Hkv, nqb, std::min(S, PREFILL_MAX_SPLITS));
+}
+
 int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int k_bits,
                      const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits,
                      const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks,
                      float scale, int causal, int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
-                     float* out, void* stream) {
+                     int splits, void* workspace, size_t workspace_bytes, float* out, void* stream) {
   int e;
   int kf, vf;
   if ((e = resolve_formats(k_bits, v_bits, &kf, &vf))) return e;
@@ -375,6 +413,7 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.T = T;
   a.cap = capacity;
   a.causal = causal != 0;
+  if ((e = plan_prefill_splits(a, splits, workspace, workspace_bytes))) return e;
   return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
 }
 
@@ -409,8 +448,8 @@ int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scale
 
 int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
                      int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale,
-                     int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T, float* out,
-                     void* stream) {
+                     int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T, int splits,
+                     void* workspace, size_t workspace_bytes, float* out, void* stream) {
   if (q_dtype != REC_BF16 && q_dtype != REC_F16)
     return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
@@ -450,6 +489,7 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.cap = T;
   a.causal = causal != 0;
   a.window = window;
+  if (int e = plan_prefill_splits(a, splits, workspace, workspace_bytes)) return e;
   return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
 }
 

@@ -60,7 +60,26 @@ struct PrefillArgs {
   int window;                  // > 0: query at position p sees keys (p - window, p] only
   int kv_bf16;                 // K/V are bf16 (B, Hkv, T, 128) tensors, strides below
   int64_t k_sb, k_sh, v_sb, v_sh;
+  // split-K over the keys (S > 1): workgroup (qb, s) scans keys
+  // [split_lo + s * split_len, + split_len) of its query block's range and
+  // writes an unnormalised partial; prefill_merge_kernel combines them
+  int S, nqb;                  // splits, query blocks of PF_QB queries
+  int64_t split_lo, split_len;
+  float* ws_acc;               // [B*Hkv][S][nqb][8][32][128]
+  float* ws_stat;              // [B*Hkv][S][nqb][8][32] x (max, sum)
 };
+
+// Prefill split plan: how many key splits a launch uses and where they lie.
+constexpr int PREFILL_MAX_SPLITS = 64;
+struct PrefillPlan {
+  int S, nqb;
+  int64_t split_lo, split_len;
+};
+// requested <= 0: automatic (splits only when the query blocks x KV heads x
+// batch grid is too small to fill the chip); else at most `requested`
+PrefillPlan prefill_plan(const PrefillArgs& a, int requested);
+// workspace bytes for S splits (0 when S == 1); accumulators then statistics
+size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S);
 
 // Cache rows [0, T) dequantized to bf16 (B, Hkv, T, 128) tensors.
 struct DequantArgs {
@@ -103,7 +122,7 @@ hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream
 hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream);
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
-hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both kernels when a.S > 1
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stream);
 hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream);

@@ -27,6 +27,8 @@
 // tokens 16j + 4g + i -- the order the cache keeps V in inside a 32-token
 // block.  P·V then takes A = V^T straight from LDS (dims x tokens, cache
 // order) and B = P'^T from the lane's own registers.
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace rec {
@@ -301,10 +303,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
-  const int q0 = blockIdx.x * PF_QB, h = blockIdx.y, b = blockIdx.z;
+  // uniform, kept in scalar registers (the division would otherwise leave
+  // them, and everything derived from them, in vector registers)
+  const int split = __builtin_amdgcn_readfirstlane((int)blockIdx.x / a.nqb);
+  const int qb = __builtin_amdgcn_readfirstlane((int)blockIdx.x - split * a.nqb);
+  const int q0 = qb * PF_QB, h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * a.Hkv + h;
   const int P = (int)(a.T - a.L);  // cached tokens before the new ones
-  const int t_end = a.causal ? min((int)a.T, P + q0 + PF_QB) : (int)a.T;
+  const int t_blk = a.causal ? min((int)a.T, P + q0 + PF_QB) : (int)a.T;  // the block's keys end here
   const bool active = w < a.G;
   const int hq = h * a.G + (active ? w : 0);
 
@@ -330,6 +336,13 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   // a sliding window (bf16 caches only) starts the scan at the first query's first visible key
   const int window = KVB ? a.window : 0;
   const int t_first = window > 0 ? max(0, P + q0 - window + 1) / PF_KT * PF_KT : 0;
+  // this workgroup's share of the keys, [lo, t_end): the split's range
+  // (tile-aligned) within the query block's [t_first, t_blk); empty for some
+  // splits.  A split that ends before t_blk ends on a tile boundary, so its
+  // tiles are whole and t_end serves every load, mask and liveness test.
+  const int64_t s_lo = a.split_lo + (int64_t)split * a.split_len;
+  const int lo = __builtin_amdgcn_readfirstlane((int)max((int64_t)t_first, s_lo));
+  const int t_end = __builtin_amdgcn_readfirstlane((int)min((int64_t)t_blk, s_lo + a.split_len));
   const auto fetch = [&](TileRegs& R, int t0) {
     if constexpr (KVB) load_tile_bf16(R, a, b, h, t0, tid, t_end);
     else load_tile(R, a, bh, t0, tid, t_end);
@@ -338,8 +351,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     if constexpr (KVB) store_tile_bf16<BF16>(R, Kl[bf], Vl[bf], KS[bf], VS[bf], tid, a.q_mul);
     else store_tile<BF16>(R, Kl[bf], Vl[bf], KS[bf], VS[bf], tid, a.q_mul);
   };
+  // unconditional even for an empty range (lo >= t_end): every load then fails
+  // its liveness test and reads nothing; a branch here costs the int8 kernel
+  // 88 bytes of register spills
   TileRegs R;
-  fetch(R, t_first);
+  fetch(R, lo);
   put(R, 0);
   __syncthreads();
 
@@ -358,7 +374,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const auto needs_mask = [&](int tu) {
     return tu + 32 > qabs0 || tu + 32 > t_end || (window > 0 && tu < qabs0 + PF_QB - window);
   };
-  for (int t0 = t_first; t0 < t_end; t0 += PF_KT) {
+  for (int t0 = lo; t0 < t_end; t0 += PF_KT) {
     const bool more = t0 + PF_KT < t_end;
     if (more) fetch(R, t0 + PF_KT);  // in flight during this tile
     if (active) {
@@ -394,6 +410,23 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
                           l_run, acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
 
   if (!active) return;
+  if (a.S > 1) {
+    // ---------------- unnormalised partial of this split ----------------
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float l = sum_xor32(sum_xor16(l_run[rt]));
+      const float M = thr[rt] == NEG_INF ? NEG_INF : m_use[rt];  // -inf: no visible key in this split
+      const int qr = q0 + 16 * rt + c;
+      if (qr < a.L) {
+        const int64_t row = ((((int64_t)bh * a.S + split) * a.nqb + qb) * 8 + w) * PF_QB + 16 * rt + c;
+        float* o = a.ws_acc + row * HEAD_DIM + 4 * g;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt];
+        if (g == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){M, l};
+      }
+    }
+    return;
+  }
   // ---------------- normalise and write ----------------
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
@@ -418,14 +451,82 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   }
 }
 
+// Merge of the key splits (S > 1): one wavefront per (query, query head,
+// batch); lane k owns the statistics of split k, the weights go through LDS,
+// and lane l sums dims 2l, 2l + 1 over the splits.  The sink logit joins here.
+__global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) {
+  __shared__ float wts[PREFILL_MAX_SPLITS];
+  const int i = blockIdx.x, hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+  const int h = hq / a.G, w = hq % a.G, qb = i / PF_QB, r = i % PF_QB;
+  const int64_t bh = (int64_t)b * a.Hkv + h;
+  const auto row = [&](int sp) { return ((((bh * a.S + sp) * a.nqb + qb) * 8 + w) * PF_QB) + r; };
+  float m = NEG_INF, l = 0.f;
+  if (lane < a.S) {
+    const v2f st = *(const v2f*)(a.ws_stat + row(lane) * 2);
+    m = st[0];
+    l = st[1];
+  }
+  const float sink = a.sinks != nullptr ? a.sinks[hq] * LOG2E : NEG_INF;
+  const float M = fmaxf(wave_max(m), sink);
+  const float f = (m == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+  float z = wave_sum(f * l);
+  if (sink != NEG_INF) z += __builtin_amdgcn_exp2f(sink - M);
+  if (lane < a.S) wts[lane] = f;
+  __syncthreads();
+  v2f acc = {0.f, 0.f};
+  for (int sp = 0; sp < a.S; ++sp) acc += wts[sp] * *(const v2f*)(a.ws_acc + row(sp) * HEAD_DIM + 2 * lane);
+  const float inv = z > 0.f ? 1.f / z : 1.f;
+  *(v2f*)(a.out + (((int64_t)b * a.Hq + hq) * a.L + i) * HEAD_DIM + 2 * lane) = acc * inv;
+}
+
+PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
+  PrefillPlan p{};
+  p.nqb = (a.L + PF_QB - 1) / PF_QB;
+  const int kt = a.kv_bf16 ? PfTile<true>::KT : PfTile<false>::KT;
+  // keys any query block scans: from the first block's window start to T
+  const int64_t P = a.T - a.L;
+  const int64_t lo = (a.kv_bf16 && a.window > 0) ? std::max<int64_t>(0, P - a.window + 1) / kt * kt : 0;
+  const int64_t tiles = (a.T - lo + kt - 1) / kt;
+  int S = requested;
+  if (S <= 0) {
+    // one workgroup per CU: split only a grid below half the chip, and keep
+    // at least two tiles per split
+    const int64_t nwg = (int64_t)p.nqb * a.Hkv * a.B;
+    S = nwg >= 128 ? 1 : (int)std::min<int64_t>(PREFILL_MAX_SPLITS, (256 + nwg - 1) / nwg);
+    S = (int)std::min<int64_t>(S, std::max<int64_t>(1, tiles / 2));
+  }
+  S = std::max(1, std::min(S, PREFILL_MAX_SPLITS));
+  S = (int)std::min<int64_t>(S, std::max<int64_t>(1, tiles));
+  const int64_t per = (tiles + S - 1) / S;  // tiles per split
+  p.S = (int)((tiles + per - 1) / per);
+  p.split_lo = lo;
+  p.split_len = per * kt;
+  if (p.S == 1) {  // one range covering everything
+    p.split_lo = 0;
+    p.split_len = a.T + kt;
+  }
+  return p;
+}
+
+size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S) {
+  if (S <= 1) return 0;
+  const size_t rows = (size_t)B * Hkv * S * nqb * 8 * PF_QB;
+  return rows * HEAD_DIM * 4 + rows * 2 * 4;
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.L + PF_QB - 1) / PF_QB), a.Hkv, a.B), block(512);
+  const dim3 grid((unsigned)(a.nqb * a.S), a.Hkv, a.B), block(512);
   if (a.kv_bf16) {
     if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, true>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((prefill_kernel<false, true>), grid, block, 0, stream, a);
   } else {
     if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, block, 0, stream, a);
+  }
+  if (a.S > 1) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)a.L, a.Hq, a.B), dim3(64), 0, stream, a);
   }
   return hipGetLastError();
 }

@@ -196,3 +196,30 @@ def test_capacity_bound(lib):
     """2^24 tokens per KV head is the largest cache the decode accepts."""
     assert _decode(lib, cap=(1 << 24) + 32, T=100) == _lib.REC_EUNSUPPORTED
     assert "16M" in _lib.last_error()
+
+
+def _prefill(lib, **kw):
+    a = dict(L=4, T=1000, cap=1024, splits=0, ws=16, wsb=1 << 30)
+    a.update(kw)
+    return lib.rec_prefill_attn(
+        16, _lib.REC_BF16, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088, 1,
+        1, 8, 1, 128, a["L"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], 16, None,
+    )
+
+
+def test_prefill_split_validation(lib):
+    """Explicit key splits need a workspace; too many splits are refused."""
+    assert _prefill(lib, splits=65) == _lib.REC_EINVAL
+    assert _prefill(lib, splits=3, ws=None, wsb=0) == _lib.REC_EWORKSPACE
+    assert _prefill(lib, splits=3, wsb=1024) == _lib.REC_EWORKSPACE
+    assert _prefill(lib, splits=3, ws=8) == _lib.REC_EALIGN
+
+
+def test_prefill_workspace_bytes(lib):
+    row = 8 * 32 * (128 + 2) * 4  # one query block of one KV head, one split
+    # 4 KV heads x 1 query block = 4 workgroups: the automatic plan allows 64 splits
+    assert lib.rec_prefill_workspace_bytes(1, 4, 20, 0) == 4 * 64 * row
+    # 64 query blocks x 4 KV heads fill the chip: no split, no workspace
+    assert lib.rec_prefill_workspace_bytes(1, 4, 2048, 0) == 0
+    assert lib.rec_prefill_workspace_bytes(2, 2, 40, 7) == 2 * 2 * 7 * 2 * row
+    assert lib.rec_prefill_workspace_bytes(1, 4, 20, 1) == 0

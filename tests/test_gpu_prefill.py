@@ -116,3 +116,60 @@ def test_prefill_full_size_rows(gpu):
         cache_np = dict(k_bits=8, v_bits=8, kq=kc[:, :, :Ti], ks=ksc[:, :, :Ti], vq=vc[:, :, :Ti], vs=vsc[:, :, :Ti])
         ref = O.split_k_decode_quantized(qf[:, :, i], cache_np, Ti, SCALE, sf, chunk=8192)
         assert_close(of[:, :, i], ref.astype(np.float64), f"row {i}")
+
+
+SPLIT_CASES = [
+    # B, Hq, Hkv, P, L, causal, sinks, dtype, splits (0 = automatic)
+    (1, 32, 4, 5000, 20, True, True, torch.bfloat16, 0),    # a short chat turn over a long cache
+    (1, 8, 1, 3000, 40, True, False, torch.float16, 0),     # two query blocks
+    (2, 16, 2, 2000, 5, False, True, torch.bfloat16, 7),
+    (1, 8, 2, 700, 33, True, True, torch.bfloat16, 64),     # more splits asked than tiles
+    (1, 8, 1, 130, 2, True, True, torch.float16, 3),        # splits past the causal end stay empty
+    (3, 12, 4, 1500, 9, True, True, torch.bfloat16, 1),     # explicitly unsplit
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES,
+                         ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_causal{}_s{}_{}_sp{}".format(*c[:7], str(c[7])[6:], c[8]))
+def test_split_prefill_matches_oracle(gpu, case):
+    """Key-split prefill (partials + merge) equals the oracle as the unsplit
+    kernel does; the automatic plan splits a short chunk over a long cache."""
+    B, Hq, Hkv, P, L, causal, with_sinks, dtype, splits = case
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 41 + T, kind="outliers", frac=0.01)
+    v = synthetic.kv((B, Hkv, T, 128), 42 + T, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, L, 43 + L, dtype=dtype)
+    sinks = torch.randn(Hq, device="cuda") if with_sinks else None
+    cache = QuantizedKVCache(32, 8, 8)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    mask = "causal" if causal else None
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32,
+                 splits=splits or None)
+    torch.cuda.synchronize()
+    rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
+    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None if sinks is None else f32(sinks), mask)
+    assert_close(f32(out), ref, f"case {case}")
+
+
+@pytest.mark.parametrize("splits", [0, 5, 64])
+@pytest.mark.parametrize("window", [0, 300])
+def test_split_prefill_bf16_window(gpu, splits, window):
+    """The bf16-cache prefill with key splits, plain causal and under a
+    sliding window (splits before the window start stay empty)."""
+    from rec_amd import scaled_dot_product_attention
+
+    B, Hq, Hkv, T, L = 1, 16, 2, 3000, 24
+    k = synthetic.kv((B, Hkv, T, 128), 141, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, T, 128), 142, dtype=torch.bfloat16)
+    q = synthetic.query(B, Hq, L, 143, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    out = scaled_dot_product_attention(q, k, v, SCALE, "causal", sinks, out_dtype=torch.float32,
+                                       splits=splits or None, window=window or None)
+    torch.cuda.synchronize()
+    qi = np.arange(T - L, T)[:, None]
+    ki = np.arange(T)[None]
+    mask = (qi >= ki) & ((qi < ki + window) if window else True)
+    kb = k.float().cpu().numpy()
+    vb = v.float().cpu().numpy()
+    ref = O.attention(f32(q), kb, vb, SCALE, sinks=f32(sinks), mask=mask)
+    assert_close(f32(out), ref, f"splits={splits} window={window}")
