@@ -20,7 +20,11 @@
 // Each 128-token K/V tile is loaded once per workgroup, converted into
 // double-buffered LDS (149 KB) and shared by the 8 waves, which compute it in
 // four 32-token units, software-pipelined so that one unit's Q·Kᵀ runs on the
-// matrix cores while the previous unit's softmax runs on the VALU.
+// matrix cores while the previous unit's softmax runs on the VALU.  A grid too
+// small to fill the chip (a short chunk over a long cache) splits the keys:
+// grid x = query blocks x splits, each workgroup writes an unnormalised
+// partial, and prefill_merge_kernel combines the splits as the decode's merge
+// does (megakernel.py:276-318).
 //
 // S^T = K Q^T on 16x16x32 MFMAs (A = 16 tokens x 32 dims from LDS, B = Q^T held
 // in registers), which leaves lane (c, g) with the scores of query row c for
