@@ -409,6 +409,8 @@ def run_prefill(P, L, steps, warmup, seed):
     out = torch.empty((1, HQ, L, D), dtype=torch.float32, device="cuda")
     c._reserve(1, HKV, T, "cuda")
     (kc, ks, _), (vc, vs, _) = c.keys, c.values
+    # key splits when the chunk is short (the automatic plan; none at 2048 queries)
+    ws = torch.empty(max(16, lib.rec_prefill_workspace_bytes(1, HKV, L, 0)), dtype=torch.uint8, device="cuda")
 
     def append():
         st = torch.cuda.current_stream().cuda_stream
@@ -421,7 +423,7 @@ def run_prefill(P, L, steps, warmup, seed):
         st = torch.cuda.current_stream().cuda_stream
         rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3], 8, kc.data_ptr(), ks.data_ptr(),
                                   None, 8, vc.data_ptr(), vs.data_ptr(), None, sinks.data_ptr(), SCALE, 1,
-                                  1, HQ, HKV, D, L, T, c.capacity, 0, None, 0, out.data_ptr(), st)
+                                  1, HQ, HKV, D, L, T, c.capacity, 0, ws.data_ptr(), ws.numel(), out.data_ptr(), st)
         _lib.check(rc, "rec_prefill_attn")
 
     for _ in range(warmup):
@@ -441,7 +443,9 @@ def run_prefill(P, L, steps, warmup, seed):
     pairs = L * P + L * (L + 1) // 2
     flops = 4.0 * D * HQ * pairs
     tflops = flops / (ms_att * 1e-3) / 1e12
-    log(f"prefill: {ms_step:.3f} ms/step, attention {ms_att:.3f} ms = {tflops:.0f} TFLOP/s")
+    kv_bytes = T * HKV * 2 * (D + 2)  # int8 K and V rows and their fp16 scales, read once
+    log(f"prefill {P}+{L}: {ms_step:.3f} ms/step, attention {ms_att:.3f} ms = {tflops:.0f} TFLOP/s, "
+        f"{kv_bytes / (ms_att * 1e-3) / 1e9:.0f} GB/s of K/V")
     del g_step, g_att, c
     torch.cuda.empty_cache()
     return dict(
@@ -454,6 +458,9 @@ def run_prefill(P, L, steps, warmup, seed):
         attention_tflops=round(tflops, 1),
         frac_of_mfma_peak=round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
         mfma_peak_tflops=MFMA_BF16_PEAK_TFLOPS,
+        kv_bytes=kv_bytes,
+        kv_gbs=round(kv_bytes / (ms_att * 1e-3) / 1e9, 2),
+        kv_frac_of_hbm_peak=round(kv_bytes / (ms_att * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         note="Q.K^T on bf16 MFMA, P.V on fp16 MFMA; peak is the dense bf16 figure",
     )
 
@@ -622,9 +629,11 @@ def main(argv=None):
     if not args.no_gemv:
         rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
 
-    rpf = None
+    rpf = rpf_short = None
     if not args.no_prefill:
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
+        # a short chunk over a long cache (a new chat turn): the keys are split
+        rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -759,6 +768,8 @@ def main(argv=None):
         )
     if rpf is not None:
         result["prefill_65536_plus_2048"] = rpf
+    if rpf_short is not None:
+        result["prefill_32768_plus_20"] = rpf_short
     print(json.dumps(result), flush=True)
     return 0
 

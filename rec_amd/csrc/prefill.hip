@@ -475,10 +475,18 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
   const float f = (m == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(m - M);
   float z = wave_sum(f * l);
   if (sink != NEG_INF) z += __builtin_amdgcn_exp2f(sink - M);
-  if (lane < a.S) wts[lane] = f;
+  wts[lane] = f;  // 0 for lanes past the last split
   __syncthreads();
+  // 16 independent loads in flight per round (slots past the last split read
+  // its row again and weigh it 0), not one memory round trip per split
   v2f acc = {0.f, 0.f};
-  for (int sp = 0; sp < a.S; ++sp) acc += wts[sp] * *(const v2f*)(a.ws_acc + row(sp) * HEAD_DIM + 2 * lane);
+  for (int s0 = 0; s0 < a.S; s0 += 16) {
+    v2f x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = *(const v2f*)(a.ws_acc + row(min(s0 + k, a.S - 1)) * HEAD_DIM + 2 * lane);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc += wts[min(s0 + k, PREFILL_MAX_SPLITS - 1)] * x[k];
+  }
   const float inv = z > 0.f ? 1.f / z : 1.f;
   *(v2f*)(a.out + (((int64_t)b * a.Hq + hq) * a.L + i) * HEAD_DIM + 2 * lane) = acc * inv;
 }
