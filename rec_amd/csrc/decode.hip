@@ -453,15 +453,13 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     }
   } else {
     // uint4 V: the A operand is q - z, exact in fp16, and the scale of the
-    // (token, group) goes into the B operand, fp16(p) * s, one B operand per
+    // (token, group) goes into the B operand, fp16(p * s) with the product
+    // formed in fp32 and rounded once (as int8 V's P'), one B operand per
     // 32-dim group.  The nibble unpack yields positions (e, e+4) of the lane's
     // run as one fp16 pair: low nibbles under the fp16 exponent of 1024 read
     // 1024 + q, high nibbles under that of 64 read 64 + q.  Scales and
     // zero-points are stored in that pair order (s4_slot), so dword e of a
     // run is the pair for unpack step e.
-    v2h pp[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) pp[e] = (v2h){(_Float16)p[e], (_Float16)p[e + 4]};
     const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -471,9 +469,12 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       for (int e = 0; e < 4; ++e) {
         // copies first: a bit_cast of a vector subscript reads element 0
         const uint32_t sw = (uint32_t)vs4[g][e], zw = (uint32_t)vz4[g][e];
-        const v2h t = pp[e] * __builtin_bit_cast(v2h, sw);
-        pb[2 * e] = t[0];
-        pb[2 * e + 1] = t[1];
+        const v2h sv = __builtin_bit_cast(v2h, sw);
+        // fma with a +0 addend (p * s but for the sign of a zero product, which
+        // the sum does not see) lowers to v_fma_mix*, which reads the fp16
+        // scale directly; a plain multiply costs a conversion per scale
+        pb[2 * e] = (_Float16)__builtin_fmaf(p[e], (float)sv[0], 0.f);
+        pb[2 * e + 1] = (_Float16)__builtin_fmaf(p[e + 4], (float)sv[1], 0.f);
         zq[e] = __builtin_bit_cast(v2h, zw) + ((e & 1) ? k64 : k1024);
       }
 #pragma unroll
