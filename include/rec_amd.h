@@ -85,7 +85,11 @@ int rec_kv_append(const void* k_new, const void* v_new, int in_dtype,
 /* Split count the library would pick for a decode over T tokens. */
 int rec_decode_default_splits(int B, int Hkv, int64_t T);
 
-/* Bytes of workspace a decode with up to `splits` splits needs. */
+/*
+ * Bytes of workspace a decode call with `splits` requested splits needs, for
+ * every entry point (a fused append launches at most max(splits, 2) splits;
+ * splits <= 0: the largest plan).
+ */
 size_t rec_decode_workspace_bytes(int B, int Hkv, int splits);
 
 /*

@@ -80,6 +80,21 @@ def _check_query(queries):
         raise NotImplementedError(f"head_dim {queries.shape[-1]} is not supported (128 only)")
 
 
+def _check_cache_shapes(queries, keys: QuantizedKV, values: QuantizedKV):
+    """The kernels index the cache by (batch, KV head) from the query shape
+    and cannot see tensor sizes: refuse a batch or head count the cache does
+    not hold before anything is launched."""
+    B, Hq = queries.shape[:2]
+    kb, kh = keys.codes.shape[:2]
+    if tuple(values.codes.shape[:2]) != (kb, kh) or values.length != keys.length:
+        raise ValueError(f"keys (B={kb}, Hkv={kh}, T={keys.length}) and values (B={values.codes.shape[0]}, "
+                         f"Hkv={values.codes.shape[1]}, T={values.length}) do not match")
+    if B != kb:
+        raise ValueError(f"queries have batch {B}, the cache holds {kb}")
+    if Hq % kh != 0:
+        raise ValueError(f"{Hq} query heads is not a multiple of the cache's {kh} KV heads")
+
+
 def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, splits, out,
                    k_new=None, v_new=None, T=None, capacity=None):
     lib = _lib.load()
@@ -197,6 +212,7 @@ def quantized_attention_with_sinks(
         raise ValueError(f"group_size={group_size} does not match the cache's format")
     if not keys.affine and 4 in (key_bits, value_bits) and group_size != 32:
         raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
+    _check_cache_shapes(queries, keys, values)
     if mask is not None and not (isinstance(mask, str) and mask == "causal"):
         raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
     if L == 1:
@@ -353,6 +369,10 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         if fused and L == 1:
             if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
                 raise ValueError("a fused decode step takes one new K/V token of a float dtype")
+            st = cache.storage
+            if tuple(keys.shape[:2]) != (st.batch, st.n_kv_heads) or B != st.batch or Hq % st.n_kv_heads != 0:
+                raise ValueError(f"queries (B={B}, Hq={Hq}) / new keys (B={keys.shape[0]}, Hkv={keys.shape[1]}) "
+                                 f"do not match the storage (B={st.batch}, Hkv={st.n_kv_heads})")
             T = cache.offset + 1
             cache._reserve(T)
             data = cache.storage.layer(cache.index)
@@ -373,8 +393,14 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         if mask is not None and not (isinstance(mask, str) and mask == "causal"):
             raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
         Bk, H = keys.shape[:2]
+        if cache.keys is not None and tuple(cache.keys[0].shape[:2]) != (Bk, H):
+            raise ValueError(f"new keys have (B, Hkv) = ({Bk}, {H}), the cache holds "
+                             f"{tuple(cache.keys[0].shape[:2])}")
+        if B != Bk:
+            raise ValueError(f"queries have batch {B}, the new keys {Bk}")
         cache._reserve(Bk, H, cache.offset + 1, keys.device)
         k_kv, v_kv = cache._view()
+        _check_cache_shapes(queries, k_kv, v_kv)
         kn = keys if _rows_aligned(keys) else keys.contiguous()
         vn = values if _rows_aligned(values) else values.contiguous()
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)

@@ -243,6 +243,9 @@ int rec_decode_default_splits(int B, int Hkv, int64_t T) {
 
 size_t rec_decode_workspace_bytes(int B, int Hkv, int splits) {
   if (splits <= 0 || splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
+  // a fused append adds the newest token's split to max(splits - 1, 1)
+  // regular ones (effective_splits), so a request for one split launches two
+  if (splits < 2) splits = 2;
   return ws_layout(B, Hkv, splits).total;
 }
 

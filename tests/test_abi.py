@@ -223,3 +223,31 @@ def test_prefill_workspace_bytes(lib):
     assert lib.rec_prefill_workspace_bytes(1, 4, 2048, 0) == 0
     assert lib.rec_prefill_workspace_bytes(2, 2, 40, 7) == 2 * 2 * 7 * 2 * row
     assert lib.rec_prefill_workspace_bytes(1, 4, 20, 1) == 0
+
+
+def _append_attn(lib, **kw):
+    a = dict(B=1, Hq=8, Hkv=1, T=100, cap=128, splits=0, ws=8, wsb=1 << 30)
+    a.update(kw)
+    return lib.rec_decode_append_attn(
+        16, 0, 0, 0, 16, 16, 0, 0, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088,
+        a["B"], a["Hq"], a["Hkv"], 128, a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], 16, None,
+    )
+
+
+@pytest.mark.parametrize("B,Hkv,splits", [(64, 4, 0), (1, 1, 1), (1, 4, 1), (2, 4, 2), (1, 4, 0)])
+def test_fused_decode_workspace_size(lib, B, Hkv, splits):
+    """A fused decode (append + attend) adds the newest token's split to the
+    regular ones, so a request for one split launches two.  The size the
+    library reports for a request must cover that plan: called with exactly
+    that many bytes, the size check passes and the (deliberately misaligned)
+    workspace pointer is what is refused -- nothing is launched either way."""
+    req = splits if splits > 0 else lib.rec_decode_default_splits(B, Hkv, 4000)
+    need = lib.rec_decode_workspace_bytes(B, Hkv, req)
+    rc = _append_attn(lib, B=B, Hq=8 * Hkv, Hkv=Hkv, T=4000, cap=4096, splits=splits, ws=8, wsb=need)
+    assert rc == _lib.REC_EALIGN, _lib.last_error()
+    assert "workspace must be 16-byte aligned" in _lib.last_error()
+    # one byte short of a two-split plan is refused for a one-split request
+    if req == 1:
+        short = lib.rec_decode_workspace_bytes(B, Hkv, 2) - 1
+        assert _append_attn(lib, B=B, Hq=8 * Hkv, Hkv=Hkv, T=4000, cap=4096, splits=1, ws=16, wsb=short) == (
+            _lib.REC_EWORKSPACE)
