@@ -28,12 +28,14 @@
 // of the query per head (relative error < 2^-16 of the head's largest
 // element), well inside the 1e-3 output tolerance.
 //
-// P·V runs on v_mfma_f32_16x16x32_f16.  int8 V: A = Vᵀ (16 dims × 32 tokens,
-// exact small integers in fp16) and B = P'ᵀ where P' = p · v_scale is rounded
-// to fp16 once, as the reference rounds probabilities to the query dtype
-// (model.py:132-133).  uint4 V: A = the dequantized (q - z) · s in fp16 (one
-// rounding) and B = p in fp16.  The token-blocked V layout makes each A operand
-// one load per lane.
+// P·V runs on v_mfma_f32_16x16x32_f16: A = Vᵀ (16 dims × 32 tokens of exact
+// small integers in fp16: int8 codes, 4-bit q - z, affine q) and B = P'ᵀ with
+// P' = p · s the probability times the token's (group's) V scale, as an fp16
+// high part in columns 0-7 and the rounding remainder in columns 8-15, which
+// would otherwise repeat columns 0-7 (see EXACT_PV_BELOW for when the 4-bit
+// and affine formats take the remainder).  The reference rounds probabilities
+// to the query dtype before its P·V (model.py:132-133).  The token-blocked V
+// layout makes each A operand one load per lane.
 //
 // Softmax runs in the log2 domain (log2(e) folded into the query scale).
 #include "kernels.h"
@@ -255,7 +257,7 @@ __device__ __forceinline__ float bf16_at(const v4i& w, int slot) {
   return __builtin_bit_cast(float, (slot & 1) ? (x & 0xffff0000u) : (x << 16));
 }
 
-template <int KB, int VB>
+template <int KB, int VB, bool EXACT>
 __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, float qsum_a,
                                               float qsum_b, int valid, int lane, char* meta) {
   const int c = lane & 15, kg = lane >> 4;
@@ -381,11 +383,27 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   // exceeds the bound iff one of its four lanes' own maxima does, so the
   // cross-lane reduction and the rescale run only then (after the first
   // chunk, rarely).
+  //
+  // Range: the fp16 operand p·s stays finite while p·|s| < 65504.  A V scale
+  // of 2 or more (fp16 / bf16 exponent bit 14; int8 |v| >= 254, a 4-bit
+  // group range >= 30) makes the chunk's gap 0 for the lanes that hold it
+  // (int8: the lane's own eight scales; 4-bit and affine: any scale of the
+  // block, a wave vote), so their p <= 1 and p·|s| <= |s| <= 65504 (fp16
+  // scales; an affine bf16 scale above that is out of range).
+  bool big;
+  if constexpr (VB == 8) {
+    big = ((uint32_t)(vs[0] | vs[1] | vs[2] | vs[3]) & 0x40004000u) != 0;
+  } else if constexpr (VB == FMT_A4) {
+    big = __ballot(lane < 32 && (R.m[2] & 0x40004000u) != 0) != 0;  // lanes 32-63 hold biases
+  } else {
+    big = __ballot((R.m[2] & 0x40004000u) != 0) != 0;
+  }
+  const float gap = big ? 0.f : RESCALE_GAP;
   float cmax = s[0];
 #pragma unroll
   for (int idx = 1; idx < 8; ++idx) cmax = maxp(cmax, s[idx]);
   cmax *= qsc;  // qsc > 0
-  if (__ballot(cmax > st.m + RESCALE_GAP)) {
+  if (__ballot(cmax > st.m + gap)) {
     cmax = max_xor32(max_xor16(cmax));
     const float m_new = fmaxf(st.m, cmax);
     const float factor = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first chunk, 1 if unchanged
@@ -406,10 +424,28 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   }
 
   // ---------------- P·V ----------------
+  // The B operand carries P' = p·s (s the V scale of the token, or of its
+  // group) in two parts: columns c < 8 the high part hi = fp16(P'), columns
+  // c >= 8 -- which would otherwise repeat columns c - 8 -- the remainder
+  // lo = fp16(P' - hi), each rounded once from the exact product (v_fma_mix),
+  // so the two column halves together hold P' to about 2^-22 and are added
+  // when the wave's partial is formed.  p_lo = p * lo_sel is p in the lanes
+  // c >= 8 and 0 elsewhere: there fp16(p_lo·s) is hi, and every lane's operand
+  // is fp16(p·s - that), i.e. hi in columns c < 8 and lo in columns c >= 8.
+  // int8 V always takes both parts (three VALU ops per element); 4-bit and
+  // affine V, whose P' has four (two) groups per token, only when EXACT
+  // (fewer than EXACT_PV_BELOW cached tokens), else every column holds hi,
+  // rounded once, and only columns c < 8 are read.
+  const float lo_sel = c < 8 ? 0.f : 1.f;
   if constexpr (VB == 8) {
     v8h pb;
 #pragma unroll
-    for (int idx = 0; idx < 8; ++idx) pb[idx] = (_Float16)(p[idx] * half_at(vs, idx));
+    for (int idx = 0; idx < 8; ++idx) {
+      const uint32_t sw = (uint32_t)vs[idx >> 1];
+      const _Float16 sh = __builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (sw >> 16) : (sw & 0xffffu)));
+      const _Float16 hi = (_Float16)__builtin_fmaf(p[idx] * lo_sel, (float)sh, 0.f);
+      pb[idx] = (_Float16)__builtin_fmaf(p[idx], (float)sh, -(float)hi);
+    }
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       const v8h a0 = i8x8_to_h8((uint32_t)R.v8[n >> 1][2 * (n & 1)], (uint32_t)R.v8[n >> 1][2 * (n & 1) + 1]);
@@ -418,11 +454,14 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   } else if constexpr (VB == FMT_A4) {
     // affine 4-bit V, v = s q + b per 64-dim group: the A operand is q, exact
     // in fp16 (nibble under the fp16 exponent of 1024 or 64, minus that
-    // offset), B = fp16(p·s) per group, and Σ p·b per group is kept aside and
-    // added to the group's dims at the end.  Scales and biases are stored in
-    // the nibble unpack's pair order (s4_slot): dword e of a run holds
-    // positions (e, e+4).
+    // offset), B = P' = p·s per group (high and low parts as above), and
+    // Σ p·b per group is kept aside and added to the group's dims at the end.
+    // Scales and biases are stored in the nibble unpack's pair order
+    // (s4_slot): dword e of a run holds positions (e, e+4).
     const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+    float p_lo[8];
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) p_lo[idx] = p[idx] * lo_sel;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       v8h pb;
@@ -431,8 +470,14 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         const uint32_t sw = (uint32_t)vs4[g][e], bw = (uint32_t)vz4[g][e];
         const float slo = __builtin_bit_cast(float, sw << 16), shi = __builtin_bit_cast(float, sw & 0xffff0000u);
         const float blo = __builtin_bit_cast(float, bw << 16), bhi = __builtin_bit_cast(float, bw & 0xffff0000u);
-        pb[2 * e] = (_Float16)(p[e] * slo);
-        pb[2 * e + 1] = (_Float16)(p[e + 4] * shi);
+        if constexpr (EXACT) {
+          const _Float16 h0 = (_Float16)(p_lo[e] * slo), h1 = (_Float16)(p_lo[e + 4] * shi);
+          pb[2 * e] = (_Float16)__builtin_fmaf(p[e], slo, -(float)h0);
+          pb[2 * e + 1] = (_Float16)__builtin_fmaf(p[e + 4], shi, -(float)h1);
+        } else {
+          pb[2 * e] = (_Float16)(p[e] * slo);
+          pb[2 * e + 1] = (_Float16)(p[e + 4] * shi);
+        }
         st.vb[g] = fmaf(p[e], blo, fmaf(p[e + 4], bhi, st.vb[g]));
       }
 #pragma unroll
@@ -453,14 +498,16 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     }
   } else {
     // uint4 V: the A operand is q - z, exact in fp16, and the scale of the
-    // (token, group) goes into the B operand, fp16(p * s) with the product
-    // formed in fp32 and rounded once (as int8 V's P'), one B operand per
-    // 32-dim group.  The nibble unpack yields positions (e, e+4) of the lane's
-    // run as one fp16 pair: low nibbles under the fp16 exponent of 1024 read
-    // 1024 + q, high nibbles under that of 64 read 64 + q.  Scales and
-    // zero-points are stored in that pair order (s4_slot), so dword e of a
-    // run is the pair for unpack step e.
+    // (token, group) goes into the B operand, P' = p·s in high and low parts
+    // as above, one B operand per 32-dim group.  The nibble unpack yields
+    // positions (e, e+4) of the lane's run as one fp16 pair: low nibbles under
+    // the fp16 exponent of 1024 read 1024 + q, high nibbles under that of 64
+    // read 64 + q.  Scales and zero-points are stored in that pair order
+    // (s4_slot), so dword e of a run is the pair for unpack step e.
     const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+    float p_lo[8];
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) p_lo[idx] = p[idx] * lo_sel;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       v8h pb;
@@ -470,11 +517,17 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         // copies first: a bit_cast of a vector subscript reads element 0
         const uint32_t sw = (uint32_t)vs4[g][e], zw = (uint32_t)vz4[g][e];
         const v2h sv = __builtin_bit_cast(v2h, sw);
-        // fma with a +0 addend (p * s but for the sign of a zero product, which
-        // the sum does not see) lowers to v_fma_mix*, which reads the fp16
-        // scale directly; a plain multiply costs a conversion per scale
-        pb[2 * e] = (_Float16)__builtin_fmaf(p[e], (float)sv[0], 0.f);
-        pb[2 * e + 1] = (_Float16)__builtin_fmaf(p[e + 4], (float)sv[1], 0.f);
+        // fmas on an fp16 scale lower to v_fma_mix*, which read the fp16
+        // operand directly (a plain multiply costs a conversion per scale)
+        if constexpr (EXACT) {
+          const _Float16 h0 = (_Float16)__builtin_fmaf(p_lo[e], (float)sv[0], 0.f);
+          const _Float16 h1 = (_Float16)__builtin_fmaf(p_lo[e + 4], (float)sv[1], 0.f);
+          pb[2 * e] = (_Float16)__builtin_fmaf(p[e], (float)sv[0], -(float)h0);
+          pb[2 * e + 1] = (_Float16)__builtin_fmaf(p[e + 4], (float)sv[1], -(float)h1);
+        } else {
+          pb[2 * e] = (_Float16)__builtin_fmaf(p[e], (float)sv[0], 0.f);
+          pb[2 * e + 1] = (_Float16)__builtin_fmaf(p[e + 4], (float)sv[1], 0.f);
+        }
         zq[e] = __builtin_bit_cast(v2h, zw) + ((e & 1) ? k64 : k1024);
       }
 #pragma unroll
@@ -504,7 +557,7 @@ struct Depth {
   static constexpr int value = 2;
 };
 
-template <int KB, int VB, int WAVES>
+template <int KB, int VB, int WAVES, bool EXACT>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) {
   using LD = Lds<WAVES>;
   __shared__ __attribute__((aligned(16))) char smem[LD::bytes];
@@ -625,13 +678,23 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
       const int i = i0 + j;
       load_chunk<KB, VB>(buf[(j + NBUF - 1) % NBUF], R, lo, i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1));
       if (i < n_w)
-        process_chunk<KB, VB>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane,
+        process_chunk<KB, VB, EXACT>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane,
                               smem + LD::meta + wave * 1024);
     }
   }
 
   // ---------------- wave partial -> LDS ----------------
   st.l = sum_xor32(sum_xor16(st.l));
+  // the P·V sums of the high (columns c < 8) and low (c + 8) parts of P'
+  if constexpr (VB == 8 || EXACT) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = st.acc[n][i];  // copy first: a bit_cast of a vector subscript reads element 0
+        st.acc[n][i] = x + dpp_ror8f(x);
+      }
+  }
   if constexpr (VB == FMT_A4) {  // the bias terms join every dim of their group
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -760,18 +823,24 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   }
 }
 
-template <int KB, int VB, int W>
+template <int KB, int VB, int W, bool EXACT>
 static void launch_partial(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_kernel<KB, VB, W>), dim3(a.S, a.Hkv, a.B), dim3(64 * W), 0, stream, a);
+  hipLaunchKernelGGL((decode_kernel<KB, VB, W, EXACT>), dim3(a.S, a.Hkv, a.B), dim3(64 * W), 0, stream, a);
+}
+
+template <int KB, int VB, int W>
+static void launch_partial_pv(const DecodeArgs& a, hipStream_t stream) {
+  if (a.T < EXACT_PV_BELOW) launch_partial<KB, VB, W, true>(a, stream);
+  else launch_partial<KB, VB, W, false>(a, stream);
 }
 
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream) {
-  if (kb == 8 && vb == 8) launch_partial<8, 8, 4>(a, stream);
-  else if (kb == 8 && vb == 4) launch_partial<8, 4, 4>(a, stream);
-  else if (kb == 4 && vb == 8) launch_partial<4, 8, 4>(a, stream);
-  else if (kb == FMT_A8 && vb == FMT_A4) launch_partial<FMT_A8, FMT_A4, 4>(a, stream);
-  else if (a.span / CH >= UINT4_WIDE_CHUNKS) launch_partial<4, 4, 8>(a, stream);
-  else launch_partial<4, 4, 4>(a, stream);
+  if (kb == 8 && vb == 8) launch_partial<8, 8, 4, true>(a, stream);
+  else if (kb == 8 && vb == 4) launch_partial_pv<8, 4, 4>(a, stream);
+  else if (kb == 4 && vb == 8) launch_partial<4, 8, 4, true>(a, stream);
+  else if (kb == FMT_A8 && vb == FMT_A4) launch_partial_pv<FMT_A8, FMT_A4, 4>(a, stream);
+  else if (a.span / CH >= UINT4_WIDE_CHUNKS) launch_partial_pv<4, 4, 8>(a, stream);
+  else launch_partial_pv<4, 4, 4>(a, stream);
   return hipGetLastError();
 }
 

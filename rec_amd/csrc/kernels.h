@@ -43,6 +43,17 @@ struct DecodeArgs {
   int t_split_end;  // end of the regular splits; a fused append adds one split [t_split_end, T)
 };
 
+// P·V takes the V-scaled probabilities P' = p·s as an fp16 operand.  Rounded
+// once, each carries a relative error up to 2^-11; for a query row that sees
+// n keys the output error is about 2^-12·|v|·sqrt(Σ w_t²) (w the softmax
+// weights), which stays inside 2e-3 once the weights spread over a few
+// hundred keys, but not for a row that sees a handful of keys with large,
+// cancelling values.  So below this many visible keys the kernels carry P'
+// as a high and a low fp16 part (exact to ~2^-22): in the decode for the
+// 4-bit and affine V formats (int8 V always takes both parts, at almost no
+// cost), and in the prefill, where the low part costs a second P·V MFMA.
+constexpr int64_t EXACT_PV_BELOW = 8192;
+
 struct PrefillArgs {
   const void* q;
   int q_dtype;                 // DT_BF16 (bf16 MFMA) or DT_F16 (fp16 MFMA)

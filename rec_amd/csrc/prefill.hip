@@ -219,12 +219,22 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
 // finite score), thr, the bound past which a score moves it (-inf until the
 // row has seen a finite score, then RESCALE_GAP), and l_run, the sum of
 // probabilities.  t = s * ksc - m_use is one fma per score.
-template <int VROW>
+template <int VROW, bool EXACT>
 __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
                                                 const float* VS, float (&m_use)[2], float (&thr)[2],
                                                 float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end, int qabs0,
                                                 int causal, int window, bool mask, int c, int g) {
-  v8h pb[2];
+  v8h pb[2], pl[2];  // P'^T: high parts, and (EXACT) the remainders
+  // Range: P' = p·s feeds an fp16 operand, finite while p·s < 65504.  A V
+  // scale of 2 or more among the lane's tokens (fp32 exponent bit 30;
+  // |v| >= 254) makes its bound 0 for this unit, so its p <= 1 and
+  // P' <= s <= 65504.
+  bool big;
+  {
+    const v4i w0 = *(const v4i*)(&VS[4 * g]), w1 = *(const v4i*)(&VS[16 + 4 * g]);
+    const v4i o = w0 | w1;
+    big = ((uint32_t)(o[0] | o[1] | o[2] | o[3]) & 0x40000000u) != 0;
+  }
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     // scale (K scale x softmax scale) and offset in one fma, mask, online
@@ -256,7 +266,7 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     // cross-lane max, an exp and 32 multiplies per row tile) runs far less
     // often (measured 2% faster).  A row's max passes the bound iff one of its
     // four lanes' maxima does.
-    if (__ballot(cmax > thr[rt])) {
+    if (__ballot(cmax > (big ? fminf(thr[rt], 0.f) : thr[rt]))) {
       cmax = max_xor32(max_xor16(cmax));  // the row's max of t
       // a row with finite scores so far moves to max(offset, row max); a new
       // row takes its first finite max; an all-masked row stays
@@ -282,7 +292,9 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
         const float p = __builtin_amdgcn_exp2f(t[4 * j + i]);
         lsum += p;
         // B operand of P·V: k index 8g + 4j + i = cache position of token 16j + 4g + i
-        pb[rt][4 * j + i] = (_Float16)(p * vsc[i]);
+        const _Float16 hi = (_Float16)(p * vsc[i]);
+        pb[rt][4 * j + i] = hi;
+        if constexpr (EXACT) pl[rt][4 * j + i] = (_Float16)__builtin_fmaf(p, vsc[i], -(float)hi);
       }
     }
     l_run[rt] += lsum;
@@ -291,11 +303,14 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
   for (int n = 0; n < 8; ++n) {
     const v8h va = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt], acc[n][rt], 0, 0, 0);
+    for (int rt = 0; rt < 2; ++rt) {
+      acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt], acc[n][rt], 0, 0, 0);
+      if constexpr (EXACT) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[rt], acc[n][rt], 0, 0, 0);
+    }
   }
 }
 
-template <bool BF16, bool KVB>
+template <bool BF16, bool KVB, bool EXACT>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   typedef typename MT<BF16>::elem E;
   typedef typename MT<BF16>::vec V8;
@@ -390,7 +405,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
         if (pend) {
           // the unit before: this tile's unit u - 1, or the previous tile's last
           const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? PF_KT - 32 : 32 * (u - 1);
-          softmax_pv_unit<VROW>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
+          softmax_pv_unit<VROW, EXACT>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
                                 acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
         }
         pend = live;
@@ -410,7 +425,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   // still pending: the last tile's last unit (every unit of a tile is visited,
   // and a tile has an even number of units, so its scores are in sc[1])
   if (active && pend)
-    softmax_pv_unit<VROW>(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_use, thr,
+    softmax_pv_unit<VROW, EXACT>(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_use, thr,
                           l_run, acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
 
   if (!active) return;
@@ -526,15 +541,29 @@ size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S) {
   return rows * HEAD_DIM * 4 + rows * 2 * 4;
 }
 
+template <bool EXACT>
+static void launch_prefill_pv(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  if (a.kv_bf16) {
+    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, true, EXACT>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((prefill_kernel<false, true, EXACT>), grid, block, 0, stream, a);
+  } else {
+    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, false, EXACT>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((prefill_kernel<false, false, EXACT>), grid, block, 0, stream, a);
+  }
+}
+
+// Fewest keys any query row of the launch sees: the first row's causal
+// prefix (and at most the window), or all T keys without a causal mask.
+static int64_t fewest_visible_keys(const PrefillArgs& a) {
+  int64_t n = a.causal ? a.T - a.L + 1 : a.T;
+  if (a.kv_bf16 && a.window > 0 && a.window < n) n = a.window;
+  return n;
+}
+
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)(a.nqb * a.S), a.Hkv, a.B), block(512);
-  if (a.kv_bf16) {
-    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((prefill_kernel<false, true>), grid, block, 0, stream, a);
-  } else {
-    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, block, 0, stream, a);
-  }
+  if (fewest_visible_keys(a) < EXACT_PV_BELOW) launch_prefill_pv<true>(a, grid, block, stream);
+  else launch_prefill_pv<false>(a, grid, block, stream);
   if (a.S > 1) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

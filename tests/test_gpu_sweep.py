@@ -1,7 +1,8 @@
 """A seeded sweep of shapes through every decode and prefill format against
 the oracle: batch sizes, GQA ratios, ragged token counts, split counts, query
 dtypes and sinks drawn from a fixed generator (the same 40 cases every run;
-REC_SWEEP_CASES=n draws n, the first 40 being these).
+REC_SWEEP_CASES=n draws n, the first 40 being these; two cases of the
+400-case draw always run as regressions).
 Outputs within 2e-3 abs + 1e-3 rel of the float64 oracle over the cache read
 back from the GPU and dequantized (bf16-rounded too for prefill over 4-bit and
 affine caches, which attends over bf16 copies)."""
@@ -62,7 +63,14 @@ def oracle_xhat(kv):
     return dequant(kv.bits, codes.cpu().numpy(), scales.cpu().numpy(), None if extra is None else extra.cpu().numpy())
 
 
-@pytest.mark.parametrize("case", draw(), ids=lambda c: "{}_B{}_Hq{}_Hkv{}_T{}_L{}_{}_sp{}_s{}_seed{}".format(
+# Cases 182 and 204 of the 400-case draw once exceeded the tolerance (prefill
+# rows that see 10 and 3 tokens, outlier channels near |v| = 25, when each
+# probability entered the P·V product rounded once to fp16): always run.
+REGRESSION = [draw(400)[182], draw(400)[204]]
+CASES = draw() + [c for c in REGRESSION if c not in draw()]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "{}_B{}_Hq{}_Hkv{}_T{}_L{}_{}_sp{}_s{}_seed{}".format(
     c[0], c[1], c[2], c[3], c[4], c[5], str(c[6])[6:], c[7], c[8], c[9]))
 def test_sweep(gpu, case):
     fmt, B, Hq, Hkv, T, L, dt, splits, with_sinks, seed = case
