@@ -13,8 +13,10 @@ independent cache instances totalling more than 1 GB (32 x 34 MB at 32K,
 4 x 268 MB at 252K).  Each instance starts ``n`` tokens short of the context
 and grows by one token per step it serves.
 
-Timing: W eager warm-up steps, then K steps captured in one HIP graph and
-replayed once between synchronisations (HIP events on the launch stream).  A
+Timing: W eager warm-up steps, then K steps captured in one HIP graph, one
+untimed warm replay, then five replays of exactly K steps each between
+synchronisations (HIP events on the launch stream); the headline is their
+median.  A
 step is two launches: the fused append + attention kernel and the split
 merge.  For the roofline, K launches of the attention kernel alone
 (``rec_decode_partial``) are captured and timed the same way.  Algorithmic
@@ -178,18 +180,35 @@ class DecodeWorkload:
         _lib.check(rc, "append")
 
 
-def _replay_timed(torch, graph, n):
-    """Replay a captured graph once between synchronisations; ms per launch."""
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
+def _queue_ahead(torch):
+    """Keep the GPU busy for ~100 us before a timed region, so the host has
+    enqueued the start event and the graph's launches by the time the GPU
+    reaches them: the region then times the steps, not the host's submission
+    latency.  Runs before the start event, outside the timed region."""
+    if hasattr(torch.cuda, "_sleep"):
+        torch.cuda._sleep(200_000)  # GPU clock cycles of a one-thread spin kernel
+
+
+def _replay_timed(torch, graph, n, reps=1):
+    """Replay a captured graph of n launches: one untimed warm replay (the
+    first replay of a graph also uploads it), then `reps` timed replays, each
+    between synchronisations with HIP events on the launch stream.  Returns
+    the ms per launch of every timed replay (the first one is the headline)."""
     graph.replay()
-    e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / n
+    out = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        _queue_ahead(torch)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) / n)
+    return out if reps > 1 else out[0]
 
 
-def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, parts=10, batch=1):
+def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, batch=1, reps=5):
     import torch
 
     total = warmup + 2 * steps
@@ -199,18 +218,15 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, pa
     for s in range(warmup):
         w.step(s)
     torch.cuda.synchronize()
-    # K whole steps (attention kernel + merge kernel) in `parts` graphs of
-    # about K / parts steps each, timed one replay apiece: the per-step time is
-    # the total over K, the spread that of the parts' per-step means
-    parts = max(1, min(parts, steps))
-    bounds = [warmup + steps * i // parts for i in range(parts + 1)]
-    g_steps, step_T = [], []
-    for i in range(parts):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for s in range(bounds[i], bounds[i + 1]):
-                step_T.append(w.step(s))
-        g_steps.append((g, bounds[i + 1] - bounds[i]))
+    # K whole steps (attention kernel + merge kernel) in one graph.  A replay
+    # rewrites the appended tokens at the same positions with the same values,
+    # so every replay does the same work: one untimed warm replay, then `reps`
+    # timed replays of exactly K steps each; the headline is their median,
+    # p10/p50/p90 their spread.
+    g_step, step_T = torch.cuda.CUDAGraph(), []
+    with torch.cuda.graph(g_step):
+        for s in range(warmup, warmup + steps):
+            step_T.append(w.step(s))
     # K launches of the attention kernel alone, the dominant kernel
     g_kern, kern_T = torch.cuda.CUDAGraph(), []
     with torch.cuda.graph(g_kern):
@@ -225,13 +241,13 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, pa
     with torch.cuda.graph(g_app):
         for s in range(steps):
             w.append_only(s)
-    part_ms = [_replay_timed(torch, g, n) for g, n in g_steps]
-    ms_per_step = sum(m * n for m, (_, n) in zip(part_ms, g_steps)) / steps
+    rep_ms = _replay_timed(torch, g_step, steps, reps)
+    ms_per_step = float(np.median(rep_ms))
     kernel_ms = _replay_timed(torch, g_kern, steps)
     att_ms = _replay_timed(torch, g_att, steps)
     app_ms = _replay_timed(torch, g_app, steps)
-    p10, p50, p90 = (float(np.percentile(part_ms, p)) for p in (10, 50, 90))
-    log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step (parts p10/p50/p90 {p10 * 1e3:.2f}/"
+    p10, p50, p90 = (float(np.percentile(rep_ms, p)) for p in (10, 50, 90))
+    log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step (replays p10/p50/p90 {p10 * 1e3:.2f}/"
         f"{p50 * 1e3:.2f}/{p90 * 1e3:.2f}); attention kernel {kernel_ms * 1e3:.2f} us; unfused: attention "
         f"{att_ms * 1e3:.2f} us + append {app_ms * 1e3:.2f} us")
     bytes_step = float(np.mean([step_bytes(t, batch, k_bits=bits, v_bits=bits) for t in step_T]))
@@ -251,7 +267,7 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, pa
         unfused_attention_us=att_ms * 1e3,
         unfused_append_us=app_ms * 1e3,
     )
-    del g_steps, g_kern, g_att, g_app, w
+    del g_step, g_kern, g_att, g_app, w
     torch.cuda.empty_cache()
     return res
 
@@ -465,6 +481,28 @@ def run_prefill(P, L, steps, warmup, seed):
     )
 
 
+def host_cores():
+    """Host cores this process may run on (its CPU affinity), bounded by the
+    thread budget OMP_NUM_THREADS when the environment sets one (a shared GPU
+    host gives each GPU's jobs a share of its cores that way)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(T, seed, budget_s=10.0):
     """The oracle's split-K decode over one 32K instance on the host cores."""
     import torch
@@ -477,7 +515,7 @@ def cpu_baseline(T, seed, budget_s=10.0):
         from threadpoolctl import threadpool_limits
     except ImportError:  # pragma: no cover
         threadpool_limits = None
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    cores = host_cores()
     c = rec_amd.QuantizedKVCache(32, 8, 8, max_tokens=T)
     k = synthetic.kv((1, HKV, T - 1, D), seed, kind="outliers", frac=0.01)
     v = synthetic.kv((1, HKV, T - 1, D), seed + 1, kind="outliers", frac=0.01)
@@ -519,6 +557,8 @@ def cpu_baseline(T, seed, budget_s=10.0):
         value=step_bytes(T) / sec / 1e9,
         unit="GB/s",
         cores=cores,
+        affinity_cores=len(os.sched_getaffinity(0)),
+        cpu_model=cpu_model(),
         kind="port",
         us_per_step=sec * 1e6,
         sample=f"{len(times)} decode steps (1-token int8 append + attention) of the 32K workload, one cache "
@@ -527,7 +567,7 @@ def cpu_baseline(T, seed, budget_s=10.0):
 
 
 def _step_detail(r):
-    """Spread of the fused step over the timed graph parts, and the two halves
+    """Spread of the fused step over the timed replays, and the two halves
     of an unfused step timed alone (attention = partial + merge launches;
     append = one rec_kv_append launch)."""
     return {
@@ -635,11 +675,13 @@ def main(argv=None):
         # a short chunk over a long cache (a new chat turn): the keys are split
         rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
 
-    traffic = None
+    traffic, traffic_source = None, None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
         traffic = t.get("hbm_bytes_per_launch")
+        traffic_source = (f"not measured by this run: {os.path.relpath(TRAFFIC_FILE, ROOT)}, rocprofv3 FETCH_SIZE and "
+                          f"WRITE_SIZE passes over this kernel at source commit {t.get('commit', 'unrecorded')}")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -670,7 +712,9 @@ def main(argv=None):
             "kv_format": "int8 symmetric, fp16 scale per (token, head); 1% outlier channels x8",
             "cache_instances": r32["instances"],
             "cache_bytes_total": r32["cache_bytes"],
-            "timing": "K steps as 10 HIP graphs of K/10 steps, one replay each between HIP events",
+            "timing": "K steps captured in one HIP graph; one untimed warm replay, then 5 timed replays of exactly "
+            "K steps each between HIP events on the launch stream, ms_per_step their median (a ~100 us spin "
+            "kernel queued before each start event keeps host submission out of the timed region)",
         },
         "us_per_step": round(r32["us_per_step"], 3),
         **_step_detail(r32),
@@ -682,10 +726,11 @@ def main(argv=None):
             "unit": "GB/s",
             "frac": round(r32["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel": "rec::decode_kernel<8, 8> (fused append + split-K attention partials)",
             "kernel_us": round(r32["kernel_us"], 3),
             "algorithmic_bytes_per_launch": r32["bytes_per_launch"],
-            "timing": "HIP events around one graph replay of K launches of the kernel",
+            "timing": "HIP events around one replay (after a warm one) of a graph of K launches of the kernel",
         },
         "cpu_baseline": cpu,
     }
