@@ -135,6 +135,27 @@ int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                            void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
+ * rec_decode_append_attn for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * same arguments without a workspace, the same kernels, and the split
+ * partials kept in a static device array of rec_decode_scratch_bytes() bytes
+ * (8 MiB, one per GPU, held until the process ends).  No allocation of any
+ * kind.  A plan whose partials exceed it (B * Hkv * splits above about 2,000)
+ * returns REC_EWORKSPACE before anything is launched.  Every call on one GPU
+ * shares that GPU's array: calls that may overlap (on different streams)
+ * race and must be ordered by the caller.  No counterpart in the reference.
+ */
+int rec_decode_append_attn_noalloc(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                                   const void* k_new, const void* v_new, int new_dtype,
+                                   int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
+                                   int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros,
+                                   int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
+                                   const float* sinks, float scale,
+                                   int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
+                                   float* out, void* stream);
+size_t rec_decode_scratch_bytes(void);
+
+/*
  * The two launches of a decode step, for callers that schedule them apart
  * (for instance to time or overlap them).  rec_decode_partial takes the
  * arguments of rec_decode_append_attn; k_new/v_new NULL means no append.  It

@@ -53,6 +53,10 @@ SIGNATURES = {
     ),
 }
 SIGNATURES["rec_decode_partial"] = SIGNATURES["rec_decode_append_attn"]
+SIGNATURES["rec_decode_append_attn_noalloc"] = (
+    _i, SIGNATURES["rec_decode_append_attn"][1][:-4] + [_p, _p]  # no workspace, workspace_bytes
+)
+SIGNATURES["rec_decode_scratch_bytes"] = (_sz, [])
 SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _p, _p])
 SIGNATURES["rec_prefill_attn"] = (
     _i,

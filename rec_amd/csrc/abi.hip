@@ -5,6 +5,7 @@
 #include <stdio.h>
 
 #include <cmath>
+#include <mutex>
 
 #include "../../include/rec_amd.h"
 #include "kernels.h"
@@ -143,8 +144,9 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   int S, span, t_split_end;
   effective_splits(T, splits, knew != nullptr, &S, &span, &t_split_end);
   const WorkspaceLayout w = ws_layout(B, Hkv, S);
-  if (!ws || ws_bytes < w.total)
+  if ((phases != 0 && !ws) || ws_bytes < w.total)
     return fail(REC_EWORKSPACE, "workspace of %zu bytes is too small (%zu needed for %d splits)", ws_bytes, w.total, S);
+  if (phases == 0) return ok();  // validation only
   if (!aligned16(ws)) return fail(REC_EALIGN, "workspace must be 16-byte aligned");
   DecodeArgs a{};
   a.q = q;
@@ -181,6 +183,45 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   }
   if (phases & 2) return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
   return ok();
+}
+
+// ---- allocation-free decode: split partials in a static device array ----
+}  // namespace
+
+constexpr size_t SCRATCH_BYTES = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+namespace {
+// `scratch` is a device-side array of every GPU the library runs on (each
+// holds its own copy until the process ends).  Host code never uses its name
+// as an address: the first call on a device resolves that device's copy with
+// hipGetSymbolAddress and keeps the pointer, which the kernels then take as
+// their workspace.
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[SCRATCH_MAX_DEVICES] = {};
+
+// This device's scratch pointer (resolved on its first use), or null with the
+// error set.
+void* device_scratch(int* rc) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= SCRATCH_MAX_DEVICES) {
+    *rc = fail(REC_ELAUNCH, "no current device for the static scratch: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *rc = fail(REC_ELAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -295,6 +336,35 @@ int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
   return append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
                      k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
                      splits, workspace, workspace_bytes, out, 3, stream);
+}
+
+size_t rec_decode_scratch_bytes(void) { return SCRATCH_BYTES; }
+
+int rec_decode_append_attn_noalloc(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new,
+                                   const void* v_new, int new_dtype, int64_t k_sb, int64_t k_sh, int64_t v_sb,
+                                   int64_t v_sh, int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros,
+                                   int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
+                                   const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
+                                   int64_t capacity, int splits, float* out, void* stream) {
+  if (!k_new || !v_new) return fail(REC_EINVAL, "new keys/values pointer is null");
+  // validate everything, the plan's partials against the scratch size included, before touching the device
+  int e = append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
+                      k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
+                      splits, nullptr, SCRATCH_BYTES, out, 0, stream);
+  if (e == REC_EWORKSPACE) {
+    char why[sizeof(g_err)];
+    snprintf(why, sizeof(why), "%s", g_err);
+    return fail(REC_EWORKSPACE,
+                "the split partials exceed the library's %zu-byte static scratch (%s); request fewer splits or "
+                "use rec_decode_append_attn with a workspace",
+                SCRATCH_BYTES, why);
+  }
+  if (e != REC_OK) return e;
+  void* ws = device_scratch(&e);
+  if (!ws) return e;
+  return append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
+                     k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
+                     splits, ws, SCRATCH_BYTES, out, 3, stream);
 }
 
 int rec_decode_partial(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
