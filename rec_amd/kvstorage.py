@@ -8,12 +8,13 @@ storage in banks of 65,536 tokens up to four banks (cache.py:46-78); here a
 layer's region is one allocation whose capacity grows in the same 65,536-token
 steps to the same 262,144-token limit, the earlier contents copied over.
 Sliding-window layers keep a ring of window slots, ``FixedSlidingKVCache``
-(cache.py:153-258); decode attends over its valid slots with the same kernel.
+(the surface of cache.py:153-258); decode attends over its occupied slots with
+the same kernel.
 """
 
 from __future__ import annotations
 
-from typing import List, Optional
+from typing import List, NamedTuple, Optional
 
 import torch
 
@@ -143,16 +144,36 @@ class FixedKVCache:
         return data[:, 0], data[:, 1]
 
 
-class FixedSlidingKVCache:
-    """Sliding-window bf16 cache (engine/src/rec_mlx/cache.py:153-258).
+class RingState(NamedTuple):
+    """What a sliding ring holds at one point of the sequence: its tokens'
+    K and V ``(B, Hkv, n, 128)`` oldest first (``n = min(offset,
+    capacity)``), as private copies that nothing writes again, and the
+    number of tokens the ring had taken."""
 
-    Two slots of ``(B, Hkv, capacity, 128)`` bf16 buffers, ``capacity =
-    min(window_size, max_sequence_tokens)``.  A single new token is written at
-    the next free slot, then round the ring; a multi-token update returns the
-    ring's tokens in order followed by the new ones (the keys a windowed
-    prefill chunk attends to) and keeps the last ``capacity`` of them in the
-    other slot.  Decode attention over the ring is order-free (softmax over a
-    set of keys), so it reads the ``size()`` valid slots in place.
+    keys: torch.Tensor
+    values: torch.Tensor
+    offset: int
+
+    @property
+    def nbytes(self) -> int:
+        return self.keys.numel() * self.keys.element_size() + self.values.numel() * self.values.element_size()
+
+
+class FixedSlidingKVCache:
+    """Sliding-window bf16 cache with the surface of
+    engine/src/rec_mlx/cache.py:153-258.
+
+    One ring of ``capacity = min(window_size, max_sequence_tokens)`` token
+    slots per (batch row, KV head): token ``p`` of the sequence lives in slot
+    ``p % capacity``, so the ring always holds the last ``size() =
+    min(offset, capacity)`` tokens.  A single new token overwrites the oldest
+    slot and the decode attends over the occupied slots in place (softmax
+    attention is order-free).  A chunk of several tokens attends over the
+    window's tokens in sequence order followed by the chunk -- what
+    ``update_and_fetch`` returns, as the reference does -- and the ring then
+    keeps the last ``capacity`` of them.  :meth:`snapshot` and
+    :meth:`restore` copy the window out and back (prompt-prefix rollback,
+    ``rec_amd.prefix``).
     """
 
     def __init__(self, *, max_sequence_tokens: int, num_kv_heads: int, head_dim: int, window_size: int,
@@ -161,103 +182,134 @@ class FixedSlidingKVCache:
             raise NotImplementedError(f"head_dim {head_dim} is not supported (128 only)")
         if dtype != torch.bfloat16:
             raise NotImplementedError("the sliding cache holds bf16")
+        if window_size < 1 or max_sequence_tokens < 1:
+            raise ValueError("window_size and max_sequence_tokens must be positive")
         self.window_size = window_size
-        self.capacity = min(window_size, max_sequence_tokens)
         self.device = torch.device(device) if device is not None else torch.device("cuda")
-        shape = (batch, num_kv_heads, self.capacity, head_dim)
-        self.key_buffers = [torch.zeros(shape, dtype=dtype, device=self.device) for _ in range(2)]
-        self.value_buffers = [torch.zeros(shape, dtype=dtype, device=self.device) for _ in range(2)]
         self.offset = 0
-        self._valid = 0
-        self._slot = 0
-        self._ring_index = 0
+        self._alloc(batch, num_kv_heads, min(window_size, max_sequence_tokens))
 
-    def grow(self, capacity: int):
-        capacity = min(self.window_size, capacity)
-        if capacity > self.capacity:
-            pad = capacity - self.capacity
-            grow = lambda t: torch.nn.functional.pad(t, (0, 0, 0, pad))  # noqa: E731
-            self.key_buffers = [grow(t) for t in self.key_buffers]
-            self.value_buffers = [grow(t) for t in self.value_buffers]
-            self.capacity = capacity
+    def _alloc(self, batch, heads, capacity):
+        self.capacity = capacity
+        shape = (batch, heads, capacity, HEAD_DIM)
+        self.keys = torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
+        self.values = torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
 
-    @property
-    def state(self):
-        return tuple(self.key_buffers), tuple(self.value_buffers)
-
-    @property
-    def nbytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in (*self.key_buffers, *self.value_buffers))
+    # ------------------------------------------------------------ window --
+    def size(self) -> int:
+        return min(self.offset, self.capacity)
 
     def empty(self) -> bool:
         return self.offset == 0
 
-    def size(self) -> int:
-        return self._valid
-
     def is_trimmable(self) -> bool:
         return False
 
+    @property
+    def state(self):
+        return self.keys, self.values
+
+    @property
+    def nbytes(self) -> int:
+        return self.keys.numel() * self.keys.element_size() + self.values.numel() * self.values.element_size()
+
+    def window(self):
+        """The held tokens' K and V in sequence order (oldest first): views
+        while the ring has not wrapped, else the two arcs joined."""
+        n = self.size()
+        head = self.offset % self.capacity  # slot of the oldest token once the ring is full
+        if self.offset <= self.capacity or head == 0:
+            return self.keys[:, :, :n], self.values[:, :, :n]
+        return (torch.cat((self.keys[:, :, head:], self.keys[:, :, :head]), dim=2),
+                torch.cat((self.values[:, :, head:], self.values[:, :, :head]), dim=2))
+
     def make_mask(self, n_tokens: int, window_size=None, return_array: bool = False):
         """None for one decode token, "causal" for a first chunk within the
-        window, else the windowed causal boolean array (cache.py:199-205)."""
+        window, else the windowed causal boolean array over the held tokens
+        and the chunk (cache.py:199-205)."""
         window = self.window_size if window_size is None else window_size
         if n_tokens == 1 and not return_array:
             return None
-        if self._valid == 0 and n_tokens <= window and not return_array:
+        held = self.size()
+        if held == 0 and n_tokens <= window and not return_array:
             return "causal"
-        T = self._valid + n_tokens
+        T = held + n_tokens
         q = torch.arange(T - n_tokens, T)[:, None]
         k = torch.arange(T)[None]
         return (q >= k) & (q < k + window)
 
-    def _next_index(self) -> int:
-        """Slot the next single token goes to; advances the ring."""
-        if self._valid < self.capacity:
-            index = self._valid
-            self._valid += 1
-        else:
-            index = self._ring_index
-            self._ring_index = (self._ring_index + 1) % self.capacity
-        return index
-
-    def _write(self, index: int, keys: torch.Tensor, values: torch.Tensor):
-        kb, vb = self.key_buffers[self._slot], self.value_buffers[self._slot]
+    # ------------------------------------------------------------ writes --
+    def _store(self, slot: int, keys: torch.Tensor, values: torch.Tensor):
+        """Write rows ``(B, Hkv, L, 128)`` into slots ``[slot, slot + L)`` (no wrap)."""
         B, H, L, D = keys.shape
         k, ksb, ksh, kst = _stride3(keys)
         v, vsb, vsh, vst = _stride3(values)
         rc = _lib.load().rec_kv_write_bf16(
             k.data_ptr(), v.data_ptr(), _DTYPES[keys.dtype], ksb, ksh, kst, vsb, vsh, vst,
-            kb.data_ptr(), kb.stride(0), kb.stride(1), vb.data_ptr(), vb.stride(0), vb.stride(1),
-            B, H, L, D, index, self.capacity, torch.cuda.current_stream(self.device).cuda_stream,
+            self.keys.data_ptr(), self.keys.stride(0), self.keys.stride(1),
+            self.values.data_ptr(), self.values.stride(0), self.values.stride(1),
+            B, H, L, D, slot, self.capacity, torch.cuda.current_stream(self.device).cuda_stream,
         )
         _lib.check(rc, "rec_kv_write_bf16")
 
-    def _prior(self):
-        keys, values = self.key_buffers[self._slot], self.value_buffers[self._slot]
-        if self._valid == self.capacity and self._ring_index:
-            r = self._ring_index
-            return (torch.cat((keys[:, :, r:], keys[:, :, :r]), dim=2),
-                    torch.cat((values[:, :, r:], values[:, :, :r]), dim=2))
-        return keys[:, :, : self._valid], values[:, :, : self._valid]
+    def _place(self, keys: torch.Tensor, values: torch.Tensor, end: int):
+        """Put the tokens ``[end - n, end)`` of the sequence (the rows of
+        ``keys``/``values``, n <= capacity) into their slots, wrapping round."""
+        n = keys.shape[2]
+        if n == 0:
+            return
+        first = (end - n) % self.capacity
+        run = min(n, self.capacity - first)
+        self._store(first, keys[:, :, :run], values[:, :, :run])
+        if run < n:
+            self._store(0, keys[:, :, run:], values[:, :, run:])
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
         if keys.shape != values.shape or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
             raise ValueError("keys/values must share a shape and a float dtype")
-        if keys.shape[-2] == 1:
-            self._write(self._next_index(), keys, values)
+        B, H, L, _ = keys.shape
+        if (B, H) != tuple(self.keys.shape[:2]):
+            raise ValueError(f"keys are (B={B}, Hkv={H}), the ring holds {tuple(self.keys.shape[:2])}")
+        if L == 1:
+            self._store(self.offset % self.capacity, keys, values)
             self.offset += 1
-            return (self.key_buffers[self._slot][:, :, : self._valid],
-                    self.value_buffers[self._slot][:, :, : self._valid])
-        prior_keys, prior_values = self._prior()
-        attention_keys = torch.cat((prior_keys, keys.to(torch.bfloat16)), dim=2)
-        attention_values = torch.cat((prior_values, values.to(torch.bfloat16)), dim=2)
-        retained = min(self.capacity, attention_keys.shape[2])
-        nxt = 1 - self._slot
-        self.key_buffers[nxt][:, :, :retained] = attention_keys[:, :, -retained:]
-        self.value_buffers[nxt][:, :, :retained] = attention_values[:, :, -retained:]
-        self._slot = nxt
-        self._valid = retained
-        self._ring_index = 0
-        self.offset += keys.shape[2]
-        return attention_keys, attention_values
+            n = self.size()
+            return self.keys[:, :, :n], self.values[:, :, :n]
+        held_k, held_v = self.window()
+        attend_k = torch.cat((held_k, keys.to(torch.bfloat16)), dim=2)
+        attend_v = torch.cat((held_v, values.to(torch.bfloat16)), dim=2)
+        keep = min(L, self.capacity)
+        self._place(keys[:, :, L - keep:], values[:, :, L - keep:], self.offset + L)
+        self.offset += L
+        return attend_k, attend_v
+
+    def grow(self, capacity: int):
+        """Widen the ring (up to the window); the held tokens move to their
+        slots under the new modulus."""
+        capacity = min(self.window_size, capacity)
+        if capacity <= self.capacity:
+            return
+        held_k, held_v = (t.clone() for t in self.window())
+        self._alloc(self.keys.shape[0], self.keys.shape[1], capacity)
+        self._place(held_k, held_v, self.offset)
+
+    # --------------------------------------------------- snapshot/restore --
+    def snapshot(self) -> RingState:
+        k, v = self.window()
+        return RingState(k.clone(), v.clone(), self.offset)
+
+    def restore(self, state: RingState):
+        """Return the ring to ``state`` (the snapshot's tensors stay untouched)."""
+        n = state.keys.shape[2]
+        if n > self.capacity:
+            self.grow(n)
+        self.offset = state.offset
+        self._place(state.keys, state.values, state.offset)
+
+    def copy(self) -> "FixedSlidingKVCache":
+        """An independent ring with the same window and contents."""
+        other = object.__new__(FixedSlidingKVCache)
+        other.window_size, other.device, other.offset, other.capacity = (
+            self.window_size, self.device, self.offset, self.capacity)
+        other.keys, other.values = self.keys.clone(), self.values.clone()
+        return other

@@ -1,122 +1,130 @@
-"""Prompt-prefix checkpoints and rollback of sliding-window rings.
+"""Prompt-prefix reuse with rollback points.
 
-Restates engine/src/rec_mlx/prefix.py:14-118 over this library's caches: a
-:class:`PromptCache` keeps the tokens already prefilled, the per-layer caches
-and up to two checkpoints, each holding a copy of every
-:class:`FixedSlidingKVCache` ring (the slot in use, its valid count and ring
-index).  :func:`select_prefix` finds the longest common prefix with a new
-prompt; when the prompt diverges inside the cached tokens it rolls every layer
-back to the newest checkpoint at or before the divergence (full-attention
-layers by offset, rings by restoring the copied slot), so only the suffix needs
-prefilling again.  Host bookkeeping plus device copies; no kernels.
+Keeps the behaviour of engine/src/rec_mlx/prefix.py:14-118 (the names the
+engine calls: ``PromptCache(tokens, layers, logits, storage)`` with
+``fork``, ``advance``, ``checkpoint`` and ``checkpoint_bytes``,
+``select_prefix`` and ``PrefillCancelled``) over this library's caches.
+
+A prompt cache remembers the tokens whose K/V its layers hold.  A
+full-attention layer keeps every token at its own position, so going back to
+an earlier position only moves its ``offset``: the positions past it are
+rewritten when the new suffix is prefilled.  A sliding ring overwrites its
+oldest tokens, so going back needs what the ring held then.  A rollback point
+is therefore the position, one :class:`~rec_amd.kvstorage.RingState` per
+sliding layer and the logits at that position.  Points are immutable (a ring
+is restored by copying a state in, never by adopting its tensors), so forks
+share them and the point a rollback lands on stays usable.  At most two are
+kept: the newest and the one before it.
 """
 
 from __future__ import annotations
 
+import copy
 import logging
-from dataclasses import dataclass, field
-from typing import Any, List, Optional
+from typing import List, NamedTuple, Optional, Sequence, Tuple
 
 import torch
 
-from .kvstorage import FixedSlidingKVCache
+from .kvstorage import FixedSlidingKVCache, RingState
+
+log = logging.getLogger(__name__)
 
 
 class PrefillCancelled(Exception):
-    pass
+    """A prefill stopped between chunks at the caller's request."""
 
 
-@dataclass
-class Checkpoint:
-    position: int
-    sliding: list
+class RollbackPoint(NamedTuple):
+    position: int  # tokens covered
+    rings: Tuple[Tuple[int, RingState], ...]  # (layer index, ring contents) for every sliding layer
     logits: Optional[torch.Tensor]
 
+    @property
+    def nbytes(self) -> int:
+        n = sum(state.nbytes for _, state in self.rings)
+        if self.logits is not None:
+            n += self.logits.numel() * self.logits.element_size()
+        return n
 
-@dataclass
+
+def _matching_length(a: Sequence[int], b: Sequence[int]) -> int:
+    n = min(len(a), len(b))
+    for i in range(n):
+        if a[i] != b[i]:
+            return i
+    return n
+
+
 class PromptCache:
-    tokens: List[int]
-    layers: list
-    logits: Optional[torch.Tensor]
-    storage: Any
-    checkpoints: List[Checkpoint] = field(default_factory=list)
+    """Tokens already prefilled, the per-layer caches holding them, the logits
+    after the last one, the storage the layers live in, and the rollback
+    points (oldest first)."""
+
+    KEEP = 2
+
+    def __init__(self, tokens, layers, logits, storage, points: Optional[List[RollbackPoint]] = None):
+        self.tokens: List[int] = list(tokens)
+        self.layers = layers
+        self.logits = logits
+        self.storage = storage
+        self.points: List[RollbackPoint] = list(points or [])
 
     def fork(self) -> "PromptCache":
-        """A copy whose rings are private (prefix.py:29-39)."""
-        layers = [_shallow_copy(layer) for layer in self.layers]
-        for layer in layers:
-            if isinstance(layer, FixedSlidingKVCache):
-                keys = layer.key_buffers[layer._slot].clone()
-                values = layer.value_buffers[layer._slot].clone()
-                layer.key_buffers = [keys, torch.zeros_like(keys)]
-                layer.value_buffers = [values, torch.zeros_like(values)]
-                layer._slot = 0
-        return PromptCache(self.tokens[:], layers, self.logits, self.storage, self.checkpoints[:])
+        """A copy that can advance on its own: private rings, private offsets
+        of the full-attention layers (over the shared storage), shared points."""
+        layers = [layer.copy() if isinstance(layer, FixedSlidingKVCache) else copy.copy(layer)
+                  for layer in self.layers]
+        return PromptCache(self.tokens, layers, self.logits, self.storage, self.points)
 
     def advance(self, tokens, logits):
-        previous = len(self.tokens)
+        """Record ``tokens`` as prefilled into the layers, ``logits`` after them."""
         self.tokens.extend(tokens)
         self.logits = logits
-        if len(self.tokens) // 8192 != previous // 8192:
-            logging.info("Prefill progress: %d tokens processed", len(self.tokens))
 
     def checkpoint(self):
-        """Keep the newest checkpoint and add one at the current position
-        (prefix.py:47-62)."""
+        """Add a rollback point at the current position (nothing before the
+        first token), keeping the newest ``KEEP``."""
         if not self.tokens:
             return
-        self.checkpoints = self.checkpoints[-1:]
-        sliding = []
-        for layer in self.layers:
-            if isinstance(layer, FixedSlidingKVCache):
-                sliding.append((layer.key_buffers[layer._slot].clone(), layer.value_buffers[layer._slot].clone(),
-                                layer._valid, layer._ring_index))
-        self.checkpoints.append(Checkpoint(len(self.tokens), sliding, self.logits))
+        rings = tuple((i, layer.snapshot()) for i, layer in enumerate(self.layers)
+                      if isinstance(layer, FixedSlidingKVCache))
+        self.points = (self.points + [RollbackPoint(len(self.tokens), rings, self.logits)])[-self.KEEP:]
 
     @property
     def checkpoint_bytes(self) -> int:
-        total = 0
-        for cp in self.checkpoints:
-            total += sum(k.numel() * k.element_size() + v.numel() * v.element_size() for k, v, _, _ in cp.sliding)
-            if cp.logits is not None:
-                total += cp.logits.numel() * cp.logits.element_size()
-        return total
+        return sum(p.nbytes for p in self.points)
+
+    def rollback(self, point: RollbackPoint):
+        """Return every layer to ``point``; later points no longer apply."""
+        for layer in self.layers:
+            if not isinstance(layer, FixedSlidingKVCache):
+                layer.offset = point.position
+        for i, state in point.rings:
+            self.layers[i].restore(state)
+        del self.tokens[point.position:]
+        self.logits = point.logits
+        self.points = [p for p in self.points if p.position <= point.position]
 
 
-def _shallow_copy(layer):
-    import copy
+def select_prefix(prefix: Optional[PromptCache], tokens) -> Tuple[Optional[PromptCache], int]:
+    """How much of ``prefix`` a prompt of ``tokens`` can reuse.
 
-    return copy.copy(layer)
-
-
-def select_prefix(prefix: Optional[PromptCache], tokens):
-    """``(prefix or None, common)``: reuse ``prefix`` as far as it matches
-    ``tokens``, rolling back to a checkpoint when they diverge inside it
-    (prefix.py:74-118)."""
+    Returns ``(cache, common)``: ``common`` is the length of the prompt's
+    match with the cached tokens.  If every cached token matches, the cache
+    is returned as it is.  Otherwise it is rolled back to its newest point at
+    or before ``common`` and returned, or ``None`` when no such point exists
+    (the prompt must be prefilled from scratch).
+    """
     common = 0
     if prefix is not None:
-        for previous, current in zip(prefix.tokens, tokens):
-            if previous != current:
-                break
-            common += 1
-        if common != len(prefix.tokens):
-            checkpoint = next((item for item in reversed(prefix.checkpoints) if item.position <= common), None)
-            if checkpoint is None:
-                prefix = None
+        common = _matching_length(prefix.tokens, tokens)
+        if common < len(prefix.tokens):
+            usable = [p for p in prefix.points if p.position <= common]
+            if usable:
+                prefix.rollback(max(usable, key=lambda p: p.position))
             else:
-                sliding = iter(checkpoint.sliding)
-                for layer in prefix.layers:
-                    layer.offset = checkpoint.position
-                    if isinstance(layer, FixedSlidingKVCache):
-                        keys, values, layer._valid, layer._ring_index = next(sliding)
-                        layer.capacity = keys.shape[-2]
-                        layer.key_buffers = [keys, torch.zeros_like(keys)]
-                        layer.value_buffers = [values, torch.zeros_like(values)]
-                        layer._slot = 0
-                prefix.tokens = prefix.tokens[: checkpoint.position]
-                prefix.logits = checkpoint.logits
-                prefix.checkpoints = [item for item in prefix.checkpoints if item.position < checkpoint.position]
-    cached = 0 if prefix is None else len(prefix.tokens)
-    logging.info("Prefill: prompt=%d common_prefix=%d reused=%d new=%d", len(tokens), common, cached,
-                 len(tokens) - cached)
+                prefix = None
+    reused = 0 if prefix is None else len(prefix.tokens)
+    log.info("prompt of %d tokens: %d match the cached prefix, %d reused, %d to prefill", len(tokens), common, reused,
+             len(tokens) - reused)
     return prefix, common
