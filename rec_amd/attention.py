@@ -195,8 +195,9 @@ def quantized_attention_with_sinks(
 
     ``keys``/``values`` are what :meth:`QuantizedKVCache.update_and_fetch`
     returns; ``sinks`` (``n_q`` logits or None) join the softmax denominator;
-    ``mask`` is None or "causal" (for ``L == 1`` both mean "every cached
-    token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` (bf16/f16
+    ``mask`` is None, "causal", a boolean array or an additive 0 / -inf array
+    whose pattern is all keys or causal (:func:`_mask_plan`; for ``L == 1``
+    both mean "every cached token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` (bf16/f16
     queries, the newest ``L`` cached tokens) the chunked prefill kernel, which
     reads an int8 cache directly; other formats are first dequantized to bf16
     (:func:`dequantize_kv`) and run the bf16 prefill kernel.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
@@ -213,8 +214,9 @@ def quantized_attention_with_sinks(
     if not keys.affine and 4 in (key_bits, value_bits) and group_size != 32:
         raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
     _check_cache_shapes(queries, keys, values)
-    if mask is not None and not (isinstance(mask, str) and mask == "causal"):
-        raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
+    causal, win = _mask_plan(mask, L, int(keys.length))
+    if win and (L == 1 or (keys.code, values.code) == (8, 8)):
+        raise NotImplementedError("sliding-window masks are not supported for this quantized-cache launch")
     if L == 1:
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
         _decode_launch(queries, keys, values, scale, sinks, splits, out)
@@ -227,10 +229,10 @@ def quantized_attention_with_sinks(
             raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
         if keys.code == 8 and values.code == 8:
-            _prefill_launch(queries, keys, values, scale, sinks, mask == "causal", out, splits or 0)
+            _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0)
         else:
             k, v = dequantize_kv(keys, values)
-            _bf16_prefill_launch(queries, k, v, scale, sinks, mask == "causal", 0, out, splits or 0)
+            _bf16_prefill_launch(queries, k, v, scale, sinks, causal, win, out, splits or 0)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 
@@ -287,27 +289,55 @@ def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, ou
     _lib.check(rc, "rec_prefill_bf16")
 
 
-def _mask_window(mask, L, T):
-    """(causal, window) of a mask: None, "causal", or a boolean (L, T) array
-    that must be the causal mask limited to the last ``window`` keys
-    (engine/src/rec_mlx/cache.py:199-205); anything else is not supported."""
+def _mask_plan(mask, L, T):
+    """How the kernels apply ``mask`` to ``L`` queries at positions
+    ``T - L .. T - 1`` over ``T`` keys: ``(causal, window)``.
+
+    The reference's rules (model.py:122-128): None keeps every key; "causal"
+    keeps keys at or before each query's position; a boolean array keeps the
+    keys where it is True; a float array is added to the scores, so here it
+    may hold only 0 (keep) and -inf (drop).  Arrays broadcast to ``(L, T)``
+    (leading dims of size one, or equal slices).  The kernels run three
+    patterns: every key ``(False, 0)``, causal ``(True, 0)``, and causal
+    limited to the last ``window`` keys ``(True, window)``
+    (engine/src/rec_mlx/cache.py:199-205); any other pattern raises
+    NotImplementedError.
+    """
     if mask is None:
         return False, 0
     if isinstance(mask, str):
         if mask != "causal":
             raise NotImplementedError(f"mask {mask!r} is not supported")
         return True, 0
-    if not isinstance(mask, torch.Tensor) or mask.dtype != torch.bool:
-        raise NotImplementedError("only boolean causal or sliding-window mask arrays are supported")
-    m = mask.reshape(mask.shape[-2:]) if mask.dim() > 2 and mask.numel() == L * T else mask
-    if tuple(m.shape) != (L, T):
-        raise NotImplementedError(f"mask of shape {tuple(mask.shape)} does not match ({L}, {T})")
-    window = int(m[-1].sum())
-    q = torch.arange(T - L, T, device=m.device)[:, None]
-    k = torch.arange(T, device=m.device)[None]
-    if torch.equal(m, (q >= k) & (q < k + window)):
-        return True, (0 if window >= T else window)
-    raise NotImplementedError("only causal or causal sliding-window mask arrays are supported")
+    m = mask if isinstance(mask, torch.Tensor) else torch.as_tensor(mask)
+    if m.dtype == torch.bool:
+        keep = m
+    elif m.is_floating_point():
+        if not bool(((m == 0) | (m == float("-inf"))).all()):
+            raise NotImplementedError("additive masks must hold only 0 and -inf")
+        keep = m == 0
+    else:
+        raise NotImplementedError(f"mask dtype {m.dtype} is not supported (bool or float)")
+    while keep.dim() > 2:  # leading (batch, head) dims: one pattern for all
+        if not bool((keep == keep[:1]).all()):
+            raise NotImplementedError("masks that differ between sequences or heads are not supported")
+        keep = keep[0]
+    if keep.dim() < 2:
+        keep = keep.reshape(1, -1)
+    if keep.shape[-1] != T or keep.shape[0] not in (1, L):
+        raise NotImplementedError(f"mask of shape {tuple(mask.shape)} does not broadcast to ({L}, {T})")
+    keep = keep.expand(L, T)
+    if bool(keep.all()):
+        return False, 0
+    q = torch.arange(T - L, T, device=keep.device)[:, None]
+    k = torch.arange(T, device=keep.device)[None]
+    causal = q >= k
+    if torch.equal(keep, causal):
+        return True, 0
+    window = int(keep[-1].sum())
+    if window > 0 and torch.equal(keep, causal & (q < k + window)):
+        return True, window
+    raise NotImplementedError("only causal or causal sliding-window mask patterns are supported")
 
 
 def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=None, *, out_dtype=None,
@@ -327,19 +357,19 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
         raise ValueError("keys/values must be bf16 GPU tensors (B, Hkv, T, 128) with token stride 128")
     if keys.shape != values.shape or keys.shape[0] != B or keys.shape[-1] != D:
         raise ValueError(f"keys {tuple(keys.shape)} / values {tuple(values.shape)} do not match queries")
+    T = keys.shape[2]
+    if L > T:
+        raise ValueError(f"{L} queries but only {T} keys")
+    causal, win = _mask_plan(mask, L, T)
+    if window is not None:
+        causal, win = True, (0 if window >= T else int(window))
     if L == 1:
-        if mask is not None and not (isinstance(mask, str) and mask == "causal"):
-            raise NotImplementedError("explicit mask arrays are not supported for one query token; use None")
+        if win:  # one query sees the last `win` keys: attend over that slice
+            keys, values = keys[:, :, T - win:], values[:, :, T - win:]
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
         _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out)
         out = out.view(B, Hq, 1, D)
     else:
-        T = keys.shape[2]
-        if L > T:
-            raise ValueError(f"{L} queries but only {T} keys")
-        causal, win = _mask_window(mask, L, T)
-        if window is not None:
-            causal, win = True, (0 if window >= T else int(window))
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
         _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
@@ -390,8 +420,8 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         cache._check_usable()
         if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
             raise ValueError("a fused decode step takes one new K/V token of a float dtype")
-        if mask is not None and not (isinstance(mask, str) and mask == "causal"):
-            raise NotImplementedError("explicit mask arrays are not supported; use None or 'causal'")
+        if _mask_plan(mask, 1, cache.offset + 1) != (False, 0):
+            raise NotImplementedError("a fused decode step attends over every cached token (mask None or causal)")
         Bk, H = keys.shape[:2]
         if cache.keys is not None and tuple(cache.keys[0].shape[:2]) != (Bk, H):
             raise ValueError(f"new keys have (B, Hkv) = ({Bk}, {H}), the cache holds "

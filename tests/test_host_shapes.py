@@ -38,3 +38,58 @@ def test_matching_shapes_pass():
 def test_mismatches_refused(qs, ks, vs, msg):
     with pytest.raises(ValueError, match=msg):
         _check_cache_shapes(q(*qs), kv(*ks), kv(*vs, blocked=True))
+
+
+# ---- mask arrays (model.py:122-128) -> the kernels' (causal, window) ----
+import numpy as np  # noqa: E402
+
+from rec_amd.attention import _mask_plan  # noqa: E402
+
+
+def causal_keep(L, T, window=0):
+    q = torch.arange(T - L, T)[:, None]
+    k = torch.arange(T)[None]
+    m = q >= k
+    return m & (q < k + window) if window else m
+
+
+def test_mask_plan_strings_and_none():
+    assert _mask_plan(None, 5, 9) == (False, 0)
+    assert _mask_plan("causal", 5, 9) == (True, 0)
+    with pytest.raises(NotImplementedError):
+        _mask_plan("sliding", 5, 9)
+
+
+@pytest.mark.parametrize("L,T", [(1, 1), (1, 50), (7, 7), (7, 40), (64, 300)])
+def test_mask_plan_boolean_and_additive(L, T):
+    keep = causal_keep(L, T)
+    want = (False, 0) if L == 1 else (True, 0)  # one query: causal keeps every key
+    assert _mask_plan(keep, L, T) == want
+    assert _mask_plan(keep[None, None], L, T) == want  # (1, 1, L, T)
+    assert _mask_plan(keep.expand(2, 3, L, T), L, T) == want  # the same pattern for every sequence and head
+    assert _mask_plan(keep.numpy(), L, T) == want
+    additive = torch.zeros(L, T).masked_fill(~keep, float("-inf"))
+    assert _mask_plan(additive, L, T) == want
+    assert _mask_plan(torch.ones(L, T, dtype=torch.bool), L, T) == (False, 0)
+    assert _mask_plan(torch.zeros(1, T), L, T) == (False, 0)  # a row broadcast over the queries
+    if T > 3:
+        w = T // 2
+        assert _mask_plan(causal_keep(L, T, w), L, T) == (True, w)
+
+
+def test_mask_plan_refuses_other_patterns():
+    L, T = 6, 20
+    keep = causal_keep(L, T)
+    odd = keep.clone()
+    odd[2, 0] = False  # a hole in one row
+    with pytest.raises(NotImplementedError):
+        _mask_plan(odd, L, T)
+    with pytest.raises(NotImplementedError, match="only 0 and -inf"):
+        _mask_plan(torch.zeros(L, T).masked_fill(~keep, -1e4), L, T)
+    per_head = torch.stack([keep, torch.ones_like(keep)])[None]
+    with pytest.raises(NotImplementedError, match="differ"):
+        _mask_plan(per_head, L, T)
+    with pytest.raises(NotImplementedError, match="broadcast"):
+        _mask_plan(keep[:, :-1], L, T)
+    with pytest.raises(NotImplementedError):
+        _mask_plan(np.zeros((L, T), np.int32), L, T)

@@ -434,3 +434,72 @@ def test_affine_planted_bias_sign_is_caught():
     q, s, b = O.quantize_affine(x, 4)
     assert not np.allclose(q * s.repeat(64, -1) - b.repeat(64, -1), x)  # wrong sign of the bias
     np.testing.assert_array_equal(O.dequantize_affine(q, s, b), x)
+
+
+def _nearest_codes(x, s, b, n):
+    """Brute force over every code 0..n: the code whose level b + k*s is
+    nearest to x (float64), a tie going to the code farther from zero on the
+    (x - b) / s axis (half away from zero; codes below 0 clamp to 0)."""
+    k = np.arange(n + 1, dtype=np.float64)
+    lv = b[..., None] + k * s[..., None]  # (..., n+1)
+    d = np.abs(x[..., None].astype(np.float64) - lv)
+    best = d.min(-1, keepdims=True)
+    ties = d == best
+    t = (x.astype(np.float64) - b) / s
+    # among tied codes pick the largest when t >= 0, else the smallest
+    idx = np.where(t >= 0, n - np.argmax(ties[..., ::-1], -1), np.argmax(ties, -1))
+    return idx
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("sign", [1, -1])
+def test_affine_codes_brute_force_exact_levels(bits, sign):
+    """Groups whose scale and bias come out exactly (+-1 and the range end, so
+    the stored bf16 values are the ones the codes were computed with) and
+    whose elements sit on quarter steps, many on exact half-way points: every
+    code is the nearest level, ties half away from zero (round-half-even
+    would give the lower code at 12.5, 14.5, ...)."""
+    n = (1 << bits) - 1
+    rng = np.random.default_rng(77 + bits)
+    groups = []
+    for _ in range(20):
+        quarters = rng.integers(0, 4 * n + 1, 62) / 4.0
+        g = np.concatenate([[0.0, float(n)], quarters])
+        groups.append(rng.permutation(g))
+    x = (sign * np.array(groups)).astype(np.float32).reshape(10, 128)
+    q, s, b = O.quantize_affine(x, bits)
+    # the larger-magnitude end is n (sign +: scale -1, bias n) or -n (sign -: scale +1, bias -n)
+    assert np.all(s == -sign) and np.all(b == sign * n)
+    want = _nearest_codes(x.reshape(10, 2, 64), s[..., None].astype(np.float64), b[..., None].astype(np.float64), n)
+    np.testing.assert_array_equal(q.reshape(10, 2, 64), want)
+    halves = np.abs((x - sign * n) * 2 % 2) == 1
+    assert halves.sum() > 100  # the draw exercises many exact ties
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_affine_codes_brute_force_random(bits):
+    """Random groups (normal, heavy-tailed, one-signed, with an outlier): each
+    code's level under the stored bf16 scale and bias is within the bf16
+    rounding of those two of the best level any code gives (the codes were
+    chosen under the float32 scale and bias, before that rounding)."""
+    n = (1 << bits) - 1
+    rng = np.random.default_rng(91 + bits)
+    parts = [
+        rng.standard_normal((40, 64)),
+        rng.standard_t(3, (40, 64)),
+        np.abs(rng.standard_normal((40, 64))) + 0.3,
+        -np.abs(rng.standard_normal((40, 64))) - 0.3,
+    ]
+    x = np.concatenate(parts).astype(np.float32) * rng.uniform(0.01, 100, (160, 1)).astype(np.float32)
+    x[::7, 5] *= 30.0
+    x = x.reshape(80, 128)
+    q, s, b = O.quantize_affine(x, bits)
+    g = x.reshape(80, 2, 64).astype(np.float64)
+    s64, b64 = s.astype(np.float64)[..., None], b.astype(np.float64)[..., None]
+    mine = np.abs(g - (q.reshape(80, 2, 64) * s64 + b64))
+    k = np.arange(n + 1, dtype=np.float64)
+    best = np.abs(g[..., None] - (b64[..., None] + k * s64[..., None])).min(-1)
+    # bf16 rounding moves each level k*s + b by up to 2^-8 (n|s| + |b|), so a
+    # comparison of two levels by up to twice that
+    slack = 2.0**-7 * (np.abs(s64) * n + np.abs(b64))
+    assert np.all(mine <= best + slack)
