@@ -184,7 +184,11 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * quantize-appended with rec_kv_append); their queries q (B, Hq, L, D), element
  * strides (q_sb, q_sh, q_st), bf16 or f16, attend over all T tokens — with
  * causal != 0, query i sees tokens [0, T-L+i] — with optional sink logits.
- * out (B, Hq, L, D) fp32.  int8 K and V.
+ * out (B, Hq, L, D) fp32.  Any cache format of rec_decode_attn (int8 or uint4
+ * in any mix, or the affine pair): K/V tiles are dequantized into on-chip
+ * memory, never to HBM — int8 codes exactly with the row scales applied to
+ * scores and probabilities, 4-bit and affine values as x̂ rounded to the
+ * query dtype, as the reference dequantizes before its attention.
  * splits: key splits (<= 0: automatic, 1: none, at most 64).  A short chunk
  * over a long cache (few query blocks x KV heads x batch) splits the keys so
  * that the launch fills the chip; the partials go to `workspace`

@@ -3,9 +3,9 @@
 * :func:`quantized_attention_with_sinks` keeps the signature of
   engine/src/rec_mlx/model.py:108-110 and runs the gfx950 split-K decode kernel
   (``rec_decode_attn``) for one query token, the chunked prefill kernel for
-  several (model.py:191-203: ``rec_prefill_attn`` reads an int8 cache
-  directly; other formats are dequantized to bf16 first, ``rec_kv_dequant_bf16``
-  then ``rec_prefill_bf16``).
+  several (model.py:191-203: ``rec_prefill_attn`` reads every cache format
+  directly, dequantizing tiles on chip; a sliding-window mask goes through bf16
+  copies, ``rec_kv_dequant_bf16`` then ``rec_prefill_bf16``).
 * :func:`attend` mirrors the cache/attention part of ``Attention.__call__``
   (model.py:177-203): append first, then attend, decode for ``L == 1`` and
   chunked prefill for ``L > 1``.  For a
@@ -199,8 +199,10 @@ def quantized_attention_with_sinks(
     whose pattern is all keys or causal (:func:`_mask_plan`; for ``L == 1``
     both mean "every cached token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` (bf16/f16
     queries, the newest ``L`` cached tokens) the chunked prefill kernel, which
-    reads an int8 cache directly; other formats are first dequantized to bf16
-    (:func:`dequantize_kv`) and run the bf16 prefill kernel.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
+    reads every cache format directly (4-bit and affine values rounded to the
+    query dtype, as the reference dequantizes, int8 codes exactly); with a
+    sliding-window mask the cache is first dequantized to bf16
+    (:func:`dequantize_kv`) for the bf16 prefill kernel's window masking.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
     (default: the query dtype, as the reference returns, model.py:132-139).
     """
     _check_query(queries)
@@ -215,8 +217,8 @@ def quantized_attention_with_sinks(
         raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
     _check_cache_shapes(queries, keys, values)
     causal, win = _mask_plan(mask, L, int(keys.length))
-    if win and (L == 1 or (keys.code, values.code) == (8, 8)):
-        raise NotImplementedError("sliding-window masks are not supported for this quantized-cache launch")
+    if win and L == 1:
+        raise NotImplementedError("sliding-window masks are not supported for a decode step over a quantized cache")
     if L == 1:
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
         _decode_launch(queries, keys, values, scale, sinks, splits, out)
@@ -228,9 +230,9 @@ def quantized_attention_with_sinks(
         if queries.dtype not in (torch.bfloat16, torch.float16):
             raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
-        if keys.code == 8 and values.code == 8:
+        if not win:
             _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0)
-        else:
+        else:  # a sliding window: over bf16 copies, through the bf16 prefill's window masking
             k, v = dequantize_kv(keys, values)
             _bf16_prefill_launch(queries, k, v, scale, sinks, causal, win, out, splits or 0)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
@@ -420,7 +422,7 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         cache._check_usable()
         if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
             raise ValueError("a fused decode step takes one new K/V token of a float dtype")
-        if _mask_plan(mask, 1, cache.offset + 1) != (False, 0):
+        if _mask_plan(mask, 1, cache.offset + 1)[1]:  # one query: causal keeps every key, a window does not
             raise NotImplementedError("a fused decode step attends over every cached token (mask None or causal)")
         Bk, H = keys.shape[:2]
         if cache.keys is not None and tuple(cache.keys[0].shape[:2]) != (Bk, H):

@@ -44,6 +44,12 @@ int launched(hipError_t e, const char* what) {
 
 size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Prefill query rows (2-byte elements) that the kernel can read with 16-byte
+// loads: aligned base, strides that keep every 8-element run aligned.
+int query_rows_vec(const void* q, int64_t sb, int64_t sh, int64_t st) {
+  return aligned16(q) && sb % 8 == 0 && sh % 8 == 0 && st % 8 == 0;
+}
+
 struct WorkspaceLayout {
   size_t stat, acc, total;
 };
@@ -449,7 +455,6 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   int e;
   int kf, vf;
   if ((e = resolve_formats(k_bits, v_bits, &kf, &vf))) return e;
-  if (kf != 8 || vf != 8) return fail(REC_EUNSUPPORTED, "prefill supports int8 K and V only");
   if (q_dtype != REC_BF16 && q_dtype != REC_F16)
     return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
@@ -462,7 +467,7 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   if (capacity > ((int64_t)1 << 24)) return fail(REC_EUNSUPPORTED, "capacity above 16M tokens per head");
   if (!q || !out) return fail(REC_EINVAL, "query/output pointer is null");
   if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
-  if ((e = check_cache(8, k_codes, k_scales, k_zeros, "key")) || (e = check_cache(8, v_codes, v_scales, v_zeros, "value")))
+  if ((e = check_cache(kf, k_codes, k_scales, k_zeros, "key")) || (e = check_cache(vf, v_codes, v_scales, v_zeros, "value")))
     return e;
   if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
   PrefillArgs a{};
@@ -471,10 +476,15 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.q_sb = q_sb;
   a.q_sh = q_sh;
   a.q_st = q_st;
+  a.q_vec = query_rows_vec(q, q_sb, q_sh, q_st);
+  a.k_fmt = kf;
+  a.v_fmt = vf;
   a.kq = k_codes;
   a.ks = k_scales;
+  a.kz = k_zeros;
   a.vq = v_codes;
   a.vs = v_scales;
+  a.vz = v_zeros;
   a.sinks = sinks;
   a.out = out;
   a.q_mul = scale * LOG2E;
@@ -543,6 +553,8 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.q_sb = q_sb;
   a.q_sh = q_sh;
   a.q_st = q_st;
+  a.q_vec = query_rows_vec(q, q_sb, q_sh, q_st);
+  a.k_fmt = a.v_fmt = FMT_BF;
   a.kq = k;
   a.vq = v;
   a.k_sb = k_sb;

@@ -38,6 +38,7 @@ constexpr int HEAD_DIM = 128;
 // scale and bias (8-bit keys / 4-bit values).
 constexpr int FMT_A8 = 18;
 constexpr int FMT_A4 = 14;
+constexpr int FMT_BF = 16;  // bf16 K/V tensors (the KVStorage cache), prefill only
 constexpr int GROUP_A = 64;
 constexpr int BLOCK_T = 32;      // tokens per cache block and per wave iteration
 constexpr int GROUP4 = 32;       // int4 group size along head_dim

@@ -58,10 +58,14 @@ struct PrefillArgs {
   const void* q;
   int q_dtype;                 // DT_BF16 (bf16 MFMA) or DT_F16 (fp16 MFMA)
   int64_t q_sb, q_sh, q_st;    // element strides of q (batch, head, position)
-  const void* kq;              // int8 K codes (cache layout)
-  const uint16_t* ks;
-  const void* vq;              // int8 V codes
+  int q_vec;                   // q rows 16-byte aligned, strides multiples of 8 elements: vector loads
+  int k_fmt, v_fmt;            // 8, 4, FMT_A8 / FMT_A4, or FMT_BF (bf16 tensors, strides below)
+  const void* kq;              // K codes (cache layout) or bf16 K
+  const uint16_t* ks;          // scales (affine: [scale, bias])
+  const uint16_t* kz;          // uint4 zero-points
+  const void* vq;
   const uint16_t* vs;
+  const uint16_t* vz;
   const float* sinks;          // [Hq] or null
   float* out;                  // [B][Hq][L][128] fp32
   float q_mul;                 // softmax scale * log2(e)
@@ -69,7 +73,7 @@ struct PrefillArgs {
   int64_t T, cap;              // cached tokens including the L new ones; capacity
   int causal;
   int window;                  // > 0: query at position p sees keys (p - window, p] only
-  int kv_bf16;                 // K/V are bf16 (B, Hkv, T, 128) tensors, strides below
+  int kv_bf16;                 // k_fmt == v_fmt == FMT_BF
   int64_t k_sb, k_sh, v_sb, v_sh;
   // split-K over the keys (S > 1): workgroup (qb, s) scans keys
   // [split_lo + s * split_len, + split_len) of its query block's range and

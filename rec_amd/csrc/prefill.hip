@@ -1,29 +1,40 @@
-// Chunked prefill attention over the int8 KV cache on bf16 / fp16 matrix cores
-// (gfx950).
+// Chunked prefill attention over the quantized or bf16 KV cache on bf16 /
+// fp16 matrix cores (gfx950).
 //
 // Restates the prefill branch of Attention.__call__
 // (engine/src/rec_mlx/model.py:191-203): the new tokens were quantize-appended
 // first (model.py:177-178), then the L new queries attend over the whole
 // cache, the new tokens included, with the causal "string" mask of
 // model.py:122-125 (query i sits at position T-L+i) and the per-head sink
-// logit in the softmax denominator.  The reference dequantizes the cache to the
-// query dtype; here K/V codes are converted to bf16/fp16 exactly (|q| <= 127)
-// and the row scales are applied outside the matrix products: the K scale to
-// the scores, the V scale folded into the probabilities before their one
-// rounding.  Q·K^T runs on bf16 MFMAs for bf16 queries (fp16 for fp16
-// queries); P·V always on fp16 MFMAs, whose 11-bit significand keeps the
-// rounded probabilities within 2^-12 (bf16 would allow 2^-9, more than the
-// 1e-3 output tolerance when one token dominates).
+// logit in the softmax denominator.  The reference dequantizes the cache to
+// the query dtype (model.py:194-195) and runs one SDPA; here every K/V tile is
+// dequantized into LDS on the way from HBM, never written back:
+//   * int8 K/V: the codes enter the matrix products exactly (|q| <= 127) and
+//     the row scales are applied outside them, the K scale to the scores, the
+//     V scale folded into the probabilities before their rounding;
+//   * 4-bit and affine K/V: x̂ = (q - z)·s or q·s + b in float32, rounded to
+//     the query dtype as the reference's dequantization does (V then held
+//     as fp16 for the P·V product);
+//   * a bf16 cache (KVStorage views, ring windows): the values as they are.
+// Q·K^T runs on bf16 MFMAs for bf16 queries (fp16 for fp16 queries); P·V on
+// fp16 MFMAs, whose 11-bit significand keeps each rounded P' within 2^-12
+// (and a second MFMA carries the rounding remainder for rows that see few
+// keys, EXACT_PV_BELOW).
 //
-// Work decomposition.  Grid (ceil(L/32), Hkv, B), 512 threads = 8 wavefronts;
-// wave w owns query head w of the KV head's GQA group and 32 query positions.
-// Each 128-token K/V tile is loaded once per workgroup, converted into
-// double-buffered LDS (149 KB) and shared by the 8 waves, which compute it in
-// four 32-token units, software-pipelined so that one unit's Q·Kᵀ runs on the
-// matrix cores while the previous unit's softmax runs on the VALU.  A grid too
-// small to fill the chip (a short chunk over a long cache) splits the keys:
-// grid x = query blocks x splits, each workgroup writes an unnormalised
-// partial, and prefill_merge_kernel combines the splits as the decode's merge
+// Work decomposition.  Grid (ceil(L/32) x key splits, Hkv, B), 512 threads =
+// 8 wavefronts; wave w owns query head w of the KV head's GQA group and 32
+// query positions.  K/V tiles of 128 tokens (64 for a bf16 cache) are
+// dequantized into double-buffered LDS and shared by the 8 waves, which
+// compute a tile in 32-token units, software-pipelined (one unit's Q·K^T on
+// the matrix cores while the previous unit's softmax runs on the VALU).  Each
+// tile's raw bytes are fetched a whole tile ahead and dequantized into the
+// other buffer between two barriers at the end of the current tile; its scale
+// bytes reach the converting threads through a small LDS staging area.
+// (Spreading the conversion over the units, behind their Q·K^T MFMAs, was
+// measured no faster: the kernel is bound by LDS traffic and latency, not
+// by the conversion's VALU work.)  A grid too small to fill the chip (a short chunk
+// over a long cache) splits the keys: each workgroup writes an unnormalised
+// partial and prefill_merge_kernel combines the splits as the decode's merge
 // does (megakernel.py:276-318).
 //
 // S^T = K Q^T on 16x16x32 MFMAs (A = 16 tokens x 32 dims from LDS, B = Q^T held
@@ -32,23 +43,33 @@
 // block.  P·V then takes A = V^T straight from LDS (dims x tokens, cache
 // order) and B = P'^T from the lane's own registers.
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 
 namespace rec {
 
-constexpr int PF_QB = 32;           // query positions per workgroup
-constexpr int PF_KROW = 144;        // LDS row pitch of K (elements): 128 + 16 pad
+constexpr int PF_QB = 32;     // query positions per workgroup
+constexpr int PF_KROW = 144;  // LDS row pitch of K (elements): 128 + 16 pad
 
-// Tile geometry per cache format: tokens per K/V tile in LDS (one barrier per
-// tile) and the LDS row pitch of V (positions + 16 pad).  A bf16 cache moves
-// twice the bytes per token, so its tiles are half as long (same registers).
-template <bool KVB>
-struct PfTile {
-  static constexpr int KT = KVB ? 64 : 128;
-  static constexpr int VROW = KT + 16;
+// Tile geometry per cache format pair.
+template <int KF, int VF>
+struct PfGeom {
+  static constexpr bool BF = KF == FMT_BF;
+  static constexpr int KT = BF ? 64 : 128;  // tokens per tile (a bf16 tile moves twice the bytes per token)
+  static constexpr int U = KT / 32;         // 32-token units per tile
+  static constexpr int VROW = KT + 16;      // LDS row pitch of V (positions + 16 pad)
   static constexpr int K_ELEMS = KT * PF_KROW;
   static constexpr int V_ELEMS = HEAD_DIM * VROW;
+  // Scale bytes per 32-token block, per staged region: [K scales][K zeros][V scales][V zeros]
+  // (int8: one fp16 per token; uint4: [4 groups][32 slots] fp16 scales, zero-points alike;
+  // affine: [scale, bias][2 groups][32 slots] bf16 in the scales region).
+  static constexpr int KS_B = KF == 8 ? 64 : (KF == 4 || KF == FMT_A8) ? 256 : 0;
+  static constexpr int KZ_B = KF == 4 ? 256 : 0;
+  static constexpr int VS_B = VF == 8 ? 64 : (VF == 4 || VF == FMT_A4) ? 256 : 0;
+  static constexpr int VZ_B = VF == 4 ? 256 : 0;
+  static constexpr int OFF_KZ = 4 * KS_B, OFF_VS = OFF_KZ + 4 * KZ_B, OFF_VZ = OFF_VS + 4 * VS_B;
+  static constexpr int STAGE = OFF_VZ + 4 * VZ_B;  // <= 4096
 };
 
 template <bool BF16>
@@ -60,8 +81,7 @@ struct MT<true> {
   static __device__ __forceinline__ v4f mfma(vec a, vec b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
-  // exact for integers |x| <= 256 and for bf16 inputs; round-to-nearest-even otherwise
-  static __device__ __forceinline__ elem from_float(float x) { return (__bf16)x; }
+  static __device__ __forceinline__ elem from_float(float x) { return (__bf16)x; }  // round to nearest even
 };
 template <>
 struct MT<false> {
@@ -73,120 +93,264 @@ struct MT<false> {
   static __device__ __forceinline__ elem from_float(float x) { return (_Float16)x; }
 };
 
-// One thread's share of a 128-token tile as loaded from HBM: 16 bytes of K
-// and of V from each of two cache blocks, and one fp16 scale (threads 0..255:
-// 128 K scales then 128 V scales).
+// fp16 value of a dequantized V element as the reference holds it: rounded
+// to the query dtype first (bf16 queries), then widened to the fp16 P·V
+// operand (exact inside fp16's range).
+template <bool BF16>
+__device__ __forceinline__ _Float16 v_elem(float x) {
+  if constexpr (BF16) return (_Float16)(float)(__bf16)x;
+  else return (_Float16)x;
+}
+
+// One thread's share of a tile's raw bytes, as loaded from HBM.
 struct TileRegs {
-  v4i k[2], v[2];
-  uint32_t s;
+  v4i k[2];  // int8 / affine-8 K: two 16-byte runs; uint4 K: k[0] = two 8-byte runs; bf16: two 16-byte rows
+  v4i v[2];  // int8 V: two 16-byte runs; 4-bit V: v[0] = two 8-byte runs; bf16: two 16-byte rows
+  v2i sc;    // 8 bytes of the tile's staged scale regions
 };
 
-__device__ __forceinline__ void load_tile(TileRegs& R, const PrefillArgs& a, int64_t bh, int t0, int tid, int t_end) {
-  const int o = (tid & 255) * 16;  // byte in block
+// ---------------------------------------------------------------- loads --
+// Thread -> bytes, per format (tile of KT tokens at t0, a multiple of KT):
+//   int8 / affine-8 K, int8 V: byte o = 16 (tid % 256) of blocks 2p + tid / 256, p = 0, 1;
+//   uint4 K: token t = tid / 4, dims 32 (tid % 4) .. +31 (runs 2(q&1), +1 of half q/2);
+//   4-bit V: block tid / 128, dims 16(4N + 2kk + k) + c (k = 0, 1), positions 8g .. 8g+7
+//     for g = 2gg, 2gg+1 (N = bit 6, c = bits 2-5, kk = bit 1, gg = bit 0 of tid);
+//   bf16: 16-byte chunks tid and tid + 512 of the 64-token tile, chunk = (token, 8 dims);
+//   scales: 8 bytes at staged offset 8 tid (regions contiguous per (b, h) in HBM).
+template <int KF, int VF>
+__device__ __forceinline__ void load_tile(TileRegs& R, const PrefillArgs& a, int b, int h, int64_t bh, int t0,
+                                          int tid, int t_end) {
+  typedef PfGeom<KF, VF> GEO;
+  const int64_t blk0 = bh * (a.cap / BLOCK_T) + (t0 >> 5);  // first cache block of the tile
+  if constexpr (KF == FMT_BF) {
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    const int bk = 2 * part + (tid >> 8);  // cache block within the tile
-    const int blk = (t0 >> 5) + bk;
-    const bool live = t0 + 32 * bk < t_end;
-    const int8_t* kb = (const int8_t*)a.kq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
-    const int8_t* vb = (const int8_t*)a.vq + (bh * (a.cap / BLOCK_T) + blk) * 4096;
-    R.k[part] = live ? __builtin_nontemporal_load((const v4i*)(kb + o)) : (v4i){0, 0, 0, 0};
-    R.v[part] = live ? __builtin_nontemporal_load((const v4i*)(vb + o)) : (v4i){0, 0, 0, 0};
-  }
-  R.s = 0;
-  if (tid < 256) {
-    const int which = tid >> 7, tt = tid & 127;  // 0 = K scale, 1 = V scale
-    const uint16_t* sp = which == 0 ? a.ks : a.vs;
-    if (t0 + tt < t_end) R.s = sp[(bh * (a.cap / BLOCK_T) + (t0 >> 5) + (tt >> 5)) * 32 + block_pos(tt & 31)];
+    for (int part = 0; part < 2; ++part) {
+      const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
+      const bool live = t0 + tok < t_end;
+      const int64_t row = (int64_t)(t0 + tok) * HEAD_DIM + d0;
+      const uint16_t* kp = (const uint16_t*)a.kq + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh + row;
+      const uint16_t* vp = (const uint16_t*)a.vq + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh + row;
+      R.k[part] = live ? __builtin_nontemporal_load((const v4i*)kp) : (v4i){0, 0, 0, 0};
+      R.v[part] = live ? __builtin_nontemporal_load((const v4i*)vp) : (v4i){0, 0, 0, 0};
+    }
+    return;
+  } else {
+    if constexpr (KF == 8 || KF == FMT_A8) {
+      const int o = (tid & 255) * 16;
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        const int bk = 2 * part + (tid >> 8);
+        const bool live = t0 + 32 * bk < t_end;
+        const int8_t* kb = (const int8_t*)a.kq + (blk0 + bk) * 4096;
+        R.k[part] = live ? __builtin_nontemporal_load((const v4i*)(kb + o)) : (v4i){0, 0, 0, 0};
+      }
+    } else {  // uint4 K
+      const int t = tid >> 2, q = tid & 3, bk = t >> 5;
+      const bool live = t0 + 32 * bk < t_end;
+      const uint8_t* kb = (const uint8_t*)a.kq + (blk0 + bk) * 2048 + (t & 31) * 64 + (2 * (q & 1)) * 16 + (q >> 1) * 8;
+      const v2i lo = live ? __builtin_nontemporal_load((const v2i*)kb) : (v2i){0, 0};
+      const v2i hi = live ? __builtin_nontemporal_load((const v2i*)(kb + 16)) : (v2i){0, 0};
+      R.k[0] = (v4i){lo[0], lo[1], hi[0], hi[1]};
+    }
+    if constexpr (VF == 8) {
+      const int o = (tid & 255) * 16;
+#pragma unroll
+      for (int part = 0; part < 2; ++part) {
+        const int bk = 2 * part + (tid >> 8);
+        const bool live = t0 + 32 * bk < t_end;
+        const int8_t* vb = (const int8_t*)a.vq + (blk0 + bk) * 4096;
+        R.v[part] = live ? __builtin_nontemporal_load((const v4i*)(vb + o)) : (v4i){0, 0, 0, 0};
+      }
+    } else {  // 4-bit V (uint4 or affine)
+      const int bk = tid >> 7, N = (tid >> 6) & 1, c = (tid >> 2) & 15, kk = (tid >> 1) & 1, gg = tid & 1;
+      const bool live = t0 + 32 * bk < t_end;
+      const uint8_t* vb = (const uint8_t*)a.vq + (blk0 + bk) * 2048 + N * 1024 + (c * 4 + 2 * gg) * 16 + kk * 8;
+      const v2i g0 = live ? __builtin_nontemporal_load((const v2i*)vb) : (v2i){0, 0};
+      const v2i g1 = live ? __builtin_nontemporal_load((const v2i*)(vb + 16)) : (v2i){0, 0};
+      R.v[0] = (v4i){g0[0], g0[1], g1[0], g1[1]};
+    }
+    // scale bytes: region (K scales, K zeros, V scales, V zeros) of the staged tile
+    R.sc = (v2i){0, 0};
+    const int off = 8 * tid;
+    if (off < GEO::STAGE) {
+      const uint16_t* base;
+      int rel, per;
+      if (off < GEO::OFF_KZ) base = a.ks, rel = off, per = GEO::KS_B;
+      else if (off < GEO::OFF_VS) base = a.kz, rel = off - GEO::OFF_KZ, per = GEO::KZ_B;
+      else if (off < GEO::OFF_VZ) base = a.vs, rel = off - GEO::OFF_VS, per = GEO::VS_B;
+      else base = a.vz, rel = off - GEO::OFF_VZ, per = GEO::VZ_B;
+      const int bk = rel / per;
+      if (t0 + 32 * bk < t_end) R.sc = *(const v2i*)((const char*)base + blk0 * per + rel);
+    }
   }
 }
 
-template <bool BF16>
-__device__ __forceinline__ void store_tile(const TileRegs& R, typename MT<BF16>::elem* Kl, _Float16* Vl, float* KS,
-                                           float* VS, int tid, float q_mul) {
+// -------------------------------------------------------------- convert --
+// The thread's raw bytes -> dequantized LDS tile (buffer of tile tokens KT).
+// Phase 0: K rows [token][dim]; phase 1: V [dim][cache position]; phase 2:
+// the K / V scale arrays of the softmax (int8: the row scales, the K one
+// times the softmax scale; dequantized formats: the softmax scale and 1).
+template <bool BF16, int KF, int VF, int PHASE>
+__device__ __forceinline__ void convert_tile(const TileRegs& R, typename MT<BF16>::elem* Kl, _Float16* Vl, float* KS,
+                                             float* VS, const char* stage, int tid, float q_mul) {
+  typedef PfGeom<KF, VF> GEO;
   typedef typename MT<BF16>::elem E;
-  const int o = (tid & 255) * 16;
+  constexpr int VROW = GEO::VROW;
+  if constexpr (KF == FMT_BF) {
+    if constexpr (PHASE == 0) {
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    const int bk = 2 * part + (tid >> 8);
-    // K block: [2 halves][32 tokens][64 B] -> LDS [token][dim]
-    {
-      const int m = o >> 11, r = (o & 2047) >> 6, e0 = o & 63;
-      E* dst = Kl + (32 * bk + r) * PF_KROW + 64 * m + e0;
+      for (int part = 0; part < 2; ++part) {
+        const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
+        if constexpr (BF16) {
+          *(v4i*)(Kl + tok * PF_KROW + d0) = R.k[part];
+        } else {
+          v8h kh;
 #pragma unroll
-      for (int w = 0; w < 4; ++w)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          dst[4 * w + b] = MT<BF16>::from_float((float)(int8_t)((uint32_t)R.k[part][w] >> (8 * b)));
-    }
-    // V block: 16-byte run o = [n/2][c][position group pg] holds positions
-    // 8pg .. 8pg+7 of dims 16n + c for n = 2(o/1024) and that + 1 -> LDS
-    // [dim][128 positions of the tile]
-    {
-      const int n0 = 2 * (o >> 10), cc = (o >> 6) & 15, pg = (o >> 4) & 3;
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        _Float16* dst = Vl + (16 * (n0 + half) + cc) * PfTile<false>::VROW + 32 * bk + 8 * pg;
-#pragma unroll
-        for (int w = 0; w < 2; ++w)
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            dst[4 * w + b] = (_Float16)(float)(int8_t)((uint32_t)R.v[part][2 * half + w] >> (8 * b));
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t w = (uint32_t)R.k[part][e];
+            kh[2 * e] = (_Float16)__builtin_bit_cast(float, w << 16);
+            kh[2 * e + 1] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
+          }
+          *(v8h*)(Kl + tok * PF_KROW + d0) = kh;
+        }
       }
-    }
-  }
-  // K scales carry the softmax scale (log2 domain)
-  if (tid < 256) (tid < 128 ? KS : VS)[tid & 127] = half_bits_to_float(R.s) * (tid < 128 ? q_mul : 1.f);
-}
-
-// bf16 cache: a 64-token tile is 16 KB of K and of V; thread tid takes the
-// 16-byte chunks tid and tid + 512 of each, chunk = (token, 8 dims).
-__device__ __forceinline__ void load_tile_bf16(TileRegs& R, const PrefillArgs& a, int b, int h, int t0, int tid,
-                                               int t_end) {
+    } else if constexpr (PHASE == 1) {
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
-    const bool live = t0 + tok < t_end;
-    const int64_t row = (int64_t)(t0 + tok) * HEAD_DIM + d0;
-    const uint16_t* kp = (const uint16_t*)a.kq + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh + row;
-    const uint16_t* vp = (const uint16_t*)a.vq + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh + row;
-    R.k[part] = live ? __builtin_nontemporal_load((const v4i*)kp) : (v4i){0, 0, 0, 0};
-    R.v[part] = live ? __builtin_nontemporal_load((const v4i*)vp) : (v4i){0, 0, 0, 0};
-  }
-}
-
-// K rows as they are (bf16 queries) or in fp16; V transposed into [dim][cache
-// position] as fp16 (exact for bf16 values in fp16's normal range), the
-// position of token t of a 32-token unit being block_pos(t) as in the int8
-// layout; the "scales" are the softmax scale and 1.
-template <bool BF16>
-__device__ __forceinline__ void store_tile_bf16(const TileRegs& R, typename MT<BF16>::elem* Kl, _Float16* Vl,
-                                                float* KS, float* VS, int tid, float q_mul) {
-  constexpr int VROW = PfTile<true>::VROW;
+      for (int part = 0; part < 2; ++part) {
+        const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
+        const int col = (tok & ~31) + block_pos(tok & 31);
 #pragma unroll
-  for (int part = 0; part < 2; ++part) {
-    const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
-    if constexpr (BF16) {
-      *(v4i*)(Kl + tok * PF_KROW + d0) = R.k[part];
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = (uint32_t)R.v[part][e];
+          Vl[(d0 + 2 * e) * VROW + col] = (_Float16)__builtin_bit_cast(float, w << 16);
+          Vl[(d0 + 2 * e + 1) * VROW + col] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
+        }
+      }
     } else {
-      v8h kh;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w = (uint32_t)R.k[part][e];
-        kh[2 * e] = (_Float16)__builtin_bit_cast(float, w << 16);
-        kh[2 * e + 1] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
-      }
-      *(v8h*)(Kl + tok * PF_KROW + d0) = kh;
+      if (tid < 2 * GEO::KT) (tid < GEO::KT ? KS : VS)[tid & (GEO::KT - 1)] = tid < GEO::KT ? q_mul : 1.f;
     }
-    const int col = (tok & ~31) + block_pos(tok & 31);
+    return;
+  } else {
+    if constexpr (PHASE == 0) {
+      if constexpr (KF == 8 || KF == FMT_A8) {
+        // block run o = [half m][token r][64 bytes]: dims 64m + e0 .. +15 of token r
+        const int o = (tid & 255) * 16, m = o >> 11, r = (o & 2047) >> 6, e0 = o & 63;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t w = (uint32_t)R.v[part][e];
-      Vl[(d0 + 2 * e) * VROW + col] = (_Float16)__builtin_bit_cast(float, w << 16);
-      Vl[(d0 + 2 * e + 1) * VROW + col] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
+        for (int part = 0; part < 2; ++part) {
+          const int bk = 2 * part + (tid >> 8);
+          E* dst = Kl + (32 * bk + r) * PF_KROW + 64 * m + e0;
+          if constexpr (KF == 8) {
+            if constexpr (BF16) {
+#pragma unroll
+              for (int w = 0; w < 4; ++w)
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb)
+                  dst[4 * w + bb] = (__bf16)(float)(int8_t)((uint32_t)R.k[part][w] >> (8 * bb));
+            } else {  // fp16: the codes glued under the exponent of 1024 (exact)
+              *(v8h*)dst = i8x8_to_h8((uint32_t)R.k[part][0], (uint32_t)R.k[part][1]);
+              *(v8h*)(dst + 8) = i8x8_to_h8((uint32_t)R.k[part][2], (uint32_t)R.k[part][3]);
+            }
+          } else {  // affine 8-bit: x = q·s + b, (s, b) of group m at the token's slot
+            const int slot = s4_slot(block_pos(r));
+            const uint16_t* sb = (const uint16_t*)(stage + bk * 256);
+            const float sc = __builtin_bit_cast(float, (uint32_t)sb[m * 32 + slot] << 16);
+            const float bi = __builtin_bit_cast(float, (uint32_t)sb[64 + m * 32 + slot] << 16);
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+#pragma unroll
+              for (int bb = 0; bb < 4; ++bb)
+                dst[4 * w + bb] = MT<BF16>::from_float(__builtin_fmaf(
+                    (float)(((uint32_t)R.k[part][w] >> (8 * bb)) & 0xffu), sc, bi));
+          }
+        }
+      } else {  // uint4 K: token t, group q (dims 32q .. 32q+31); x = (q - z)·s
+        const int t = tid >> 2, q = tid & 3, bk = t >> 5, slot = s4_slot(block_pos(t & 31));
+        const uint16_t* ss = (const uint16_t*)(stage + bk * 256);
+        const uint16_t* zz = (const uint16_t*)(stage + GEO::OFF_KZ + bk * 256);
+        const float sc = half_bits_to_float(ss[q * 32 + slot]), z = half_bits_to_float(zz[q * 32 + slot]);
+        E* dst = Kl + t * PF_KROW + 32 * q;
+        // run A (dims 32q + 2i, +1 for byte i) then run B (dims 32q + 16 + 2i, +1)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t word = (uint32_t)R.k[0][w];
+#pragma unroll
+          for (int bb = 0; bb < 4; ++bb) {
+            const uint32_t byte = (word >> (8 * bb)) & 0xffu;
+            const int d = 16 * (w >> 1) + 2 * (4 * (w & 1) + bb);
+            dst[d] = MT<BF16>::from_float(((float)(byte & 15u) - z) * sc);
+            dst[d + 1] = MT<BF16>::from_float(((float)(byte >> 4) - z) * sc);
+          }
+        }
+      }
+    } else if constexpr (PHASE == 1) {
+      if constexpr (VF == 8) {
+        // run o = [n/2][c][position group pg][n%2][8 positions]: positions
+        // 8pg .. 8pg+7 of dims 16n + c, n = n0 and n0 + 1
+        const int o = (tid & 255) * 16, n0 = 2 * (o >> 10), cc = (o >> 6) & 15, pg = (o >> 4) & 3;
+#pragma unroll
+        for (int part = 0; part < 2; ++part) {
+          const int bk = 2 * part + (tid >> 8);
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            _Float16* dst = Vl + (16 * (n0 + half) + cc) * VROW + 32 * bk + 8 * pg;
+            *(v8h*)dst = i8x8_to_h8((uint32_t)R.v[part][2 * half], (uint32_t)R.v[part][2 * half + 1]);
+          }
+        }
+      } else {  // 4-bit V: dims 16(4N + 2kk + k) + c, positions 8g + e of block bk
+        const int bk = tid >> 7, N = (tid >> 6) & 1, c = (tid >> 2) & 15, kk = (tid >> 1) & 1, gg = tid & 1;
+        const int grp = VF == 4 ? 2 * N + kk : N;  // the dims' scale group (32 or 64 dims)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int g = 2 * gg + j;
+          // slots 8g .. 8g+7 hold positions 8g + {0, 4, 1, 5, 2, 6, 3, 7} (s4_slot)
+          float sc[8], zb[8];
+          if constexpr (VF == 4) {
+            const v4i s4 = *(const v4i*)(stage + GEO::OFF_VS + bk * 256 + (grp * 32 + 8 * g) * 2);
+            const v4i z4 = *(const v4i*)(stage + GEO::OFF_VZ + bk * 256 + (grp * 32 + 8 * g) * 2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int sl = 2 * (e & 3) + (e >> 2);  // slot of position e inside the run
+              const uint32_t sw = (uint32_t)s4[sl >> 1], zw = (uint32_t)z4[sl >> 1];
+              sc[e] = half_bits_to_float((sl & 1) ? sw >> 16 : sw & 0xffffu);
+              zb[e] = half_bits_to_float((sl & 1) ? zw >> 16 : zw & 0xffffu);
+            }
+          } else {  // affine: [scale g][bias g] rows of bf16
+            const v4i s4 = *(const v4i*)(stage + GEO::OFF_VS + bk * 256 + (grp * 32 + 8 * g) * 2);
+            const v4i b4 = *(const v4i*)(stage + GEO::OFF_VS + bk * 256 + (64 + grp * 32 + 8 * g) * 2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int sl = 2 * (e & 3) + (e >> 2);
+              const uint32_t sw = (uint32_t)s4[sl >> 1], bw = (uint32_t)b4[sl >> 1];
+              sc[e] = __builtin_bit_cast(float, (sl & 1) ? sw & 0xffff0000u : sw << 16);
+              zb[e] = __builtin_bit_cast(float, (sl & 1) ? bw & 0xffff0000u : bw << 16);
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const uint32_t word = (uint32_t)R.v[0][2 * j + k];  // 8 nibbles: position 8g + e at nibble e
+            v8h out;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float qv = (float)((word >> (4 * e)) & 15u);
+              out[e] = v_elem<BF16>(VF == 4 ? (qv - zb[e]) * sc[e] : __builtin_fmaf(qv, sc[e], zb[e]));
+            }
+            *(v8h*)(Vl + (16 * (4 * N + 2 * kk + k) + c) * VROW + 32 * bk + 8 * g) = out;
+          }
+        }
+      }
+    } else {
+      if (tid < 2 * GEO::KT) {
+        const bool is_k = tid < GEO::KT;
+        const int t = tid & (GEO::KT - 1);
+        float x = is_k ? q_mul : 1.f;
+        if ((is_k && KF == 8) || (!is_k && VF == 8)) {
+          const uint16_t* s8 = (const uint16_t*)(stage + (is_k ? 0 : GEO::OFF_VS));
+          x *= half_bits_to_float(s8[(t >> 5) * 32 + block_pos(t & 31)]);
+        }
+        (is_k ? KS : VS)[t] = x;
+      }
     }
   }
-  if (tid < 2 * PfTile<true>::KT) (tid < PfTile<true>::KT ? KS : VS)[tid & (PfTile<true>::KT - 1)] = tid < PfTile<true>::KT ? q_mul : 1.f;
 }
 
 // S^T = K Q^T for one 32-token unit of one wave: 32 query rows (two column
@@ -310,15 +474,42 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
   }
 }
 
-template <bool BF16, bool KVB, bool EXACT>
+// Q^T operands: column tile rt holds query rows q0+16rt .. +15 (the last row
+// repeated past L), k-step ks dims 32ks + 8g .. +7 of the lane's row c.
+template <bool BF16>
+__device__ __forceinline__ void load_query(typename MT<BF16>::vec (&qop)[2][4], const PrefillArgs& a, int b, int hq,
+                                           int q0, int c, int g) {
+  typedef typename MT<BF16>::vec V8;
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int qr = min(q0 + 16 * rt + c, a.L - 1);
+    const int64_t base = (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)qr * a.q_st;
+    const uint16_t* row = (const uint16_t*)a.q + base;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (a.q_vec) {
+        qop[rt][ks] = __builtin_bit_cast(V8, *(const v4i*)(row + 32 * ks + 8 * g));
+      } else {
+        v8s e;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = (short)row[32 * ks + 8 * g + i];
+        qop[rt][ks] = __builtin_bit_cast(V8, e);
+      }
+    }
+  }
+}
+
+template <bool BF16, int KF, int VF, bool EXACT>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
+  typedef PfGeom<KF, VF> GEO;
   typedef typename MT<BF16>::elem E;
   typedef typename MT<BF16>::vec V8;
-  constexpr int PF_KT = PfTile<KVB>::KT, VROW = PfTile<KVB>::VROW;
-  __shared__ __attribute__((aligned(16))) E Kl[2][PfTile<KVB>::K_ELEMS];
-  __shared__ __attribute__((aligned(16))) _Float16 Vl[2][PfTile<KVB>::V_ELEMS];
-  __shared__ __attribute__((aligned(16))) float KS[2][PF_KT];
-  __shared__ __attribute__((aligned(16))) float VS[2][PF_KT];
+  constexpr int KT = GEO::KT, U = GEO::U, VROW = GEO::VROW;
+  __shared__ __attribute__((aligned(16))) E Kl[2][GEO::K_ELEMS];
+  __shared__ __attribute__((aligned(16))) _Float16 Vl[2][GEO::V_ELEMS];
+  __shared__ __attribute__((aligned(16))) float KS[2][KT];
+  __shared__ __attribute__((aligned(16))) float VS[2][KT];
+  __shared__ __attribute__((aligned(16))) char stage[GEO::STAGE > 0 ? GEO::STAGE : 16];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
@@ -333,17 +524,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const bool active = w < a.G;
   const int hq = h * a.G + (active ? w : 0);
 
-  // Q^T operands: column tile rt holds query rows q0+16rt .. +15, k-step ks dims 32ks..32ks+31.
   V8 qop[2][4];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int qr = min(q0 + 16 * rt + c, a.L - 1);
-    const int64_t base = (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)qr * a.q_st;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qop[rt][ks][e] = MT<BF16>::from_float(load_as_float(a.q, base + 32 * ks + 8 * g + e, a.q_dtype));
-  }
+  load_query<BF16>(qop, a, b, hq, q0, c, g);
 
   float m_use[2] = {0.f, 0.f}, thr[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
   v4f acc[8][2];
@@ -353,8 +535,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     for (int rt = 0; rt < 2; ++rt) acc[n][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   // a sliding window (bf16 caches only) starts the scan at the first query's first visible key
-  const int window = KVB ? a.window : 0;
-  const int t_first = window > 0 ? max(0, P + q0 - window + 1) / PF_KT * PF_KT : 0;
+  const int window = GEO::BF ? a.window : 0;
+  const int t_first = window > 0 ? max(0, P + q0 - window + 1) / KT * KT : 0;
   // this workgroup's share of the keys, [lo, t_end): the split's range
   // (tile-aligned) within the query block's [t_first, t_blk); empty for some
   // splits.  A split that ends before t_blk ends on a tile boundary, so its
@@ -362,27 +544,33 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const int64_t s_lo = a.split_lo + (int64_t)split * a.split_len;
   const int lo = __builtin_amdgcn_readfirstlane((int)max((int64_t)t_first, s_lo));
   const int t_end = __builtin_amdgcn_readfirstlane((int)min((int64_t)t_blk, s_lo + a.split_len));
-  const auto fetch = [&](TileRegs& R, int t0) {
-    if constexpr (KVB) load_tile_bf16(R, a, b, h, t0, tid, t_end);
-    else load_tile(R, a, bh, t0, tid, t_end);
+  const auto stage_scales = [&](const TileRegs& R) {
+    if (GEO::STAGE > 0 && 8 * tid < GEO::STAGE) *(v2i*)(stage + 8 * tid) = R.sc;
   };
-  const auto put = [&](const TileRegs& R, int bf) {
-    if constexpr (KVB) store_tile_bf16<BF16>(R, Kl[bf], Vl[bf], KS[bf], VS[bf], tid, a.q_mul);
-    else store_tile<BF16>(R, Kl[bf], Vl[bf], KS[bf], VS[bf], tid, a.q_mul);
+  const auto convert = [&](const TileRegs& R, int bf, auto phase) {
+    convert_tile<BF16, KF, VF, decltype(phase)::value>(R, Kl[bf], Vl[bf], KS[bf], VS[bf], stage, tid, a.q_mul);
   };
-  // unconditional even for an empty range (lo >= t_end): every load then fails
-  // its liveness test and reads nothing; a branch here costs the int8 kernel
-  // 88 bytes of register spills
-  TileRegs R;
-  fetch(R, lo);
-  put(R, 0);
-  __syncthreads();
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
 
-  // Software pipeline over 32-token units (four per 128-token tile): the
-  // scores of unit k+1 are computed on the matrix cores while the VALU runs
-  // the softmax of unit k, so every unit's Q·Kᵀ overlaps another unit's
-  // softmax.  A tile's last unit is finished (softmax + P·V) in the next
-  // iteration, from the tile's buffer, which is refilled only after a barrier.
+  // Prologue: tile lo into buffer 0 (all phases), the next tile's bytes in
+  // flight.  Unconditional even for an empty range (lo >= t_end): every load
+  // then fails its liveness test and reads nothing.
+  TileRegs R;
+  load_tile<KF, VF>(R, a, b, h, bh, lo, tid, t_end);
+  stage_scales(R);
+  __syncthreads();
+  convert(R, 0, P0{});
+  convert(R, 0, P1{});
+  convert(R, 0, P2{});
+  __syncthreads();
+  if (lo + KT < t_end) load_tile<KF, VF>(R, a, b, h, bh, lo + KT, tid, t_end);
+
+  // Software pipeline over 32-token units: the scores of unit u+1 are computed
+  // on the matrix cores while the VALU runs the softmax of unit u.  A tile's
+  // last unit is finished (softmax + P·V) at unit 0 of the next tile, from the
+  // other buffer, which is refilled only at the end of that tile.
   v4f sc[2][2][2];    // scores of two units in flight: [unit parity][rt][j]
   bool pend = false;  // the previous unit awaits its softmax + P·V
   int pend_t = 0;
@@ -393,31 +581,33 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const auto needs_mask = [&](int tu) {
     return tu + 32 > qabs0 || tu + 32 > t_end || (window > 0 && tu < qabs0 + PF_QB - window);
   };
-  for (int t0 = lo; t0 < t_end; t0 += PF_KT) {
-    const bool more = t0 + PF_KT < t_end;
-    if (more) fetch(R, t0 + PF_KT);  // in flight during this tile
-    if (active) {
+  for (int t0 = lo; t0 < t_end; t0 += KT) {
+    const bool more = t0 + KT < t_end;  // uniform
 #pragma unroll
-      for (int u = 0; u < PF_KT / 32; ++u) {
-        const int tu = t0 + 32 * u;
-        const bool live = tu < t_end;
-        if (live) qk_unit<BF16>(Kl[buf] + 32 * u * PF_KROW, qop, sc[u & 1], c, g);
-        if (pend) {
-          // the unit before: this tile's unit u - 1, or the previous tile's last
-          const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? PF_KT - 32 : 32 * (u - 1);
-          softmax_pv_unit<VROW, EXACT>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
-                                acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
-        }
-        pend = live;
-        pend_t = tu;
+    for (int u = 0; u < U; ++u) {
+      const int tu = t0 + 32 * u;
+      const bool live = tu < t_end;
+      if (active && live) qk_unit<BF16>(Kl[buf] + 32 * u * PF_KROW, qop, sc[u & 1], c, g);
+      if (active && pend) {
+        // the unit before: this tile's unit u - 1, or the previous tile's last
+        const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? KT - 32 : 32 * (u - 1);
+        softmax_pv_unit<VROW, EXACT>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
+                                     acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
       }
+      pend = live;
+      pend_t = tu;
     }
     if (more) {
-      // Other waves may still be finishing the previous tile's last unit,
-      // which reads the other buffer: all of them pass this barrier before it
-      // is refilled.
+      // The next tile, whose bytes had this whole tile to arrive, into the
+      // other buffer: its scale bytes to the staging area, then (once every
+      // wave has finished the unit that read the other buffer) the
+      // dequantization; then the tile after next starts its way from HBM.
+      stage_scales(R);
       __syncthreads();
-      put(R, buf ^ 1);
+      convert(R, buf ^ 1, P0{});
+      convert(R, buf ^ 1, P1{});
+      convert(R, buf ^ 1, P2{});
+      if (t0 + 2 * KT < t_end) load_tile<KF, VF>(R, a, b, h, bh, t0 + 2 * KT, tid, t_end);
       __syncthreads();
       buf ^= 1;
     }
@@ -425,8 +615,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   // still pending: the last tile's last unit (every unit of a tile is visited,
   // and a tile has an even number of units, so its scores are in sc[1])
   if (active && pend)
-    softmax_pv_unit<VROW, EXACT>(sc[1], Vl[buf] + PF_KT - 32, KS[buf] + PF_KT - 32, VS[buf] + PF_KT - 32, m_use, thr,
-                          l_run, acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
+    softmax_pv_unit<VROW, EXACT>(sc[1], Vl[buf] + KT - 32, KS[buf] + KT - 32, VS[buf] + KT - 32, m_use, thr, l_run,
+                                 acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
 
   if (!active) return;
   if (a.S > 1) {
@@ -509,7 +699,7 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
 PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
   PrefillPlan p{};
   p.nqb = (a.L + PF_QB - 1) / PF_QB;
-  const int kt = a.kv_bf16 ? PfTile<true>::KT : PfTile<false>::KT;
+  const int kt = a.kv_bf16 ? PfGeom<FMT_BF, FMT_BF>::KT : PfGeom<8, 8>::KT;
   // keys any query block scans: from the first block's window start to T
   const int64_t P = a.T - a.L;
   const int64_t lo = (a.kv_bf16 && a.window > 0) ? std::max<int64_t>(0, P - a.window + 1) / kt * kt : 0;
@@ -541,15 +731,15 @@ size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S) {
   return rows * HEAD_DIM * 4 + rows * 2 * 4;
 }
 
-template <bool EXACT>
-static void launch_prefill_pv(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
-  if (a.kv_bf16) {
-    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, true, EXACT>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((prefill_kernel<false, true, EXACT>), grid, block, 0, stream, a);
-  } else {
-    if (a.q_dtype == DT_BF16) hipLaunchKernelGGL((prefill_kernel<true, false, EXACT>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((prefill_kernel<false, false, EXACT>), grid, block, 0, stream, a);
-  }
+template <bool BF16, bool EXACT>
+static void launch_formats(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  const int kf = a.k_fmt, vf = a.v_fmt;
+  if (kf == FMT_BF) hipLaunchKernelGGL((prefill_kernel<BF16, FMT_BF, FMT_BF, EXACT>), grid, block, 0, stream, a);
+  else if (kf == 8 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 8, EXACT>), grid, block, 0, stream, a);
+  else if (kf == 8 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 4, EXACT>), grid, block, 0, stream, a);
+  else if (kf == 4 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 8, EXACT>), grid, block, 0, stream, a);
+  else if (kf == 4 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 4, EXACT>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8, FMT_A4, EXACT>), grid, block, 0, stream, a);
 }
 
 // Fewest keys any query row of the launch sees: the first row's causal
@@ -562,8 +752,14 @@ static int64_t fewest_visible_keys(const PrefillArgs& a) {
 
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)(a.nqb * a.S), a.Hkv, a.B), block(512);
-  if (fewest_visible_keys(a) < EXACT_PV_BELOW) launch_prefill_pv<true>(a, grid, block, stream);
-  else launch_prefill_pv<false>(a, grid, block, stream);
+  const bool exact = fewest_visible_keys(a) < EXACT_PV_BELOW;
+  if (a.q_dtype == DT_BF16) {
+    if (exact) launch_formats<true, true>(a, grid, block, stream);
+    else launch_formats<true, false>(a, grid, block, stream);
+  } else {
+    if (exact) launch_formats<false, true>(a, grid, block, stream);
+    else launch_formats<false, false>(a, grid, block, stream);
+  }
   if (a.S > 1) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

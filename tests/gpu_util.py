@@ -50,3 +50,22 @@ def assert_close(got: np.ndarray, ref: np.ndarray, what=""):
     assert np.all(err <= bound), (
         f"{what}: max |err| {err.max():.3e} (at {worst}: got {got[worst]:.6f} ref {ref[worst]:.6f})"
     )
+
+
+def round_to(x: np.ndarray, dtype) -> np.ndarray:
+    """float32 values rounded to nearest even in a 16-bit torch dtype."""
+    if dtype == torch.bfloat16:
+        return O.bf16_rn(x)
+    if dtype == torch.float16:
+        return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+    return np.asarray(x, np.float32)
+
+
+def prefill_side(xhat: np.ndarray, quantized_kv, qdtype) -> np.ndarray:
+    """One side (K or V) of a quantized cache as the prefill kernel attends
+    over it: int8 codes exactly (x̂ as dequantized), 4-bit and affine values
+    rounded to the query dtype, as the reference dequantizes the cache to it
+    before its attention (model.py:194-195)."""
+    if quantized_kv.bits == 8 and not quantized_kv.affine:
+        return xhat
+    return round_to(xhat, qdtype)

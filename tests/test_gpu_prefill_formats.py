@@ -1,14 +1,16 @@
-"""Prefill over the 4-bit and affine cache formats (dequantize, then bf16 prefill).
+"""Prefill over the 4-bit, mixed and affine cache formats.
 
-The reference's prefill branch dequantizes the cache to bf16 before its
-attention (engine/src/rec_mlx/model.py:191-203); here ``rec_kv_dequant_bf16``
-writes bf16 K/V and ``rec_prefill_bf16`` attends over them.
+The reference's prefill branch dequantizes the cache to the query dtype
+before its attention (engine/src/rec_mlx/model.py:191-203); ``rec_prefill_attn``
+dequantizes each K/V tile into on-chip memory instead, 4-bit and affine values
+rounded to the query dtype, int8 codes exactly.
 
-* the dequantized tensors are bit-exact: bf16 round-to-nearest-even of the
+* ``dequantize_kv`` (bf16 copies, ``rec_kv_dequant_bf16``, kept for callers and
+  for sliding-window masks) is bit-exact: bf16 round-to-nearest-even of the
   oracle's float32 x̂ (int8 q·s, uint4 (q - z)·s, affine q·s + b; every product
   is exact in float32, so one rounding in both);
 * the attention output lies within 2e-3 absolute + 1e-3 relative of the
-  float64 oracle over those bf16 values.
+  float64 oracle over the values the kernel attends over.
 """
 
 import numpy as np
@@ -17,7 +19,7 @@ import torch
 
 import oracle as O
 from rec_amd import MixedQuantizedKVCache, QuantizedKVCache, attend, dequantize_kv, synthetic, to_logical
-from tests.gpu_util import SCALE, assert_close, dequant, f32
+from tests.gpu_util import SCALE, assert_close, dequant, f32, prefill_side
 
 pytestmark = pytest.mark.gpu
 
@@ -90,14 +92,14 @@ def test_prefill_formats_match_oracle(gpu, case):
     out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32)
     torch.cuda.synchronize()
     kv_k, kv_v = cache.keys_and_values()
-    kh, vh = O.bf16_rn(oracle_xhat(kv_k)), O.bf16_rn(oracle_xhat(kv_v))
+    kh, vh = prefill_side(oracle_xhat(kv_k), kv_k, dtype), prefill_side(oracle_xhat(kv_v), kv_v, dtype)
     ref = O.attention(f32(q), kh, vh, SCALE, None if sinks is None else f32(sinks), mask)
     assert_close(f32(out), ref, f"case {case}")
 
 
 def test_affine_chunked_prefill_then_decode(gpu):
-    """The MixedQuantizedKVCache flow of Attention.__call__: chunked prefill
-    (dequantize + bf16 prefill), then fused decode steps over the same cache."""
+    """The MixedQuantizedKVCache flow of Attention.__call__: chunked prefill,
+    then fused decode steps over the same cache."""
     B, Hq, Hkv, T, steps = 1, 32, 4, 700, 3
     k = synthetic.kv((B, Hkv, T + steps, 128), 31, dtype=torch.bfloat16)
     v = synthetic.kv((B, Hkv, T + steps, 128), 32, dtype=torch.bfloat16)
@@ -108,7 +110,8 @@ def test_affine_chunked_prefill_then_decode(gpu):
         out = attend(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], cache, SCALE, "causal", sinks, out_dtype=torch.float32)
         torch.cuda.synchronize()
         kv_k, kv_v = cache.keys_and_values()
-        kh, vh = O.bf16_rn(oracle_xhat(kv_k)), O.bf16_rn(oracle_xhat(kv_v))
+        kh = prefill_side(oracle_xhat(kv_k), kv_k, torch.bfloat16)
+        vh = prefill_side(oracle_xhat(kv_v), kv_v, torch.bfloat16)
         ref = O.attention(f32(q[:, :, a:b]), kh, vh, SCALE, f32(sinks), "causal")
         assert_close(f32(out), ref, f"chunk [{a}, {b})")
     for t in range(T, T + steps):

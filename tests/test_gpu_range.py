@@ -21,7 +21,7 @@ import torch
 
 import oracle as O
 from rec_amd import QuantizedKVCache, attend, synthetic
-from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize
+from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize, prefill_side
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +53,7 @@ CASES = [
     (8, 4, 1200.0, 3000, 1, None),  # 4-bit V group ranges near 5,000
     (4, 4, 1200.0, 5000, 1, 2),  # eight-wave uint4 workgroups
     (8, 8, 16000.0, 700, 40, None),  # int8 prefill
-    (8, 4, 1200.0, 700, 40, None),  # prefill over a 4-bit V cache (bf16 copies)
+    (8, 4, 1200.0, 700, 40, None),  # prefill over a 4-bit V cache
 ]
 
 
@@ -76,8 +76,9 @@ def test_large_v_scales_rising_scores(gpu, case):
     torch.cuda.synchronize()
     rk, rv = oracle_quantize(f32(k), kb), oracle_quantize(f32(v), vb)
     kh, vh = dequant(kb, *rk), dequant(vb, *rv)
-    if L > 1 and (kb, vb) != (8, 8):  # prefill over a 4-bit cache attends over bf16 copies
-        kh, vh = O.bf16_rn(kh), O.bf16_rn(vh)
+    if L > 1:  # the prefill rounds 4-bit values to the query dtype
+        kq, vq = cache.keys_and_values()
+        kh, vh = prefill_side(kh, kq, q.dtype), prefill_side(vh, vq, q.dtype)
     ref = O.attention(f32(q), kh, vh, SCALE, f32(sinks), "causal")
     got = f32(out).astype(np.float64)
     assert np.all(np.isfinite(got)), "non-finite output"

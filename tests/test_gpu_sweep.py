@@ -4,8 +4,8 @@ dtypes and sinks drawn from a fixed generator (the same 40 cases every run;
 REC_SWEEP_CASES=n draws n, the first 40 being these; two cases of the
 400-case draw always run as regressions).
 Outputs within 2e-3 abs + 1e-3 rel of the float64 oracle over the cache read
-back from the GPU and dequantized (bf16-rounded too for prefill over 4-bit and
-affine caches, which attends over bf16 copies)."""
+back from the GPU and dequantized (for a prefill, 4-bit and affine values
+rounded to the query dtype, as the kernel and the reference dequantize them)."""
 
 import os
 
@@ -16,7 +16,7 @@ import torch
 import oracle as O
 from rec_amd import (FixedKVCache, KVStorage, MixedQuantizedKVCache, QuantizedKVCache, attend, synthetic,
                      to_logical)
-from tests.gpu_util import SCALE, assert_close, dequant, f32
+from tests.gpu_util import SCALE, assert_close, dequant, f32, prefill_side
 
 pytestmark = pytest.mark.gpu
 
@@ -91,7 +91,7 @@ def test_sweep(gpu, case):
     else:
         kv_k, kv_v = cache.keys_and_values()
         kh, vh = oracle_xhat(kv_k), oracle_xhat(kv_v)
-        if L > 1 and fmt != "i8":  # prefill over these formats runs on the bf16-rounded cache
-            kh, vh = O.bf16_rn(kh), O.bf16_rn(vh)
+        if L > 1:  # the prefill rounds 4-bit and affine values to the query dtype
+            kh, vh = prefill_side(kh, kv_k, dt), prefill_side(vh, kv_v, dt)
     ref = O.attention(f32(q), kh, vh, SCALE, None if sinks is None else f32(sinks), "causal")
     assert_close(f32(out), ref, f"case {case}")
