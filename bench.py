@@ -681,7 +681,7 @@ def main(argv=None):
             t = json.load(f)
         traffic = t.get("hbm_bytes_per_launch")
         traffic_source = (f"not measured by this run: {os.path.relpath(TRAFFIC_FILE, ROOT)}, rocprofv3 FETCH_SIZE and "
-                          f"WRITE_SIZE passes over this kernel at source commit {t.get('commit', 'unrecorded')}")
+                          f"WRITE_SIZE passes over this kernel at source commit {t.get('source_commit', 'unrecorded')}")
 
     cpu = None
     if not args.no_cpu_baseline:
