@@ -399,10 +399,18 @@ def run_q4_gemv(steps, seed):
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
-def run_prefill(P, L, steps, warmup, seed):
-    """Chunked prefill: quantize-append L new tokens after a P-token int8 prefix,
-    then L causal bf16 queries attend over all P + L tokens.  Each step rewrites
-    the same L positions, so every step does identical work."""
+PREFILL_FORMATS = {
+    "int8": "int8 symmetric, fp16 scale per (token, head)",
+    "uint4": "uint4 asymmetric, fp16 scale + zero-point per 32 dims",
+    "affine": "MLX-style affine group 64: 8-bit K, 4-bit V, bf16 scale + bias",
+}
+
+
+def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
+    """Chunked prefill: quantize-append L new tokens after a P-token prefix in
+    the cache format `fmt`, then L causal bf16 queries attend over all P + L
+    tokens, every K/V tile dequantized on chip.  Each step rewrites the same L
+    positions, so every step does identical work."""
     import torch
 
     import rec_amd
@@ -410,8 +418,12 @@ def run_prefill(P, L, steps, warmup, seed):
 
     lib = rec_amd.library()
     T = P + L
-    log(f"prefill: building a {P}-token prefix")
-    c = rec_amd.QuantizedKVCache(32, 8, 8, max_tokens=T)
+    log(f"prefill ({fmt}): building a {P}-token prefix")
+    if fmt == "affine":
+        c = rec_amd.MixedQuantizedKVCache(max_tokens=T)
+    else:
+        bits = 8 if fmt == "int8" else 4
+        c = rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T)
     k = synthetic.kv((1, HKV, P, D), seed, kind="outliers", frac=0.01)
     v = synthetic.kv((1, HKV, P, D), seed + 1, kind="outliers", frac=0.01)
     c.update_and_fetch(k, v)
@@ -424,21 +436,28 @@ def run_prefill(P, L, steps, warmup, seed):
     sinks = torch.randn(HQ, generator=g, device="cuda")
     out = torch.empty((1, HQ, L, D), dtype=torch.float32, device="cuda")
     c._reserve(1, HKV, T, "cuda")
-    (kc, ks, _), (vc, vs, _) = c.keys, c.values
+    kq, vq = c.keys_and_values()
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    # cache bytes per (token, kv head): codes + scales (+ zero-points) of K and V
+    tok_bytes = sum(t.nbytes for kv in (kq, vq) for t in (kv.codes, kv.scales, kv.zeros) if t is not None)
+    tok_bytes /= HKV * c.capacity
     # key splits when the chunk is short (the automatic plan; none at 2048 queries)
     ws = torch.empty(max(16, lib.rec_prefill_workspace_bytes(1, HKV, L, 0)), dtype=torch.uint8, device="cuda")
 
     def append():
         st = torch.cuda.current_stream().cuda_stream
         rc = lib.rec_kv_append(kn.data_ptr(), vn.data_ptr(), _lib.REC_BF16, *kn.stride()[:3], *vn.stride()[:3],
-                               8, kc.data_ptr(), ks.data_ptr(), None, 8, vc.data_ptr(), vs.data_ptr(), None,
+                               kq.code, kq.codes.data_ptr(), kq.scales.data_ptr(), ptr(kq.zeros),
+                               vq.code, vq.codes.data_ptr(), vq.scales.data_ptr(), ptr(vq.zeros),
                                1, HKV, L, D, P, c.capacity, st)
         _lib.check(rc, "rec_kv_append")
 
     def attention():
         st = torch.cuda.current_stream().cuda_stream
-        rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3], 8, kc.data_ptr(), ks.data_ptr(),
-                                  None, 8, vc.data_ptr(), vs.data_ptr(), None, sinks.data_ptr(), SCALE, 1,
+        rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3],
+                                  kq.code, kq.codes.data_ptr(), kq.scales.data_ptr(), ptr(kq.zeros),
+                                  vq.code, vq.codes.data_ptr(), vq.scales.data_ptr(), ptr(vq.zeros),
+                                  sinks.data_ptr(), SCALE, 1,
                                   1, HQ, HKV, D, L, T, c.capacity, 0, ws.data_ptr(), ws.numel(), out.data_ptr(), st)
         _lib.check(rc, "rec_prefill_attn")
 
@@ -459,14 +478,15 @@ def run_prefill(P, L, steps, warmup, seed):
     pairs = L * P + L * (L + 1) // 2
     flops = 4.0 * D * HQ * pairs
     tflops = flops / (ms_att * 1e-3) / 1e12
-    kv_bytes = T * HKV * 2 * (D + 2)  # int8 K and V rows and their fp16 scales, read once
-    log(f"prefill {P}+{L}: {ms_step:.3f} ms/step, attention {ms_att:.3f} ms = {tflops:.0f} TFLOP/s, "
+    kv_bytes = round(T * HKV * tok_bytes)  # every cached K/V row and its scales, read once
+    log(f"prefill ({fmt}) {P}+{L}: {ms_step:.3f} ms/step, attention {ms_att:.3f} ms = {tflops:.0f} TFLOP/s, "
         f"{kv_bytes / (ms_att * 1e-3) / 1e9:.0f} GB/s of K/V")
     del g_step, g_att, c
     torch.cuda.empty_cache()
     return dict(
         prefix=P,
         new_tokens=L,
+        kv_format=PREFILL_FORMATS[fmt],
         ms_per_step=round(ms_step, 4),
         append_ms=round(ms_step - ms_att, 4),
         attention_ms=round(ms_att, 4),
@@ -670,10 +690,14 @@ def main(argv=None):
         rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
 
     rpf = rpf_short = None
+    rpf_fmt = {}
     if not args.no_prefill:
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
         # a short chunk over a long cache (a new chat turn): the keys are split
         rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
+        # the same long chunk over the 4-bit and affine caches
+        for i, fmt in enumerate(("uint4", "affine")):
+            rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
 
     traffic, traffic_source = None, None
     if os.path.exists(TRAFFIC_FILE):
@@ -815,6 +839,8 @@ def main(argv=None):
         result["prefill_65536_plus_2048"] = rpf
     if rpf_short is not None:
         result["prefill_32768_plus_20"] = rpf_short
+    for fmt, r in rpf_fmt.items():
+        result[f"prefill_65536_plus_2048_{fmt}"] = r
     print(json.dumps(result), flush=True)
     return 0
 
