@@ -279,6 +279,30 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
+ * Growable bf16 layer region (KVStorage's banks): reserves the address range
+ * of `rows` rows (B * 2 * Hkv for a layer: K then V per batch row) of
+ * `max_tokens` tokens of `token_bytes` each, row r at base + r * max_tokens *
+ * token_bytes, and maps device memory into it one bank of `bank_tokens`
+ * tokens per row at a time.  Mapped banks never move, so growing copies
+ * nothing and the region is one strided tensor (token stride token_bytes,
+ * row stride max_tokens * token_bytes) for rec_kv_write_bf16,
+ * rec_decode_bf16 and rec_prefill_bf16.  New banks hold undefined bytes.
+ * rec_region_create: device ordinal; bank_tokens * token_bytes must be a
+ * multiple of the device's mapping granularity (2 MiB on MI355X); *handle
+ * and *base receive the region and its device address (nothing mapped yet).
+ * rec_region_grow: map banks until `tokens` tokens per row are backed;
+ * *capacity (may be NULL) receives the tokens now backed.
+ * rec_region_destroy: unmap and free; no work on the region may be in flight.
+ * Replaces the bank list of KVStorage, engine/src/rec_mlx/cache.py:46-84
+ * (four 65,536-token banks added without copying, the kernel picking a bank
+ * per token, engine/src/rec_mlx/kernels/megakernel.py:115-135).
+ */
+int rec_region_create(int device, int64_t rows, int64_t max_tokens, int64_t token_bytes, int64_t bank_tokens,
+                      void** handle, void** base);
+int rec_region_grow(void* handle, int64_t tokens, int64_t* capacity);
+int rec_region_destroy(void* handle);
+
+/*
  * int4 group-64 GEMV (MLX affine 4-bit, the format of the decoder's
  * projections, experts and lm head): y[m] = x[m] · Wᵀ for an (N, K) matrix
  * given as MLX words w (N, K/8) uint32 (code e of a word at bits 4e), bf16

@@ -36,6 +36,9 @@ SIGNATURES = {
         [_p, _p, _i, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _p],
     ),
     "rec_decode_default_splits": (_i, [_i, _i, _i64]),
+    "rec_region_create": (_i, [_i, _i64, _i64, _i64, _i64, ctypes.POINTER(_p), ctypes.POINTER(_p)]),
+    "rec_region_grow": (_i, [_p, _i64, ctypes.POINTER(_i64)]),
+    "rec_region_destroy": (_i, [_p]),
     "rec_decode_workspace_bytes": (_sz, [_i, _i, _i]),
     "rec_workspace_init": (_i, [_p, _sz, _p]),
     "rec_decode_attn": (

@@ -6,6 +6,7 @@
 
 #include <cmath>
 #include <mutex>
+#include <vector>
 
 #include "../../include/rec_amd.h"
 #include "kernels.h"
@@ -728,6 +729,140 @@ int rec_q4_gemv(const void* packed, int64_t N, int64_t K, const uint16_t* x, int
   a.out_dtype = out_dtype == REC_F32 ? DT_F32 : DT_BF16;
   a.out_stride = out_stride;
   return launched(launch_q4_gemv(a, (hipStream_t)stream), "q4 gemv launch");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------
+// Growable KV regions on HIP virtual memory.  A region reserves the address
+// range of `rows` rows of `max_tokens` tokens each once, and backs it with
+// device memory one bank (bank_tokens tokens of every row) at a time; a
+// bank, once mapped, stays at its address until the region is destroyed, so
+// growing never copies and every kernel addresses the region as one strided
+// tensor (row r at base + r * max_tokens * token_bytes).
+namespace {
+
+struct Region {
+  int device = 0;
+  char* base = nullptr;
+  size_t reserved = 0;
+  int64_t rows = 0, max_tokens = 0, token_bytes = 0, bank_tokens = 0;
+  int banks = 0;                                  // banks mapped so far
+  std::vector<hipMemGenericAllocationHandle_t> handles;  // rows x banks, row-major per bank
+};
+
+size_t bank_bytes(const Region& r) { return (size_t)r.bank_tokens * (size_t)r.token_bytes; }
+char* bank_addr(const Region& r, int64_t row, int bank) {
+  return r.base + (size_t)row * (size_t)r.max_tokens * (size_t)r.token_bytes + (size_t)bank * bank_bytes(r);
+}
+
+// Unmap and release everything mapped so far, then free the reservation.
+void region_release(Region* r) {
+  for (int b = 0; b < r->banks; ++b)
+    for (int64_t row = 0; row < r->rows; ++row) hipMemUnmap(bank_addr(*r, row, b), bank_bytes(*r));
+  for (auto h : r->handles) hipMemRelease(h);
+  r->handles.clear();
+  r->banks = 0;
+  if (r->base) hipMemAddressFree(r->base, r->reserved);
+  r->base = nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rec_region_create(int device, int64_t rows, int64_t max_tokens, int64_t token_bytes, int64_t bank_tokens,
+                      void** handle, void** base) {
+  if (!handle || !base) return fail(REC_EINVAL, "region: null output pointer");
+  *handle = nullptr;
+  *base = nullptr;
+  if (rows < 1 || token_bytes < 1 || bank_tokens < 1 || max_tokens < bank_tokens || max_tokens % bank_tokens != 0)
+    return fail(REC_EINVAL, "region: rows %lld, token_bytes %lld, bank_tokens %lld, max_tokens %lld (a multiple of "
+                "bank_tokens) must be positive", (long long)rows, (long long)token_bytes, (long long)bank_tokens,
+                (long long)max_tokens);
+  int vmm = 0;
+  hipError_t e = hipDeviceGetAttribute(&vmm, hipDeviceAttributeVirtualMemoryManagementSupported, device);
+  if (e != hipSuccess) return fail(REC_EINVAL, "region: device %d: %s", device, hipGetErrorString(e));
+  if (!vmm) return fail(REC_EUNSUPPORTED, "region: device %d has no virtual memory management", device);
+  hipMemAllocationProp prop{};
+  prop.type = hipMemAllocationTypePinned;
+  prop.location.type = hipMemLocationTypeDevice;
+  prop.location.id = device;
+  size_t gran = 0;
+  e = hipMemGetAllocationGranularity(&gran, &prop, hipMemAllocationGranularityMinimum);
+  if (e != hipSuccess || gran == 0) return fail(REC_ELAUNCH, "region: allocation granularity: %s", hipGetErrorString(e));
+  const size_t bank = (size_t)bank_tokens * (size_t)token_bytes;
+  if (bank % gran != 0)
+    return fail(REC_EINVAL, "region: a bank of %zu bytes per row is not a multiple of the %zu-byte mapping granularity",
+                bank, gran);
+  Region* r = new Region();
+  r->device = device;
+  r->rows = rows;
+  r->max_tokens = max_tokens;
+  r->token_bytes = token_bytes;
+  r->bank_tokens = bank_tokens;
+  r->reserved = (size_t)rows * (size_t)max_tokens * (size_t)token_bytes;
+  void* p = nullptr;
+  e = hipMemAddressReserve(&p, r->reserved, gran, nullptr, 0);
+  if (e != hipSuccess) {
+    size_t n = r->reserved;
+    delete r;
+    return fail(REC_ELAUNCH, "region: reserving %zu bytes of address space: %s", n, hipGetErrorString(e));
+  }
+  r->base = (char*)p;
+  *handle = r;
+  *base = p;
+  return ok();
+}
+
+int rec_region_grow(void* handle, int64_t tokens, int64_t* capacity) {
+  Region* r = (Region*)handle;
+  if (!r) return fail(REC_EINVAL, "region: null handle");
+  if (tokens < 0 || tokens > r->max_tokens)
+    return fail(REC_ECAPACITY, "region: %lld tokens exceed the %lld reserved", (long long)tokens,
+                (long long)r->max_tokens);
+  const int want = (int)((tokens + r->bank_tokens - 1) / r->bank_tokens);
+  hipMemAllocationProp prop{};
+  prop.type = hipMemAllocationTypePinned;
+  prop.location.type = hipMemLocationTypeDevice;
+  prop.location.id = r->device;
+  hipMemAccessDesc access{};
+  access.location = prop.location;
+  access.flags = hipMemAccessFlagsProtReadWrite;
+  const size_t bytes = bank_bytes(*r);
+  while (r->banks < want) {
+    // map bank r->banks of every row; on failure undo this bank's maps
+    std::vector<hipMemGenericAllocationHandle_t> made;
+    hipError_t e = hipSuccess;
+    for (int64_t row = 0; row < r->rows; ++row) {
+      hipMemGenericAllocationHandle_t h{};
+      if ((e = hipMemCreate(&h, bytes, &prop, 0)) != hipSuccess) break;
+      if ((e = hipMemMap(bank_addr(*r, row, r->banks), bytes, 0, h, 0)) != hipSuccess) {
+        hipMemRelease(h);
+        break;
+      }
+      made.push_back(h);  // made[k] is mapped at row k
+      if ((e = hipMemSetAccess(bank_addr(*r, row, r->banks), bytes, &access, 1)) != hipSuccess) break;
+    }
+    if (e != hipSuccess) {
+      for (int64_t k = 0; k < (int64_t)made.size(); ++k) hipMemUnmap(bank_addr(*r, k, r->banks), bytes);
+      for (auto h : made) hipMemRelease(h);
+      return fail(REC_ELAUNCH, "region: mapping bank %d (%zu bytes per row, %lld rows): %s", r->banks, bytes,
+                  (long long)r->rows, hipGetErrorString(e));
+    }
+    r->handles.insert(r->handles.end(), made.begin(), made.end());
+    ++r->banks;
+  }
+  if (capacity) *capacity = (int64_t)r->banks * r->bank_tokens;
+  return ok();
+}
+
+int rec_region_destroy(void* handle) {
+  Region* r = (Region*)handle;
+  if (!r) return ok();
+  region_release(r);
+  delete r;
+  return ok();
 }
 
 }  // extern "C"

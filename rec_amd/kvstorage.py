@@ -1,12 +1,15 @@
 """bf16 KV cache with the reference's production cache surface.
 
 Mirrors ``KVStorage`` / ``FixedKVCache`` (engine/src/rec_mlx/cache.py:48-150):
-each layer owns a token-major bf16 region ``[2][Hkv][capacity][128]`` (K
+each layer owns a token-major bf16 region ``[B][2][Hkv][tokens][128]`` (K
 then V, per batch row), written by ``rec_kv_write_bf16`` and read in place by
-the bf16 decode kernel (``rec_decode_bf16``).  The reference grows its
-storage in banks of 65,536 tokens up to four banks (cache.py:46-78); here a
-layer's region is one allocation whose capacity grows in the same 65,536-token
-steps to the same 262,144-token limit, the earlier contents copied over.
+the bf16 decode and prefill kernels.  The reference grows its storage by
+adding banks of 65,536 tokens, up to four, without copying, and its kernels
+pick a bank per token (cache.py:46-84, megakernel.py:115-135).  Here each
+layer reserves the address range of all four banks once (HIP virtual memory,
+``rec_region_*``) and device memory is mapped into it a bank at a time:
+growing copies nothing, mapped banks keep their addresses (views taken
+before a growth stay valid), and the kernels see one strided tensor.
 Sliding-window layers keep a ring of window slots, ``FixedSlidingKVCache``
 (the surface of cache.py:153-258); decode attends over its occupied slots with
 the same kernel.
@@ -14,6 +17,7 @@ the same kernel.
 
 from __future__ import annotations
 
+import ctypes
 from typing import List, NamedTuple, Optional
 
 import torch
@@ -23,6 +27,7 @@ from .cache import _DTYPES, HEAD_DIM
 
 BLOCK_TOKENS = 65536
 MAX_BLOCKS = 4
+MAX_TOKENS = BLOCK_TOKENS * MAX_BLOCKS
 
 
 def _stride3(x):
@@ -31,40 +36,98 @@ def _stride3(x):
     return x, x.stride(0), x.stride(1), x.stride(2)
 
 
+class _RegionMemory:
+    """Exports a region's mapped range to torch; tensors made from it keep
+    it, and so the region, alive."""
+
+    def __init__(self, interface: dict, region: "_Region"):
+        self.__cuda_array_interface__ = interface
+        self.region = region
+
+
+class _Region:
+    """One layer's growable region: ``rows`` rows of MAX_TOKENS bf16 tokens
+    reserved, banks of BLOCK_TOKENS mapped on demand (``rec_region_*``)."""
+
+    def __init__(self, device: torch.device, batch: int, n_kv_heads: int):
+        lib = _lib.load()
+        self.device, self.shape = device, (batch, 2, n_kv_heads)
+        rows = batch * 2 * n_kv_heads
+        h, base = ctypes.c_void_p(), ctypes.c_void_p()
+        with torch.cuda.device(device):
+            rc = lib.rec_region_create(device.index, rows, MAX_TOKENS, HEAD_DIM * 2, BLOCK_TOKENS,
+                                       ctypes.byref(h), ctypes.byref(base))
+        _lib.check(rc, "rec_region_create")
+        self.handle, self.base, self.capacity = h.value, base.value, 0
+
+    def grow(self, tokens: int) -> torch.Tensor:
+        """Back the first ``tokens`` tokens of every row, zero the new banks,
+        and return the ``(B, 2, Hkv, capacity, 128)`` bf16 view."""
+        cap = ctypes.c_int64()
+        with torch.cuda.device(self.device):
+            rc = _lib.load().rec_region_grow(self.handle, tokens, ctypes.byref(cap))
+        _lib.check(rc, "rec_region_grow")
+        old, self.capacity = self.capacity, cap.value
+        view = self.view()
+        if self.capacity > old:
+            view[:, :, :, old:].zero_()  # the reference's banks start as zeros
+        return view
+
+    def view(self) -> torch.Tensor:
+        B, two, H = self.shape
+        row = MAX_TOKENS * HEAD_DIM  # elements between consecutive rows
+        cai = {
+            "shape": (B, two, H, self.capacity, HEAD_DIM),
+            "strides": tuple(2 * x for x in (two * H * row, H * row, row, HEAD_DIM, 1)),
+            "typestr": "<i2",
+            "data": (self.base, False),
+            "version": 3,
+            "stream": None,
+        }
+        return torch.as_tensor(_RegionMemory(cai, self), device=self.device).view(torch.bfloat16)
+
+    def __del__(self):
+        handle, self.handle = getattr(self, "handle", None), None
+        if handle:
+            try:
+                torch.cuda.synchronize(self.device)  # no kernel may still read or write the banks
+            except Exception:  # interpreter shutdown: the process exit releases the mappings
+                return
+            _lib.load().rec_region_destroy(handle)
+
+
 class KVStorage:
     """bf16 K/V regions of ``layers`` full-attention layers.
 
     ``layer(i, count)`` returns the ``(B, 2, Hkv, count, 128)`` view of layer
     ``i`` (the reference's ``(2, Hkv, count, 128)`` for ``B == 1``, cache.py:86-95);
     ``write(i, offset, keys, values)`` stores ``(B, Hkv, L, 128)`` rows at
-    ``[offset, offset + L)`` (cache.py:97-119).
+    ``[offset, offset + L)`` (cache.py:97-119).  ``grow`` maps further
+    65,536-token banks (cache.py:63-70); the capacity never shrinks.
     """
 
     def __init__(self, layers: int, capacity: int, n_kv_heads: int = 4, *, batch: int = 1, device=None):
         if layers < 1 or n_kv_heads < 1 or batch < 1:
             raise ValueError("layers, n_kv_heads and batch must be positive")
         self.n_layers, self.n_kv_heads, self.batch = layers, n_kv_heads, batch
-        self.device = torch.device(device) if device is not None else torch.device("cuda")
-        self.regions: List[Optional[torch.Tensor]] = [None] * layers
+        dev = torch.device(device) if device is not None else torch.device("cuda")
+        self.device = torch.device(dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+        self._banks = [_Region(self.device, batch, n_kv_heads) for _ in range(layers)]
+        self.regions: List[torch.Tensor] = []
         self.capacity = 0
         self.grow(capacity)
 
     @property
     def nbytes(self) -> int:
-        return sum(r.numel() * r.element_size() for r in self.regions if r is not None)
+        return sum(r.numel() * r.element_size() for r in self.regions)
 
     def grow(self, capacity: int):
-        if not 0 < capacity <= BLOCK_TOKENS * MAX_BLOCKS:
+        if not 0 < capacity <= MAX_TOKENS:
             raise ValueError("Decode context limit exhausted")
-        cap = -(-capacity // BLOCK_TOKENS) * BLOCK_TOKENS
-        if cap <= self.capacity:
+        if capacity <= self.capacity:
             return
-        for i, old in enumerate(self.regions):
-            new = torch.zeros((self.batch, 2, self.n_kv_heads, cap, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
-            if old is not None:
-                new[:, :, :, : old.shape[3]] = old
-            self.regions[i] = new
-        self.capacity = cap
+        self.regions = [r.grow(capacity) for r in self._banks]
+        self.capacity = self._banks[0].capacity
 
     def layer(self, index: int, count: Optional[int] = None) -> torch.Tensor:
         count = self.capacity if count is None else count

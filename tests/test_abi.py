@@ -251,3 +251,16 @@ def test_fused_decode_workspace_size(lib, B, Hkv, splits):
         short = lib.rec_decode_workspace_bytes(B, Hkv, 2) - 1
         assert _append_attn(lib, B=B, Hq=8 * Hkv, Hkv=Hkv, T=4000, cap=4096, splits=1, ws=16, wsb=short) == (
             _lib.REC_EWORKSPACE)
+
+
+def test_region_validation(lib):
+    import ctypes
+
+    h, base = ctypes.c_void_p(), ctypes.c_void_p()
+    # rows, token bytes and bank size must be positive, max_tokens a multiple of the bank
+    assert lib.rec_region_create(0, 0, 262144, 256, 65536, ctypes.byref(h), ctypes.byref(base)) == _lib.REC_EINVAL
+    assert lib.rec_region_create(0, 8, 100000, 256, 65536, ctypes.byref(h), ctypes.byref(base)) == _lib.REC_EINVAL
+    assert "bank_tokens" in _lib.last_error()
+    assert lib.rec_region_create(0, 8, 262144, 256, 65536, None, None) == _lib.REC_EINVAL
+    assert lib.rec_region_grow(None, 1, None) == _lib.REC_EINVAL
+    assert lib.rec_region_destroy(None) == _lib.REC_OK

@@ -166,6 +166,48 @@ def test_bf16_rejects_bad_inputs(gpu):
                                torch.zeros((1, 4, 262145, 128), dtype=torch.bfloat16, device="cuda"))
 
 
+def test_storage_grows_by_banks_without_moving(gpu):
+    """Growing past a 65,536-token bank maps the next bank behind the first
+    (cache.py:63-84): earlier rows keep their addresses and bytes, views taken
+    before the growth stay valid, new banks read zeros, and a decode step and a
+    prefill chunk that straddle the bank boundary match the oracle."""
+    B, Hq, Hkv, P, L = 1, 8, 1, 65530, 20
+    store = KVStorage(2, 1000, Hkv)
+    assert store.capacity == 65536 and store.nbytes == 2 * (2 * Hkv * 65536 * 128 * 2)
+    base = [r.data_ptr() for r in store.regions]
+    cache = FixedKVCache(store, 1)
+    k = synthetic.kv((B, Hkv, P + L + 1, 128), 71, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, P + L + 1, 128), 72, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    early = store.layer(1, 64)  # a view taken before the growth
+    # a chunk across the bank boundary: the storage grows to two banks
+    q = synthetic.query(B, Hq, L, 73, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    out = attend(q, k[:, :, P : P + L], v[:, :, P : P + L], cache, SCALE, "causal", sinks, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert store.capacity == 2 * 65536 and [r.data_ptr() for r in store.regions] == base
+    assert store.nbytes == 2 * (2 * Hkv * 2 * 65536 * 128 * 2)
+    T = P + L
+    ref = O.attention(f32(q), f32(k[:, :, :T]), f32(v[:, :, :T]), SCALE, sinks=f32(sinks), mask="causal")
+    assert_close(f32(out), ref, "prefill chunk across the bank boundary")
+    # one decode token after it
+    q1 = synthetic.query(B, Hq, 1, 74, dtype=torch.bfloat16)
+    out1 = attend(q1, k[:, :, T : T + 1], v[:, :, T : T + 1], cache, SCALE, None, sinks, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref1 = O.attention(f32(q1), f32(k[:, :, : T + 1]), f32(v[:, :, : T + 1]), SCALE, sinks=f32(sinks))
+    assert_close(f32(out1), ref1, "decode step after the bank boundary")
+    data = store.layer(1, T + 1)
+    assert torch.equal(data[:, 0], k) and torch.equal(data[:, 1], v)
+    assert torch.equal(early[:, 0], k[:, :, :64]) and torch.equal(early[:, 1], v[:, :, :64])
+    assert torch.count_nonzero(store.layer(1)[:, :, :, T + 1 :]) == 0
+    assert torch.count_nonzero(store.layer(0)) == 0
+    with pytest.raises(ValueError, match="Decode context limit exhausted"):
+        store.grow(4 * 65536 + 1)
+    store.grow(4 * 65536)  # the last two banks at once
+    assert store.capacity == 4 * 65536 and [r.data_ptr() for r in store.regions] == base
+    assert torch.equal(store.layer(1, T + 1)[:, 0], k)
+
+
 def test_sliding_window_ring_decode(gpu):
     """A window-40 ring fed 1-token steps well past the window (and one
     multi-token chunk): every decode step attends exactly the last
