@@ -759,11 +759,11 @@ char* bank_addr(const Region& r, int64_t row, int bank) {
 // Unmap and release everything mapped so far, then free the reservation.
 void region_release(Region* r) {
   for (int b = 0; b < r->banks; ++b)
-    for (int64_t row = 0; row < r->rows; ++row) hipMemUnmap(bank_addr(*r, row, b), bank_bytes(*r));
-  for (auto h : r->handles) hipMemRelease(h);
+    for (int64_t row = 0; row < r->rows; ++row) (void)hipMemUnmap(bank_addr(*r, row, b), bank_bytes(*r));
+  for (auto h : r->handles) (void)hipMemRelease(h);
   r->handles.clear();
   r->banks = 0;
-  if (r->base) hipMemAddressFree(r->base, r->reserved);
+  if (r->base) (void)hipMemAddressFree(r->base, r->reserved);
   r->base = nullptr;
 }
 
@@ -838,15 +838,15 @@ int rec_region_grow(void* handle, int64_t tokens, int64_t* capacity) {
       hipMemGenericAllocationHandle_t h{};
       if ((e = hipMemCreate(&h, bytes, &prop, 0)) != hipSuccess) break;
       if ((e = hipMemMap(bank_addr(*r, row, r->banks), bytes, 0, h, 0)) != hipSuccess) {
-        hipMemRelease(h);
+        (void)hipMemRelease(h);
         break;
       }
       made.push_back(h);  // made[k] is mapped at row k
       if ((e = hipMemSetAccess(bank_addr(*r, row, r->banks), bytes, &access, 1)) != hipSuccess) break;
     }
     if (e != hipSuccess) {
-      for (int64_t k = 0; k < (int64_t)made.size(); ++k) hipMemUnmap(bank_addr(*r, k, r->banks), bytes);
-      for (auto h : made) hipMemRelease(h);
+      for (int64_t k = 0; k < (int64_t)made.size(); ++k) (void)hipMemUnmap(bank_addr(*r, k, r->banks), bytes);
+      for (auto h : made) (void)hipMemRelease(h);
       return fail(REC_ELAUNCH, "region: mapping bank %d (%zu bytes per row, %lld rows): %s", r->banks, bytes,
                   (long long)r->rows, hipGetErrorString(e));
     }

@@ -463,6 +463,7 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     }
     l_run[rt] += lsum;
   }
+  __builtin_amdgcn_s_setprio(1);  // as around the Q·Kᵀ burst
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
     const v8h va = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
@@ -472,6 +473,7 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
       if constexpr (EXACT) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[rt], acc[n][rt], 0, 0, 0);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // Q^T operands: column tile rt holds query rows q0+16rt .. +15 (the last row
@@ -587,7 +589,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     for (int u = 0; u < U; ++u) {
       const int tu = t0 + 32 * u;
       const bool live = tu < t_end;
-      if (active && live) qk_unit<BF16>(Kl[buf] + 32 * u * PF_KROW, qop, sc[u & 1], c, g);
+      if (active && live) {
+        // the matrix-core bursts at raised wave priority: the SIMD's other
+        // wave, in its softmax, fills the issue slots they leave (measured
+        // 1.4% faster at 65,536 + 2,048 keys, 5% at 4,096 + 2,048)
+        __builtin_amdgcn_s_setprio(1);
+        qk_unit<BF16>(Kl[buf] + 32 * u * PF_KROW, qop, sc[u & 1], c, g);
+        __builtin_amdgcn_s_setprio(0);
+      }
       if (active && pend) {
         // the unit before: this tile's unit u - 1, or the previous tile's last
         const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? KT - 32 : 32 * (u - 1);
