@@ -409,13 +409,15 @@ PREFILL_FORMATS = {
     "int8": "int8 symmetric, fp16 scale per (token, head)",
     "uint4": "uint4 asymmetric, fp16 scale + zero-point per 32 dims",
     "affine": "MLX-style affine group 64: 8-bit K, 4-bit V, bf16 scale + bias",
+    "bf16": "bf16 token-major (KVStorage / FixedKVCache, the reference's production cache)",
 }
 
 
 def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
-    """Chunked prefill: quantize-append L new tokens after a P-token prefix in
-    the cache format `fmt`, then L causal bf16 queries attend over all P + L
-    tokens, every K/V tile dequantized on chip.  Each step rewrites the same L
+    """Chunked prefill: append L new tokens after a P-token prefix in the
+    cache format `fmt` (quantized, or written as bf16 into a KVStorage), then
+    L causal bf16 queries attend over all P + L tokens, every K/V tile
+    dequantized (or converted) on chip.  Each step rewrites the same L
     positions, so every step does identical work."""
     import torch
 
@@ -425,13 +427,17 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
     lib = rec_amd.library()
     T = P + L
     log(f"prefill ({fmt}): building a {P}-token prefix")
-    if fmt == "affine":
+    bf = fmt == "bf16"
+    if bf:
+        c = rec_amd.FixedKVCache(rec_amd.KVStorage(1, T, HKV), 0)
+    elif fmt == "affine":
         c = rec_amd.MixedQuantizedKVCache(max_tokens=T)
     else:
         bits = 8 if fmt == "int8" else 4
         c = rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T)
-    k = synthetic.kv((1, HKV, P, D), seed, kind="outliers", frac=0.01)
-    v = synthetic.kv((1, HKV, P, D), seed + 1, kind="outliers", frac=0.01)
+    kdt = torch.bfloat16 if bf else torch.float16
+    k = synthetic.kv((1, HKV, P, D), seed, kind="outliers", frac=0.01, dtype=kdt)
+    v = synthetic.kv((1, HKV, P, D), seed + 1, kind="outliers", frac=0.01, dtype=kdt)
     c.update_and_fetch(k, v)
     del k, v
     kn = synthetic.kv((1, HKV, L, D), seed + 2, kind="outliers", frac=0.01, dtype=torch.bfloat16)
@@ -441,17 +447,28 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
     g.manual_seed(seed)
     sinks = torch.randn(HQ, generator=g, device="cuda")
     out = torch.empty((1, HQ, L, D), dtype=torch.float32, device="cuda")
-    c._reserve(1, HKV, T, "cuda")
-    kq, vq = c.keys_and_values()
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-    # cache bytes per (token, kv head): codes + scales (+ zero-points) of K and V
-    tok_bytes = sum(t.nbytes for kv in (kq, vq) for t in (kv.codes, kv.scales, kv.zeros) if t is not None)
-    tok_bytes /= HKV * c.capacity
+    if bf:
+        data = c.storage.layer(0)
+        kr, vr = data[:, 0], data[:, 1]
+        tok_bytes = 2 * D * 2  # bf16 K and V rows
+    else:
+        c._reserve(1, HKV, T, "cuda")
+        kq, vq = c.keys_and_values()
+        # cache bytes per (token, kv head): codes + scales (+ zero-points) of K and V
+        tok_bytes = sum(t.nbytes for kv in (kq, vq) for t in (kv.codes, kv.scales, kv.zeros) if t is not None)
+        tok_bytes /= HKV * c.capacity
     # key splits when the chunk is short (the automatic plan; none at 2048 queries)
     ws = torch.empty(max(16, lib.rec_prefill_workspace_bytes(1, HKV, L, 0)), dtype=torch.uint8, device="cuda")
 
     def append():
         st = torch.cuda.current_stream().cuda_stream
+        if bf:
+            rc = lib.rec_kv_write_bf16(kn.data_ptr(), vn.data_ptr(), _lib.REC_BF16, *kn.stride()[:3], *vn.stride()[:3],
+                                       kr.data_ptr(), kr.stride(0), kr.stride(1), vr.data_ptr(), vr.stride(0),
+                                       vr.stride(1), 1, HKV, L, D, P, c.storage.capacity, st)
+            _lib.check(rc, "rec_kv_write_bf16")
+            return
         rc = lib.rec_kv_append(kn.data_ptr(), vn.data_ptr(), _lib.REC_BF16, *kn.stride()[:3], *vn.stride()[:3],
                                kq.code, kq.codes.data_ptr(), kq.scales.data_ptr(), ptr(kq.zeros),
                                vq.code, vq.codes.data_ptr(), vq.scales.data_ptr(), ptr(vq.zeros),
@@ -460,6 +477,12 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
 
     def attention():
         st = torch.cuda.current_stream().cuda_stream
+        if bf:
+            rc = lib.rec_prefill_bf16(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3], kr.data_ptr(), kr.stride(0),
+                                      kr.stride(1), vr.data_ptr(), vr.stride(0), vr.stride(1), sinks.data_ptr(), SCALE,
+                                      1, 0, 1, HQ, HKV, D, L, T, 0, ws.data_ptr(), ws.numel(), out.data_ptr(), st)
+            _lib.check(rc, "rec_prefill_bf16")
+            return
         rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3],
                                   kq.code, kq.codes.data_ptr(), kq.scales.data_ptr(), ptr(kq.zeros),
                                   vq.code, vq.codes.data_ptr(), vq.scales.data_ptr(), ptr(vq.zeros),
@@ -701,8 +724,8 @@ def main(argv=None):
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
         # a short chunk over a long cache (a new chat turn): the keys are split
         rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
-        # the same long chunk over the 4-bit and affine caches
-        for i, fmt in enumerate(("uint4", "affine")):
+        # the same long chunk over the 4-bit, affine and bf16 caches
+        for i, fmt in enumerate(("uint4", "affine", "bf16")):
             rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
 
     traffic, traffic_source = None, None

@@ -59,8 +59,16 @@ struct PfGeom {
   static constexpr int KT = BF ? 64 : 128;  // tokens per tile (a bf16 tile moves twice the bytes per token)
   static constexpr int U = KT / 32;         // 32-token units per tile
   static constexpr int VROW = KT + 16;      // LDS row pitch of V (positions + 16 pad)
+  // A bf16 cache holds V token-major: its tile keeps V as rows (token at
+  // block position within its 32-token unit, 144-element pitch) and P·V reads
+  // the Vᵀ operand with transposing LDS reads; the quantized layouts already
+  // group a dim's tokens, so their tiles hold V as [dim][position] rows.
+  static constexpr bool VTR = BF;
+  static constexpr int VPB = 144;
   static constexpr int K_ELEMS = KT * PF_KROW;
-  static constexpr int V_ELEMS = HEAD_DIM * VROW;
+  static constexpr int V_ELEMS = VTR ? KT * VPB : HEAD_DIM * VROW;
+  // element offset of unit u's V in the tile
+  static constexpr int vunit(int u) { return VTR ? 32 * u * VPB : 32 * u; }
   // Scale bytes per 32-token block, per staged region: [K scales][K zeros][V scales][V zeros]
   // (int8: one fp16 per token; uint4: [4 groups][32 slots] fp16 scales, zero-points alike;
   // affine: [scale, bias][2 groups][32 slots] bf16 in the scales region).
@@ -215,16 +223,20 @@ __device__ __forceinline__ void convert_tile(const TileRegs& R, typename MT<BF16
         }
       }
     } else if constexpr (PHASE == 1) {
+      // V rows as fp16 (the P·V operand type), token t of the tile at row
+      // 32 (t / 32) + block_pos(t % 32)
 #pragma unroll
       for (int part = 0; part < 2; ++part) {
         const int id = part * 512 + tid, tok = id >> 4, d0 = (id & 15) * 8;
-        const int col = (tok & ~31) + block_pos(tok & 31);
+        const int row = (tok & ~31) + block_pos(tok & 31);
+        v8h vh;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t w = (uint32_t)R.v[part][e];
-          Vl[(d0 + 2 * e) * VROW + col] = (_Float16)__builtin_bit_cast(float, w << 16);
-          Vl[(d0 + 2 * e + 1) * VROW + col] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
+          vh[2 * e] = (_Float16)__builtin_bit_cast(float, w << 16);
+          vh[2 * e + 1] = (_Float16)__builtin_bit_cast(float, w & 0xffff0000u);
         }
+        *(v8h*)(Vl + row * GEO::VPB + d0) = vh;
       }
     } else {
       if (tid < 2 * GEO::KT) (tid < GEO::KT ? KS : VS)[tid & (GEO::KT - 1)] = tid < GEO::KT ? q_mul : 1.f;
@@ -383,7 +395,7 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
 // finite score), thr, the bound past which a score moves it (-inf until the
 // row has seen a finite score, then RESCALE_GAP), and l_run, the sum of
 // probabilities.  t = s * ksc - m_use is one fma per score.
-template <int VROW, bool EXACT>
+template <int VROW, bool VTR, bool EXACT>
 __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
                                                 const float* VS, float (&m_use)[2], float (&thr)[2],
                                                 float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end, int qabs0,
@@ -464,9 +476,22 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     l_run[rt] += lsum;
   }
   __builtin_amdgcn_s_setprio(1);  // as around the Q·Kᵀ burst
+  const int sk = c >> 2, sa = c & 3;  // transposed reads: rows 8g + sk (+4), dims 16n + 4sa
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
-    const v8h va = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
+    v8h va;
+    if constexpr (VTR) {
+      // in a group of 16 lanes, lane 4a+b receives element b of the 8-byte
+      // rows addressed by lanes 4k+a: lane c gets dim 16n + c of rows 8g .. 8g+7
+      typedef __fp16 v4fp16 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+      typedef __attribute__((address_space(3))) v4fp16 lds_v4fp16;
+      const _Float16* base = Vv + (8 * g + sk) * 144 + 16 * n + 4 * sa;
+      const v2i r0 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4fp16*)base));
+      const v2i r1 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4fp16*)(base + 4 * 144)));
+      va = __builtin_bit_cast(v8h, (v4i){r0[0], r0[1], r1[0], r1[1]});
+    } else {
+      va = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
+    }
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt], acc[n][rt], 0, 0, 0);
@@ -600,7 +625,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       if (active && pend) {
         // the unit before: this tile's unit u - 1, or the previous tile's last
         const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? KT - 32 : 32 * (u - 1);
-        softmax_pv_unit<VROW, EXACT>(sc[(u + 1) & 1], Vl[pb_] + po, KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
+        softmax_pv_unit<VROW, GEO::VTR, EXACT>(sc[(u + 1) & 1], Vl[pb_] + (GEO::VTR ? po * GEO::VPB : po),
+                                               KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
                                      acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
       }
       pend = live;
@@ -624,7 +650,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   // still pending: the last tile's last unit (every unit of a tile is visited,
   // and a tile has an even number of units, so its scores are in sc[1])
   if (active && pend)
-    softmax_pv_unit<VROW, EXACT>(sc[1], Vl[buf] + KT - 32, KS[buf] + KT - 32, VS[buf] + KT - 32, m_use, thr, l_run,
+    softmax_pv_unit<VROW, GEO::VTR, EXACT>(sc[1], Vl[buf] + GEO::vunit(U - 1), KS[buf] + KT - 32, VS[buf] + KT - 32,
+                                           m_use, thr, l_run,
                                  acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
 
   if (!active) return;
