@@ -530,6 +530,48 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
     )
 
 
+def run_read_floor(steps):
+    """The one-launch read floor of this part: rec_stream_read (a plain
+    streaming read, 1 KB per wavefront and load, four loads in flight per
+    lane) over the K/V bytes of the 32K and 252K int8 configurations, rotating
+    buffers of >= 1 GB in all; the best of five workgroup counts."""
+    import torch
+
+    import rec_amd
+
+    lib = rec_amd.library()
+    out = torch.zeros(65536, dtype=torch.int32, device="cuda")
+    res = {}
+    for name, T, R, n in (("32k", 32768, 32, steps), ("252k", 258048, 4, max(16, steps // 8))):
+        nbytes = T * HKV * 2 * (D + 2)
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(R)]
+        best = None
+        for wg in (256, 512, 1024, 2048, 4096):
+            def launch(i, wg=wg):
+                rc = lib.rec_stream_read(bufs[i % R].data_ptr(), nbytes, wg, out.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream)
+                assert rc == 0, rc
+            launch(0)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(n):
+                    launch(i)
+            us = _median_timed(torch, g, n) * 1e3
+            log(f"read floor {name}: {wg} workgroups {us:.2f} us")
+            if best is None or us < best[0]:
+                best = (us, wg)
+            del g
+        us, wg = best
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"read floor {name}: {nbytes} B in {us:.2f} us = {gbs:.0f} GB/s ({wg} workgroups)")
+        res[name] = dict(bytes=nbytes, us=round(us, 3), gbs=round(gbs, 1), frac_of_peak=round(gbs / HBM_PEAK_GBS, 4),
+                         workgroups=wg)
+        del bufs
+        torch.cuda.empty_cache()
+    return res
+
+
 def host_cores():
     """Host cores this process may run on (its CPU affinity), bounded by the
     thread budget OMP_NUM_THREADS when the environment sets one (a shared GPU
@@ -640,6 +682,7 @@ def main(argv=None):
     ap.add_argument("--no-gemv", action="store_true", help="skip the int4 GEMV measurements")
     ap.add_argument("--no-affine", action="store_true", help="skip the group-64 affine cache measurement")
     ap.add_argument("--prefill-steps", type=int, default=6)
+    ap.add_argument("--no-floor", action="store_true", help="skip the plain streaming-read floor")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--seed", type=int, default=1234)
@@ -727,6 +770,8 @@ def main(argv=None):
         # the same long chunk over the 4-bit, affine and bf16 caches
         for i, fmt in enumerate(("uint4", "affine", "bf16")):
             rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
+
+    floor = None if args.no_floor else run_read_floor(max(20, args.steps // 5))
 
     traffic, traffic_source = None, None
     if os.path.exists(TRAFFIC_FILE):
@@ -871,6 +916,11 @@ def main(argv=None):
         result["prefill_32768_plus_20"] = rpf_short
     for fmt, r in rpf_fmt.items():
         result[f"prefill_65536_plus_2048_{fmt}"] = r
+    if floor is not None:
+        result["read_floor"] = dict(
+            floor,
+            note="rec_stream_read: a plain streaming read of the configuration's K/V bytes in one launch, the "
+                 "practical ceiling the decode kernel's roofline fraction is read against")
     print(json.dumps(result), flush=True)
     return 0
 

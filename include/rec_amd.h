@@ -279,6 +279,15 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
+ * A plain streaming read of `bytes` (a positive multiple of 16) at p (16-byte
+ * aligned) by `workgroups` workgroups of 256 threads; `out` (workgroups
+ * uint32, device memory) is written only in the rare case the XOR of the
+ * data hits a fixed value.  No counterpart in the reference: the one-launch
+ * read floor of this part, against which the decode kernels are measured.
+ */
+int rec_stream_read(const void* p, int64_t bytes, int workgroups, uint32_t* out, void* stream);
+
+/*
  * Growable bf16 layer region (KVStorage's banks): reserves the address range
  * of `rows` rows (B * 2 * Hkv for a layer: K then V per batch row) of
  * `max_tokens` tokens of `token_bytes` each, row r at base + r * max_tokens *

@@ -36,6 +36,7 @@ SIGNATURES = {
         [_p, _p, _i, _i64, _i64, _i64, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i64, _i64, _p],
     ),
     "rec_decode_default_splits": (_i, [_i, _i, _i64]),
+    "rec_stream_read": (_i, [_p, _i64, _i, _p, _p]),
     "rec_region_create": (_i, [_i, _i64, _i64, _i64, _i64, ctypes.POINTER(_p), ctypes.POINTER(_p)]),
     "rec_region_grow": (_i, [_p, _i64, ctypes.POINTER(_i64)]),
     "rec_region_destroy": (_i, [_p]),

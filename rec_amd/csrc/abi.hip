@@ -771,6 +771,15 @@ void region_release(Region* r) {
 
 extern "C" {
 
+int rec_stream_read(const void* p, int64_t bytes, int workgroups, uint32_t* out, void* stream) {
+  if (!p || !out) return fail(REC_EINVAL, "stream read: null pointer");
+  if (bytes <= 0 || bytes % 16 != 0) return fail(REC_EINVAL, "stream read: %lld bytes (a positive multiple of 16)",
+                                                 (long long)bytes);
+  if (!aligned16(p)) return fail(REC_EALIGN, "stream read: the buffer must be 16-byte aligned");
+  if (workgroups < 1 || workgroups > 65536) return fail(REC_EINVAL, "stream read: %d workgroups (1..65536)", workgroups);
+  return launched(launch_stream_read(p, bytes / 16, workgroups, out, (hipStream_t)stream), "stream read launch");
+}
+
 int rec_region_create(int device, int64_t rows, int64_t max_tokens, int64_t token_bytes, int64_t bank_tokens,
                       void** handle, void** base) {
   if (!handle || !base) return fail(REC_EINVAL, "region: null output pointer");

@@ -135,6 +135,7 @@ constexpr int Q4_MAX_M = 8;
 
 hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream);
 hipError_t launch_fill_zero(uint32_t* p, int64_t words, hipStream_t stream);
+hipError_t launch_stream_read(const void* p, int64_t n16, int workgroups, uint32_t* out, hipStream_t stream);
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both kernels when a.S > 1
