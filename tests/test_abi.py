@@ -264,3 +264,11 @@ def test_region_validation(lib):
     assert lib.rec_region_create(0, 8, 262144, 256, 65536, None, None) == _lib.REC_EINVAL
     assert lib.rec_region_grow(None, 1, None) == _lib.REC_EINVAL
     assert lib.rec_region_destroy(None) == _lib.REC_OK
+
+
+def test_stream_read_validation(lib):
+    assert lib.rec_stream_read(None, 1024, 256, 16, None) == _lib.REC_EINVAL
+    assert lib.rec_stream_read(16, 1000, 256, 16, None) == _lib.REC_EINVAL  # not a multiple of 16
+    assert "multiple of 16" in _lib.last_error()
+    assert lib.rec_stream_read(8, 1024, 256, 16, None) == _lib.REC_EALIGN
+    assert lib.rec_stream_read(16, 1024, 0, 16, None) == _lib.REC_EINVAL
