@@ -459,7 +459,7 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
         tok_bytes = sum(t.nbytes for kv in (kq, vq) for t in (kv.codes, kv.scales, kv.zeros) if t is not None)
         tok_bytes /= HKV * c.capacity
     # key splits when the chunk is short (the automatic plan; none at 2048 queries)
-    ws = torch.empty(max(16, lib.rec_prefill_workspace_bytes(1, HKV, L, 0)), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(max(16, lib.rec_prefill_workspace_bytes(1, HQ, HKV, L, 0)), dtype=torch.uint8, device="cuda")
 
     def append():
         st = torch.cuda.current_stream().cuda_stream

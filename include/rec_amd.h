@@ -205,11 +205,12 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
                      int splits, void* workspace, size_t workspace_bytes, float* out, void* stream);
 
-/* Workspace bytes a prefill launch of L queries needs for `splits` key splits
- * (<= 0: the most the automatic plan can use); 0 when it does not split.
+/* Workspace bytes a prefill launch of L queries with Hq query and Hkv KV heads
+ * needs for `splits` key splits (<= 0: the most the automatic plan can use);
+ * 0 when it does not split (or for an invalid shape).
  * Serves rec_prefill_attn and rec_prefill_bf16; no counterpart in the
  * reference, whose prefill is one library call. */
-size_t rec_prefill_workspace_bytes(int B, int Hkv, int L, int splits);
+size_t rec_prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int splits);
 
 /*
  * bf16 KV cache (the reference's production format): K and V are (B, Hkv,

@@ -67,7 +67,7 @@ SIGNATURES["rec_prefill_attn"] = (
     [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i64, _i64,
      _i, _p, _sz, _p, _p],
 )
-SIGNATURES["rec_prefill_workspace_bytes"] = (_sz, [_i, _i, _i, _i])
+SIGNATURES["rec_prefill_workspace_bytes"] = (_sz, [_i, _i, _i, _i, _i])
 
 SIGNATURES["rec_kv_write_bf16"] = (
     _i,

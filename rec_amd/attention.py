@@ -135,13 +135,14 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
         _lib.check(rc, "rec_decode_append_attn")
 
 
-def prefill_workspace(device: torch.device, B: int, Hkv: int, L: int, splits: int, stream: int) -> torch.Tensor:
+def prefill_workspace(device: torch.device, B: int, Hq: int, Hkv: int, L: int, splits: int,
+                      stream: int) -> torch.Tensor:
     """The prefill workspace (key-split partials) for (device, stream), grown on
     demand; an empty tensor when the launch does not split.  Kept apart from the
     decode workspace: a chunk's prefill and the decode steps after it may
     interleave on one stream, but each launch pair (partials, merge) is ordered."""
     lib = _lib.load()
-    need = lib.rec_prefill_workspace_bytes(B, Hkv, L, splits)
+    need = lib.rec_prefill_workspace_bytes(B, Hq, Hkv, L, splits)
     key = ("prefill", device.index, stream)
     with _ws_lock:
         ws = _workspaces.get(key)
@@ -158,7 +159,7 @@ def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sink
     dev = queries.device
     sk = _sinks(sinks, Hq, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    ws = prefill_workspace(dev, B, keys.n_kv_heads, L, splits, stream)
+    ws = prefill_workspace(dev, B, Hq, keys.n_kv_heads, L, splits, stream)
     rc = lib.rec_prefill_attn(
         q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), q.stride(2),
         keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
@@ -281,7 +282,7 @@ def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, ou
     dev = queries.device
     sk = _sinks(sinks, Hq, dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
-    ws = prefill_workspace(dev, B, Hkv, L, splits, stream)
+    ws = prefill_workspace(dev, B, Hq, Hkv, L, splits, stream)
     rc = lib.rec_prefill_bf16(
         queries.data_ptr(), _DTYPES[queries.dtype], queries.stride(0), queries.stride(1), queries.stride(2),
         keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),

@@ -430,16 +430,16 @@ static int plan_prefill_splits(PrefillArgs& a, int splits, void* workspace, size
   a.split_lo = p.split_lo;
   a.split_len = p.split_len;
   if (p.S > 1) {
-    const size_t rows = (size_t)a.B * a.Hkv * p.S * p.nqb * 8 * 32;
+    const size_t rows = (size_t)a.B * a.Hkv * p.S * p.nqb * PREFILL_BLOCK_ROWS;
     a.ws_acc = (float*)workspace;
     a.ws_stat = (float*)((char*)workspace + rows * HEAD_DIM * 4);
   }
   return REC_OK;
 }
 
-size_t rec_prefill_workspace_bytes(int B, int Hkv, int L, int splits) {
-  if (B < 1 || Hkv < 1 || L < 1) return 0;
-  const int nqb = (L + 31) / 32;
+size_t rec_prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int splits) {
+  if (B < 1 || Hkv < 1 || L < 1 || Hq < Hkv || Hq % Hkv != 0) return 0;
+  const int nqb = (int)(((int64_t)L * (Hq / Hkv) + PREFILL_BLOCK_ROWS - 1) / PREFILL_BLOCK_ROWS);
   int S = splits;
   if (S <= 0) {
     const int64_t nwg = (int64_t)nqb * Hkv * B;

@@ -78,14 +78,17 @@ struct PrefillArgs {
   // split-K over the keys (S > 1): workgroup (qb, s) scans keys
   // [split_lo + s * split_len, + split_len) of its query block's range and
   // writes an unnormalised partial; prefill_merge_kernel combines them
-  int S, nqb;                  // splits, query blocks of PF_QB queries
+  int S, nqb;                  // splits, row blocks (PREFILL_BLOCK_ROWS (query, head) rows each)
   int64_t split_lo, split_len;
-  float* ws_acc;               // [B*Hkv][S][nqb][8][32][128]
-  float* ws_stat;              // [B*Hkv][S][nqb][8][32] x (max, sum)
+  float* ws_acc;               // [B*Hkv][S][nqb][256][128]
+  float* ws_stat;              // [B*Hkv][S][nqb][256] x (max, sum)
 };
 
 // Prefill split plan: how many key splits a launch uses and where they lie.
 constexpr int PREFILL_MAX_SPLITS = 64;
+// (query, head) rows per prefill workgroup: a KV head's rows are numbered
+// query * G + head, and workgroup qb takes rows [256 qb, 256 qb + 256)
+constexpr int PREFILL_BLOCK_ROWS = 256;
 struct PrefillPlan {
   int S, nqb;
   int64_t split_lo, split_len;

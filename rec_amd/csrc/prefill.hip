@@ -21,9 +21,13 @@
 // (and a second MFMA carries the rounding remainder for rows that see few
 // keys, EXACT_PV_BELOW).
 //
-// Work decomposition.  Grid (ceil(L/32) x key splits, Hkv, B), 512 threads =
-// 8 wavefronts; wave w owns query head w of the KV head's GQA group and 32
-// query positions.  K/V tiles of 128 tokens (64 for a bf16 cache) are
+// Work decomposition.  Grid (ceil(L*G/256) x key splits, Hkv, B), 512
+// threads = 8 wavefronts.  The rows of a KV head's attention are its (query,
+// head) pairs, query-major (row query*G + head over the G query heads of the
+// GQA group); a workgroup takes 256 consecutive rows as 16 row tiles of 16,
+// and wave w owns tiles w and w + 8.  A chunk of a few queries thus fills
+// its row tiles with those queries' heads instead of padding every head to a
+// tile, and a wave whose tiles lie past the last row skips them.  K/V tiles of 128 tokens (64 for a bf16 cache) are
 // dequantized into double-buffered LDS and shared by the 8 waves, which
 // compute a tile in 32-token units, software-pipelined (one unit's Q·K^T on
 // the matrix cores while the previous unit's softmax runs on the VALU).  Each
@@ -49,7 +53,7 @@
 
 namespace rec {
 
-constexpr int PF_QB = 32;     // query positions per workgroup
+constexpr int PF_ROWS = PREFILL_BLOCK_ROWS;  // (query, head) rows per workgroup: 16 tiles of 16
 constexpr int PF_KROW = 144;  // LDS row pitch of K (elements): 128 + 16 pad
 
 // Tile geometry per cache format pair.
@@ -382,15 +386,15 @@ __device__ __forceinline__ void convert_tile(const TileRegs& R, typename MT<BF16
   }
 }
 
-// S^T = K Q^T for one 32-token unit of one wave: 32 query rows (two column
-// tiles of 16) of one head; lane (c, g) receives the scores of query row c for
-// tokens 16j + 4g + i of the unit.
-template <bool BF16>
+// S^T = K Q^T for one 32-token unit of one wave: its first NRT row tiles of
+// 16; lane (c, g) receives the scores of row c of each tile for tokens
+// 16j + 4g + i of the unit.
+template <bool BF16, int NRT>
 __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const typename MT<BF16>::vec (&qop)[2][4],
                                         v4f (&s4)[2][2], int c, int g) {
   typedef typename MT<BF16>::vec V8;
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
     for (int j = 0; j < 2; ++j) s4[rt][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -399,7 +403,7 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
     for (int j = 0; j < 2; ++j) {
       const V8 ka = *(const V8*)(K + (16 * j + c) * PF_KROW + 32 * ks + 8 * g);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) s4[rt][j] = MT<BF16>::mfma(ka, qop[rt][ks], s4[rt][j]);
+      for (int rt = 0; rt < NRT; ++rt) s4[rt][j] = MT<BF16>::mfma(ka, qop[rt][ks], s4[rt][j]);
     }
 }
 
@@ -412,11 +416,12 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
 // finite score), thr, the bound past which a score moves it (-inf until the
 // row has seen a finite score, then RESCALE_GAP), and l_run, the sum of
 // probabilities.  t = s * ksc - m_use is one fma per score.
-template <int VROW, bool VTR, bool EXACT>
+template <int VROW, bool VTR, bool EXACT, int NRT>
 __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
                                                 const float* VS, float (&m_use)[2], float (&thr)[2],
-                                                float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end, int qabs0,
-                                                int causal, int window, bool mask, int c, int g) {
+                                                float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end,
+                                                const int (&qabs)[2], int causal, int window, bool mask,
+                                                int c, int g) {
   v8h pb[2], pl[2];  // P'^T: high parts, and (EXACT) the remainders
   // Range: P' = p·s feeds an fp16 operand, finite while p·s < 65504.  A V
   // scale of 2 or more among the lane's tokens (fp32 exponent bit 30;
@@ -429,11 +434,10 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     big = ((uint32_t)(o[0] | o[1] | o[2] | o[3]) & 0x40000000u) != 0;
   }
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < NRT; ++rt) {
     // scale (K scale x softmax scale) and offset in one fma, mask, online
-    // softmax per query row (lane column c of tile rt)
+    // softmax per row (lane column c of tile rt; its query sits at qabs[rt])
     float t[8];
-    const int qabs = qabs0 + 16 * rt + c;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const v4f ksc = *(const v4f*)(&KS[16 * j + 4 * g]);
@@ -442,8 +446,8 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     }
     if (mask) {
       // first and last visible token of this row, relative to the lane's first token t0 + 4g
-      const int last = (causal ? min(qabs, t_end - 1) : t_end - 1) - t0 - 4 * g;
-      const int first = window > 0 ? qabs - window + 1 - t0 - 4 * g : INT32_MIN;
+      const int last = (causal ? min(qabs[rt], t_end - 1) : t_end - 1) - t0 - 4 * g;
+      const int first = window > 0 ? qabs[rt] - window + 1 - t0 - 4 * g : INT32_MIN;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int pos = 16 * (k >> 2) + (k & 3);
@@ -510,7 +514,7 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
       va = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
     }
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < NRT; ++rt) {
       acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt], acc[n][rt], 0, 0, 0);
       if constexpr (EXACT) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[rt], acc[n][rt], 0, 0, 0);
     }
@@ -518,16 +522,15 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
   __builtin_amdgcn_s_setprio(0);
 }
 
-// Q^T operands: column tile rt holds query rows q0+16rt .. +15 (the last row
-// repeated past L), k-step ks dims 32ks + 8g .. +7 of the lane's row c.
+// Q^T operands: lane column c of row tile rt holds the query row (qr[rt],
+// head hq[rt]); k-step ks dims 32ks + 8g .. +7.
 template <bool BF16>
-__device__ __forceinline__ void load_query(typename MT<BF16>::vec (&qop)[2][4], const PrefillArgs& a, int b, int hq,
-                                           int q0, int c, int g) {
+__device__ __forceinline__ void load_query(typename MT<BF16>::vec (&qop)[2][4], const PrefillArgs& a, int b,
+                                           const int (&hq)[2], const int (&qr)[2], int g) {
   typedef typename MT<BF16>::vec V8;
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const int qr = min(q0 + 16 * rt + c, a.L - 1);
-    const int64_t base = (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)qr * a.q_st;
+    const int64_t base = (int64_t)b * a.q_sb + (int64_t)hq[rt] * a.q_sh + (int64_t)qr[rt] * a.q_st;
     const uint16_t* row = (const uint16_t*)a.q + base;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -555,32 +558,47 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) float VS[2][KT];
   __shared__ __attribute__((aligned(16))) char stage[GEO::STAGE > 0 ? GEO::STAGE : 16];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
-  // uniform, kept in scalar registers (the division would otherwise leave
-  // them, and everything derived from them, in vector registers)
+  // uniform, kept in scalar registers (the compiler would otherwise treat
+  // them, and everything derived from them, as varying across the lanes)
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int split = __builtin_amdgcn_readfirstlane((int)blockIdx.x / a.nqb);
   const int qb = __builtin_amdgcn_readfirstlane((int)blockIdx.x - split * a.nqb);
-  const int q0 = qb * PF_QB, h = blockIdx.y, b = blockIdx.z;
+  const int h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * a.Hkv + h;
+  const int p0 = qb * PF_ROWS;                       // the block's first row
+  const int n_p = min(PF_ROWS, a.L * a.G - p0);      // and its row count
+  const int q_lo = __builtin_amdgcn_readfirstlane(p0 / a.G);  // its first and last query
+  const int q_hi = __builtin_amdgcn_readfirstlane((p0 + n_p - 1) / a.G);
   const int P = (int)(a.T - a.L);  // cached tokens before the new ones
-  const int t_blk = a.causal ? min((int)a.T, P + q0 + PF_QB) : (int)a.T;  // the block's keys end here
-  const bool active = w < a.G;
-  const int hq = h * a.G + (active ? w : 0);
-
+  const int t_blk = a.causal ? min((int)a.T, P + q_hi + 1) : (int)a.T;  // the block's keys end here
+  // the wave's row tiles w and w + 8: how many exist (0, 1 or 2, uniform per
+  // wave), and per lane its row in each (rows past the last repeat it) with
+  // the row's query and query head
+  const int nrt = 16 * w >= n_p ? 0 : 16 * (w + 8) >= n_p ? 1 : 2;
+  const auto rows = [&](int cc, int (&prow)[2], int (&qr)[2], int (&hq)[2]) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      prow[rt] = 16 * (w + 8 * rt) + cc;
+      const int p = p0 + min(prow[rt], n_p - 1);
+      qr[rt] = p / a.G;
+      hq[rt] = h * a.G + (p - qr[rt] * a.G);
+    }
+  };
   V8 qop[2][4];
-  load_query<BF16>(qop, a, b, hq, q0, c, g);
-
-  float m_use[2] = {0.f, 0.f}, thr[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
-  v4f acc[8][2];
-#pragma unroll
-  for (int n = 0; n < 8; ++n)
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) acc[n][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
+  int qabs[2];  // the rows' query positions: all the main loop keeps of them
+  {
+    int prow[2], qr[2], hq[2];
+    rows(c, prow, qr, hq);
+    load_query<BF16>(qop, a, b, hq, qr, g);
+    qabs[0] = P + qr[0];
+    qabs[1] = P + qr[1];
+  }
 
   // a sliding window (bf16 caches only) starts the scan at the first query's first visible key
   const int window = GEO::BF ? a.window : 0;
-  const int t_first = window > 0 ? max(0, P + q0 - window + 1) / KT * KT : 0;
+  const int t_first = window > 0 ? max(0, P + q_lo - window + 1) / KT * KT : 0;
   // this workgroup's share of the keys, [lo, t_end): the split's range
   // (tile-aligned) within the query block's [t_first, t_blk); empty for some
   // splits.  A split that ends before t_blk ends on a tile boundary, so its
@@ -597,120 +615,146 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
   using P2 = std::integral_constant<int, 2>;
-
-  // Prologue: tile lo into buffer 0 (all phases), the next tile's bytes in
-  // flight.  Unconditional even for an empty range (lo >= t_end): every load
-  // then fails its liveness test and reads nothing.
-  TileRegs R;
-  load_tile<KF, VF>(R, a, b, h, bh, lo, tid, t_end);
-  stage_scales(R);
-  __syncthreads();
-  convert(R, 0, P0{});
-  convert(R, 0, P1{});
-  convert(R, 0, P2{});
-  __syncthreads();
-  if (lo + KT < t_end) load_tile<KF, VF>(R, a, b, h, bh, lo + KT, tid, t_end);
-
-  // Software pipeline over 32-token units: the scores of unit u+1 are computed
-  // on the matrix cores while the VALU runs the softmax of unit u.  A tile's
-  // last unit is finished (softmax + P·V) at unit 0 of the next tile, from the
-  // other buffer, which is refilled only at the end of that tile.
-  v4f sc[2][2][2];    // scores of two units in flight: [unit parity][rt][j]
-  bool pend = false;  // the previous unit awaits its softmax + P·V
-  int pend_t = 0;
-  int buf = 0;
-  const int qabs0 = P + q0;
-  // a unit needs the mask loop if it reaches a query block's diagonal, the
-  // cache end, or (sliding window) lies before some query's window start
+  const int qabs_lo = P + q_lo, qabs_hi = P + q_hi;
+  // a unit needs the mask loop if it reaches the block's first diagonal, the
+  // cache end, or (sliding window) lies before its last query's window start
   const auto needs_mask = [&](int tu) {
-    return tu + 32 > qabs0 || tu + 32 > t_end || (window > 0 && tu < qabs0 + PF_QB - window);
+    return tu + 32 > qabs_lo || tu + 32 > t_end || (window > 0 && tu < qabs_hi - window + 1);
   };
-  for (int t0 = lo; t0 < t_end; t0 += KT) {
-    const bool more = t0 + KT < t_end;  // uniform
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int tu = t0 + 32 * u;
-      const bool live = tu < t_end;
-      if (active && live) {
-        // the matrix-core bursts at raised wave priority: the SIMD's other
-        // wave, in its softmax, fills the issue slots they leave (measured
-        // 1.4% faster at 65,536 + 2,048 keys, 5% at 4,096 + 2,048)
-        __builtin_amdgcn_s_setprio(1);
-        qk_unit<BF16>(Kl[buf] + 32 * u * PF_KROW, qop, sc[u & 1], c, g);
-        __builtin_amdgcn_s_setprio(0);
-      }
-      if (active && pend) {
-        // the unit before: this tile's unit u - 1, or the previous tile's last
-        const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? KT - 32 : 32 * (u - 1);
-        softmax_pv_unit<VROW, GEO::VTR, EXACT>(sc[(u + 1) & 1], Vl[pb_] + (GEO::VTR ? po * GEO::VPB : po),
-                                               KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run,
-                                     acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
-      }
-      pend = live;
-      pend_t = tu;
-    }
-    if (more) {
-      // The next tile, whose bytes had this whole tile to arrive, into the
-      // other buffer: its scale bytes to the staging area, then (once every
-      // wave has finished the unit that read the other buffer) the
-      // dequantization; then the tile after next starts its way from HBM.
-      stage_scales(R);
-      __syncthreads();
-      convert(R, buf ^ 1, P0{});
-      convert(R, buf ^ 1, P1{});
-      convert(R, buf ^ 1, P2{});
-      if (t0 + 2 * KT < t_end) load_tile<KF, VF>(R, a, b, h, bh, t0 + 2 * KT, tid, t_end);
-      __syncthreads();
-      buf ^= 1;
-    }
-  }
-  // still pending: the last tile's last unit (every unit of a tile is visited,
-  // and a tile has an even number of units, so its scores are in sc[1])
-  if (active && pend)
-    softmax_pv_unit<VROW, GEO::VTR, EXACT>(sc[1], Vl[buf] + GEO::vunit(U - 1), KS[buf] + KT - 32, VS[buf] + KT - 32,
-                                           m_use, thr, l_run,
-                                 acc, pend_t, t_end, qabs0, a.causal, window, needs_mask(pend_t), c, g);
 
-  if (!active) return;
-  if (a.S > 1) {
-    // ---------------- unnormalised partial of this split ----------------
+  // The scan, compiled once per row-tile count NRT of the wave: a wave with
+  // fewer tiles (the last block of a launch whose row count is not a
+  // multiple of 256) runs the same pipeline with fewer matrix products, and
+  // a wave with none only helps to load and dequantize the tiles.
+  const auto scan = [&](auto nrt_c) {
+    constexpr int NRT = decltype(nrt_c)::value;
+    float m_use[2] = {0.f, 0.f}, thr[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
+    v4f acc[8][2];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const float l = sum_xor32(sum_xor16(l_run[rt]));
-      const float M = thr[rt] == NEG_INF ? NEG_INF : m_use[rt];  // -inf: no visible key in this split
-      const int qr = q0 + 16 * rt + c;
-      if (qr < a.L) {
-        const int64_t row = ((((int64_t)bh * a.S + split) * a.nqb + qb) * 8 + w) * PF_QB + 16 * rt + c;
-        float* o = a.ws_acc + row * HEAD_DIM + 4 * g;
+    for (int n = 0; n < 8; ++n)
 #pragma unroll
-        for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt];
-        if (g == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){M, l};
+      for (int rt = 0; rt < 2; ++rt) acc[n][rt] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    // Prologue: tile lo into buffer 0 (all phases), the next tile's bytes in
+    // flight.  Unconditional even for an empty range (lo >= t_end): every load
+    // then fails its liveness test and reads nothing.
+    TileRegs R;
+    load_tile<KF, VF>(R, a, b, h, bh, lo, tid, t_end);
+    stage_scales(R);
+    __syncthreads();
+    convert(R, 0, P0{});
+    convert(R, 0, P1{});
+    convert(R, 0, P2{});
+    __syncthreads();
+    if (lo + KT < t_end) load_tile<KF, VF>(R, a, b, h, bh, lo + KT, tid, t_end);
+
+    // Software pipeline over 32-token units: the scores of unit u+1 are computed
+    // on the matrix cores while the VALU runs the softmax of unit u.  A tile's
+    // last unit is finished (softmax + P·V) at unit 0 of the next tile, from the
+    // other buffer, which is refilled only at the end of that tile.
+    v4f sc[2][2][2];    // scores of two units in flight: [unit parity][rt][j]
+    bool pend = false;  // the previous unit awaits its softmax + P·V
+    int pend_t = 0;
+    int buf = 0;
+    for (int t0 = lo; t0 < t_end; t0 += KT) {
+      const bool more = t0 + KT < t_end;  // uniform
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tu = t0 + 32 * u;
+        const bool live = tu < t_end;
+        if constexpr (NRT > 0) {
+          if (live) {
+            // the matrix-core bursts at raised wave priority: the SIMD's other
+            // wave, in its softmax, fills the issue slots they leave (measured
+            // 1.4% faster at 65,536 + 2,048 keys, 5% at 4,096 + 2,048)
+            __builtin_amdgcn_s_setprio(1);
+            qk_unit<BF16, NRT>(Kl[buf] + 32 * u * PF_KROW, qop, sc[u & 1], c, g);
+            __builtin_amdgcn_s_setprio(0);
+          }
+          if (pend) {
+            // the unit before: this tile's unit u - 1, or the previous tile's last
+            const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? KT - 32 : 32 * (u - 1);
+            softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT>(sc[(u + 1) & 1], Vl[pb_] + (GEO::VTR ? po * GEO::VPB : po),
+                                                        KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run, acc, pend_t,
+                                                        t_end, qabs, a.causal, window, needs_mask(pend_t), c, g);
+          }
+        }
+        pend = live;
+        pend_t = tu;
+      }
+      if (more) {
+        // The next tile, whose bytes had this whole tile to arrive, into the
+        // other buffer: its scale bytes to the staging area, then (once every
+        // wave has finished the unit that read the other buffer) the
+        // dequantization; then the tile after next starts its way from HBM.
+        stage_scales(R);
+        __syncthreads();
+        convert(R, buf ^ 1, P0{});
+        convert(R, buf ^ 1, P1{});
+        convert(R, buf ^ 1, P2{});
+        if (t0 + 2 * KT < t_end) load_tile<KF, VF>(R, a, b, h, bh, t0 + 2 * KT, tid, t_end);
+        __syncthreads();
+        buf ^= 1;
       }
     }
-    return;
-  }
-  // ---------------- normalise and write ----------------
+    if constexpr (NRT > 0) {
+      // still pending: the last tile's last unit (every unit of a tile is
+      // visited, and a tile has an even number of units, so its scores are in sc[1])
+      if (pend)
+        softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT>(sc[1], Vl[buf] + GEO::vunit(U - 1), KS[buf] + KT - 32,
+                                                    VS[buf] + KT - 32, m_use, thr, l_run, acc, pend_t, t_end, qabs,
+                                                    a.causal, window, needs_mask(pend_t), c, g);
+
+      // the rows again, from an opaque copy of the lane's column: recomputed
+      // here rather than held in registers through the main loop
+      int prow[2], qr[2], hq[2];
+      {
+        int cc = c;
+        asm volatile("" : "+v"(cc));
+        rows(cc, prow, qr, hq);
+      }
+      if (a.S > 1) {
+        // ---------------- unnormalised partial of this split ----------------
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    float l = l_run[rt];
-    l = sum_xor32(sum_xor16(l));
-    float M = thr[rt] == NEG_INF ? NEG_INF : m_use[rt];  // -inf: no visible key
-    if (a.sinks != nullptr) {
-      const float sink = a.sinks[hq] * LOG2E;
-      const float Mn = fmaxf(M, sink);
-      const float f = M == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
-      l = l * f + __builtin_amdgcn_exp2f(sink - Mn);
+        for (int rt = 0; rt < NRT; ++rt) {
+          const float l = sum_xor32(sum_xor16(l_run[rt]));
+          const float M = thr[rt] == NEG_INF ? NEG_INF : m_use[rt];  // -inf: no visible key in this split
+          if (prow[rt] < n_p) {
+            const int64_t row = (((int64_t)bh * a.S + split) * a.nqb + qb) * PF_ROWS + prow[rt];
+            float* o = a.ws_acc + row * HEAD_DIM + 4 * g;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) acc[n][rt] *= f;
+            for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt];
+            if (g == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){M, l};
+          }
+        }
+        return;
+      }
+      // ---------------- normalise and write ----------------
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) {
+        float l = l_run[rt];
+        l = sum_xor32(sum_xor16(l));
+        float M = thr[rt] == NEG_INF ? NEG_INF : m_use[rt];  // -inf: no visible key
+        if (a.sinks != nullptr) {
+          const float sink = a.sinks[hq[rt]] * LOG2E;
+          const float Mn = fmaxf(M, sink);
+          const float f = M == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+          l = l * f + __builtin_amdgcn_exp2f(sink - Mn);
+#pragma unroll
+          for (int n = 0; n < 8; ++n) acc[n][rt] *= f;
+        }
+        const float inv = l > 0.f ? 1.f / l : 1.f;
+        if (prow[rt] < n_p) {
+          float* o = a.out + (((int64_t)b * a.Hq + hq[rt]) * a.L + qr[rt]) * HEAD_DIM + 4 * g;
+#pragma unroll
+          for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt] * inv;
+        }
+      }
     }
-    const float inv = l > 0.f ? 1.f / l : 1.f;
-    const int qr = q0 + 16 * rt + c;
-    if (qr < a.L) {
-      float* o = a.out + (((int64_t)b * a.Hq + hq) * a.L + qr) * HEAD_DIM + 4 * g;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt] * inv;
-    }
-  }
+  };
+  if (nrt == 2) scan(std::integral_constant<int, 2>{});
+  else if (nrt == 1) scan(std::integral_constant<int, 1>{});
+  else scan(std::integral_constant<int, 0>{});
 }
 
 // Merge of the key splits (S > 1): one wavefront per (query, query head,
@@ -719,9 +763,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) {
   __shared__ float wts[PREFILL_MAX_SPLITS];
   const int i = blockIdx.x, hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
-  const int h = hq / a.G, w = hq % a.G, qb = i / PF_QB, r = i % PF_QB;
+  const int h = hq / a.G, p = i * a.G + (hq - h * a.G);  // the (query, head) row
+  const int qb = p / PF_ROWS, r = p - qb * PF_ROWS;
   const int64_t bh = (int64_t)b * a.Hkv + h;
-  const auto row = [&](int sp) { return ((((bh * a.S + sp) * a.nqb + qb) * 8 + w) * PF_QB) + r; };
+  const auto row = [&](int sp) { return ((bh * a.S + sp) * a.nqb + qb) * PF_ROWS + r; };
   float m = NEG_INF, l = 0.f;
   if (lane < a.S) {
     const v2f st = *(const v2f*)(a.ws_stat + row(lane) * 2);
@@ -751,7 +796,7 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
 
 PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
   PrefillPlan p{};
-  p.nqb = (a.L + PF_QB - 1) / PF_QB;
+  p.nqb = (a.L * a.G + PF_ROWS - 1) / PF_ROWS;
   const int kt = a.kv_bf16 ? PfGeom<FMT_BF, FMT_BF>::KT : PfGeom<8, 8>::KT;
   // keys any query block scans: from the first block's window start to T
   const int64_t P = a.T - a.L;
@@ -780,7 +825,7 @@ PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
 
 size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S) {
   if (S <= 1) return 0;
-  const size_t rows = (size_t)B * Hkv * S * nqb * 8 * PF_QB;
+  const size_t rows = (size_t)B * Hkv * S * nqb * PF_ROWS;
   return rows * HEAD_DIM * 4 + rows * 2 * 4;
 }
 

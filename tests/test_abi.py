@@ -216,13 +216,17 @@ def test_prefill_split_validation(lib):
 
 
 def test_prefill_workspace_bytes(lib):
-    row = 8 * 32 * (128 + 2) * 4  # one query block of one KV head, one split
-    # 4 KV heads x 1 query block = 4 workgroups: the automatic plan allows 64 splits
-    assert lib.rec_prefill_workspace_bytes(1, 4, 20, 0) == 4 * 64 * row
-    # 64 query blocks x 4 KV heads fill the chip: no split, no workspace
-    assert lib.rec_prefill_workspace_bytes(1, 4, 2048, 0) == 0
-    assert lib.rec_prefill_workspace_bytes(2, 2, 40, 7) == 2 * 2 * 7 * 2 * row
-    assert lib.rec_prefill_workspace_bytes(1, 4, 20, 1) == 0
+    row = 256 * (128 + 2) * 4  # one block of 256 (query, head) rows of one KV head, one split
+    # 20 queries x 8 heads = 160 rows: one block per KV head, 4 workgroups;
+    # the automatic plan allows 64 splits
+    assert lib.rec_prefill_workspace_bytes(1, 32, 4, 20, 0) == 4 * 64 * row
+    # 64 blocks x 4 KV heads fill the chip: no split, no workspace
+    assert lib.rec_prefill_workspace_bytes(1, 32, 4, 2048, 0) == 0
+    # one query head per KV head: 2048 rows = 8 blocks x 4 KV heads, 8 splits
+    assert lib.rec_prefill_workspace_bytes(1, 4, 4, 2048, 0) == 4 * 8 * 8 * row
+    assert lib.rec_prefill_workspace_bytes(2, 16, 2, 40, 7) == 2 * 2 * 7 * 2 * row
+    assert lib.rec_prefill_workspace_bytes(1, 32, 4, 20, 1) == 0
+    assert lib.rec_prefill_workspace_bytes(1, 30, 4, 20, 0) == 0  # Hq not a multiple of Hkv
 
 
 def _append_attn(lib, **kw):

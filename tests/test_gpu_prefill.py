@@ -126,6 +126,7 @@ SPLIT_CASES = [
     (1, 8, 2, 700, 33, True, True, torch.bfloat16, 64),     # more splits asked than tiles
     (1, 8, 1, 130, 2, True, True, torch.float16, 3),        # splits past the causal end stay empty
     (3, 12, 4, 1500, 9, True, True, torch.bfloat16, 1),     # explicitly unsplit
+    (1, 12, 4, 3000, 100, True, True, torch.bfloat16, 0),   # 300 rows: the second block starts inside query 85
 ]
 
 
