@@ -73,6 +73,12 @@ struct PfGeom {
   static constexpr int V_ELEMS = VTR ? KT * VPB : HEAD_DIM * VROW;
   // element offset of unit u's V in the tile
   static constexpr int vunit(int u) { return VTR ? 32 * u * VPB : 32 * u; }
+  // V^T operands of a unit read ahead of its softmax (of 8): as many as the
+  // registers hold (a mixed int8/uint4 pair, or the exact P·V, leaves fewer);
+  // the bf16 cache's transposed reads measured fastest issued at the P·V
+  static constexpr int vpre(bool exact) {
+    return VTR ? 0 : ((KF == 8 && VF == 4) || (KF == 4 && VF == 8)) ? (exact ? 2 : 4) : exact ? 4 : 8;
+  }
   // Scale bytes per 32-token block, per staged region: [K scales][K zeros][V scales][V zeros]
   // (int8: one fp16 per token; uint4: [4 groups][32 slots] fp16 scales, zero-points alike;
   // affine: [scale, bias][2 groups][32 slots] bf16 in the scales region).
@@ -397,14 +403,19 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
   for (int rt = 0; rt < NRT; ++rt)
 #pragma unroll
     for (int j = 0; j < 2; ++j) s4[rt][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  // all eight operand reads first, so that the MFMAs wait for the LDS once
+  V8 ka[4][2];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const V8 ka = *(const V8*)(K + (16 * j + c) * PF_KROW + 32 * ks + 8 * g);
+    for (int j = 0; j < 2; ++j) ka[ks][j] = *(const V8*)(K + (16 * j + c) * PF_KROW + 32 * ks + 8 * g);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int rt = 0; rt < NRT; ++rt) s4[rt][j] = MT<BF16>::mfma(ka, qop[rt][ks], s4[rt][j]);
-    }
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int rt = 0; rt < NRT; ++rt) s4[rt][j] = MT<BF16>::mfma(ka[ks][j], qop[rt][ks], s4[rt][j]);
 }
 
 // Softmax of one unit's scores, then O^T += V^T P'^T.  mask: some token of the
@@ -416,21 +427,48 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
 // finite score), thr, the bound past which a score moves it (-inf until the
 // row has seen a finite score, then RESCALE_GAP), and l_run, the sum of
 // probabilities.  t = s * ksc - m_use is one fma per score.
-template <int VROW, bool VTR, bool EXACT, int NRT>
+template <int VROW, bool VTR, bool EXACT, int NRT, int VPRE>
 __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
                                                 const float* VS, float (&m_use)[2], float (&thr)[2],
                                                 float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end,
                                                 const int (&qabs)[2], int causal, int window, bool mask,
                                                 int c, int g) {
   v8h pb[2], pl[2];  // P'^T: high parts, and (EXACT) the remainders
+  // The unit's LDS reads first: the row scales and the first VPRE of the
+  // eight V^T operands, whose latency the softmax arithmetic then covers
+  // (one wait instead of one per pair of operands).
+  v4f ksc[2], vsc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    ksc[j] = *(const v4f*)(&KS[16 * j + 4 * g]);
+    vsc[j] = *(const v4f*)(&VS[16 * j + 4 * g]);
+  }
+  v8h va[8];
+  const int sk = c >> 2, sa = c & 3;  // transposed reads: rows 8g + sk (+4), dims 16n + 4sa
+  const auto load_va = [&](int n) {
+    if constexpr (VTR) {
+      // in a group of 16 lanes, lane 4a+b receives element b of the 8-byte
+      // rows addressed by lanes 4k+a: lane c gets dim 16n + c of rows 8g .. 8g+7
+      typedef __fp16 v4fp16 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+      typedef __attribute__((address_space(3))) v4fp16 lds_v4fp16;
+      const _Float16* base = Vv + (8 * g + sk) * 144 + 16 * n + 4 * sa;
+      const v2i r0 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4fp16*)base));
+      const v2i r1 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4fp16*)(base + 4 * 144)));
+      va[n] = __builtin_bit_cast(v8h, (v4i){r0[0], r0[1], r1[0], r1[1]});
+    } else {
+      va[n] = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
+    }
+  };
+#pragma unroll
+  for (int n = 0; n < VPRE; ++n) load_va(n);
+  if constexpr (VPRE > 0) __builtin_amdgcn_sched_barrier(0);
   // Range: P' = p·s feeds an fp16 operand, finite while p·s < 65504.  A V
   // scale of 2 or more among the lane's tokens (fp32 exponent bit 30;
   // |v| >= 254) makes its bound 0 for this unit, so its p <= 1 and
   // P' <= s <= 65504.
   bool big;
   {
-    const v4i w0 = *(const v4i*)(&VS[4 * g]), w1 = *(const v4i*)(&VS[16 + 4 * g]);
-    const v4i o = w0 | w1;
+    const v4i o = __builtin_bit_cast(v4i, vsc[0]) | __builtin_bit_cast(v4i, vsc[1]);
     big = ((uint32_t)(o[0] | o[1] | o[2] | o[3]) & 0x40000000u) != 0;
   }
 #pragma unroll
@@ -439,11 +477,9 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     // softmax per row (lane column c of tile rt; its query sits at qabs[rt])
     float t[8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const v4f ksc = *(const v4f*)(&KS[16 * j + 4 * g]);
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) t[4 * j + i] = __builtin_fmaf(s4[rt][j][i], ksc[i], -m_use[rt]);
-    }
+      for (int i = 0; i < 4; ++i) t[4 * j + i] = __builtin_fmaf(s4[rt][j][i], ksc[j][i], -m_use[rt]);
     if (mask) {
       // first and last visible token of this row, relative to the lane's first token t0 + 4g
       const int last = (causal ? min(qabs[rt], t_end - 1) : t_end - 1) - t0 - 4 * g;
@@ -483,40 +519,27 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     float lsum = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const v4f vsc = *(const v4f*)(&VS[16 * j + 4 * g]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = __builtin_amdgcn_exp2f(t[4 * j + i]);
         lsum += p;
         // B operand of P·V: k index 8g + 4j + i = cache position of token 16j + 4g + i
-        const _Float16 hi = (_Float16)(p * vsc[i]);
+        const _Float16 hi = (_Float16)(p * vsc[j][i]);
         pb[rt][4 * j + i] = hi;
-        if constexpr (EXACT) pl[rt][4 * j + i] = (_Float16)__builtin_fmaf(p, vsc[i], -(float)hi);
+        if constexpr (EXACT) pl[rt][4 * j + i] = (_Float16)__builtin_fmaf(p, vsc[j][i], -(float)hi);
       }
     }
     l_run[rt] += lsum;
   }
   __builtin_amdgcn_s_setprio(1);  // as around the Q·Kᵀ burst
-  const int sk = c >> 2, sa = c & 3;  // transposed reads: rows 8g + sk (+4), dims 16n + 4sa
+#pragma unroll
+  for (int n = VPRE; n < 8; ++n) load_va(n);
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
-    v8h va;
-    if constexpr (VTR) {
-      // in a group of 16 lanes, lane 4a+b receives element b of the 8-byte
-      // rows addressed by lanes 4k+a: lane c gets dim 16n + c of rows 8g .. 8g+7
-      typedef __fp16 v4fp16 __attribute__((__vector_size__(4 * sizeof(__fp16))));
-      typedef __attribute__((address_space(3))) v4fp16 lds_v4fp16;
-      const _Float16* base = Vv + (8 * g + sk) * 144 + 16 * n + 4 * sa;
-      const v2i r0 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4fp16*)base));
-      const v2i r1 = __builtin_bit_cast(v2i, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_v4fp16*)(base + 4 * 144)));
-      va = __builtin_bit_cast(v8h, (v4i){r0[0], r0[1], r1[0], r1[1]});
-    } else {
-      va = *(const v8h*)(Vv + (16 * n + c) * VROW + 8 * g);
-    }
 #pragma unroll
     for (int rt = 0; rt < NRT; ++rt) {
-      acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[rt], acc[n][rt], 0, 0, 0);
-      if constexpr (EXACT) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[rt], acc[n][rt], 0, 0, 0);
+      acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[n], pb[rt], acc[n][rt], 0, 0, 0);
+      if constexpr (EXACT) acc[n][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[n], pl[rt], acc[n][rt], 0, 0, 0);
     }
   }
   __builtin_amdgcn_s_setprio(0);
@@ -674,7 +697,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
           if (pend) {
             // the unit before: this tile's unit u - 1, or the previous tile's last
             const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? KT - 32 : 32 * (u - 1);
-            softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT>(sc[(u + 1) & 1], Vl[pb_] + (GEO::VTR ? po * GEO::VPB : po),
+            softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT, GEO::vpre(EXACT)>(sc[(u + 1) & 1], Vl[pb_] + (GEO::VTR ? po * GEO::VPB : po),
                                                         KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run, acc, pend_t,
                                                         t_end, qabs, a.causal, window, needs_mask(pend_t), c, g);
           }
@@ -701,7 +724,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       // still pending: the last tile's last unit (every unit of a tile is
       // visited, and a tile has an even number of units, so its scores are in sc[1])
       if (pend)
-        softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT>(sc[1], Vl[buf] + GEO::vunit(U - 1), KS[buf] + KT - 32,
+        softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT, GEO::vpre(EXACT)>(sc[1], Vl[buf] + GEO::vunit(U - 1), KS[buf] + KT - 32,
                                                     VS[buf] + KT - 32, m_use, thr, l_run, acc, pend_t, t_end, qabs,
                                                     a.causal, window, needs_mask(pend_t), c, g);
 
