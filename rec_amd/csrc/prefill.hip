@@ -73,11 +73,12 @@ struct PfGeom {
   static constexpr int V_ELEMS = VTR ? KT * VPB : HEAD_DIM * VROW;
   // element offset of unit u's V in the tile
   static constexpr int vunit(int u) { return VTR ? 32 * u * VPB : 32 * u; }
-  // V^T operands of a unit read ahead of its softmax (of 8): as many as the
-  // registers hold (a mixed int8/uint4 pair, or the exact P·V, leaves fewer);
-  // the bf16 cache's transposed reads measured fastest issued at the P·V
+  // V^T operands of a unit read ahead of its softmax (of 8): all of them,
+  // or half where the registers would spill in the hot loop (a mixed
+  // int8/uint4 pair; the affine pair with the exact P·V); the bf16 cache's
+  // transposed reads measured fastest issued at the P·V
   static constexpr int vpre(bool exact) {
-    return VTR ? 0 : ((KF == 8 && VF == 4) || (KF == 4 && VF == 8)) ? (exact ? 2 : 4) : exact ? 4 : 8;
+    return VTR ? 0 : ((KF == 8 && VF == 4) || (KF == 4 && VF == 8) || (exact && KF == FMT_A8)) ? 4 : 8;
   }
   // Scale bytes per 32-token block, per staged region: [K scales][K zeros][V scales][V zeros]
   // (int8: one fp16 per token; uint4: [4 groups][32 slots] fp16 scales, zero-points alike;
@@ -516,20 +517,35 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
 #pragma unroll
       for (int k = 0; k < 8; ++k) t[k] -= delta;
     }
-    float lsum = 0.f;
+    // B operand of P·V: k index 8g + 4j + i = cache position of token 16j + 4g + i
+    float pr[8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int k = 0; k < 8; ++k) pr[k] = __builtin_amdgcn_exp2f(t[k]);
+    float lsum = pr[0];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(t[4 * j + i]);
-        lsum += p;
-        // B operand of P·V: k index 8g + 4j + i = cache position of token 16j + 4g + i
-        const _Float16 hi = (_Float16)(p * vsc[j][i]);
-        pb[rt][4 * j + i] = hi;
-        if constexpr (EXACT) pl[rt][4 * j + i] = (_Float16)__builtin_fmaf(p, vsc[j][i], -(float)hi);
-      }
-    }
+    for (int k = 1; k < 8; ++k) lsum += pr[k];
     l_run[rt] += lsum;
+    if constexpr (EXACT) {
+      // P' = p·s rounded to fp16 once by v_fma_mix, straight into the
+      // operand's halves (fewer registers than a multiply, a conversion and
+      // a pack; the room goes to the V operands read ahead), then the
+      // remainder
+#pragma unroll
+      for (int k = 0; k < 8; k += 2) {
+        const int j = k >> 2, i = k & 3;
+        uint32_t w;
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(w) : "v"(pr[k]), "v"(vsc[j][i]));
+        asm("v_fma_mixhi_f16 %0, %1, %2, 0" : "+v"(w) : "v"(pr[k + 1]), "v"(vsc[j][i + 1]));
+        const v2h hh = __builtin_bit_cast(v2h, w);
+        pb[rt][k] = hh[0];
+        pb[rt][k + 1] = hh[1];
+        pl[rt][k] = (_Float16)__builtin_fmaf(pr[k], vsc[j][i], -(float)hh[0]);
+        pl[rt][k + 1] = (_Float16)__builtin_fmaf(pr[k + 1], vsc[j][i + 1], -(float)hh[1]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) pb[rt][k] = (_Float16)(pr[k] * vsc[k >> 2][k & 3]);
+    }
   }
   __builtin_amdgcn_s_setprio(1);  // as around the Q·Kᵀ burst
 #pragma unroll
