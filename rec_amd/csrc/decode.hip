@@ -168,9 +168,12 @@ struct Chunk {
   v4i v8[4];      // int8 V: dim blocks 2h, 2h+1 (8 bytes each), this lane's 8 tokens
   v4i v4[2];      // int4 V: dim blocks 4h..4h+3, this lane's 8 tokens packed
   v4i s8[2];      // int8 scales of this lane's 8 positions: [0] K, [1] V
-  uint32_t m[4];  // int4 scales and zero-points of the block, one dword per lane:
-                  // [0] K scales, [1] K zeros, [2] V scales, [3] V zeros; handed out
-                  // through LDS
+  v4i m4;         // uint4 K and V: the block's four metadata arrays (K scales, K
+                  // zeros, V scales, V zeros), 16 bytes per lane: lanes 16a .. 16a+15
+                  // hold array a; handed out through LDS
+  uint32_t m[4];  // one 4-bit side's (or the affine format's) metadata, one dword per
+                  // lane: [0] K scales, [1] K zeros, [2] V scales, [3] V zeros;
+                  // handed out through LDS
 };
 
 // Buffer resources of one (b, h) slice of the cache, plus an empty one.  Every
@@ -207,9 +210,13 @@ __device__ __forceinline__ LaneOff lane_offsets(int lane) {
 }
 
 // Issue every load of cache block `blk` of the slice, or (ok false) the same
-// loads through the empty resource.
+// loads through the empty resource.  uint4 K and V bring the block's metadata
+// in one 16-byte load per lane from `mbase` (the lane's own array and
+// offset; block 0 when ok is false), instead of four 4-byte loads: 3% faster
+// at 32K and 131K tokens.
 template <int KB, int VB>
-__device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff& o, bool ok, uint32_t blk) {
+__device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff& o, bool ok, uint32_t blk,
+                                           const char* mbase) {
   const __amdgpu_buffer_rsrc_t rk = ok ? S.k : S.none, rks = ok ? S.ks : S.none, rkz = ok ? S.kz : S.none;
   const __amdgpu_buffer_rsrc_t rv = ok ? S.v : S.none, rvs = ok ? S.vs : S.none, rvz = ok ? S.vz : S.none;
   // Q·Kᵀ tile j, row r is token 16j + r of the block; the MFMA leaves lane
@@ -224,7 +231,9 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
       R.k4[j] = ld128(rk, o.k[j], blk * 2048);
     }
   }
-  if constexpr (KB == 8) {
+  if constexpr (KB == 4 && VB == 4) {
+    R.m4 = __builtin_nontemporal_load((const v4i*)(mbase + (size_t)(ok ? blk : 0u) * 256));
+  } else if constexpr (KB == 8) {
     R.s8[0] = ld128(rks, o.s8, blk * 64);
   } else if constexpr (KB == FMT_A8) {
     R.m[0] = ld32(rks, o.m4, blk * 256);  // scales and biases
@@ -240,8 +249,10 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
   } else {
     R.v4[0] = ld128(rv, o.v, blk * 2048);
     R.v4[1] = ld128(rv, o.v + 1024, blk * 2048);
-    R.m[2] = ld32(rvs, o.m4, blk * 256);  // affine: scales and biases
-    if constexpr (VB == 4) R.m[3] = ld32(rvz, o.m4, blk * 256);
+    if constexpr (KB != 4 || VB != 4) {
+      R.m[2] = ld32(rvs, o.m4, blk * 256);  // affine: scales and biases
+      if constexpr (VB == 4) R.m[3] = ld32(rvz, o.m4, blk * 256);
+    }
   }
 }
 
@@ -271,12 +282,14 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   if constexpr (VB == 8) vs = R.s8[1];
   if constexpr (KB == 4 || VB == 4 || KB == FMT_A8 || VB == FMT_A4) {
     uint32_t* mw = (uint32_t*)meta;
-    if constexpr (KB == 4) {
+    if constexpr (KB == 4 && VB == 4) {
+      *(v4i*)(meta + 16 * lane) = R.m4;  // array lane / 16, bytes 16 (lane % 16) ..
+    } else if constexpr (KB == 4) {
       mw[lane] = R.m[0];
       mw[64 + lane] = R.m[1];
     }
     if constexpr (KB == FMT_A8) mw[lane] = R.m[0];
-    if constexpr (VB == 4) {
+    if constexpr (VB == 4 && KB != 4) {
       mw[128 + lane] = R.m[2];
       mw[192 + lane] = R.m[3];
     }
@@ -395,6 +408,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     big = ((uint32_t)(vs[0] | vs[1] | vs[2] | vs[3]) & 0x40004000u) != 0;
   } else if constexpr (VB == FMT_A4) {
     big = __ballot(lane < 32 && (R.m[2] & 0x40004000u) != 0) != 0;  // lanes 32-63 hold biases
+  } else if constexpr (KB == 4) {
+    const uint32_t w = (uint32_t)(R.m4[0] | R.m4[1] | R.m4[2] | R.m4[3]);
+    big = __ballot((lane >> 4) == 2 && (w & 0x40004000u) != 0) != 0;  // lanes 32-47 hold the V scales
   } else {
     big = __ballot((R.m[2] & 0x40004000u) != 0) != 0;
   }
@@ -622,9 +638,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
   const int n_w = n_split > wave ? (n_split - wave + WAVES - 1) / WAVES : 0;
   const int blk0 = t_begin / CH + wave;
   const LaneOff lo = lane_offsets<KB, VB>(lane);
+  const char* mbase = nullptr;  // uint4 K and V: this lane's metadata array and offset
+  if constexpr (KB == 4 && VB == 4) {
+    const int sel = lane >> 4;
+    const uint16_t* arr = sel == 0 ? a.ks : sel == 1 ? a.kz : sel == 2 ? a.vs : a.vz;
+    mbase = (const char*)arr + bh * cap * 8 + (lane & 15) * 16;
+  }
   Chunk buf[NBUF];
 #pragma unroll
-  for (int i = 0; i < NBUF - 1; ++i) load_chunk<KB, VB>(buf[i], R, lo, i < n_w, blk0 + WAVES * i);
+  for (int i = 0; i < NBUF - 1; ++i) load_chunk<KB, VB>(buf[i], R, lo, i < n_w, blk0 + WAVES * i, mbase);
 
   // Quantize the query into MFMA operands while the chunks stream in.
   {
@@ -676,7 +698,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
 #pragma unroll
     for (int j = 0; j < NBUF; ++j) {
       const int i = i0 + j;
-      load_chunk<KB, VB>(buf[(j + NBUF - 1) % NBUF], R, lo, i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1));
+      load_chunk<KB, VB>(buf[(j + NBUF - 1) % NBUF], R, lo, i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1),
+                         mbase);
       if (i < n_w)
         process_chunk<KB, VB, EXACT>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane,
                               smem + LD::meta + wave * 1024);

@@ -282,10 +282,20 @@ def test_bf16_prefill_matches_oracle(gpu, case):
     assert_close(f32(out), ref, f"case {case}")
 
 
-def test_bf16_prefill_window_mask_array(gpu):
+WINDOW_CASES = [
+    # Hq, Hkv, T, L, W
+    (16, 2, 400, 150, 97),
+    (12, 4, 700, 200, 40),  # 3 heads per KV head: a 256-row block spans 85 queries, more than the window
+    (4, 4, 600, 300, 40),   # one head per KV head: 256 queries per block
+]
+
+
+@pytest.mark.parametrize("case", WINDOW_CASES, ids=lambda c: "Hq{}_Hkv{}_T{}_L{}_W{}".format(*c))
+def test_bf16_prefill_window_mask_array(gpu, case):
     """A boolean sliding-window mask array (make_mask(..., return_array=True))
     is recognised and gives the same result as the oracle with that mask."""
-    B, Hq, Hkv, T, L, W = 1, 16, 2, 400, 150, 97
+    Hq, Hkv, T, L, W = case
+    B = 1
     k = synthetic.kv((B, Hkv, T, 128), 121, dtype=torch.bfloat16)
     v = synthetic.kv((B, Hkv, T, 128), 122, dtype=torch.bfloat16)
     q = synthetic.query(B, Hq, L, 123, dtype=torch.bfloat16)
