@@ -799,7 +799,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 // Merge of the key splits (S > 1): one wavefront per (query, query head,
 // batch); lane k owns the statistics of split k, the weights go through LDS,
 // and lane l sums dims 2l, 2l + 1 over the splits.  The sink logit joins here.
+// NR rounds of 16 split loads (S <= 16 NR), all issued before the first is
+// used: one trip to memory, not one per round.
+template <int NR>
 __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) {
+  static_assert(16 * NR <= PREFILL_MAX_SPLITS && PREFILL_MAX_SPLITS <= 64, "one split per lane");
   __shared__ float wts[PREFILL_MAX_SPLITS];
   const int i = blockIdx.x, hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
   const int h = hq / a.G, p = i * a.G + (hq - h * a.G);  // the (query, head) row
@@ -819,16 +823,13 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
   if (sink != NEG_INF) z += __builtin_amdgcn_exp2f(sink - M);
   wts[lane] = f;  // 0 for lanes past the last split
   __syncthreads();
-  // 16 independent loads in flight per round (slots past the last split read
-  // its row again and weigh it 0), not one memory round trip per split
+  // slots past the last split read its row again and weigh it 0
+  v2f x[16 * NR];
+#pragma unroll
+  for (int k = 0; k < 16 * NR; ++k) x[k] = *(const v2f*)(a.ws_acc + row(min(k, a.S - 1)) * HEAD_DIM + 2 * lane);
   v2f acc = {0.f, 0.f};
-  for (int s0 = 0; s0 < a.S; s0 += 16) {
-    v2f x[16];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = *(const v2f*)(a.ws_acc + row(min(s0 + k, a.S - 1)) * HEAD_DIM + 2 * lane);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) acc += wts[min(s0 + k, PREFILL_MAX_SPLITS - 1)] * x[k];
-  }
+  for (int k = 0; k < 16 * NR; ++k) acc += wts[k] * x[k];
   const float inv = z > 0.f ? 1.f / z : 1.f;
   *(v2f*)(a.out + (((int64_t)b * a.Hq + hq) * a.L + i) * HEAD_DIM + 2 * lane) = acc * inv;
 }
@@ -900,7 +901,11 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   if (a.S > 1) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3((unsigned)a.L, a.Hq, a.B), dim3(64), 0, stream, a);
+    const dim3 grid((unsigned)a.L, a.Hq, a.B), block(64);
+    if (a.S <= 16) hipLaunchKernelGGL(prefill_merge_kernel<1>, grid, block, 0, stream, a);
+    else if (a.S <= 32) hipLaunchKernelGGL(prefill_merge_kernel<2>, grid, block, 0, stream, a);
+    else if (a.S <= 48) hipLaunchKernelGGL(prefill_merge_kernel<3>, grid, block, 0, stream, a);
+    else hipLaunchKernelGGL(prefill_merge_kernel<4>, grid, block, 0, stream, a);
   }
   return hipGetLastError();
 }
