@@ -27,16 +27,20 @@
 // GQA group); a workgroup takes 256 consecutive rows as 16 row tiles of 16,
 // and wave w owns tiles w and w + 8.  A chunk of a few queries thus fills
 // its row tiles with those queries' heads instead of padding every head to a
-// tile, and a wave whose tiles lie past the last row skips them.  K/V tiles of 128 tokens (64 for a bf16 cache) are
-// dequantized into double-buffered LDS and shared by the 8 waves, which
-// compute a tile in 32-token units, software-pipelined (one unit's Q·K^T on
-// the matrix cores while the previous unit's softmax runs on the VALU).  Each
-// tile's raw bytes are fetched a whole tile ahead and dequantized into the
-// other buffer between two barriers at the end of the current tile; its scale
-// bytes reach the converting threads through a small LDS staging area.
-// (Spreading the conversion over the units, behind their Q·K^T MFMAs, was
-// measured no faster: the kernel is bound by LDS traffic and latency, not
-// by the conversion's VALU work.)  A grid too small to fill the chip (a short chunk
+// tile, and a wave whose tiles lie past the last row skips them.
+//
+// K/V tiles of 128 tokens (64 for a bf16 cache) are dequantized into
+// double-buffered LDS and shared by the 8 waves, which compute a tile in
+// 32-token units, software-pipelined (one unit's Q·K^T on the matrix cores
+// while the previous unit's softmax runs on the VALU); each burst issues its
+// LDS operand reads together ahead of its MFMAs, so it waits for the LDS
+// once.  Each tile's raw bytes are fetched a whole tile ahead and dequantized
+// into the other buffer between two barriers at the end of the current tile;
+// its scale bytes reach the converting threads through a small LDS staging
+// area.  (Spreading the conversion over the units, behind their Q·K^T MFMAs,
+// was measured no faster: with two waves per SIMD the kernel is bound by each
+// wave's in-order chain of LDS reads, MFMAs and softmax, not by the
+// conversion's VALU work.)  A grid too small to fill the chip (a short chunk
 // over a long cache) splits the keys: each workgroup writes an unnormalised
 // partial and prefill_merge_kernel combines the splits as the decode's merge
 // does (megakernel.py:276-318).
