@@ -93,11 +93,17 @@ def test_chunked_prefill_then_decode(gpu):
         assert_close(f32(out), ref, f"decode {t}")
 
 
-def test_prefill_full_size_rows(gpu):
-    """2048 causal queries over a 65536-token prefix: sampled rows equal a
-    decode over their prefix (a size-independent property), checked against the
-    chunked CPU oracle."""
-    B, Hq, Hkv, P, L = 1, 32, 4, 65536, 2048
+@pytest.mark.parametrize("Hq,Hkv,P,L,rows", [
+    (32, 4, 65536, 2048, [0, 1, 777, 1500, 2047]),
+    # 3 query heads per KV head: 256-row blocks start inside queries (query 85
+    # holds rows 255-257), the last block is partial
+    (12, 4, 16384, 1000, [0, 85, 86, 170, 999]),
+], ids=["Hq32_Hkv4_P65536_L2048", "Hq12_Hkv4_P16384_L1000"])
+def test_prefill_full_size_rows(gpu, Hq, Hkv, P, L, rows):
+    """Long causal chunks over a long prefix: sampled rows equal a decode over
+    their prefix (a size-independent property), checked against the chunked
+    CPU oracle."""
+    B = 1
     T = P + L
     cache = QuantizedKVCache(32, 8, 8, max_tokens=T)
     k = synthetic.kv((B, Hkv, T, 128), 7, kind="outliers", frac=0.01)
@@ -111,7 +117,7 @@ def test_prefill_full_size_rows(gpu):
     vc, vsc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(vq))
     del k, v
     qf, of, sf = f32(q), f32(out), f32(sinks)
-    for i in [0, 1, 777, 1500, 2047]:
+    for i in rows:
         Ti = P + i + 1
         cache_np = dict(k_bits=8, v_bits=8, kq=kc[:, :, :Ti], ks=ksc[:, :, :Ti], vq=vc[:, :, :Ti], vs=vsc[:, :, :Ti])
         ref = O.split_k_decode_quantized(qf[:, :, i], cache_np, Ti, SCALE, sf, chunk=8192)
