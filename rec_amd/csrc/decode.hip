@@ -383,7 +383,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       }
     }
   }
-  if (valid < CH) {  // tail chunk: tokens past the split end
+  // tail chunk: tokens past the split end (rare: without the hint the
+  // compiler turns this into compares and selects on every chunk)
+  if (__builtin_expect(valid < CH, 0)) {
 #pragma unroll
     for (int idx = 0; idx < 8; ++idx)
       if (16 * (idx >> 2) + 4 * kg + (idx & 3) >= valid) s[idx] = NEG_INF;
