@@ -100,7 +100,9 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[4 * j + i] = d[i] + dpp_ror8f(d[i]);  // high part + low part
   }
-  if (valid < BCH) {  // tail chunk: tokens past the split end
+  // tail chunk: tokens past the split end (rare: without the hint the
+  // compiler turns this into compares and selects on every chunk)
+  if (__builtin_expect(valid < BCH, 0)) {
 #pragma unroll
     for (int idx = 0; idx < 8; ++idx)
       if (16 * (idx >> 2) + 4 * kg + (idx & 3) >= valid) s[idx] = NEG_INF;
