@@ -28,6 +28,8 @@ CASES = [
     (3, 4, 4, 40, 33, True, True, torch.bfloat16),    # one query head per KV head, three sequences
     (1, 12, 4, 256, 96, True, True, torch.float16),   # three per KV head
     (2, 8, 1, 31, 1, True, True, torch.bfloat16),     # a one-token chunk (attend takes the decode path)
+    (1, 20, 4, 300, 77, True, True, torch.bfloat16),  # five per KV head: 385 rows, the second block starts in query 51
+    (2, 7, 1, 500, 100, False, True, torch.float16),  # seven per KV head, full attention
 ]
 
 
@@ -133,6 +135,7 @@ SPLIT_CASES = [
     (1, 8, 1, 130, 2, True, True, torch.float16, 3),        # splits past the causal end stay empty
     (3, 12, 4, 1500, 9, True, True, torch.bfloat16, 1),     # explicitly unsplit
     (1, 12, 4, 3000, 100, True, True, torch.bfloat16, 0),   # 300 rows: the second block starts inside query 85
+    (1, 28, 4, 4000, 45, True, True, torch.float16, 0),     # seven per KV head: 315 rows over two blocks
 ]
 
 
