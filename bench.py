@@ -201,8 +201,18 @@ class _TimingEvents:
 
     FLAGS = 0x20000000  # hipEventDisableSystemFence
 
+    @staticmethod
+    def _loaded_runtime():
+        """The HIP runtime file this process has mapped (torch's), so that
+        the events and the work share one runtime."""
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64" in line:
+                    return line.split()[-1]
+        raise RuntimeError("the HIP runtime is not loaded (initialise the GPU first)")
+
     def __init__(self):
-        hip = ctypes.CDLL("libamdhip64.so.7")
+        hip = ctypes.CDLL(self._loaded_runtime())
         hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
         hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
