@@ -545,7 +545,7 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
         rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3],
                                   kq.code, kq.codes.data_ptr(), kq.scales.data_ptr(), ptr(kq.zeros),
                                   vq.code, vq.codes.data_ptr(), vq.scales.data_ptr(), ptr(vq.zeros),
-                                  sinks.data_ptr(), SCALE, 1,
+                                  sinks.data_ptr(), SCALE, 1, 0,
                                   1, HQ, HKV, D, L, T, c.capacity, 0, ws.data_ptr(), ws.numel(), out.data_ptr(), st)
         _lib.check(rc, "rec_prefill_attn")
 
@@ -553,7 +553,7 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
         append()
         attention()
     torch.cuda.synchronize()
-    g_step, g_att = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    g_step, g_att, g_app = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_step):
         for _ in range(steps):
             append()
@@ -561,22 +561,26 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
     with torch.cuda.graph(g_att):
         for _ in range(steps):
             attention()
+    with torch.cuda.graph(g_app):
+        for _ in range(steps):
+            append()
     ms_step = _median_timed(torch, g_step, steps)
     ms_att = _median_timed(torch, g_att, steps)
+    ms_app = _median_timed(torch, g_app, steps)
     pairs = L * P + L * (L + 1) // 2
     flops = 4.0 * D * HQ * pairs
     tflops = flops / (ms_att * 1e-3) / 1e12
     kv_bytes = round(T * HKV * tok_bytes)  # every cached K/V row and its scales, read once
     log(f"prefill ({fmt}) {P}+{L}: {ms_step:.3f} ms/step, attention {ms_att:.3f} ms = {tflops:.0f} TFLOP/s, "
         f"{kv_bytes / (ms_att * 1e-3) / 1e9:.0f} GB/s of K/V")
-    del g_step, g_att, c
+    del g_step, g_att, g_app, c
     torch.cuda.empty_cache()
     return dict(
         prefix=P,
         new_tokens=L,
         kv_format=PREFILL_FORMATS[fmt],
         ms_per_step=round(ms_step, 4),
-        append_ms=round(ms_step - ms_att, 4),
+        append_ms=round(ms_app, 4),
         attention_ms=round(ms_att, 4),
         attention_flops=flops,
         attention_tflops=round(tflops, 1),
@@ -586,6 +590,55 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
         kv_gbs=round(kv_bytes / (ms_att * 1e-3) / 1e9, 2),
         kv_frac_of_hbm_peak=round(kv_bytes / (ms_att * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         note="Q.K^T on bf16 MFMA, P.V on fp16 MFMA; peak is the dense bf16 figure",
+    )
+
+
+def run_sdpa_yardstick(P, L, steps):
+    """A library yardstick for the prefill, not this build's kernel: PyTorch's
+    own fused attention (torch.nn.functional.scaled_dot_product_attention,
+    flash backend, bf16 K/V already in HBM with the KV heads expanded to the
+    query heads, causal aligned to the last query) over the same P + L keys,
+    timed on the current stream over `steps` back-to-back calls."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    from torch.nn.attention.bias import causal_lower_right
+
+    T = P + L
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    q = torch.randn(1, HQ, L, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    k = torch.randn(1, HQ, T, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    v = torch.randn(1, HQ, T, D, device="cuda", dtype=torch.bfloat16, generator=g)
+    mask = causal_lower_right(L, T)
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            call = lambda: F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=float(SCALE))  # noqa: E731
+            call()
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(5):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                for _ in range(steps):
+                    call()
+                b.record()
+                torch.cuda.synchronize()
+                times.append(a.elapsed_time(b) / steps)
+    except Exception as e:  # no fused kernel for this device or shape
+        log(f"sdpa yardstick unavailable: {e}")
+        return None
+    finally:
+        del q, k, v
+        torch.cuda.empty_cache()
+    ms = sorted(times)[2]
+    flops = 4.0 * D * HQ * (L * P + L * (L + 1) // 2)
+    log(f"sdpa yardstick {P}+{L}: {ms:.3f} ms = {flops / (ms * 1e-3) / 1e12:.0f} TFLOP/s")
+    return dict(
+        ms=round(ms, 4),
+        tflops=round(flops / (ms * 1e-3) / 1e12, 1),
+        what="torch.nn.functional.scaled_dot_product_attention (flash backend) over the same causal chunk, bf16 K/V "
+             "expanded to 32 heads, no quantization and no sinks; PyTorch's own kernel, not this library's",
     )
 
 
@@ -742,6 +795,7 @@ def main(argv=None):
     ap.add_argument("--no-affine", action="store_true", help="skip the group-64 affine cache measurement")
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-floor", action="store_true", help="skip the plain streaming-read floor")
+    ap.add_argument("--no-yardstick", action="store_true", help="skip timing PyTorch's own fused attention")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--seed", type=int, default=1234)
@@ -829,6 +883,8 @@ def main(argv=None):
         # the same long chunk over the 4-bit, affine and bf16 caches
         for i, fmt in enumerate(("uint4", "affine", "bf16")):
             rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
+        if not args.no_yardstick:
+            rpf["library_yardstick"] = run_sdpa_yardstick(65536, 2048, args.prefill_steps)
 
     floor = None if args.no_floor else run_read_floor(max(20, args.steps // 5))
 

@@ -183,7 +183,9 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * Chunked prefill: the last L of the T cached tokens are new (already
  * quantize-appended with rec_kv_append); their queries q (B, Hq, L, D), element
  * strides (q_sb, q_sh, q_st), bf16 or f16, attend over all T tokens — with
- * causal != 0, query i sees tokens [0, T-L+i] — with optional sink logits.
+ * causal != 0, query i sees tokens [0, T-L+i]; window > 0 further limits
+ * query position p to keys > p - window (a sliding-window mask array of
+ * model.py:122-128; window 0 = none) — with optional sink logits.
  * out (B, Hq, L, D) fp32.  Any cache format of rec_decode_attn (int8 or uint4
  * in any mix, or the affine pair): K/V tiles are dequantized into on-chip
  * memory, never to HBM — int8 codes exactly with the row scales applied to
@@ -201,7 +203,7 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
 int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
                      int k_bits, const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros,
                      int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
-                     const float* sinks, float scale, int causal,
+                     const float* sinks, float scale, int causal, int window,
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
                      int splits, void* workspace, size_t workspace_bytes, float* out, void* stream);
 

@@ -64,7 +64,7 @@ SIGNATURES["rec_decode_scratch_bytes"] = (_sz, [])
 SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _p, _p])
 SIGNATURES["rec_prefill_attn"] = (
     _i,
-    [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i64, _i64,
+    [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64, _i64,
      _i, _p, _sz, _p, _p],
 )
 SIGNATURES["rec_prefill_workspace_bytes"] = (_sz, [_i, _i, _i, _i, _i])

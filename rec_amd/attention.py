@@ -4,8 +4,8 @@
   engine/src/rec_mlx/model.py:108-110 and runs the gfx950 split-K decode kernel
   (``rec_decode_attn``) for one query token, the chunked prefill kernel for
   several (model.py:191-203: ``rec_prefill_attn`` reads every cache format
-  directly, dequantizing tiles on chip; a sliding-window mask goes through bf16
-  copies, ``rec_kv_dequant_bf16`` then ``rec_prefill_bf16``).
+  directly, dequantizing tiles on chip, and applies sliding-window masks, also
+  for a single windowed query).
 * :func:`attend` mirrors the cache/attention part of ``Attention.__call__``
   (model.py:177-203): append first, then attend, decode for ``L == 1`` and
   chunked prefill for ``L > 1``.  For a
@@ -152,7 +152,7 @@ def prefill_workspace(device: torch.device, B: int, Hq: int, Hkv: int, L: int, s
         return ws
 
 
-def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out, splits=0):
+def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out, splits=0, window=0):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     q = queries if queries.stride(-1) == 1 else queries.contiguous()
@@ -164,7 +164,8 @@ def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sink
         q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), q.stride(2),
         keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
         values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
-        _ptr(sk), float(scale), int(causal), B, Hq, keys.n_kv_heads, D, L, int(keys.length), int(keys.capacity),
+        _ptr(sk), float(scale), int(causal), int(window), B, Hq, keys.n_kv_heads, D, L, int(keys.length),
+        int(keys.capacity),
         int(splits), ws.data_ptr(), ws.numel(), out.data_ptr(), stream,
     )
     _lib.check(rc, "rec_prefill_attn")
@@ -201,9 +202,9 @@ def quantized_attention_with_sinks(
     both mean "every cached token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` (bf16/f16
     queries, the newest ``L`` cached tokens) the chunked prefill kernel, which
     reads every cache format directly (4-bit and affine values rounded to the
-    query dtype, as the reference dequantizes, int8 codes exactly); with a
-    sliding-window mask the cache is first dequantized to bf16
-    (:func:`dequantize_kv`) for the bf16 prefill kernel's window masking.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
+    query dtype, as the reference dequantizes, int8 codes exactly).  A
+    sliding-window mask is applied by the prefill kernel, also for one query
+    (bf16/f16), which then sees the last ``window`` tokens.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
     (default: the query dtype, as the reference returns, model.py:132-139).
     """
     _check_query(queries)
@@ -218,9 +219,7 @@ def quantized_attention_with_sinks(
         raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
     _check_cache_shapes(queries, keys, values)
     causal, win = _mask_plan(mask, L, int(keys.length))
-    if win and L == 1:
-        raise NotImplementedError("sliding-window masks are not supported for a decode step over a quantized cache")
-    if L == 1:
+    if L == 1 and not win:
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
         _decode_launch(queries, keys, values, scale, sinks, splits, out)
         out = out.view(B, Hq, 1, D)
@@ -229,13 +228,9 @@ def quantized_attention_with_sinks(
         if L > keys.length:
             raise ValueError(f"{L} queries but only {keys.length} cached tokens")
         if queries.dtype not in (torch.bfloat16, torch.float16):
-            raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
+            raise NotImplementedError("prefill (and windowed) queries must be bf16 or f16 (the matrix-core input type)")
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
-        if not win:
-            _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0)
-        else:  # a sliding window: over bf16 copies, through the bf16 prefill's window masking
-            k, v = dequantize_kv(keys, values)
-            _bf16_prefill_launch(queries, k, v, scale, sinks, causal, win, out, splits or 0)
+        _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0, win)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 
@@ -419,12 +414,12 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
             return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
         k, v = cache.update_and_fetch(keys, values)
         return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits)
-    if fused and L == 1:
+    # one query under a sliding window (a causal mask keeps every key) takes
+    # the append, then the windowed prefill kernel
+    if fused and L == 1 and not _mask_plan(mask, 1, cache.offset + 1)[1]:
         cache._check_usable()
         if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
             raise ValueError("a fused decode step takes one new K/V token of a float dtype")
-        if _mask_plan(mask, 1, cache.offset + 1)[1]:  # one query: causal keeps every key, a window does not
-            raise NotImplementedError("a fused decode step attends over every cached token (mask None or causal)")
         Bk, H = keys.shape[:2]
         if cache.keys is not None and tuple(cache.keys[0].shape[:2]) != (Bk, H):
             raise ValueError(f"new keys have (B, Hkv) = ({Bk}, {H}), the cache holds "

@@ -451,8 +451,8 @@ size_t rec_prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int splits) {
 int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int k_bits,
                      const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits,
                      const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks,
-                     float scale, int causal, int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
-                     int splits, void* workspace, size_t workspace_bytes, float* out, void* stream) {
+                     float scale, int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T,
+                     int64_t capacity, int splits, void* workspace, size_t workspace_bytes, float* out, void* stream) {
   int e;
   int kf, vf;
   if ((e = resolve_formats(k_bits, v_bits, &kf, &vf))) return e;
@@ -466,6 +466,7 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   if (capacity % BLOCK_T != 0) return fail(REC_EINVAL, "capacity %lld is not a multiple of 32", (long long)capacity);
   if (T > capacity) return fail(REC_ECAPACITY, "T=%lld exceeds the cache capacity %lld", (long long)T, (long long)capacity);
   if (capacity > ((int64_t)1 << 24)) return fail(REC_EUNSUPPORTED, "capacity above 16M tokens per head");
+  if (window < 0) return fail(REC_EINVAL, "negative window");
   if (!q || !out) return fail(REC_EINVAL, "query/output pointer is null");
   if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
   if ((e = check_cache(kf, k_codes, k_scales, k_zeros, "key")) || (e = check_cache(vf, v_codes, v_scales, v_zeros, "value")))
@@ -497,6 +498,7 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.T = T;
   a.cap = capacity;
   a.causal = causal != 0;
+  a.window = window;
   if ((e = plan_prefill_splits(a, splits, workspace, workspace_bytes))) return e;
   return launched(launch_prefill(a, (hipStream_t)stream), "prefill launch");
 }

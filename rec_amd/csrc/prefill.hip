@@ -589,7 +589,7 @@ __device__ __forceinline__ void load_query(typename MT<BF16>::vec (&qop)[2][4], 
   }
 }
 
-template <bool BF16, int KF, int VF, bool EXACT>
+template <bool BF16, int KF, int VF, bool EXACT, bool WIN>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   typedef PfGeom<KF, VF> GEO;
   typedef typename MT<BF16>::elem E;
@@ -639,8 +639,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     qabs[1] = P + qr[1];
   }
 
-  // a sliding window (bf16 caches only) starts the scan at the first query's first visible key
-  const int window = GEO::BF ? a.window : 0;
+  // a sliding window starts the scan at the first query's first visible key
+  // (WIN: compiled in; without it the window is 0 and its terms vanish, which
+  // keeps the quantized scans clear of register spills)
+  const int window = WIN ? a.window : 0;
   const int t_first = window > 0 ? max(0, P + q_lo - window + 1) / KT * KT : 0;
   // this workgroup's share of the keys, [lo, t_end): the split's range
   // (tile-aligned) within the query block's [t_first, t_blk); empty for some
@@ -844,7 +846,7 @@ PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
   const int kt = a.kv_bf16 ? PfGeom<FMT_BF, FMT_BF>::KT : PfGeom<8, 8>::KT;
   // keys any query block scans: from the first block's window start to T
   const int64_t P = a.T - a.L;
-  const int64_t lo = (a.kv_bf16 && a.window > 0) ? std::max<int64_t>(0, P - a.window + 1) / kt * kt : 0;
+  const int64_t lo = a.window > 0 ? std::max<int64_t>(0, P - a.window + 1) / kt * kt : 0;
   const int64_t tiles = (a.T - lo + kt - 1) / kt;
   int S = requested;
   if (S <= 0) {
@@ -873,22 +875,30 @@ size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S) {
   return rows * HEAD_DIM * 4 + rows * 2 * 4;
 }
 
+template <bool BF16, bool EXACT, bool WIN>
+static void launch_quantized(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  const int kf = a.k_fmt, vf = a.v_fmt;
+  if (kf == 8 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 8, EXACT, WIN>), grid, block, 0, stream, a);
+  else if (kf == 8 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 4, EXACT, WIN>), grid, block, 0, stream, a);
+  else if (kf == 4 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 8, EXACT, WIN>), grid, block, 0, stream, a);
+  else if (kf == 4 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 4, EXACT, WIN>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8, FMT_A4, EXACT, WIN>), grid, block, 0, stream, a);
+}
+
+// The bf16 cache (ring windows) always takes the window at run time; the
+// quantized formats have a variant with it and one without.
 template <bool BF16, bool EXACT>
 static void launch_formats(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
-  const int kf = a.k_fmt, vf = a.v_fmt;
-  if (kf == FMT_BF) hipLaunchKernelGGL((prefill_kernel<BF16, FMT_BF, FMT_BF, EXACT>), grid, block, 0, stream, a);
-  else if (kf == 8 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 8, EXACT>), grid, block, 0, stream, a);
-  else if (kf == 8 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 4, EXACT>), grid, block, 0, stream, a);
-  else if (kf == 4 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 8, EXACT>), grid, block, 0, stream, a);
-  else if (kf == 4 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 4, EXACT>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8, FMT_A4, EXACT>), grid, block, 0, stream, a);
+  if (a.k_fmt == FMT_BF) hipLaunchKernelGGL((prefill_kernel<BF16, FMT_BF, FMT_BF, EXACT, true>), grid, block, 0, stream, a);
+  else if (a.window > 0) launch_quantized<BF16, EXACT, true>(a, grid, block, stream);
+  else launch_quantized<BF16, EXACT, false>(a, grid, block, stream);
 }
 
 // Fewest keys any query row of the launch sees: the first row's causal
 // prefix (and at most the window), or all T keys without a causal mask.
 static int64_t fewest_visible_keys(const PrefillArgs& a) {
   int64_t n = a.causal ? a.T - a.L + 1 : a.T;
-  if (a.kv_bf16 && a.window > 0 && a.window < n) n = a.window;
+  if (a.window > 0 && a.window < n) n = a.window;
   return n;
 }
 

@@ -69,3 +69,16 @@ def prefill_side(xhat: np.ndarray, quantized_kv, qdtype) -> np.ndarray:
     if quantized_kv.bits == 8 and not quantized_kv.affine:
         return xhat
     return round_to(xhat, qdtype)
+
+
+def oracle_xhat(kv) -> np.ndarray:
+    """float32 x̂ of the valid rows of one quantized cache tensor, from its
+    stored bytes (int8 q·s, uint4 (q - z)·s, affine q·s + b)."""
+    codes, scales, extra = to_logical(kv)
+    if kv.affine:
+        c = codes.cpu().numpy()
+        if kv.bits == 4:
+            c = O.unpack_int4(c)
+        return O.dequantize_affine(c, f32(scales), f32(extra))
+    z = None if extra is None else extra.cpu().numpy()
+    return dequant(kv.bits, codes.cpu().numpy(), scales.cpu().numpy(), z)

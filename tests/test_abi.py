@@ -199,10 +199,10 @@ def test_capacity_bound(lib):
 
 
 def _prefill(lib, **kw):
-    a = dict(L=4, T=1000, cap=1024, splits=0, ws=16, wsb=1 << 30)
+    a = dict(L=4, T=1000, cap=1024, splits=0, ws=16, wsb=1 << 30, window=0)
     a.update(kw)
     return lib.rec_prefill_attn(
-        16, _lib.REC_BF16, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088, 1,
+        16, _lib.REC_BF16, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088, 1, a["window"],
         1, 8, 1, 128, a["L"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], 16, None,
     )
 
@@ -213,6 +213,8 @@ def test_prefill_split_validation(lib):
     assert _prefill(lib, splits=3, ws=None, wsb=0) == _lib.REC_EWORKSPACE
     assert _prefill(lib, splits=3, wsb=1024) == _lib.REC_EWORKSPACE
     assert _prefill(lib, splits=3, ws=8) == _lib.REC_EALIGN
+    assert _prefill(lib, window=-1) == _lib.REC_EINVAL
+    assert "window" in _lib.last_error()
 
 
 def test_prefill_workspace_bytes(lib):

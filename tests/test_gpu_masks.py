@@ -8,9 +8,10 @@ import pytest
 import torch
 
 import oracle as O
-from rec_amd import (FixedKVCache, KVStorage, QuantizedKVCache, quantized_attention_with_sinks,
-                     scaled_dot_product_attention, synthetic)
-from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize
+from rec_amd import (FixedKVCache, KVStorage, MixedQuantizedKVCache, QuantizedKVCache, attend,
+                     quantized_attention_with_sinks, scaled_dot_product_attention, synthetic)
+from tests.gpu_util import (SCALE, assert_cache_equal, assert_close, dequant, f32, oracle_quantize, oracle_xhat,
+                            prefill_side)
 
 pytestmark = pytest.mark.gpu
 
@@ -60,22 +61,70 @@ def test_decode_all_keys_mask_arrays(gpu):
             for m in (None, torch.ones((1, T), dtype=torch.bool, device="cuda"), torch.zeros((1, 1, 1, T), device="cuda"))]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     assert_close(f32(outs[0]), O.attention(f32(q), kh, vh, SCALE), "decode")
-    with pytest.raises(NotImplementedError):  # a window over a quantized cache at one query
-        quantized_attention_with_sinks(q, kq, vq, SCALE, torch.from_numpy(keep_pattern(1, T, 100)).cuda(), None,
-                                       32, 8, 4)
+    with pytest.raises(NotImplementedError):  # a window at one query runs on the matrix cores: bf16/f16 only
+        quantized_attention_with_sinks(q.float(), kq, vq, SCALE, torch.from_numpy(keep_pattern(1, T, 100)).cuda(),
+                                       None, 32, 8, 4)
 
 
-def test_uint4_prefill_window_mask(gpu):
-    """A sliding-window pattern over a 4-bit cache runs on the bf16 prefill's
-    window masking (the cache is dequantized to bf16 first)."""
-    L, T, W = 33, 500, 64
-    kq, vq, kh, vh = quantized_cache((4, 4), T, 31)
-    q = synthetic.query(1, 16, L, 32, dtype=torch.float16)
+WINDOW_FORMATS = {
+    "i8_i8": lambda: QuantizedKVCache(32, 8, 8),
+    "u4_u4": lambda: QuantizedKVCache(32, 4, 4),
+    "i8_u4": lambda: QuantizedKVCache(32, 8, 4),
+    "affine": lambda: MixedQuantizedKVCache(),
+}
+WINDOW_CASES = [
+    # format, L, T, window, splits (0 = automatic), query dtype
+    ("u4_u4", 33, 500, 64, 0, torch.float16),
+    ("i8_i8", 100, 2000, 300, 7, torch.bfloat16),   # splits before the window start stay empty
+    ("i8_u4", 40, 1500, 97, 0, torch.float16),
+    ("affine", 64, 1200, 200, 0, torch.bfloat16),
+    ("i8_i8", 64, 9000, 8500, 0, torch.bfloat16),   # every row sees > 8192 keys: the plain P·V
+    ("i8_i8", 1, 3000, 200, 0, torch.bfloat16),     # one query: the last 200 tokens
+    ("u4_u4", 1, 5000, 4000, 5, torch.float16),
+    ("affine", 1, 777, 33, 0, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", WINDOW_CASES, ids=lambda c: "{}_L{}_T{}_W{}_sp{}_{}".format(*c[:5], str(c[5])[6:]))
+def test_quantized_window_mask(gpu, case):
+    """A sliding-window pattern over a quantized cache runs on the prefill
+    kernel's own window masking, tiles dequantized on chip (one query too),
+    and matches the oracle under the same boolean array."""
+    fmt, L, T, W, splits, dtype = case
+    cache = WINDOW_FORMATS[fmt]()
+    k = synthetic.kv((1, 2, T, 128), 31 + W, kind="outliers", frac=0.02)
+    v = synthetic.kv((1, 2, T, 128), 32 + W, kind="outliers", frac=0.02)
+    kq, vq = cache.update_and_fetch(k, v)
+    q = synthetic.query(1, 16, L, 33 + L, dtype=dtype)
+    sinks = torch.randn(16, device="cuda")
     keep = keep_pattern(L, T, W)
-    out = quantized_attention_with_sinks(q, kq, vq, SCALE, torch.from_numpy(keep).cuda(), None, 32, 4, 4,
-                                         out_dtype=torch.float32)
-    ref = O.attention(f32(q), O.bf16_rn(kh), O.bf16_rn(vh), SCALE, None, keep)
-    assert_close(f32(out), ref, "window")
+    out = quantized_attention_with_sinks(q, kq, vq, SCALE, torch.from_numpy(keep).cuda(), sinks, cache.group_size,
+                                         cache.key_bits, cache.value_bits, out_dtype=torch.float32,
+                                         splits=splits or None)
+    torch.cuda.synchronize()
+    kh, vh = prefill_side(oracle_xhat(kq), kq, dtype), prefill_side(oracle_xhat(vq), vq, dtype)
+    ref = O.attention(f32(q), kh, vh, SCALE, f32(sinks), keep)
+    assert_close(f32(out), ref, f"{case}")
+
+
+def test_attend_one_query_window(gpu):
+    """attend() with one new token under a window pattern appends the token,
+    then attends over the last W cached tokens (the unfused path)."""
+    T, W = 1000, 150
+    cache = QuantizedKVCache(32, 8, 8)
+    k = synthetic.kv((1, 2, T + 1, 128), 51, kind="outliers", frac=0.02)
+    v = synthetic.kv((1, 2, T + 1, 128), 52, kind="outliers", frac=0.02)
+    cache.update_and_fetch(k[:, :, :T], v[:, :, :T])
+    q = synthetic.query(1, 16, 1, 53, dtype=torch.bfloat16)
+    keep = keep_pattern(1, T + 1, W)
+    out = attend(q, k[:, :, T:], v[:, :, T:], cache, SCALE, torch.from_numpy(keep).cuda(), None,
+                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert cache.offset == T + 1
+    kq, vq = cache.keys_and_values()
+    assert_cache_equal(kq, oracle_quantize(f32(k), 8))
+    ref = O.attention(f32(q), oracle_xhat(kq), oracle_xhat(vq), SCALE, None, keep)
+    assert_close(f32(out), ref, "attend window")
 
 
 def test_bf16_decode_window_mask(gpu):

@@ -5,8 +5,8 @@ before its attention (engine/src/rec_mlx/model.py:191-203); ``rec_prefill_attn``
 dequantizes each K/V tile into on-chip memory instead, 4-bit and affine values
 rounded to the query dtype, int8 codes exactly.
 
-* ``dequantize_kv`` (bf16 copies, ``rec_kv_dequant_bf16``, kept for callers and
-  for sliding-window masks) is bit-exact: bf16 round-to-nearest-even of the
+* ``dequantize_kv`` (bf16 copies, ``rec_kv_dequant_bf16``, kept for callers)
+  is bit-exact: bf16 round-to-nearest-even of the
   oracle's float32 x̂ (int8 q·s, uint4 (q - z)·s, affine q·s + b; every product
   is exact in float32, so one rounding in both);
 * the attention output lies within 2e-3 absolute + 1e-3 relative of the
@@ -18,8 +18,8 @@ import pytest
 import torch
 
 import oracle as O
-from rec_amd import MixedQuantizedKVCache, QuantizedKVCache, attend, dequantize_kv, synthetic, to_logical
-from tests.gpu_util import SCALE, assert_close, dequant, f32, prefill_side
+from rec_amd import MixedQuantizedKVCache, QuantizedKVCache, attend, dequantize_kv, synthetic
+from tests.gpu_util import SCALE, assert_close, f32, oracle_xhat, prefill_side
 
 pytestmark = pytest.mark.gpu
 
@@ -30,18 +30,6 @@ FORMATS = {
     "u4_i8": lambda: QuantizedKVCache(32, 4, 8),
     "affine": lambda: MixedQuantizedKVCache(),
 }
-
-
-def oracle_xhat(kv):
-    """float32 x̂ of the valid rows of one cache tensor, from its stored bytes."""
-    codes, scales, extra = to_logical(kv)
-    if kv.affine:
-        c = codes.cpu().numpy()
-        if kv.bits == 4:
-            c = O.unpack_int4(c)
-        return O.dequantize_affine(c, f32(scales), f32(extra))
-    z = None if extra is None else extra.cpu().numpy()
-    return dequant(kv.bits, codes.cpu().numpy(), scales.cpu().numpy(), z)
 
 
 def bits16(a):
