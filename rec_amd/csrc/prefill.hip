@@ -204,7 +204,10 @@ __device__ __forceinline__ void load_tile(TileRegs& R, const PrefillArgs& a, int
       const int per = r3 ? GEO::VZ_B : r2 ? GEO::VS_B : r1 ? GEO::KZ_B : GEO::KS_B;
       const int rel = off - start;
       const int bk = rel / per;
-      if (t0 + 32 * bk < t_end) R.sc = *(const v2i*)(base + (uint64_t)(blk0 * per + rel));
+      // a global-memory pointer: through a generic one this would be a flat
+      // load, which the LDS waits of the whole next tile would count too
+      typedef const __attribute__((address_space(1))) v2i global_v2i;
+      if (t0 + 32 * bk < t_end) R.sc = *(global_v2i*)(base + (uint64_t)(blk0 * per + rel));
     }
   }
 }
