@@ -283,7 +283,19 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   if constexpr (KB == 4 || VB == 4 || KB == FMT_A8 || VB == FMT_A4) {
     uint32_t* mw = (uint32_t*)meta;
     if constexpr (KB == 4 && VB == 4) {
-      *(v4i*)(meta + 16 * lane) = R.m4;  // array lane / 16, bytes 16 (lane % 16) ..
+      // lanes 48-63 carry the V zero-points, dword e of a run being the pair
+      // of unpack step e: the unpack's exponent offsets (1024 for even e, 64
+      // for odd) are added here once instead of per group in every lane
+      v4i m4 = R.m4;
+      const bool vz_lane = lane >= 48;
+      const v2h o_even = vz_lane ? (v2h){(_Float16)1024.0f, (_Float16)1024.0f} : (v2h){(_Float16)0.0f, (_Float16)0.0f};
+      const v2h o_odd = vz_lane ? (v2h){(_Float16)64.0f, (_Float16)64.0f} : (v2h){(_Float16)0.0f, (_Float16)0.0f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int x = m4[e];  // a copy: a bit_cast of a vector subscript reads element 0
+        m4[e] = __builtin_bit_cast(int, __builtin_bit_cast(v2h, x) + ((e & 1) ? o_odd : o_even));
+      }
+      *(v4i*)(meta + 16 * lane) = m4;  // array lane / 16, bytes 16 (lane % 16) ..
     } else if constexpr (KB == 4) {
       mw[lane] = R.m[0];
       mw[64 + lane] = R.m[1];
@@ -291,7 +303,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     if constexpr (KB == FMT_A8) mw[lane] = R.m[0];
     if constexpr (VB == 4 && KB != 4) {
       mw[128 + lane] = R.m[2];
-      mw[192 + lane] = R.m[3];
+      // the V zero-points with the unpack's exponent offset of their step e = lane % 4
+      const v2h off = (lane & 1) ? (v2h){(_Float16)64.0f, (_Float16)64.0f} : (v2h){(_Float16)1024.0f, (_Float16)1024.0f};
+      mw[192 + lane] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, R.m[3]) + off);
     }
     if constexpr (VB == FMT_A4) mw[128 + lane] = R.m[2];
     wave_lds_sync();
@@ -521,8 +535,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     // positions (e, e+4) of the lane's run as one fp16 pair: low nibbles under
     // the fp16 exponent of 1024 read 1024 + q, high nibbles under that of 64
     // read 64 + q.  Scales and zero-points are stored in that pair order
-    // (s4_slot), so dword e of a run is the pair for unpack step e.
-    const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+    // (s4_slot), so dword e of a run is the pair for unpack step e; the
+    // zero-points arrive here with that step's offset already added (z + 1024
+    // or z + 64, exact: z is a small integer), so one subtraction gives q - z.
     float p_lo[8];
 #pragma unroll
     for (int idx = 0; idx < 8; ++idx) p_lo[idx] = p[idx] * lo_sel;
@@ -543,10 +558,15 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
           pb[2 * e] = (_Float16)__builtin_fmaf(p[e], (float)sv[0], -(float)h0);
           pb[2 * e + 1] = (_Float16)__builtin_fmaf(p[e + 4], (float)sv[1], -(float)h1);
         } else {
-          pb[2 * e] = (_Float16)__builtin_fmaf(p[e], (float)sv[0], 0.f);
-          pb[2 * e + 1] = (_Float16)__builtin_fmaf(p[e + 4], (float)sv[1], 0.f);
+          // p·s rounded to fp16 once, into the two halves of one register
+          uint32_t w2;
+          asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(w2) : "v"(p[e]), "v"(sw));
+          asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(w2) : "v"(p[e + 4]), "v"(sw));
+          const v2h pp = __builtin_bit_cast(v2h, w2);
+          pb[2 * e] = pp[0];
+          pb[2 * e + 1] = pp[1];
         }
-        zq[e] = __builtin_bit_cast(v2h, zw) + ((e & 1) ? k64 : k1024);
+        zq[e] = __builtin_bit_cast(v2h, zw);  // z plus the unpack offset, added at the LDS hand-out
       }
 #pragma unroll
       for (int nn = 0; nn < 2; ++nn) {
