@@ -88,15 +88,32 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
   wave_lds_sync();
 
   // ---------------- scores (log2 domain: the query carries scale * log2 e) ----------------
+  // every LDS operand read of the chunk first -- the eight K operands, then
+  // the sixteen transposed V reads -- so that the matrix products wait for
+  // the LDS once and the V reads arrive behind the Q·Kᵀ and the softmax
+  v8bf ka[2][4], va[8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ka[j][ks] = *(const v8bf*)(kl + (16 * j + c) * KPITCH + 64 * ks + 16 * kg);
+  {
+    const int sk = (lane & 15) >> 2, sa = lane & 3;  // this lane addresses row 8kg + sk (+4), dims 16n + 4sa
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      typedef __attribute__((address_space(3))) v4bf lds_v4bf;
+      char* base = vl + (8 * kg + sk) * VPITCH + (16 * n + 4 * sa) * 2;
+      const v4bf r0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base));
+      const v4bf r1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base + 4 * VPITCH));
+      va[n] = (v8bf){r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float s[8];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     v4f d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const v8bf ka = *(const v8bf*)(kl + (16 * j + c) * KPITCH + 64 * ks + 16 * kg);
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qop[ks], d, 0, 0, 0);
-    }
+    for (int ks = 0; ks < 4; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[j][ks], qop[ks], d, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[4 * j + i] = d[i] + dpp_ror8f(d[i]);  // high part + low part
   }
@@ -131,17 +148,9 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
     pb[idx] = c < 8 ? hi : (__bf16)(p - (float)hi);
   }
 
-  // ---------------- P·V: Vᵀ operands by transposed LDS reads ----------------
-  const int sk = (lane & 15) >> 2, sa = lane & 3;  // this lane addresses row 8kg + sk (+4), dims 16n + 4sa
+  // ---------------- P·V: the Vᵀ operands read above ----------------
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    typedef __attribute__((address_space(3))) v4bf lds_v4bf;
-    char* base = vl + (8 * kg + sk) * VPITCH + (16 * n + 4 * sa) * 2;
-    const v4bf r0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base));
-    const v4bf r1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base + 4 * VPITCH));
-    const v8bf a = {r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
-    st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, st.acc[n], 0, 0, 0);
-  }
+  for (int n = 0; n < 8; ++n) st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[n], pb, st.acc[n], 0, 0, 0);
   wave_lds_sync();  // the next chunk's staging overwrites these rows (K and V)
 }
 
