@@ -384,6 +384,13 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
+    if queries.dtype not in (torch.bfloat16, torch.float16):
+        # chunks, and a single query under a window over a quantized cache,
+        # run on the matrix cores: refused here, before the append changes
+        # the cache
+        quantized = not isinstance(cache, (FixedSlidingKVCache, FixedKVCache))
+        if L > 1 or (quantized and mask is not None and _mask_plan(mask, 1, cache.offset + 1)[1]):
+            raise NotImplementedError("prefill (and windowed) queries must be bf16 or f16 (the matrix-core input type)")
     if isinstance(cache, FixedSlidingKVCache):
         # a new token goes to its ring slot and decode attends over the valid
         # slots (order-free); a chunk attends over the ring in order plus

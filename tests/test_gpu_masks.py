@@ -127,6 +127,25 @@ def test_attend_one_query_window(gpu):
     assert_close(f32(out), ref, "attend window")
 
 
+def test_attend_refuses_f32_matrix_core_queries_before_append(gpu):
+    """A float32 chunk, or one float32 query under a window over a quantized
+    cache, is refused before the new tokens touch the cache."""
+    cache = QuantizedKVCache(32, 8, 8)
+    k = synthetic.kv((1, 2, 103, 128), 61)
+    v = synthetic.kv((1, 2, 103, 128), 62)
+    cache.update_and_fetch(k[:, :, :100], v[:, :, :100])
+    q3 = synthetic.query(1, 16, 3, 63, dtype=torch.float32)
+    with pytest.raises(NotImplementedError):
+        attend(q3, k[:, :, 100:], v[:, :, 100:], cache, SCALE, "causal")
+    assert cache.offset == 100
+    q1 = synthetic.query(1, 16, 1, 64, dtype=torch.float32)
+    with pytest.raises(NotImplementedError):
+        attend(q1, k[:, :, 100:101], v[:, :, 100:101], cache, SCALE, torch.from_numpy(keep_pattern(1, 101, 50)).cuda())
+    assert cache.offset == 100
+    out = attend(q1, k[:, :, 100:101], v[:, :, 100:101], cache, SCALE, "causal", out_dtype=torch.float32)
+    assert cache.offset == 101 and torch.isfinite(out).all()
+
+
 def test_bf16_decode_window_mask(gpu):
     """One query over a bf16 cache with a window pattern attends over the last W keys."""
     T, W = 1000, 129
