@@ -819,6 +819,18 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
   const int qb = p / PF_ROWS, r = p - qb * PF_ROWS;
   const int64_t bh = (int64_t)b * a.Hkv + h;
   const auto row = [&](int sp) { return ((bh * a.S + sp) * a.nqb + qb) * PF_ROWS + r; };
+  // every load first -- the splits' partial rows and their statistics -- so
+  // that the merge waits for memory once (slots past the last split read its
+  // row again and weigh it 0).  The rows of one (query, head) are a fixed
+  // stride apart: each load takes its split's offset as a scalar, so the 64
+  // addresses cost no vector instructions.
+  const uint32_t step_b = (uint32_t)a.nqb * PF_ROWS * HEAD_DIM * 4;  // bytes between consecutive splits' rows
+  const uint32_t last_b = (uint32_t)(a.S - 1) * step_b;              // below 2^31 (prefill_plan)
+  const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.ws_acc + row(0) * HEAD_DIM, (int64_t)last_b + HEAD_DIM * 4);
+  v2f x[16 * NR];
+#pragma unroll
+  for (int k = 0; k < 16 * NR; ++k)
+    x[k] = __builtin_bit_cast(v2f, ld64<0>(racc, 8 * lane, (uint32_t)min(k, a.S - 1) * step_b));
   float m = NEG_INF, l = 0.f;
   if (lane < a.S) {
     const v2f st = *(const v2f*)(a.ws_stat + row(lane) * 2);
@@ -832,10 +844,6 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
   if (sink != NEG_INF) z += __builtin_amdgcn_exp2f(sink - M);
   wts[lane] = f;  // 0 for lanes past the last split
   __syncthreads();
-  // slots past the last split read its row again and weigh it 0
-  v2f x[16 * NR];
-#pragma unroll
-  for (int k = 0; k < 16 * NR; ++k) x[k] = *(const v2f*)(a.ws_acc + row(min(k, a.S - 1)) * HEAD_DIM + 2 * lane);
   v2f acc = {0.f, 0.f};
 #pragma unroll
   for (int k = 0; k < 16 * NR; ++k) acc += wts[k] * x[k];
@@ -861,6 +869,10 @@ PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
   }
   S = std::max(1, std::min(S, PREFILL_MAX_SPLITS));
   S = (int)std::min<int64_t>(S, std::max<int64_t>(1, tiles));
+  // the merge addresses one row's partials with 32-bit offsets from its first
+  // split: (S - 1) strides of nqb * 256 rows of 512 bytes stay below 2^31
+  const int64_t stride_b = (int64_t)p.nqb * PF_ROWS * HEAD_DIM * 4;
+  S = (int)std::min<int64_t>(S, 1 + (((int64_t)1 << 31) - 1 - HEAD_DIM * 4) / stride_b);
   const int64_t per = (tiles + S - 1) / S;  // tiles per split
   p.S = (int)((tiles + per - 1) / per);
   p.split_lo = lo;
