@@ -16,7 +16,7 @@ import tempfile
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "librec_amd.so")
-SOURCES = ["abi.hip", "append.hip", "decode.hip", "decode_bf16.hip", "gemv.hip", "prefill.hip"]
+SOURCES = ["abi.hip", "append.hip", "decode.hip", "decode_bf16.hip", "gemv.hip", "prefill.hip", "prefill_few.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -142,6 +142,12 @@ hipError_t launch_stream_read(const void* p, int64_t n16, int workgroups, uint32
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both kernels when a.S > 1
+// A few queries over the int8 cache (at most this many (query, head) rows
+// per KV head, no window): the streaming kernel of prefill_few.hip, whose
+// partials share the tiled kernel's workspace layout and merge
+constexpr int PREFILL_FEW_ROWS = 32;
+bool prefill_few_fits(const PrefillArgs& a);
+hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stream);
 hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream);

@@ -920,7 +920,10 @@ static int64_t fewest_visible_keys(const PrefillArgs& a) {
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)(a.nqb * a.S), a.Hkv, a.B), block(512);
   const bool exact = fewest_visible_keys(a) < EXACT_PV_BELOW;
-  if (a.q_dtype == DT_BF16) {
+  if (prefill_few_fits(a)) {
+    const hipError_t e = launch_prefill_few(a, stream);
+    if (e != hipSuccess) return e;
+  } else if (a.q_dtype == DT_BF16) {
     if (exact) launch_formats<true, true>(a, grid, block, stream);
     else launch_formats<true, false>(a, grid, block, stream);
   } else {

@@ -1,0 +1,325 @@
+// Chunked prefill of a few queries over the int8 cache: the decode's
+// streaming structure with the chunk's (query, head) rows as matrix columns.
+//
+// Restates the same branch as prefill.hip (engine/src/rec_mlx/model.py:191-203:
+// the L new tokens are cached first, then their queries attend over the whole
+// cache with the causal mask of model.py:122-125 and the per-head sinks).
+// For a short chunk -- a few draft tokens, a short turn -- the tiled prefill
+// kernel spends each 128-token tile's conversion, LDS staging and barriers on
+// 16-row tiles that are mostly empty; here, as in the decode, every wave
+// streams its 32-token chunks from HBM into registers and the tile is never
+// staged.  The L·G <= 16·NT (query, head) rows of one KV head, numbered
+// query·G + head as in prefill.hip, fill NT column tiles of 16:
+//   * Q·Kᵀ on 16x16x32 bf16 (fp16 for fp16 queries) MFMAs: A = 16 tokens x 32
+//     dims of the int8 K block converted in registers (exact), B = the rows'
+//     query elements of the same dims (a lane holds dims 64m + 16kg + 8h ..
+//     +7 for k-step 2m + h, the order the int8 block hands its bytes out);
+//   * online softmax per column with the decode's lazy running max, the K
+//     row scale and the softmax scale applied to the fp32 scores;
+//   * P·V on 16x16x32 fp16 MFMAs: A = Vᵀ (int8 codes, exact in fp16), B =
+//     P' = p·s (the token's V scale) as an fp16 high part and its rounding
+//     remainder, one MFMA each.
+// Work decomposition: grid (splits, Hkv, B) with the prefill's split plan
+// (128-token aligned ranges), 4 waves taking 32-token chunks in turn, a
+// 2-deep ring of loads.  Each workgroup merges its waves in LDS and writes
+// the normalised output (one split) or its unnormalised partial in the
+// prefill workspace layout, which prefill_merge_kernel combines.
+#include "kernels.h"
+
+namespace rec {
+namespace {
+
+constexpr int FW = 4;        // wavefronts per workgroup
+constexpr int FCH = 32;      // tokens per chunk (one cache block)
+constexpr int FPR = HEAD_DIM + 4;  // LDS row pitch of a wave partial (floats)
+
+template <bool BF16>
+struct FewT;
+template <>
+struct FewT<true> {
+  typedef v8bf vec;
+  static __device__ __forceinline__ v4f mfma(vec a, vec b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // eight int8 codes (two dwords) -> bf16, exactly
+  static __device__ __forceinline__ vec codes(uint32_t w0, uint32_t w1) {
+    vec r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[e] = (__bf16)(float)(int8_t)(w0 >> (8 * e));
+      r[4 + e] = (__bf16)(float)(int8_t)(w1 >> (8 * e));
+    }
+    return r;
+  }
+};
+template <>
+struct FewT<false> {
+  typedef v8h vec;
+  static __device__ __forceinline__ v4f mfma(vec a, vec b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ vec codes(uint32_t w0, uint32_t w1) { return i8x8_to_h8(w0, w1); }
+};
+
+// One chunk's registers as they arrive: K block bytes of tile j (tokens 16j +
+// c), dims 64m + 16kg .. +15; V dims 16n + c at block positions 8kg .. +7
+// (n = 2h, 2h+1 in v[h]); the K and V scales of positions 8kg .. 8kg+7.
+struct FewChunk {
+  v4i k[2][2];
+  v4i v[4];
+  v4i ks, vs;
+};
+
+__device__ __forceinline__ void few_load(FewChunk& R, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                         __amdgpu_buffer_rsrc_t rks, __amdgpu_buffer_rsrc_t rvs,
+                                         __amdgpu_buffer_rsrc_t none, bool ok, uint32_t blk, int c, int kg) {
+  const __amdgpu_buffer_rsrc_t a = ok ? rk : none, b = ok ? rv : none, sa = ok ? rks : none, sb = ok ? rvs : none;
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int m = 0; m < 2; ++m) R.k[j][m] = ld128(a, (uint32_t)((16 * j + c) * 64 + 16 * kg + 2048 * m), blk * 4096);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 4096);
+  R.ks = ld128(sa, (uint32_t)(16 * kg), blk * 64);
+  R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
+}
+
+template <bool BF16, int NT>
+__global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs a) {
+  typedef typename FewT<BF16>::vec V8;
+  constexpr int NC = 16 * NT;  // (query, head) columns of the workgroup
+  __shared__ __attribute__((aligned(16))) float part[FW][NC][FPR];
+  __shared__ float pstat[FW][NC][2];
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, kg = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * a.Hkv + h;
+  const int rows = a.L * a.G;  // valid columns
+  const int P = (int)(a.T - a.L);
+  const int64_t s_lo = a.split_lo + (int64_t)split * a.split_len;
+  const int lo = __builtin_amdgcn_readfirstlane((int)s_lo);
+  const int t_end = __builtin_amdgcn_readfirstlane((int)min(a.T, s_lo + a.split_len));
+
+  // ---- the columns' query operands and causal limits ----
+  V8 qop[NT][4];
+  int qpos[NT];  // last visible token of the lane's column (causal), or past every token
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int p = 16 * t + c;
+    const bool valid = p < rows;
+    const int qi = valid ? p / a.G : 0, hq = h * a.G + (valid ? p - qi * a.G : 0);
+    qpos[t] = (valid && a.causal) ? P + qi : INT32_MAX;
+    const uint16_t* row = (const uint16_t*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)qi * a.q_st;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int d0 = 64 * (ks >> 1) + 16 * kg + 8 * (ks & 1);
+      v8s e = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (valid) {
+        if (a.q_vec) {
+          e = __builtin_bit_cast(v8s, *(const v4i*)(row + d0));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) e[i] = (short)row[d0 + i];
+        }
+      }
+      qop[t][ks] = __builtin_bit_cast(V8, e);
+    }
+  }
+
+  // ---- resources of this (b, h) slice ----
+  const int64_t cap = a.cap;
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const int8_t*)a.kq + bh * cap * HEAD_DIM, cap * HEAD_DIM);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const int8_t*)a.vq + bh * cap * HEAD_DIM, cap * HEAD_DIM);
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(a.ks + bh * cap, cap * 2);
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(a.vs + bh * cap, cap * 2);
+  const __amdgpu_buffer_rsrc_t none = make_rsrc(a.ks, 0);
+
+  // ---- softmax state per column (log2 domain) ----
+  // The running max starts at a finite floor, not -inf: a chunk whose tokens
+  // all lie past a column's causal limit then gives p = exp2(-inf) = 0 for it
+  // and no rescale, even as the wave's first chunk.
+  constexpr float M_FLOOR = -1e30f;
+  float m_run[NT], l_run[NT];
+  v4f acc[NT][8];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    m_run[t] = M_FLOOR;
+    l_run[t] = 0.f;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) acc[t][n] = (v4f){0.f, 0.f, 0.f, 0.f};
+  }
+
+  const auto process = [&](const FewChunk& R, int t0) {
+    // Q·Kᵀ: lane (c, kg) receives the scores of column c for tokens 16j + 4kg + i
+    v4f s4[NT][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      V8 ka[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const v4i w = R.k[j][ks >> 1];
+        ka[ks] = FewT<BF16>::codes((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1]);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        v4f d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) d = FewT<BF16>::mfma(ka[ks], qop[t][ks], d);
+        s4[t][j] = d;
+      }
+    }
+    // the K row scale times the softmax scale, and the V scale, of the lane's 8 positions
+    float ksm[8], vsf[8];
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) {
+      ksm[idx] = half_at(R.ks, idx) * a.q_mul;
+      vsf[idx] = half_at(R.vs, idx);
+    }
+    // Range (as in the decode): a V scale of 2 or more among the lane's
+    // positions makes its bound 0, so p <= 1 and P' = p·s stays finite in fp16
+    const bool big = ((uint32_t)(R.vs[0] | R.vs[1] | R.vs[2] | R.vs[3]) & 0x40004000u) != 0;
+    const float gap = big ? 0.f : RESCALE_GAP;
+    // tokens past the split end or past a column's causal limit: only the
+    // chunks at the end of the range (uniform test)
+    const bool edge = t0 + FCH > t_end || t0 + FCH - 1 > P;
+    v8h pb[NT], pl[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * j + i] = s4[t][j][i] * ksm[4 * j + i];
+      if (edge) {
+        const int last = min(qpos[t], t_end - 1) - t0 - 4 * kg;  // last visible token, relative
+#pragma unroll
+        for (int idx = 0; idx < 8; ++idx)
+          if (16 * (idx >> 2) + (idx & 3) > last) x[idx] = NEG_INF;
+      }
+      float cmax = x[0];
+#pragma unroll
+      for (int idx = 1; idx < 8; ++idx) cmax = maxp(cmax, x[idx]);
+      if (__ballot(cmax > m_run[t] + gap)) {
+        cmax = max_xor32(max_xor16(cmax));  // the column's max over its four lanes
+        const float m_new = fmaxf(m_run[t], cmax);
+        const float f = __builtin_amdgcn_exp2f(m_run[t] - m_new);
+        l_run[t] *= f;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) acc[t][n] *= f;
+        m_run[t] = m_new;
+      }
+#pragma unroll
+      for (int idx = 0; idx < 8; idx += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(x[idx] - m_run[t]);
+        const float p1 = __builtin_amdgcn_exp2f(x[idx + 1] - m_run[t]);
+        l_run[t] += p0 + p1;
+        // P' = p·s rounded to fp16 once, then its remainder
+        uint32_t w;
+        asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(w) : "v"(p0), "v"(vsf[idx]));
+        asm("v_fma_mixhi_f16 %0, %1, %2, 0" : "+v"(w) : "v"(p1), "v"(vsf[idx + 1]));
+        const v2h hh = __builtin_bit_cast(v2h, w);
+        pb[t][idx] = hh[0];
+        pb[t][idx + 1] = hh[1];
+        pl[t][idx] = (_Float16)__builtin_fmaf(p0, vsf[idx], -(float)hh[0]);
+        pl[t][idx + 1] = (_Float16)__builtin_fmaf(p1, vsf[idx + 1], -(float)hh[1]);
+      }
+    }
+    // P·V
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const v8h va = i8x8_to_h8((uint32_t)R.v[n >> 1][2 * (n & 1)], (uint32_t)R.v[n >> 1][2 * (n & 1) + 1]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t], acc[t][n], 0, 0, 0);
+        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[t], acc[t][n], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- the wave's chunks w, w + 4, ... of [lo, t_end), a 2-deep ring ----
+  const int n_chunks = (t_end - lo + FCH - 1) / FCH;
+  const int n_w = n_chunks > wave ? (n_chunks - wave + FW - 1) / FW : 0;
+  const uint32_t blk0 = (uint32_t)(lo / FCH + wave);
+  FewChunk buf[2];
+  few_load(buf[0], rk, rv, rks, rvs, none, 0 < n_w, blk0, c, kg);
+  const int n_pad = (n_w + 1) / 2 * 2;
+  for (int i0 = 0; i0 < n_pad; i0 += 2) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = i0 + j;
+      few_load(buf[(j + 1) & 1], rk, rv, rks, rvs, none, i + 1 < n_w, blk0 + FW * (i + 1), c, kg);
+      if (i < n_w) process(buf[j], (int)(blk0 + FW * i) * FCH);
+    }
+  }
+
+  // ---- wave partials -> LDS ----
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const float l = sum_xor32(sum_xor16(l_run[t]));
+#pragma unroll
+    for (int n = 0; n < 8; ++n) *(v4f*)&part[wave][16 * t + c][16 * n + 4 * kg] = acc[t][n];
+    if (kg == 0) {
+      pstat[wave][16 * t + c][0] = m_run[t];
+      pstat[wave][16 * t + c][1] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- workgroup merge: thread (column, 4 dims) items ----
+  for (int it = tid; it < rows * 32; it += 64 * FW) {
+    const int p = it >> 5, d0 = 4 * (it & 31);
+    float mw[FW], M = M_FLOOR;
+#pragma unroll
+    for (int w = 0; w < FW; ++w) {
+      mw[w] = pstat[w][p][0];
+      M = fmaxf(M, mw[w]);
+    }
+    v4f o = {0.f, 0.f, 0.f, 0.f};
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < FW; ++w) {
+      const float f = __builtin_amdgcn_exp2f(mw[w] - M);
+      o += f * *(const v4f*)&part[w][p][d0];
+      l += f * pstat[w][p][1];
+    }
+    const int qi = p / a.G, hq = h * a.G + (p - qi * a.G);
+    if (a.S == 1) {
+      if (a.sinks != nullptr) {
+        const float sink = a.sinks[hq] * LOG2E;
+        const float Mn = fmaxf(M, sink);
+        const float f = __builtin_amdgcn_exp2f(M - Mn);
+        l = l * f + __builtin_amdgcn_exp2f(sink - Mn);
+        o *= f;
+      }
+      const v4f r = l > 0.f ? o * (1.f / l) : o;
+      *(v4f*)(a.out + (((int64_t)b * a.Hq + hq) * a.L + qi) * HEAD_DIM + d0) = r;
+    } else {
+      // no visible key in this split: (-inf, 0, 0), as the tiled kernel writes
+      const int64_t row = (((int64_t)bh * a.S + split) * a.nqb) * PREFILL_BLOCK_ROWS + p;
+      *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = o;
+      if (d0 == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){l > 0.f ? M : NEG_INF, l};
+    }
+  }
+}
+
+template <bool BF16>
+static void launch_nt(const PrefillArgs& a, int nt, dim3 grid, hipStream_t stream) {
+  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, 1>), grid, dim3(64 * FW), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_few_kernel<BF16, 2>), grid, dim3(64 * FW), 0, stream, a);
+}
+
+}  // namespace
+
+bool prefill_few_fits(const PrefillArgs& a) {
+  return a.k_fmt == 8 && a.v_fmt == 8 && a.window == 0 && a.L * a.G <= PREFILL_FEW_ROWS;
+}
+
+hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
+  const dim3 grid((unsigned)a.S, a.Hkv, a.B);
+  const int nt = (a.L * a.G + 15) / 16;
+  if (a.q_dtype == DT_BF16) launch_nt<true>(a, nt, grid, stream);
+  else launch_nt<false>(a, nt, grid, stream);
+  return hipGetLastError();
+}
+
+}  // namespace rec

@@ -1,0 +1,70 @@
+"""Parity of the few-query prefill path (prefill_few.hip) with the CPU oracle.
+
+Chunks of at most 32 (query, head) rows per KV head over an int8 cache run on
+the streaming kernel instead of the tiled one; the outputs must lie within
+2e-3 absolute + 1e-3 relative of the oracle, as the tiled kernel's do, for
+causal and full masks, sinks, GQA ratios 1 to 8, bf16 and fp16 queries, key
+splits (automatic, explicit, one) and ranges whose last chunk lies wholly past
+some queries' causal limits.
+"""
+
+import pytest
+import torch
+
+import oracle as O
+from rec_amd import QuantizedKVCache, attend, synthetic
+from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # B, Hq, Hkv, P, L, causal, sinks, dtype, splits (0 = automatic)
+    (1, 32, 4, 5000, 4, True, True, torch.bfloat16, 0),     # 32 rows: two column tiles
+    (1, 32, 4, 65536, 2, True, True, torch.bfloat16, 0),    # a long cache, 64 splits
+    (2, 8, 2, 300, 7, True, False, torch.float16, 0),       # 28 rows, two sequences
+    (1, 4, 4, 1000, 16, True, True, torch.bfloat16, 0),     # one head per KV head, 16 queries
+    (1, 8, 1, 33, 3, False, True, torch.bfloat16, 5),       # full attention, explicit splits
+    (1, 16, 2, 31, 4, True, True, torch.float16, 0),        # the chunk at 32 lies past query 0's limit
+    (1, 8, 1, 62, 3, True, True, torch.bfloat16, 1),        # unsplit, last chunk partly masked
+    (3, 12, 4, 1500, 9, True, True, torch.bfloat16, 0),     # 27 rows, three sequences
+    (1, 24, 8, 4096, 10, True, False, torch.float16, 7),    # 30 rows, G = 3
+    (1, 8, 1, 130, 2, True, True, torch.float16, 3),        # splits past the causal end stay empty
+]
+
+
+@pytest.mark.parametrize("case", CASES,
+                         ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_causal{}_s{}_{}_sp{}".format(*c[:7], str(c[7])[6:], c[8]))
+def test_few_query_prefill_matches_oracle(gpu, case):
+    B, Hq, Hkv, P, L, causal, with_sinks, dtype, splits = case
+    assert L * (Hq // Hkv) <= 32
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 71 + T, kind="outliers", frac=0.01)
+    v = synthetic.kv((B, Hkv, T, 128), 72 + T, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, L, 73 + L, dtype=dtype)
+    sinks = torch.randn(Hq, device="cuda") if with_sinks else None
+    cache = QuantizedKVCache(32, 8, 8)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    mask = "causal" if causal else None
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32,
+                 splits=splits or None)
+    torch.cuda.synchronize()
+    rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
+    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None if sinks is None else f32(sinks), mask)
+    assert_close(f32(out), ref, f"case {case}")
+
+
+def test_few_query_prefill_large_v_scale(gpu):
+    """V rows with |v| in the thousands (int8 scales of 2 or more): the
+    probabilities stay at most 1 for those tokens, so P' = p·s stays finite."""
+    B, Hq, Hkv, P, L = 1, 16, 2, 700, 4
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 81)
+    v = synthetic.kv((B, Hkv, T, 128), 82) * 3000.0
+    q = synthetic.query(B, Hq, L, 83, dtype=torch.bfloat16)
+    cache = QuantizedKVCache(32, 8, 8)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, "causal", None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
+    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None, "causal")
+    assert_close(f32(out), ref, "large V")
