@@ -874,12 +874,14 @@ def main(argv=None):
     if not args.no_gemv:
         rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
 
-    rpf = rpf_short = None
+    rpf = rpf_short = rpf_few = None
     rpf_fmt = {}
     if not args.no_prefill:
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
         # a short chunk over a long cache (a new chat turn): the keys are split
         rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
+        # four draft tokens over a long cache: the streaming few-query kernel
+        rpf_few = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 54)
         # the same long chunk over the 4-bit, affine and bf16 caches
         for i, fmt in enumerate(("uint4", "affine", "bf16")):
             rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
@@ -1030,6 +1032,8 @@ def main(argv=None):
         result["prefill_65536_plus_2048"] = rpf
     if rpf_short is not None:
         result["prefill_32768_plus_20"] = rpf_short
+    if rpf_few is not None:
+        result["prefill_65536_plus_4"] = rpf_few
     for fmt, r in rpf_fmt.items():
         result[f"prefill_65536_plus_2048_{fmt}"] = r
     if floor is not None:

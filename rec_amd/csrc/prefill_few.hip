@@ -17,8 +17,9 @@
 //   * online softmax per column with the decode's lazy running max, the K
 //     row scale and the softmax scale applied to the fp32 scores;
 //   * P·V on 16x16x32 fp16 MFMAs: A = Vᵀ (int8 codes, exact in fp16), B =
-//     P' = p·s (the token's V scale) as an fp16 high part and its rounding
-//     remainder, one MFMA each.
+//     P' = p·s (the token's V scale) as an fp16 high part and, when the first
+//     query sees fewer than EXACT_PV_BELOW keys, its rounding remainder in a
+//     second MFMA (as the tiled kernel does).
 // Work decomposition: grid (splits, Hkv, B) with the prefill's split plan
 // (128-token aligned ranges), 4 waves taking 32-token chunks in turn, a
 // 2-deep ring of loads.  Each workgroup merges its waves in LDS and writes
@@ -84,7 +85,7 @@ __device__ __forceinline__ void few_load(FewChunk& R, __amdgpu_buffer_rsrc_t rk,
   R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
 }
 
-template <bool BF16, int NT>
+template <bool BF16, int NT, bool EXACT>
 __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs a) {
   typedef typename FewT<BF16>::vec V8;
   constexpr int NC = 16 * NT;  // (query, head) columns of the workgroup
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     // tokens past the split end or past a column's causal limit: only the
     // chunks at the end of the range (uniform test)
     const bool edge = t0 + FCH > t_end || t0 + FCH - 1 > P;
-    v8h pb[NT], pl[NT];
+    v8h pb[NT], pl[NT];  // pl: EXACT only
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       float x[8];
@@ -213,15 +214,17 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
         const float p0 = __builtin_amdgcn_exp2f(x[idx] - m_run[t]);
         const float p1 = __builtin_amdgcn_exp2f(x[idx + 1] - m_run[t]);
         l_run[t] += p0 + p1;
-        // P' = p·s rounded to fp16 once, then its remainder
+        // P' = p·s rounded to fp16 once (and, EXACT, its remainder)
         uint32_t w;
         asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(w) : "v"(p0), "v"(vsf[idx]));
         asm("v_fma_mixhi_f16 %0, %1, %2, 0" : "+v"(w) : "v"(p1), "v"(vsf[idx + 1]));
         const v2h hh = __builtin_bit_cast(v2h, w);
         pb[t][idx] = hh[0];
         pb[t][idx + 1] = hh[1];
-        pl[t][idx] = (_Float16)__builtin_fmaf(p0, vsf[idx], -(float)hh[0]);
-        pl[t][idx + 1] = (_Float16)__builtin_fmaf(p1, vsf[idx + 1], -(float)hh[1]);
+        if constexpr (EXACT) {
+          pl[t][idx] = (_Float16)__builtin_fmaf(p0, vsf[idx], -(float)hh[0]);
+          pl[t][idx + 1] = (_Float16)__builtin_fmaf(p1, vsf[idx + 1], -(float)hh[1]);
+        }
       }
     }
     // P·V
@@ -231,7 +234,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t], acc[t][n], 0, 0, 0);
-        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[t], acc[t][n], 0, 0, 0);
+        if constexpr (EXACT) acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[t], acc[t][n], 0, 0, 0);
       }
     }
   };
@@ -302,10 +305,10 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   }
 }
 
-template <bool BF16>
+template <bool BF16, bool EXACT>
 static void launch_nt(const PrefillArgs& a, int nt, dim3 grid, hipStream_t stream) {
-  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, 1>), grid, dim3(64 * FW), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_few_kernel<BF16, 2>), grid, dim3(64 * FW), 0, stream, a);
+  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, 1, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_few_kernel<BF16, 2, EXACT>), grid, dim3(64 * FW), 0, stream, a);
 }
 
 }  // namespace
@@ -317,8 +320,15 @@ bool prefill_few_fits(const PrefillArgs& a) {
 hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)a.S, a.Hkv, a.B);
   const int nt = (a.L * a.G + 15) / 16;
-  if (a.q_dtype == DT_BF16) launch_nt<true>(a, nt, grid, stream);
-  else launch_nt<false>(a, nt, grid, stream);
+  // the first query sees the fewest keys; from EXACT_PV_BELOW on, P' in one fp16 part
+  const bool exact = (a.causal ? a.T - a.L + 1 : a.T) < EXACT_PV_BELOW;
+  if (a.q_dtype == DT_BF16) {
+    if (exact) launch_nt<true, true>(a, nt, grid, stream);
+    else launch_nt<true, false>(a, nt, grid, stream);
+  } else {
+    if (exact) launch_nt<false, true>(a, nt, grid, stream);
+    else launch_nt<false, false>(a, nt, grid, stream);
+  }
   return hipGetLastError();
 }
 
