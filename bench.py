@@ -593,6 +593,62 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
     )
 
 
+def run_sliding(steps, seed, window=513, held=4096, chunk=512):
+    """A sliding-window layer (FixedSlidingKVCache, the reference's 513-token
+    window, bf16 ring): one decode step (token written into its ring slot,
+    attention over the window) and one 512-token chunk (written into the ring,
+    attending over the window in order plus itself under the causal window
+    mask), each through attend() in a graph of `steps` calls.  Every replay
+    writes the same slots, so every call does identical work."""
+    import torch
+
+    import rec_amd
+    from rec_amd import synthetic
+
+    c = rec_amd.FixedSlidingKVCache(max_sequence_tokens=held + 2 * chunk, num_kv_heads=HKV, head_dim=D,
+                                    window_size=window)
+    k = synthetic.kv((1, HKV, held, D), seed, dtype=torch.bfloat16)
+    v = synthetic.kv((1, HKV, held, D), seed + 1, dtype=torch.bfloat16)
+    for a in range(0, held, chunk):
+        c.update_and_fetch(k[:, :, a:a + chunk], v[:, :, a:a + chunk])
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    sinks = torch.randn(HQ, generator=g, device="cuda")
+    q1 = synthetic.query(1, HQ, 1, seed + 2, dtype=torch.bfloat16)
+    k1 = synthetic.kv((1, HKV, 1, D), seed + 3, dtype=torch.bfloat16)
+    v1 = synthetic.kv((1, HKV, 1, D), seed + 4, dtype=torch.bfloat16)
+    qc = synthetic.query(1, HQ, chunk, seed + 5, dtype=torch.bfloat16)
+    kc = synthetic.kv((1, HKV, chunk, D), seed + 6, dtype=torch.bfloat16)
+    vc = synthetic.kv((1, HKV, chunk, D), seed + 7, dtype=torch.bfloat16)
+    out = {}
+    # the library keeps one workspace per stream: a first call on the capture
+    # stream, outside the capture, allocates it there, so the graph reuses it
+    cap_stream = torch.cuda.Stream()
+    for name, (q, kk, vv) in (("decode", (q1, k1, v1)), ("chunk", (qc, kc, vc))):
+        call = lambda: rec_amd.attend(q, kk, vv, c, SCALE, None, sinks)  # noqa: E731
+        cap_stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap_stream):
+            call()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap_stream):
+            for _ in range(steps):
+                call()
+        out[name] = _median_timed(torch, graph, steps) * 1e3
+        del graph
+    log(f"sliding window {window}: decode step {out['decode']:.2f} us, {chunk}-token chunk {out['chunk']:.2f} us")
+    return dict(
+        window=window,
+        decode_step_us=round(out["decode"], 3),
+        chunk_tokens=chunk,
+        chunk_us=round(out["chunk"], 3),
+        note="FixedSlidingKVCache (bf16 ring, 513-token window as the reference's sliding layers), through "
+             "attend(): decode = token write + attention over the window + merge; chunk = 512 tokens written "
+             "into the ring, then attention over the window in order plus the chunk under the causal window mask; "
+             "both latency-bound (the window is 513 tokens)",
+    )
+
+
 def run_sdpa_yardstick(P, L, steps):
     """A library yardstick for the prefill, not this build's kernel: PyTorch's
     own fused attention (torch.nn.functional.scaled_dot_product_attention,
@@ -796,6 +852,7 @@ def main(argv=None):
     ap.add_argument("--prefill-steps", type=int, default=6)
     ap.add_argument("--no-floor", action="store_true", help="skip the plain streaming-read floor")
     ap.add_argument("--no-yardstick", action="store_true", help="skip timing PyTorch's own fused attention")
+    ap.add_argument("--no-sliding", action="store_true", help="skip the sliding-window layer measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--seed", type=int, default=1234)
@@ -887,6 +944,13 @@ def main(argv=None):
             rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
         if not args.no_yardstick:
             rpf["library_yardstick"] = run_sdpa_yardstick(65536, 2048, args.prefill_steps)
+
+    sliding = None
+    if not args.no_bf16 and not args.no_sliding:
+        try:
+            sliding = run_sliding(max(10, args.steps // 20), args.seed + 61)
+        except Exception as e:  # a measurement beside the headline; the line is printed without it
+            log(f"sliding-window measurement failed: {e}")
 
     floor = None if args.no_floor else run_read_floor(max(20, args.steps // 5))
 
@@ -1036,6 +1100,8 @@ def main(argv=None):
         result["prefill_65536_plus_4"] = rpf_few
     for fmt, r in rpf_fmt.items():
         result[f"prefill_65536_plus_2048_{fmt}"] = r
+    if sliding is not None:
+        result["sliding_window_513"] = sliding
     if floor is not None:
         result["read_floor"] = dict(
             floor,
