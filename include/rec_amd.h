@@ -190,7 +190,10 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * in any mix, or the affine pair): K/V tiles are dequantized into on-chip
  * memory, never to HBM — int8 codes exactly with the row scales applied to
  * scores and probabilities, 4-bit and affine values as x̂ rounded to the
- * query dtype, as the reference dequantizes before its attention.
+ * query dtype, as the reference dequantizes before its attention.  A chunk
+ * of at most 32 (query, head) rows per KV head over an int8 cache (no
+ * window) streams the cache through registers instead, as the decode does;
+ * its splits and workspace are the same.
  * splits: key splits (<= 0: automatic, 1: none, at most 64).  A short chunk
  * over a long cache (few query blocks x KV heads x batch) splits the keys so
  * that the launch fills the chip; the partials go to `workspace`
