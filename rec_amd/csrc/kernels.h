@@ -143,9 +143,10 @@ hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both kernels when a.S > 1
 // A few queries over the int8 cache (at most this many (query, head) rows
-// per KV head, no window): the streaming kernel of prefill_few.hip, whose
-// partials share the tiled kernel's workspace layout and merge
-constexpr int PREFILL_FEW_ROWS = 32;
+// per KV head, more than 32 only over long caches; no window): the streaming
+// kernel of prefill_few.hip, whose partials share the tiled kernel's
+// workspace layout and merge
+constexpr int PREFILL_FEW_ROWS = 64;
 bool prefill_few_fits(const PrefillArgs& a);
 hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream);

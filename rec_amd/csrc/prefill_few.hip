@@ -8,8 +8,8 @@
 // kernel spends each 128-token tile's conversion, LDS staging and barriers on
 // 16-row tiles that are mostly empty; here, as in the decode, every wave
 // streams its 32-token chunks from HBM into registers and the tile is never
-// staged.  The L·G <= 16·NT (query, head) rows of one KV head, numbered
-// query·G + head as in prefill.hip, fill NT column tiles of 16:
+// staged.  The L·G <= 16·NT (query, head) rows of one KV head (NT <= 4),
+// numbered query·G + head as in prefill.hip, fill NT column tiles of 16:
 //   * Q·Kᵀ on 16x16x32 bf16 (fp16 for fp16 queries) MFMAs: A = 16 tokens x 32
 //     dims of the int8 K block converted in registers (exact), B = the rows'
 //     query elements of the same dims (a lane holds dims 64m + 16kg + 8h ..
@@ -308,13 +308,21 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
 template <bool BF16, bool EXACT>
 static void launch_nt(const PrefillArgs& a, int nt, dim3 grid, hipStream_t stream) {
   if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, 1, EXACT>), grid, dim3(64 * FW), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_few_kernel<BF16, 2, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 2) hipLaunchKernelGGL((prefill_few_kernel<BF16, 2, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 3) hipLaunchKernelGGL((prefill_few_kernel<BF16, 3, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_few_kernel<BF16, 4, EXACT>), grid, dim3(64 * FW), 0, stream, a);
 }
 
 }  // namespace
 
+// Up to 32 rows (two column tiles) the streaming kernel is the faster one at
+// every cache length measured; three or four tiles (one wave per SIMD, the
+// accumulators partly in AGPRs) only over long caches: 8 queries x 8 heads
+// over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.
 bool prefill_few_fits(const PrefillArgs& a) {
-  return a.k_fmt == 8 && a.v_fmt == 8 && a.window == 0 && a.L * a.G <= PREFILL_FEW_ROWS;
+  const int rows = a.L * a.G;
+  return a.k_fmt == 8 && a.v_fmt == 8 && a.window == 0 &&
+         (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384));
 }
 
 hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
