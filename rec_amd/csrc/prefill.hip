@@ -813,7 +813,6 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
 template <int NR>
 __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) {
   static_assert(16 * NR <= PREFILL_MAX_SPLITS && PREFILL_MAX_SPLITS <= 64, "one split per lane");
-  __shared__ float wts[PREFILL_MAX_SPLITS];
   const int i = blockIdx.x, hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
   const int h = hq / a.G, p = i * a.G + (hq - h * a.G);  // the (query, head) row
   const int qb = p / PF_ROWS, r = p - qb * PF_ROWS;
@@ -842,11 +841,11 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
   const float f = (m == NEG_INF || M == NEG_INF) ? 0.f : __builtin_amdgcn_exp2f(m - M);
   float z = wave_sum(f * l);
   if (sink != NEG_INF) z += __builtin_amdgcn_exp2f(sink - M);
-  wts[lane] = f;  // 0 for lanes past the last split
-  __syncthreads();
+  // split k's weight is lane k's f (0 past the last split), read as a scalar
   v2f acc = {0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < 16 * NR; ++k) acc += wts[k] * x[k];
+  for (int k = 0; k < 16 * NR; ++k)
+    acc += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), k)) * x[k];
   const float inv = z > 0.f ? 1.f / z : 1.f;
   *(v2f*)(a.out + (((int64_t)b * a.Hq + hq) * a.L + i) * HEAD_DIM + 2 * lane) = acc * inv;
 }
