@@ -191,8 +191,9 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * memory, never to HBM — int8 codes exactly with the row scales applied to
  * scores and probabilities, 4-bit and affine values as x̂ rounded to the
  * query dtype, as the reference dequantizes before its attention.  A chunk
- * of at most 32 (query, head) rows per KV head over an int8 cache (no
- * window) streams the cache through registers instead, as the decode does;
+ * of at most 32 (query, head) rows per KV head (64 over a cache of 16,384
+ * tokens or more) over an int8 or affine cache (no window) streams the cache
+ * through registers instead, as the decode does, with the same values;
  * its splits and workspace are the same.
  * splits: key splits (<= 0: automatic, 1: none, at most 64).  A short chunk
  * over a long cache (few query blocks x KV heads x batch) splits the keys so

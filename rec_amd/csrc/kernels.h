@@ -142,7 +142,7 @@ hipError_t launch_stream_read(const void* p, int64_t n16, int workgroups, uint32
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both kernels when a.S > 1
-// A few queries over the int8 cache (at most this many (query, head) rows
+// A few queries over the int8 or affine cache (at most this many (query, head) rows
 // per KV head, more than 32 only over long caches; no window): the streaming
 // kernel of prefill_few.hip, whose partials share the tiled kernel's
 // workspace layout and merge

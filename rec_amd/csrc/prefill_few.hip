@@ -1,5 +1,6 @@
-// Chunked prefill of a few queries over the int8 cache: the decode's
-// streaming structure with the chunk's (query, head) rows as matrix columns.
+// Chunked prefill of a few queries over the int8 and affine caches: the
+// decode's streaming structure with the chunk's (query, head) rows as matrix
+// columns.
 //
 // Restates the same branch as prefill.hip (engine/src/rec_mlx/model.py:191-203:
 // the L new tokens are cached first, then their queries attend over the whole
@@ -20,6 +21,10 @@
 //     P' = p·s (the token's V scale) as an fp16 high part and, when the first
 //     query sees fewer than EXACT_PV_BELOW keys, its rounding remainder in a
 //     second MFMA (as the tiled kernel does).
+// The affine pair (8-bit K, 4-bit V, group 64, bf16 scale and bias) takes the
+// same loop with the values formed in registers as the tiled kernel forms
+// them in LDS: K x̂ = q·s + b in one fp32 fma rounded to the query dtype (the
+// A operand), V x̂ likewise, then widened to fp16 for P·V, and P' = p.
 // Work decomposition: grid (splits, Hkv, B) with the prefill's split plan
 // (128-token aligned ranges), 4 waves taking 32-token chunks in turn, a
 // 2-deep ring of loads.  Each workgroup merges its waves in LDS and writes
@@ -52,6 +57,9 @@ struct FewT<true> {
     }
     return r;
   }
+  static __device__ __forceinline__ __bf16 from_float(float x) { return (__bf16)x; }  // nearest even
+  // a dequantized V value as the reference holds it (bf16), widened to fp16
+  static __device__ __forceinline__ _Float16 v_elem(float x) { return (_Float16)(float)(__bf16)x; }
 };
 template <>
 struct FewT<false> {
@@ -60,18 +68,49 @@ struct FewT<false> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ vec codes(uint32_t w0, uint32_t w1) { return i8x8_to_h8(w0, w1); }
+  static __device__ __forceinline__ _Float16 from_float(float x) { return (_Float16)x; }
+  static __device__ __forceinline__ _Float16 v_elem(float x) { return (_Float16)x; }
 };
 
+// eight affine 8-bit K codes (two dwords, unsigned) -> x̂ = q·s + b in the
+// query dtype, one fp32 fma and one rounding each
+template <bool BF16>
+__device__ __forceinline__ typename FewT<BF16>::vec affine8(uint32_t w0, uint32_t w1, float s, float b) {
+  typename FewT<BF16>::vec r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = FewT<BF16>::from_float(__builtin_fmaf((float)((w0 >> (8 * e)) & 0xffu), s, b));
+    r[4 + e] = FewT<BF16>::from_float(__builtin_fmaf((float)((w1 >> (8 * e)) & 0xffu), s, b));
+  }
+  return r;
+}
+
 // One chunk's registers as they arrive: K block bytes of tile j (tokens 16j +
-// c), dims 64m + 16kg .. +15; V dims 16n + c at block positions 8kg .. +7
-// (n = 2h, 2h+1 in v[h]); the K and V scales of positions 8kg .. 8kg+7.
+// c), dims 64m + 16kg .. +15 (int8 and affine alike).
+//   int8: V dims 16n + c at block positions 8kg .. +7 (n = 2h, 2h+1 in v[h]);
+//     the K and V scales of positions 8kg .. 8kg+7.
+//   affine: 4-bit V dims 16n + c at positions 8kg .. +7 (n = 4h .. 4h+3 in
+//     v[h], dword n%4, nibble e = position 8kg + e); kx[2w + m] the K scale
+//     (w 0) or bias (w 1) of group m for tokens c (low half) and 16 + c (high
+//     half), whose slots s4_slot(block_pos(16j + c)) = 8(c/4) + 2(c%4) + j
+//     make dword c of the group's row; vx[2w + g] the V scales (w 0) or biases
+//     (w 1) of group g at slots 8kg .. 8kg+7 (positions (e, e+4) in dword e).
+template <bool AF>
 struct FewChunk {
   v4i k[2][2];
   v4i v[4];
   v4i ks, vs;
 };
+template <>
+struct FewChunk<true> {
+  v4i k[2][2];
+  v4i v[2];
+  v4i kx;
+  v4i vx[4];
+};
 
-__device__ __forceinline__ void few_load(FewChunk& R, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+template <bool AF>
+__device__ __forceinline__ void few_load(FewChunk<AF>& R, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
                                          __amdgpu_buffer_rsrc_t rks, __amdgpu_buffer_rsrc_t rvs,
                                          __amdgpu_buffer_rsrc_t none, bool ok, uint32_t blk, int c, int kg) {
   const __amdgpu_buffer_rsrc_t a = ok ? rk : none, b = ok ? rv : none, sa = ok ? rks : none, sb = ok ? rvs : none;
@@ -79,13 +118,22 @@ __device__ __forceinline__ void few_load(FewChunk& R, __amdgpu_buffer_rsrc_t rk,
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int m = 0; m < 2; ++m) R.k[j][m] = ld128(a, (uint32_t)((16 * j + c) * 64 + 16 * kg + 2048 * m), blk * 4096);
+  if constexpr (AF) {
 #pragma unroll
-  for (int h = 0; h < 4; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 4096);
-  R.ks = ld128(sa, (uint32_t)(16 * kg), blk * 64);
-  R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
+    for (int h = 0; h < 2; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 2048);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) R.kx[w] = (int)ld32(sa, (uint32_t)(64 * w + 4 * c), blk * 256);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) R.vx[w] = ld128(sb, (uint32_t)(64 * w + 16 * kg), blk * 256);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 4096);
+    R.ks = ld128(sa, (uint32_t)(16 * kg), blk * 64);
+    R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
+  }
 }
 
-template <bool BF16, int NT, bool EXACT>
+template <bool BF16, bool AF, int NT, bool EXACT>
 __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs a) {
   typedef typename FewT<BF16>::vec V8;
   constexpr int NC = 16 * NT;  // (query, head) columns of the workgroup
@@ -129,10 +177,12 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
 
   // ---- resources of this (b, h) slice ----
   const int64_t cap = a.cap;
+  constexpr int64_t VROW = AF ? HEAD_DIM / 2 : HEAD_DIM;  // V code bytes per token
+  constexpr int64_t SROW = AF ? 4 : 1;                    // scale entries per token
   const __amdgpu_buffer_rsrc_t rk = make_rsrc((const int8_t*)a.kq + bh * cap * HEAD_DIM, cap * HEAD_DIM);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const int8_t*)a.vq + bh * cap * HEAD_DIM, cap * HEAD_DIM);
-  const __amdgpu_buffer_rsrc_t rks = make_rsrc(a.ks + bh * cap, cap * 2);
-  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(a.vs + bh * cap, cap * 2);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc((const int8_t*)a.vq + bh * cap * VROW, cap * VROW);
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(a.ks + bh * cap * SROW, cap * SROW * 2);
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(a.vs + bh * cap * SROW, cap * SROW * 2);
   const __amdgpu_buffer_rsrc_t none = make_rsrc(a.ks, 0);
 
   // ---- softmax state per column (log2 domain) ----
@@ -150,7 +200,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     for (int n = 0; n < 8; ++n) acc[t][n] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
 
-  const auto process = [&](const FewChunk& R, int t0) {
+  const auto process = [&](const FewChunk<AF>& R, int t0) {
     // Q·Kᵀ: lane (c, kg) receives the scores of column c for tokens 16j + 4kg + i
     v4f s4[NT][2];
 #pragma unroll
@@ -159,7 +209,15 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const v4i w = R.k[j][ks >> 1];
-        ka[ks] = FewT<BF16>::codes((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1]);
+        if constexpr (AF) {
+          const int m = ks >> 1;
+          const uint32_t sw = (uint32_t)R.kx[m], bw = (uint32_t)R.kx[2 + m];
+          const float sc = __builtin_bit_cast(float, j ? sw & 0xffff0000u : sw << 16);
+          const float bi = __builtin_bit_cast(float, j ? bw & 0xffff0000u : bw << 16);
+          ka[ks] = affine8<BF16>((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1], sc, bi);
+        } else {
+          ka[ks] = FewT<BF16>::codes((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1]);
+        }
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -169,16 +227,23 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
         s4[t][j] = d;
       }
     }
-    // the K row scale times the softmax scale, and the V scale, of the lane's 8 positions
+    // the K row scale times the softmax scale, and the V scale, of the lane's
+    // 8 positions (affine: the softmax scale alone, and P' = p)
     float ksm[8], vsf[8];
 #pragma unroll
     for (int idx = 0; idx < 8; ++idx) {
-      ksm[idx] = half_at(R.ks, idx) * a.q_mul;
-      vsf[idx] = half_at(R.vs, idx);
+      if constexpr (AF) {
+        ksm[idx] = a.q_mul;
+        vsf[idx] = 1.f;
+      } else {
+        ksm[idx] = half_at(R.ks, idx) * a.q_mul;
+        vsf[idx] = half_at(R.vs, idx);
+      }
     }
     // Range (as in the decode): a V scale of 2 or more among the lane's
     // positions makes its bound 0, so p <= 1 and P' = p·s stays finite in fp16
-    const bool big = ((uint32_t)(R.vs[0] | R.vs[1] | R.vs[2] | R.vs[3]) & 0x40004000u) != 0;
+    bool big = false;
+    if constexpr (!AF) big = ((uint32_t)(R.vs[0] | R.vs[1] | R.vs[2] | R.vs[3]) & 0x40004000u) != 0;
     const float gap = big ? 0.f : RESCALE_GAP;
     // tokens past the split end or past a column's causal limit: only the
     // chunks at the end of the range (uniform test)
@@ -230,7 +295,30 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     // P·V
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      const v8h va = i8x8_to_h8((uint32_t)R.v[n >> 1][2 * (n & 1)], (uint32_t)R.v[n >> 1][2 * (n & 1) + 1]);
+      v8h va;
+      if constexpr (AF) {
+        // nibble e = position 8kg + e; the fp16 unpack under the exponent of
+        // 1024 (64) yields the pair (e, e+4) exactly, whose scales and biases
+        // share dword e of the slot run (s4_slot)
+        const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+        const int g = n >> 2;
+        const uint32_t W = (uint32_t)R.v[g][n & 3], W8 = W >> 8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t sw = (uint32_t)R.vx[g][e], bw = (uint32_t)R.vx[2 + g][e];
+          const uint32_t t = (e & 1) ? and_or(e < 2 ? W : W8, 0x00f000f0u, 0x54005400u)
+                                     : and_or(e < 2 ? W : W8, 0x000f000fu, 0x64006400u);
+          const v2h qv = __builtin_bit_cast(v2h, t) - ((e & 1) ? k64 : k1024);
+          const float x0 = __builtin_fmaf((float)qv[0], __builtin_bit_cast(float, sw << 16),
+                                          __builtin_bit_cast(float, bw << 16));
+          const float x1 = __builtin_fmaf((float)qv[1], __builtin_bit_cast(float, sw & 0xffff0000u),
+                                          __builtin_bit_cast(float, bw & 0xffff0000u));
+          va[e] = FewT<BF16>::v_elem(x0);
+          va[e + 4] = FewT<BF16>::v_elem(x1);
+        }
+      } else {
+        va = i8x8_to_h8((uint32_t)R.v[n >> 1][2 * (n & 1)], (uint32_t)R.v[n >> 1][2 * (n & 1) + 1]);
+      }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t], acc[t][n], 0, 0, 0);
@@ -243,7 +331,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   const int n_chunks = (t_end - lo + FCH - 1) / FCH;
   const int n_w = n_chunks > wave ? (n_chunks - wave + FW - 1) / FW : 0;
   const uint32_t blk0 = (uint32_t)(lo / FCH + wave);
-  FewChunk buf[2];
+  FewChunk<AF> buf[2];
   few_load(buf[0], rk, rv, rks, rvs, none, 0 < n_w, blk0, c, kg);
   const int n_pad = (n_w + 1) / 2 * 2;
   for (int i0 = 0; i0 < n_pad; i0 += 2) {
@@ -305,12 +393,23 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   }
 }
 
-template <bool BF16, bool EXACT>
+template <bool BF16, bool AF, bool EXACT>
 static void launch_nt(const PrefillArgs& a, int nt, dim3 grid, hipStream_t stream) {
-  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, 1, EXACT>), grid, dim3(64 * FW), 0, stream, a);
-  else if (nt == 2) hipLaunchKernelGGL((prefill_few_kernel<BF16, 2, EXACT>), grid, dim3(64 * FW), 0, stream, a);
-  else if (nt == 3) hipLaunchKernelGGL((prefill_few_kernel<BF16, 3, EXACT>), grid, dim3(64 * FW), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_few_kernel<BF16, 4, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 1, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 2) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 2, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 3) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 3, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 4, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+}
+
+template <bool AF>
+static void launch_af(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipStream_t stream) {
+  if (a.q_dtype == DT_BF16) {
+    if (exact) launch_nt<true, AF, true>(a, nt, grid, stream);
+    else launch_nt<true, AF, false>(a, nt, grid, stream);
+  } else {
+    if (exact) launch_nt<false, AF, true>(a, nt, grid, stream);
+    else launch_nt<false, AF, false>(a, nt, grid, stream);
+  }
 }
 
 }  // namespace
@@ -321,7 +420,8 @@ static void launch_nt(const PrefillArgs& a, int nt, dim3 grid, hipStream_t strea
 // over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.
 bool prefill_few_fits(const PrefillArgs& a) {
   const int rows = a.L * a.G;
-  return a.k_fmt == 8 && a.v_fmt == 8 && a.window == 0 &&
+  const bool fmt = (a.k_fmt == 8 && a.v_fmt == 8) || (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4);
+  return fmt && a.window == 0 &&
          (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384));
 }
 
@@ -330,13 +430,8 @@ hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
   const int nt = (a.L * a.G + 15) / 16;
   // the first query sees the fewest keys; from EXACT_PV_BELOW on, P' in one fp16 part
   const bool exact = (a.causal ? a.T - a.L + 1 : a.T) < EXACT_PV_BELOW;
-  if (a.q_dtype == DT_BF16) {
-    if (exact) launch_nt<true, true>(a, nt, grid, stream);
-    else launch_nt<true, false>(a, nt, grid, stream);
-  } else {
-    if (exact) launch_nt<false, true>(a, nt, grid, stream);
-    else launch_nt<false, false>(a, nt, grid, stream);
-  }
+  if (a.k_fmt == FMT_A8) launch_af<true>(a, nt, exact, grid, stream);
+  else launch_af<false>(a, nt, exact, grid, stream);
   return hipGetLastError();
 }
 

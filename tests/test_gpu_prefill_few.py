@@ -1,7 +1,8 @@
 """Parity of the few-query prefill path (prefill_few.hip) with the CPU oracle.
 
-Chunks of at most 32 (query, head) rows per KV head over an int8 cache (64
-over long caches) run on the streaming kernel instead of the tiled one; the outputs must lie within
+Chunks of at most 32 (query, head) rows per KV head over an int8 or affine
+cache (64 over long caches) run on the streaming kernel instead of the tiled
+one; the outputs must lie within
 2e-3 absolute + 1e-3 relative of the oracle, as the tiled kernel's do, for
 causal and full masks, sinks, GQA ratios 1 to 8, bf16 and fp16 queries, key
 splits (automatic, explicit, one) and ranges whose last chunk lies wholly past
@@ -12,8 +13,8 @@ import pytest
 import torch
 
 import oracle as O
-from rec_amd import QuantizedKVCache, attend, synthetic
-from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize
+from rec_amd import MixedQuantizedKVCache, QuantizedKVCache, attend, synthetic
+from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize, oracle_xhat, prefill_side
 
 pytestmark = pytest.mark.gpu
 
@@ -73,3 +74,41 @@ def test_few_query_prefill_large_v_scale(gpu):
     rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
     ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None, "causal")
     assert_close(f32(out), ref, "large V")
+
+
+AFFINE_CASES = [
+    # B, Hq, Hkv, P, L, causal, sinks, dtype, splits (0 = automatic)
+    (1, 32, 4, 5000, 4, True, True, torch.bfloat16, 0),     # 32 rows, exact P·V
+    (1, 32, 4, 40000, 2, True, True, torch.bfloat16, 0),    # a long cache: P' in one fp16 part
+    (2, 8, 2, 300, 7, True, False, torch.float16, 0),       # 28 rows, two sequences, fp16 queries
+    (1, 8, 1, 33, 3, False, True, torch.bfloat16, 5),       # full attention, explicit splits
+    (1, 16, 2, 31, 4, True, True, torch.float16, 0),        # the chunk at 32 lies past query 0's limit
+    (1, 8, 1, 62, 2, True, True, torch.bfloat16, 1),        # 16 rows: one column tile, unsplit
+    (1, 32, 4, 20000, 8, True, True, torch.bfloat16, 0),    # 64 rows: four column tiles
+    (1, 24, 8, 16384, 14, True, False, torch.float16, 3),   # 42 rows, G = 3
+]
+
+
+@pytest.mark.parametrize("case", AFFINE_CASES,
+                         ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_causal{}_s{}_{}_sp{}".format(*c[:7], str(c[7])[6:], c[8]))
+def test_few_query_prefill_affine_matches_oracle(gpu, case):
+    """The affine pair (8-bit K, 4-bit V, group 64): K and V values formed in
+    registers as q·s + b rounded to the query dtype, as the reference
+    dequantizes the cache before its attention."""
+    B, Hq, Hkv, P, L, causal, with_sinks, dtype, splits = case
+    assert L * (Hq // Hkv) <= 64
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 91 + T, kind="outliers", frac=0.01)
+    v = synthetic.kv((B, Hkv, T, 128), 92 + T, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, L, 93 + L, dtype=dtype)
+    sinks = torch.randn(Hq, device="cuda") if with_sinks else None
+    cache = MixedQuantizedKVCache()
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    mask = "causal" if causal else None
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32,
+                 splits=splits or None)
+    torch.cuda.synchronize()
+    kv_k, kv_v = cache.keys_and_values()
+    kh, vh = prefill_side(oracle_xhat(kv_k), kv_k, dtype), prefill_side(oracle_xhat(kv_v), kv_v, dtype)
+    ref = O.attention(f32(q), kh, vh, SCALE, None if sinks is None else f32(sinks), mask)
+    assert_close(f32(out), ref, f"affine case {case}")
