@@ -24,7 +24,9 @@
 // The affine pair (8-bit K, 4-bit V, group 64, bf16 scale and bias) takes the
 // same loop with the values formed in registers as the tiled kernel forms
 // them in LDS: K x̂ = q·s + b in one fp32 fma rounded to the query dtype (the
-// A operand), V x̂ likewise, then widened to fp16 for P·V, and P' = p.
+// A operand), V x̂ likewise, and P' = p.  Under fp16 queries P·V is the fp16
+// product as above; under bf16 queries the bf16 V value enters a bf16 MFMA
+// as it is, with P split into bf16 high and low parts.
 // Work decomposition: grid (splits, Hkv, B) with the prefill's split plan
 // (128-token aligned ranges), 4 waves taking 32-token chunks in turn, a
 // 2-deep ring of loads.  Each workgroup merges its waves in LDS and writes
@@ -38,6 +40,7 @@ namespace {
 constexpr int FW = 4;        // wavefronts per workgroup
 constexpr int FCH = 32;      // tokens per chunk (one cache block)
 constexpr int FPR = HEAD_DIM + 4;  // LDS row pitch of a wave partial (floats)
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 template <bool BF16>
 struct FewT;
@@ -248,10 +251,15 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     // tokens past the split end or past a column's causal limit: only the
     // chunks at the end of the range (uniform test)
     const bool edge = t0 + FCH > t_end || t0 + FCH - 1 > P;
+    // affine V under bf16 queries: V x̂ enters P·V as the bf16 value itself
+    // (no widening to fp16) and P as bf16 high and low parts, positions
+    // (e, e+4) at operand elements (2e, 2e+1), the order of the nibble unpack
+    constexpr bool BPV = AF && BF16;
     v8h pb[NT], pl[NT];  // pl: EXACT only
+    v8bf ph[NT], plo[NT];  // BPV only
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      float x[8];
+      float x[8], pv[8];
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -279,6 +287,11 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
         const float p0 = __builtin_amdgcn_exp2f(x[idx] - m_run[t]);
         const float p1 = __builtin_amdgcn_exp2f(x[idx + 1] - m_run[t]);
         l_run[t] += p0 + p1;
+        if constexpr (BPV) {
+          pv[idx] = p0;
+          pv[idx + 1] = p1;
+          continue;
+        }
         // P' = p·s rounded to fp16 once (and, EXACT, its remainder)
         uint32_t w;
         asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(w) : "v"(p0), "v"(vsf[idx]));
@@ -291,11 +304,23 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
           pl[t][idx + 1] = (_Float16)__builtin_fmaf(p1, vsf[idx + 1], -(float)hh[1]);
         }
       }
+      if constexpr (BPV) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const v2bf hi = __builtin_convertvector((v2f){pv[e], pv[e + 4]}, v2bf);
+          const v2bf lo = __builtin_convertvector((v2f){pv[e] - (float)hi[0], pv[e + 4] - (float)hi[1]}, v2bf);
+          ph[t][2 * e] = hi[0];
+          ph[t][2 * e + 1] = hi[1];
+          plo[t][2 * e] = lo[0];
+          plo[t][2 * e + 1] = lo[1];
+        }
+      }
     }
     // P·V
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       v8h va;
+      v8bf vb;  // BPV
       if constexpr (AF) {
         // nibble e = position 8kg + e; the fp16 unpack under the exponent of
         // 1024 (64) yields the pair (e, e+4) exactly, whose scales and biases
@@ -313,16 +338,27 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
                                           __builtin_bit_cast(float, bw << 16));
           const float x1 = __builtin_fmaf((float)qv[1], __builtin_bit_cast(float, sw & 0xffff0000u),
                                           __builtin_bit_cast(float, bw & 0xffff0000u));
-          va[e] = FewT<BF16>::v_elem(x0);
-          va[e + 4] = FewT<BF16>::v_elem(x1);
+          if constexpr (BPV) {
+            const v2bf xb = __builtin_convertvector((v2f){x0, x1}, v2bf);  // nearest even
+            vb[2 * e] = xb[0];
+            vb[2 * e + 1] = xb[1];
+          } else {
+            va[e] = FewT<BF16>::v_elem(x0);
+            va[e + 4] = FewT<BF16>::v_elem(x1);
+          }
         }
       } else {
         va = i8x8_to_h8((uint32_t)R.v[n >> 1][2 * (n & 1)], (uint32_t)R.v[n >> 1][2 * (n & 1) + 1]);
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t], acc[t][n], 0, 0, 0);
-        if constexpr (EXACT) acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[t], acc[t][n], 0, 0, 0);
+        if constexpr (BPV) {
+          acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, ph[t], acc[t][n], 0, 0, 0);
+          acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vb, plo[t], acc[t][n], 0, 0, 0);
+        } else {
+          acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[t], acc[t][n], 0, 0, 0);
+          if constexpr (EXACT) acc[t][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[t], acc[t][n], 0, 0, 0);
+        }
       }
     }
   };
