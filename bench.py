@@ -931,7 +931,7 @@ def main(argv=None):
     if not args.no_gemv:
         rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
 
-    rpf = rpf_short = rpf_few = None
+    rpf = rpf_short = rpf_few = rpf_few_affine = None
     rpf_fmt = {}
     if not args.no_prefill:
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
@@ -939,6 +939,7 @@ def main(argv=None):
         rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
         # four draft tokens over a long cache: the streaming few-query kernel
         rpf_few = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 54)
+        rpf_few_affine = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 54, "affine")
         # the same long chunk over the 4-bit, affine and bf16 caches
         for i, fmt in enumerate(("uint4", "affine", "bf16")):
             rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
@@ -1098,6 +1099,8 @@ def main(argv=None):
         result["prefill_32768_plus_20"] = rpf_short
     if rpf_few is not None:
         result["prefill_65536_plus_4"] = rpf_few
+    if rpf_few_affine is not None:
+        result["prefill_65536_plus_4_affine"] = rpf_few_affine
     for fmt, r in rpf_fmt.items():
         result[f"prefill_65536_plus_2048_{fmt}"] = r
     if sliding is not None:
