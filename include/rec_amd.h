@@ -237,6 +237,23 @@ int rec_kv_write_bf16(const void* k_new, const void* v_new, int in_dtype,
                       int B, int Hkv, int L, int D, int64_t offset, int64_t capacity, void* stream);
 
 /*
+ * rec_ring_join_bf16: the keys and values a chunk attends over in a
+ * sliding-window ring, in one launch — the n_held tokens in sequence order
+ * (token i at ring slot (head + i) mod capacity; the ring is (B, Hkv,
+ * capacity, 128) bf16 with element strides (r*_sb, r*_sh), token stride 128)
+ * followed by rows [0, L) of k_new / v_new (any float dtype, rounded to
+ * bf16), into contiguous (B, Hkv, n_held + L, 128) bf16 k_out / v_out.
+ * Replaces the concatenation of the held window and the chunk in
+ * FixedSlidingKVCache.update_and_fetch, engine/src/rec_mlx/cache.py:227-247.
+ */
+int rec_ring_join_bf16(const void* k_ring, const void* v_ring, int64_t rk_sb, int64_t rk_sh,
+                       int64_t rv_sb, int64_t rv_sh, int64_t capacity, int64_t head, int64_t n_held,
+                       const void* k_new, const void* v_new, int in_dtype,
+                       int64_t k_sb, int64_t k_sh, int64_t k_st,
+                       int64_t v_sb, int64_t v_sh, int64_t v_st,
+                       void* k_out, void* v_out, int B, int Hkv, int L, int D, void* stream);
+
+/*
  * GQA decode attention over the first T tokens of a bf16 K/V cache, with an
  * optional fused write of the newest token (k_new / v_new (B, Hkv, 1, D), any
  * float dtype, stored at position T-1 first; NULL: no write).  Query, sinks,

@@ -612,6 +612,38 @@ int rec_kv_write_bf16(const void* k_new, const void* v_new, int in_dtype, int64_
   return launched(launch_write_bf16(a, kc_sb, kc_sh, vc_sb, vc_sh, (hipStream_t)stream), "bf16 write launch");
 }
 
+int rec_ring_join_bf16(const void* k_ring, const void* v_ring, int64_t rk_sb, int64_t rk_sh, int64_t rv_sb,
+                       int64_t rv_sh, int64_t capacity, int64_t head, int64_t n_held, const void* k_new,
+                       const void* v_new, int in_dtype, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
+                       int64_t v_sh, int64_t v_st, void* k_out, void* v_out, int B, int Hkv, int L, int D,
+                       void* stream) {
+  int e;
+  if ((e = check_dtype(in_dtype, "input"))) return e;
+  if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
+  if (B < 1 || Hkv < 1 || L < 0) return fail(REC_EINVAL, "bad shape B=%d Hkv=%d L=%d", B, Hkv, L);
+  if (capacity < 1 || n_held < 0 || n_held > capacity || head < 0 || head >= capacity)
+    return fail(REC_EINVAL, "ring of capacity %lld cannot hold %lld tokens from slot %lld", (long long)capacity,
+                (long long)n_held, (long long)head);
+  if (n_held + L == 0) return ok();
+  if (!k_out || !v_out || (n_held > 0 && (!k_ring || !v_ring)) || (L > 0 && (!k_new || !v_new)))
+    return fail(REC_EINVAL, "null key/value pointer");
+  if ((reinterpret_cast<uintptr_t>(k_out) | reinterpret_cast<uintptr_t>(v_out)) & 3)
+    return fail(REC_EALIGN, "joined K/V must be 4-byte aligned");
+  if (n_held > 0 && (((reinterpret_cast<uintptr_t>(k_ring) | reinterpret_cast<uintptr_t>(v_ring)) & 3) ||
+                     ((rk_sb | rk_sh | rv_sb | rv_sh) & 1)))
+    return fail(REC_EALIGN, "ring K/V must be 4-byte aligned with even strides");
+  AppendArgs a{};
+  a.k = RowSrc{k_new, in_dtype, k_sb, k_sh, k_st, L > 0 && vec_rows(k_new, k_sb, k_sh, k_st)};
+  a.v = RowSrc{v_new, in_dtype, v_sb, v_sh, v_st, L > 0 && vec_rows(v_new, v_sb, v_sh, v_st)};
+  a.B = B;
+  a.Hkv = Hkv;
+  a.L = L;
+  a.cap = capacity;
+  return launched(launch_ring_join_bf16(a, k_ring, v_ring, rk_sb, rk_sh, rv_sb, rv_sh, head, n_held, k_out, v_out,
+                                        (hipStream_t)stream),
+                  "ring join launch");
+}
+
 int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
                     int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k, int64_t k_sb,
                     int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale, int B, int Hq,

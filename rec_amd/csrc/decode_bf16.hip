@@ -326,7 +326,49 @@ __global__ __launch_bounds__(256) void write_bf16_kernel(const AppendArgs a, int
   }
 }
 
+// The keys (values) a chunk attends over in a sliding-window ring
+// (FixedSlidingKVCache.update_and_fetch, cache.py:227-247): the n held tokens
+// in sequence order -- token i at ring slot (head + i) mod capacity -- then
+// the L new rows rounded to bf16, into one (B, Hkv, n + L, 128) tensor.  One
+// wavefront per (row, K or V), two elements per lane, as write_bf16_kernel.
+__global__ __launch_bounds__(256) void ring_join_kernel(const AppendArgs a, const __bf16* rk, const __bf16* rv,
+                                                        int64_t rk_sb, int64_t rk_sh, int64_t rv_sb, int64_t rv_sh,
+                                                        int64_t head, int64_t n, __bf16* ok, __bf16* ov) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = n + a.L;
+  const int64_t total = (int64_t)a.B * a.Hkv * rows;
+  const bool isv = blockIdx.y == 1;
+  const RowSrc& src = isv ? a.v : a.k;
+  for (int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); unit < total; unit += (int64_t)gridDim.x * 4) {
+    const int64_t bh = unit / rows, u = unit % rows;
+    const int b = (int)(bh / a.Hkv), h = (int)(bh % a.Hkv);
+    uint32_t w;
+    if (u < n) {
+      const int64_t slot = (head + u) % a.cap;
+      const __bf16* ring = isv ? rv + (int64_t)b * rv_sb + (int64_t)h * rv_sh : rk + (int64_t)b * rk_sb + (int64_t)h * rk_sh;
+      w = *(const uint32_t*)(ring + slot * HEAD_DIM + 2 * lane);
+    } else {
+      float x0, x1;
+      load2_as_float(src, row_base(src, b, h, (int)(u - n)) + 2 * lane, x0, x1);
+      const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+      w = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    }
+    *(uint32_t*)((isv ? ov : ok) + unit * HEAD_DIM + 2 * lane) = w;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_ring_join_bf16(const AppendArgs& a, const void* rk, const void* rv, int64_t rk_sb, int64_t rk_sh,
+                                 int64_t rv_sb, int64_t rv_sh, int64_t head, int64_t n, void* ok, void* ov,
+                                 hipStream_t stream) {
+  const int64_t rows = (int64_t)a.B * a.Hkv * (n + a.L);
+  const int64_t wgs = (rows + 3) / 4;
+  const unsigned grid_x = (unsigned)(wgs < (1 << 20) ? (wgs > 0 ? wgs : 1) : (1 << 20));  // the kernel strides over rows
+  hipLaunchKernelGGL(ring_join_kernel, dim3(grid_x, 2), dim3(256), 0, stream, a, (const __bf16*)rk,
+                     (const __bf16*)rv, rk_sb, rk_sh, rv_sb, rv_sh, head, n, (__bf16*)ok, (__bf16*)ov);
+  return hipGetLastError();
+}
 
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(decode_bf16_kernel, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);

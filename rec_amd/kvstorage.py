@@ -338,9 +338,21 @@ class FixedSlidingKVCache:
             self.offset += 1
             n = self.size()
             return self.keys[:, :, :n], self.values[:, :, :n]
-        held_k, held_v = self.window()
-        attend_k = torch.cat((held_k, keys.to(torch.bfloat16)), dim=2)
-        attend_v = torch.cat((held_v, values.to(torch.bfloat16)), dim=2)
+        # the held window in order, then the chunk: one gather launch
+        n = self.size()
+        head = self.offset % self.capacity if self.offset > self.capacity else 0
+        attend_k = torch.empty((B, H, n + L, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+        attend_v = torch.empty_like(attend_k)
+        k, ksb, ksh, kst = _stride3(keys)
+        v, vsb, vsh, vst = _stride3(values)
+        rc = _lib.load().rec_ring_join_bf16(
+            self.keys.data_ptr(), self.values.data_ptr(), self.keys.stride(0), self.keys.stride(1),
+            self.values.stride(0), self.values.stride(1), self.capacity, head, n,
+            k.data_ptr(), v.data_ptr(), _DTYPES[keys.dtype], ksb, ksh, kst, vsb, vsh, vst,
+            attend_k.data_ptr(), attend_v.data_ptr(), B, H, L, HEAD_DIM,
+            torch.cuda.current_stream(self.device).cuda_stream,
+        )
+        _lib.check(rc, "rec_ring_join_bf16")
         keep = min(L, self.capacity)
         self._place(keys[:, :, L - keep:], values[:, :, L - keep:], self.offset + L)
         self.offset += L

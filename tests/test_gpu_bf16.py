@@ -338,3 +338,31 @@ def test_sliding_window_prefill_chunks(gpu):
         ref = O.attention(f32(q), kk, vv, SCALE, sinks=f32(sinks), mask=(qi >= ki) & (qi < ki + W))
         assert_close(f32(out), ref, f"chunk at {pos} of {L}")
         pos = end
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_ring_join_bit_exact(gpu, dtype):
+    """rec_ring_join_bf16 (FixedSlidingKVCache.update_and_fetch of a chunk):
+    the held window in sequence order, then the chunk rounded to bf16, equal
+    bit for bit to joining the same tokens of the full sequence, before and
+    after the ring wraps and for chunks longer than the window."""
+    from rec_amd import FixedSlidingKVCache
+
+    B, Hkv, W = 2, 3, 100
+    n = 700
+    k = synthetic.kv((B, Hkv, n, 128), 151, dtype=dtype)
+    v = synthetic.kv((B, Hkv, n, 128), 152, dtype=dtype)
+    cache = FixedSlidingKVCache(max_sequence_tokens=4096, num_kv_heads=Hkv, head_dim=128, window_size=W, batch=B)
+    pos = 0
+    for L in (40, 30, 1, 57, 150, 1, 1, 99, 203):
+        held = min(pos, W)
+        kk, vv = cache.update_and_fetch(k[:, :, pos:pos + L], v[:, :, pos:pos + L])
+        torch.cuda.synchronize()
+        end = pos + L
+        if L > 1:
+            assert kk.shape == (B, Hkv, held + L, 128) and kk.dtype == torch.bfloat16
+            want_k = k[:, :, end - held - L:end].to(torch.bfloat16)
+            want_v = v[:, :, end - held - L:end].to(torch.bfloat16)
+            assert torch.equal(kk.view(torch.int16), want_k.contiguous().view(torch.int16)), f"K at {pos}+{L}"
+            assert torch.equal(vv.view(torch.int16), want_v.contiguous().view(torch.int16)), f"V at {pos}+{L}"
+        pos = end
