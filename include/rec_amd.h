@@ -243,12 +243,16 @@ int rec_kv_write_bf16(const void* k_new, const void* v_new, int in_dtype,
  * capacity, 128) bf16 with element strides (r*_sb, r*_sh), token stride 128)
  * followed by rows [0, L) of k_new / v_new (any float dtype, rounded to
  * bf16), into contiguous (B, Hkv, n_held + L, 128) bf16 k_out / v_out.
- * Replaces the concatenation of the held window and the chunk in
- * FixedSlidingKVCache.update_and_fetch, engine/src/rec_mlx/cache.py:227-247.
+ * place != 0: the chunk's last min(L, capacity) rows (sequence positions
+ * offset + j) also go to their slots (offset + j) mod capacity, each held
+ * token read before its slot is rewritten — the whole update of the ring.
+ * Replaces the concatenation of the held window and the chunk, and the
+ * ring's rewrite, in FixedSlidingKVCache.update_and_fetch,
+ * engine/src/rec_mlx/cache.py:227-247.
  */
-int rec_ring_join_bf16(const void* k_ring, const void* v_ring, int64_t rk_sb, int64_t rk_sh,
+int rec_ring_join_bf16(void* k_ring, void* v_ring, int64_t rk_sb, int64_t rk_sh,
                        int64_t rv_sb, int64_t rv_sh, int64_t capacity, int64_t head, int64_t n_held,
-                       const void* k_new, const void* v_new, int in_dtype,
+                       int64_t offset, int place, const void* k_new, const void* v_new, int in_dtype,
                        int64_t k_sb, int64_t k_sh, int64_t k_st,
                        int64_t v_sb, int64_t v_sh, int64_t v_st,
                        void* k_out, void* v_out, int B, int Hkv, int L, int D, void* stream);

@@ -75,7 +75,7 @@ SIGNATURES["rec_kv_write_bf16"] = (
 )
 SIGNATURES["rec_ring_join_bf16"] = (
     _i,
-    [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # ring
+    [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i,  # ring
      _p, _p, _i, _i64, _i64, _i64, _i64, _i64, _i64,  # new rows
      _p, _p, _i, _i, _i, _i, _p],
 )

@@ -612,8 +612,9 @@ int rec_kv_write_bf16(const void* k_new, const void* v_new, int in_dtype, int64_
   return launched(launch_write_bf16(a, kc_sb, kc_sh, vc_sb, vc_sh, (hipStream_t)stream), "bf16 write launch");
 }
 
-int rec_ring_join_bf16(const void* k_ring, const void* v_ring, int64_t rk_sb, int64_t rk_sh, int64_t rv_sb,
-                       int64_t rv_sh, int64_t capacity, int64_t head, int64_t n_held, const void* k_new,
+int rec_ring_join_bf16(void* k_ring, void* v_ring, int64_t rk_sb, int64_t rk_sh, int64_t rv_sb,
+                       int64_t rv_sh, int64_t capacity, int64_t head, int64_t n_held, int64_t offset, int place,
+                       const void* k_new,
                        const void* v_new, int in_dtype, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t v_sb,
                        int64_t v_sh, int64_t v_st, void* k_out, void* v_out, int B, int Hkv, int L, int D,
                        void* stream) {
@@ -624,12 +625,13 @@ int rec_ring_join_bf16(const void* k_ring, const void* v_ring, int64_t rk_sb, in
   if (capacity < 1 || n_held < 0 || n_held > capacity || head < 0 || head >= capacity)
     return fail(REC_EINVAL, "ring of capacity %lld cannot hold %lld tokens from slot %lld", (long long)capacity,
                 (long long)n_held, (long long)head);
+  if (offset < 0) return fail(REC_EINVAL, "negative offset");
   if (n_held + L == 0) return ok();
-  if (!k_out || !v_out || (n_held > 0 && (!k_ring || !v_ring)) || (L > 0 && (!k_new || !v_new)))
+  if (!k_out || !v_out || ((n_held > 0 || place) && (!k_ring || !v_ring)) || (L > 0 && (!k_new || !v_new)))
     return fail(REC_EINVAL, "null key/value pointer");
   if ((reinterpret_cast<uintptr_t>(k_out) | reinterpret_cast<uintptr_t>(v_out)) & 3)
     return fail(REC_EALIGN, "joined K/V must be 4-byte aligned");
-  if (n_held > 0 && (((reinterpret_cast<uintptr_t>(k_ring) | reinterpret_cast<uintptr_t>(v_ring)) & 3) ||
+  if ((n_held > 0 || place) && (((reinterpret_cast<uintptr_t>(k_ring) | reinterpret_cast<uintptr_t>(v_ring)) & 3) ||
                      ((rk_sb | rk_sh | rv_sb | rv_sh) & 1)))
     return fail(REC_EALIGN, "ring K/V must be 4-byte aligned with even strides");
   AppendArgs a{};
@@ -639,8 +641,10 @@ int rec_ring_join_bf16(const void* k_ring, const void* v_ring, int64_t rk_sb, in
   a.Hkv = Hkv;
   a.L = L;
   a.cap = capacity;
-  return launched(launch_ring_join_bf16(a, k_ring, v_ring, rk_sb, rk_sh, rv_sb, rv_sh, head, n_held, k_out, v_out,
-                                        (hipStream_t)stream),
+  a.offset = offset;
+  const int64_t keep_from = L - std::min<int64_t>(L, capacity);
+  return launched(launch_ring_join_bf16(a, k_ring, v_ring, rk_sb, rk_sh, rv_sb, rv_sh, head, n_held, keep_from,
+                                        place != 0, k_out, v_out, (hipStream_t)stream),
                   "ring join launch");
 }
 

@@ -331,9 +331,14 @@ __global__ __launch_bounds__(256) void write_bf16_kernel(const AppendArgs a, int
 // in sequence order -- token i at ring slot (head + i) mod capacity -- then
 // the L new rows rounded to bf16, into one (B, Hkv, n + L, 128) tensor.  One
 // wavefront per (row, K or V), two elements per lane, as write_bf16_kernel.
-__global__ __launch_bounds__(256) void ring_join_kernel(const AppendArgs a, const __bf16* rk, const __bf16* rv,
+// With place, chunk rows j >= keep_from (sequence position a.offset + j) also
+// go to their ring slots.  A slot that holds a token of the window is
+// rewritten by the wavefront that reads it, after its read: no other
+// wavefront touches it, so the launch needs no ordering between them.
+__global__ __launch_bounds__(256) void ring_join_kernel(const AppendArgs a, __bf16* rk, __bf16* rv,
                                                         int64_t rk_sb, int64_t rk_sh, int64_t rv_sb, int64_t rv_sh,
-                                                        int64_t head, int64_t n, __bf16* ok, __bf16* ov) {
+                                                        int64_t head, int64_t n, int64_t keep_from, bool place,
+                                                        __bf16* ok, __bf16* ov) {
   const int lane = threadIdx.x & 63;
   const int64_t rows = n + a.L;
   const int64_t total = (int64_t)a.B * a.Hkv * rows;
@@ -342,31 +347,46 @@ __global__ __launch_bounds__(256) void ring_join_kernel(const AppendArgs a, cons
   for (int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); unit < total; unit += (int64_t)gridDim.x * 4) {
     const int64_t bh = unit / rows, u = unit % rows;
     const int b = (int)(bh / a.Hkv), h = (int)(bh % a.Hkv);
-    uint32_t w;
+    __bf16* ring = isv ? rv + (int64_t)b * rv_sb + (int64_t)h * rv_sh : rk + (int64_t)b * rk_sb + (int64_t)h * rk_sh;
+    const auto chunk_row = [&](int64_t j) {
+      float x0, x1;
+      load2_as_float(src, row_base(src, b, h, (int)j) + 2 * lane, x0, x1);
+      const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+      return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    };
+    uint32_t* dst = (uint32_t*)((isv ? ov : ok) + unit * HEAD_DIM + 2 * lane);
     if (u < n) {
       const int64_t slot = (head + u) % a.cap;
-      const __bf16* ring = isv ? rv + (int64_t)b * rv_sb + (int64_t)h * rv_sh : rk + (int64_t)b * rk_sb + (int64_t)h * rk_sh;
-      w = *(const uint32_t*)(ring + slot * HEAD_DIM + 2 * lane);
+      uint32_t* rs = (uint32_t*)(ring + slot * HEAD_DIM + 2 * lane);
+      *dst = *rs;  // the old token's bytes are stored before the slot is rewritten
+      if (place) {
+        // the chunk row landing on this slot, if any: j >= keep_from with
+        // a.offset + j = slot (mod capacity)
+        const int64_t j = keep_from + ((slot - (a.offset + keep_from)) % a.cap + a.cap) % a.cap;
+        if (j < a.L) *rs = chunk_row(j);
+      }
     } else {
-      float x0, x1;
-      load2_as_float(src, row_base(src, b, h, (int)(u - n)) + 2 * lane, x0, x1);
-      const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
-      w = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+      const int64_t j = u - n;
+      const uint32_t w = chunk_row(j);
+      *dst = w;
+      if (place && j >= keep_from) {
+        const int64_t slot = (a.offset + j) % a.cap;
+        if ((slot - head + a.cap) % a.cap >= n) *(uint32_t*)(ring + slot * HEAD_DIM + 2 * lane) = w;  // not held
+      }
     }
-    *(uint32_t*)((isv ? ov : ok) + unit * HEAD_DIM + 2 * lane) = w;
   }
 }
 
 }  // namespace
 
-hipError_t launch_ring_join_bf16(const AppendArgs& a, const void* rk, const void* rv, int64_t rk_sb, int64_t rk_sh,
-                                 int64_t rv_sb, int64_t rv_sh, int64_t head, int64_t n, void* ok, void* ov,
-                                 hipStream_t stream) {
+hipError_t launch_ring_join_bf16(const AppendArgs& a, void* rk, void* rv, int64_t rk_sb, int64_t rk_sh,
+                                 int64_t rv_sb, int64_t rv_sh, int64_t head, int64_t n, int64_t keep_from, bool place,
+                                 void* ok, void* ov, hipStream_t stream) {
   const int64_t rows = (int64_t)a.B * a.Hkv * (n + a.L);
   const int64_t wgs = (rows + 3) / 4;
   const unsigned grid_x = (unsigned)(wgs < (1 << 20) ? (wgs > 0 ? wgs : 1) : (1 << 20));  // the kernel strides over rows
-  hipLaunchKernelGGL(ring_join_kernel, dim3(grid_x, 2), dim3(256), 0, stream, a, (const __bf16*)rk,
-                     (const __bf16*)rv, rk_sb, rk_sh, rv_sb, rv_sh, head, n, (__bf16*)ok, (__bf16*)ov);
+  hipLaunchKernelGGL(ring_join_kernel, dim3(grid_x, 2), dim3(256), 0, stream, a, (__bf16*)rk, (__bf16*)rv, rk_sb,
+                     rk_sh, rv_sb, rv_sh, head, n, keep_from, place, (__bf16*)ok, (__bf16*)ov);
   return hipGetLastError();
 }
 

@@ -154,9 +154,9 @@ hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stre
 hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream);
 hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream);
 size_t q4_gemv_lds_bytes(int M, int64_t K);
-hipError_t launch_ring_join_bf16(const AppendArgs& a, const void* rk, const void* rv, int64_t rk_sb, int64_t rk_sh,
-                                 int64_t rv_sb, int64_t rv_sh, int64_t head, int64_t n, void* ok, void* ov,
-                                 hipStream_t stream);
+hipError_t launch_ring_join_bf16(const AppendArgs& a, void* rk, void* rv, int64_t rk_sb, int64_t rk_sh,
+                                 int64_t rv_sb, int64_t rv_sh, int64_t head, int64_t n, int64_t keep_from, bool place,
+                                 void* ok, void* ov, hipStream_t stream);
 hipError_t launch_write_bf16(const AppendArgs& a, int64_t k_sb, int64_t k_sh, int64_t v_sb, int64_t v_sh,
                              hipStream_t stream);
 

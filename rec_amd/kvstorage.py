@@ -338,7 +338,8 @@ class FixedSlidingKVCache:
             self.offset += 1
             n = self.size()
             return self.keys[:, :, :n], self.values[:, :, :n]
-        # the held window in order, then the chunk: one gather launch
+        # the held window in order, then the chunk, and the chunk's last
+        # rows into their slots: one launch
         n = self.size()
         head = self.offset % self.capacity if self.offset > self.capacity else 0
         attend_k = torch.empty((B, H, n + L, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
@@ -347,14 +348,12 @@ class FixedSlidingKVCache:
         v, vsb, vsh, vst = _stride3(values)
         rc = _lib.load().rec_ring_join_bf16(
             self.keys.data_ptr(), self.values.data_ptr(), self.keys.stride(0), self.keys.stride(1),
-            self.values.stride(0), self.values.stride(1), self.capacity, head, n,
+            self.values.stride(0), self.values.stride(1), self.capacity, head, n, self.offset, 1,
             k.data_ptr(), v.data_ptr(), _DTYPES[keys.dtype], ksb, ksh, kst, vsb, vsh, vst,
             attend_k.data_ptr(), attend_v.data_ptr(), B, H, L, HEAD_DIM,
             torch.cuda.current_stream(self.device).cuda_stream,
         )
-        _lib.check(rc, "rec_ring_join_bf16")
-        keep = min(L, self.capacity)
-        self._place(keys[:, :, L - keep:], values[:, :, L - keep:], self.offset + L)
+        _lib.check(rc, "rec_ring_join_bf16")  # the chunk's last rows are in their slots too
         self.offset += L
         return attend_k, attend_v
 

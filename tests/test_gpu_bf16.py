@@ -345,7 +345,8 @@ def test_ring_join_bit_exact(gpu, dtype):
     """rec_ring_join_bf16 (FixedSlidingKVCache.update_and_fetch of a chunk):
     the held window in sequence order, then the chunk rounded to bf16, equal
     bit for bit to joining the same tokens of the full sequence, before and
-    after the ring wraps and for chunks longer than the window."""
+    after the ring wraps and for chunks longer than the window; the ring
+    then holds the last window of tokens (placed by the same launch)."""
     from rec_amd import FixedSlidingKVCache
 
     B, Hkv, W = 2, 3, 100
@@ -365,4 +366,11 @@ def test_ring_join_bit_exact(gpu, dtype):
             want_v = v[:, :, end - held - L:end].to(torch.bfloat16)
             assert torch.equal(kk.view(torch.int16), want_k.contiguous().view(torch.int16)), f"K at {pos}+{L}"
             assert torch.equal(vv.view(torch.int16), want_v.contiguous().view(torch.int16)), f"V at {pos}+{L}"
+        # the ring afterwards holds the last min(end, W) tokens
+        wk, wv = cache.window()
+        hold = min(end, W)
+        assert torch.equal(wk.contiguous().view(torch.int16),
+                           k[:, :, end - hold:end].to(torch.bfloat16).contiguous().view(torch.int16)), f"ring K at {end}"
+        assert torch.equal(wv.contiguous().view(torch.int16),
+                           v[:, :, end - hold:end].to(torch.bfloat16).contiguous().view(torch.int16)), f"ring V at {end}"
         pos = end
