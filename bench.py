@@ -643,7 +643,7 @@ def run_sliding(steps, seed, window=513, held=4096, chunk=512):
         chunk_tokens=chunk,
         chunk_us=round(out["chunk"], 3),
         note="FixedSlidingKVCache (bf16 ring, 513-token window as the reference's sliding layers), through "
-             "attend(): decode = token write + attention over the window + merge; chunk = 512 tokens written "
+             "attend(): decode = token written into its slot by the attention launch + merge; chunk = 512 tokens written "
              "into the ring, then attention over the window in order plus the chunk under the causal window mask; "
              "both latency-bound (the window is 513 tokens)",
     )

@@ -277,6 +277,24 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     void* workspace, size_t workspace_bytes, float* out, void* stream);
 
 /*
+ * rec_decode_bf16_ring: one decode step of a sliding-window ring (token p of
+ * the sequence in slot p mod capacity): the new token (k_new / v_new, both
+ * required) is written into `slot` and the query attends over the T
+ * occupied slots — softmax is order-free, so the slots are read as they lie.
+ * Arguments otherwise as rec_decode_bf16; 0 <= slot < T.
+ * Replaces FixedSlidingKVCache.update_and_fetch of one token and the
+ * attention over it, engine/src/rec_mlx/cache.py:227-247 and
+ * engine/src/rec_mlx/model.py:204-211.
+ */
+int rec_decode_bf16_ring(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
+                         const void* k_new, const void* v_new, int new_dtype,
+                         int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh,
+                         void* k, int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh,
+                         const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
+                         int64_t capacity, int64_t slot, int splits, void* workspace,
+                         size_t workspace_bytes, float* out, void* stream);
+
+/*
  * Dequantize cache rows [0, T) of any format (k_bits / v_bits as rec_kv_append)
  * into bf16 K and V tensors (B, Hkv, T, 128), contiguous and 16-byte aligned:
  * x̂ formed in float32 (int8 q*s, uint4 (q - z)*s, affine q*s + b), rounded to

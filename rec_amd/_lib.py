@@ -88,6 +88,15 @@ SIGNATURES["rec_decode_bf16"] = (
         _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _p, _p,
     ],
 )
+SIGNATURES["rec_decode_bf16_ring"] = (
+    _i,
+    [
+        _p, _i, _i64, _i64,  # q
+        _p, _p, _i, _i64, _i64, _i64, _i64,  # new k/v
+        _p, _i64, _i64, _p, _i64, _i64,  # the ring's K, V
+        _p, _f, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p, _sz, _p, _p,  # ... T, capacity, slot, splits ...
+    ],
+)
 
 SIGNATURES["rec_kv_dequant_bf16"] = (_i, [_i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i64, _i64, _p, _p, _p])
 SIGNATURES["rec_prefill_bf16"] = (

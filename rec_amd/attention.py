@@ -239,7 +239,7 @@ def _bf16_kv_ok(t: torch.Tensor) -> bool:
 
 
 def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=None, v_new=None, T=None,
-                        capacity=None):
+                        capacity=None, slot=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv = keys.shape[1]
@@ -259,13 +259,14 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
     else:
         new = (k_new.data_ptr(), v_new.data_ptr(), _DTYPES[k_new.dtype], k_new.stride(0), k_new.stride(1),
                v_new.stride(0), v_new.stride(1))
-    rc = lib.rec_decode_bf16(
-        q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), *new,
-        keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
-        _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity), int(splits), ws.data_ptr(), ws.numel(),
-        out.data_ptr(), stream,
-    )
-    _lib.check(rc, "rec_decode_bf16")
+    head = (q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), *new,
+            keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
+            _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity))
+    tail = (int(splits), ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
+    if slot is None:
+        _lib.check(lib.rec_decode_bf16(*head, *tail), "rec_decode_bf16")
+    else:  # a ring step: the new token goes to `slot`
+        _lib.check(lib.rec_decode_bf16_ring(*head, int(slot), *tail), "rec_decode_bf16_ring")
 
 
 def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out, splits=0):
@@ -395,6 +396,25 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         # a new token goes to its ring slot and decode attends over the valid
         # slots (order-free); a chunk attends over the ring in order plus
         # itself, causally within the window
+        if L == 1 and fused:
+            # one launch pair: the token written into its slot by the split
+            # that reads it, attention over the occupied slots (order-free)
+            if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
+                raise ValueError("a fused decode step takes one new K/V token of a float dtype")
+            if tuple(keys.shape[:2]) != tuple(cache.keys.shape[:2]) or B != cache.keys.shape[0] \
+                    or Hq % cache.keys.shape[1] != 0:
+                raise ValueError(f"queries (B={B}, Hq={Hq}) / new keys {tuple(keys.shape[:2])} do not match the ring "
+                                 f"{tuple(cache.keys.shape[:2])}")
+            slot = cache.offset % cache.capacity
+            n = min(cache.offset + 1, cache.capacity)
+            kn = keys if _rows_aligned(keys) else keys.contiguous()
+            vn = values if _rows_aligned(values) else values.contiguous()
+            out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+            _bf16_decode_launch(queries, cache.keys, cache.values, scale, sinks, splits, out, kn, vn, T=n,
+                                capacity=cache.capacity, slot=slot)
+            cache.offset += 1
+            out = out.view(B, Hq, 1, D)
+            return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
         k, v = cache.update_and_fetch(keys, values)
         if L == 1:
             return scaled_dot_product_attention(queries, k, v, scale, None, sinks, out_dtype=out_dtype, splits=splits)

@@ -648,11 +648,11 @@ int rec_ring_join_bf16(void* k_ring, void* v_ring, int64_t rk_sb, int64_t rk_sh,
                   "ring join launch");
 }
 
-int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
-                    int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k, int64_t k_sb,
-                    int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale, int B, int Hq,
-                    int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
-                    size_t workspace_bytes, float* out, void* stream) {
+static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
+                       int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k,
+                       int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks,
+                       float scale, int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
+                       void* workspace, size_t workspace_bytes, float* out, void* stream, int64_t new_pos) {
   int e;
   if ((e = check_dtype(q_dtype, "query"))) return e;
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
@@ -712,9 +712,33 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, cons
   a.S = S;
   a.span = span;
   a.t_split_end = t_split_end;
+  a.new_pos = new_pos;
   const int e1 = launched(launch_decode_bf16(a, (hipStream_t)stream), "bf16 decode launch");
   if (e1 != REC_OK) return e1;
   return launched(launch_decode_merge(a, (hipStream_t)stream), "merge launch");
+}
+
+int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
+                    int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k, int64_t k_sb,
+                    int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale, int B, int Hq,
+                    int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
+                    size_t workspace_bytes, float* out, void* stream) {
+  return decode_bf16(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, kn_sb, kn_sh, vn_sb, vn_sh, k, k_sb, k_sh, v,
+                     v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out,
+                     stream, T - 1);
+}
+
+int rec_decode_bf16_ring(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new,
+                         const void* v_new, int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh,
+                         void* k, int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh,
+                         const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
+                         int64_t capacity, int64_t slot, int splits, void* workspace, size_t workspace_bytes,
+                         float* out, void* stream) {
+  if (!k_new || !v_new) return fail(REC_EINVAL, "a ring decode step writes its new token: k_new and v_new are required");
+  if (slot < 0 || slot >= T) return fail(REC_EINVAL, "slot %lld outside the %lld occupied slots", (long long)slot, (long long)T);
+  return decode_bf16(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, kn_sb, kn_sh, vn_sb, vn_sh, k, k_sb, k_sh, v,
+                     v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out,
+                     stream, slot);
 }
 
 size_t rec_q4_packed_bytes(int64_t N, int64_t K) {

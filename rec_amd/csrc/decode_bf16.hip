@@ -186,10 +186,12 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, a.T * ROWB), rv = make_rsrc(vbase, a.T * ROWB);
   const __amdgpu_buffer_rsrc_t none = make_rsrc(kbase, 0);
 
-  // Fused write of the newest token (position T-1), before this split reads it.
-  if (tail) {
-    if (wave == 0) store_bf16_row_pair(a.knew, b, h, (void*)a.kq, a.k_sb, a.k_sh, a.T - 1, lane);
-    else if (wave == 1) store_bf16_row_pair(a.vnew, b, h, (void*)a.vq, a.v_sb, a.v_sh, a.T - 1, lane);
+  // Fused write of the newest token (position new_pos: T-1, or a ring slot),
+  // by the split whose range holds it, before that split reads it.  Ranges
+  // start on chunk boundaries, so no other split loads that position.
+  if (fused && t_begin <= a.new_pos && a.new_pos < t_end) {
+    if (wave == 0) store_bf16_row_pair(a.knew, b, h, (void*)a.kq, a.k_sb, a.k_sh, a.new_pos, lane);
+    else if (wave == 1) store_bf16_row_pair(a.vnew, b, h, (void*)a.vq, a.v_sb, a.v_sh, a.new_pos, lane);
     __threadfence_block();
     __syncthreads();
   }

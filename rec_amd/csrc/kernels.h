@@ -41,6 +41,7 @@ struct DecodeArgs {
   int S;     // number of splits
   int span;         // tokens per regular split (multiple of 32)
   int t_split_end;  // end of the regular splits; a fused append adds one split [t_split_end, T)
+  int64_t new_pos;  // bf16 fused write: the new token's position (T - 1, or its ring slot)
 };
 
 // P·V takes the V-scaled probabilities P' = p·s as an fp16 operand.  Rounded

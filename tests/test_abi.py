@@ -278,3 +278,18 @@ def test_stream_read_validation(lib):
     assert "multiple of 16" in _lib.last_error()
     assert lib.rec_stream_read(8, 1024, 256, 16, None) == _lib.REC_EALIGN
     assert lib.rec_stream_read(16, 1024, 0, 16, None) == _lib.REC_EINVAL
+
+
+def test_decode_bf16_ring_validation(lib):
+    """rec_decode_bf16_ring: the new token is required and its slot must be
+    one of the T occupied slots (checked before anything is launched)."""
+    def call(kn, slot, T=10):
+        return lib.rec_decode_bf16_ring(
+            16, 1, 0, 0, kn, kn, 1, 0, 0, 0, 0, 16, 0, 0, 16, 0, 0, None, 0.088, 1, 8, 1, 128, T, 64, slot, 0, 16,
+            1 << 30, 16, None,
+        )
+    assert call(None, 3) == _lib.REC_EINVAL
+    assert "required" in _lib.last_error()
+    assert call(16, 10) == _lib.REC_EINVAL
+    assert call(16, -1) == _lib.REC_EINVAL
+    assert "slot" in _lib.last_error()
