@@ -13,6 +13,13 @@ Reference semantics restated here (paths relative to the rec repository):
 * decode attention with sinks: ``engine/src/rec_mlx/model.py:108-139``
   (``quantized_attention_with_sinks``: scores = (q*scale)·k̂, optional mask,
   the per-head sink logit joins the softmax and is then dropped, out = P·v̂).
+* sink logits per call site: the quantized decode casts the per-head offsets
+  to float32 (``model.py:129``); the prefill branch over the quantized cache
+  and the SDPA call over the bf16 caches hand them over in the query dtype
+  (``sinks=self.softmax_offset.astype(q.dtype)``, ``model.py:202`` and
+  ``:211``), as the fused decoder reads them as bf16
+  (``kernels/megakernel.py:621,631``).  ``sink_logits`` / ``attention(...,
+  sink_dtype=...)`` restate that rounding.
 * masks: ``engine/src/rec_mlx/model.py:122-128`` ("causal" string →
   ``arange(kL-L, kL)[:, None] >= arange(kL)``; bool → where; float → add).
 * split-K flash decode and merge: ``engine/src/rec_mlx/kernels/megakernel.py``
@@ -87,6 +94,7 @@ __all__ = [
     "pack_int4",
     "unpack_int4",
     "attention",
+    "sink_logits",
     "split_k_decode",
     "split_k_decode_quantized",
     "causal_mask",
@@ -247,15 +255,41 @@ def _expand_mask(mask, L, T):
     return m
 
 
-def attention(q, k_hat, v_hat, scale, sinks=None, mask=None):
+def sink_logits(sinks, dtype="float32"):
+    """The sink logits a softmax sees after the call site's cast, as float64.
+
+    ``dtype`` is the type the call site casts the per-head offsets to:
+    ``"float32"`` for the quantized decode (``model.py:129``:
+    ``sinks.astype(mx.float32)``), the query dtype (``"bfloat16"`` or
+    ``"float16"``) for the prefill branch over the quantized cache and for the
+    SDPA call over the bf16 caches (``model.py:202,211``:
+    ``softmax_offset.astype(q.dtype)``).  Rounding is to nearest even.
+    """
+    s = np.asarray(sinks, np.float32)
+    if dtype == "float32":
+        r = s
+    elif dtype == "bfloat16":
+        r = bf16_rn(s)
+    elif dtype == "float16":
+        r = s.astype(np.float16).astype(np.float32)
+    else:
+        raise ValueError(f"unknown sink dtype {dtype!r}")
+    return np.asarray(r, np.float64)
+
+
+def attention(q, k_hat, v_hat, scale, sinks=None, mask=None, sink_dtype=None):
     """Textbook GQA attention with sinks in float64.
 
     ``q`` is ``(B, Hq, L, D)``, ``k_hat``/``v_hat`` are dequantized
     ``(B, Hkv, T, D)``; q-head h reads kv-head ``h // (Hq // Hkv)``
     (``model.py:111-116``).  Returns ``(B, Hq, L, D)`` float64.  A row whose
     denominator is zero (every key masked and no sink) returns zeros, like the
-    merge's ``z == 0`` branch (``megakernel.py:302-316``).
+    merge's ``z == 0`` branch (``megakernel.py:302-316``).  ``sink_dtype``,
+    when given, first rounds the sinks as the call site does
+    (:func:`sink_logits`); None takes them as given.
     """
+    if sinks is not None and sink_dtype is not None:
+        sinks = sink_logits(sinks, sink_dtype)
     q = np.asarray(q, np.float64)
     k = np.asarray(k_hat, np.float64)
     v = np.asarray(v_hat, np.float64)

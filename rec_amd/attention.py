@@ -18,6 +18,7 @@ There is no CPU path: without the built HIP library every call raises.
 from __future__ import annotations
 
 import threading
+import weakref
 from typing import Optional
 
 import torch
@@ -60,10 +61,38 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
 
-def _sinks(sinks, Hq, device):
+_sink_lock = threading.Lock()
+_sink_copies = weakref.WeakKeyDictionary()
+
+
+def _sinks(sinks, Hq, device, dtype=None):
+    """The per-head sink logits as a float32 device vector, first rounded to
+    ``dtype`` when that is a 16-bit float type.
+
+    The reference casts the offsets to float32 in the quantized decode
+    (engine/src/rec_mlx/model.py:129) and to the query dtype where it calls
+    the fused SDPA (model.py:202, :211); ``attend`` passes the query dtype for
+    those paths.  A rounded copy is made once per tensor and in-place version
+    (kept while the tensor lives), so decode steps launch no cast kernel; a
+    copy first needed under HIP-graph capture is made inside the graph and not
+    kept (its bytes exist only once the graph runs).
+    """
     if sinks is None:
         return None
-    s = torch.as_tensor(sinks, device=device).to(torch.float32).reshape(-1).contiguous()
+    if dtype not in (torch.bfloat16, torch.float16):
+        s = torch.as_tensor(sinks, device=device).to(torch.float32).reshape(-1).contiguous()
+    else:
+        key = None
+        if isinstance(sinks, torch.Tensor):
+            key = (sinks._version, dtype, device)
+            with _sink_lock:
+                hit = _sink_copies.get(sinks)
+            if hit is not None and hit[0] == key and hit[1].numel() == Hq:
+                return hit[1]
+        s = torch.as_tensor(sinks, device=device).to(dtype).to(torch.float32).reshape(-1).contiguous()
+        if key is not None and not torch.cuda.is_current_stream_capturing():
+            with _sink_lock:
+                _sink_copies[sinks] = (key, s)
     if s.numel() != Hq:
         raise ValueError(f"sinks has {s.numel()} entries, expected {Hq}")
     return s
@@ -96,7 +125,7 @@ def _check_cache_shapes(queries, keys: QuantizedKV, values: QuantizedKV):
 
 
 def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, splits, out,
-                   k_new=None, v_new=None, T=None, capacity=None):
+                   k_new=None, v_new=None, T=None, capacity=None, sink_dtype=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv = keys.n_kv_heads
@@ -110,7 +139,7 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
     if splits is None or splits <= 0:
         splits = lib.rec_decode_default_splits(B, Hkv, T)
     ws = workspace(dev, B, Hkv, splits, stream)
-    sk = _sinks(sinks, Hq, dev)
+    sk = _sinks(sinks, Hq, dev, sink_dtype)
     common_tail = (
         _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity), int(splits),
         ws.data_ptr(), ws.numel(), out.data_ptr(), stream,
@@ -152,12 +181,13 @@ def prefill_workspace(device: torch.device, B: int, Hq: int, Hkv: int, L: int, s
         return ws
 
 
-def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out, splits=0, window=0):
+def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out, splits=0, window=0,
+                    sink_dtype=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     q = queries if queries.stride(-1) == 1 else queries.contiguous()
     dev = queries.device
-    sk = _sinks(sinks, Hq, dev)
+    sk = _sinks(sinks, Hq, dev, sink_dtype)
     stream = torch.cuda.current_stream(dev).cuda_stream
     ws = prefill_workspace(dev, B, Hq, keys.n_kv_heads, L, splits, stream)
     rc = lib.rec_prefill_attn(
@@ -191,7 +221,8 @@ def dequantize_kv(keys: QuantizedKV, values: QuantizedKV):
 
 
 def quantized_attention_with_sinks(
-    queries, keys, values, scale, mask, sinks, group_size, key_bits, value_bits, *, out_dtype=None, splits=None
+    queries, keys, values, scale, mask, sinks, group_size, key_bits, value_bits, *, out_dtype=None, splits=None,
+    sink_dtype=None,
 ):
     """GQA attention of ``queries`` ``(B, n_q, L, 128)`` over a quantized cache.
 
@@ -206,6 +237,10 @@ def quantized_attention_with_sinks(
     sliding-window mask is applied by the prefill kernel, also for one query
     (bf16/f16), which then sees the last ``window`` tokens.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
     (default: the query dtype, as the reference returns, model.py:132-139).
+    The sinks enter as float32 values at every ``L``, the cast this function
+    makes in the reference (model.py:129); ``sink_dtype`` (bf16/f16) rounds
+    them first, as the reference's prefill branch hands its SDPA the offsets
+    in the query dtype (model.py:202) -- :func:`attend` passes it for chunks.
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
@@ -221,7 +256,7 @@ def quantized_attention_with_sinks(
     causal, win = _mask_plan(mask, L, int(keys.length))
     if L == 1 and not win:
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
-        _decode_launch(queries, keys, values, scale, sinks, splits, out)
+        _decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype)
         out = out.view(B, Hq, 1, D)
     else:
         # the L queries are the newest L cached tokens (model.py:122-125)
@@ -230,7 +265,7 @@ def quantized_attention_with_sinks(
         if queries.dtype not in (torch.bfloat16, torch.float16):
             raise NotImplementedError("prefill (and windowed) queries must be bf16 or f16 (the matrix-core input type)")
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
-        _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0, win)
+        _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0, win, sink_dtype)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 
@@ -239,7 +274,7 @@ def _bf16_kv_ok(t: torch.Tensor) -> bool:
 
 
 def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=None, v_new=None, T=None,
-                        capacity=None, slot=None):
+                        capacity=None, slot=None, sink_dtype=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv = keys.shape[1]
@@ -253,7 +288,7 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
     if splits is None or splits <= 0:
         splits = lib.rec_decode_default_splits(B, Hkv, T)
     ws = workspace(dev, B, Hkv, splits, stream)
-    sk = _sinks(sinks, Hq, dev)
+    sk = _sinks(sinks, Hq, dev, sink_dtype)
     if k_new is None:
         new = (None, None, _lib.REC_BF16, 0, 0, 0, 0)
     else:
@@ -269,14 +304,14 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
         _lib.check(lib.rec_decode_bf16_ring(*head, int(slot), *tail), "rec_decode_bf16_ring")
 
 
-def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out, splits=0):
+def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out, splits=0, sink_dtype=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv, T = keys.shape[1], keys.shape[2]
     if queries.dtype not in (torch.bfloat16, torch.float16):
         raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
     dev = queries.device
-    sk = _sinks(sinks, Hq, dev)
+    sk = _sinks(sinks, Hq, dev, sink_dtype)
     stream = torch.cuda.current_stream(dev).cuda_stream
     ws = prefill_workspace(dev, B, Hq, Hkv, L, splits, stream)
     rc = lib.rec_prefill_bf16(
@@ -340,7 +375,7 @@ def _mask_plan(mask, L, T):
 
 
 def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=None, *, out_dtype=None,
-                                 splits=None, window=None):
+                                 splits=None, window=None, sink_dtype=None):
     """Attention of ``queries`` ``(B, n_q, L, 128)`` over bf16 ``keys``/``values``
     ``(B, Hkv, T, 128)`` with token stride 128 (a :class:`FixedKVCache`'s views,
     or the keys a :class:`FixedSlidingKVCache` returns), the per-head ``sinks``
@@ -348,7 +383,10 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
     caches (model.py:204-211, the fused SDPA's sinks argument).  One query
     token decodes; ``L > 1`` queries are the newest ``L`` of the ``T`` keys,
     under ``mask`` None, "causal" or a causal (sliding-window) boolean array;
-    ``window`` limits a causal mask to the last ``window`` keys.
+    ``window`` limits a causal mask to the last ``window`` keys.  The sinks
+    are taken as given (as float32 values); ``sink_dtype`` (bf16/f16) rounds
+    them first -- the reference's caller hands them over in the query dtype
+    (model.py:211), and :func:`attend` passes it.
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
@@ -366,11 +404,11 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
         if win:  # one query sees the last `win` keys: attend over that slice
             keys, values = keys[:, :, T - win:], values[:, :, T - win:]
         out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
-        _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out)
+        _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype)
         out = out.view(B, Hq, 1, D)
     else:
         out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
-        _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0)
+        _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0, sink_dtype)
     return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
 
 
@@ -382,9 +420,17 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
     (quantized for a :class:`QuantizedKVCache`, stored as bf16 for a
     :class:`FixedKVCache`), then ``queries`` attend over the whole cache, the
     new tokens included.  A single decode token takes one fused launch.
+
+    Sinks as the reference's branches see them: float32 in the quantized
+    decode (model.py:129), rounded to the query dtype for chunks over the
+    quantized cache (model.py:202) and on every call over the bf16 caches
+    (model.py:211).  A :class:`FixedSlidingKVCache` applies its own window: a
+    single decode token takes a mask that keeps every held token (None, as its
+    ``make_mask`` returns), anything else raises NotImplementedError.
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
+    qdt = queries.dtype
     if queries.dtype not in (torch.bfloat16, torch.float16):
         # chunks, and a single query under a window over a quantized cache,
         # run on the matrix cores: refused here, before the append changes
@@ -396,6 +442,9 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         # a new token goes to its ring slot and decode attends over the valid
         # slots (order-free); a chunk attends over the ring in order plus
         # itself, causally within the window
+        # (for one query, "causal" or a causal array keeps every key: window 0)
+        if L == 1 and mask is not None and _mask_plan(mask, 1, min(cache.offset + 1, cache.capacity))[1]:
+            raise NotImplementedError("a decode step over the sliding ring sees every held token (mask None)")
         if L == 1 and fused:
             # one launch pair: the token written into its slot by the split
             # that reads it, attention over the occupied slots (order-free)
@@ -411,17 +460,20 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
             vn = values if _rows_aligned(values) else values.contiguous()
             out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
             _bf16_decode_launch(queries, cache.keys, cache.values, scale, sinks, splits, out, kn, vn, T=n,
-                                capacity=cache.capacity, slot=slot)
+                                capacity=cache.capacity, slot=slot, sink_dtype=qdt)
             cache.offset += 1
             out = out.view(B, Hq, 1, D)
             return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
         k, v = cache.update_and_fetch(keys, values)
         if L == 1:
-            return scaled_dot_product_attention(queries, k, v, scale, None, sinks, out_dtype=out_dtype, splits=splits)
+            return scaled_dot_product_attention(queries, k, v, scale, None, sinks, out_dtype=out_dtype, splits=splits,
+                                                sink_dtype=qdt)
         return scaled_dot_product_attention(queries, k, v, scale, "causal", sinks, out_dtype=out_dtype,
-                                            window=cache.window_size)
+                                            window=cache.window_size, sink_dtype=qdt)
     if isinstance(cache, FixedKVCache):
-        if fused and L == 1:
+        # the fused step attends over every token; any other single-query
+        # mask pattern (a window) takes the write, then the masked attention
+        if fused and L == 1 and (mask is None or not _mask_plan(mask, 1, cache.offset + 1)[1]):
             if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
                 raise ValueError("a fused decode step takes one new K/V token of a float dtype")
             st = cache.storage
@@ -435,12 +487,13 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
             vn = values if _rows_aligned(values) else values.contiguous()
             out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
             _bf16_decode_launch(queries, data[:, 0], data[:, 1], scale, sinks, splits, out, kn, vn, T=T,
-                                capacity=cache.storage.capacity)
+                                capacity=cache.storage.capacity, sink_dtype=qdt)
             cache.offset = T
             out = out.view(B, Hq, 1, D)
             return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
         k, v = cache.update_and_fetch(keys, values)
-        return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits)
+        return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits,
+                                            sink_dtype=qdt)
     # one query under a sliding window (a causal mask keeps every key) takes
     # the append, then the windowed prefill kernel
     if fused and L == 1 and not _mask_plan(mask, 1, cache.offset + 1)[1]:
@@ -470,4 +523,5 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
     k, v = cache.update_and_fetch(keys, values)
     return quantized_attention_with_sinks(queries, k, v, scale, mask, sinks, cache.group_size, cache.key_bits,
-                                          cache.value_bits, out_dtype=out_dtype, splits=splits)
+                                          cache.value_bits, out_dtype=out_dtype, splits=splits,
+                                          sink_dtype=qdt if L > 1 else None)

@@ -12,6 +12,7 @@ import shutil
 import subprocess
 import sys
 import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -44,19 +45,30 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the ROCm toolchain is required to build rec_amd")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into ``librec_amd.so`` (always rebuilds)."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    fd, tmp = tempfile.mkstemp(suffix=".so", dir=HERE, prefix=".librec_amd.")
-    os.close(fd)
-    cmd = [hipcc(), *HIPCC_FLAGS, *srcs, "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        os.unlink(tmp)
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-8000:]}")
-    os.replace(tmp, LIB)
+
+
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every HIP source into ``librec_amd.so`` (always rebuilds).
+
+    Each source compiles to its own object (its own device code object) in a
+    temporary directory, ``jobs`` at a time (default: one per source, at most
+    the CPUs this process may use), then one link makes the library."""
+    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    jobs = jobs or max(1, min(len(srcs), len(os.sched_getaffinity(0))))
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(dir=HERE, prefix=".build.") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.basename(s) + ".o") for s in srcs]
+        with ThreadPoolExecutor(jobs) as ex:
+            list(ex.map(lambda so: _run([hipcc(), *compile_flags, "-c", so[0], "-o", so[1]], verbose), zip(srcs, objs)))
+        tmp = os.path.join(tmpdir, "librec_amd.so")
+        _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+        os.replace(tmp, LIB)
     return LIB
 
 

@@ -15,7 +15,9 @@ Fixtures:
 * mixed_k8v4.npz — 8 query / 2 KV heads, 96 tokens, int8 K and uint4 V, 1%
   outlier channels x8.
 * prefill_causal.npz — 8 query / 1 KV head, 192 cached + 64 new causal queries,
-  int8 KV.
+  int8 KV; outputs with the sinks as float32 values (``out_sinks``, the
+  function of model.py:108-139) and rounded to the fp16 query dtype
+  (``out_sinks_qdtype``, the prefill branch of model.py:202).
 """
 
 import os
@@ -78,7 +80,10 @@ def prefill_fixture(path, seed, Hq, Hkv, P, L):
     kq, kh = _quant(k, 8)
     vq, vh = _quant(v, 8)
     out = O.attention(q, kh, vh, SCALE, sinks, "causal").astype(np.float32)
-    np.savez_compressed(path, q=q, k=k, v=v, sinks=sinks, out_sinks=out, prefix=P,
+    # the prefill branch of Attention.__call__ hands the sinks over in the
+    # query dtype (model.py:202)
+    out_q = O.attention(q, kh, vh, SCALE, sinks, "causal", sink_dtype="float16").astype(np.float32)
+    np.savez_compressed(path, q=q, k=k, v=v, sinks=sinks, out_sinks=out, out_sinks_qdtype=out_q, prefix=P,
                         **{f"k_{n}": a for n, a in kq.items()}, **{f"v_{n}": a for n, a in vq.items()})
 
 
@@ -90,4 +95,7 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["prefill"]:
+        prefill_fixture(os.path.join(HERE, "prefill_causal.npz"), 20261204, 8, 1, 192, 64)
+    else:
+        main()

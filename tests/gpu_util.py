@@ -82,3 +82,15 @@ def oracle_xhat(kv) -> np.ndarray:
         return O.dequantize_affine(c, f32(scales), f32(extra))
     z = None if extra is None else extra.cpu().numpy()
     return dequant(kv.bits, codes.cpu().numpy(), scales.cpu().numpy(), z)
+
+
+_DT_NAMES = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}
+
+
+def q_sinks(sinks, qdtype):
+    """The sink logits of a path that hands them over in the query dtype (the
+    prefill branch over the quantized cache and every call over the bf16
+    caches, model.py:202,211), as float64 NumPy; None stays None."""
+    if sinks is None:
+        return None
+    return O.sink_logits(f32(sinks), _DT_NAMES[qdtype])

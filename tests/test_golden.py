@@ -64,6 +64,12 @@ def test_prefill_fixture():
     kh, vh = O.dequantize_int8(f["k_codes"], f["k_scales"]), O.dequantize_int8(f["v_codes"], f["v_scales"])
     out = O.attention(f["q"], kh, vh, SCALE, f["sinks"], "causal").astype(np.float32)
     np.testing.assert_array_equal(out, f["out_sinks"])
+    out_q = O.attention(f["q"], kh, vh, SCALE, f["sinks"], "causal", sink_dtype="float16").astype(np.float32)
+    np.testing.assert_array_equal(out_q, f["out_sinks_qdtype"])
+    # the fp16-rounded sinks are torch's own cast of the stored float32 ones
+    s16 = torch.from_numpy(f["sinks"]).half().double().numpy()
+    np.testing.assert_array_equal(
+        O.attention(f["q"], kh, vh, SCALE, s16, "causal").astype(np.float32), f["out_sinks_qdtype"])
     # the last query row sees every key: equal to a plain decode over the whole cache
     last = O.attention(f["q"][:, :, -1:], kh, vh, SCALE, f["sinks"]).astype(np.float32)
     np.testing.assert_allclose(out[:, :, -1:], last, rtol=1e-6, atol=1e-7)

@@ -13,7 +13,7 @@ import torch
 
 import oracle as O
 from rec_amd import FixedKVCache, KVStorage, attend, scaled_dot_product_attention, synthetic
-from tests.gpu_util import SCALE, assert_close, f32
+from tests.gpu_util import SCALE, assert_close, f32, q_sinks
 
 pytestmark = pytest.mark.gpu
 
@@ -70,7 +70,7 @@ def test_fixed_kv_cache_prefill_then_fused_decode(gpu):
         out = attend(q, k[:, :, T - 1 : T], v[:, :, T - 1 : T], cache, SCALE, None, sinks, out_dtype=torch.float32)
         torch.cuda.synchronize()
         assert cache.offset == T
-        ref = O.attention(f32(q), bf16_np(k[:, :, :T]), bf16_np(v[:, :, :T]), SCALE, sinks=f32(sinks))
+        ref = O.attention(f32(q), bf16_np(k[:, :, :T]), bf16_np(v[:, :, :T]), SCALE, sinks=q_sinks(sinks, q.dtype))
         assert_close(f32(out), ref, f"step {step}")
     data = store.layer(1, cache.offset)
     np.testing.assert_array_equal(data[:, 0].float().cpu().numpy(), bf16_np(k))
@@ -188,13 +188,13 @@ def test_storage_grows_by_banks_without_moving(gpu):
     assert store.capacity == 2 * 65536 and [r.data_ptr() for r in store.regions] == base
     assert store.nbytes == 2 * (2 * Hkv * 2 * 65536 * 128 * 2)
     T = P + L
-    ref = O.attention(f32(q), f32(k[:, :, :T]), f32(v[:, :, :T]), SCALE, sinks=f32(sinks), mask="causal")
+    ref = O.attention(f32(q), f32(k[:, :, :T]), f32(v[:, :, :T]), SCALE, sinks=q_sinks(sinks, q.dtype), mask="causal")
     assert_close(f32(out), ref, "prefill chunk across the bank boundary")
     # one decode token after it
     q1 = synthetic.query(B, Hq, 1, 74, dtype=torch.bfloat16)
     out1 = attend(q1, k[:, :, T : T + 1], v[:, :, T : T + 1], cache, SCALE, None, sinks, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    ref1 = O.attention(f32(q1), f32(k[:, :, : T + 1]), f32(v[:, :, : T + 1]), SCALE, sinks=f32(sinks))
+    ref1 = O.attention(f32(q1), f32(k[:, :, : T + 1]), f32(v[:, :, : T + 1]), SCALE, sinks=q_sinks(sinks, q1.dtype))
     assert_close(f32(out1), ref1, "decode step after the bank boundary")
     data = store.layer(1, T + 1)
     assert torch.equal(data[:, 0], k) and torch.equal(data[:, 1], v)
@@ -237,7 +237,7 @@ def test_sliding_window_ring_decode(gpu):
         lo = max(0, pos - W)
         torch.cuda.synchronize()
         assert cache.size() == pos - lo
-        ref = O.attention(f32(q), bf16_np(k[:, :, lo:pos]), bf16_np(v[:, :, lo:pos]), SCALE, sinks=f32(sinks))
+        ref = O.attention(f32(q), bf16_np(k[:, :, lo:pos]), bf16_np(v[:, :, lo:pos]), SCALE, sinks=q_sinks(sinks, q.dtype))
         assert_close(f32(out), ref, f"step {step}")
     assert cache.make_mask(1) is None
     m = cache.make_mask(3, return_array=True)
@@ -278,7 +278,7 @@ def test_bf16_prefill_matches_oracle(gpu, case):
     out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert cache.offset == T
-    ref = O.attention(f32(q), bf16_np(k), bf16_np(v), SCALE, sinks=None if sinks is None else f32(sinks), mask=mask)
+    ref = O.attention(f32(q), bf16_np(k), bf16_np(v), SCALE, sinks=q_sinks(sinks, q.dtype), mask=mask)
     assert_close(f32(out), ref, f"case {case}")
 
 
@@ -335,7 +335,7 @@ def test_sliding_window_prefill_chunks(gpu):
         kk, vv = bf16_np(k[:, :, end - Tk : end]), bf16_np(v[:, :, end - Tk : end])
         qi = np.arange(Tk - L, Tk)[:, None]
         ki = np.arange(Tk)[None]
-        ref = O.attention(f32(q), kk, vv, SCALE, sinks=f32(sinks), mask=(qi >= ki) & (qi < ki + W))
+        ref = O.attention(f32(q), kk, vv, SCALE, sinks=q_sinks(sinks, q.dtype), mask=(qi >= ki) & (qi < ki + W))
         assert_close(f32(out), ref, f"chunk at {pos} of {L}")
         pos = end
 

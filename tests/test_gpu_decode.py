@@ -138,21 +138,36 @@ def test_unfused_equals_fused(gpu):
 
 @pytest.mark.parametrize("T", [32768, 258048])
 def test_long_context_int8(gpu, T):
-    """Full-size 32K / 252K int8 decode against the chunked CPU oracle."""
-    B, Hq, Hkv = 1, 32, 4
-    cache = QuantizedKVCache(32, 8, 8, max_tokens=T)
-    fill(cache, B, Hkv, T, seed=3, kind="outliers", frac=0.01)
-    q = synthetic.query(B, Hq, 1, seed=4)
-    sinks = torch.randn(Hq, device="cuda")
-    kq, vq = cache.keys_and_values()
-    out = quantized_attention_with_sinks(q, kq, vq, SCALE, None, sinks, 32, 8, 8, out_dtype=torch.float32)
+    """Full-size 32K / 252K int8 decode against the chunked CPU oracle: the
+    cache filled to T - 3, then three decode steps that each quantize one new
+    token into the cache inside the attention launch (the benchmarked step),
+    then the unfused attention over all T tokens."""
     from rec_amd import to_logical
 
-    kc, ksc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(kq))
-    vc, vsc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(vq))
-    cache_np = dict(k_bits=8, v_bits=8, kq=kc, ks=ksc, vq=vc, vs=vsc)
-    ref = O.split_k_decode_quantized(f32(q)[:, :, 0], cache_np, T, SCALE, f32(sinks), chunk=8192)
-    assert_close(f32(out)[:, :, 0], ref.astype(np.float64), f"T={T}")
+    B, Hq, Hkv = 1, 32, 4
+    cache = QuantizedKVCache(32, 8, 8, max_tokens=T)
+    fill(cache, B, Hkv, T - 3, seed=3, kind="outliers", frac=0.01)
+    sinks = torch.randn(Hq, device="cuda")
+    for step in range(3):
+        q = synthetic.query(B, Hq, 1, seed=4 + step)
+        kn = synthetic.kv((B, Hkv, 1, 128), 30 + step, kind="outliers", frac=0.01)
+        vn = synthetic.kv((B, Hkv, 1, 128), 40 + step, kind="outliers", frac=0.01)
+        print(f"T={T} fused step {step}", flush=True)
+        out = attend(q, kn, vn, cache, SCALE, None, sinks, out_dtype=torch.float32)
+        Ti = T - 2 + step
+        assert cache.offset == Ti
+        kq, vq = cache.keys_and_values()
+        kc, ksc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(kq))
+        vc, vsc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(vq))
+        for got, x in (((kc, ksc), kn), ((vc, vsc), vn)):  # the appended row, bit for bit
+            c, sc = O.quantize_int8(f32(x))
+            np.testing.assert_array_equal(got[0][:, :, Ti - 1 :], c)
+            np.testing.assert_array_equal(got[1][:, :, Ti - 1 :].view(np.uint16), sc.view(np.uint16))
+        cache_np = dict(k_bits=8, v_bits=8, kq=kc, ks=ksc, vq=vc, vs=vsc)
+        ref = O.split_k_decode_quantized(f32(q)[:, :, 0], cache_np, Ti, SCALE, f32(sinks), chunk=8192)
+        assert_close(f32(out)[:, :, 0], ref.astype(np.float64), f"T={Ti} fused step {step}")
+    out = quantized_attention_with_sinks(q, kq, vq, SCALE, None, sinks, 32, 8, 8, out_dtype=torch.float32)
+    assert_close(f32(out)[:, :, 0], ref.astype(np.float64), f"T={T} unfused")
 
 
 def test_repeated_launches_share_workspace(gpu):

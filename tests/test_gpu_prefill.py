@@ -13,7 +13,7 @@ import torch
 
 import oracle as O
 from rec_amd import QuantizedKVCache, attend, quantized_attention_with_sinks, synthetic, to_logical
-from tests.gpu_util import SCALE, assert_close, f32, oracle_quantize, dequant
+from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize, q_sinks
 
 pytestmark = pytest.mark.gpu
 
@@ -47,8 +47,9 @@ def test_prefill_matches_oracle(gpu, case):
     out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, "causal" if causal else None, sinks,
                  out_dtype=torch.float32)
     rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
-    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None if sinks is None else f32(sinks),
-                      "causal" if causal else None)
+    # chunks hand the sinks over in the query dtype (model.py:202); one token decodes (float32, model.py:129)
+    sk = q_sinks(sinks, q.dtype) if L > 1 else (None if sinks is None else f32(sinks))
+    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, sk, "causal" if causal else None)
     assert_close(f32(out), ref, f"case {case}")
 
 
@@ -62,14 +63,20 @@ def test_prefill_golden(gpu):
     cache = QuantizedKVCache(32, 8, 8)
     cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
     q = torch.from_numpy(g["q"]).to(dev)
-    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, "causal", torch.from_numpy(g["sinks"]).to(dev),
-                 out_dtype=torch.float32)
+    sinks = torch.from_numpy(g["sinks"]).to(dev)
+    # attend() is the prefill branch of Attention.__call__: sinks in the
+    # query dtype (model.py:202); quantized_attention_with_sinks keeps the
+    # function's float32 cast (model.py:129)
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, "causal", sinks, out_dtype=torch.float32)
+    kq_, vq_ = cache.keys_and_values()
+    out32 = quantized_attention_with_sinks(q, kq_, vq_, SCALE, "causal", sinks, 32, 8, 8, out_dtype=torch.float32)
+    assert_close(f32(out32), g["out_sinks"].astype(np.float64), "golden prefill, float32 sinks")
     kq, vq = cache.keys_and_values()
     for kv, p in ((kq, "k"), (vq, "v")):
         c, s, _ = (None if t is None else t.cpu().numpy() for t in to_logical(kv))
         np.testing.assert_array_equal(c, g[p + "_codes"])
         np.testing.assert_array_equal(s.view(np.uint16), g[p + "_scales"].view(np.uint16))
-    assert_close(f32(out), g["out_sinks"].astype(np.float64), "golden prefill")
+    assert_close(f32(out), g["out_sinks_qdtype"].astype(np.float64), "golden prefill")
 
 
 def test_chunked_prefill_then_decode(gpu):
@@ -86,7 +93,7 @@ def test_chunked_prefill_then_decode(gpu):
     for a in range(0, T, chunk):
         b = min(T, a + chunk)
         out = attend(q[:, :, a:b], k[:, :, a:b], v[:, :, a:b], cache, SCALE, "causal", sinks, out_dtype=torch.float32)
-        ref = O.attention(f32(q[:, :, a:b]), kh[:, :, :b], vh[:, :, :b], SCALE, f32(sinks), "causal")
+        ref = O.attention(f32(q[:, :, a:b]), kh[:, :, :b], vh[:, :, :b], SCALE, q_sinks(sinks, q.dtype), "causal")
         assert_close(f32(out), ref, f"chunk {a}:{b}")
     for t in range(T, T + 3):
         out = attend(q[:, :, t : t + 1], k[:, :, t : t + 1], v[:, :, t : t + 1], cache, SCALE, None, sinks,
@@ -118,7 +125,7 @@ def test_prefill_full_size_rows(gpu, Hq, Hkv, P, L, rows):
     kc, ksc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(kq))
     vc, vsc, _ = (t.cpu().numpy() if t is not None else None for t in to_logical(vq))
     del k, v
-    qf, of, sf = f32(q), f32(out), f32(sinks)
+    qf, of, sf = f32(q), f32(out), q_sinks(sinks, q.dtype).astype(np.float32)
     for i in rows:
         Ti = P + i + 1
         cache_np = dict(k_bits=8, v_bits=8, kq=kc[:, :, :Ti], ks=ksc[:, :, :Ti], vq=vc[:, :, :Ti], vs=vsc[:, :, :Ti])
@@ -157,7 +164,7 @@ def test_split_prefill_matches_oracle(gpu, case):
                  splits=splits or None)
     torch.cuda.synchronize()
     rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
-    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None if sinks is None else f32(sinks), mask)
+    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, q_sinks(sinks, q.dtype), mask)
     assert_close(f32(out), ref, f"case {case}")
 
 

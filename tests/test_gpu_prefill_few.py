@@ -14,7 +14,7 @@ import torch
 
 import oracle as O
 from rec_amd import MixedQuantizedKVCache, QuantizedKVCache, attend, synthetic
-from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize, oracle_xhat, prefill_side
+from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize, oracle_xhat, prefill_side, q_sinks
 
 pytestmark = pytest.mark.gpu
 
@@ -55,7 +55,7 @@ def test_few_query_prefill_matches_oracle(gpu, case):
                  splits=splits or None)
     torch.cuda.synchronize()
     rk, rv = oracle_quantize(f32(k), 8), oracle_quantize(f32(v), 8)
-    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, None if sinks is None else f32(sinks), mask)
+    ref = O.attention(f32(q), dequant(8, *rk), dequant(8, *rv), SCALE, q_sinks(sinks, q.dtype), mask)
     assert_close(f32(out), ref, f"case {case}")
 
 
@@ -110,5 +110,5 @@ def test_few_query_prefill_affine_matches_oracle(gpu, case):
     torch.cuda.synchronize()
     kv_k, kv_v = cache.keys_and_values()
     kh, vh = prefill_side(oracle_xhat(kv_k), kv_k, dtype), prefill_side(oracle_xhat(kv_v), kv_v, dtype)
-    ref = O.attention(f32(q), kh, vh, SCALE, None if sinks is None else f32(sinks), mask)
+    ref = O.attention(f32(q), kh, vh, SCALE, q_sinks(sinks, q.dtype), mask)
     assert_close(f32(out), ref, f"affine case {case}")

@@ -19,7 +19,7 @@ import torch
 
 import oracle as O
 from rec_amd import MixedQuantizedKVCache, QuantizedKVCache, attend, dequantize_kv, synthetic
-from tests.gpu_util import SCALE, assert_close, f32, oracle_xhat, prefill_side
+from tests.gpu_util import SCALE, assert_close, f32, oracle_xhat, prefill_side, q_sinks
 
 pytestmark = pytest.mark.gpu
 
@@ -81,7 +81,7 @@ def test_prefill_formats_match_oracle(gpu, case):
     torch.cuda.synchronize()
     kv_k, kv_v = cache.keys_and_values()
     kh, vh = prefill_side(oracle_xhat(kv_k), kv_k, dtype), prefill_side(oracle_xhat(kv_v), kv_v, dtype)
-    ref = O.attention(f32(q), kh, vh, SCALE, None if sinks is None else f32(sinks), mask)
+    ref = O.attention(f32(q), kh, vh, SCALE, q_sinks(sinks, q.dtype), mask)
     assert_close(f32(out), ref, f"case {case}")
 
 
@@ -100,7 +100,7 @@ def test_affine_chunked_prefill_then_decode(gpu):
         kv_k, kv_v = cache.keys_and_values()
         kh = prefill_side(oracle_xhat(kv_k), kv_k, torch.bfloat16)
         vh = prefill_side(oracle_xhat(kv_v), kv_v, torch.bfloat16)
-        ref = O.attention(f32(q[:, :, a:b]), kh, vh, SCALE, f32(sinks), "causal")
+        ref = O.attention(f32(q[:, :, a:b]), kh, vh, SCALE, q_sinks(sinks, q.dtype), "causal")
         assert_close(f32(out), ref, f"chunk [{a}, {b})")
     for t in range(T, T + steps):
         out = attend(q[:, :, t : t + 1], k[:, :, t : t + 1], v[:, :, t : t + 1], cache, SCALE, None, sinks,

@@ -21,7 +21,7 @@ import torch
 
 import oracle as O
 from rec_amd import QuantizedKVCache, attend, synthetic
-from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize, prefill_side
+from tests.gpu_util import SCALE, assert_close, dequant, f32, oracle_quantize, prefill_side, q_sinks
 
 pytestmark = pytest.mark.gpu
 
@@ -79,7 +79,7 @@ def test_large_v_scales_rising_scores(gpu, case):
     if L > 1:  # the prefill rounds 4-bit values to the query dtype
         kq, vq = cache.keys_and_values()
         kh, vh = prefill_side(kh, kq, q.dtype), prefill_side(vh, vq, q.dtype)
-    ref = O.attention(f32(q), kh, vh, SCALE, f32(sinks), "causal")
+    ref = O.attention(f32(q), kh, vh, SCALE, q_sinks(sinks, q.dtype), "causal")
     got = f32(out).astype(np.float64)
     assert np.all(np.isfinite(got)), "non-finite output"
     # An output here is a weighted mean of values up to ~65,000, so fp32

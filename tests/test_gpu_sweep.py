@@ -16,7 +16,7 @@ import torch
 import oracle as O
 from rec_amd import (FixedKVCache, KVStorage, MixedQuantizedKVCache, QuantizedKVCache, attend, synthetic,
                      to_logical)
-from tests.gpu_util import SCALE, assert_close, dequant, f32, prefill_side
+from tests.gpu_util import SCALE, assert_close, dequant, f32, prefill_side, q_sinks
 
 pytestmark = pytest.mark.gpu
 
@@ -93,5 +93,7 @@ def test_sweep(gpu, case):
         kh, vh = oracle_xhat(kv_k), oracle_xhat(kv_v)
         if L > 1:  # the prefill rounds 4-bit and affine values to the query dtype
             kh, vh = prefill_side(kh, kv_k, dt), prefill_side(vh, kv_v, dt)
-    ref = O.attention(f32(q), kh, vh, SCALE, None if sinks is None else f32(sinks), "causal")
+    # sinks in the query dtype for chunks and over the bf16 cache (model.py:202,211), float32 in the quantized decode
+    sk = q_sinks(sinks, dt) if (L > 1 or fmt == "bf16") else (None if sinks is None else f32(sinks))
+    ref = O.attention(f32(q), kh, vh, SCALE, sk, "causal")
     assert_close(f32(out), ref, f"case {case}")

@@ -299,6 +299,42 @@ def test_mutation_in_oracle_is_caught():
     assert not np.allclose(wrong, ref, rtol=1e-6, atol=1e-9)
 
 
+def _sinks_bf16_unrepresentable(rng, n):
+    """Sink logits with a 16-bit remainder under bf16: each is a bf16 value plus
+    a quarter of its last place or more, so rounding moves it visibly."""
+    base = torch.from_numpy(rng.uniform(-1.0, 3.0, n).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    ulp = np.abs(base) * 2.0**-7 + 2.0**-10
+    return (base + rng.uniform(0.3, 0.45, n).astype(np.float32) * ulp).astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_sink_logits_rounded_to_query_dtype_match_torch(dtype):
+    """The SDPA call sites hand the sinks over in the query dtype
+    (model.py:202,211).  On rows that see few keys, where the sink carries a
+    large share of the weight, the oracle's rounding must equal torch's own
+    cast of the sinks fed to torch SDPA, and the sinks taken as float32 (a
+    planted mistake: no rounding) must not."""
+    rng = np.random.default_rng(17)
+    B, Hq, Hkv, P, L = 1, 8, 2, 2, 6
+    kh, vh = _cache(rng, B, Hkv, P + L)
+    vh = vh * 8.0
+    q = rng.standard_normal((B, Hq, L, 128)).astype(np.float32)
+    sinks = _sinks_bf16_unrepresentable(rng, Hq)
+    tdt = getattr(torch, dtype)
+    cast = torch.from_numpy(sinks).to(tdt).double().numpy()
+    assert not np.array_equal(cast, sinks.astype(np.float64))
+    np.testing.assert_array_equal(O.sink_logits(sinks, dtype), cast)
+    ref = _torch_reference(q, kh, vh, 0.088, cast, "causal")
+    ours = O.attention(q, kh, vh, 0.088, sinks, "causal", sink_dtype=dtype)
+    np.testing.assert_allclose(ours, ref, rtol=1e-12, atol=1e-12)
+    planted = O.attention(q, kh, vh, 0.088, sinks, "causal", sink_dtype="float32")
+    # bf16 keeps 8 significant bits: the rounding moves outputs past the 2e-3
+    # tolerance; fp16 keeps 11, its rounding is smaller but still seen
+    assert np.abs(planted - ref).max() > (2e-3 if dtype == "bfloat16" else 1e-4)
+    # float32 is the quantized decode's cast (model.py:129): values as given
+    np.testing.assert_array_equal(O.sink_logits(sinks, "float32"), sinks.astype(np.float64))
+
+
 # ---------------------------------------------------------------------------
 # int4 group-64 GEMV
 
