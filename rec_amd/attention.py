@@ -62,7 +62,14 @@ def _ptr(t: Optional[torch.Tensor]):
 
 
 _sink_lock = threading.Lock()
-_sink_copies = weakref.WeakKeyDictionary()
+_sink_copies = {}  # id(sinks tensor) -> (weak reference to it, (version, dtype, device), rounded copy)
+
+
+def _forget_sinks(i):
+    def drop(_ref):
+        with _sink_lock:
+            _sink_copies.pop(i, None)
+    return drop
 
 
 def _sinks(sinks, Hq, device, dtype=None):
@@ -84,15 +91,16 @@ def _sinks(sinks, Hq, device, dtype=None):
     else:
         key = None
         if isinstance(sinks, torch.Tensor):
-            key = (sinks._version, dtype, device)
+            key = (sinks._version, dtype, torch.device(device))
             with _sink_lock:
-                hit = _sink_copies.get(sinks)
-            if hit is not None and hit[0] == key and hit[1].numel() == Hq:
-                return hit[1]
+                hit = _sink_copies.get(id(sinks))
+            if hit is not None and hit[0]() is sinks and hit[1] == key and hit[2].numel() == Hq:
+                return hit[2]
         s = torch.as_tensor(sinks, device=device).to(dtype).to(torch.float32).reshape(-1).contiguous()
-        if key is not None and not torch.cuda.is_current_stream_capturing():
+        if key is not None and not (s.is_cuda and torch.cuda.is_current_stream_capturing()):
+            i = id(sinks)
             with _sink_lock:
-                _sink_copies[sinks] = (key, s)
+                _sink_copies[i] = (weakref.ref(sinks, _forget_sinks(i)), key, s)
     if s.numel() != Hq:
         raise ValueError(f"sinks has {s.numel()} entries, expected {Hq}")
     return s

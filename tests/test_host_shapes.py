@@ -93,3 +93,28 @@ def test_mask_plan_refuses_other_patterns():
         _mask_plan(keep[:, :-1], L, T)
     with pytest.raises(NotImplementedError):
         _mask_plan(np.zeros((L, T), np.int32), L, T)
+
+
+def test_sink_rounding_on_the_host():
+    """The sinks the SDPA-style paths see: rounded to the query dtype once per
+    tensor version (a kept copy, so decode steps launch no cast), float32 as
+    given otherwise; an in-place change makes a new copy."""
+    from rec_amd.attention import _sink_copies, _sinks
+
+    s = torch.tensor([2.5 + 0.4 * 2.0**-6, -1.0, 3.0 + 2.0**-9, 0.1])
+    f = _sinks(s, 4, "cpu")
+    assert torch.equal(f, s)
+    b = _sinks(s, 4, "cpu", torch.bfloat16)
+    assert torch.equal(b, s.to(torch.bfloat16).float()) and not torch.equal(b, s)
+    assert _sinks(s, 4, "cpu", torch.bfloat16) is b  # the kept copy
+    h = _sinks(s, 4, "cpu", torch.float16)
+    assert torch.equal(h, s.half().float()) and h is not b
+    s.mul_(2.0)
+    b2 = _sinks(s, 4, "cpu", torch.bfloat16)
+    assert b2 is not b and torch.equal(b2, s.to(torch.bfloat16).float())
+    n = len(_sink_copies)
+    del s, f  # (f is s: float32 sinks pass through as they are)
+    assert len(_sink_copies) == n - 1  # dropped with the tensor
+    assert torch.equal(_sinks([0.3, 7.0], 2, "cpu", torch.bfloat16), torch.tensor([0.3, 7.0]).bfloat16().float())
+    with pytest.raises(ValueError, match="expected 8"):
+        _sinks(torch.zeros(4), 8, "cpu", torch.bfloat16)
