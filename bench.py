@@ -65,21 +65,22 @@ def row_bytes(bits, is_v=False):
     return D + 2 if bits == 8 else D // 2 + 16  # codes + fp16 scale (+ zero-points)
 
 
-def step_bytes(T, B=1, k_bits=8, v_bits=8, output=True):
+def step_bytes(T, B=1, k_bits=8, v_bits=8, output=True, hq=HQ, hkv=HKV):
     """Algorithmic HBM bytes of one decode step over T tokens: K/V codes and
     scales read once, query read, appended token read (fp16) and written
     (codes + scale), fp32 output written (by the merge when output=False)."""
-    kv = B * T * HKV * (row_bytes(k_bits) + row_bytes(v_bits, True))
-    q = B * HQ * D * 2
-    out = B * HQ * D * 4 if output else 0
-    append = B * HKV * (2 * D * 2 + row_bytes(k_bits) + row_bytes(v_bits, True))
+    kv = B * T * hkv * (row_bytes(k_bits) + row_bytes(v_bits, True))
+    q = B * hq * D * 2
+    out = B * hq * D * 4 if output else 0
+    append = B * hkv * (2 * D * 2 + row_bytes(k_bits) + row_bytes(v_bits, True))
     return kv + q + out + append
 
 
 class DecodeWorkload:
     """R cache instances of one context length plus a pool of new tokens."""
 
-    def __init__(self, T, R, total_steps, seed, splits=0, bits=8, kind="outliers", frac=0.01, batch=1):
+    def __init__(self, T, R, total_steps, seed, splits=0, bits=8, kind="outliers", frac=0.01, batch=1,
+                 hq=HQ, hkv=HKV):
         import torch
 
         import rec_amd
@@ -87,7 +88,8 @@ class DecodeWorkload:
 
         self.torch, self.lib = torch, rec_amd.library()
         self.T, self.R, self.splits, self.bits, self.B = T, R, splits, bits, batch
-        B = batch
+        self.hq, self.hkv = hq, hkv
+        B, HQ, HKV = batch, hq, hkv
         counts = [len(range(i, total_steps, R)) for i in range(R)]
         self.caches = []
         for i in range(R):
@@ -135,7 +137,7 @@ class DecodeWorkload:
             kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
-            self.sinks.data_ptr(), SCALE, self.B, HQ, HKV, D, T, c.capacity, self.splits,
+            self.sinks.data_ptr(), SCALE, self.B, self.hq, self.hkv, D, T, c.capacity, self.splits,
             self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), stream,
         )
         _lib.check(rc, "decode step")
@@ -156,7 +158,7 @@ class DecodeWorkload:
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
-            self.sinks.data_ptr(), SCALE, self.B, HQ, HKV, D, c.offset, c.capacity, self.splits,
+            self.sinks.data_ptr(), SCALE, self.B, self.hq, self.hkv, D, c.offset, c.capacity, self.splits,
             self.ws.data_ptr(), self.ws.numel(), self.out.data_ptr(), self.torch.cuda.current_stream().cuda_stream,
         )
         _lib.check(rc, "decode attention")
@@ -176,7 +178,7 @@ class DecodeWorkload:
             vn.stride(0), vn.stride(1), vn.stride(2),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
-            self.B, HKV, 1, D, c.offset - 1, c.capacity, self.torch.cuda.current_stream().cuda_stream,
+            self.B, self.hkv, 1, D, c.offset - 1, c.capacity, self.torch.cuda.current_stream().cuda_stream,
         )
         _lib.check(rc, "append")
 
@@ -273,12 +275,12 @@ def _median_timed(torch, graph, n, reps=5):
     return float(np.median(_replay_timed(torch, graph, n, reps)))
 
 
-def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, batch=1, reps=5):
+def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, batch=1, reps=5, hq=HQ, hkv=HKV):
     import torch
 
     total = warmup + 2 * steps
     log(f"T={T}: building {R} cache instances")
-    w = DecodeWorkload(T, R, total, seed, bits=bits, kind=kind, frac=frac, batch=batch)
+    w = DecodeWorkload(T, R, total, seed, bits=bits, kind=kind, frac=frac, batch=batch, hq=hq, hkv=hkv)
     log(f"T={T}: warm-up {warmup} steps")
     for s in range(warmup):
         w.step(s)
@@ -315,8 +317,9 @@ def run_decode(T, R, steps, warmup, seed, bits=8, kind="outliers", frac=0.01, ba
     log(f"T={T}: {steps} steps, {ms_per_step * 1e3:.2f} us/step (replays p10/p50/p90 {p10 * 1e3:.2f}/"
         f"{p50 * 1e3:.2f}/{p90 * 1e3:.2f}); attention kernel {kernel_ms * 1e3:.2f} us; unfused: attention "
         f"{att_ms * 1e3:.2f} us + append {app_ms * 1e3:.2f} us")
-    bytes_step = float(np.mean([step_bytes(t, batch, k_bits=bits, v_bits=bits) for t in step_T]))
-    bytes_kernel = float(np.mean([step_bytes(t, batch, k_bits=bits, v_bits=bits, output=False) for t in kern_T]))
+    bytes_step = float(np.mean([step_bytes(t, batch, k_bits=bits, v_bits=bits, hq=hq, hkv=hkv) for t in step_T]))
+    bytes_kernel = float(np.mean([step_bytes(t, batch, k_bits=bits, v_bits=bits, output=False, hq=hq, hkv=hkv)
+                                  for t in kern_T]))
     res = dict(
         T=T,
         instances=R,
@@ -701,8 +704,9 @@ def run_sdpa_yardstick(P, L, steps):
 def run_read_floor(steps):
     """The one-launch read floor of this part: rec_stream_read (a plain
     streaming read, 1 KB per wavefront and load, four loads in flight per
-    lane) over the K/V bytes of the 32K and 252K int8 configurations, rotating
-    buffers of >= 1 GB in all; the best of five workgroup counts."""
+    lane) over the K/V bytes of the 32K and 252K int8 configurations and the
+    131K uint4 one, rotating buffers of >= 1 GB in all; the best of five
+    workgroup counts."""
     import torch
 
     import rec_amd
@@ -710,8 +714,9 @@ def run_read_floor(steps):
     lib = rec_amd.library()
     out = torch.zeros(65536, dtype=torch.int32, device="cuda")
     res = {}
-    for name, T, R, n in (("32k", 32768, 32, steps), ("252k", 258048, 4, max(16, steps // 8))):
-        nbytes = T * HKV * 2 * (D + 2)
+    for name, T, R, n, bits in (("32k", 32768, 32, steps, 8), ("252k", 258048, 4, max(16, steps // 8), 8),
+                                ("131k_int4", 131072, 12, max(16, steps // 8), 4)):
+        nbytes = T * HKV * (row_bytes(bits) + row_bytes(bits, True))
         bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(R)]
         best = None
         for wg in (256, 512, 1024, 2048, 4096):
@@ -762,8 +767,11 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(T, seed, budget_s=10.0):
-    """The oracle's split-K decode over one 32K instance on the host cores."""
+def cpu_baseline(T, seed, budget_s=10.0, bits=8, hq=HQ, hkv=HKV, kind="outliers", frac=0.01, label="32K"):
+    """The oracle's split-K decode over one cache instance of the configuration
+    on the host cores: each step quantizes the new token (the oracle's
+    quantizer) into the last slot and runs the float32 split-K over 4096-token
+    chunks (chunked dequantization, attention with sinks, merge)."""
     import torch
 
     import oracle as O
@@ -775,35 +783,38 @@ def cpu_baseline(T, seed, budget_s=10.0):
     except ImportError:  # pragma: no cover
         threadpool_limits = None
     cores = host_cores()
-    c = rec_amd.QuantizedKVCache(32, 8, 8, max_tokens=T)
-    k = synthetic.kv((1, HKV, T - 1, D), seed, kind="outliers", frac=0.01)
-    v = synthetic.kv((1, HKV, T - 1, D), seed + 1, kind="outliers", frac=0.01)
+    c = rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T)
+    k = synthetic.kv((1, hkv, T - 1, D), seed, kind=kind, frac=frac)
+    v = synthetic.kv((1, hkv, T - 1, D), seed + 1, kind=kind, frac=frac)
     kq, vq = c.update_and_fetch(k, v)
-    kc, ksc = (x.cpu().numpy() for x in rec_amd.to_logical(kq)[:2])
-    vc, vsc = (x.cpu().numpy() for x in rec_amd.to_logical(vq)[:2])
-    del k, v, c
+    logical = [[None if x is None else x.cpu().numpy() for x in rec_amd.to_logical(t)] for t in (kq, vq)]
+    del k, v, c, kq, vq
     torch.cuda.empty_cache()
+    bufs = {}
+    for p, (codes, scales, zeros) in zip("kv", logical):
+        for name, a in (("q", codes), ("s", scales), ("z", zeros)):
+            if a is None:
+                continue
+            full = np.zeros(a.shape[:2] + (T,) + a.shape[3:], a.dtype)
+            full[:, :, : T - 1] = a
+            bufs[p + name] = full
+    del logical
+    quant = O.quantize_int8 if bits == 8 else (lambda x: O.quantize_int4(x, 32))
     rng = np.random.default_rng(seed)
-    kbuf = np.zeros((1, HKV, T, D), np.int8)
-    vbuf = np.zeros((1, HKV, T, D), np.int8)
-    ksb = np.zeros((1, HKV, T), np.float16)
-    vsb = np.zeros((1, HKV, T), np.float16)
-    kbuf[:, :, : T - 1], vbuf[:, :, : T - 1], ksb[:, :, : T - 1], vsb[:, :, : T - 1] = kc, vc, ksc, vsc
-    sinks = rng.standard_normal(HQ).astype(np.float32)
+    sinks = rng.standard_normal(hq).astype(np.float32)
     times = []
     limiter = threadpool_limits(1) if threadpool_limits else None
     try:
         start = time.perf_counter()
         while True:
-            q = rng.standard_normal((1, HQ, D)).astype(np.float16).astype(np.float32)
-            kn = rng.standard_normal((1, HKV, 1, D)).astype(np.float16)
-            vn = rng.standard_normal((1, HKV, 1, D)).astype(np.float16)
+            q = rng.standard_normal((1, hq, D)).astype(np.float16).astype(np.float32)
+            kn = rng.standard_normal((1, hkv, 1, D)).astype(np.float16)
+            vn = rng.standard_normal((1, hkv, 1, D)).astype(np.float16)
             t0 = time.perf_counter()
-            a, b = O.quantize_int8(kn)
-            kbuf[:, :, T - 1 :], ksb[:, :, T - 1 :] = a, b
-            a, b = O.quantize_int8(vn)
-            vbuf[:, :, T - 1 :], vsb[:, :, T - 1 :] = a, b
-            cache = dict(k_bits=8, v_bits=8, kq=kbuf, ks=ksb, vq=vbuf, vs=vsb)
+            for p, x in (("k", kn), ("v", vn)):
+                for name, a in zip("qsz", quant(x)):
+                    bufs[p + name][:, :, T - 1 :] = a
+            cache = dict(k_bits=bits, v_bits=bits, **bufs)
             O.split_k_decode_quantized(q, cache, T, SCALE, sinks, chunk=4096, workers=cores)
             times.append(time.perf_counter() - t0)
             if time.perf_counter() - start > budget_s and len(times) >= 3:
@@ -812,16 +823,18 @@ def cpu_baseline(T, seed, budget_s=10.0):
         if limiter is not None:
             limiter.unregister()
     sec = float(np.median(times))
+    fmt = "int8" if bits == 8 else "uint4"
     return dict(
-        value=step_bytes(T) / sec / 1e9,
+        value=step_bytes(T, k_bits=bits, v_bits=bits, hq=hq, hkv=hkv) / sec / 1e9,
         unit="GB/s",
         cores=cores,
         affinity_cores=len(os.sched_getaffinity(0)),
         cpu_model=cpu_model(),
         kind="port",
         us_per_step=sec * 1e6,
-        sample=f"{len(times)} decode steps (1-token int8 append + attention) of the 32K workload, one cache "
-        f"instance, NumPy float32 split-K over 4096-token chunks on {cores} threads; median step time",
+        sample=f"{len(times)} decode steps (1-token {fmt} append + attention) of the {label} workload "
+        f"({hq} q / {hkv} kv heads, {T} tokens), one cache instance, NumPy float32 split-K over 4096-token "
+        f"chunks on {cores} threads; median step time",
     )
 
 
@@ -854,6 +867,7 @@ def main(argv=None):
     ap.add_argument("--no-yardstick", action="store_true", help="skip timing PyTorch's own fused attention")
     ap.add_argument("--no-sliding", action="store_true", help="skip the sliding-window layer measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-tiny", action="store_true", help="skip the 1,024-token 8:1 configuration")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument(
@@ -891,6 +905,14 @@ def main(argv=None):
 
     r32 = run_decode(32768, 32, args.steps, args.warmup, args.seed)
     log(f"32K: {r32['us_per_step']:.2f} us/step, {r32['gbs']:.0f} GB/s; kernel {r32['kernel_us']:.2f} us")
+    r1k = None
+    if not args.no_tiny:
+        # the CPU-sized parity configuration: 8 q heads over 1 KV head, 1,024
+        # tokens, N(0, 1) K/V; 64 instances (17 MB) stay in the MALL, so this
+        # is a launch-latency figure
+        r1k = run_decode(1024, 64, max(16, args.steps // 4), max(4, args.warmup // 4), args.seed + 11, kind="normal",
+                         frac=0.0, hq=8, hkv=1)
+        log(f"1K tiny: {r1k['us_per_step']:.2f} us/step; kernel {r1k['kernel_us']:.2f} us")
     r252 = None
     if not args.no_long:
         ls = args.long_steps or max(16, args.steps // 8)
@@ -964,9 +986,22 @@ def main(argv=None):
                           f"WRITE_SIZE passes over this kernel at source commit {t.get('source_commit', 'unrecorded')}")
 
     cpu = None
+    cpu_more = {}
     if not args.no_cpu_baseline:
         log("CPU baseline")
         cpu = cpu_baseline(32768, args.seed + 7, args.cpu_budget)
+        # the other decode configurations, each beside its GPU figure
+        b = max(3.0, 0.6 * args.cpu_budget)
+        if r1k is not None:
+            cpu_more["context_1k_tiny"] = cpu_baseline(1024, args.seed + 8, b, hq=8, hkv=1, kind="normal", frac=0.0,
+                                                       label="1K 8:1")
+        if r252 is not None:
+            cpu_more["context_252k"] = cpu_baseline(258048, args.seed + 9, b, label="252K")
+        if r4 is not None:
+            cpu_more["context_131k_int4"] = cpu_baseline(131072, args.seed + 10, b, bits=4, kind="heavy", frac=0.05,
+                                                         label="131K uint4")
+        for name, c in cpu_more.items():
+            log(f"CPU baseline {name}: {c['us_per_step']:.0f} us/step, {c['value']:.1f} GB/s on {c['cores']} threads")
 
     result = {
         "metric": METRIC,
@@ -1016,6 +1051,21 @@ def main(argv=None):
         },
         "cpu_baseline": cpu,
     }
+    if r1k is not None:
+        result["context_1k_tiny"] = {
+            "context": 1024,
+            "q_heads": 8,
+            "kv_heads": 1,
+            "kv_format": "int8 symmetric, fp16 scale per (token, head); N(0, 1) K/V",
+            "note": "the CPU-sized parity configuration; 64 instances (17 MB) fit the MALL, so the figure is "
+                    "launch latency, not HBM streaming",
+            "us_per_step": round(r1k["us_per_step"], 3),
+            **_step_detail(r1k),
+            "gbs": round(r1k["gbs"], 2),
+            "kernel_us": round(r1k["kernel_us"], 3),
+            "bytes_per_step": r1k["bytes_per_step"],
+            "cache_instances": r1k["instances"],
+        }
     if r252 is not None:
         result["context_252k"] = {
             "context": 258048,
@@ -1086,6 +1136,8 @@ def main(argv=None):
             "bytes_per_step": raf252["bytes_per_step"],
             "cache_instances": raf252["instances"],
         }
+    for name, c in cpu_more.items():
+        result[name]["cpu_baseline"] = c
     result.update(rbf)
     if rq4 is not None:
         result["q4_gemv"] = dict(
