@@ -47,7 +47,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "decode-attn HBM GB/s (% of peak) and µs/step per layer at 32K and 252K ctx"
 HQ, HKV, D = 32, 4, 128
 SCALE = 1.0 / np.sqrt(D)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_i8_32k_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_kernel_traffic.json")
 CALIB_BYTES = 256 << 20
 
 
@@ -977,13 +977,19 @@ def main(argv=None):
 
     floor = None if args.no_floor else run_read_floor(max(20, args.steps // 5))
 
-    traffic, traffic_source = None, None
+    traffic, traffic_source, traffic_cfg = None, None, {}
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
-        traffic = t.get("hbm_bytes_per_launch")
+        traffic_cfg = t.get("configs", {})
+        traffic = traffic_cfg.get("32k_int8", {}).get("hbm_bytes_per_launch")
         traffic_source = (f"not measured by this run: {os.path.relpath(TRAFFIC_FILE, ROOT)}, rocprofv3 FETCH_SIZE and "
                           f"WRITE_SIZE passes over this kernel at source commit {t.get('source_commit', 'unrecorded')}")
+
+    def traffic_of(name):
+        c = traffic_cfg.get(name)
+        return None if c is None else dict(hbm_bytes_per_launch=c["hbm_bytes_per_launch"], ratio_to_algorithmic=c["ratio"],
+                                           source=traffic_source)
 
     cpu = None
     cpu_more = {}
@@ -1078,6 +1084,7 @@ def main(argv=None):
             "kernel_frac_of_peak": round(r252["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_step": r252["bytes_per_step"],
             "cache_instances": r252["instances"],
+            "traffic": traffic_of("252k_int8"),
         }
     if rb4 is not None:
         result["context_32k_batch4"] = {
@@ -1107,6 +1114,7 @@ def main(argv=None):
             "kernel_frac_of_peak": round(r4["kernel_gbs"] / HBM_PEAK_GBS, 4),
             "bytes_per_step": r4["bytes_per_step"],
             "cache_instances": r4["instances"],
+            "traffic": traffic_of("131k_uint4"),
         }
     if raf is not None:
         result["context_32k_affine"] = {
