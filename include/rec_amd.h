@@ -104,7 +104,10 @@ int rec_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
  * sequence: q (B, Hq, D) with element strides (q_sb, q_sh), q-head h reads
  * kv-head h / (Hq/Hkv), Hq/Hkv <= 8; q rows start 16-byte aligned with strides
  * that are multiples of 4 elements (else REC_EALIGN).  scores = scale * q·k̂; `sinks` (Hq fp32
- * logits, or NULL) join the softmax denominator; out (B, Hq, D) fp32.
+ * logits, or NULL) join the softmax denominator; out (B, Hq, D), 16-byte
+ * aligned, of out_dtype: REC_F32, or REC_BF16 / REC_F16 (the fp32 result
+ * rounded to nearest even, the query dtype the reference returns,
+ * model.py:132-139 — no separate cast launch).
  * splits <= 0 picks rec_decode_default_splits().
  * Replaces quantized_attention_with_sinks, engine/src/rec_mlx/model.py:108-139
  * (split-K structure of engine/src/rec_mlx/kernels/megakernel.py:619-693 and
@@ -115,7 +118,7 @@ int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
                     const float* sinks, float scale,
                     int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
-                    void* workspace, size_t workspace_bytes, float* out, void* stream);
+                    void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 /*
  * One decode step: quantize-append the single new token k_new / v_new
@@ -132,7 +135,7 @@ int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                            int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
                            const float* sinks, float scale,
                            int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
-                           void* workspace, size_t workspace_bytes, float* out, void* stream);
+                           void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 /*
  * rec_decode_append_attn for callers that cannot allocate (code under HIP
@@ -152,7 +155,7 @@ int rec_decode_append_attn_noalloc(const void* q, int q_dtype, int64_t q_sb, int
                                    int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
                                    const float* sinks, float scale,
                                    int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
-                                   float* out, void* stream);
+                                   int out_dtype, void* out, void* stream);
 size_t rec_decode_scratch_bytes(void);
 
 /*
@@ -174,10 +177,10 @@ int rec_decode_partial(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                        int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
                        const float* sinks, float scale,
                        int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
-                       void* workspace, size_t workspace_bytes, float* out, void* stream);
+                       void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int splits, int appended,
-                     void* workspace, size_t workspace_bytes, float* out, void* stream);
+                     void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 /*
  * Chunked prefill: the last L of the T cached tokens are new (already
@@ -186,7 +189,7 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * causal != 0, query i sees tokens [0, T-L+i]; window > 0 further limits
  * query position p to keys > p - window (a sliding-window mask array of
  * model.py:122-128; window 0 = none) — with optional sink logits.
- * out (B, Hq, L, D) fp32.  Any cache format of rec_decode_attn (int8 or uint4
+ * out (B, Hq, L, D) of out_dtype (REC_F32, REC_BF16 or REC_F16, as the decode).  Any cache format of rec_decode_attn (int8 or uint4
  * in any mix, or the affine pair): K/V tiles are dequantized into on-chip
  * memory, never to HBM — int8 codes exactly with the row scales applied to
  * scores and probabilities, 4-bit and affine values as x̂ rounded to the
@@ -209,7 +212,7 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
                      const float* sinks, float scale, int causal, int window,
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
-                     int splits, void* workspace, size_t workspace_bytes, float* out, void* stream);
+                     int splits, void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 /* Workspace bytes a prefill launch of L queries with Hq query and Hkv KV heads
  * needs for `splits` key splits (<= 0: the most the automatic plan can use);
@@ -274,7 +277,7 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     void* k, int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh,
                     const float* sinks, float scale,
                     int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
-                    void* workspace, size_t workspace_bytes, float* out, void* stream);
+                    void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 /*
  * rec_decode_bf16_ring: one decode step of a sliding-window ring (token p of
@@ -292,7 +295,7 @@ int rec_decode_bf16_ring(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          void* k, int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh,
                          const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
                          int64_t capacity, int64_t slot, int splits, void* workspace,
-                         size_t workspace_bytes, float* out, void* stream);
+                         size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 /*
  * Dequantize cache rows [0, T) of any format (k_bits / v_bits as rec_kv_append)
@@ -322,7 +325,7 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      const void* k, int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh,
                      const float* sinks, float scale, int causal, int window,
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int splits,
-                     void* workspace, size_t workspace_bytes, float* out, void* stream);
+                     void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
 /*
  * A plain streaming read of `bytes` (a positive multiple of 16) at p (16-byte

@@ -44,7 +44,8 @@ SIGNATURES = {
     "rec_workspace_init": (_i, [_p, _sz, _p]),
     "rec_decode_attn": (
         _i,
-        [_p, _i, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _p, _p],
+        [_p, _i, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p,
+         _p],
     ),
     "rec_decode_append_attn": (
         _i,
@@ -52,20 +53,20 @@ SIGNATURES = {
             _p, _i, _i64, _i64,  # q
             _p, _p, _i, _i64, _i64, _i64, _i64,  # new k/v
             _i, _p, _p, _p, _i, _p, _p, _p,  # cache
-            _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _p, _p,
+            _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p, _p,  # ... workspace, out_dtype, out, stream
         ],
     ),
 }
 SIGNATURES["rec_decode_partial"] = SIGNATURES["rec_decode_append_attn"]
 SIGNATURES["rec_decode_append_attn_noalloc"] = (
-    _i, SIGNATURES["rec_decode_append_attn"][1][:-4] + [_p, _p]  # no workspace, workspace_bytes
+    _i, SIGNATURES["rec_decode_append_attn"][1][:-5] + [_i, _p, _p]  # no workspace, workspace_bytes
 )
 SIGNATURES["rec_decode_scratch_bytes"] = (_sz, [])
-SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _p, _p])
+SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _i, _p, _p])
 SIGNATURES["rec_prefill_attn"] = (
     _i,
     [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64, _i64,
-     _i, _p, _sz, _p, _p],
+     _i, _p, _sz, _i, _p, _p],
 )
 SIGNATURES["rec_prefill_workspace_bytes"] = (_sz, [_i, _i, _i, _i, _i])
 
@@ -85,7 +86,7 @@ SIGNATURES["rec_decode_bf16"] = (
         _p, _i, _i64, _i64,  # q
         _p, _p, _i, _i64, _i64, _i64, _i64,  # new k/v
         _p, _i64, _i64, _p, _i64, _i64,  # bf16 K, V
-        _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _p, _p,
+        _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p, _p,
     ],
 )
 SIGNATURES["rec_decode_bf16_ring"] = (
@@ -94,7 +95,7 @@ SIGNATURES["rec_decode_bf16_ring"] = (
         _p, _i, _i64, _i64,  # q
         _p, _p, _i, _i64, _i64, _i64, _i64,  # new k/v
         _p, _i64, _i64, _p, _i64, _i64,  # the ring's K, V
-        _p, _f, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p, _sz, _p, _p,  # ... T, capacity, slot, splits ...
+        _p, _f, _i, _i, _i, _i, _i64, _i64, _i64, _i, _p, _sz, _i, _p, _p,  # ... T, capacity, slot, splits ...
     ],
 )
 
@@ -102,7 +103,7 @@ SIGNATURES["rec_kv_dequant_bf16"] = (_i, [_i, _p, _p, _p, _i, _p, _p, _p, _i, _i
 SIGNATURES["rec_prefill_bf16"] = (
     _i,
     [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64,
-     _i, _p, _sz, _p, _p],
+     _i, _p, _sz, _i, _p, _p],
 )
 SIGNATURES["rec_q4_packed_bytes"] = (_sz, [_i64, _i64])
 SIGNATURES["rec_q4_pack"] = (_i, [_p, _p, _p, _i64, _i64, _p, _sz, _p])

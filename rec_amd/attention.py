@@ -106,6 +106,20 @@ def _sinks(sinks, Hq, device, dtype=None):
     return s
 
 
+def _new_out(shape, out_dtype, queries):
+    """The output tensor the kernels write: the requested dtype (default: the
+    query dtype, as the reference returns) when it is one they store (fp32,
+    bf16, fp16, rounded to nearest even in the kernel), else fp32 converted
+    by the caller (:func:`_finish`)."""
+    want = out_dtype or queries.dtype
+    dt = want if want in _DTYPES else torch.float32
+    return torch.empty(shape, dtype=dt, device=queries.device), want
+
+
+def _finish(out, want):
+    return out if out.dtype == want else out.to(want)
+
+
 def _check_query(queries):
     if queries.dim() != 4:
         raise ValueError(f"queries must be (B, n_heads, L, head_dim), got {tuple(queries.shape)}")
@@ -150,7 +164,7 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
     sk = _sinks(sinks, Hq, dev, sink_dtype)
     common_tail = (
         _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity), int(splits),
-        ws.data_ptr(), ws.numel(), out.data_ptr(), stream,
+        ws.data_ptr(), ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream,
     )
     if k_new is None:
         rc = lib.rec_decode_attn(
@@ -204,7 +218,7 @@ def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sink
         values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
         _ptr(sk), float(scale), int(causal), int(window), B, Hq, keys.n_kv_heads, D, L, int(keys.length),
         int(keys.capacity),
-        int(splits), ws.data_ptr(), ws.numel(), out.data_ptr(), stream,
+        int(splits), ws.data_ptr(), ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream,
     )
     _lib.check(rc, "rec_prefill_attn")
 
@@ -263,7 +277,7 @@ def quantized_attention_with_sinks(
     _check_cache_shapes(queries, keys, values)
     causal, win = _mask_plan(mask, L, int(keys.length))
     if L == 1 and not win:
-        out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+        out, want = _new_out((B, Hq, D), out_dtype, queries)
         _decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype)
         out = out.view(B, Hq, 1, D)
     else:
@@ -272,9 +286,9 @@ def quantized_attention_with_sinks(
             raise ValueError(f"{L} queries but only {keys.length} cached tokens")
         if queries.dtype not in (torch.bfloat16, torch.float16):
             raise NotImplementedError("prefill (and windowed) queries must be bf16 or f16 (the matrix-core input type)")
-        out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
+        out, want = _new_out((B, Hq, L, D), out_dtype, queries)
         _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0, win, sink_dtype)
-    return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+    return _finish(out, want)
 
 
 def _bf16_kv_ok(t: torch.Tensor) -> bool:
@@ -305,7 +319,7 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
     head = (q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), *new,
             keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
             _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity))
-    tail = (int(splits), ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
+    tail = (int(splits), ws.data_ptr(), ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream)
     if slot is None:
         _lib.check(lib.rec_decode_bf16(*head, *tail), "rec_decode_bf16")
     else:  # a ring step: the new token goes to `slot`
@@ -326,7 +340,7 @@ def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, ou
         queries.data_ptr(), _DTYPES[queries.dtype], queries.stride(0), queries.stride(1), queries.stride(2),
         keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
         _ptr(sk), float(scale), int(causal), int(window), B, Hq, Hkv, D, L, T, int(splits), ws.data_ptr(),
-        ws.numel(), out.data_ptr(), stream,
+        ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream,
     )
     _lib.check(rc, "rec_prefill_bf16")
 
@@ -411,13 +425,13 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
     if L == 1:
         if win:  # one query sees the last `win` keys: attend over that slice
             keys, values = keys[:, :, T - win:], values[:, :, T - win:]
-        out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+        out, want = _new_out((B, Hq, D), out_dtype, queries)
         _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype)
         out = out.view(B, Hq, 1, D)
     else:
-        out = torch.empty((B, Hq, L, D), dtype=torch.float32, device=queries.device)
+        out, want = _new_out((B, Hq, L, D), out_dtype, queries)
         _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0, sink_dtype)
-    return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+    return _finish(out, want)
 
 
 def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dtype=None,
@@ -466,12 +480,12 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
             n = min(cache.offset + 1, cache.capacity)
             kn = keys if _rows_aligned(keys) else keys.contiguous()
             vn = values if _rows_aligned(values) else values.contiguous()
-            out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+            out, want = _new_out((B, Hq, D), out_dtype, queries)
             _bf16_decode_launch(queries, cache.keys, cache.values, scale, sinks, splits, out, kn, vn, T=n,
                                 capacity=cache.capacity, slot=slot, sink_dtype=qdt)
             cache.offset += 1
             out = out.view(B, Hq, 1, D)
-            return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+            return _finish(out, want)
         k, v = cache.update_and_fetch(keys, values)
         if L == 1:
             return scaled_dot_product_attention(queries, k, v, scale, None, sinks, out_dtype=out_dtype, splits=splits,
@@ -493,12 +507,12 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
             data = cache.storage.layer(cache.index)
             kn = keys if _rows_aligned(keys) else keys.contiguous()
             vn = values if _rows_aligned(values) else values.contiguous()
-            out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+            out, want = _new_out((B, Hq, D), out_dtype, queries)
             _bf16_decode_launch(queries, data[:, 0], data[:, 1], scale, sinks, splits, out, kn, vn, T=T,
                                 capacity=cache.storage.capacity, sink_dtype=qdt)
             cache.offset = T
             out = out.view(B, Hq, 1, D)
-            return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+            return _finish(out, want)
         k, v = cache.update_and_fetch(keys, values)
         return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits,
                                             sink_dtype=qdt)
@@ -519,7 +533,7 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         _check_cache_shapes(queries, k_kv, v_kv)
         kn = keys if _rows_aligned(keys) else keys.contiguous()
         vn = values if _rows_aligned(values) else values.contiguous()
-        out = torch.empty((B, Hq, D), dtype=torch.float32, device=queries.device)
+        out, want = _new_out((B, Hq, D), out_dtype, queries)
         try:
             _decode_launch(queries, k_kv, v_kv, scale, sinks, splits, out, kn, vn, T=cache.offset + 1,
                            capacity=cache.capacity)
@@ -528,7 +542,7 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
             raise
         cache.offset += 1
         out = out.view(B, Hq, 1, D)
-        return out if (out_dtype or queries.dtype) == torch.float32 else out.to(out_dtype or queries.dtype)
+        return _finish(out, want)
     k, v = cache.update_and_fetch(keys, values)
     return quantized_attention_with_sinks(queries, k, v, scale, mask, sinks, cache.group_size, cache.key_bits,
                                           cache.value_bits, out_dtype=out_dtype, splits=splits,

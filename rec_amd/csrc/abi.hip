@@ -127,11 +127,12 @@ void effective_splits(int64_t T, int req, bool fused, int* S, int* span, int* t_
 int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_bits, const void* kq,
                   const uint16_t* ks, const uint16_t* kz, int v_bits, const void* vq, const uint16_t* vs,
                   const uint16_t* vz, const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
-                  int64_t cap, int splits, void* ws, size_t ws_bytes, float* out, const RowSrc* knew,
-                  const RowSrc* vnew, int phases, void* stream) {
+                  int64_t cap, int splits, void* ws, size_t ws_bytes, int out_dtype, void* out,
+                  const RowSrc* knew, const RowSrc* vnew, int phases, void* stream) {
   int e;
   if ((e = resolve_formats(k_bits, v_bits, &k_bits, &v_bits))) return e;
   if ((e = check_dtype(q_dtype, "query"))) return e;
+  if ((e = check_dtype(out_dtype, "output"))) return e;
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
   if (B < 1 || Hkv < 1 || Hq < 1) return fail(REC_EINVAL, "B, Hq and Hkv must be positive");
   if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
@@ -168,6 +169,7 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   a.vz = vz;
   a.sinks = sinks;
   a.out = out;
+  a.out_dtype = out_dtype;
   a.ws_stat = (float*)((char*)ws + w.stat);
   a.ws_acc = (float*)((char*)ws + w.acc);
   if (knew) {
@@ -308,10 +310,10 @@ int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int 
                     const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits, const void* v_codes,
                     const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks, float scale, int B,
                     int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
-                    size_t workspace_bytes, float* out, void* stream) {
+                    size_t workspace_bytes, int out_dtype, void* out, void* stream) {
   return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
-                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out, nullptr,
-                       nullptr, 3, stream);
+                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out_dtype, out,
+                       nullptr, nullptr, 3, stream);
 }
 
 static int append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
@@ -319,7 +321,7 @@ static int append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
                        void* k_codes, uint16_t* k_scales, uint16_t* k_zeros, int v_bits, void* v_codes,
                        uint16_t* v_scales, uint16_t* v_zeros, const float* sinks, float scale, int B, int Hq, int Hkv,
                        int D, int64_t T, int64_t capacity, int splits, void* workspace, size_t workspace_bytes,
-                       float* out, int phases, void* stream) {
+                       int out_dtype, void* out, int phases, void* stream) {
   const bool append = k_new != nullptr || v_new != nullptr;
   if (append) {
     int e;
@@ -329,7 +331,7 @@ static int append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
   const RowSrc kn{k_new, new_dtype, k_sb, k_sh, 0, vec_rows(k_new, k_sb, k_sh, 0)},
       vn{v_new, new_dtype, v_sb, v_sh, 0, vec_rows(v_new, v_sb, v_sh, 0)};
   return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
-                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out,
+                       sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out_dtype, out,
                        append ? &kn : nullptr, append ? &vn : nullptr, phases, stream);
 }
 
@@ -338,11 +340,11 @@ int rec_decode_append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_s
                            int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros, int v_bits,
                            void* v_codes, uint16_t* v_scales, uint16_t* v_zeros, const float* sinks, float scale,
                            int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
-                           size_t workspace_bytes, float* out, void* stream) {
+                           size_t workspace_bytes, int out_dtype, void* out, void* stream) {
   if (!k_new || !v_new) return fail(REC_EINVAL, "new keys/values pointer is null");
   return append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
                      k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
-                     splits, workspace, workspace_bytes, out, 3, stream);
+                     splits, workspace, workspace_bytes, out_dtype, out, 3, stream);
 }
 
 size_t rec_decode_scratch_bytes(void) { return SCRATCH_BYTES; }
@@ -352,12 +354,12 @@ int rec_decode_append_attn_noalloc(const void* q, int q_dtype, int64_t q_sb, int
                                    int64_t v_sh, int k_bits, void* k_codes, uint16_t* k_scales, uint16_t* k_zeros,
                                    int v_bits, void* v_codes, uint16_t* v_scales, uint16_t* v_zeros,
                                    const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
-                                   int64_t capacity, int splits, float* out, void* stream) {
+                                   int64_t capacity, int splits, int out_dtype, void* out, void* stream) {
   if (!k_new || !v_new) return fail(REC_EINVAL, "new keys/values pointer is null");
   // validate everything, the plan's partials against the scratch size included, before touching the device
   int e = append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
                       k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
-                      splits, nullptr, SCRATCH_BYTES, out, 0, stream);
+                      splits, nullptr, SCRATCH_BYTES, out_dtype, out, 0, stream);
   if (e == REC_EWORKSPACE) {
     char why[sizeof(g_err)];
     snprintf(why, sizeof(why), "%s", g_err);
@@ -371,7 +373,7 @@ int rec_decode_append_attn_noalloc(const void* q, int q_dtype, int64_t q_sb, int
   if (!ws) return e;
   return append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
                      k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
-                     splits, ws, SCRATCH_BYTES, out, 3, stream);
+                     splits, ws, SCRATCH_BYTES, out_dtype, out, 3, stream);
 }
 
 int rec_decode_partial(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
@@ -379,16 +381,17 @@ int rec_decode_partial(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
                        void* k_codes, uint16_t* k_scales, uint16_t* k_zeros, int v_bits, void* v_codes,
                        uint16_t* v_scales, uint16_t* v_zeros, const float* sinks, float scale, int B, int Hq, int Hkv,
                        int D, int64_t T, int64_t capacity, int splits, void* workspace, size_t workspace_bytes,
-                       float* out, void* stream) {
+                       int out_dtype, void* out, void* stream) {
   return append_attn(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, k_sb, k_sh, v_sb, v_sh, k_bits, k_codes,
                      k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros, sinks, scale, B, Hq, Hkv, D, T, capacity,
-                     splits, workspace, workspace_bytes, out, 1, stream);
+                     splits, workspace, workspace_bytes, out_dtype, out, 1, stream);
 }
 
 int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int splits, int appended, void* workspace,
-                     size_t workspace_bytes, float* out, void* stream) {
+                     size_t workspace_bytes, int out_dtype, void* out, void* stream) {
   if (B < 1 || Hkv < 1 || Hq < 1 || Hq % Hkv != 0 || Hq / Hkv > 8 || T < 1)
     return fail(REC_EINVAL, "bad shape B=%d Hq=%d Hkv=%d T=%lld", B, Hq, Hkv, (long long)T);
+  if (int e = check_dtype(out_dtype, "output")) return e;
   if (!out || !aligned16(out)) return fail(REC_EALIGN, "output must be a 16-byte aligned buffer");
   if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
   if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
@@ -399,6 +402,7 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
   DecodeArgs a{};
   a.sinks = sinks;
   a.out = out;
+  a.out_dtype = out_dtype;
   a.ws_stat = (float*)((char*)workspace + w.stat);
   a.ws_acc = (float*)((char*)workspace + w.acc);
   a.B = B;
@@ -452,10 +456,12 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits,
                      const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks,
                      float scale, int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T,
-                     int64_t capacity, int splits, void* workspace, size_t workspace_bytes, float* out, void* stream) {
+                     int64_t capacity, int splits, void* workspace, size_t workspace_bytes, int out_dtype, void* out,
+                     void* stream) {
   int e;
   int kf, vf;
   if ((e = resolve_formats(k_bits, v_bits, &kf, &vf))) return e;
+  if ((e = check_dtype(out_dtype, "output"))) return e;
   if (q_dtype != REC_BF16 && q_dtype != REC_F16)
     return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
@@ -489,6 +495,7 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.vz = v_zeros;
   a.sinks = sinks;
   a.out = out;
+  a.out_dtype = out_dtype;
   a.q_mul = scale * LOG2E;
   a.B = B;
   a.Hq = Hq;
@@ -535,9 +542,10 @@ int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scale
 int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
                      int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale,
                      int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T, int splits,
-                     void* workspace, size_t workspace_bytes, float* out, void* stream) {
+                     void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream) {
   if (q_dtype != REC_BF16 && q_dtype != REC_F16)
     return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
+  if (int e = check_dtype(out_dtype, "output")) return e;
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
   if (B < 1 || Hkv < 1 || Hq < 1 || L < 1) return fail(REC_EINVAL, "bad shape B=%d Hq=%d Hkv=%d L=%d", B, Hq, Hkv, L);
   if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
@@ -567,6 +575,7 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.kv_bf16 = 1;
   a.sinks = sinks;
   a.out = out;
+  a.out_dtype = out_dtype;
   a.q_mul = scale * LOG2E;
   a.B = B;
   a.Hq = Hq;
@@ -648,13 +657,19 @@ int rec_ring_join_bf16(void* k_ring, void* v_ring, int64_t rk_sb, int64_t rk_sh,
                   "ring join launch");
 }
 
+// bf16 decodes over at most this many tokens with the automatic plan run as
+// one eight-wave workgroup per (sequence, KV head): 32 chunks, four per wave
+constexpr int64_t BF16_ONE_WORKGROUP_TOKENS = 1024;
+
 static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
                        int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k,
                        int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks,
                        float scale, int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
-                       void* workspace, size_t workspace_bytes, float* out, void* stream, int64_t new_pos) {
+                       void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream,
+                       int64_t new_pos) {
   int e;
   if ((e = check_dtype(q_dtype, "query"))) return e;
+  if ((e = check_dtype(out_dtype, "output"))) return e;
   if (D != HEAD_DIM) return fail(REC_EUNSUPPORTED, "head_dim %d is not supported (128 only)", D);
   if (B < 1 || Hkv < 1 || Hq < 1) return fail(REC_EINVAL, "B, Hq and Hkv must be positive");
   if (Hq % Hkv != 0) return fail(REC_EINVAL, "Hq (%d) must be a multiple of Hkv (%d)", Hq, Hkv);
@@ -674,12 +689,21 @@ static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
     if ((e = check_dtype(new_dtype, "new keys/values"))) return e;
     if (!k_new || !v_new) return fail(REC_EINVAL, "new keys and values must both be given");
   }
-  if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
-  if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
   int S, span, t_split_end;
-  effective_splits(T, splits, append, &S, &span, &t_split_end);
+  if (splits <= 0 && T <= BF16_ONE_WORKGROUP_TOKENS) {
+    // a short cache (a sliding window): one workgroup per (sequence, KV
+    // head) attends over all of it, the new token written first, and writes
+    // the output itself -- one launch, no partials
+    S = 1;
+    span = (int)((T + CHUNK - 1) / CHUNK * CHUNK);
+    t_split_end = append ? 0 : (int)T;  // with a write, the one split is the "newest token" split [0, T)
+  } else {
+    if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
+    if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
+    effective_splits(T, splits, append, &S, &span, &t_split_end);
+  }
   const WorkspaceLayout w = ws_layout(B, Hkv, S);
-  if (!workspace || workspace_bytes < w.total)
+  if (S > 1 && (!workspace || workspace_bytes < w.total))
     return fail(REC_EWORKSPACE, "workspace of %zu bytes is too small (%zu needed for %d splits)", workspace_bytes,
                 w.total, S);
   if (!aligned16(workspace)) return fail(REC_EALIGN, "workspace must be 16-byte aligned");
@@ -696,6 +720,7 @@ static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
   a.v_sh = v_sh;
   a.sinks = sinks;
   a.out = out;
+  a.out_dtype = out_dtype;
   a.ws_stat = (float*)((char*)workspace + w.stat);
   a.ws_acc = (float*)((char*)workspace + w.acc);
   if (append) {
@@ -722,10 +747,10 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, cons
                     int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k, int64_t k_sb,
                     int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale, int B, int Hq,
                     int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
-                    size_t workspace_bytes, float* out, void* stream) {
+                    size_t workspace_bytes, int out_dtype, void* out, void* stream) {
   return decode_bf16(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, kn_sb, kn_sh, vn_sb, vn_sh, k, k_sb, k_sh, v,
-                     v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out,
-                     stream, T - 1);
+                     v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes,
+                     out_dtype, out, stream, T - 1);
 }
 
 int rec_decode_bf16_ring(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new,
@@ -733,12 +758,12 @@ int rec_decode_bf16_ring(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                          void* k, int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh,
                          const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
                          int64_t capacity, int64_t slot, int splits, void* workspace, size_t workspace_bytes,
-                         float* out, void* stream) {
+                         int out_dtype, void* out, void* stream) {
   if (!k_new || !v_new) return fail(REC_EINVAL, "a ring decode step writes its new token: k_new and v_new are required");
   if (slot < 0 || slot >= T) return fail(REC_EINVAL, "slot %lld outside the %lld occupied slots", (long long)slot, (long long)T);
   return decode_bf16(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, kn_sb, kn_sh, vn_sb, vn_sh, k, k_sb, k_sh, v,
-                     v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out,
-                     stream, slot);
+                     v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes,
+                     out_dtype, out, stream, slot);
 }
 
 size_t rec_q4_packed_bytes(int64_t N, int64_t K) {

@@ -81,6 +81,31 @@ __device__ __forceinline__ float load_as_float(const void* p, int64_t i, int dt)
   return ((const float*)p)[i];
 }
 
+// Store consecutive output elements i, i+1 (, i+2, i+3) of an fp32, bf16 or
+// fp16 array (dt a DT_* code); 16-bit outputs are rounded to nearest even by
+// the hardware conversions, as a cast of the fp32 result would round them.
+__device__ __forceinline__ void store_out2(void* out, int64_t i, v2f o, int dt) {
+  if (dt == DT_F32) {
+    *(v2f*)((float*)out + i) = o;
+  } else if (dt == DT_BF16) {
+    const __bf16 a = (__bf16)o[0], b = (__bf16)o[1];
+    *(uint32_t*)((uint16_t*)out + i) =
+        (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  } else {
+    const _Float16 a = (_Float16)o[0], b = (_Float16)o[1];
+    *(uint32_t*)((uint16_t*)out + i) =
+        (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  }
+}
+__device__ __forceinline__ void store_out4(void* out, int64_t i, v4f o, int dt) {
+  if (dt == DT_F32) {
+    *(v4f*)((float*)out + i) = o;
+  } else {
+    store_out2(out, i, (v2f){o[0], o[1]}, dt);
+    store_out2(out, i + 2, (v2f){o[2], o[3]}, dt);
+  }
+}
+
 // fp16 round-to-nearest-even of a non-negative float, saturating at 65504.
 // float -> bf16 bits, round to nearest even (finite inputs).
 __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {

@@ -789,7 +789,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
     if (a.S == 1) {
       if (sink != NEG_INF) l += __builtin_amdgcn_exp2f(sink - M);
       const v4f o = l > 0.f ? acc4 / l : acc4;
-      *(v4f*)(a.out + ((int64_t)b * a.Hq + h * a.G + hh) * HEAD_DIM + d0) = o;
+      store_out4(a.out, ((int64_t)b * a.Hq + h * a.G + hh) * HEAD_DIM + d0, o, a.out_dtype);
     } else {
       const int64_t row = (bh * a.S + split) * 8 + hh;
       *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = acc4;
@@ -864,7 +864,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
   if (sg == 0) {
     const float L = sink != NEG_INF ? lw + __builtin_amdgcn_exp2f(sink - M) : lw;
     const v4f o = L > 0.f ? acc * (1.f / L) : acc;
-    *(v4f*)(a.out + ((int64_t)b * a.Hq + hq) * HEAD_DIM + 32 * qd + 4 * d4) = o;
+    store_out4(a.out, ((int64_t)b * a.Hq + hq) * HEAD_DIM + 32 * qd + 4 * d4, o, a.out_dtype);
   }
 }
 

@@ -41,17 +41,26 @@
 namespace rec {
 namespace {
 
-constexpr int BW = 4;          // wavefronts per workgroup
 constexpr int BCH = 32;        // tokens per chunk
 constexpr int ROWB = 256;      // bytes per K/V row (128 bf16)
 constexpr int VPITCH = 288;    // LDS bytes per staged V row: 256 + 32 keeps the transposed reads conflict-free
 constexpr int KPITCH = 272;    // LDS bytes per staged K row: 256 + 16
-constexpr int BL_QOP = 0;                             // 4 k-steps x 64 lanes x 16 B
-constexpr int BL_PART = 4096;                         // wave partials: 4 x 8 x 128 floats
-constexpr int BL_PSTAT = BL_PART + BW * 8 * 128 * 4;  // 4 x 8 x (m, l)
-constexpr int BL_V = BL_PSTAT + BW * 8 * 8;           // per wave: 32 rows x VPITCH
-constexpr int BL_K = BL_V + BW * BCH * VPITCH;        // per wave: 32 rows x KPITCH
-constexpr int BL_BYTES = BL_K + BW * BCH * KPITCH;
+
+// LDS layout (bytes) for NW wavefronts.  Four waves (split plans): the query
+// operand, the wave partials (NW x 8 x 128 floats) and their (m, l), then each
+// wave's staged V and K rows.  Eight waves (one workgroup per (sequence, KV
+// head) over a short cache, 147 KB): the partials reuse the staging rows
+// once every wave has left the loop.
+template <int NW>
+struct BLayout {
+  static constexpr int QOP = 0;  // 4 k-steps x 64 lanes x 16 B
+  static constexpr int PART = 4096;
+  static constexpr int PSTAT = PART + NW * 8 * 128 * 4;
+  static constexpr int V = NW == 4 ? PSTAT + NW * 8 * 8 : 4096;
+  static constexpr int K = V + NW * BCH * VPITCH;
+  static constexpr int BYTES = K + NW * BCH * KPITCH;
+  static_assert(NW == 4 || PSTAT + NW * 8 * 8 <= BYTES, "partials fit over the staging rows");
+};
 
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
@@ -163,8 +172,11 @@ __device__ __forceinline__ void store_bf16_row_pair(const RowSrc& src, int b, in
   *(uint32_t*)((__bf16*)dst_base + (int64_t)b * sb + (int64_t)h * sh + pos * HEAD_DIM + 2 * lane) = w;
 }
 
-__global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[BL_BYTES];
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void decode_bf16_kernel(const DecodeArgs a) {
+  using BL = BLayout<NW>;
+  constexpr int BW = NW;
+  __shared__ __attribute__((aligned(16))) char smem[BL::BYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, kg = lane >> 4;
@@ -214,7 +226,7 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
   load_bchunk(buf[0], rk, rv, none, 0 < n_w, blk0, loff);
 
   {
-    __bf16* qop = (__bf16*)(smem + BL_QOP);
+    __bf16* qop = (__bf16*)(smem + BL::QOP);
     if (tid < 256) {
       const v4i raw = {qw0[0], qw0[1], qw1[0], qw1[1]};
 #pragma unroll
@@ -236,15 +248,15 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
   __syncthreads();
   v8bf qop[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) qop[ks] = ((const v8bf*)(smem + BL_QOP))[ks * 64 + lane];
+  for (int ks = 0; ks < 4; ++ks) qop[ks] = ((const v8bf*)(smem + BL::QOP))[ks * 64 + lane];
 
   BState st;
   st.m = NEG_INF;
   st.l = 0.f;
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
-  char* vl = smem + BL_V + wave * BCH * VPITCH;
-  char* kl = smem + BL_K + wave * BCH * KPITCH;
+  char* vl = smem + BL::V + wave * BCH * VPITCH;
+  char* kl = smem + BL::K + wave * BCH * KPITCH;
 
   // Ring as in the quantized decode: step i loads chunk i+1, computes chunk i;
   // padded to whole revolutions, only the padding's compute is skipped.
@@ -260,8 +272,9 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
 
   // ---------------- wave partial -> LDS (columns c and c+8 summed) ----------------
   st.l = sum_xor32(sum_xor16(st.l));
-  float* part = (float*)(smem + BL_PART);
-  float* pstat = (float*)(smem + BL_PSTAT);
+  float* part = (float*)(smem + BL::PART);
+  float* pstat = (float*)(smem + BL::PSTAT);
+  if constexpr (NW != 4) __syncthreads();  // the partials overwrite staging rows other waves may still read
 #pragma unroll
   for (int n = 0; n < 8; ++n)
 #pragma unroll
@@ -299,7 +312,7 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
     if (a.S == 1) {
       if (sink != NEG_INF) l += __builtin_amdgcn_exp2f(sink - M);
       const v4f o = l > 0.f ? acc4 / l : acc4;
-      *(v4f*)(a.out + ((int64_t)b * a.Hq + h * a.G + hh) * HEAD_DIM + d0) = o;
+      store_out4(a.out, ((int64_t)b * a.Hq + h * a.G + hh) * HEAD_DIM + d0, o, a.out_dtype);
     } else {
       const int64_t row = (bh * a.S + split) * 8 + hh;
       *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = acc4;
@@ -393,7 +406,13 @@ hipError_t launch_ring_join_bf16(const AppendArgs& a, void* rk, void* rv, int64_
 }
 
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(decode_bf16_kernel, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
+  // a one-split plan (a short cache: one workgroup per (sequence, KV head)
+  // writes the output) runs eight waves, so that a 513-token window has all
+  // its chunks in flight at once
+  if (a.S == 1)
+    hipLaunchKernelGGL(decode_bf16_kernel<8>, dim3(1, a.Hkv, a.B), dim3(512), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_bf16_kernel<4>, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -30,7 +30,8 @@ struct DecodeArgs {
   const uint16_t* vs;
   const uint16_t* vz;
   const float* sinks;  // [Hq] or null
-  float* out;          // [B][Hq][128] fp32
+  void* out;           // [B][Hq][128], out_dtype
+  int out_dtype;       // DT_F32, DT_BF16 or DT_F16
   float* ws_acc;       // [B*Hkv][S][8][128]
   float* ws_stat;      // [B*Hkv][S][8][2]
   int64_t k_sb, k_sh, v_sb, v_sh;  // bf16 K/V (B, Hkv, T, 128) element strides (token stride 128)
@@ -68,7 +69,8 @@ struct PrefillArgs {
   const uint16_t* vs;
   const uint16_t* vz;
   const float* sinks;          // [Hq] or null
-  float* out;                  // [B][Hq][L][128] fp32
+  void* out;                   // [B][Hq][L][128], out_dtype
+  int out_dtype;               // DT_F32, DT_BF16 or DT_F16
   float q_mul;                 // softmax scale * log2(e)
   int B, Hq, Hkv, G, L;
   int64_t T, cap;              // cached tokens including the L new ones; capacity

@@ -793,9 +793,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
         }
         const float inv = l > 0.f ? 1.f / l : 1.f;
         if (prow[rt] < n_p) {
-          float* o = a.out + (((int64_t)b * a.Hq + hq[rt]) * a.L + qr[rt]) * HEAD_DIM + 4 * g;
+          const int64_t o = (((int64_t)b * a.Hq + hq[rt]) * a.L + qr[rt]) * HEAD_DIM + 4 * g;
 #pragma unroll
-          for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt] * inv;
+          for (int n = 0; n < 8; ++n) store_out4(a.out, o + 16 * n, acc[n][rt] * inv, a.out_dtype);
         }
       }
     }
@@ -847,7 +847,7 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
   for (int k = 0; k < 16 * NR; ++k)
     acc += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), k)) * x[k];
   const float inv = z > 0.f ? 1.f / z : 1.f;
-  *(v2f*)(a.out + (((int64_t)b * a.Hq + hq) * a.L + i) * HEAD_DIM + 2 * lane) = acc * inv;
+  store_out2(a.out, (((int64_t)b * a.Hq + hq) * a.L + i) * HEAD_DIM + 2 * lane, acc * inv, a.out_dtype);
 }
 
 PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {

@@ -419,7 +419,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
         o *= f;
       }
       const v4f r = l > 0.f ? o * (1.f / l) : o;
-      *(v4f*)(a.out + (((int64_t)b * a.Hq + hq) * a.L + qi) * HEAD_DIM + d0) = r;
+      store_out4(a.out, (((int64_t)b * a.Hq + hq) * a.L + qi) * HEAD_DIM + d0, r, a.out_dtype);
     } else {
       // no visible key in this split: (-inf, 0, 0), as the tiled kernel writes
       const int64_t row = (((int64_t)bh * a.S + split) * a.nqb) * PREFILL_BLOCK_ROWS + p;

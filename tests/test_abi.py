@@ -70,11 +70,12 @@ def test_append_validation(lib):
 
 
 def _decode(lib, **kw):
-    a = dict(q=16, dt=0, kb=8, vb=8, B=1, Hq=8, Hkv=1, D=128, T=10, cap=64, splits=0, ws=16, wsb=1 << 30, out=16)
+    a = dict(q=16, dt=0, kb=8, vb=8, B=1, Hq=8, Hkv=1, D=128, T=10, cap=64, splits=0, ws=16, wsb=1 << 30, out=16,
+             odt=_lib.REC_F32)
     a.update(kw)
     return lib.rec_decode_attn(
         a["q"], a["dt"], 0, 0, a["kb"], 16, 16, 16, a["vb"], 16, 16, 16, None, 0.088,
-        a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["out"], None,
+        a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["odt"], a["out"], None,
     )
 
 
@@ -88,6 +89,8 @@ def test_decode_validation(lib):
     assert _decode(lib, ws=8) == _lib.REC_EALIGN
     assert _decode(lib, out=4) == _lib.REC_EALIGN
     assert _decode(lib, D=96) == _lib.REC_EUNSUPPORTED
+    assert _decode(lib, odt=5) == _lib.REC_EINVAL  # output dtype: REC_F32, REC_BF16 or REC_F16
+    assert "output" in _lib.last_error()
     # the affine format comes as REC_AFFINE8 keys with REC_AFFINE4 values only
     assert _decode(lib, kb=_lib.REC_AFFINE8, vb=8) == _lib.REC_EUNSUPPORTED
     assert _decode(lib, kb=_lib.REC_AFFINE4, vb=_lib.REC_AFFINE8) == _lib.REC_EUNSUPPORTED
@@ -108,12 +111,12 @@ def test_error_mapping():
 
 def _decode_bf16(lib, **kw):
     a = dict(q=16, dt=1, kn=None, vn=None, k=16, sb=0, sh=0, v=16, B=1, Hq=8, Hkv=1, D=128, T=10, cap=64,
-             splits=0, ws=16, wsb=1 << 30, out=16)
+             splits=0, ws=16, wsb=1 << 30, out=16, odt=_lib.REC_F32)
     a.update(kw)
     return lib.rec_decode_bf16(
         a["q"], a["dt"], 0, 0, a["kn"], a["vn"], 1, 0, 0, 0, 0, a["k"], a["sb"], a["sh"], a["v"], a["sb"], a["sh"],
-        None, 0.088, a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["out"],
-        None,
+        None, 0.088, a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["odt"],
+        a["out"], None,
     )
 
 
@@ -124,7 +127,11 @@ def test_decode_bf16_validation(lib):
     assert _decode_bf16(lib, sh=4) == _lib.REC_EALIGN
     assert "multiples of 8" in _lib.last_error()
     assert _decode_bf16(lib, Hq=16, Hkv=1) == _lib.REC_EUNSUPPORTED
-    assert _decode_bf16(lib, wsb=16) == _lib.REC_EWORKSPACE
+    # split plans need the workspace; the automatic plan over a short cache
+    # (one workgroup per KV head writing the output) needs none
+    assert _decode_bf16(lib, T=100, cap=128, wsb=16, splits=3) == _lib.REC_EWORKSPACE
+    assert _decode_bf16(lib, T=1025, cap=2048, wsb=16) == _lib.REC_EWORKSPACE
+    assert _decode_bf16(lib, odt=3) == _lib.REC_EINVAL
     assert _decode_bf16(lib, kn=16) == _lib.REC_EINVAL  # new keys without new values
     assert _decode_bf16(lib, D=64) == _lib.REC_EUNSUPPORTED
     assert _decode_bf16(lib, q=8) == _lib.REC_EALIGN
@@ -203,7 +210,7 @@ def _prefill(lib, **kw):
     a.update(kw)
     return lib.rec_prefill_attn(
         16, _lib.REC_BF16, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088, 1, a["window"],
-        1, 8, 1, 128, a["L"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], 16, None,
+        1, 8, 1, 128, a["L"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], _lib.REC_F32, 16, None,
     )
 
 
@@ -236,7 +243,7 @@ def _append_attn(lib, **kw):
     a.update(kw)
     return lib.rec_decode_append_attn(
         16, 0, 0, 0, 16, 16, 0, 0, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088,
-        a["B"], a["Hq"], a["Hkv"], 128, a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], 16, None,
+        a["B"], a["Hq"], a["Hkv"], 128, a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], _lib.REC_F32, 16, None,
     )
 
 
@@ -286,7 +293,7 @@ def test_decode_bf16_ring_validation(lib):
     def call(kn, slot, T=10):
         return lib.rec_decode_bf16_ring(
             16, 1, 0, 0, kn, kn, 1, 0, 0, 0, 0, 16, 0, 0, 16, 0, 0, None, 0.088, 1, 8, 1, 128, T, 64, slot, 0, 16,
-            1 << 30, 16, None,
+            1 << 30, _lib.REC_F32, 16, None,
         )
     assert call(None, 3) == _lib.REC_EINVAL
     assert "required" in _lib.last_error()

@@ -216,11 +216,11 @@ def test_partial_then_merge_equals_one_call(gpu):
         args = (q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1), kn.data_ptr(), vn.data_ptr(), _lib.REC_F16,
                 kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1), 8, kc.data_ptr(), ks.data_ptr(), None,
                 8, vc.data_ptr(), vs.data_ptr(), None, sinks.data_ptr(), SCALE, B, Hq, Hkv, 128, T0 + 1,
-                c.capacity, 0, ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
+                c.capacity, 0, ws.data_ptr(), ws.numel(), _lib.REC_F32, out.data_ptr(), stream)
         if phased:
             _lib.check(lib.rec_decode_partial(*args), "partial")
             _lib.check(lib.rec_decode_merge(sinks.data_ptr(), B, Hq, Hkv, T0 + 1, 0, 1, ws.data_ptr(), ws.numel(),
-                                            out.data_ptr(), stream), "merge")
+                                            _lib.REC_F32, out.data_ptr(), stream), "merge")
         else:
             _lib.check(lib.rec_decode_append_attn(*args), "append_attn")
         outs.append(out.clone())

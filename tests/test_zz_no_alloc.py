@@ -41,10 +41,10 @@ def call(lib, noalloc, c, q, kn, vn, sinks, out, splits):
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
             sinks.data_ptr(), SCALE, B, HQ, HKV, 128, c.offset + 1, c.capacity, splits)
     if noalloc:
-        return lib.rec_decode_append_attn_noalloc(*head, out.data_ptr(), stream)
+        return lib.rec_decode_append_attn_noalloc(*head, _lib.REC_F32, out.data_ptr(), stream)
     ws = workspace(q.device, B, HKV, splits if splits > 0 else lib.rec_decode_default_splits(B, HKV, c.offset + 1),
                    stream)
-    return lib.rec_decode_append_attn(*head, ws.data_ptr(), ws.numel(), out.data_ptr(), stream)
+    return lib.rec_decode_append_attn(*head, ws.data_ptr(), ws.numel(), _lib.REC_F32, out.data_ptr(), stream)
 
 
 @pytest.mark.parametrize("fmt", [8, 4, "affine"])
