@@ -307,9 +307,11 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
         q = q.contiguous()
     dev = queries.device
     stream = torch.cuda.current_stream(dev).cuda_stream
-    if splits is None or splits <= 0:
-        splits = lib.rec_decode_default_splits(B, Hkv, T)
-    ws = workspace(dev, B, Hkv, splits, stream)
+    # the library picks the plan when splits is 0 (a short cache runs one
+    # workgroup per KV head and needs no partials); the workspace covers the
+    # default split plan
+    splits = 0 if splits is None or splits <= 0 else int(splits)
+    ws = workspace(dev, B, Hkv, splits or lib.rec_decode_default_splits(B, Hkv, T), stream)
     sk = _sinks(sinks, Hq, dev, sink_dtype)
     if k_new is None:
         new = (None, None, _lib.REC_BF16, 0, 0, 0, 0)

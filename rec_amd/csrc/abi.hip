@@ -657,10 +657,6 @@ int rec_ring_join_bf16(void* k_ring, void* v_ring, int64_t rk_sb, int64_t rk_sh,
                   "ring join launch");
 }
 
-// bf16 decodes over at most this many tokens with the automatic plan run as
-// one eight-wave workgroup per (sequence, KV head): 32 chunks, four per wave
-constexpr int64_t BF16_ONE_WORKGROUP_TOKENS = 1024;
-
 static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
                        int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k,
                        int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks,
@@ -689,19 +685,10 @@ static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
     if ((e = check_dtype(new_dtype, "new keys/values"))) return e;
     if (!k_new || !v_new) return fail(REC_EINVAL, "new keys and values must both be given");
   }
+  if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
+  if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
   int S, span, t_split_end;
-  if (splits <= 0 && T <= BF16_ONE_WORKGROUP_TOKENS) {
-    // a short cache (a sliding window): one workgroup per (sequence, KV
-    // head) attends over all of it, the new token written first, and writes
-    // the output itself -- one launch, no partials
-    S = 1;
-    span = (int)((T + CHUNK - 1) / CHUNK * CHUNK);
-    t_split_end = append ? 0 : (int)T;  // with a write, the one split is the "newest token" split [0, T)
-  } else {
-    if (splits <= 0) splits = rec_decode_default_splits(B, Hkv, T);
-    if (splits > DECODE_MAX_SPLITS) splits = DECODE_MAX_SPLITS;
-    effective_splits(T, splits, append, &S, &span, &t_split_end);
-  }
+  effective_splits(T, splits, append, &S, &span, &t_split_end);
   const WorkspaceLayout w = ws_layout(B, Hkv, S);
   if (S > 1 && (!workspace || workspace_bytes < w.total))
     return fail(REC_EWORKSPACE, "workspace of %zu bytes is too small (%zu needed for %d splits)", workspace_bytes,

@@ -46,21 +46,13 @@ constexpr int ROWB = 256;      // bytes per K/V row (128 bf16)
 constexpr int VPITCH = 288;    // LDS bytes per staged V row: 256 + 32 keeps the transposed reads conflict-free
 constexpr int KPITCH = 272;    // LDS bytes per staged K row: 256 + 16
 
-// LDS layout (bytes) for NW wavefronts.  Four waves (split plans): the query
-// operand, the wave partials (NW x 8 x 128 floats) and their (m, l), then each
-// wave's staged V and K rows.  Eight waves (one workgroup per (sequence, KV
-// head) over a short cache, 147 KB): the partials reuse the staging rows
-// once every wave has left the loop.
-template <int NW>
-struct BLayout {
-  static constexpr int QOP = 0;  // 4 k-steps x 64 lanes x 16 B
-  static constexpr int PART = 4096;
-  static constexpr int PSTAT = PART + NW * 8 * 128 * 4;
-  static constexpr int V = NW == 4 ? PSTAT + NW * 8 * 8 : 4096;
-  static constexpr int K = V + NW * BCH * VPITCH;
-  static constexpr int BYTES = K + NW * BCH * KPITCH;
-  static_assert(NW == 4 || PSTAT + NW * 8 * 8 <= BYTES, "partials fit over the staging rows");
-};
+constexpr int BW = 4;          // wavefronts per workgroup
+constexpr int BL_QOP = 0;                             // 4 k-steps x 64 lanes x 16 B
+constexpr int BL_PART = 4096;                         // wave partials: 4 x 8 x 128 floats
+constexpr int BL_PSTAT = BL_PART + BW * 8 * 128 * 4;  // 4 x 8 x (m, l)
+constexpr int BL_V = BL_PSTAT + BW * 8 * 8;           // per wave: 32 rows x VPITCH
+constexpr int BL_K = BL_V + BW * BCH * VPITCH;        // per wave: 32 rows x KPITCH
+constexpr int BL_BYTES = BL_K + BW * BCH * KPITCH;
 
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 
@@ -85,15 +77,41 @@ __device__ __forceinline__ void load_bchunk(BChunk& R, __amdgpu_buffer_rsrc_t rk
   for (int i = 0; i < 8; ++i) R.v[i] = ld128(b, loff + i * 1024, blk * BCH * ROWB);
 }
 
-__device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, const v8bf* qop, int valid, int lane,
-                                               char* vl, char* kl) {
+// Stage a chunk's rows in the wave's LDS rows: K token t at row t, V token t
+// at row block_pos(t).  new_row >= 0: that row is the token this launch
+// writes, and its bf16 values (kw, vw: this lane's two dims of K and V)
+// replace what the load returned -- the write to memory need not land before
+// the chunk's load.
+__device__ __forceinline__ void stage_bchunk(const BChunk& R, int lane, char* vl, char* kl, int new_row, uint32_t kw,
+                                             uint32_t vw) {
   const int c = lane & 15, kg = lane >> 4;
-  // stage the rows: K token t at row t, V token t at row block_pos(t)
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     *(v4i*)(kl + (4 * i + kg) * KPITCH + 16 * c) = R.k[i];
     *(v4i*)(vl + block_pos(4 * i + kg) * VPITCH + 16 * c) = R.v[i];
   }
+  if (__builtin_expect(new_row >= 0, 0)) {
+    *(uint32_t*)(kl + new_row * KPITCH + 4 * lane) = kw;
+    *(uint32_t*)(vl + block_pos(new_row) * VPITCH + 4 * lane) = vw;
+  }
+}
+
+// The Vᵀ operands of a staged chunk (ds_read_b64_tr_b16, see the file header).
+__device__ __forceinline__ void read_vt(v8bf* va, int lane, const char* vl) {
+  const int kg = lane >> 4, sk = (lane & 15) >> 2, sa = lane & 3;  // lane addresses row 8kg + sk (+4), dims 16n + 4sa
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    typedef __attribute__((address_space(3))) v4bf lds_v4bf;
+    const char* base = vl + (8 * kg + sk) * VPITCH + (16 * n + 4 * sa) * 2;
+    const v4bf r0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base));
+    const v4bf r1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base + 4 * VPITCH));
+    va[n] = (v8bf){r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
+  }
+}
+
+// One staged chunk: Q·Kᵀ, online softmax, P·V.
+__device__ __forceinline__ void compute_bchunk(BState& st, const v8bf* qop, int valid, int lane, char* vl, char* kl) {
+  const int c = lane & 15, kg = lane >> 4;
   wave_lds_sync();
 
   // ---------------- scores (log2 domain: the query carries scale * log2 e) ----------------
@@ -105,17 +123,7 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) ka[j][ks] = *(const v8bf*)(kl + (16 * j + c) * KPITCH + 64 * ks + 16 * kg);
-  {
-    const int sk = (lane & 15) >> 2, sa = lane & 3;  // this lane addresses row 8kg + sk (+4), dims 16n + 4sa
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      typedef __attribute__((address_space(3))) v4bf lds_v4bf;
-      char* base = vl + (8 * kg + sk) * VPITCH + (16 * n + 4 * sa) * 2;
-      const v4bf r0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base));
-      const v4bf r1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(base + 4 * VPITCH));
-      va[n] = (v8bf){r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]};
-    }
-  }
+  read_vt(va, lane, vl);
   __builtin_amdgcn_sched_barrier(0);
   float s[8];
 #pragma unroll
@@ -163,20 +171,16 @@ __device__ __forceinline__ void process_bchunk(const BChunk& R, BState& st, cons
   wave_lds_sync();  // the next chunk's staging overwrites these rows (K and V)
 }
 
-__device__ __forceinline__ void store_bf16_row_pair(const RowSrc& src, int b, int h, void* dst_base, int64_t sb,
-                                                    int64_t sh, int64_t pos, int lane) {
+// This lane's two dims (2 lane, 2 lane + 1) of the new token's row, rounded to bf16 and packed.
+__device__ __forceinline__ uint32_t bf16_row_pair(const RowSrc& src, int b, int h, int lane) {
   float x0, x1;
   load2_as_float(src, row_base(src, b, h, 0) + 2 * lane, x0, x1);
   const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
-  const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-  *(uint32_t*)((__bf16*)dst_base + (int64_t)b * sb + (int64_t)h * sh + pos * HEAD_DIM + 2 * lane) = w;
+  return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
 }
 
-template <int NW>
-__global__ __launch_bounds__(NW * 64) void decode_bf16_kernel(const DecodeArgs a) {
-  using BL = BLayout<NW>;
-  constexpr int BW = NW;
-  __shared__ __attribute__((aligned(16))) char smem[BL::BYTES];
+__global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[BL_BYTES];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, kg = lane >> 4;
@@ -198,17 +202,8 @@ __global__ __launch_bounds__(NW * 64) void decode_bf16_kernel(const DecodeArgs a
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, a.T * ROWB), rv = make_rsrc(vbase, a.T * ROWB);
   const __amdgpu_buffer_rsrc_t none = make_rsrc(kbase, 0);
 
-  // Fused write of the newest token (position new_pos: T-1, or a ring slot),
-  // by the split whose range holds it, before that split reads it.  Ranges
-  // start on chunk boundaries, so no other split loads that position.
-  if (fused && t_begin <= a.new_pos && a.new_pos < t_end) {
-    if (wave == 0) store_bf16_row_pair(a.knew, b, h, (void*)a.kq, a.k_sb, a.k_sh, a.new_pos, lane);
-    else if (wave == 1) store_bf16_row_pair(a.vnew, b, h, (void*)a.vq, a.v_sb, a.v_sh, a.new_pos, lane);
-    __threadfence_block();
-    __syncthreads();
-  }
-
-  // Query first, then the first chunk; the query is split while it streams.
+  // Query first, then the first chunks, then (fused) the new token's row:
+  // nothing waits for anything before the loads are out.
   const int hh = tid >> 5, d0 = (tid & 31) * 4;
   const int hq_ld = h * a.G + (hh < a.G ? hh : 0);
   const int64_t qi = (int64_t)b * a.q_sb + (int64_t)hq_ld * a.q_sh + d0;
@@ -217,7 +212,7 @@ __global__ __launch_bounds__(NW * 64) void decode_bf16_kernel(const DecodeArgs a
   const v2i qw0 = *(const v2i*)qp;
   const v2i qw1 = *(const v2i*)(qp + (es == 4 ? 8 : 0));
 
-  constexpr int NBUF = 2;
+  constexpr int NBUF = 2;  // chunks in flight per wave
   const int n_split = (t_end - t_begin + BCH - 1) / BCH;
   const int n_w = n_split > wave ? (n_split - wave + BW - 1) / BW : 0;
   const int blk0 = t_begin / BCH + wave;
@@ -225,8 +220,26 @@ __global__ __launch_bounds__(NW * 64) void decode_bf16_kernel(const DecodeArgs a
   BChunk buf[NBUF];
   load_bchunk(buf[0], rk, rv, none, 0 < n_w, blk0, loff);
 
+  // Fused write of the newest token (position new_pos: T-1, or a ring slot)
+  // by the wave whose chunk holds it, in the split whose range holds it:
+  // ranges start on chunk boundaries, so no other wave or split reads that
+  // position.  The wave puts the token's bf16 values into its staged chunk
+  // (stage_bchunk) and stores them for later steps: nothing waits for the
+  // store, and the chunk's own load of that row (old or new bytes) is
+  // overwritten in LDS.
+  const bool writes = fused && t_begin <= a.new_pos && a.new_pos < t_end;
+  const int new_chunk = writes ? (int)(a.new_pos / BCH) - t_begin / BCH : -1;  // chunk within the split
+  const bool owner = writes && new_chunk % BW == wave;
+  const int new_step = owner ? new_chunk / BW : -1;  // this wave's step that holds the new token
+  const int new_row = writes ? (int)(a.new_pos % BCH) : -1;
+  uint32_t knew_w = 0, vnew_w = 0;
+  if (owner) {
+    knew_w = bf16_row_pair(a.knew, b, h, lane);
+    vnew_w = bf16_row_pair(a.vnew, b, h, lane);
+  }
+
   {
-    __bf16* qop = (__bf16*)(smem + BL::QOP);
+    __bf16* qop = (__bf16*)(smem + BL_QOP);
     if (tid < 256) {
       const v4i raw = {qw0[0], qw0[1], qw1[0], qw1[1]};
 #pragma unroll
@@ -246,35 +259,43 @@ __global__ __launch_bounds__(NW * 64) void decode_bf16_kernel(const DecodeArgs a
     }
   }
   __syncthreads();
+  if (owner) {
+    *(uint32_t*)((__bf16*)a.kq + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh + a.new_pos * HEAD_DIM + 2 * lane) = knew_w;
+    *(uint32_t*)((__bf16*)a.vq + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh + a.new_pos * HEAD_DIM + 2 * lane) = vnew_w;
+  }
   v8bf qop[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) qop[ks] = ((const v8bf*)(smem + BL::QOP))[ks * 64 + lane];
+  for (int ks = 0; ks < 4; ++ks) qop[ks] = ((const v8bf*)(smem + BL_QOP))[ks * 64 + lane];
 
   BState st;
   st.m = NEG_INF;
   st.l = 0.f;
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.acc[n] = (v4f){0.f, 0.f, 0.f, 0.f};
-  char* vl = smem + BL::V + wave * BCH * VPITCH;
-  char* kl = smem + BL::K + wave * BCH * KPITCH;
+  char* vl = smem + BL_V + wave * BCH * VPITCH;
+  char* kl = smem + BL_K + wave * BCH * KPITCH;
 
-  // Ring as in the quantized decode: step i loads chunk i+1, computes chunk i;
-  // padded to whole revolutions, only the padding's compute is skipped.
+  // Ring as in the quantized decode: step i loads chunk i+1, then stages and
+  // computes chunk i (its freed registers take the operands); padded to whole
+  // revolutions, padding steps load through an empty resource (no load sits
+  // under a branch) and only their staging and compute are skipped.
   const int n_pad = (n_w + NBUF - 1) / NBUF * NBUF;
   for (int i0 = 0; i0 < n_pad; i0 += NBUF) {
 #pragma unroll
     for (int j = 0; j < NBUF; ++j) {
       const int i = i0 + j;
       load_bchunk(buf[(j + 1) % NBUF], rk, rv, none, i + 1 < n_w, blk0 + BW * (i + 1), loff);
-      if (i < n_w) process_bchunk(buf[j], st, qop, t_end - (blk0 + BW * i) * BCH, lane, vl, kl);
+      if (i < n_w) {
+        stage_bchunk(buf[j], lane, vl, kl, i == new_step ? new_row : -1, knew_w, vnew_w);
+        compute_bchunk(st, qop, t_end - (blk0 + BW * i) * BCH, lane, vl, kl);
+      }
     }
   }
 
   // ---------------- wave partial -> LDS (columns c and c+8 summed) ----------------
   st.l = sum_xor32(sum_xor16(st.l));
-  float* part = (float*)(smem + BL::PART);
-  float* pstat = (float*)(smem + BL::PSTAT);
-  if constexpr (NW != 4) __syncthreads();  // the partials overwrite staging rows other waves may still read
+  float* part = (float*)(smem + BL_PART);
+  float* pstat = (float*)(smem + BL_PSTAT);
 #pragma unroll
   for (int n = 0; n < 8; ++n)
 #pragma unroll
@@ -406,13 +427,7 @@ hipError_t launch_ring_join_bf16(const AppendArgs& a, void* rk, void* rv, int64_
 }
 
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream) {
-  // a one-split plan (a short cache: one workgroup per (sequence, KV head)
-  // writes the output) runs eight waves, so that a 513-token window has all
-  // its chunks in flight at once
-  if (a.S == 1)
-    hipLaunchKernelGGL(decode_bf16_kernel<8>, dim3(1, a.Hkv, a.B), dim3(512), 0, stream, a);
-  else
-    hipLaunchKernelGGL(decode_bf16_kernel<4>, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(decode_bf16_kernel, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
