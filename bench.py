@@ -158,7 +158,8 @@ class DecodeWorkload:
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
             vcode, vc.data_ptr(), vs.data_ptr(), None if vz is None else vz.data_ptr(),
-            self.sinks.data_ptr(), SCALE, self.B, self.hq, self.hkv, D, c.offset, c.capacity, self.splits,
+            self.sinks.data_ptr(), SCALE, None, 0, 0, 0, 0, self.B, self.hq, self.hkv, D, c.offset, c.capacity,
+            self.splits,
             self.ws.data_ptr(), self.ws.numel(), _lib.REC_F32, self.out.data_ptr(),
             self.torch.cuda.current_stream().cuda_stream,
         )
@@ -543,14 +544,15 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
         if bf:
             rc = lib.rec_prefill_bf16(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3], kr.data_ptr(), kr.stride(0),
                                       kr.stride(1), vr.data_ptr(), vr.stride(0), vr.stride(1), sinks.data_ptr(), SCALE,
-                                      1, 0, 1, HQ, HKV, D, L, T, 0, ws.data_ptr(), ws.numel(), _lib.REC_F32,
+                                      1, 0, None, 0, 0, 0, 0, 0, 1, HQ, HKV, D, L, T, 0, ws.data_ptr(), ws.numel(),
+                                      _lib.REC_F32,
                                       out.data_ptr(), st)
             _lib.check(rc, "rec_prefill_bf16")
             return
         rc = lib.rec_prefill_attn(q.data_ptr(), _lib.REC_BF16, *q.stride()[:3],
                                   kq.code, kq.codes.data_ptr(), kq.scales.data_ptr(), ptr(kq.zeros),
                                   vq.code, vq.codes.data_ptr(), vq.scales.data_ptr(), ptr(vq.zeros),
-                                  sinks.data_ptr(), SCALE, 1, 0,
+                                  sinks.data_ptr(), SCALE, 1, 0, None, 0, 0, 0, 0, 0,
                                   1, HQ, HKV, D, L, T, c.capacity, 0, ws.data_ptr(), ws.numel(), _lib.REC_F32,
                                   out.data_ptr(), st)
         _lib.check(rc, "rec_prefill_attn")

@@ -108,6 +108,14 @@ int rec_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
  * aligned, of out_dtype: REC_F32, or REC_BF16 / REC_F16 (the fp32 result
  * rounded to nearest even, the query dtype the reference returns,
  * model.py:132-139 — no separate cast launch).
+ * bias (NULL: none): an additive score bias, the reference's mask array
+ * (model.py:122-128) after its broadcasting — a bool mask as 0 / -inf, a float
+ * mask as it is, in natural-log units like the scores — with element
+ * (b, kv head h, group member g, key t) at bias[b*bias_sb + h*bias_skv +
+ * g*bias_sg + t] (strides 0 where the mask broadcasts, non-negative
+ * multiples of 4; 16-byte aligned; bias_extent = elements readable from
+ * bias, below 2^29).  A row that every key leaves out gets the sink alone
+ * (zeros without sinks).
  * splits <= 0 picks rec_decode_default_splits().
  * Replaces quantized_attention_with_sinks, engine/src/rec_mlx/model.py:108-139
  * (split-K structure of engine/src/rec_mlx/kernels/megakernel.py:619-693 and
@@ -117,6 +125,7 @@ int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     int k_bits, const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros,
                     int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
                     const float* sinks, float scale,
+                    const float* bias, int64_t bias_sb, int64_t bias_skv, int64_t bias_sg, int64_t bias_extent,
                     int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
                     void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
@@ -189,7 +198,10 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * causal != 0, query i sees tokens [0, T-L+i]; window > 0 further limits
  * query position p to keys > p - window (a sliding-window mask array of
  * model.py:122-128; window 0 = none) — with optional sink logits.
- * out (B, Hq, L, D) of out_dtype (REC_F32, REC_BF16 or REC_F16, as the decode).  Any cache format of rec_decode_attn (int8 or uint4
+ * out (B, Hq, L, D) of out_dtype (REC_F32, REC_BF16 or REC_F16, as the decode).
+ * bias: as rec_decode_attn's, with query l of the chunk at + l*bias_sl; with a
+ * bias, causal and window must be 0 (the bias carries the whole mask) and the
+ * chunk takes the tiled kernel.  Any cache format of rec_decode_attn (int8 or uint4
  * in any mix, or the affine pair): K/V tiles are dequantized into on-chip
  * memory, never to HBM — int8 codes exactly with the row scales applied to
  * scores and probabilities, 4-bit and affine values as x̂ rounded to the
@@ -211,6 +223,8 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
                      int k_bits, const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros,
                      int v_bits, const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros,
                      const float* sinks, float scale, int causal, int window,
+                     const float* bias, int64_t bias_sb, int64_t bias_skv, int64_t bias_sg, int64_t bias_sl,
+                     int64_t bias_extent,
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int64_t capacity,
                      int splits, void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
@@ -264,8 +278,8 @@ int rec_ring_join_bf16(void* k_ring, void* v_ring, int64_t rk_sb, int64_t rk_sh,
  * GQA decode attention over the first T tokens of a bf16 K/V cache, with an
  * optional fused write of the newest token (k_new / v_new (B, Hkv, 1, D), any
  * float dtype, stored at position T-1 first; NULL: no write).  Query, sinks,
- * scale, splits, workspace and output as rec_decode_attn; the split-K partial
- * and the merge are both launched.
+ * scale, bias, splits, workspace and output as rec_decode_attn; the split-K
+ * partial and the merge are both launched.
  * Replaces the attention of Attention.__call__ over a FixedKVCache,
  * engine/src/rec_mlx/model.py:204-211 (FixedKVCache.update_and_fetch first,
  * cache.py:145-150), whose fused-decoder form is the bf16 split-K partial of
@@ -276,6 +290,7 @@ int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
                     int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh,
                     void* k, int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh,
                     const float* sinks, float scale,
+                    const float* bias, int64_t bias_sb, int64_t bias_skv, int64_t bias_sg, int64_t bias_extent,
                     int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
                     void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 
@@ -324,6 +339,8 @@ int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scale
 int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st,
                      const void* k, int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh,
                      const float* sinks, float scale, int causal, int window,
+                     const float* bias, int64_t bias_sb, int64_t bias_skv, int64_t bias_sg, int64_t bias_sl,
+                     int64_t bias_extent,
                      int B, int Hq, int Hkv, int D, int L, int64_t T, int splits,
                      void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream);
 

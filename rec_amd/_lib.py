@@ -44,8 +44,9 @@ SIGNATURES = {
     "rec_workspace_init": (_i, [_p, _sz, _p]),
     "rec_decode_attn": (
         _i,
-        [_p, _i, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p,
-         _p],
+        [_p, _i, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f,
+         _p, _i64, _i64, _i64, _i64,  # bias, strides (b, kv head, group member), extent
+         _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p, _p],
     ),
     "rec_decode_append_attn": (
         _i,
@@ -65,8 +66,9 @@ SIGNATURES["rec_decode_scratch_bytes"] = (_sz, [])
 SIGNATURES["rec_decode_merge"] = (_i, [_p, _i, _i, _i, _i64, _i, _i, _p, _sz, _i, _p, _p])
 SIGNATURES["rec_prefill_attn"] = (
     _i,
-    [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64, _i64,
-     _i, _p, _sz, _i, _p, _p],
+    [_p, _i, _i64, _i64, _i64, _i, _p, _p, _p, _i, _p, _p, _p, _p, _f, _i, _i,
+     _p, _i64, _i64, _i64, _i64, _i64,  # bias, strides (b, kv head, group member, query), extent
+     _i, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p, _p],
 )
 SIGNATURES["rec_prefill_workspace_bytes"] = (_sz, [_i, _i, _i, _i, _i])
 
@@ -86,7 +88,7 @@ SIGNATURES["rec_decode_bf16"] = (
         _p, _i, _i64, _i64,  # q
         _p, _p, _i, _i64, _i64, _i64, _i64,  # new k/v
         _p, _i64, _i64, _p, _i64, _i64,  # bf16 K, V
-        _p, _f, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p, _p,
+        _p, _f, _p, _i64, _i64, _i64, _i64, _i, _i, _i, _i, _i64, _i64, _i, _p, _sz, _i, _p, _p,
     ],
 )
 SIGNATURES["rec_decode_bf16_ring"] = (
@@ -102,8 +104,9 @@ SIGNATURES["rec_decode_bf16_ring"] = (
 SIGNATURES["rec_kv_dequant_bf16"] = (_i, [_i, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i64, _i64, _p, _p, _p])
 SIGNATURES["rec_prefill_bf16"] = (
     _i,
-    [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _f, _i, _i, _i, _i, _i, _i, _i, _i64,
-     _i, _p, _sz, _i, _p, _p],
+    [_p, _i, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _f, _i, _i,
+     _p, _i64, _i64, _i64, _i64, _i64,  # bias
+     _i, _i, _i, _i, _i, _i64, _i, _p, _sz, _i, _p, _p],
 )
 SIGNATURES["rec_q4_packed_bytes"] = (_sz, [_i64, _i64])
 SIGNATURES["rec_q4_pack"] = (_i, [_p, _p, _p, _i64, _i64, _p, _sz, _p])

@@ -147,7 +147,7 @@ def _check_cache_shapes(queries, keys: QuantizedKV, values: QuantizedKV):
 
 
 def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, splits, out,
-                   k_new=None, v_new=None, T=None, capacity=None, sink_dtype=None):
+                   k_new=None, v_new=None, T=None, capacity=None, sink_dtype=None, bias=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv = keys.n_kv_heads
@@ -162,16 +162,17 @@ def _decode_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks
         splits = lib.rec_decode_default_splits(B, Hkv, T)
     ws = workspace(dev, B, Hkv, splits, stream)
     sk = _sinks(sinks, Hq, dev, sink_dtype)
-    common_tail = (
-        _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity), int(splits),
+    shape_tail = (
+        B, Hq, Hkv, D, int(T), int(capacity), int(splits),
         ws.data_ptr(), ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream,
     )
+    common_tail = (_ptr(sk), float(scale), *shape_tail)
     if k_new is None:
         rc = lib.rec_decode_attn(
             q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1),
             keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
             values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
-            *common_tail,
+            _ptr(sk), float(scale), *_bias_args(bias, True), *shape_tail,
         )
         _lib.check(rc, "rec_decode_attn")
     else:
@@ -204,7 +205,7 @@ def prefill_workspace(device: torch.device, B: int, Hq: int, Hkv: int, L: int, s
 
 
 def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sinks, causal, out, splits=0, window=0,
-                    sink_dtype=None):
+                    sink_dtype=None, bias=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     q = queries if queries.stride(-1) == 1 else queries.contiguous()
@@ -216,7 +217,8 @@ def _prefill_launch(queries, keys: QuantizedKV, values: QuantizedKV, scale, sink
         q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), q.stride(2),
         keys.code, keys.codes.data_ptr(), keys.scales.data_ptr(), _ptr(keys.zeros),
         values.code, values.codes.data_ptr(), values.scales.data_ptr(), _ptr(values.zeros),
-        _ptr(sk), float(scale), int(causal), int(window), B, Hq, keys.n_kv_heads, D, L, int(keys.length),
+        _ptr(sk), float(scale), int(causal), int(window), *_bias_args(bias, False),
+        B, Hq, keys.n_kv_heads, D, L, int(keys.length),
         int(keys.capacity),
         int(splits), ws.data_ptr(), ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream,
     )
@@ -250,14 +252,18 @@ def quantized_attention_with_sinks(
 
     ``keys``/``values`` are what :meth:`QuantizedKVCache.update_and_fetch`
     returns; ``sinks`` (``n_q`` logits or None) join the softmax denominator;
-    ``mask`` is None, "causal", a boolean array or an additive 0 / -inf array
-    whose pattern is all keys or causal (:func:`_mask_plan`; for ``L == 1``
-    both mean "every cached token").  ``L == 1`` runs the split-K decode kernel; ``L > 1`` (bf16/f16
-    queries, the newest ``L`` cached tokens) the chunked prefill kernel, which
-    reads every cache format directly (4-bit and affine values rounded to the
-    query dtype, as the reference dequantizes, int8 codes exactly).  A
-    sliding-window mask is applied by the prefill kernel, also for one query
-    (bf16/f16), which then sees the last ``window`` tokens.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
+    ``mask`` is None, "causal", or a boolean or additive float array with the
+    reference's broadcasting against the scores (model.py:122-128: a
+    four-dimensional mask is ``(B, n_kv, L, T)``): host arrays holding the
+    causal or causal sliding-window pattern take those kernels' own masking
+    (:func:`_mask_plan`), any other array is added to the scores as a bias
+    inside the kernels (:func:`_mask_bias`; padding masks of a ragged batch,
+    per-head masks, finite additive masks).  ``L == 1`` runs the split-K
+    decode kernel (a window pattern as a bias over the keys); ``L > 1``
+    (bf16/f16 queries, the newest ``L`` cached tokens) the chunked prefill
+    kernel, which reads every cache format directly (4-bit and affine values
+    rounded to the query dtype, as the reference dequantizes, int8 codes
+    exactly) and applies a sliding-window pattern itself.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
     (default: the query dtype, as the reference returns, model.py:132-139).
     The sinks enter as float32 values at every ``L``, the cast this function
     makes in the reference (model.py:129); ``sink_dtype`` (bf16/f16) rounds
@@ -275,19 +281,27 @@ def quantized_attention_with_sinks(
     if not keys.affine and 4 in (key_bits, value_bits) and group_size != 32:
         raise ValueError(f"4-bit caches use groups of 32, got group_size={group_size}")
     _check_cache_shapes(queries, keys, values)
-    causal, win = _mask_plan(mask, L, int(keys.length))
-    if L == 1 and not win:
+    if L > keys.length:  # the L queries are the newest L cached tokens (model.py:122-125)
+        raise ValueError(f"{L} queries but only {keys.length} cached tokens")
+    Hkv = keys.n_kv_heads
+    T = int(keys.length)
+    causal, win, bias = _resolve_mask(mask, B, Hkv, Hq // Hkv, L, T, queries.device)
+    if L == 1 and win:
+        # one query under a window: the decode kernel with the window as a
+        # bias over the keys (-inf before the last `win`), the reference's
+        # single-query arithmetic on the exact dequantized values (model.py:108-139)
+        keep = torch.full((1, T), float("-inf"), dtype=torch.float32, device=queries.device)
+        keep[:, T - win:] = 0.0
+        bias, win = _mask_bias(keep, B, Hkv, Hq // Hkv, 1, T, queries.device), 0
+    if L == 1:
         out, want = _new_out((B, Hq, D), out_dtype, queries)
-        _decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype)
+        _decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype, bias=bias)
         out = out.view(B, Hq, 1, D)
     else:
-        # the L queries are the newest L cached tokens (model.py:122-125)
-        if L > keys.length:
-            raise ValueError(f"{L} queries but only {keys.length} cached tokens")
         if queries.dtype not in (torch.bfloat16, torch.float16):
-            raise NotImplementedError("prefill (and windowed) queries must be bf16 or f16 (the matrix-core input type)")
+            raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
         out, want = _new_out((B, Hq, L, D), out_dtype, queries)
-        _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0, win, sink_dtype)
+        _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0, win, sink_dtype, bias)
     return _finish(out, want)
 
 
@@ -296,7 +310,7 @@ def _bf16_kv_ok(t: torch.Tensor) -> bool:
 
 
 def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=None, v_new=None, T=None,
-                        capacity=None, slot=None, sink_dtype=None):
+                        capacity=None, slot=None, sink_dtype=None, bias=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv = keys.shape[1]
@@ -320,15 +334,17 @@ def _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, k_new=
                v_new.stride(0), v_new.stride(1))
     head = (q.data_ptr(), _DTYPES[q.dtype], q.stride(0), q.stride(1), *new,
             keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
-            _ptr(sk), float(scale), B, Hq, Hkv, D, int(T), int(capacity))
+            _ptr(sk), float(scale))
+    shape = (B, Hq, Hkv, D, int(T), int(capacity))
     tail = (int(splits), ws.data_ptr(), ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream)
     if slot is None:
-        _lib.check(lib.rec_decode_bf16(*head, *tail), "rec_decode_bf16")
+        _lib.check(lib.rec_decode_bf16(*head, *_bias_args(bias, True), *shape, *tail), "rec_decode_bf16")
     else:  # a ring step: the new token goes to `slot`
-        _lib.check(lib.rec_decode_bf16_ring(*head, int(slot), *tail), "rec_decode_bf16_ring")
+        _lib.check(lib.rec_decode_bf16_ring(*head, *shape, int(slot), *tail), "rec_decode_bf16_ring")
 
 
-def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out, splits=0, sink_dtype=None):
+def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, out, splits=0, sink_dtype=None,
+                         bias=None):
     lib = _lib.load()
     B, Hq, L, D = queries.shape
     Hkv, T = keys.shape[1], keys.shape[2]
@@ -341,25 +357,32 @@ def _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, window, ou
     rc = lib.rec_prefill_bf16(
         queries.data_ptr(), _DTYPES[queries.dtype], queries.stride(0), queries.stride(1), queries.stride(2),
         keys.data_ptr(), keys.stride(0), keys.stride(1), values.data_ptr(), values.stride(0), values.stride(1),
-        _ptr(sk), float(scale), int(causal), int(window), B, Hq, Hkv, D, L, T, int(splits), ws.data_ptr(),
+        _ptr(sk), float(scale), int(causal), int(window), *_bias_args(bias, False), B, Hq, Hkv, D, L, T,
+        int(splits), ws.data_ptr(),
         ws.numel(), _DTYPES[out.dtype], out.data_ptr(), stream,
     )
     _lib.check(rc, "rec_prefill_bf16")
 
 
+def _is_host(mask) -> bool:
+    return not (isinstance(mask, torch.Tensor) and mask.device.type != "cpu")
+
+
 def _mask_plan(mask, L, T):
-    """How the kernels apply ``mask`` to ``L`` queries at positions
-    ``T - L .. T - 1`` over ``T`` keys: ``(causal, window)``.
+    """The fast pattern of a host-resident ``mask`` for ``L`` queries at
+    positions ``T - L .. T - 1`` over ``T`` keys: ``(causal, window)``, or
+    None when the array holds another pattern (it then runs as a bias,
+    :func:`_mask_bias`).
 
     The reference's rules (model.py:122-128): None keeps every key; "causal"
     keeps keys at or before each query's position; a boolean array keeps the
-    keys where it is True; a float array is added to the scores, so here it
-    may hold only 0 (keep) and -inf (drop).  Arrays broadcast to ``(L, T)``
-    (leading dims of size one, or equal slices).  The kernels run three
-    patterns: every key ``(False, 0)``, causal ``(True, 0)``, and causal
+    keys where it is True; a float array is added to the scores (here a
+    pattern only when it holds just 0 and -inf).  Three patterns have kernels
+    of their own: every key ``(False, 0)``, causal ``(True, 0)``, and causal
     limited to the last ``window`` keys ``(True, window)``
-    (engine/src/rec_mlx/cache.py:199-205); any other pattern raises
-    NotImplementedError.
+    (engine/src/rec_mlx/cache.py:199-205).  Host arrays are checked here, on
+    the host; device arrays are not inspected (that would wait for the GPU,
+    and could not run under HIP-graph capture): they always run as a bias.
     """
     if mask is None:
         return False, 0
@@ -367,35 +390,99 @@ def _mask_plan(mask, L, T):
         if mask != "causal":
             raise NotImplementedError(f"mask {mask!r} is not supported")
         return True, 0
-    m = mask if isinstance(mask, torch.Tensor) else torch.as_tensor(mask)
+    if not _is_host(mask):
+        return None
+    m = torch.as_tensor(mask)
     if m.dtype == torch.bool:
         keep = m
     elif m.is_floating_point():
         if not bool(((m == 0) | (m == float("-inf"))).all()):
-            raise NotImplementedError("additive masks must hold only 0 and -inf")
+            return None
         keep = m == 0
     else:
         raise NotImplementedError(f"mask dtype {m.dtype} is not supported (bool or float)")
-    while keep.dim() > 2:  # leading (batch, head) dims: one pattern for all
+    if keep.dim() > 4:
+        raise NotImplementedError(f"masks of {keep.dim()} dimensions are not supported (at most 4)")
+    if keep.dim() == 0 or keep.shape[-1] not in (1, T) or (keep.dim() >= 2 and keep.shape[-2] not in (1, L)):
+        raise ValueError(f"mask of shape {tuple(m.shape)} does not broadcast to ({L}, {T})")
+    while keep.dim() > 2:  # leading (head, batch) dims: a pattern only if every slice is alike
         if not bool((keep == keep[:1]).all()):
-            raise NotImplementedError("masks that differ between sequences or heads are not supported")
+            return None
         keep = keep[0]
     if keep.dim() < 2:
         keep = keep.reshape(1, -1)
-    if keep.shape[-1] != T or keep.shape[0] not in (1, L):
-        raise NotImplementedError(f"mask of shape {tuple(mask.shape)} does not broadcast to ({L}, {T})")
     keep = keep.expand(L, T)
     if bool(keep.all()):
         return False, 0
-    q = torch.arange(T - L, T, device=keep.device)[:, None]
-    k = torch.arange(T, device=keep.device)[None]
+    q = torch.arange(T - L, T)[:, None]
+    k = torch.arange(T)[None]
     causal = q >= k
     if torch.equal(keep, causal):
         return True, 0
     window = int(keep[-1].sum())
     if window > 0 and torch.equal(keep, causal & (q < k + window)):
         return True, window
-    raise NotImplementedError("only causal or causal sliding-window mask patterns are supported")
+    return None
+
+
+def _mask_bias(mask, B, Hkv, G, L, T, device):
+    """``mask`` as the additive score bias the kernels read: ``(tensor,
+    (sb, skv, sg, sl, extent))``.
+
+    As the reference (model.py:122-128): a boolean mask keeps the keys where
+    it is True (bias 0, else -inf), a float mask is added to the scores; the
+    mask broadcasts against the scores ``(B, Hkv, G, L, T)`` (G query heads
+    per KV head) after a mask of four dimensions ``(B, Hkv, L, T)`` gains a
+    group axis (``expand_dims(mask, -3)``).  The bias keeps the mask's own
+    extents (strides 0 where it broadcasts), as float32 with the key axis
+    padded to a multiple of 4 and 16-byte aligned rows: one copy on the
+    device, no host synchronisation.
+    """
+    m = torch.as_tensor(mask, device=device)
+    if m.dtype == torch.bool:
+        m = torch.where(m, 0.0, float("-inf")).to(torch.float32)
+    elif m.is_floating_point():
+        m = m.to(torch.float32)
+    else:
+        raise NotImplementedError(f"mask dtype {m.dtype} is not supported (bool or float)")
+    if m.dim() > 4:
+        raise NotImplementedError(f"masks of {m.dim()} dimensions are not supported (at most 4)")
+    if m.dim() == 4:
+        m = m.unsqueeze(-3)
+    while m.dim() < 5:
+        m = m.unsqueeze(0)
+    try:
+        m.expand(B, Hkv, G, L, T)
+    except RuntimeError:
+        raise ValueError(f"mask of shape {tuple(mask.shape)} does not broadcast to the scores "
+                         f"({B}, {Hkv}, {G}, {L}, {T})") from None
+    lead = tuple(m.shape[:4])
+    Tp = (T + 3) // 4 * 4
+    buf = torch.empty(lead + (Tp,), dtype=torch.float32, device=device)
+    buf[..., :T] = m.expand(lead + (T,))
+    st = [buf.stride(i) if lead[i] > 1 else 0 for i in range(4)]
+    if buf.numel() >= 1 << 29:
+        raise NotImplementedError(f"a mask of {buf.numel()} elements is not supported (below 2^29)")
+    return buf, (st[0], st[1], st[2], st[3], buf.numel())
+
+
+def _resolve_mask(mask, B, Hkv, G, L, T, device):
+    """``(causal, window, bias)`` for the kernels: a fast pattern
+    (:func:`_mask_plan`) with ``bias`` None, or ``(False, 0, bias)`` with the
+    bias of any other mask array (:func:`_mask_bias`)."""
+    plan = _mask_plan(mask, L, T)
+    if plan is not None:
+        return plan[0], plan[1], None
+    return False, 0, _mask_bias(mask, B, Hkv, G, L, T, device)
+
+
+def _bias_args(bias, decode):
+    """The bias arguments of a launch: pointer, strides (b, kv head, group
+    member[, query]) and extent, or all zero."""
+    if bias is None:
+        return (None, 0, 0, 0, 0) if decode else (None, 0, 0, 0, 0, 0)
+    t, (sb, skv, sg, sl, ext) = bias
+    return (t.data_ptr(), sb, skv, sg, ext) if decode else (t.data_ptr(), sb, skv, sg, sl, ext)
 
 
 def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=None, *, out_dtype=None,
@@ -406,8 +493,9 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
     in the softmax denominator: the call Attention.__call__ makes for those
     caches (model.py:204-211, the fused SDPA's sinks argument).  One query
     token decodes; ``L > 1`` queries are the newest ``L`` of the ``T`` keys,
-    under ``mask`` None, "causal" or a causal (sliding-window) boolean array;
-    ``window`` limits a causal mask to the last ``window`` keys.  The sinks
+    under ``mask`` None, "causal" or a boolean / additive array (the rules of
+    :func:`quantized_attention_with_sinks`); ``window`` limits a causal mask
+    to the last ``window`` keys.  The sinks
     are taken as given (as float32 values); ``sink_dtype`` (bf16/f16) rounds
     them first -- the reference's caller hands them over in the query dtype
     (model.py:211), and :func:`attend` passes it.
@@ -421,18 +509,22 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
     T = keys.shape[2]
     if L > T:
         raise ValueError(f"{L} queries but only {T} keys")
-    causal, win = _mask_plan(mask, L, T)
+    Hkv = keys.shape[1]
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads is not a multiple of {Hkv} KV heads")
     if window is not None:
-        causal, win = True, (0 if window >= T else int(window))
+        causal, win, bias = True, (0 if window >= T else int(window)), None
+    else:
+        causal, win, bias = _resolve_mask(mask, B, Hkv, Hq // Hkv, L, T, queries.device)
     if L == 1:
         if win:  # one query sees the last `win` keys: attend over that slice
             keys, values = keys[:, :, T - win:], values[:, :, T - win:]
         out, want = _new_out((B, Hq, D), out_dtype, queries)
-        _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype)
+        _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype, bias=bias)
         out = out.view(B, Hq, 1, D)
     else:
         out, want = _new_out((B, Hq, L, D), out_dtype, queries)
-        _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0, sink_dtype)
+        _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0, sink_dtype, bias)
     return _finish(out, want)
 
 
@@ -450,24 +542,32 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
     quantized cache (model.py:202) and on every call over the bf16 caches
     (model.py:211).  A :class:`FixedSlidingKVCache` applies its own window: a
     single decode token takes a mask that keeps every held token (None, as its
-    ``make_mask`` returns), anything else raises NotImplementedError.
+    ``make_mask`` returns, "causal", or such a host array), anything else
+    raises NotImplementedError.  A decode step fuses its append with the
+    attention when the mask keeps every key (None, "causal", a host array of
+    that pattern); a mask array on the GPU (never inspected: :func:`_mask_plan`)
+    takes the append, then the masked attention.
     """
     _check_query(queries)
     B, Hq, L, D = queries.shape
     qdt = queries.dtype
-    if queries.dtype not in (torch.bfloat16, torch.float16):
-        # chunks, and a single query under a window over a quantized cache,
-        # run on the matrix cores: refused here, before the append changes
-        # the cache
-        quantized = not isinstance(cache, (FixedSlidingKVCache, FixedKVCache))
-        if L > 1 or (quantized and mask is not None and _mask_plan(mask, 1, cache.offset + 1)[1]):
-            raise NotImplementedError("prefill (and windowed) queries must be bf16 or f16 (the matrix-core input type)")
-    if isinstance(cache, FixedSlidingKVCache):
+    ring = isinstance(cache, FixedSlidingKVCache)
+    # one query's host-checked pattern over the cache after the append (None:
+    # a device array, or another pattern: a bias); for one query "causal"
+    # keeps every key (window 0)
+    plan1 = None
+    if L == 1:
+        plan1 = _mask_plan(mask, 1, min(cache.offset + 1, cache.capacity) if ring else cache.offset + 1)
+    keeps_all = mask is None or (plan1 is not None and plan1[1] == 0)
+    if queries.dtype not in (torch.bfloat16, torch.float16) and L > 1:
+        # chunks run on the matrix cores: refused here, before the append
+        # changes the cache
+        raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
+    if ring:
         # a new token goes to its ring slot and decode attends over the valid
         # slots (order-free); a chunk attends over the ring in order plus
         # itself, causally within the window
-        # (for one query, "causal" or a causal array keeps every key: window 0)
-        if L == 1 and mask is not None and _mask_plan(mask, 1, min(cache.offset + 1, cache.capacity))[1]:
+        if L == 1 and not keeps_all:
             raise NotImplementedError("a decode step over the sliding ring sees every held token (mask None)")
         if L == 1 and fused:
             # one launch pair: the token written into its slot by the split
@@ -496,8 +596,8 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
                                             window=cache.window_size, sink_dtype=qdt)
     if isinstance(cache, FixedKVCache):
         # the fused step attends over every token; any other single-query
-        # mask pattern (a window) takes the write, then the masked attention
-        if fused and L == 1 and (mask is None or not _mask_plan(mask, 1, cache.offset + 1)[1]):
+        # mask (a window, a bias) takes the write, then the masked attention
+        if fused and L == 1 and keeps_all:
             if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
                 raise ValueError("a fused decode step takes one new K/V token of a float dtype")
             st = cache.storage
@@ -518,9 +618,9 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
         k, v = cache.update_and_fetch(keys, values)
         return scaled_dot_product_attention(queries, k, v, scale, mask, sinks, out_dtype=out_dtype, splits=splits,
                                             sink_dtype=qdt)
-    # one query under a sliding window (a causal mask keeps every key) takes
-    # the append, then the windowed prefill kernel
-    if fused and L == 1 and not _mask_plan(mask, 1, cache.offset + 1)[1]:
+    # one query under a sliding window, or a mask array (a bias), takes the
+    # append, then the masked attention
+    if fused and L == 1 and keeps_all:
         cache._check_usable()
         if keys.shape != values.shape or keys.shape[2] != 1 or keys.dtype not in _DTYPES or values.dtype != keys.dtype:
             raise ValueError("a fused decode step takes one new K/V token of a float dtype")

@@ -102,6 +102,21 @@ int check_dtype(int dt, const char* name) {
   return REC_OK;
 }
 
+// A score bias (mask array): 16-byte aligned, strides non-negative multiples
+// of 4 elements (the kernels read four keys per 16-byte load), extent below
+// 2^29 elements (byte offsets fit a 32-bit buffer offset).  null: no bias.
+int make_bias(const float* p, int64_t sb, int64_t skv, int64_t sg, int64_t sl, int64_t extent, BiasArgs* out) {
+  *out = BiasArgs{};
+  if (!p) return REC_OK;
+  if (!aligned16(p)) return fail(REC_EALIGN, "bias must be 16-byte aligned");
+  if (sb < 0 || skv < 0 || sg < 0 || sl < 0 || sb % 4 || skv % 4 || sg % 4 || sl % 4)
+    return fail(REC_EALIGN, "bias strides must be non-negative multiples of 4 elements");
+  if (extent < 1 || extent >= ((int64_t)1 << 29))
+    return fail(REC_EUNSUPPORTED, "bias extent of %lld elements (1 .. 2^29 - 1 supported)", (long long)extent);
+  *out = BiasArgs{p, sb, skv, sg, sl, extent};
+  return REC_OK;
+}
+
 // Splits actually launched for a request.  Regular splits cover
 // [0, t_split_end) in spans of whole 32-token chunks; with a fused append the
 // newest token's chunk [t_split_end, T) is one more split of its own, so the
@@ -128,7 +143,7 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
                   const uint16_t* ks, const uint16_t* kz, int v_bits, const void* vq, const uint16_t* vs,
                   const uint16_t* vz, const float* sinks, float scale, int B, int Hq, int Hkv, int D, int64_t T,
                   int64_t cap, int splits, void* ws, size_t ws_bytes, int out_dtype, void* out,
-                  const RowSrc* knew, const RowSrc* vnew, int phases, void* stream) {
+                  const RowSrc* knew, const RowSrc* vnew, int phases, void* stream, const BiasArgs* bias = nullptr) {
   int e;
   if ((e = resolve_formats(k_bits, v_bits, &k_bits, &v_bits))) return e;
   if ((e = check_dtype(q_dtype, "query"))) return e;
@@ -170,6 +185,7 @@ int decode_common(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_
   a.sinks = sinks;
   a.out = out;
   a.out_dtype = out_dtype;
+  if (bias) a.bias = *bias;
   a.ws_stat = (float*)((char*)ws + w.stat);
   a.ws_acc = (float*)((char*)ws + w.acc);
   if (knew) {
@@ -308,12 +324,15 @@ int rec_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
 
 int rec_decode_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int k_bits, const void* k_codes,
                     const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits, const void* v_codes,
-                    const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks, float scale, int B,
-                    int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
+                    const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks, float scale,
+                    const float* bias, int64_t bias_sb, int64_t bias_skv, int64_t bias_sg, int64_t bias_extent,
+                    int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
                     size_t workspace_bytes, int out_dtype, void* out, void* stream) {
+  BiasArgs bz;
+  if (int e = make_bias(bias, bias_sb, bias_skv, bias_sg, 0, bias_extent, &bz)) return e;
   return decode_common(q, q_dtype, q_sb, q_sh, k_bits, k_codes, k_scales, k_zeros, v_bits, v_codes, v_scales, v_zeros,
                        sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes, out_dtype, out,
-                       nullptr, nullptr, 3, stream);
+                       nullptr, nullptr, 3, stream, &bz);
 }
 
 static int append_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
@@ -455,7 +474,8 @@ size_t rec_prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int splits) {
 int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int k_bits,
                      const void* k_codes, const uint16_t* k_scales, const uint16_t* k_zeros, int v_bits,
                      const void* v_codes, const uint16_t* v_scales, const uint16_t* v_zeros, const float* sinks,
-                     float scale, int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T,
+                     float scale, int causal, int window, const float* bias, int64_t bias_sb, int64_t bias_skv,
+                     int64_t bias_sg, int64_t bias_sl, int64_t bias_extent, int B, int Hq, int Hkv, int D, int L, int64_t T,
                      int64_t capacity, int splits, void* workspace, size_t workspace_bytes, int out_dtype, void* out,
                      void* stream) {
   int e;
@@ -477,6 +497,10 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   if (!aligned16(out)) return fail(REC_EALIGN, "output must be 16-byte aligned");
   if ((e = check_cache(kf, k_codes, k_scales, k_zeros, "key")) || (e = check_cache(vf, v_codes, v_scales, v_zeros, "value")))
     return e;
+  BiasArgs bz;
+  if ((e = make_bias(bias, bias_sb, bias_skv, bias_sg, bias_sl, bias_extent, &bz))) return e;
+  if (bias && (causal || window))
+    return fail(REC_EINVAL, "a bias (mask array) carries the whole mask: causal and window must be 0 with it");
   if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
   PrefillArgs a{};
   a.q = q;
@@ -496,6 +520,7 @@ int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.sinks = sinks;
   a.out = out;
   a.out_dtype = out_dtype;
+  a.bias = bz;
   a.q_mul = scale * LOG2E;
   a.B = B;
   a.Hq = Hq;
@@ -541,7 +566,8 @@ int rec_kv_dequant_bf16(int k_bits, const void* k_codes, const uint16_t* k_scale
 
 int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
                      int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale,
-                     int causal, int window, int B, int Hq, int Hkv, int D, int L, int64_t T, int splits,
+                     int causal, int window, const float* bias, int64_t bias_sb, int64_t bias_skv, int64_t bias_sg,
+                     int64_t bias_sl, int64_t bias_extent, int B, int Hq, int Hkv, int D, int L, int64_t T, int splits,
                      void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream) {
   if (q_dtype != REC_BF16 && q_dtype != REC_F16)
     return fail(REC_EUNSUPPORTED, "prefill queries must be bf16 or f16 (the matrix-core input type)");
@@ -558,6 +584,10 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   if (k_sb % 8 || k_sh % 8 || v_sb % 8 || v_sh % 8)
     return fail(REC_EALIGN, "K/V batch and head strides must be multiples of 8 elements");
   if (!std::isfinite(scale)) return fail(REC_EINVAL, "scale must be finite");
+  BiasArgs bz;
+  if (int e = make_bias(bias, bias_sb, bias_skv, bias_sg, bias_sl, bias_extent, &bz)) return e;
+  if (bias && (causal || window))
+    return fail(REC_EINVAL, "a bias (mask array) carries the whole mask: causal and window must be 0 with it");
   PrefillArgs a{};
   a.q = q;
   a.q_dtype = q_dtype;
@@ -576,6 +606,7 @@ int rec_prefill_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int
   a.sinks = sinks;
   a.out = out;
   a.out_dtype = out_dtype;
+  a.bias = bz;
   a.q_mul = scale * LOG2E;
   a.B = B;
   a.Hq = Hq;
@@ -662,7 +693,7 @@ static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
                        int64_t k_sb, int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks,
                        float scale, int B, int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits,
                        void* workspace, size_t workspace_bytes, int out_dtype, void* out, void* stream,
-                       int64_t new_pos) {
+                       int64_t new_pos, const BiasArgs& bias) {
   int e;
   if ((e = check_dtype(q_dtype, "query"))) return e;
   if ((e = check_dtype(out_dtype, "output"))) return e;
@@ -708,6 +739,7 @@ static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
   a.sinks = sinks;
   a.out = out;
   a.out_dtype = out_dtype;
+  a.bias = bias;
   a.ws_stat = (float*)((char*)workspace + w.stat);
   a.ws_acc = (float*)((char*)workspace + w.acc);
   if (append) {
@@ -732,12 +764,15 @@ static int decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, c
 
 int rec_decode_bf16(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new, const void* v_new,
                     int new_dtype, int64_t kn_sb, int64_t kn_sh, int64_t vn_sb, int64_t vn_sh, void* k, int64_t k_sb,
-                    int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale, int B, int Hq,
-                    int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
+                    int64_t k_sh, void* v, int64_t v_sb, int64_t v_sh, const float* sinks, float scale,
+                    const float* bias, int64_t bias_sb, int64_t bias_skv, int64_t bias_sg, int64_t bias_extent, int B,
+                    int Hq, int Hkv, int D, int64_t T, int64_t capacity, int splits, void* workspace,
                     size_t workspace_bytes, int out_dtype, void* out, void* stream) {
+  BiasArgs bz;
+  if (int e = make_bias(bias, bias_sb, bias_skv, bias_sg, 0, bias_extent, &bz)) return e;
   return decode_bf16(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, kn_sb, kn_sh, vn_sb, vn_sh, k, k_sb, k_sh, v,
                      v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes,
-                     out_dtype, out, stream, T - 1);
+                     out_dtype, out, stream, T - 1, bz);
 }
 
 int rec_decode_bf16_ring(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, const void* k_new,
@@ -750,7 +785,7 @@ int rec_decode_bf16_ring(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh,
   if (slot < 0 || slot >= T) return fail(REC_EINVAL, "slot %lld outside the %lld occupied slots", (long long)slot, (long long)T);
   return decode_bf16(q, q_dtype, q_sb, q_sh, k_new, v_new, new_dtype, kn_sb, kn_sh, vn_sb, vn_sh, k, k_sb, k_sh, v,
                      v_sb, v_sh, sinks, scale, B, Hq, Hkv, D, T, capacity, splits, workspace, workspace_bytes,
-                     out_dtype, out, stream, slot);
+                     out_dtype, out, stream, slot, BiasArgs{});
 }
 
 size_t rec_q4_packed_bytes(int64_t N, int64_t K) {

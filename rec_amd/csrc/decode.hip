@@ -268,9 +268,10 @@ __device__ __forceinline__ float bf16_at(const v4i& w, int slot) {
   return __builtin_bit_cast(float, (slot & 1) ? (x & 0xffff0000u) : (x << 16));
 }
 
-template <int KB, int VB, bool EXACT>
+template <int KB, int VB, bool EXACT, bool MASK>
 __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v4i* qop, float qsc, float qsum_a,
-                                              float qsum_b, int valid, int lane, char* meta) {
+                                              float qsum_b, int valid, int lane, char* meta, const v4i* bz,
+                                              float bmul) {
   const int c = lane & 15, kg = lane >> 4;
   // int8 scales arrive as the lane's own 16-byte run (positions 8kg ..
   // 8kg+7).  int4 scales and zero-points arrive one dword per lane; this
@@ -397,6 +398,16 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       }
     }
   }
+  // MASK: the bias of the lane's tokens 16j + 4kg + i (bz[j][i], natural
+  // log units) joins each score, in the score's units (bmul = log2 e / qsc);
+  // -inf drops the token
+  if constexpr (MASK) {
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) {
+      const int w = bz[idx >> 2][idx & 3];  // a copy: a bit_cast of a vector subscript reads element 0
+      s[idx] = __builtin_fmaf(__builtin_bit_cast(float, w), bmul, s[idx]);
+    }
+  }
   // tail chunk: tokens past the split end (rare: without the hint the
   // compiler turns this into compares and selects on every chunk)
   if (__builtin_expect(valid < CH, 0)) {
@@ -438,7 +449,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   if (__ballot(cmax > st.m + gap)) {
     cmax = max_xor32(max_xor16(cmax));
     const float m_new = fmaxf(st.m, cmax);
-    const float factor = __builtin_amdgcn_exp2f(st.m - m_new);  // 0 on the first chunk, 1 if unchanged
+    // 0 on the first chunk, 1 if unchanged (MASK: a head whose every score so
+    // far is -inf keeps m = -inf and zero sums)
+    const float factor = MASK && st.m == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(st.m - m_new);
     st.l *= factor;
     if constexpr (VB == FMT_A4) {
       st.vb[0] *= factor;
@@ -449,9 +462,12 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     st.m = m_new;
   }
   float p[8];
+  // MASK: while a head's running max is still -inf every score it has seen is
+  // -inf, and p = exp2(-inf - 0) = 0 (not exp2(NaN))
+  const float moff = MASK && st.m == NEG_INF ? 0.f : st.m;
 #pragma unroll
   for (int idx = 0; idx < 8; ++idx) {
-    p[idx] = __builtin_amdgcn_exp2f(fmaf(s[idx], qsc, -st.m));
+    p[idx] = __builtin_amdgcn_exp2f(fmaf(s[idx], qsc, -moff));
     st.l += p[idx];
   }
 
@@ -595,7 +611,7 @@ struct Depth {
   static constexpr int value = 2;
 };
 
-template <int KB, int VB, int WAVES, bool EXACT>
+template <int KB, int VB, int WAVES, bool EXACT, bool MASK>
 __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) {
   using LD = Lds<WAVES>;
   __shared__ __attribute__((aligned(16))) char smem[LD::bytes];
@@ -669,6 +685,27 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
   Chunk buf[NBUF];
 #pragma unroll
   for (int i = 0; i < NBUF - 1; ++i) load_chunk<KB, VB>(buf[i], R, lo, i < n_w, blk0 + WAVES * i, mbase);
+  // MASK: the bias row of this lane's head (column c, head c mod 8), two
+  // 16-byte runs per chunk, loaded with the chunk into a ring of its own
+  v4i bz[NBUF][2];
+  __amdgpu_buffer_rsrc_t rb = R.none;
+  uint32_t boff = 0;
+  if constexpr (MASK) {
+    const int64_t base = (int64_t)b * a.bias.sb + (int64_t)h * a.bias.skv;
+    rb = make_rsrc(a.bias.p + base, (a.bias.extent - base) * 4);
+    const int gq = (c & 7) < a.G ? (c & 7) : 0;
+    boff = (uint32_t)(((int64_t)gq * a.bias.sg + 4 * kg) * 4);
+  }
+  const auto load_bias = [&](v4i(&z)[2], bool ok, int blk) {
+    if constexpr (MASK) {
+      const __amdgpu_buffer_rsrc_t r = ok ? rb : R.none;
+      const uint32_t t0 = (uint32_t)blk * CH * 4;
+      z[0] = ld128<0>(r, boff + t0, 0);
+      z[1] = ld128<0>(r, boff + t0 + 64, 0);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i) load_bias(bz[i], i < n_w, blk0 + WAVES * i);
 
   // Quantize the query into MFMA operands while the chunks stream in.
   {
@@ -689,6 +726,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
   // and all-zero scores, for which any positive step is exact
   const float qsc_h = ((const float*)(smem + LDS_QSC))[c & 7];
   const float qsc = qsc_h > 0.f ? qsc_h : 1.f;
+  const float bmul = MASK ? LOG2E / qsc : 0.f;
   // query sums per group of this lane's head (exact integers): int4 K, the
   // lane's two 32-dim groups; affine K, the two 64-dim groups
   float qsum_a = 0.f, qsum_b = 0.f;
@@ -722,9 +760,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
       const int i = i0 + j;
       load_chunk<KB, VB>(buf[(j + NBUF - 1) % NBUF], R, lo, i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1),
                          mbase);
+      load_bias(bz[(j + NBUF - 1) % NBUF], i + NBUF - 1 < n_w, blk0 + WAVES * (i + NBUF - 1));
       if (i < n_w)
-        process_chunk<KB, VB, EXACT>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH, lane,
-                              smem + LD::meta + wave * 1024);
+        process_chunk<KB, VB, EXACT, MASK>(buf[j], st, qop, qsc, qsum_a, qsum_b, t_end - (blk0 + WAVES * i) * CH,
+                                           lane, smem + LD::meta + wave * 1024, bz[j], bmul);
     }
   }
 
@@ -870,7 +909,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(const DecodeArgs a) {
 
 template <int KB, int VB, int W, bool EXACT>
 static void launch_partial(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_kernel<KB, VB, W, EXACT>), dim3(a.S, a.Hkv, a.B), dim3(64 * W), 0, stream, a);
+  hipLaunchKernelGGL((decode_kernel<KB, VB, W, EXACT, false>), dim3(a.S, a.Hkv, a.B), dim3(64 * W), 0, stream, a);
 }
 
 template <int KB, int VB, int W>
@@ -879,7 +918,22 @@ static void launch_partial_pv(const DecodeArgs& a, hipStream_t stream) {
   else launch_partial<KB, VB, W, false>(a, stream);
 }
 
+// A bias (mask array) may leave any row a few visible keys: the exact P·V,
+// four waves, every format.
+template <int KB, int VB>
+static void launch_masked(const DecodeArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_kernel<KB, VB, 4, true, true>), dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
+}
+
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream) {
+  if (a.bias.p != nullptr) {
+    if (kb == 8 && vb == 8) launch_masked<8, 8>(a, stream);
+    else if (kb == 8 && vb == 4) launch_masked<8, 4>(a, stream);
+    else if (kb == 4 && vb == 8) launch_masked<4, 8>(a, stream);
+    else if (kb == 4 && vb == 4) launch_masked<4, 4>(a, stream);
+    else launch_masked<FMT_A8, FMT_A4>(a, stream);
+    return hipGetLastError();
+  }
   if (kb == 8 && vb == 8) launch_partial<8, 8, 4, true>(a, stream);
   else if (kb == 8 && vb == 4) launch_partial_pv<8, 4, 4>(a, stream);
   else if (kb == 4 && vb == 8) launch_partial<4, 8, 4, true>(a, stream);

@@ -109,8 +109,11 @@ __device__ __forceinline__ void read_vt(v8bf* va, int lane, const char* vl) {
   }
 }
 
-// One staged chunk: Q·Kᵀ, online softmax, P·V.
-__device__ __forceinline__ void compute_bchunk(BState& st, const v8bf* qop, int valid, int lane, char* vl, char* kl) {
+// One staged chunk: Q·Kᵀ, online softmax, P·V.  MASK: bz holds the bias of
+// the lane's tokens 16j + 4kg + i (natural-log units, -inf drops a token).
+template <bool MASK>
+__device__ __forceinline__ void compute_bchunk(BState& st, const v8bf* qop, int valid, int lane, char* vl, char* kl,
+                                               const v4i* bz) {
   const int c = lane & 15, kg = lane >> 4;
   wave_lds_sync();
 
@@ -134,6 +137,13 @@ __device__ __forceinline__ void compute_bchunk(BState& st, const v8bf* qop, int 
 #pragma unroll
     for (int i = 0; i < 4; ++i) s[4 * j + i] = d[i] + dpp_ror8f(d[i]);  // high part + low part
   }
+  if constexpr (MASK) {
+#pragma unroll
+    for (int idx = 0; idx < 8; ++idx) {
+      const int w = bz[idx >> 2][idx & 3];  // a copy: a bit_cast of a vector subscript reads element 0
+      s[idx] = __builtin_fmaf(__builtin_bit_cast(float, w), LOG2E, s[idx]);
+    }
+  }
   // tail chunk: tokens past the split end (rare: without the hint the
   // compiler turns this into compares and selects on every chunk)
   if (__builtin_expect(valid < BCH, 0)) {
@@ -149,7 +159,8 @@ __device__ __forceinline__ void compute_bchunk(BState& st, const v8bf* qop, int 
   if (__ballot(cmax > st.m + RESCALE_GAP)) {
     cmax = max_xor32(max_xor16(cmax));
     const float m_new = fmaxf(st.m, cmax);
-    const float factor = __builtin_amdgcn_exp2f(st.m - m_new);
+    // (MASK: a head whose every score so far is -inf keeps m = -inf, zero sums)
+    const float factor = MASK && st.m == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(st.m - m_new);
     st.l *= factor;
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.acc[n] *= factor;
@@ -159,7 +170,7 @@ __device__ __forceinline__ void compute_bchunk(BState& st, const v8bf* qop, int 
   v8bf pb;
 #pragma unroll
   for (int idx = 0; idx < 8; ++idx) {
-    const float p = __builtin_amdgcn_exp2f(s[idx] - st.m);
+    const float p = __builtin_amdgcn_exp2f(s[idx] - (MASK && st.m == NEG_INF ? 0.f : st.m));
     st.l += p;
     const __bf16 hi = (__bf16)p;
     pb[idx] = c < 8 ? hi : (__bf16)(p - (float)hi);
@@ -179,6 +190,7 @@ __device__ __forceinline__ uint32_t bf16_row_pair(const RowSrc& src, int b, int 
   return (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
 }
 
+template <bool MASK>
 __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[BL_BYTES];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -219,6 +231,26 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
   const uint32_t loff = (uint32_t)(16 * lane);
   BChunk buf[NBUF];
   load_bchunk(buf[0], rk, rv, none, 0 < n_w, blk0, loff);
+  // MASK: the bias row of this lane's head (column c, head c mod 8), two
+  // 16-byte runs per chunk, loaded with the chunk into a ring of its own
+  v4i bz[NBUF][2];
+  __amdgpu_buffer_rsrc_t rb = none;
+  uint32_t boff = 0;
+  if constexpr (MASK) {
+    const int64_t base = (int64_t)b * a.bias.sb + (int64_t)h * a.bias.skv;
+    rb = make_rsrc(a.bias.p + base, (a.bias.extent - base) * 4);
+    const int gq = (c & 7) < a.G ? (c & 7) : 0;
+    boff = (uint32_t)(((int64_t)gq * a.bias.sg + 4 * kg) * 4);
+  }
+  const auto load_bias = [&](v4i(&z)[2], bool ok, int blk) {
+    if constexpr (MASK) {
+      const __amdgpu_buffer_rsrc_t r = ok ? rb : none;
+      const uint32_t t0 = (uint32_t)blk * BCH * 4;
+      z[0] = ld128<0>(r, boff + t0, 0);
+      z[1] = ld128<0>(r, boff + t0 + 64, 0);
+    }
+  };
+  load_bias(bz[0], 0 < n_w, blk0);
 
   // Fused write of the newest token (position new_pos: T-1, or a ring slot)
   // by the wave whose chunk holds it, in the split whose range holds it:
@@ -285,9 +317,10 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(const DecodeArgs a) {
     for (int j = 0; j < NBUF; ++j) {
       const int i = i0 + j;
       load_bchunk(buf[(j + 1) % NBUF], rk, rv, none, i + 1 < n_w, blk0 + BW * (i + 1), loff);
+      load_bias(bz[(j + 1) % NBUF], i + 1 < n_w, blk0 + BW * (i + 1));
       if (i < n_w) {
         stage_bchunk(buf[j], lane, vl, kl, i == new_step ? new_row : -1, knew_w, vnew_w);
-        compute_bchunk(st, qop, t_end - (blk0 + BW * i) * BCH, lane, vl, kl);
+        compute_bchunk<MASK>(st, qop, t_end - (blk0 + BW * i) * BCH, lane, vl, kl, bz[j]);
       }
     }
   }
@@ -427,7 +460,10 @@ hipError_t launch_ring_join_bf16(const AppendArgs& a, void* rk, void* rv, int64_
 }
 
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(decode_bf16_kernel, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
+  if (a.bias.p != nullptr)
+    hipLaunchKernelGGL(decode_bf16_kernel<true>, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL(decode_bf16_kernel<false>, dim3(a.S, a.Hkv, a.B), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -6,6 +6,19 @@
 
 namespace rec {
 
+// An additive bias on the attention scores (natural-log units, -inf drops a
+// key): element (b, kv head h, group member g, query l, key t) at
+//   p[b * sb + h * skv + g * sg + l * sl + t]   (key stride 1, strides 0 where
+// a dimension broadcasts), the reference's mask array after its broadcasting
+// (engine/src/rec_mlx/model.py:122-128).  extent: elements readable from p
+// (reads past a row's T keys fall on masked positions or past the extent,
+// where the buffer loads read zero).
+struct BiasArgs {
+  const float* p;  // null: no bias
+  int64_t sb, skv, sg, sl;
+  int64_t extent;
+};
+
 struct AppendArgs {
   RowSrc k, v;
   void* kq;
@@ -43,6 +56,7 @@ struct DecodeArgs {
   int span;         // tokens per regular split (multiple of 32)
   int t_split_end;  // end of the regular splits; a fused append adds one split [t_split_end, T)
   int64_t new_pos;  // bf16 fused write: the new token's position (T - 1, or its ring slot)
+  BiasArgs bias;    // additive score bias (a mask array), or none
 };
 
 // P·V takes the V-scaled probabilities P' = p·s as an fp16 operand.  Rounded
@@ -83,6 +97,7 @@ struct PrefillArgs {
   // writes an unnormalised partial; prefill_merge_kernel combines them
   int S, nqb;                  // splits, row blocks (PREFILL_BLOCK_ROWS (query, head) rows each)
   int64_t split_lo, split_len;
+  BiasArgs bias;               // additive score bias (a mask array), or none
   float* ws_acc;               // [B*Hkv][S][nqb][256][128]
   float* ws_stat;              // [B*Hkv][S][nqb][256] x (max, sum)
 };

@@ -435,13 +435,23 @@ __device__ __forceinline__ void qk_unit(const typename MT<BF16>::elem* K, const 
 // finite score), thr, the bound past which a score moves it (-inf until the
 // row has seen a finite score, then RESCALE_GAP), and l_run, the sum of
 // probabilities.  t = s * ksc - m_use is one fma per score.
-template <int VROW, bool VTR, bool EXACT, int NRT, int VPRE>
+template <int VROW, bool VTR, bool EXACT, int NRT, int VPRE, bool BIAS>
 __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Float16* Vv, const float* KS,
                                                 const float* VS, float (&m_use)[2], float (&thr)[2],
                                                 float (&l_run)[2], v4f (&acc)[8][2], int t0, int t_end,
                                                 const int (&qabs)[2], int causal, int window, bool mask,
-                                                int c, int g) {
+                                                int c, int g, __amdgpu_buffer_rsrc_t rb, const uint32_t (&brow)[2]) {
   v8h pb[2], pl[2];  // P'^T: high parts, and (EXACT) the remainders
+  // BIAS: the rows' bias (a mask array, natural-log units) for the lane's
+  // tokens t0 + 16j + 4g + i, from HBM first of all
+  v4f bz[2][2];
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int rt = 0; rt < NRT; ++rt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bz[rt][j] = __builtin_bit_cast(v4f, ld128<0>(rb, (brow[rt] + (uint32_t)(t0 + 16 * j + 4 * g)) * 4u, 0));
+  }
   // The unit's LDS reads first: the row scales and the first VPRE of the
   // eight V^T operands, whose latency the softmax arithmetic then covers
   // (one wait instead of one per pair of operands).
@@ -488,6 +498,12 @@ __device__ __forceinline__ void softmax_pv_unit(const v4f (&s4)[2][2], const _Fl
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) t[4 * j + i] = __builtin_fmaf(s4[rt][j][i], ksc[j][i], -m_use[rt]);
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[4 * j + i] = __builtin_fmaf(bz[rt][j][i], LOG2E, t[4 * j + i]);
+    }
     if (mask) {
       // first and last visible token of this row, relative to the lane's first token t0 + 4g
       const int last = (causal ? min(qabs[rt], t_end - 1) : t_end - 1) - t0 - 4 * g;
@@ -592,7 +608,9 @@ __device__ __forceinline__ void load_query(typename MT<BF16>::vec (&qop)[2][4], 
   }
 }
 
-template <bool BF16, int KF, int VF, bool EXACT, bool WIN>
+// MM, the mask mode: 0 causal or none, 1 + a sliding window, 2 + a bias
+// (mask array) read per unit and row
+template <bool BF16, int KF, int VF, bool EXACT, int MM>
 __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   typedef PfGeom<KF, VF> GEO;
   typedef typename MT<BF16>::elem E;
@@ -641,11 +659,24 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
     qabs[0] = P + qr[0];
     qabs[1] = P + qr[1];
   }
+  // MM == 2: each row's bias row (element offset; the host keeps the extent
+  // below 2^29 elements), read through a resource bounded by the extent
+  uint32_t brow[2] = {0u, 0u};
+  __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias.p, 0);
+  if constexpr (MM == 2) {
+    int prow[2], qr[2], hq[2];
+    rows(c, prow, qr, hq);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+      brow[rt] = (uint32_t)((int64_t)b * a.bias.sb + (int64_t)h * a.bias.skv +
+                            (int64_t)(hq[rt] - h * a.G) * a.bias.sg + (int64_t)qr[rt] * a.bias.sl);
+    rb = make_rsrc(a.bias.p, a.bias.extent * 4);
+  }
 
   // a sliding window starts the scan at the first query's first visible key
-  // (WIN: compiled in; without it the window is 0 and its terms vanish, which
-  // keeps the quantized scans clear of register spills)
-  const int window = WIN ? a.window : 0;
+  // (MM == 1: compiled in; without it the window is 0 and its terms vanish,
+  // which keeps the quantized scans clear of register spills)
+  const int window = MM == 1 ? a.window : 0;
   const int t_first = window > 0 ? max(0, P + q_lo - window + 1) / KT * KT : 0;
   // this workgroup's share of the keys, [lo, t_end): the split's range
   // (tile-aligned) within the query block's [t_first, t_blk); empty for some
@@ -722,9 +753,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
           if (pend) {
             // the unit before: this tile's unit u - 1, or the previous tile's last
             const int pb_ = u == 0 ? buf ^ 1 : buf, po = u == 0 ? KT - 32 : 32 * (u - 1);
-            softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT, GEO::vpre(EXACT)>(sc[(u + 1) & 1], Vl[pb_] + (GEO::VTR ? po * GEO::VPB : po),
-                                                        KS[pb_] + po, VS[pb_] + po, m_use, thr, l_run, acc, pend_t,
-                                                        t_end, qabs, a.causal, window, needs_mask(pend_t), c, g);
+            softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT, GEO::vpre(EXACT), MM == 2>(
+                sc[(u + 1) & 1], Vl[pb_] + (GEO::VTR ? po * GEO::VPB : po), KS[pb_] + po, VS[pb_] + po, m_use, thr,
+                l_run, acc, pend_t, t_end, qabs, a.causal, window, needs_mask(pend_t), c, g, rb, brow);
           }
         }
         pend = live;
@@ -749,9 +780,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
       // still pending: the last tile's last unit (every unit of a tile is
       // visited, and a tile has an even number of units, so its scores are in sc[1])
       if (pend)
-        softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT, GEO::vpre(EXACT)>(sc[1], Vl[buf] + GEO::vunit(U - 1), KS[buf] + KT - 32,
-                                                    VS[buf] + KT - 32, m_use, thr, l_run, acc, pend_t, t_end, qabs,
-                                                    a.causal, window, needs_mask(pend_t), c, g);
+        softmax_pv_unit<VROW, GEO::VTR, EXACT, NRT, GEO::vpre(EXACT), MM == 2>(
+            sc[1], Vl[buf] + GEO::vunit(U - 1), KS[buf] + KT - 32, VS[buf] + KT - 32, m_use, thr, l_run, acc,
+            pend_t, t_end, qabs, a.causal, window, needs_mask(pend_t), c, g, rb, brow);
 
       // the rows again, from an opaque copy of the lane's column: recomputed
       // here rather than held in registers through the main loop
@@ -889,23 +920,32 @@ size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S) {
   return rows * HEAD_DIM * 4 + rows * 2 * 4;
 }
 
-template <bool BF16, bool EXACT, bool WIN>
+template <bool BF16, bool EXACT, int MM>
 static void launch_quantized(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
   const int kf = a.k_fmt, vf = a.v_fmt;
-  if (kf == 8 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 8, EXACT, WIN>), grid, block, 0, stream, a);
-  else if (kf == 8 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 4, EXACT, WIN>), grid, block, 0, stream, a);
-  else if (kf == 4 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 8, EXACT, WIN>), grid, block, 0, stream, a);
-  else if (kf == 4 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 4, EXACT, WIN>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8, FMT_A4, EXACT, WIN>), grid, block, 0, stream, a);
+  if (kf == 8 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 8, EXACT, MM>), grid, block, 0, stream, a);
+  else if (kf == 8 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 4, EXACT, MM>), grid, block, 0, stream, a);
+  else if (kf == 4 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 8, EXACT, MM>), grid, block, 0, stream, a);
+  else if (kf == 4 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 4, EXACT, MM>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8, FMT_A4, EXACT, MM>), grid, block, 0, stream, a);
 }
 
 // The bf16 cache (ring windows) always takes the window at run time; the
-// quantized formats have a variant with it and one without.
+// quantized formats have a variant with it and one without.  A bias (mask
+// array) takes its own variants, always with the exact P·V: a mask may leave
+// any row a few visible keys.
 template <bool BF16, bool EXACT>
 static void launch_formats(const PrefillArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
-  if (a.k_fmt == FMT_BF) hipLaunchKernelGGL((prefill_kernel<BF16, FMT_BF, FMT_BF, EXACT, true>), grid, block, 0, stream, a);
-  else if (a.window > 0) launch_quantized<BF16, EXACT, true>(a, grid, block, stream);
-  else launch_quantized<BF16, EXACT, false>(a, grid, block, stream);
+  if (a.bias.p != nullptr) {
+    if (a.k_fmt == FMT_BF) hipLaunchKernelGGL((prefill_kernel<BF16, FMT_BF, FMT_BF, true, 2>), grid, block, 0, stream, a);
+    else launch_quantized<BF16, true, 2>(a, grid, block, stream);
+  } else if (a.k_fmt == FMT_BF) {
+    hipLaunchKernelGGL((prefill_kernel<BF16, FMT_BF, FMT_BF, EXACT, 1>), grid, block, 0, stream, a);
+  } else if (a.window > 0) {
+    launch_quantized<BF16, EXACT, 1>(a, grid, block, stream);
+  } else {
+    launch_quantized<BF16, EXACT, 0>(a, grid, block, stream);
+  }
 }
 
 // Fewest keys any query row of the launch sees: the first row's causal

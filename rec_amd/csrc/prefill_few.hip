@@ -457,7 +457,7 @@ static void launch_af(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipSt
 bool prefill_few_fits(const PrefillArgs& a) {
   const int rows = a.L * a.G;
   const bool fmt = (a.k_fmt == 8 && a.v_fmt == 8) || (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4);
-  return fmt && a.window == 0 &&
+  return fmt && a.window == 0 && a.bias.p == nullptr &&
          (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384));
 }
 

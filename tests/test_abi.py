@@ -71,10 +71,10 @@ def test_append_validation(lib):
 
 def _decode(lib, **kw):
     a = dict(q=16, dt=0, kb=8, vb=8, B=1, Hq=8, Hkv=1, D=128, T=10, cap=64, splits=0, ws=16, wsb=1 << 30, out=16,
-             odt=_lib.REC_F32)
+             odt=_lib.REC_F32, bias=(None, 0, 0, 0, 0))
     a.update(kw)
     return lib.rec_decode_attn(
-        a["q"], a["dt"], 0, 0, a["kb"], 16, 16, 16, a["vb"], 16, 16, 16, None, 0.088,
+        a["q"], a["dt"], 0, 0, a["kb"], 16, 16, 16, a["vb"], 16, 16, 16, None, 0.088, *a["bias"],
         a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["odt"], a["out"], None,
     )
 
@@ -91,6 +91,12 @@ def test_decode_validation(lib):
     assert _decode(lib, D=96) == _lib.REC_EUNSUPPORTED
     assert _decode(lib, odt=5) == _lib.REC_EINVAL  # output dtype: REC_F32, REC_BF16 or REC_F16
     assert "output" in _lib.last_error()
+    # a score bias (mask array): 16-byte aligned, strides multiples of 4, extent below 2^29
+    assert _decode(lib, bias=(8, 0, 0, 0, 64)) == _lib.REC_EALIGN
+    assert _decode(lib, bias=(16, 6, 0, 0, 64)) == _lib.REC_EALIGN
+    assert "multiples of 4" in _lib.last_error()
+    assert _decode(lib, bias=(16, 0, 0, 0, 1 << 29)) == _lib.REC_EUNSUPPORTED
+    assert _decode(lib, bias=(16, 0, 0, 0, 0)) == _lib.REC_EUNSUPPORTED
     # the affine format comes as REC_AFFINE8 keys with REC_AFFINE4 values only
     assert _decode(lib, kb=_lib.REC_AFFINE8, vb=8) == _lib.REC_EUNSUPPORTED
     assert _decode(lib, kb=_lib.REC_AFFINE4, vb=_lib.REC_AFFINE8) == _lib.REC_EUNSUPPORTED
@@ -111,12 +117,12 @@ def test_error_mapping():
 
 def _decode_bf16(lib, **kw):
     a = dict(q=16, dt=1, kn=None, vn=None, k=16, sb=0, sh=0, v=16, B=1, Hq=8, Hkv=1, D=128, T=10, cap=64,
-             splits=0, ws=16, wsb=1 << 30, out=16, odt=_lib.REC_F32)
+             splits=0, ws=16, wsb=1 << 30, out=16, odt=_lib.REC_F32, bias=(None, 0, 0, 0, 0))
     a.update(kw)
     return lib.rec_decode_bf16(
         a["q"], a["dt"], 0, 0, a["kn"], a["vn"], 1, 0, 0, 0, 0, a["k"], a["sb"], a["sh"], a["v"], a["sb"], a["sh"],
-        None, 0.088, a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], a["odt"],
-        a["out"], None,
+        None, 0.088, *a["bias"], a["B"], a["Hq"], a["Hkv"], a["D"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"],
+        a["odt"], a["out"], None,
     )
 
 
@@ -132,6 +138,7 @@ def test_decode_bf16_validation(lib):
     assert _decode_bf16(lib, T=100, cap=128, wsb=16, splits=3) == _lib.REC_EWORKSPACE
     assert _decode_bf16(lib, T=1025, cap=2048, wsb=16) == _lib.REC_EWORKSPACE
     assert _decode_bf16(lib, odt=3) == _lib.REC_EINVAL
+    assert _decode_bf16(lib, bias=(16, 0, 2, 0, 64)) == _lib.REC_EALIGN
     assert _decode_bf16(lib, kn=16) == _lib.REC_EINVAL  # new keys without new values
     assert _decode_bf16(lib, D=64) == _lib.REC_EUNSUPPORTED
     assert _decode_bf16(lib, q=8) == _lib.REC_EALIGN
@@ -206,11 +213,11 @@ def test_capacity_bound(lib):
 
 
 def _prefill(lib, **kw):
-    a = dict(L=4, T=1000, cap=1024, splits=0, ws=16, wsb=1 << 30, window=0)
+    a = dict(L=4, T=1000, cap=1024, splits=0, ws=16, wsb=1 << 30, window=0, causal=1, bias=(None, 0, 0, 0, 0, 0))
     a.update(kw)
     return lib.rec_prefill_attn(
-        16, _lib.REC_BF16, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088, 1, a["window"],
-        1, 8, 1, 128, a["L"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], _lib.REC_F32, 16, None,
+        16, _lib.REC_BF16, 0, 0, 0, 8, 16, 16, None, 8, 16, 16, None, None, 0.088, a["causal"], a["window"],
+        *a["bias"], 1, 8, 1, 128, a["L"], a["T"], a["cap"], a["splits"], a["ws"], a["wsb"], _lib.REC_F32, 16, None,
     )
 
 
@@ -222,6 +229,10 @@ def test_prefill_split_validation(lib):
     assert _prefill(lib, splits=3, ws=8) == _lib.REC_EALIGN
     assert _prefill(lib, window=-1) == _lib.REC_EINVAL
     assert "window" in _lib.last_error()
+    # a bias carries the whole mask: no causal flag or window beside it
+    assert _prefill(lib, bias=(16, 0, 0, 0, 1000, 4000)) == _lib.REC_EINVAL
+    assert "bias" in _lib.last_error()
+    assert _prefill(lib, causal=0, bias=(16, 0, 0, 0, 1001, 4004)) == _lib.REC_EALIGN
 
 
 def test_prefill_workspace_bytes(lib):

@@ -306,9 +306,14 @@ def test_bf16_prefill_window_mask_array(gpu, case):
     out = scaled_dot_product_attention(q, k, v, SCALE, mask, sinks, out_dtype=torch.float32)
     torch.cuda.synchronize()
     ref = O.attention(f32(q), bf16_np(k), bf16_np(v), SCALE, sinks=f32(sinks), mask=mask.cpu().numpy())
-    assert_close(f32(out), ref, "window mask array")
-    with pytest.raises(NotImplementedError):  # not a causal-window pattern
-        scaled_dot_product_attention(q, k, v, SCALE, ~mask, sinks)
+    assert_close(f32(out), ref, "window mask array (a bias)")
+    host = scaled_dot_product_attention(q, k, v, SCALE, mask.cpu(), sinks, out_dtype=torch.float32)  # the window kernel
+    assert_close(f32(host), ref, "window mask array (host: the window kernel)")
+    # the complement is no pattern of its own: a bias (a row may see no key at all)
+    inv = ~mask
+    out = scaled_dot_product_attention(q, k, v, SCALE, inv, sinks, out_dtype=torch.float32)
+    ref = O.attention(f32(q), bf16_np(k), bf16_np(v), SCALE, sinks=f32(sinks), mask=inv.cpu().numpy())
+    assert_close(f32(out), ref, "complement of the window")
 
 
 def test_sliding_window_prefill_chunks(gpu):

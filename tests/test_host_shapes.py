@@ -43,7 +43,7 @@ def test_mismatches_refused(qs, ks, vs, msg):
 # ---- mask arrays (model.py:122-128) -> the kernels' (causal, window) ----
 import numpy as np  # noqa: E402
 
-from rec_amd.attention import _mask_plan  # noqa: E402
+from rec_amd.attention import _mask_bias, _mask_plan  # noqa: E402
 
 
 def causal_keep(L, T, window=0):
@@ -77,22 +77,79 @@ def test_mask_plan_boolean_and_additive(L, T):
         assert _mask_plan(causal_keep(L, T, w), L, T) == (True, w)
 
 
-def test_mask_plan_refuses_other_patterns():
+def test_mask_plan_leaves_other_patterns_to_the_bias():
+    """Host arrays of another pattern have no fast path (None: they run as a
+    bias); shapes that do not broadcast and integer masks are refused."""
     L, T = 6, 20
     keep = causal_keep(L, T)
     odd = keep.clone()
     odd[2, 0] = False  # a hole in one row
-    with pytest.raises(NotImplementedError):
-        _mask_plan(odd, L, T)
-    with pytest.raises(NotImplementedError, match="only 0 and -inf"):
-        _mask_plan(torch.zeros(L, T).masked_fill(~keep, -1e4), L, T)
+    assert _mask_plan(odd, L, T) is None
+    assert _mask_plan(torch.zeros(L, T).masked_fill(~keep, -1e4), L, T) is None  # finite additive
     per_head = torch.stack([keep, torch.ones_like(keep)])[None]
-    with pytest.raises(NotImplementedError, match="differ"):
-        _mask_plan(per_head, L, T)
-    with pytest.raises(NotImplementedError, match="broadcast"):
+    assert _mask_plan(per_head, L, T) is None  # differs between heads
+    with pytest.raises(ValueError, match="broadcast"):
         _mask_plan(keep[:, :-1], L, T)
     with pytest.raises(NotImplementedError):
         _mask_plan(np.zeros((L, T), np.int32), L, T)
+
+
+def test_mask_plan_does_not_inspect_device_arrays():
+    """A mask array on the GPU is never read on the host (no synchronisation,
+    capturable): it always runs as a bias.  A stand-in object with a device
+    other than the CPU shows the rule without a GPU."""
+
+    class OnDevice(torch.Tensor):
+        @property
+        def device(self):
+            return torch.device("cuda", 0)
+
+    m = torch.ones(3, 9, dtype=torch.bool).as_subclass(OnDevice)
+    assert _mask_plan(m, 3, 9) is None
+
+
+def _scores_bias(mask, B, Hkv, G, L, T):
+    """The bias the kernels would read, gathered back into (B, Hkv, G, L, T)
+    from its strides (on the CPU)."""
+    buf, (sb, skv, sg, sl, ext) = _mask_bias(mask, B, Hkv, G, L, T, "cpu")
+    flat = buf.reshape(-1)
+    assert flat.numel() == ext and buf.data_ptr() % 16 == 0
+    assert all(x % 4 == 0 for x in (sb, skv, sg, sl))
+    out = torch.empty(B, Hkv, G, L, T)
+    for b in range(B):
+        for h in range(Hkv):
+            for g in range(G):
+                for l in range(L):
+                    o = b * sb + h * skv + g * sg + l * sl
+                    out[b, h, g, l] = flat[o : o + T]
+    return out
+
+
+def test_mask_bias_follows_the_reference_broadcasting():
+    """model.py:122-128: bool -> 0 / -inf, float as it is; a 4-D mask
+    (B, Hkv, L, T) gains the group axis; 3-D (G, L, T) and 2-D (L, T) broadcast
+    from the right.  Checked against explicit broadcasting of the same array."""
+    B, Hkv, G, L, T = 2, 3, 4, 5, 11
+    g = torch.Generator().manual_seed(3)
+    cases = [
+        torch.rand(L, T, generator=g) > 0.3,                  # (L, T)
+        torch.rand(1, T, generator=g) > 0.3,                  # one row for every query
+        torch.randn(G, L, T, generator=g),                    # per group member, additive
+        torch.rand(B, 1, 1, T, generator=g) > 0.5,            # padding: per sequence
+        torch.randn(B, Hkv, L, T, generator=g),               # per sequence and KV head
+        torch.rand(1, Hkv, 1, T, generator=g) > 0.5,
+        torch.rand(L, 1, generator=g) > 0.5,                  # broadcast over the keys
+    ]
+    for m in cases:
+        got = _scores_bias(m, B, Hkv, G, L, T)
+        ref = m.float() if m.is_floating_point() else torch.where(m, 0.0, float("-inf"))
+        if ref.dim() == 4:
+            ref = ref.unsqueeze(-3)
+        assert torch.equal(got, ref.expand(B, Hkv, G, L, T)), tuple(m.shape)
+    with pytest.raises(ValueError, match="broadcast"):
+        _mask_bias(torch.ones(3, L, T, dtype=torch.bool), B, Hkv, G, L, T, "cpu")  # 3 is neither 1 nor G
+    with pytest.raises(NotImplementedError):
+        _mask_bias(torch.ones(1, 1, 1, L, T, dtype=torch.bool), B, Hkv, G, L, T, "cpu")
 
 
 def test_sink_rounding_on_the_host():
