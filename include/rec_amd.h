@@ -33,7 +33,9 @@
  * Quantizer: MLX's affine_quantize (w_max = max(0, max w), w_min = min w,
  * step (w_max - w_min)/n_bins, the larger-magnitude extreme made exact, codes
  * round-half-away((w - b)/s) clamped to [0, n_bins]), scale and bias rounded to
- * bf16.
+ * bf16.  REC_AFFINE8_F16 with REC_AFFINE4_F16 is the same format with fp16
+ * scales and biases (rounded to nearest even): the reference allocates them in
+ * the keys' dtype (model.py:57-58), fp16 for an fp16 model.
  */
 #ifndef REC_AMD_H
 #define REC_AMD_H
@@ -58,8 +60,9 @@ enum {
 /* Element types of the float inputs (queries, new keys/values). */
 enum { REC_F16 = 0, REC_BF16 = 1, REC_F32 = 2 };
 
-/* k_bits / v_bits: 8 (int8 symmetric), 4 (uint4 group 32), or the affine pair */
-enum { REC_AFFINE8 = 0x108, REC_AFFINE4 = 0x104 };
+/* k_bits / v_bits: 8 (int8 symmetric), 4 (uint4 group 32), or an affine pair
+ * (bf16 or fp16 scales and biases) */
+enum { REC_AFFINE8 = 0x108, REC_AFFINE4 = 0x104, REC_AFFINE8_F16 = 0x208, REC_AFFINE4_F16 = 0x204 };
 
 /* Library version, e.g. "rec_amd 0.1.0 gfx950". */
 const char* rec_version(void);

@@ -202,11 +202,13 @@ def round_half_away(x):
     return (t + np.where(np.abs(frac) >= np.float32(0.5), np.sign(x), np.float32(0))).astype(np.float32)
 
 
-def quantize_affine(x, bits, group=64):
+def quantize_affine(x, bits, group=64, meta="bfloat16"):
     """MLX-style affine quantization of the last axis (module docstring).
 
     Returns ``(codes uint8 [..., D] (unpacked), scale [..., D/group],
-    bias [..., D/group])``; scale and bias are bf16 values held in float32.
+    bias [..., D/group])``; scale and bias are ``meta`` values ("bfloat16" or
+    "float16", the dtype the reference allocates them in: the keys' dtype,
+    model.py:57-58) held in float32, rounded to nearest even once at the end.
     """
     xf = np.asarray(x, dtype=np.float32)
     D = xf.shape[-1]
@@ -225,6 +227,9 @@ def quantize_affine(x, bits, group=64):
     bias = np.where(at_zero, np.float32(0), edge).astype(np.float32)
     q = round_half_away((g - bias[..., None]) / scale[..., None])
     q = np.minimum(np.maximum(q, 0), n_bins)
+    if meta == "float16":
+        return (q.reshape(xf.shape).astype(np.uint8), scale.astype(np.float16).astype(np.float32),
+                bias.astype(np.float16).astype(np.float32))
     return q.reshape(xf.shape).astype(np.uint8), bf16_rn(scale), bf16_rn(bias)
 
 

@@ -25,6 +25,7 @@ REC_EUNSUPPORTED = -6
 
 REC_F16, REC_BF16, REC_F32 = 0, 1, 2
 REC_AFFINE8, REC_AFFINE4 = 0x108, 0x104  # MLX-style affine group 64: 8-bit keys, 4-bit values
+REC_AFFINE8_F16, REC_AFFINE4_F16 = 0x208, 0x204  # the same with fp16 scales and biases
 
 # Every symbol include/rec_amd.h declares, with (restype, argtypes).
 _i, _i64, _f, _p, _sz = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t

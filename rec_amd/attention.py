@@ -630,7 +630,7 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
                              f"{tuple(cache.keys[0].shape[:2])}")
         if B != Bk:
             raise ValueError(f"queries have batch {B}, the new keys {Bk}")
-        cache._reserve(Bk, H, cache.offset + 1, keys.device)
+        cache._reserve(Bk, H, cache.offset + 1, keys.device, keys.dtype)
         k_kv, v_kv = cache._view()
         _check_cache_shapes(queries, k_kv, v_kv)
         kn = keys if _rows_aligned(keys) else keys.contiguous()

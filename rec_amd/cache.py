@@ -13,8 +13,11 @@ Formats (bits per K and V independently, ``group_size=32``):
 * 4-bit: asymmetric uint4, fp16 scale and zero-point per 32 dims.
 
 With ``group_size=64`` (the reference's default) the cache holds MLX-style
-affine codes, 8-bit keys and 4-bit values with a bf16 scale and bias per 64
-dims (``mx.quantize``'s algorithm, restated by the kernel).
+affine codes, 8-bit keys and 4-bit values with a scale and bias per 64 dims
+(``mx.quantize``'s algorithm, restated by the kernel), stored in the keys'
+dtype as the reference allocates them (model.py:57-58): fp16 for fp16 keys,
+bf16 for bf16 keys (and for fp32 keys, whose fp32 scales the kernels do not
+read: they are rounded to bf16).
 
 Codes and scales are stored in 32-token blocks laid out for the matrix-core
 operands of the decode kernel (table in ``rec_amd/csrc/common.h``), so the
@@ -56,8 +59,11 @@ class QuantizedKV(NamedTuple):
 
     @property
     def code(self) -> int:
-        """Format code of the C ABI (8, 4, REC_AFFINE8 or REC_AFFINE4)."""
+        """Format code of the C ABI (8, 4, REC_AFFINE8 / REC_AFFINE4, or with
+        fp16 scales REC_AFFINE8_F16 / REC_AFFINE4_F16)."""
         if self.affine:
+            if self.scales.dtype == torch.float16:
+                return _lib.REC_AFFINE8_F16 if self.bits == 8 else _lib.REC_AFFINE4_F16
             return _lib.REC_AFFINE8 if self.bits == 8 else _lib.REC_AFFINE4
         return self.bits
 
@@ -70,12 +76,19 @@ class QuantizedKV(NamedTuple):
         return self.codes.shape[2] * BLOCK
 
 
-def _alloc(B, H, cap, bits, is_v, device, affine=False):
+def affine_meta_dtype(dtype: torch.dtype) -> torch.dtype:
+    """dtype of the affine scales and biases for keys of ``dtype``: the keys'
+    own (model.py:57-58), fp32 keys excepted (bf16: the kernels read 16-bit
+    scales)."""
+    return torch.float16 if dtype == torch.float16 else torch.bfloat16
+
+
+def _alloc(B, H, cap, bits, is_v, device, affine=False, meta_dtype=torch.bfloat16):
     """Zeroed codes/scales/zeros of one cache tensor (layout table in rec_amd/csrc/common.h)."""
     nb = cap // BLOCK
-    if affine:  # [scale, bias] x 2 groups x 32 slots of bf16 per block
+    if affine:  # [scale, bias] x 2 groups x 32 slots of bf16 (or fp16) per block
         codes = torch.zeros((B, H, nb, BLOCK * HEAD_DIM * bits // 8), dtype=torch.uint8, device=device)
-        scales = torch.zeros((B, H, nb, 2, HEAD_DIM // GROUP_AFFINE, BLOCK), dtype=torch.bfloat16, device=device)
+        scales = torch.zeros((B, H, nb, 2, HEAD_DIM // GROUP_AFFINE, BLOCK), dtype=meta_dtype, device=device)
         return codes, scales, None
     if bits == 8:
         codes = torch.zeros((B, H, nb, BLOCK * HEAD_DIM), dtype=torch.int8, device=device)
@@ -207,7 +220,9 @@ class QuantizedKVCache:
         if not self._usable:
             raise RuntimeError("Quantized KV cache was invalidated by a failed GPU call")
 
-    def _reserve(self, B, H, needed, device):
+    def _reserve(self, B, H, needed, device, dtype=torch.bfloat16):
+        """Room for ``needed`` tokens; the first allocation fixes the affine
+        scale dtype from the keys' ``dtype``, growth keeps it."""
         if self.max_tokens is not None and needed > self.max_tokens:
             raise ValueError("Decode context limit exhausted")
         if self.keys is not None and needed <= self.capacity:
@@ -216,8 +231,9 @@ class QuantizedKVCache:
             cap = -(-self.max_tokens // BLOCK) * BLOCK
         else:
             cap = -(-needed // self.step) * self.step
-        k = _alloc(B, H, cap, self.key_bits, False, device, self.affine)
-        v = _alloc(B, H, cap, self.value_bits, True, device, self.affine)
+        meta = self.keys[1].dtype if self.keys is not None else affine_meta_dtype(dtype)
+        k = _alloc(B, H, cap, self.key_bits, False, device, self.affine, meta)
+        v = _alloc(B, H, cap, self.value_bits, True, device, self.affine, meta)
         if self.keys is not None:
             k = tuple(_grow_tensor(o, n) if n is not None else None for o, n in zip(self.keys, k))
             v = tuple(_grow_tensor(o, n) if n is not None else None for o, n in zip(self.values, v))
@@ -246,7 +262,7 @@ class QuantizedKVCache:
         if self.keys is not None and (self.keys[0].shape[0], self.keys[0].shape[1]) != (B, H):
             raise ValueError("batch/head shape differs from the cached one")
         prev = self.offset
-        self._reserve(B, H, prev + L, keys.device)
+        self._reserve(B, H, prev + L, keys.device, keys.dtype)
         k, ksb, ksh, kst = _stride3(keys)
         v, vsb, vsh, vst = _stride3(values)
         lib = _lib.load()

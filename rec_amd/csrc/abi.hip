@@ -71,15 +71,25 @@ int check_bits(int bits, const char* name) {
 }
 
 // (k_bits, v_bits) -> kernel formats: this library's 8 / 4 in any mix, or
-// the MLX-style affine pair REC_AFFINE8 keys with REC_AFFINE4 values.
+// the MLX-style affine pair REC_AFFINE8 keys with REC_AFFINE4 values (bf16
+// scales and biases), or REC_AFFINE8_F16 with REC_AFFINE4_F16 (fp16).
 int resolve_formats(int k_bits, int v_bits, int* kf, int* vf) {
-  const bool ka = k_bits == REC_AFFINE8 || k_bits == REC_AFFINE4, va = v_bits == REC_AFFINE8 || v_bits == REC_AFFINE4;
-  if (ka || va) {
-    if (k_bits != REC_AFFINE8 || v_bits != REC_AFFINE4)
-      return fail(REC_EUNSUPPORTED, "the affine format is REC_AFFINE8 keys with REC_AFFINE4 values (got %#x, %#x)",
+  const auto affine = [](int c) {
+    return c == REC_AFFINE8 || c == REC_AFFINE4 || c == REC_AFFINE8_F16 || c == REC_AFFINE4_F16;
+  };
+  if (affine(k_bits) || affine(v_bits)) {
+    if (k_bits == REC_AFFINE8 && v_bits == REC_AFFINE4) {
+      *kf = FMT_A8;
+      *vf = FMT_A4;
+    } else if (k_bits == REC_AFFINE8_F16 && v_bits == REC_AFFINE4_F16) {
+      *kf = FMT_A8H;
+      *vf = FMT_A4H;
+    } else {
+      return fail(REC_EUNSUPPORTED,
+                  "the affine formats are REC_AFFINE8 keys with REC_AFFINE4 values, or REC_AFFINE8_F16 with "
+                  "REC_AFFINE4_F16 (got %#x, %#x)",
                   k_bits, v_bits);
-    *kf = FMT_A8;
-    *vf = FMT_A4;
+    }
     return REC_OK;
   }
   int e;
@@ -290,7 +300,7 @@ int rec_kv_append(const void* k_new, const void* v_new, int in_dtype, int64_t k_
   a.L = L;
   a.offset = offset;
   a.cap = capacity;
-  a.v_units = v_bits == 4 || v_bits == FMT_A4 ? ((offset + L - 1) >> 1) - (offset >> 1) + 1 : L;
+  a.v_units = v_bits == 4 || is_a4(v_bits) ? ((offset + L - 1) >> 1) - (offset >> 1) + 1 : L;
   return launched(launch_append(k_bits, v_bits, a, (hipStream_t)stream), "append launch");
 }
 

@@ -37,8 +37,8 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendArgs a) {
       const int64_t pos_even = ((a.offset >> 1) + u) * 2;
       const bool has_even = pos_even >= a.offset && pos_even < a.offset + a.L;
       const bool has_odd = pos_even + 1 >= a.offset && pos_even + 1 < a.offset + a.L;
-      append_v4_pair<VB == FMT_A4>(a.v, b, h, (int)(pos_even - a.offset), has_even, has_odd, (uint8_t*)a.vq, a.vs,
-                                   a.vz, bh, a.cap, pos_even, lane);
+      append_v4_pair<is_a4(VB), meta_f16(VB)>(a.v, b, h, (int)(pos_even - a.offset), has_even, has_odd,
+                                              (uint8_t*)a.vq, a.vs, a.vz, bh, a.cap, pos_even, lane);
     }
   }
 }
@@ -79,10 +79,10 @@ __device__ __forceinline__ void dequant_pair(const void* codes, const uint16_t* 
     const float z = half_bits_to_float(zeros[s4_off(bh, cap, t, g)]);
     x0 = ((float)q0 - z) * s;
     x1 = ((float)q1 - z) * s;
-  } else {  // affine: FMT_A8 keys (uint8 in the int8 K layout), FMT_A4 values (uint4 in the int4 V layout)
+  } else {  // affine: 8-bit keys (uint8 in the int8 K layout), 4-bit values (uint4 in the int4 V layout)
     const uint8_t* c = (const uint8_t*)codes;
     int q0, q1;
-    if constexpr (BITS == FMT_A8) {
+    if constexpr (is_a8(BITS)) {
       q0 = c[k8_off(bh, cap, t, d)];
       q1 = c[k8_off(bh, cap, t, d + 1)];
     } else {
@@ -92,8 +92,8 @@ __device__ __forceinline__ void dequant_pair(const void* codes, const uint16_t* 
       q1 = (p & 1) ? b1 >> 4 : b1 & 15;
     }
     const int g = d >> 6;
-    const float s = __builtin_bit_cast(float, (uint32_t)scales[sa_off(bh, cap, t, 0, g)] << 16);
-    const float b = __builtin_bit_cast(float, (uint32_t)scales[sa_off(bh, cap, t, 1, g)] << 16);
+    const float s = meta_bits<meta_f16(BITS)>(scales[sa_off(bh, cap, t, 0, g)]);
+    const float b = meta_bits<meta_f16(BITS)>(scales[sa_off(bh, cap, t, 1, g)]);
     x0 = (float)q0 * s + b;
     x1 = (float)q1 * s + b;
   }
@@ -121,6 +121,8 @@ hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stre
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((dequant_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((dequant_kernel<4, 8>), grid, block, 0, stream, a);
   else if (kb == FMT_A8 && vb == FMT_A4) hipLaunchKernelGGL((dequant_kernel<FMT_A8, FMT_A4>), grid, block, 0, stream, a);
+  else if (kb == FMT_A8H && vb == FMT_A4H)
+    hipLaunchKernelGGL((dequant_kernel<FMT_A8H, FMT_A4H>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((dequant_kernel<4, 4>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
@@ -138,6 +140,8 @@ hipError_t launch_append(int kb, int vb, const AppendArgs& a, hipStream_t stream
   else if (kb == 8 && vb == 4) hipLaunchKernelGGL((append_kernel<8, 4>), grid, block, 0, stream, a);
   else if (kb == 4 && vb == 8) hipLaunchKernelGGL((append_kernel<4, 8>), grid, block, 0, stream, a);
   else if (kb == FMT_A8 && vb == FMT_A4) hipLaunchKernelGGL((append_kernel<FMT_A8, FMT_A4>), grid, block, 0, stream, a);
+  else if (kb == FMT_A8H && vb == FMT_A4H)
+    hipLaunchKernelGGL((append_kernel<FMT_A8H, FMT_A4H>), grid, block, 0, stream, a);
   else hipLaunchKernelGGL((append_kernel<4, 4>), grid, block, 0, stream, a);
   return hipGetLastError();
 }

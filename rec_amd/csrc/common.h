@@ -35,9 +35,16 @@ typedef short v8s __attribute__((ext_vector_type(8)));
 constexpr int HEAD_DIM = 128;
 // Cache formats (kernel template arguments): 8 = int8 symmetric, 4 = uint4
 // asymmetric group 32, FMT_A8 / FMT_A4 = MLX-style affine group 64 with bf16
-// scale and bias (8-bit keys / 4-bit values).
+// scale and bias (8-bit keys / 4-bit values), FMT_A8H / FMT_A4H the same with
+// fp16 scale and bias (the keys' dtype of an fp16 model).
 constexpr int FMT_A8 = 18;
 constexpr int FMT_A4 = 14;
+constexpr int FMT_A8H = 19;
+constexpr int FMT_A4H = 15;
+__host__ __device__ constexpr bool is_a8(int f) { return f == FMT_A8 || f == FMT_A8H; }
+__host__ __device__ constexpr bool is_a4(int f) { return f == FMT_A4 || f == FMT_A4H; }
+__host__ __device__ constexpr bool is_affine(int f) { return is_a8(f) || is_a4(f); }
+__host__ __device__ constexpr bool meta_f16(int f) { return f == FMT_A8H || f == FMT_A4H; }
 constexpr int FMT_BF = 16;  // bf16 K/V tensors (the KVStorage cache), prefill only
 constexpr int GROUP_A = 64;
 constexpr int BLOCK_T = 32;      // tokens per cache block and per wave iteration
@@ -68,6 +75,23 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
   _Float16 h = (_Float16)f;  // v_cvt_f16_f32, round-to-nearest-even
   return __builtin_bit_cast(uint16_t, h);
+}
+
+// Affine scale / bias words: two 16-bit values per dword, bf16 or (F16) fp16.
+template <bool F16>
+__device__ __forceinline__ float meta_lo(uint32_t w) {
+  if constexpr (F16) return half_bits_to_float(w & 0xffffu);
+  return __builtin_bit_cast(float, w << 16);
+}
+template <bool F16>
+__device__ __forceinline__ float meta_hi(uint32_t w) {
+  if constexpr (F16) return half_bits_to_float(w >> 16);
+  return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+template <bool F16>
+__device__ __forceinline__ float meta_bits(uint32_t bits16) {
+  if constexpr (F16) return half_bits_to_float(bits16);
+  return __builtin_bit_cast(float, bits16 << 16);
 }
 
 // Load element i of a half/bfloat16/float array as float (exact).

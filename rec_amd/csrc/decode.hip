@@ -133,7 +133,7 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
     const int lo = q16 - hi * 256;
     gsum += q16;
     const int d = d0 + i;
-    if constexpr (KB == 8 || KB == FMT_A8) {
+    if constexpr (KB == 8 || is_a8(KB)) {
       hi4 |= (uint32_t)(hi & 0xff) << (8 * i);
       lo4 |= (uint32_t)(lo & 0xff) << (8 * i);
     } else {
@@ -143,13 +143,13 @@ __device__ void prepare_query(const float x[4], char* smem, int tid) {
       qop[((pr * 2 + 1) * 64 + kg * 16 + c) * 16 + j] = (int8_t)lo;
     }
   }
-  if constexpr (KB == 8 || KB == FMT_A8) {
+  if constexpr (KB == 8 || is_a8(KB)) {
     // dims d0 .. d0+3 share operand m and lane row kg*16 + hh; bytes j .. j+3
     const int m = d0 >> 6, kg = (d0 >> 4) & 3, j = d0 & 15;
     *(uint32_t*)(qop + (m * 64 + kg * 16 + hh) * 16 + j) = hi4;
     *(uint32_t*)(qop + (m * 64 + kg * 16 + hh + 8) * 16 + j) = lo4;
   }
-  if constexpr (KB == 4 || KB == FMT_A8) {
+  if constexpr (KB == 4 || is_a8(KB)) {
     // group of 32 dims = 8 consecutive threads
     gsum = group8_sum(gsum);
     if ((tid & 7) == 0) qsum[hh * 4 + ((tid & 31) >> 3)] = gsum;
@@ -224,7 +224,7 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
   // 8kg .. 8kg+7 in the order idx = 4j + i.
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    if constexpr (KB == 8 || KB == FMT_A8) {
+    if constexpr (KB == 8 || is_a8(KB)) {
       R.k8[j][0] = ld128(rk, o.k[j], blk * 4096);
       R.k8[j][1] = ld128(rk, o.k[j] + 2048, blk * 4096);
     } else {
@@ -235,7 +235,7 @@ __device__ __forceinline__ void load_chunk(Chunk& R, const Res& S, const LaneOff
     R.m4 = __builtin_nontemporal_load((const v4i*)(mbase + (size_t)(ok ? blk : 0u) * 256));
   } else if constexpr (KB == 8) {
     R.s8[0] = ld128(rks, o.s8, blk * 64);
-  } else if constexpr (KB == FMT_A8) {
+  } else if constexpr (is_a8(KB)) {
     R.m[0] = ld32(rks, o.m4, blk * 256);  // scales and biases
   } else {
     R.m[0] = ld32(rks, o.m4, blk * 256);
@@ -262,10 +262,11 @@ struct State {
   float vb[2];    // affine V: Σ p·bias over this lane's tokens, per 64-dim group
 };
 
-// bf16 element `slot` of 8 packed in a v4i, as float
-__device__ __forceinline__ float bf16_at(const v4i& w, int slot) {
+// bf16 (F16: fp16) element `slot` of 8 packed in a v4i, as float
+template <bool F16>
+__device__ __forceinline__ float meta_at(const v4i& w, int slot) {
   const uint32_t x = (uint32_t)w[slot >> 1];
-  return __builtin_bit_cast(float, (slot & 1) ? (x & 0xffff0000u) : (x << 16));
+  return (slot & 1) ? meta_hi<F16>(x) : meta_lo<F16>(x);
 }
 
 template <int KB, int VB, bool EXACT, bool MASK>
@@ -281,7 +282,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   v4i ks, vs, ks4[2], kz4[2], vs4[4], vz4[4];
   if constexpr (KB == 8) ks = R.s8[0];
   if constexpr (VB == 8) vs = R.s8[1];
-  if constexpr (KB == 4 || VB == 4 || KB == FMT_A8 || VB == FMT_A4) {
+  if constexpr (KB == 4 || VB == 4 || is_a8(KB) || is_a4(VB)) {
     uint32_t* mw = (uint32_t*)meta;
     if constexpr (KB == 4 && VB == 4) {
       // lanes 48-63 carry the V zero-points, dword e of a run being the pair
@@ -301,23 +302,23 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       mw[lane] = R.m[0];
       mw[64 + lane] = R.m[1];
     }
-    if constexpr (KB == FMT_A8) mw[lane] = R.m[0];
+    if constexpr (is_a8(KB)) mw[lane] = R.m[0];
     if constexpr (VB == 4 && KB != 4) {
       mw[128 + lane] = R.m[2];
       // the V zero-points with the unpack's exponent offset of their step e = lane % 4
       const v2h off = (lane & 1) ? (v2h){(_Float16)64.0f, (_Float16)64.0f} : (v2h){(_Float16)1024.0f, (_Float16)1024.0f};
       mw[192 + lane] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, R.m[3]) + off);
     }
-    if constexpr (VB == FMT_A4) mw[128 + lane] = R.m[2];
+    if constexpr (is_a4(VB)) mw[128 + lane] = R.m[2];
     wave_lds_sync();
-    if constexpr (KB == FMT_A8) {
+    if constexpr (is_a8(KB)) {
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         ks4[g] = *(const v4i*)(meta + g * 64 + 16 * kg);        // scales, slots 8kg .. 8kg+7
         kz4[g] = *(const v4i*)(meta + 128 + g * 64 + 16 * kg);  // biases
       }
     }
-    if constexpr (VB == FMT_A4) {
+    if constexpr (is_a4(VB)) {
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         vs4[g] = *(const v4i*)(meta + 512 + g * 64 + 16 * kg);
@@ -359,7 +360,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         const int full = (mine << sh_mine) + (partner << (8 - sh_mine));
         s[4 * j + i] = (float)full * half_at(ks, 4 * j + i);
       }
-    } else if constexpr (KB == FMT_A8) {
+    } else if constexpr (is_a8(KB)) {
       // uint8 codes k enter as k - 128 (top bit flipped), one MFMA per 64-dim
       // group: Σ q (s k + b) = s·Σ q (k - 128) + (128 s + b)·Q over the group,
       // Q = the group's query sum (exact)
@@ -374,8 +375,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
         const int m0 = d0[i], p0 = dpp_ror8(m0), m1 = d1[i], p1 = dpp_ror8(m1);
         const float f0 = (float)((m0 << sh_mine) + (p0 << (8 - sh_mine)));
         const float f1 = (float)((m1 << sh_mine) + (p1 << (8 - sh_mine)));
-        const float s0 = bf16_at(ks4[0], sl), s1 = bf16_at(ks4[1], sl);
-        const float c0 = fmaf(128.f, s0, bf16_at(kz4[0], sl)), c1 = fmaf(128.f, s1, bf16_at(kz4[1], sl));
+        constexpr bool F16 = meta_f16(KB);
+        const float s0 = meta_at<F16>(ks4[0], sl), s1 = meta_at<F16>(ks4[1], sl);
+        const float c0 = fmaf(128.f, s0, meta_at<F16>(kz4[0], sl)), c1 = fmaf(128.f, s1, meta_at<F16>(kz4[1], sl));
         s[4 * j + i] = fmaf(s0, f0, fmaf(s1, f1, fmaf(c0, qsum_a, c1 * qsum_b)));
       }
     } else {
@@ -433,7 +435,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
   bool big;
   if constexpr (VB == 8) {
     big = ((uint32_t)(vs[0] | vs[1] | vs[2] | vs[3]) & 0x40004000u) != 0;
-  } else if constexpr (VB == FMT_A4) {
+  } else if constexpr (is_a4(VB)) {
     big = __ballot(lane < 32 && (R.m[2] & 0x40004000u) != 0) != 0;  // lanes 32-63 hold biases
   } else if constexpr (KB == 4) {
     const uint32_t w = (uint32_t)(R.m4[0] | R.m4[1] | R.m4[2] | R.m4[3]);
@@ -453,7 +455,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
     // far is -inf keeps m = -inf and zero sums)
     const float factor = MASK && st.m == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(st.m - m_new);
     st.l *= factor;
-    if constexpr (VB == FMT_A4) {
+    if constexpr (is_a4(VB)) {
       st.vb[0] *= factor;
       st.vb[1] *= factor;
     }
@@ -499,7 +501,7 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
       const v8h a0 = i8x8_to_h8((uint32_t)R.v8[n >> 1][2 * (n & 1)], (uint32_t)R.v8[n >> 1][2 * (n & 1) + 1]);
       st.acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, pb, st.acc[n], 0, 0, 0);
     }
-  } else if constexpr (VB == FMT_A4) {
+  } else if constexpr (is_a4(VB)) {
     // affine 4-bit V, v = s q + b per 64-dim group: the A operand is q, exact
     // in fp16 (nibble under the fp16 exponent of 1024 or 64, minus that
     // offset), B = P' = p·s per group (high and low parts as above), and
@@ -516,8 +518,9 @@ __device__ __forceinline__ void process_chunk(const Chunk& R, State& st, const v
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t sw = (uint32_t)vs4[g][e], bw = (uint32_t)vz4[g][e];
-        const float slo = __builtin_bit_cast(float, sw << 16), shi = __builtin_bit_cast(float, sw & 0xffff0000u);
-        const float blo = __builtin_bit_cast(float, bw << 16), bhi = __builtin_bit_cast(float, bw & 0xffff0000u);
+        constexpr bool F16 = meta_f16(VB);
+        const float slo = meta_lo<F16>(sw), shi = meta_hi<F16>(sw);
+        const float blo = meta_lo<F16>(bw), bhi = meta_hi<F16>(bw);
         if constexpr (EXACT) {
           const _Float16 h0 = (_Float16)(p_lo[e] * slo), h1 = (_Float16)(p_lo[e + 4] * shi);
           pb[2 * e] = (_Float16)__builtin_fmaf(p[e], slo, -(float)h0);
@@ -632,7 +635,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
     t_end = t_begin + a.span < a.t_split_end ? t_begin + a.span : a.t_split_end;
   }
 
-  constexpr int64_t KROW = KB == 8 || KB == FMT_A8 ? HEAD_DIM : HEAD_DIM / 2;  // code bytes per token
+  constexpr int64_t KROW = KB == 8 || is_a8(KB) ? HEAD_DIM : HEAD_DIM / 2;  // code bytes per token
   constexpr int64_t VROW = VB == 8 ? HEAD_DIM : HEAD_DIM / 2;
   constexpr int64_t KSROW = KB == 8 ? 1 : 4;                   // fp16 scales per token
   constexpr int64_t VSROW = VB == 8 ? 1 : 4;
@@ -655,7 +658,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
         append_row<8>(a.vnew, b, h, 0, 1, (void*)a.vq, (uint16_t*)a.vs, nullptr, bh, cap, pos, lane);
       } else {
         const bool odd = (pos & 1) != 0;
-        append_v4_pair<VB == FMT_A4>(a.vnew, b, h, odd ? -1 : 0, !odd, odd, (uint8_t*)a.vq, (uint16_t*)a.vs,
+        append_v4_pair<is_a4(VB), meta_f16(VB)>(a.vnew, b, h, odd ? -1 : 0, !odd, odd, (uint8_t*)a.vq, (uint16_t*)a.vs,
                                      (uint16_t*)a.vz, bh, cap, pos & ~(int64_t)1, lane);
       }
     }
@@ -718,7 +721,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
   }
   __syncthreads();
 
-  constexpr int NOP = KB == 8 || KB == FMT_A8 ? 2 : 4;
+  constexpr int NOP = KB == 8 || is_a8(KB) ? 2 : 4;
   v4i qop[NOP];
 #pragma unroll
   for (int o = 0; o < NOP; ++o) qop[o] = ((const v4i*)(smem + LDS_QOP))[o * 64 + lane];
@@ -734,7 +737,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
     const int* qsum = (const int*)(smem + LDS_QSUM);
     qsum_a = (float)qsum[(c & 7) * 4 + (c >> 3)];
     qsum_b = (float)qsum[(c & 7) * 4 + 2 + (c >> 3)];
-  } else if constexpr (KB == FMT_A8) {
+  } else if constexpr (is_a8(KB)) {
     const int* qsum = (const int*)(smem + LDS_QSUM);
     qsum_a = (float)(qsum[(c & 7) * 4] + qsum[(c & 7) * 4 + 1]);
     qsum_b = (float)(qsum[(c & 7) * 4 + 2] + qsum[(c & 7) * 4 + 3]);
@@ -779,7 +782,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_kernel(const DecodeArgs a) 
         st.acc[n][i] = x + dpp_ror8f(x);
       }
   }
-  if constexpr (VB == FMT_A4) {  // the bias terms join every dim of their group
+  if constexpr (is_a4(VB)) {  // the bias terms join every dim of their group
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       float vb = st.vb[g];
@@ -931,13 +934,15 @@ hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_
     else if (kb == 8 && vb == 4) launch_masked<8, 4>(a, stream);
     else if (kb == 4 && vb == 8) launch_masked<4, 8>(a, stream);
     else if (kb == 4 && vb == 4) launch_masked<4, 4>(a, stream);
-    else launch_masked<FMT_A8, FMT_A4>(a, stream);
+    else if (kb == FMT_A8) launch_masked<FMT_A8, FMT_A4>(a, stream);
+    else launch_masked<FMT_A8H, FMT_A4H>(a, stream);
     return hipGetLastError();
   }
   if (kb == 8 && vb == 8) launch_partial<8, 8, 4, true>(a, stream);
   else if (kb == 8 && vb == 4) launch_partial_pv<8, 4, 4>(a, stream);
   else if (kb == 4 && vb == 8) launch_partial<4, 8, 4, true>(a, stream);
   else if (kb == FMT_A8 && vb == FMT_A4) launch_partial_pv<FMT_A8, FMT_A4, 4>(a, stream);
+  else if (kb == FMT_A8H && vb == FMT_A4H) launch_partial_pv<FMT_A8H, FMT_A4H, 4>(a, stream);
   else if (a.span / CH >= UINT4_WIDE_CHUNKS) launch_partial_pv<4, 4, 8>(a, stream);
   else launch_partial_pv<4, 4, 4>(a, stream);
   return hipGetLastError();

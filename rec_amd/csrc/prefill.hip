@@ -82,14 +82,14 @@ struct PfGeom {
   // int8/uint4 pair; the affine pair with the exact P·V); the bf16 cache's
   // transposed reads measured fastest issued at the P·V
   static constexpr int vpre(bool exact) {
-    return VTR ? 0 : ((KF == 8 && VF == 4) || (KF == 4 && VF == 8) || (exact && KF == FMT_A8)) ? 4 : 8;
+    return VTR ? 0 : ((KF == 8 && VF == 4) || (KF == 4 && VF == 8) || (exact && is_a8(KF))) ? 4 : 8;
   }
   // Scale bytes per 32-token block, per staged region: [K scales][K zeros][V scales][V zeros]
   // (int8: one fp16 per token; uint4: [4 groups][32 slots] fp16 scales, zero-points alike;
   // affine: [scale, bias][2 groups][32 slots] bf16 in the scales region).
-  static constexpr int KS_B = KF == 8 ? 64 : (KF == 4 || KF == FMT_A8) ? 256 : 0;
+  static constexpr int KS_B = KF == 8 ? 64 : (KF == 4 || is_a8(KF)) ? 256 : 0;
   static constexpr int KZ_B = KF == 4 ? 256 : 0;
-  static constexpr int VS_B = VF == 8 ? 64 : (VF == 4 || VF == FMT_A4) ? 256 : 0;
+  static constexpr int VS_B = VF == 8 ? 64 : (VF == 4 || is_a4(VF)) ? 256 : 0;
   static constexpr int VZ_B = VF == 4 ? 256 : 0;
   static constexpr int OFF_KZ = 4 * KS_B, OFF_VS = OFF_KZ + 4 * KZ_B, OFF_VZ = OFF_VS + 4 * VS_B;
   static constexpr int STAGE = OFF_VZ + 4 * VZ_B;  // <= 4096
@@ -158,7 +158,7 @@ __device__ __forceinline__ void load_tile(TileRegs& R, const PrefillArgs& a, int
     }
     return;
   } else {
-    if constexpr (KF == 8 || KF == FMT_A8) {
+    if constexpr (KF == 8 || is_a8(KF)) {
       const int o = (tid & 255) * 16;
 #pragma unroll
       for (int part = 0; part < 2; ++part) {
@@ -263,7 +263,7 @@ __device__ __forceinline__ void convert_tile(const TileRegs& R, typename MT<BF16
     return;
   } else {
     if constexpr (PHASE == 0) {
-      if constexpr (KF == 8 || KF == FMT_A8) {
+      if constexpr (KF == 8 || is_a8(KF)) {
         // block run o = [half m][token r][64 bytes]: dims 64m + e0 .. +15 of token r
         const int o = (tid & 255) * 16, m = o >> 11, r = (o & 2047) >> 6, e0 = o & 63;
 #pragma unroll
@@ -284,8 +284,8 @@ __device__ __forceinline__ void convert_tile(const TileRegs& R, typename MT<BF16
           } else {  // affine 8-bit: x = q·s + b, (s, b) of group m at the token's slot
             const int slot = s4_slot(block_pos(r));
             const uint16_t* sb = (const uint16_t*)(stage + bk * 256);
-            const float sc = __builtin_bit_cast(float, (uint32_t)sb[m * 32 + slot] << 16);
-            const float bi = __builtin_bit_cast(float, (uint32_t)sb[64 + m * 32 + slot] << 16);
+            const float sc = meta_bits<meta_f16(KF)>(sb[m * 32 + slot]);
+            const float bi = meta_bits<meta_f16(KF)>(sb[64 + m * 32 + slot]);
             // (v_cvt_f32_ubyte reads each code byte directly: one conversion
             // and one fma per element; the fp16 unpack measured 3% slower here)
 #pragma unroll
@@ -374,9 +374,9 @@ __device__ __forceinline__ void convert_tile(const TileRegs& R, typename MT<BF16
                 x1 = __builtin_fmaf((float)d[1], (float)sv[1], 0.f);
               } else {  // q·s + b in one fma
                 const v2h qv = __builtin_bit_cast(v2h, t) - ((e & 1) ? k64 : k1024);
-                x0 = __builtin_fmaf((float)qv[0], __builtin_bit_cast(float, sw << 16), __builtin_bit_cast(float, zw << 16));
-                x1 = __builtin_fmaf((float)qv[1], __builtin_bit_cast(float, sw & 0xffff0000u),
-                                    __builtin_bit_cast(float, zw & 0xffff0000u));
+                constexpr bool F16 = meta_f16(VF);
+                x0 = __builtin_fmaf((float)qv[0], meta_lo<F16>(sw), meta_lo<F16>(zw));
+                x1 = __builtin_fmaf((float)qv[1], meta_hi<F16>(sw), meta_hi<F16>(zw));
               }
               out[e] = v_elem<BF16>(x0);
               out[e + 4] = v_elem<BF16>(x1);
@@ -927,7 +927,8 @@ static void launch_quantized(const PrefillArgs& a, dim3 grid, dim3 block, hipStr
   else if (kf == 8 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 8, 4, EXACT, MM>), grid, block, 0, stream, a);
   else if (kf == 4 && vf == 8) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 8, EXACT, MM>), grid, block, 0, stream, a);
   else if (kf == 4 && vf == 4) hipLaunchKernelGGL((prefill_kernel<BF16, 4, 4, EXACT, MM>), grid, block, 0, stream, a);
-  else hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8, FMT_A4, EXACT, MM>), grid, block, 0, stream, a);
+  else if (kf == FMT_A8) hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8, FMT_A4, EXACT, MM>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((prefill_kernel<BF16, FMT_A8H, FMT_A4H, EXACT, MM>), grid, block, 0, stream, a);
 }
 
 // The bf16 cache (ring windows) always takes the window at run time; the

@@ -82,9 +82,10 @@ __device__ __forceinline__ void quantize_u4_pair(float x0, float x1, int& q0, in
 // [min w, max(0, max w)], the extreme of larger magnitude (the edge) is made
 // exact by stretching the step, codes are round((w - bias) / scale) clamped to
 // [0, 2^BITS - 1] (round = half away from zero), scale and bias are stored as
-// bf16.  Float32 arithmetic with correctly rounded division, so the codes and
-// bits match the CPU restatement exactly.
-template <int BITS>
+// bf16 (F16: fp16, the keys' dtype of an fp16 model), rounded to nearest even.
+// Float32 arithmetic with correctly rounded division, so the codes and bits
+// match the CPU restatement exactly.
+template <int BITS, bool F16 = false>
 __device__ __forceinline__ void quantize_affine_pair(float x0, float x1, int& q0, int& q1, uint16_t& sbits,
                                                      uint16_t& bbits) {
   constexpr float n_bins = (float)((1 << BITS) - 1);
@@ -104,8 +105,8 @@ __device__ __forceinline__ void quantize_affine_pair(float x0, float x1, int& q0
   const float bias = at_zero ? 0.0f : edge;
   q0 = (int)fminf(fmaxf(__builtin_roundf((x0 - bias) / scale), 0.0f), n_bins);
   q1 = (int)fminf(fmaxf(__builtin_roundf((x1 - bias) / scale), 0.0f), n_bins);
-  sbits = float_to_bf16_bits(scale);
-  bbits = float_to_bf16_bits(bias);
+  sbits = F16 ? float_to_half_bits(scale) : float_to_bf16_bits(scale);
+  bbits = F16 ? float_to_half_bits(bias) : float_to_bf16_bits(bias);
 }
 
 // Cache addressing in elements (bytes for codes), see the layout table in common.h.
@@ -162,10 +163,10 @@ __device__ __forceinline__ void append_row(const RowSrc& src, int b, int h, int 
   const int64_t base = row_base(src, b, h, t_src);
   float x0, x1;
   load2_as_float(src, base + 2 * lane, x0, x1);
-  if constexpr (BITS == FMT_A8) {  // affine 8-bit keys: uint8 codes in the int8 K layout
+  if constexpr (is_a8(BITS)) {  // affine 8-bit keys: uint8 codes in the int8 K layout
     int q0, q1;
     uint16_t sb, bb;
-    quantize_affine_pair<8>(x0, x1, q0, q1, sb, bb);
+    quantize_affine_pair<8, meta_f16(BITS)>(x0, x1, q0, q1, sb, bb);
     *(uint16_t*)((uint8_t*)codes + k8_off(bh, cap, pos, 2 * lane)) = (uint16_t)(q0 | (q1 << 8));
     if ((lane & 31) == 0) {
       scales[sa_off(bh, cap, pos, 0, lane >> 5)] = sb;
@@ -199,8 +200,9 @@ __device__ __forceinline__ void append_row(const RowSrc& src, int b, int h, int 
 // uint4 V: the byte shared by tokens (2p, 2p+1) (block positions p', p'^1 with
 // the even token in the low nibble).  Rows whose flag is false keep the nibble
 // already in the cache; each byte is written once.
-// AFFINE: MLX-style affine group 64 (scale and bias in `scales`, `zeros` unused).
-template <bool AFFINE = false>
+// AFFINE: MLX-style affine group 64 (scale and bias in `scales`, `zeros`
+// unused), F16: stored as fp16 rather than bf16.
+template <bool AFFINE = false, bool F16 = false>
 __device__ __forceinline__ void append_v4_pair(const RowSrc& src, int b, int h, int t_even, bool has_even,
                                                bool has_odd, uint8_t* codes, uint16_t* scales, uint16_t* zeros,
                                                int64_t bh, int64_t cap, int64_t pos_even, int lane) {
@@ -215,7 +217,7 @@ __device__ __forceinline__ void append_v4_pair(const RowSrc& src, int b, int h, 
     int q0, q1;
     uint16_t sb, zb;
     if constexpr (AFFINE) {
-      quantize_affine_pair<4>(x0, x1, q0, q1, sb, zb);
+      quantize_affine_pair<4, F16>(x0, x1, q0, q1, sb, zb);
       if ((lane & 31) == 0) {
         scales[sa_off(bh, cap, pos_even + r, 0, lane >> 5)] = sb;
         scales[sa_off(bh, cap, pos_even + r, 1, lane >> 5)] = zb;

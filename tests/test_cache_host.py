@@ -209,6 +209,34 @@ def test_to_logical_affine_roundtrip():
     va = _alloc(1, 4, 64, 4, True, "cpu", True)
     assert ka[0].shape == (1, 4, 2, 4096) and ka[1].shape == (1, 4, 2, 2, 2, 32) and ka[2] is None
     assert va[0].shape == (1, 4, 2, 2048) and va[1].dtype == torch.bfloat16
+    # fp16 scales and biases: the fp16 affine codes of the C ABI
+    k16 = QuantizedKV(torch.from_numpy(_store_k(kq, 8)), sb.view(torch.float16), None, 8, 50, False, True)
+    v16 = QuantizedKV(torch.from_numpy(_store_v4(vq)), sb.view(torch.float16), None, 4, 50, True, True)
+    assert (k16.code, v16.code) == (0x208, 0x204)
+
+
+def test_affine_scales_take_the_keys_dtype():
+    """The reference allocates the affine scales and biases in the keys' dtype
+    (model.py:57-58): fp16 keys give fp16, bf16 keys bf16; fp32 keys bf16 (the
+    kernels read 16-bit scales).  Growth keeps the first allocation's dtype."""
+    from rec_amd import MixedQuantizedKVCache
+    from rec_amd.cache import affine_meta_dtype
+
+    assert affine_meta_dtype(torch.float16) == torch.float16
+    assert affine_meta_dtype(torch.bfloat16) == torch.bfloat16
+    assert affine_meta_dtype(torch.float32) == torch.bfloat16
+    c = MixedQuantizedKVCache()
+    c._reserve(1, 2, 10, "cpu", torch.float16)
+    assert c.keys[1].dtype == torch.float16 and c.values[1].dtype == torch.float16
+    c._reserve(1, 2, 1000, "cpu", torch.bfloat16)  # growth: the dtype stays
+    assert c.capacity == 1024 and c.keys[1].dtype == torch.float16
+    st = c.state
+    assert st[0][1].dtype == torch.float16
+    k, v = c.keys_and_values()
+    assert (k.code, v.code) == (0x208, 0x204)
+    d = QuantizedKVCache(32, 8, 8)  # int8 / uint4 scales are fp16 whatever the keys
+    d._reserve(1, 1, 10, "cpu", torch.bfloat16)
+    assert d.keys[1].dtype == torch.float16
 
 
 def test_mask_trim_state():

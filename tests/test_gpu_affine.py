@@ -4,8 +4,10 @@ the reference's MixedQuantizedKVCache format) with the CPU oracle.
 Codes, scales and biases written by the append kernel must equal the oracle's
 restatement of the affine quantizer bit for bit; attention outputs lie within
 2e-3 absolute + 1e-3 relative of the float64 oracle over the dequantized cache
-(x̂ = s·q + b with the stored bf16 scale and bias).  Byte parity with MLX
-itself is not pinned (MLX cannot run here).
+(x̂ = s·q + b with the stored scale and bias).  Scales and biases are
+stored in the keys' dtype as the reference allocates them (model.py:57-58):
+bf16, or fp16 for fp16 keys.  Byte parity with MLX itself is not pinned (MLX
+cannot run here).
 """
 
 import numpy as np
@@ -14,17 +16,17 @@ import torch
 
 import oracle as O
 from rec_amd import MixedQuantizedKVCache, attend, quantized_attention_with_sinks, synthetic, to_logical
-from tests.gpu_util import SCALE, assert_close, f32
+from tests.gpu_util import SCALE, assert_close, f32, oracle_xhat, prefill_side, q_sinks
 
 pytestmark = pytest.mark.gpu
 
 
-def bf16_bits(t):
-    return t.contiguous().view(torch.int16).cpu().numpy()
-
-
-def oracle_bits(a):
-    return np.ascontiguousarray(a, np.float32).view(np.uint32).__rshift__(16).astype(np.uint16).view(np.int16)
+def value_bits(a):
+    """float32 bit patterns of stored 16-bit values (a tensor) or of oracle
+    values held in float32 (an array): equal patterns, equal values and signs."""
+    if isinstance(a, torch.Tensor):
+        a = f32(a)
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
 def fill(cache, B, H, T, seed, dtype=torch.bfloat16, chunks=None, kind="outliers", frac=0.01):
@@ -41,12 +43,13 @@ def check_cache(cache, k, v):
     kv_k, kv_v = cache.keys_and_values()
     for kv, x, bits in ((kv_k, k, 8), (kv_v, v, 4)):
         codes, sc, bi = to_logical(kv)
-        q, s, b = O.quantize_affine(x, bits)
+        meta = {torch.float16: "float16", torch.bfloat16: "bfloat16"}[sc.dtype]
+        q, s, b = O.quantize_affine(x, bits, meta=meta)
         if bits == 4:
             q = q[..., 0::2] | (q[..., 1::2] << 4)
         np.testing.assert_array_equal(codes.cpu().numpy(), q, err_msg=f"{bits}-bit codes differ")
-        np.testing.assert_array_equal(bf16_bits(sc), oracle_bits(s), err_msg=f"{bits}-bit scales differ")
-        np.testing.assert_array_equal(bf16_bits(bi), oracle_bits(b), err_msg=f"{bits}-bit biases differ")
+        np.testing.assert_array_equal(value_bits(sc), value_bits(s), err_msg=f"{bits}-bit scales differ")
+        np.testing.assert_array_equal(value_bits(bi), value_bits(b), err_msg=f"{bits}-bit biases differ")
 
 
 def dequantized(cache):
@@ -64,6 +67,9 @@ def test_affine_append_bit_exact(gpu, dtype):
     assert cache.affine and cache.group_size == 64
     chunks = [5, 64, 1, 1, 70, 3, 200]
     k, v = fill(cache, 2, 3, sum(chunks), 41, dtype=dtype, chunks=chunks, kind="heavy", frac=0.05)
+    # the keys' dtype (model.py:57-58); fp32 keys keep bf16 (16-bit scales only)
+    want = torch.float16 if dtype == torch.float16 else torch.bfloat16
+    assert cache.state[0][1].dtype == want and cache.state[1][1].dtype == want
     check_cache(cache, k, v)
 
 
@@ -152,3 +158,69 @@ def test_affine_rejections(gpu):
     q8 = synthetic.query(1, 32, 8, 93, dtype=torch.float32)
     with pytest.raises(NotImplementedError):  # prefill queries must be a matrix-core input type
         quantized_attention_with_sinks(q8, kv_k, kv_v, SCALE, "causal", None, 64, 8, 4)
+
+
+F16_CASES = [
+    # B, Hq, Hkv, P (cached first), L (queries, appended with them), splits
+    (1, 32, 4, 3000, 1, None),
+    (2, 16, 2, 777, 1, 3),
+    (1, 32, 4, 2000, 4, None),   # a few queries: the tiled kernel (the streaming one reads bf16 scales only)
+    (1, 8, 1, 500, 64, None),
+    (2, 12, 4, 300, 100, 2),
+]
+
+
+@pytest.mark.parametrize("case", F16_CASES, ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_sp{}".format(*c))
+def test_affine_f16_scales_decode_and_prefill(gpu, case):
+    """An fp16 model: fp16 keys, queries and scales.  The append writes fp16
+    scale and bias bits equal to the oracle's; decode and prefill read them as
+    fp16 and match the oracle (the prefill side rounded to the query dtype, its
+    sinks in that dtype, model.py:194-202)."""
+    B, Hq, Hkv, P, L, splits = case
+    cache = MixedQuantizedKVCache()
+    k = synthetic.kv((B, Hkv, P + L, 128), 900 + L, kind="heavy", frac=0.05, dtype=torch.float16)
+    v = synthetic.kv((B, Hkv, P + L, 128), 901 + L, kind="heavy", frac=0.05, dtype=torch.float16)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    q = synthetic.query(B, Hq, L, 902 + L, dtype=torch.float16)
+    sinks = torch.randn(Hq, device="cuda")
+    mask = "causal" if L > 1 else None
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32, splits=splits)
+    torch.cuda.synchronize()
+    assert cache.keys[1].dtype == torch.float16 and cache.offset == P + L
+    check_cache(cache, f32(k), f32(v))
+    kq, vq = cache.keys_and_values()
+    kh, vh = oracle_xhat(kq), oracle_xhat(vq)
+    if L > 1:
+        kh, vh = prefill_side(kh, kq, q.dtype), prefill_side(vh, vq, q.dtype)
+    sk = q_sinks(sinks, q.dtype) if L > 1 else f32(sinks)
+    ref = O.attention(f32(q), kh, vh, SCALE, sk, mask)
+    assert_close(f32(out), ref, f"case {case}")
+
+
+def test_affine_f16_scales_masked_and_fused_steps(gpu):
+    """fp16 scales through the masked decode (a bool mask array) and through
+    fused decode steps (the new token quantized inside the attention launch,
+    both nibbles of a shared byte)."""
+    B, Hq, Hkv, P = 1, 16, 2, 401
+    cache = MixedQuantizedKVCache()
+    k = synthetic.kv((B, Hkv, P + 4, 128), 911, dtype=torch.float16)
+    v = synthetic.kv((B, Hkv, P + 4, 128), 912, dtype=torch.float16)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    sinks = torch.randn(Hq, device="cuda")
+    for step in range(4):
+        T = P + step + 1
+        q = synthetic.query(B, Hq, 1, 913 + step, dtype=torch.float16)
+        out = attend(q, k[:, :, T - 1 : T], v[:, :, T - 1 : T], cache, SCALE, None, sinks, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        kq, vq = cache.keys_and_values()
+        ref = O.attention(f32(q), oracle_xhat(kq), oracle_xhat(vq), SCALE, f32(sinks))
+        assert_close(f32(out), ref, f"fused step {step}")
+    check_cache(cache, f32(k), f32(v))
+    kq, vq = cache.keys_and_values()
+    T = P + 4
+    keep = np.random.default_rng(914).random((1, T)) < 0.3
+    q = synthetic.query(B, Hq, 1, 915, dtype=torch.float16)
+    out = quantized_attention_with_sinks(q, kq, vq, SCALE, torch.from_numpy(keep).cuda(), sinks, 64, 8, 4,
+                                         out_dtype=torch.float32)
+    ref = O.attention(f32(q), oracle_xhat(kq), oracle_xhat(vq), SCALE, f32(sinks), keep)
+    assert_close(f32(out), ref, "masked decode")

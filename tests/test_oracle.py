@@ -465,6 +465,35 @@ def test_affine_error_bound_and_edges(bits):
     assert np.all(np.abs(q0) <= (1 << bits) - 1)
 
 
+@pytest.mark.parametrize("bits", [8, 4])
+def test_affine_f16_metadata(bits):
+    """fp16 scales and biases (the keys' dtype of an fp16 model, model.py:57-58):
+    the codes are the bf16 variant's (the rounding comes after them), the values
+    are fp16 numbers within half an ulp of fp16 and of bf16 of one float32
+    source, and the reconstruction error has fp16's rounding slack."""
+    n = (1 << bits) - 1
+    rng = np.random.default_rng(61 + bits)
+    x = (rng.standard_normal((40, 128)) * rng.uniform(0.1, 10, (40, 1))).astype(np.float32)
+    q, s, b = O.quantize_affine(x, bits, meta="float16")
+    qb, sb, bb = O.quantize_affine(x, bits)
+    np.testing.assert_array_equal(q, qb)
+    for v in (s, b):
+        np.testing.assert_array_equal(v, v.astype(np.float16).astype(np.float32))
+    assert not np.array_equal(s, sb)  # the two roundings differ somewhere
+    assert np.all(np.abs(s - sb) <= np.abs(sb) * (2.0**-8 + 2.0**-11) * 1.0001)
+    err = np.abs(O.dequantize_affine(q, s, b) - x).reshape(40, 2, 64)
+    slack = np.abs(s) * (1.0 + n * 2.0**-11) + np.abs(b) * 2.0**-11
+    assert np.all(err <= slack[..., None] * 1.001 + 1e-6)
+    # the edge element (code 0, x̂ = bias) is the edge rounded once: to fp16
+    # here, within 2^-11 of it, which bf16 metadata would miss
+    g = x.reshape(40, 2, 64)
+    w_min, w_max = g.min(-1), np.maximum(g.max(-1), 0)
+    edge = np.where(np.abs(w_min) > np.abs(w_max), w_min, w_max)
+    np.testing.assert_array_equal(b, edge.astype(np.float16).astype(np.float32))
+    assert np.all(np.abs(b - edge) <= np.abs(edge) * 2.0**-11)
+    assert np.any(np.abs(bb - edge) > np.abs(edge) * 2.0**-11)
+
+
 def test_affine_planted_bias_sign_is_caught():
     x = (0.5 * (np.arange(64) % 16)).astype(np.float32)[None]
     q, s, b = O.quantize_affine(x, 4)
