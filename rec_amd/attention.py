@@ -611,7 +611,7 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
             vn = values if _rows_aligned(values) else values.contiguous()
             out, want = _new_out((B, Hq, D), out_dtype, queries)
             _bf16_decode_launch(queries, data[:, 0], data[:, 1], scale, sinks, splits, out, kn, vn, T=T,
-                                capacity=cache.storage.capacity, sink_dtype=qdt)
+                                capacity=st.layer_capacity(cache.index), sink_dtype=qdt)
             cache.offset = T
             out = out.view(B, Hq, 1, D)
             return _finish(out, want)

@@ -20,6 +20,7 @@ from __future__ import annotations
 import ctypes
 from typing import List, NamedTuple, Optional
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -28,6 +29,8 @@ from .cache import _DTYPES, HEAD_DIM
 BLOCK_TOKENS = 65536
 MAX_BLOCKS = 4
 MAX_TOKENS = BLOCK_TOKENS * MAX_BLOCKS
+LOCAL_TOKENS = 513  # a sliding-window layer's region in the metadata form (cache.py:60-63)
+META_LAYERS = 49    # metadata rows that describe layers (cache.py:54-58)
 
 
 def _stride3(x):
@@ -96,8 +99,37 @@ class _Region:
             _lib.load().rec_region_destroy(handle)
 
 
+def _metadata_rows(metadata):
+    """The reference's layer table (cache.py:52-66): rows of uint32 columns,
+    column 1 set for a full-attention layer; columns 61-62 receive the
+    layer's (element offset, tokens per bank) in the reference's bank layout,
+    full-attention layers first, then the 513-token sliding-window regions."""
+    rows = [[int(x) for x in row] for row in metadata]
+    if not rows or any(len(r) < 63 for r in rows[:META_LAYERS]):
+        raise ValueError("metadata rows must have at least 63 columns")
+    layers = rows[:META_LAYERS]
+    n_global = sum(bool(r[1]) for r in layers)
+    g = l = 0
+    for r in layers:
+        if r[1]:
+            r[61:63] = [g * BLOCK_TOKENS * 1024, BLOCK_TOKENS]
+            g += 1
+        else:
+            r[61:63] = [n_global * BLOCK_TOKENS * 1024 + l * LOCAL_TOKENS * 1024, LOCAL_TOKENS]
+            l += 1
+    return rows
+
+
 class KVStorage:
-    """bf16 K/V regions of ``layers`` full-attention layers.
+    """bf16 K/V regions of the attention layers of one model.
+
+    ``KVStorage(layers, capacity, n_kv_heads)``: ``layers`` full-attention
+    layers.  ``KVStorage(metadata, capacity)``: the reference's constructor
+    (cache.py:52-73) — the first 49 rows of the layer table, column 1 marking
+    full-attention layers, four KV heads; the other (sliding-window) layers
+    get fixed 513-token regions, as the reference places them beside the
+    full-attention ones in its first bank; ``rows`` and ``metadata`` hold the
+    table with the reference's columns 61-62 filled in.
 
     ``layer(i, count)`` returns the ``(B, 2, Hkv, count, 128)`` view of layer
     ``i`` (the reference's ``(2, Hkv, count, 128)`` for ``B == 1``, cache.py:86-95);
@@ -106,14 +138,25 @@ class KVStorage:
     65,536-token banks (cache.py:63-70); the capacity never shrinks.
     """
 
-    def __init__(self, layers: int, capacity: int, n_kv_heads: int = 4, *, batch: int = 1, device=None):
-        if layers < 1 or n_kv_heads < 1 or batch < 1:
+    def __init__(self, layers, capacity: int, n_kv_heads: int = 4, *, batch: int = 1, device=None):
+        self.rows = self.metadata = None
+        if isinstance(layers, int):
+            is_global = [True] * layers
+        else:  # the reference's layer table
+            self.rows = _metadata_rows(layers)
+            self.metadata = np.array(self.rows, dtype=np.uint32)
+            is_global = [bool(r[1]) for r in self.rows[:META_LAYERS]]
+        if not is_global or n_kv_heads < 1 or batch < 1:
             raise ValueError("layers, n_kv_heads and batch must be positive")
-        self.n_layers, self.n_kv_heads, self.batch = layers, n_kv_heads, batch
+        self.n_layers, self.n_kv_heads, self.batch = len(is_global), n_kv_heads, batch
+        self.is_global = is_global
         dev = torch.device(device) if device is not None else torch.device("cuda")
         self.device = torch.device(dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
-        self._banks = [_Region(self.device, batch, n_kv_heads) for _ in range(layers)]
-        self.regions: List[torch.Tensor] = []
+        self._banks = {i: _Region(self.device, batch, n_kv_heads) for i, gl in enumerate(is_global) if gl}
+        self._local = {i: torch.zeros((batch, 2, n_kv_heads, LOCAL_TOKENS, HEAD_DIM), dtype=torch.bfloat16,
+                                      device=self.device)
+                       for i, gl in enumerate(is_global) if not gl}
+        self.regions: List[torch.Tensor] = [self._local.get(i) for i in range(self.n_layers)]
         self.capacity = 0
         self.grow(capacity)
 
@@ -126,11 +169,18 @@ class KVStorage:
             raise ValueError("Decode context limit exhausted")
         if capacity <= self.capacity:
             return
-        self.regions = [r.grow(capacity) for r in self._banks]
-        self.capacity = self._banks[0].capacity
+        for i, r in self._banks.items():
+            self.regions[i] = r.grow(capacity)
+        mapped = [r.capacity for r in self._banks.values()]
+        self.capacity = mapped[0] if mapped else -(-capacity // BLOCK_TOKENS) * BLOCK_TOKENS
+
+    def layer_capacity(self, index: int) -> int:
+        """Tokens layer ``index`` holds: the storage's capacity, or 513 for a
+        sliding-window layer of the metadata form."""
+        return self.capacity if self.is_global[index] else LOCAL_TOKENS
 
     def layer(self, index: int, count: Optional[int] = None) -> torch.Tensor:
-        count = self.capacity if count is None else count
+        count = self.layer_capacity(index) if count is None else count
         return self.regions[index][:, :, :, :count]
 
     def write(self, index: int, offset: int, keys: torch.Tensor, values: torch.Tensor):
@@ -143,7 +193,8 @@ class KVStorage:
             raise NotImplementedError(f"head_dim {D} is not supported (128 only)")
         if keys.dtype not in _DTYPES or values.dtype != keys.dtype:
             raise ValueError(f"keys/values must share a float16/bfloat16/float32 dtype, got {keys.dtype}/{values.dtype}")
-        if offset < 0 or offset + L > self.capacity:
+        cap = self.layer_capacity(index)
+        if offset < 0 or offset + L > cap:
             raise ValueError("Decode context limit exhausted")
         region = self.regions[index]
         kr, vr = region[:, 0], region[:, 1]
@@ -152,7 +203,7 @@ class KVStorage:
         rc = _lib.load().rec_kv_write_bf16(
             k.data_ptr(), v.data_ptr(), _DTYPES[keys.dtype], ksb, ksh, kst, vsb, vsh, vst,
             kr.data_ptr(), kr.stride(0), kr.stride(1), vr.data_ptr(), vr.stride(0), vr.stride(1),
-            B, H, L, D, offset, self.capacity, torch.cuda.current_stream(self.device).cuda_stream,
+            B, H, L, D, offset, cap, torch.cuda.current_stream(self.device).cuda_stream,
         )
         _lib.check(rc, "rec_kv_write_bf16")
 
@@ -193,6 +244,10 @@ class FixedKVCache:
     def _reserve(self, needed: int):
         if needed > BLOCK_TOKENS * MAX_BLOCKS:
             raise ValueError("Decode context limit exhausted")
+        if not self.storage.is_global[self.index]:  # a 513-token region of the metadata form
+            if needed > LOCAL_TOKENS:
+                raise ValueError("Decode context limit exhausted")
+            return
         if needed > self.storage.capacity:
             self.storage.grow(needed)
 

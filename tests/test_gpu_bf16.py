@@ -379,3 +379,50 @@ def test_ring_join_bit_exact(gpu, dtype):
         assert torch.equal(wv.contiguous().view(torch.int16),
                            v[:, :, end - hold:end].to(torch.bfloat16).contiguous().view(torch.int16)), f"ring V at {end}"
         pos = end
+
+
+def shared_metadata():
+    """The layer table of the reference's shared-storage test (50 rows of 64
+    columns, every fourth of the first 49 layers full-attention)."""
+    rows = [[0] * 64 for _ in range(50)]
+    for i, row in enumerate(rows[:49]):
+        row[1] = int(i % 4 == 0)
+    return rows
+
+
+def test_storage_from_the_reference_metadata(gpu):
+    """KVStorage(metadata, capacity), the reference's constructor
+    (cache.py:52-73), restating its shared-storage test: a full-attention
+    layer's writes show in its views and survive a growth past one bank; a
+    sliding-window layer holds 513 tokens beside them and keeps its bytes
+    across the growth; a fused decode step on it attends over its region."""
+    from rec_amd.kvstorage import BLOCK_TOKENS
+
+    storage = KVStorage(shared_metadata(), 17)
+    assert storage.n_layers == 49 and storage.capacity == BLOCK_TOKENS and storage.metadata.shape == (50, 64)
+    cache = FixedKVCache(storage, 0)
+    keys = torch.arange(4 * 9 * 128, device="cuda").reshape(1, 4, 9, 128).to(torch.bfloat16)
+    k, v = cache.update_and_fetch(keys, -keys)
+    assert torch.equal(k, keys) and torch.equal(storage.layer(0)[:, 1, :, :9], -keys)
+    ring = torch.arange(4 * 513 * 128, device="cuda").reshape(1, 4, 513, 128).to(torch.bfloat16)
+    storage.write(1, 0, ring, -ring)
+    assert storage.layer(1).shape == (1, 2, 4, 513, 128)
+    with pytest.raises(ValueError):
+        storage.write(1, 1, ring[:, :, :1].expand(1, 4, 513, 128).contiguous(), -ring)
+    storage.grow(BLOCK_TOKENS + 65)
+    assert storage.capacity == 2 * BLOCK_TOKENS
+    assert torch.equal(storage.layer(1)[:, 0], ring) and torch.equal(storage.layer(1)[:, 1], -ring)
+    cache.offset = BLOCK_TOKENS - 2
+    k, v = cache.update_and_fetch(keys, -keys)
+    assert torch.equal(k[:, :, BLOCK_TOKENS - 2 :], keys) and torch.equal(v[:, :, BLOCK_TOKENS - 2 :], -keys)
+    assert torch.equal(k[:, :, :9], keys)  # the first bank's tokens stay in place
+    # a sliding-window layer through FixedKVCache: 512 tokens, then one fused step (513 = its region)
+    local = FixedKVCache(storage, 2)
+    kk = synthetic.kv((1, 4, 513, 128), 71, dtype=torch.bfloat16)
+    vv = synthetic.kv((1, 4, 513, 128), 72, dtype=torch.bfloat16)
+    local.update_and_fetch(kk[:, :, :512], vv[:, :, :512])
+    q = synthetic.query(1, 32, 1, 73, dtype=torch.bfloat16)
+    out = attend(q, kk[:, :, 512:], vv[:, :, 512:], local, SCALE, None, None, out_dtype=torch.float32)
+    assert_close(f32(out), O.attention(f32(q), f32(kk), f32(vv), SCALE), "sliding-window layer of the storage")
+    with pytest.raises(ValueError, match="exhausted"):
+        attend(q, kk[:, :, :1], vv[:, :, :1], local, SCALE, None, None)

@@ -175,3 +175,25 @@ def test_sink_rounding_on_the_host():
     assert torch.equal(_sinks([0.3, 7.0], 2, "cpu", torch.bfloat16), torch.tensor([0.3, 7.0]).bfloat16().float())
     with pytest.raises(ValueError, match="expected 8"):
         _sinks(torch.zeros(4), 8, "cpu", torch.bfloat16)
+
+
+def test_storage_metadata_rows_follow_the_reference():
+    """Columns 61-62 of the reference's layer table (cache.py:54-63): a
+    full-attention layer's element offset in its bank (layers in order,
+    65,536 x 1,024 elements each) and 65,536 tokens; a sliding-window layer's
+    offset past all of them (513 x 1,024 each) and 513 tokens."""
+    from rec_amd.kvstorage import _metadata_rows
+
+    rows = [[0] * 64 for _ in range(50)]
+    for i, row in enumerate(rows[:49]):
+        row[1] = int(i % 4 == 0)
+    out = _metadata_rows(rows)
+    n_global = 13
+    assert out[0][61:63] == [0, 65536] and out[4][61:63] == [65536 * 1024, 65536]
+    assert out[48][61:63] == [12 * 65536 * 1024, 65536]
+    assert out[1][61:63] == [n_global * 65536 * 1024, 513]
+    assert out[2][61:63] == [n_global * 65536 * 1024 + 513 * 1024, 513]
+    assert out[47][61:63] == [n_global * 65536 * 1024 + 35 * 513 * 1024, 513]
+    assert out[49] == rows[49] and rows[0][61] == 0  # row 50 untouched, the input not modified
+    with pytest.raises(ValueError):
+        _metadata_rows([[0] * 10])
