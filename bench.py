@@ -958,12 +958,13 @@ def main(argv=None):
     if not args.no_gemv:
         rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
 
-    rpf = rpf_short = rpf_few = rpf_few_affine = None
+    rpf = rpf_short = rpf_short_u4 = rpf_few = rpf_few_affine = None
     rpf_fmt = {}
     if not args.no_prefill:
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
         # a short chunk over a long cache (a new chat turn): the keys are split
         rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
+        rpf_short_u4 = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 56, "uint4")
         # four draft tokens over a long cache: the streaming few-query kernel
         rpf_few = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 54)
         rpf_few_affine = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 54, "affine")
@@ -1162,6 +1163,8 @@ def main(argv=None):
         result["prefill_65536_plus_2048"] = rpf
     if rpf_short is not None:
         result["prefill_32768_plus_20"] = rpf_short
+    if rpf_short_u4 is not None:
+        result["prefill_32768_plus_20_uint4"] = rpf_short_u4
     if rpf_few is not None:
         result["prefill_65536_plus_4"] = rpf_few
     if rpf_few_affine is not None:
