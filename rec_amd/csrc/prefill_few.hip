@@ -21,7 +21,7 @@
 //     P' = p·s (the token's V scale) as an fp16 high part and, when the first
 //     query sees fewer than EXACT_PV_BELOW keys, its rounding remainder in a
 //     second MFMA (as the tiled kernel does).
-// The affine pair (8-bit K, 4-bit V, group 64, bf16 scale and bias) takes the
+// The affine pair (8-bit K, 4-bit V, group 64, bf16 or fp16 scale and bias) takes the
 // same loop with the values formed in registers as the tiled kernel forms
 // them in LDS: K x̂ = q·s + b in one fp32 fma rounded to the query dtype (the
 // A operand), V x̂ likewise, and P' = p.  Under fp16 queries P·V is the fp16
@@ -136,7 +136,7 @@ __device__ __forceinline__ void few_load(FewChunk<AF>& R, __amdgpu_buffer_rsrc_t
   }
 }
 
-template <bool BF16, bool AF, int NT, bool EXACT>
+template <bool BF16, bool AF, int NT, bool EXACT, bool MH>  // MH: affine scales and biases in fp16
 __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs a) {
   typedef typename FewT<BF16>::vec V8;
   constexpr int NC = 16 * NT;  // (query, head) columns of the workgroup
@@ -215,8 +215,8 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
         if constexpr (AF) {
           const int m = ks >> 1;
           const uint32_t sw = (uint32_t)R.kx[m], bw = (uint32_t)R.kx[2 + m];
-          const float sc = __builtin_bit_cast(float, j ? sw & 0xffff0000u : sw << 16);
-          const float bi = __builtin_bit_cast(float, j ? bw & 0xffff0000u : bw << 16);
+          const float sc = j ? meta_hi<MH>(sw) : meta_lo<MH>(sw);
+          const float bi = j ? meta_hi<MH>(bw) : meta_lo<MH>(bw);
           ka[ks] = affine8<BF16>((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1], sc, bi);
         } else {
           ka[ks] = FewT<BF16>::codes((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1]);
@@ -334,10 +334,8 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
           const uint32_t t = (e & 1) ? and_or(e < 2 ? W : W8, 0x00f000f0u, 0x54005400u)
                                      : and_or(e < 2 ? W : W8, 0x000f000fu, 0x64006400u);
           const v2h qv = __builtin_bit_cast(v2h, t) - ((e & 1) ? k64 : k1024);
-          const float x0 = __builtin_fmaf((float)qv[0], __builtin_bit_cast(float, sw << 16),
-                                          __builtin_bit_cast(float, bw << 16));
-          const float x1 = __builtin_fmaf((float)qv[1], __builtin_bit_cast(float, sw & 0xffff0000u),
-                                          __builtin_bit_cast(float, bw & 0xffff0000u));
+          const float x0 = __builtin_fmaf((float)qv[0], meta_lo<MH>(sw), meta_lo<MH>(bw));
+          const float x1 = __builtin_fmaf((float)qv[1], meta_hi<MH>(sw), meta_hi<MH>(bw));
           if constexpr (BPV) {
             const v2bf xb = __builtin_convertvector((v2f){x0, x1}, v2bf);  // nearest even
             vb[2 * e] = xb[0];
@@ -429,22 +427,22 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   }
 }
 
-template <bool BF16, bool AF, bool EXACT>
+template <bool BF16, bool AF, bool EXACT, bool MH>
 static void launch_nt(const PrefillArgs& a, int nt, dim3 grid, hipStream_t stream) {
-  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 1, EXACT>), grid, dim3(64 * FW), 0, stream, a);
-  else if (nt == 2) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 2, EXACT>), grid, dim3(64 * FW), 0, stream, a);
-  else if (nt == 3) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 3, EXACT>), grid, dim3(64 * FW), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 4, EXACT>), grid, dim3(64 * FW), 0, stream, a);
+  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 1, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 2) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 2, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 3) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 3, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 4, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
 }
 
-template <bool AF>
+template <bool AF, bool MH = false>
 static void launch_af(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipStream_t stream) {
   if (a.q_dtype == DT_BF16) {
-    if (exact) launch_nt<true, AF, true>(a, nt, grid, stream);
-    else launch_nt<true, AF, false>(a, nt, grid, stream);
+    if (exact) launch_nt<true, AF, true, MH>(a, nt, grid, stream);
+    else launch_nt<true, AF, false, MH>(a, nt, grid, stream);
   } else {
-    if (exact) launch_nt<false, AF, true>(a, nt, grid, stream);
-    else launch_nt<false, AF, false>(a, nt, grid, stream);
+    if (exact) launch_nt<false, AF, true, MH>(a, nt, grid, stream);
+    else launch_nt<false, AF, false, MH>(a, nt, grid, stream);
   }
 }
 
@@ -456,7 +454,8 @@ static void launch_af(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipSt
 // over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.
 bool prefill_few_fits(const PrefillArgs& a) {
   const int rows = a.L * a.G;
-  const bool fmt = (a.k_fmt == 8 && a.v_fmt == 8) || (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4);
+  const bool fmt = (a.k_fmt == 8 && a.v_fmt == 8) || (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4) ||
+                   (a.k_fmt == FMT_A8H && a.v_fmt == FMT_A4H);
   return fmt && a.window == 0 && a.bias.p == nullptr &&
          (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384));
 }
@@ -467,6 +466,7 @@ hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
   // the first query sees the fewest keys; from EXACT_PV_BELOW on, P' in one fp16 part
   const bool exact = (a.causal ? a.T - a.L + 1 : a.T) < EXACT_PV_BELOW;
   if (a.k_fmt == FMT_A8) launch_af<true>(a, nt, exact, grid, stream);
+  else if (a.k_fmt == FMT_A8H) launch_af<true, true>(a, nt, exact, grid, stream);
   else launch_af<false>(a, nt, exact, grid, stream);
   return hipGetLastError();
 }

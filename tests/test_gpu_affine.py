@@ -164,7 +164,9 @@ F16_CASES = [
     # B, Hq, Hkv, P (cached first), L (queries, appended with them), splits
     (1, 32, 4, 3000, 1, None),
     (2, 16, 2, 777, 1, 3),
-    (1, 32, 4, 2000, 4, None),   # a few queries: the tiled kernel (the streaming one reads bf16 scales only)
+    (1, 32, 4, 2000, 4, None),   # a few queries: the streaming few-query kernel
+    (1, 32, 4, 17000, 8, None),  # 64 rows per KV head over a long cache: the streaming kernel, four column tiles
+    (1, 16, 2, 900, 3, 4),       # streaming, split
     (1, 8, 1, 500, 64, None),
     (2, 12, 4, 300, 100, 2),
 ]
