@@ -958,7 +958,7 @@ def main(argv=None):
     if not args.no_gemv:
         rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
 
-    rpf = rpf_short = rpf_short_u4 = rpf_few = rpf_few_affine = None
+    rpf = rpf_short = rpf_short_u4 = rpf_few = rpf_few_affine = rpf_few_u4 = None
     rpf_fmt = {}
     if not args.no_prefill:
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
@@ -968,6 +968,7 @@ def main(argv=None):
         # four draft tokens over a long cache: the streaming few-query kernel
         rpf_few = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 54)
         rpf_few_affine = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 54, "affine")
+        rpf_few_u4 = run_prefill(65536, 4, max(10, args.steps // 20), 2, args.seed + 57, "uint4")
         # the same long chunk over the 4-bit, affine and bf16 caches
         for i, fmt in enumerate(("uint4", "affine", "bf16")):
             rpf_fmt[fmt] = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 55 + 2 * i, fmt)
@@ -1169,6 +1170,8 @@ def main(argv=None):
         result["prefill_65536_plus_4"] = rpf_few
     if rpf_few_affine is not None:
         result["prefill_65536_plus_4_affine"] = rpf_few_affine
+    if rpf_few_u4 is not None:
+        result["prefill_65536_plus_4_uint4"] = rpf_few_u4
     for fmt, r in rpf_fmt.items():
         result[f"prefill_65536_plus_2048_{fmt}"] = r
     if sliding is not None:

@@ -1,4 +1,4 @@
-// Chunked prefill of a few queries over the int8 and affine caches: the
+// Chunked prefill of a few queries over the int8, uint4 and affine caches: the
 // decode's streaming structure with the chunk's (query, head) rows as matrix
 // columns.
 //
@@ -21,10 +21,12 @@
 //     P' = p·s (the token's V scale) as an fp16 high part and, when the first
 //     query sees fewer than EXACT_PV_BELOW keys, its rounding remainder in a
 //     second MFMA (as the tiled kernel does).
-// The affine pair (8-bit K, 4-bit V, group 64, bf16 or fp16 scale and bias) takes the
+// The uint4 pair (4-bit K and V, fp16 scale and zero-point per 32 dims) and
+// the affine pair (8-bit K, 4-bit V, group 64, bf16 or fp16 scale and bias) take the
 // same loop with the values formed in registers as the tiled kernel forms
-// them in LDS: K x̂ = q·s + b in one fp32 fma rounded to the query dtype (the
-// A operand), V x̂ likewise, and P' = p.  Under fp16 queries P·V is the fp16
+// them in LDS: K x̂ = q·s + b (affine) or (q − z)·s (uint4, q − z exact in
+// fp16) in fp32, rounded once to the query dtype (the A operand), V x̂
+// likewise, and P' = p.  Under fp16 queries P·V is the fp16
 // product as above; under bf16 queries the bf16 V value enters a bf16 MFMA
 // as it is, with P split into bf16 high and low parts.
 // Work decomposition: grid (splits, Hkv, B) with the prefill's split plan
@@ -98,46 +100,81 @@ __device__ __forceinline__ typename FewT<BF16>::vec affine8(uint32_t w0, uint32_
 //     half), whose slots s4_slot(block_pos(16j + c)) = 8(c/4) + 2(c%4) + j
 //     make dword c of the group's row; vx[2w + g] the V scales (w 0) or biases
 //     (w 1) of group g at slots 8kg .. 8kg+7 (positions (e, e+4) in dword e).
-template <bool AF>
+//   uint4: K bytes of token 16j + c, dims 64m + 16kg .. +15 for m = 0, 1 (one
+//     16-byte run of the row, dword 2m + h = dims 64m + 16kg + 8h .. +7); V as
+//     affine; kx[m] / kx[2 + m] the K scale / zero-point of group 2m + kg/2
+//     for tokens c and 16 + c (dword c of the group's row); vx[g] / vz[g] the
+//     V scales / zero-points of 32-dim group g at slots 8kg .. 8kg+7.
+constexpr int FEW_I8 = 0, FEW_AF = 1, FEW_U4 = 2;  // cache formats of the kernel
+template <int FM>
 struct FewChunk {
   v4i k[2][2];
   v4i v[4];
   v4i ks, vs;
 };
 template <>
-struct FewChunk<true> {
+struct FewChunk<FEW_AF> {
   v4i k[2][2];
   v4i v[2];
   v4i kx;
   v4i vx[4];
 };
+template <>
+struct FewChunk<FEW_U4> {
+  v4i k4[2];
+  v4i v[2];
+  v4i kx;
+  v4i vx[4], vz[4];
+};
 
-template <bool AF>
-__device__ __forceinline__ void few_load(FewChunk<AF>& R, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+template <int FM>
+__device__ __forceinline__ void few_load(FewChunk<FM>& R, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
                                          __amdgpu_buffer_rsrc_t rks, __amdgpu_buffer_rsrc_t rvs,
+                                         __amdgpu_buffer_rsrc_t rkz, __amdgpu_buffer_rsrc_t rvz,
                                          __amdgpu_buffer_rsrc_t none, bool ok, uint32_t blk, int c, int kg) {
   const __amdgpu_buffer_rsrc_t a = ok ? rk : none, b = ok ? rv : none, sa = ok ? rks : none, sb = ok ? rvs : none;
+  if constexpr (FM == FEW_U4) {
+    const __amdgpu_buffer_rsrc_t za = ok ? rkz : none, zb = ok ? rvz : none;
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int m = 0; m < 2; ++m) R.k[j][m] = ld128(a, (uint32_t)((16 * j + c) * 64 + 16 * kg + 2048 * m), blk * 4096);
-  if constexpr (AF) {
+    for (int j = 0; j < 2; ++j) R.k4[j] = ld128(a, (uint32_t)((16 * j + c) * 64 + 16 * kg), blk * 2048);
 #pragma unroll
     for (int h = 0; h < 2; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 2048);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) R.kx[w] = (int)ld32(sa, (uint32_t)(64 * w + 4 * c), blk * 256);
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t off = (uint32_t)(64 * (2 * m + (kg >> 1)) + 4 * c);
+      R.kx[m] = (int)ld32(sa, off, blk * 256);
+      R.kx[2 + m] = (int)ld32(za, off, blk * 256);
+    }
 #pragma unroll
-    for (int w = 0; w < 4; ++w) R.vx[w] = ld128(sb, (uint32_t)(64 * w + 16 * kg), blk * 256);
+    for (int g = 0; g < 4; ++g) {
+      R.vx[g] = ld128(sb, (uint32_t)(64 * g + 16 * kg), blk * 256);
+      R.vz[g] = ld128(zb, (uint32_t)(64 * g + 16 * kg), blk * 256);
+    }
   } else {
 #pragma unroll
-    for (int h = 0; h < 4; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 4096);
-    R.ks = ld128(sa, (uint32_t)(16 * kg), blk * 64);
-    R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) R.k[j][m] = ld128(a, (uint32_t)((16 * j + c) * 64 + 16 * kg + 2048 * m), blk * 4096);
+    if constexpr (FM == FEW_AF) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 2048);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) R.kx[w] = (int)ld32(sa, (uint32_t)(64 * w + 4 * c), blk * 256);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) R.vx[w] = ld128(sb, (uint32_t)(64 * w + 16 * kg), blk * 256);
+    } else {
+#pragma unroll
+      for (int h = 0; h < 4; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 4096);
+      R.ks = ld128(sa, (uint32_t)(16 * kg), blk * 64);
+      R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
+    }
   }
 }
 
-template <bool BF16, bool AF, int NT, bool EXACT, bool MH>  // MH: affine scales and biases in fp16
+template <bool BF16, int FM, int NT, bool EXACT, bool MH>  // MH: affine scales and biases in fp16
 __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs a) {
+  constexpr bool AF = FM == FEW_AF, U4 = FM == FEW_U4;
+  constexpr bool XV = AF || U4;  // values dequantized in registers (P' = p)
   typedef typename FewT<BF16>::vec V8;
   constexpr int NC = 16 * NT;  // (query, head) columns of the workgroup
   __shared__ __attribute__((aligned(16))) float part[FW][NC][FPR];
@@ -180,13 +217,16 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
 
   // ---- resources of this (b, h) slice ----
   const int64_t cap = a.cap;
-  constexpr int64_t VROW = AF ? HEAD_DIM / 2 : HEAD_DIM;  // V code bytes per token
-  constexpr int64_t SROW = AF ? 4 : 1;                    // scale entries per token
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const int8_t*)a.kq + bh * cap * HEAD_DIM, cap * HEAD_DIM);
+  constexpr int64_t KROW = U4 ? HEAD_DIM / 2 : HEAD_DIM;  // K code bytes per token
+  constexpr int64_t VROW = XV ? HEAD_DIM / 2 : HEAD_DIM;  // V code bytes per token
+  constexpr int64_t SROW = XV ? 4 : 1;                    // scale entries per token
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc((const int8_t*)a.kq + bh * cap * KROW, cap * KROW);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc((const int8_t*)a.vq + bh * cap * VROW, cap * VROW);
   const __amdgpu_buffer_rsrc_t rks = make_rsrc(a.ks + bh * cap * SROW, cap * SROW * 2);
   const __amdgpu_buffer_rsrc_t rvs = make_rsrc(a.vs + bh * cap * SROW, cap * SROW * 2);
   const __amdgpu_buffer_rsrc_t none = make_rsrc(a.ks, 0);
+  const __amdgpu_buffer_rsrc_t rkz = U4 ? make_rsrc(a.kz + bh * cap * 4, cap * 8) : none;
+  const __amdgpu_buffer_rsrc_t rvz = U4 ? make_rsrc(a.vz + bh * cap * 4, cap * 8) : none;
 
   // ---- softmax state per column (log2 domain) ----
   // The running max starts at a finite floor, not -inf: a chunk whose tokens
@@ -203,7 +243,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     for (int n = 0; n < 8; ++n) acc[t][n] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
 
-  const auto process = [&](const FewChunk<AF>& R, int t0) {
+  const auto process = [&](const FewChunk<FM>& R, int t0) {
     // Q·Kᵀ: lane (c, kg) receives the scores of column c for tokens 16j + 4kg + i
     v4f s4[NT][2];
 #pragma unroll
@@ -211,15 +251,41 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
       V8 ka[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const v4i w = R.k[j][ks >> 1];
-        if constexpr (AF) {
+        if constexpr (U4) {
+          // x̂ = (q - z)·s: the nibble unpack under the fp16 exponent of 1024
+          // (64) and the zero-point plus that offset give q - z exactly in
+          // fp16, bytes (0, 2) and (1, 3) of the dword as pairs; the product
+          // with the fp16 scale is exact in fp32, rounded once to the query
+          // dtype.  Elements in dim order: byte i holds dims 2i (low nibble), 2i+1.
           const int m = ks >> 1;
-          const uint32_t sw = (uint32_t)R.kx[m], bw = (uint32_t)R.kx[2 + m];
-          const float sc = j ? meta_hi<MH>(sw) : meta_lo<MH>(sw);
-          const float bi = j ? meta_hi<MH>(bw) : meta_lo<MH>(bw);
-          ka[ks] = affine8<BF16>((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1], sc, bi);
+          const uint32_t w = (uint32_t)R.k4[j][ks], w8 = w >> 8;
+          const uint32_t sw = (uint32_t)R.kx[m], zw = (uint32_t)R.kx[2 + m];
+          const float sc = half_bits_to_float(j ? sw >> 16 : sw & 0xffffu);
+          const _Float16 zh = __builtin_bit_cast(_Float16, (uint16_t)(j ? zw >> 16 : zw & 0xffffu));
+          const v2h z1024 = {(_Float16)(zh + (_Float16)1024.0f), (_Float16)(zh + (_Float16)1024.0f)};
+          const v2h z64 = {(_Float16)(zh + (_Float16)64.0f), (_Float16)(zh + (_Float16)64.0f)};
+          const v2h lo02 = __builtin_bit_cast(v2h, and_or(w, 0x000f000fu, 0x64006400u)) - z1024;
+          const v2h hi02 = __builtin_bit_cast(v2h, and_or(w, 0x00f000f0u, 0x54005400u)) - z64;
+          const v2h lo13 = __builtin_bit_cast(v2h, and_or(w8, 0x000f000fu, 0x64006400u)) - z1024;
+          const v2h hi13 = __builtin_bit_cast(v2h, and_or(w8, 0x00f000f0u, 0x54005400u)) - z64;
+          const v2h pairs[4] = {lo02, hi02, lo13, hi13};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const v2h pr = pairs[e & 3];
+            const _Float16 d = (e < 4) ? pr[0] : pr[1];  // bytes 0, 1 then 2, 3
+            ka[ks][e] = FewT<BF16>::from_float(__builtin_fmaf((float)d, sc, 0.f));
+          }
         } else {
-          ka[ks] = FewT<BF16>::codes((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1]);
+          const v4i w = R.k[j][ks >> 1];
+          if constexpr (AF) {
+            const int m = ks >> 1;
+            const uint32_t sw = (uint32_t)R.kx[m], bw = (uint32_t)R.kx[2 + m];
+            const float sc = j ? meta_hi<MH>(sw) : meta_lo<MH>(sw);
+            const float bi = j ? meta_hi<MH>(bw) : meta_lo<MH>(bw);
+            ka[ks] = affine8<BF16>((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1], sc, bi);
+          } else {
+            ka[ks] = FewT<BF16>::codes((uint32_t)w[2 * (ks & 1)], (uint32_t)w[2 * (ks & 1) + 1]);
+          }
         }
       }
 #pragma unroll
@@ -235,7 +301,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     float ksm[8], vsf[8];
 #pragma unroll
     for (int idx = 0; idx < 8; ++idx) {
-      if constexpr (AF) {
+      if constexpr (XV) {
         ksm[idx] = a.q_mul;
         vsf[idx] = 1.f;
       } else {
@@ -246,7 +312,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     // Range (as in the decode): a V scale of 2 or more among the lane's
     // positions makes its bound 0, so p <= 1 and P' = p·s stays finite in fp16
     bool big = false;
-    if constexpr (!AF) big = ((uint32_t)(R.vs[0] | R.vs[1] | R.vs[2] | R.vs[3]) & 0x40004000u) != 0;
+    if constexpr (!XV) big = ((uint32_t)(R.vs[0] | R.vs[1] | R.vs[2] | R.vs[3]) & 0x40004000u) != 0;
     const float gap = big ? 0.f : RESCALE_GAP;
     // tokens past the split end or past a column's causal limit: only the
     // chunks at the end of the range (uniform test)
@@ -254,7 +320,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     // affine V under bf16 queries: V x̂ enters P·V as the bf16 value itself
     // (no widening to fp16) and P as bf16 high and low parts, positions
     // (e, e+4) at operand elements (2e, 2e+1), the order of the nibble unpack
-    constexpr bool BPV = AF && BF16;
+    constexpr bool BPV = XV && BF16;
     v8h pb[NT], pl[NT];  // pl: EXACT only
     v8bf ph[NT], plo[NT];  // BPV only
 #pragma unroll
@@ -321,7 +387,31 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     for (int n = 0; n < 8; ++n) {
       v8h va;
       v8bf vb;  // BPV
-      if constexpr (AF) {
+      if constexpr (U4) {
+        // uint4 V: dims 16n + c sit in 32-dim group n / 2; (q - z)·s as in
+        // the tiled kernel, positions (e, e+4) from dword e of the slot run
+        const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
+        const int g = n >> 1;
+        const uint32_t W = (uint32_t)R.v[n >> 2][n & 3], W8 = W >> 8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t sw = (uint32_t)R.vx[g][e], zw = (uint32_t)R.vz[g][e];
+          const uint32_t t = (e & 1) ? and_or(e < 2 ? W : W8, 0x00f000f0u, 0x54005400u)
+                                     : and_or(e < 2 ? W : W8, 0x000f000fu, 0x64006400u);
+          const v2h d = __builtin_bit_cast(v2h, t) - (__builtin_bit_cast(v2h, zw) + ((e & 1) ? k64 : k1024));
+          const v2h sv = __builtin_bit_cast(v2h, sw);
+          const float x0 = __builtin_fmaf((float)d[0], (float)sv[0], 0.f);
+          const float x1 = __builtin_fmaf((float)d[1], (float)sv[1], 0.f);
+          if constexpr (BPV) {
+            const v2bf xb = __builtin_convertvector((v2f){x0, x1}, v2bf);  // nearest even
+            vb[2 * e] = xb[0];
+            vb[2 * e + 1] = xb[1];
+          } else {
+            va[e] = FewT<BF16>::v_elem(x0);
+            va[e + 4] = FewT<BF16>::v_elem(x1);
+          }
+        }
+      } else if constexpr (AF) {
         // nibble e = position 8kg + e; the fp16 unpack under the exponent of
         // 1024 (64) yields the pair (e, e+4) exactly, whose scales and biases
         // share dword e of the slot run (s4_slot)
@@ -365,14 +455,14 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   const int n_chunks = (t_end - lo + FCH - 1) / FCH;
   const int n_w = n_chunks > wave ? (n_chunks - wave + FW - 1) / FW : 0;
   const uint32_t blk0 = (uint32_t)(lo / FCH + wave);
-  FewChunk<AF> buf[2];
-  few_load(buf[0], rk, rv, rks, rvs, none, 0 < n_w, blk0, c, kg);
+  FewChunk<FM> buf[2];
+  few_load(buf[0], rk, rv, rks, rvs, rkz, rvz, none, 0 < n_w, blk0, c, kg);
   const int n_pad = (n_w + 1) / 2 * 2;
   for (int i0 = 0; i0 < n_pad; i0 += 2) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int i = i0 + j;
-      few_load(buf[(j + 1) & 1], rk, rv, rks, rvs, none, i + 1 < n_w, blk0 + FW * (i + 1), c, kg);
+      few_load(buf[(j + 1) & 1], rk, rv, rks, rvs, rkz, rvz, none, i + 1 < n_w, blk0 + FW * (i + 1), c, kg);
       if (i < n_w) process(buf[j], (int)(blk0 + FW * i) * FCH);
     }
   }
@@ -427,22 +517,22 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   }
 }
 
-template <bool BF16, bool AF, bool EXACT, bool MH>
+template <bool BF16, int FM, bool EXACT, bool MH>
 static void launch_nt(const PrefillArgs& a, int nt, dim3 grid, hipStream_t stream) {
-  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 1, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
-  else if (nt == 2) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 2, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
-  else if (nt == 3) hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 3, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
-  else hipLaunchKernelGGL((prefill_few_kernel<BF16, AF, 4, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
+  if (nt == 1) hipLaunchKernelGGL((prefill_few_kernel<BF16, FM, 1, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 2) hipLaunchKernelGGL((prefill_few_kernel<BF16, FM, 2, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
+  else if (nt == 3) hipLaunchKernelGGL((prefill_few_kernel<BF16, FM, 3, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
+  else hipLaunchKernelGGL((prefill_few_kernel<BF16, FM, 4, EXACT, MH>), grid, dim3(64 * FW), 0, stream, a);
 }
 
-template <bool AF, bool MH = false>
-static void launch_af(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipStream_t stream) {
+template <int FM, bool MH = false>
+static void launch_fm(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipStream_t stream) {
   if (a.q_dtype == DT_BF16) {
-    if (exact) launch_nt<true, AF, true, MH>(a, nt, grid, stream);
-    else launch_nt<true, AF, false, MH>(a, nt, grid, stream);
+    if (exact) launch_nt<true, FM, true, MH>(a, nt, grid, stream);
+    else launch_nt<true, FM, false, MH>(a, nt, grid, stream);
   } else {
-    if (exact) launch_nt<false, AF, true, MH>(a, nt, grid, stream);
-    else launch_nt<false, AF, false, MH>(a, nt, grid, stream);
+    if (exact) launch_nt<false, FM, true, MH>(a, nt, grid, stream);
+    else launch_nt<false, FM, false, MH>(a, nt, grid, stream);
   }
 }
 
@@ -454,8 +544,8 @@ static void launch_af(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipSt
 // over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.
 bool prefill_few_fits(const PrefillArgs& a) {
   const int rows = a.L * a.G;
-  const bool fmt = (a.k_fmt == 8 && a.v_fmt == 8) || (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4) ||
-                   (a.k_fmt == FMT_A8H && a.v_fmt == FMT_A4H);
+  const bool fmt = (a.k_fmt == 8 && a.v_fmt == 8) || (a.k_fmt == 4 && a.v_fmt == 4) ||
+                   (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4) || (a.k_fmt == FMT_A8H && a.v_fmt == FMT_A4H);
   return fmt && a.window == 0 && a.bias.p == nullptr &&
          (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384));
 }
@@ -465,9 +555,10 @@ hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
   const int nt = (a.L * a.G + 15) / 16;
   // the first query sees the fewest keys; from EXACT_PV_BELOW on, P' in one fp16 part
   const bool exact = (a.causal ? a.T - a.L + 1 : a.T) < EXACT_PV_BELOW;
-  if (a.k_fmt == FMT_A8) launch_af<true>(a, nt, exact, grid, stream);
-  else if (a.k_fmt == FMT_A8H) launch_af<true, true>(a, nt, exact, grid, stream);
-  else launch_af<false>(a, nt, exact, grid, stream);
+  if (a.k_fmt == FMT_A8) launch_fm<FEW_AF>(a, nt, exact, grid, stream);
+  else if (a.k_fmt == FMT_A8H) launch_fm<FEW_AF, true>(a, nt, exact, grid, stream);
+  else if (a.k_fmt == 4) launch_fm<FEW_U4>(a, nt, exact, grid, stream);
+  else launch_fm<FEW_I8>(a, nt, exact, grid, stream);
   return hipGetLastError();
 }
 

@@ -190,3 +190,40 @@ def test_split_prefill_bf16_window(gpu, splits, window):
     vb = v.float().cpu().numpy()
     ref = O.attention(f32(q), kb, vb, SCALE, sinks=f32(sinks), mask=mask)
     assert_close(f32(out), ref, f"splits={splits} window={window}")
+
+
+U4_FEW_CASES = [
+    # B, Hq, Hkv, P, L, causal, sinks, dtype, splits (0 = automatic)
+    (1, 32, 4, 65536, 4, True, True, torch.bfloat16, 0),   # draft tokens over a long cache: 32 rows, split
+    (1, 32, 4, 17000, 8, True, True, torch.float16, 0),    # 64 rows over >= 16,384 keys: four column tiles
+    (2, 16, 2, 500, 3, True, False, torch.bfloat16, 1),    # unsplit, 24 rows
+    (1, 4, 4, 700, 32, True, True, torch.float16, 3),      # one query head per KV head: 32 rows
+    (1, 8, 1, 9000, 2, False, True, torch.bfloat16, 0),    # full attention, past the exact-P·V length
+]
+
+
+@pytest.mark.parametrize("case", U4_FEW_CASES,
+                         ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_causal{}_s{}_{}_sp{}".format(*c[:7], str(c[7])[6:], c[8]))
+def test_uint4_few_query_prefill_matches_oracle(gpu, case):
+    """A short chunk over the uint4 cache streams through the few-query
+    kernel: K and V dequantized in registers ((q - z)·s rounded to the query
+    dtype, as the reference dequantizes its cache to it, model.py:194-195),
+    equal to the oracle over those values."""
+    from tests.gpu_util import oracle_xhat, prefill_side
+
+    B, Hq, Hkv, P, L, causal, with_sinks, dtype, splits = case
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 51 + L, kind="heavy", frac=0.05)
+    v = synthetic.kv((B, Hkv, T, 128), 52 + L, kind="heavy", frac=0.05)
+    q = synthetic.query(B, Hq, L, 53 + L, dtype=dtype)
+    sinks = torch.randn(Hq, device="cuda") if with_sinks else None
+    cache = QuantizedKVCache(32, 4, 4)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    mask = "causal" if causal else None
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32,
+                 splits=splits or None)
+    torch.cuda.synchronize()
+    kq, vq = cache.keys_and_values()
+    kh, vh = prefill_side(oracle_xhat(kq), kq, dtype), prefill_side(oracle_xhat(vq), vq, dtype)
+    ref = O.attention(f32(q), kh, vh, SCALE, q_sinks(sinks, q.dtype), mask)
+    assert_close(f32(out), ref, f"case {case}")
