@@ -96,8 +96,10 @@ class DecodeWorkload:
             T0 = T - counts[i]
             c = (rec_amd.QuantizedKVCache(64, 8, 4, max_tokens=T) if bits == AFFINE
                  else rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T))
-            k = synthetic.kv((B, HKV, T0, D), seed + 2 * i, kind=kind, frac=frac)
-            v = synthetic.kv((B, HKV, T0, D), seed + 2 * i + 1, kind=kind, frac=frac)
+            # the affine cache of a bf16 model (the reference's): scales and biases in bf16
+            kdt = torch.bfloat16 if bits == AFFINE else torch.float16
+            k = synthetic.kv((B, HKV, T0, D), seed + 2 * i, kind=kind, frac=frac, dtype=kdt)
+            v = synthetic.kv((B, HKV, T0, D), seed + 2 * i + 1, kind=kind, frac=frac, dtype=kdt)
             c.update_and_fetch(k, v)
             del k, v
             self.caches.append(c)
@@ -131,7 +133,7 @@ class DecodeWorkload:
         vc, vs, vz = c.values
         stream = self.torch.cuda.current_stream().cuda_stream
         fn = self.lib.rec_decode_partial if partial_only else self.lib.rec_decode_append_attn
-        kcode, vcode = (_lib.REC_AFFINE8, _lib.REC_AFFINE4) if self.bits == AFFINE else (self.bits, self.bits)
+        kcode, vcode = (kv.code for kv in c.keys_and_values())  # the formats the cache holds
         rc = fn(
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), vn.stride(0), vn.stride(1),
@@ -153,7 +155,7 @@ class DecodeWorkload:
         q = self.pool[s % len(self.pool)][0]
         kc, ks, kz = c.keys
         vc, vs, vz = c.values
-        kcode, vcode = (_lib.REC_AFFINE8, _lib.REC_AFFINE4) if self.bits == AFFINE else (self.bits, self.bits)
+        kcode, vcode = (kv.code for kv in c.keys_and_values())  # the formats the cache holds
         rc = self.lib.rec_decode_attn(
             q.data_ptr(), _lib.REC_F16, q.stride(0), q.stride(1),
             kcode, kc.data_ptr(), ks.data_ptr(), None if kz is None else kz.data_ptr(),
@@ -174,7 +176,7 @@ class DecodeWorkload:
         _, kn, vn = self.pool[s % len(self.pool)]
         kc, ks, kz = c.keys
         vc, vs, vz = c.values
-        kcode, vcode = (_lib.REC_AFFINE8, _lib.REC_AFFINE4) if self.bits == AFFINE else (self.bits, self.bits)
+        kcode, vcode = (kv.code for kv in c.keys_and_values())  # the formats the cache holds
         rc = self.lib.rec_kv_append(
             kn.data_ptr(), vn.data_ptr(), _lib.REC_F16, kn.stride(0), kn.stride(1), kn.stride(2),
             vn.stride(0), vn.stride(1), vn.stride(2),
@@ -499,7 +501,7 @@ def run_prefill(P, L, steps, warmup, seed, fmt="int8"):
     else:
         bits = 8 if fmt == "int8" else 4
         c = rec_amd.QuantizedKVCache(32, bits, bits, max_tokens=T)
-    kdt = torch.bfloat16 if bf else torch.float16
+    kdt = torch.bfloat16 if bf or fmt == "affine" else torch.float16  # affine: a bf16 model's cache
     k = synthetic.kv((1, HKV, P, D), seed, kind="outliers", frac=0.01, dtype=kdt)
     v = synthetic.kv((1, HKV, P, D), seed + 1, kind="outliers", frac=0.01, dtype=kdt)
     c.update_and_fetch(k, v)
