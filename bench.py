@@ -660,7 +660,7 @@ def run_sliding(steps, seed, window=513, held=4096, chunk=512):
 
 
 def run_sdpa_yardstick(P, L, steps):
-    """A library yardstick for the prefill, not this build's kernel: PyTorch's
+    """A library yardstick for the prefill, not this library's kernel: PyTorch's
     own fused attention (torch.nn.functional.scaled_dot_product_attention,
     flash backend, bf16 K/V already in HBM with the KV heads expanded to the
     query heads, causal aligned to the last query) over the same P + L keys,
