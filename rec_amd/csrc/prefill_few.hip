@@ -1,4 +1,5 @@
-// Chunked prefill of a few queries over the int8, uint4 and affine caches: the
+// Chunked prefill of a few queries over the quantized caches (int8, uint4,
+// mixed int8 / uint4 and affine): the
 // decode's streaming structure with the chunk's (query, head) rows as matrix
 // columns.
 //
@@ -105,76 +106,92 @@ __device__ __forceinline__ typename FewT<BF16>::vec affine8(uint32_t w0, uint32_
 //     affine; kx[m] / kx[2 + m] the K scale / zero-point of group 2m + kg/2
 //     for tokens c and 16 + c (dword c of the group's row); vx[g] / vz[g] the
 //     V scales / zero-points of 32-dim group g at slots 8kg .. 8kg+7.
-constexpr int FEW_I8 = 0, FEW_AF = 1, FEW_U4 = 2;  // cache formats of the kernel
-template <int FM>
-struct FewChunk {
+//   mixed pairs: the K part of one format with the V part of the other.
+// Format pair FM = 4·KX + VX: K (KX) and V (VX) each 0 int8, 1 affine, 2 uint4.
+constexpr int FX_I8 = 0, FX_AF = 1, FX_U4 = 2;
+constexpr int FEW_I8 = 0, FEW_AF = 5, FEW_U4 = 10, FEW_I8U4 = 2, FEW_U4I8 = 8;
+template <int KX>
+struct FewK {  // int8: codes and the row scales
   v4i k[2][2];
-  v4i v[4];
-  v4i ks, vs;
+  v4i ks;
 };
 template <>
-struct FewChunk<FEW_AF> {
+struct FewK<FX_AF> {
   v4i k[2][2];
-  v4i v[2];
   v4i kx;
+};
+template <>
+struct FewK<FX_U4> {
+  v4i k4[2];
+  v4i kx;
+};
+template <int VX>
+struct FewV {  // int8: codes and the row scales
+  v4i v[4];
+  v4i vs;
+};
+template <>
+struct FewV<FX_AF> {
+  v4i v[2];
   v4i vx[4];
 };
 template <>
-struct FewChunk<FEW_U4> {
-  v4i k4[2];
+struct FewV<FX_U4> {
   v4i v[2];
-  v4i kx;
   v4i vx[4], vz[4];
 };
+template <int FM>
+struct FewChunk : FewK<FM / 4>, FewV<FM % 4> {};
 
 template <int FM>
 __device__ __forceinline__ void few_load(FewChunk<FM>& R, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
                                          __amdgpu_buffer_rsrc_t rks, __amdgpu_buffer_rsrc_t rvs,
                                          __amdgpu_buffer_rsrc_t rkz, __amdgpu_buffer_rsrc_t rvz,
                                          __amdgpu_buffer_rsrc_t none, bool ok, uint32_t blk, int c, int kg) {
+  constexpr int KX = FM / 4, VX = FM % 4;
   const __amdgpu_buffer_rsrc_t a = ok ? rk : none, b = ok ? rv : none, sa = ok ? rks : none, sb = ok ? rvs : none;
-  if constexpr (FM == FEW_U4) {
-    const __amdgpu_buffer_rsrc_t za = ok ? rkz : none, zb = ok ? rvz : none;
+  if constexpr (KX == FX_U4) {
+    const __amdgpu_buffer_rsrc_t za = ok ? rkz : none;
 #pragma unroll
     for (int j = 0; j < 2; ++j) R.k4[j] = ld128(a, (uint32_t)((16 * j + c) * 64 + 16 * kg), blk * 2048);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 2048);
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const uint32_t off = (uint32_t)(64 * (2 * m + (kg >> 1)) + 4 * c);
       R.kx[m] = (int)ld32(sa, off, blk * 256);
       R.kx[2 + m] = (int)ld32(za, off, blk * 256);
     }
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      R.vx[g] = ld128(sb, (uint32_t)(64 * g + 16 * kg), blk * 256);
-      R.vz[g] = ld128(zb, (uint32_t)(64 * g + 16 * kg), blk * 256);
-    }
   } else {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int m = 0; m < 2; ++m) R.k[j][m] = ld128(a, (uint32_t)((16 * j + c) * 64 + 16 * kg + 2048 * m), blk * 4096);
-    if constexpr (FM == FEW_AF) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 2048);
+    if constexpr (KX == FX_AF) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) R.kx[w] = (int)ld32(sa, (uint32_t)(64 * w + 4 * c), blk * 256);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) R.vx[w] = ld128(sb, (uint32_t)(64 * w + 16 * kg), blk * 256);
     } else {
-#pragma unroll
-      for (int h = 0; h < 4; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 4096);
       R.ks = ld128(sa, (uint32_t)(16 * kg), blk * 64);
-      R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
+    }
+  }
+  if constexpr (VX == FX_I8) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 4096);
+    R.vs = ld128(sb, (uint32_t)(16 * kg), blk * 64);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) R.v[h] = ld128(b, (uint32_t)((c * 4 + kg) * 16 + 1024 * h), blk * 2048);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) R.vx[g] = ld128(sb, (uint32_t)(64 * g + 16 * kg), blk * 256);
+    if constexpr (VX == FX_U4) {
+      const __amdgpu_buffer_rsrc_t zb = ok ? rvz : none;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) R.vz[g] = ld128(zb, (uint32_t)(64 * g + 16 * kg), blk * 256);
     }
   }
 }
 
 template <bool BF16, int FM, int NT, bool EXACT, bool MH>  // MH: affine scales and biases in fp16
 __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs a) {
-  constexpr bool AF = FM == FEW_AF, U4 = FM == FEW_U4;
-  constexpr bool XV = AF || U4;  // values dequantized in registers (P' = p)
+  constexpr int KX = FM / 4, VX = FM % 4;  // K and V formats
   typedef typename FewT<BF16>::vec V8;
   constexpr int NC = 16 * NT;  // (query, head) columns of the workgroup
   __shared__ __attribute__((aligned(16))) float part[FW][NC][FPR];
@@ -217,16 +234,17 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
 
   // ---- resources of this (b, h) slice ----
   const int64_t cap = a.cap;
-  constexpr int64_t KROW = U4 ? HEAD_DIM / 2 : HEAD_DIM;  // K code bytes per token
-  constexpr int64_t VROW = XV ? HEAD_DIM / 2 : HEAD_DIM;  // V code bytes per token
-  constexpr int64_t SROW = XV ? 4 : 1;                    // scale entries per token
+  constexpr int64_t KROW = KX == FX_U4 ? HEAD_DIM / 2 : HEAD_DIM;  // K code bytes per token
+  constexpr int64_t VROW = VX == FX_I8 ? HEAD_DIM : HEAD_DIM / 2;  // V code bytes per token
+  constexpr int64_t KSROW = KX == FX_I8 ? 1 : 4;                   // K scale entries per token
+  constexpr int64_t VSROW = VX == FX_I8 ? 1 : 4;
   const __amdgpu_buffer_rsrc_t rk = make_rsrc((const int8_t*)a.kq + bh * cap * KROW, cap * KROW);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc((const int8_t*)a.vq + bh * cap * VROW, cap * VROW);
-  const __amdgpu_buffer_rsrc_t rks = make_rsrc(a.ks + bh * cap * SROW, cap * SROW * 2);
-  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(a.vs + bh * cap * SROW, cap * SROW * 2);
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(a.ks + bh * cap * KSROW, cap * KSROW * 2);
+  const __amdgpu_buffer_rsrc_t rvs = make_rsrc(a.vs + bh * cap * VSROW, cap * VSROW * 2);
   const __amdgpu_buffer_rsrc_t none = make_rsrc(a.ks, 0);
-  const __amdgpu_buffer_rsrc_t rkz = U4 ? make_rsrc(a.kz + bh * cap * 4, cap * 8) : none;
-  const __amdgpu_buffer_rsrc_t rvz = U4 ? make_rsrc(a.vz + bh * cap * 4, cap * 8) : none;
+  const __amdgpu_buffer_rsrc_t rkz = KX == FX_U4 ? make_rsrc(a.kz + bh * cap * 4, cap * 8) : none;
+  const __amdgpu_buffer_rsrc_t rvz = VX == FX_U4 ? make_rsrc(a.vz + bh * cap * 4, cap * 8) : none;
 
   // ---- softmax state per column (log2 domain) ----
   // The running max starts at a finite floor, not -inf: a chunk whose tokens
@@ -251,7 +269,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
       V8 ka[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        if constexpr (U4) {
+        if constexpr (KX == FX_U4) {
           // x̂ = (q - z)·s: the nibble unpack under the fp16 exponent of 1024
           // (64) and the zero-point plus that offset give q - z exactly in
           // fp16, bytes (0, 2) and (1, 3) of the dword as pairs; the product
@@ -277,7 +295,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
           }
         } else {
           const v4i w = R.k[j][ks >> 1];
-          if constexpr (AF) {
+          if constexpr (KX == FX_AF) {
             const int m = ks >> 1;
             const uint32_t sw = (uint32_t)R.kx[m], bw = (uint32_t)R.kx[2 + m];
             const float sc = j ? meta_hi<MH>(sw) : meta_lo<MH>(sw);
@@ -297,22 +315,19 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
       }
     }
     // the K row scale times the softmax scale, and the V scale, of the lane's
-    // 8 positions (affine: the softmax scale alone, and P' = p)
+    // 8 positions (values formed in registers: the softmax scale alone, and P' = p)
     float ksm[8], vsf[8];
 #pragma unroll
     for (int idx = 0; idx < 8; ++idx) {
-      if constexpr (XV) {
-        ksm[idx] = a.q_mul;
-        vsf[idx] = 1.f;
-      } else {
-        ksm[idx] = half_at(R.ks, idx) * a.q_mul;
-        vsf[idx] = half_at(R.vs, idx);
-      }
+      if constexpr (KX == FX_I8) ksm[idx] = half_at(R.ks, idx) * a.q_mul;
+      else ksm[idx] = a.q_mul;
+      if constexpr (VX == FX_I8) vsf[idx] = half_at(R.vs, idx);
+      else vsf[idx] = 1.f;
     }
     // Range (as in the decode): a V scale of 2 or more among the lane's
     // positions makes its bound 0, so p <= 1 and P' = p·s stays finite in fp16
     bool big = false;
-    if constexpr (!XV) big = ((uint32_t)(R.vs[0] | R.vs[1] | R.vs[2] | R.vs[3]) & 0x40004000u) != 0;
+    if constexpr (VX == FX_I8) big = ((uint32_t)(R.vs[0] | R.vs[1] | R.vs[2] | R.vs[3]) & 0x40004000u) != 0;
     const float gap = big ? 0.f : RESCALE_GAP;
     // tokens past the split end or past a column's causal limit: only the
     // chunks at the end of the range (uniform test)
@@ -320,7 +335,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     // affine V under bf16 queries: V x̂ enters P·V as the bf16 value itself
     // (no widening to fp16) and P as bf16 high and low parts, positions
     // (e, e+4) at operand elements (2e, 2e+1), the order of the nibble unpack
-    constexpr bool BPV = XV && BF16;
+    constexpr bool BPV = VX != FX_I8 && BF16;
     v8h pb[NT], pl[NT];  // pl: EXACT only
     v8bf ph[NT], plo[NT];  // BPV only
 #pragma unroll
@@ -387,7 +402,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
     for (int n = 0; n < 8; ++n) {
       v8h va;
       v8bf vb;  // BPV
-      if constexpr (U4) {
+      if constexpr (VX == FX_U4) {
         // uint4 V: dims 16n + c sit in 32-dim group n / 2; (q - z)·s as in
         // the tiled kernel, positions (e, e+4) from dword e of the slot run
         const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f}, k64 = {(_Float16)64.0f, (_Float16)64.0f};
@@ -411,7 +426,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
             va[e + 4] = FewT<BF16>::v_elem(x1);
           }
         }
-      } else if constexpr (AF) {
+      } else if constexpr (VX == FX_AF) {
         // nibble e = position 8kg + e; the fp16 unpack under the exponent of
         // 1024 (64) yields the pair (e, e+4) exactly, whose scales and biases
         // share dword e of the slot run (s4_slot)
@@ -544,7 +559,7 @@ static void launch_fm(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipSt
 // over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.
 bool prefill_few_fits(const PrefillArgs& a) {
   const int rows = a.L * a.G;
-  const bool fmt = (a.k_fmt == 8 && a.v_fmt == 8) || (a.k_fmt == 4 && a.v_fmt == 4) ||
+  const bool fmt = ((a.k_fmt == 8 || a.k_fmt == 4) && (a.v_fmt == 8 || a.v_fmt == 4)) ||
                    (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4) || (a.k_fmt == FMT_A8H && a.v_fmt == FMT_A4H);
   return fmt && a.window == 0 && a.bias.p == nullptr &&
          (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384));
@@ -557,7 +572,9 @@ hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
   const bool exact = (a.causal ? a.T - a.L + 1 : a.T) < EXACT_PV_BELOW;
   if (a.k_fmt == FMT_A8) launch_fm<FEW_AF>(a, nt, exact, grid, stream);
   else if (a.k_fmt == FMT_A8H) launch_fm<FEW_AF, true>(a, nt, exact, grid, stream);
-  else if (a.k_fmt == 4) launch_fm<FEW_U4>(a, nt, exact, grid, stream);
+  else if (a.k_fmt == 4 && a.v_fmt == 4) launch_fm<FEW_U4>(a, nt, exact, grid, stream);
+  else if (a.k_fmt == 8 && a.v_fmt == 4) launch_fm<FEW_I8U4>(a, nt, exact, grid, stream);
+  else if (a.k_fmt == 4 && a.v_fmt == 8) launch_fm<FEW_U4I8>(a, nt, exact, grid, stream);
   else launch_fm<FEW_I8>(a, nt, exact, grid, stream);
   return hipGetLastError();
 }

@@ -202,13 +202,15 @@ U4_FEW_CASES = [
 ]
 
 
+@pytest.mark.parametrize("bits", [(4, 4), (8, 4), (4, 8)], ids=["k4v4", "k8v4", "k4v8"])
 @pytest.mark.parametrize("case", U4_FEW_CASES,
                          ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_causal{}_s{}_{}_sp{}".format(*c[:7], str(c[7])[6:], c[8]))
-def test_uint4_few_query_prefill_matches_oracle(gpu, case):
-    """A short chunk over the uint4 cache streams through the few-query
-    kernel: K and V dequantized in registers ((q - z)·s rounded to the query
-    dtype, as the reference dequantizes its cache to it, model.py:194-195),
-    equal to the oracle over those values."""
+def test_4bit_few_query_prefill_matches_oracle(gpu, case, bits):
+    """A short chunk over the uint4 cache, or a mixed int8 / uint4 pair,
+    streams through the few-query kernel: uint4 K and V dequantized in
+    registers ((q - z)·s rounded to the query dtype, as the reference
+    dequantizes its cache to it, model.py:194-195), int8 ones as codes with
+    their row scales, equal to the oracle over those values."""
     from tests.gpu_util import oracle_xhat, prefill_side
 
     B, Hq, Hkv, P, L, causal, with_sinks, dtype, splits = case
@@ -217,7 +219,7 @@ def test_uint4_few_query_prefill_matches_oracle(gpu, case):
     v = synthetic.kv((B, Hkv, T, 128), 52 + L, kind="heavy", frac=0.05)
     q = synthetic.query(B, Hq, L, 53 + L, dtype=dtype)
     sinks = torch.randn(Hq, device="cuda") if with_sinks else None
-    cache = QuantizedKVCache(32, 4, 4)
+    cache = QuantizedKVCache(32, *bits)
     cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
     mask = "causal" if causal else None
     out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32,
