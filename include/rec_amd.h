@@ -205,13 +205,13 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
  * bias: as rec_decode_attn's, with query l of the chunk at + l*bias_sl; with a
  * bias, causal and window must be 0 (the bias carries the whole mask) and the
  * chunk takes the tiled kernel.  Any cache format of rec_decode_attn (int8 or uint4
- * in any mix, or the affine pair): K/V tiles are dequantized into on-chip
+ * in any mix, or an affine pair): K/V tiles are dequantized into on-chip
  * memory, never to HBM — int8 codes exactly with the row scales applied to
  * scores and probabilities, 4-bit and affine values as x̂ rounded to the
  * query dtype, as the reference dequantizes before its attention.  A chunk
  * of at most 32 (query, head) rows per KV head (64 over a cache of 16,384
- * tokens or more) over an int8 or affine cache (no window) streams the cache
- * through registers instead, as the decode does, with the same values;
+ * tokens or more) over any of these caches (no window, no bias) streams the
+ * cache through registers instead, as the decode does, with the same values;
  * its splits and workspace are the same.
  * splits: key splits (<= 0: automatic, 1: none, at most 64).  A short chunk
  * over a long cache (few query blocks x KV heads x batch) splits the keys so
