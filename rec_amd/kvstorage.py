@@ -18,6 +18,7 @@ the same kernel.
 from __future__ import annotations
 
 import ctypes
+import warnings
 from typing import List, NamedTuple, Optional
 
 import numpy as np
@@ -39,6 +40,21 @@ def _stride3(x):
     return x, x.stride(0), x.stride(1), x.stride(2)
 
 
+# Regions dropped while a graph capture ran: their release needs a device
+# synchronisation, which a capture forbids, so they wait here for the next
+# region created or grown outside a capture.
+_RETIRED: List[tuple] = []
+
+
+def _release_retired():
+    if not _RETIRED or torch.cuda.is_current_stream_capturing():
+        return
+    while _RETIRED:
+        handle, device = _RETIRED.pop()
+        torch.cuda.synchronize(device)
+        _lib.load().rec_region_destroy(handle)
+
+
 class _RegionMemory:
     """Exports a region's mapped range to torch; tensors made from it keep
     it, and so the region, alive."""
@@ -54,6 +70,7 @@ class _Region:
 
     def __init__(self, device: torch.device, batch: int, n_kv_heads: int):
         lib = _lib.load()
+        _release_retired()
         self.device, self.shape = device, (batch, 2, n_kv_heads)
         rows = batch * 2 * n_kv_heads
         h, base = ctypes.c_void_p(), ctypes.c_void_p()
@@ -66,6 +83,7 @@ class _Region:
     def grow(self, tokens: int) -> torch.Tensor:
         """Back the first ``tokens`` tokens of every row, zero the new banks,
         and return the ``(B, 2, Hkv, capacity, 128)`` bf16 view."""
+        _release_retired()
         cap = ctypes.c_int64()
         with torch.cuda.device(self.device):
             rc = _lib.load().rec_region_grow(self.handle, tokens, ctypes.byref(cap))
@@ -91,12 +109,20 @@ class _Region:
 
     def __del__(self):
         handle, self.handle = getattr(self, "handle", None), None
-        if handle:
-            try:
-                torch.cuda.synchronize(self.device)  # no kernel may still read or write the banks
-            except Exception:  # interpreter shutdown: the process exit releases the mappings
+        if not handle:
+            return
+        try:
+            if torch.cuda.is_current_stream_capturing():
+                _RETIRED.append((handle, self.device))  # no synchronisation inside a capture
                 return
-            _lib.load().rec_region_destroy(handle)
+            torch.cuda.synchronize(self.device)  # no kernel may still read or write the banks
+        except Exception as e:  # e.g. interpreter shutdown: the process exit releases the mappings
+            try:
+                warnings.warn(f"KV region not released ({e}); its memory stays mapped until the process exits")
+            except Exception:
+                pass
+            return
+        _lib.load().rec_region_destroy(handle)
 
 
 def _metadata_rows(metadata):

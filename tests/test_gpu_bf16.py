@@ -151,6 +151,33 @@ def test_fused_decode_in_hip_graph(gpu):
             torch.testing.assert_close(graph_out[i], eager[i], rtol=0, atol=0, msg=f"replay {rep} step {i}")
 
 
+def test_region_dropped_inside_a_capture_is_released_later(gpu):
+    """A storage dropped while a graph is being captured cannot synchronise
+    the device to release its region: the region waits and is released by
+    the next region created outside the capture; the graph replays."""
+    import gc
+
+    from rec_amd import kvstorage
+
+    kvstorage._release_retired()
+    store = KVStorage(1, 256, 2)
+    store.layer(0).fill_(1)
+    x = torch.zeros(8, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        x.add_(1)
+        del store
+        gc.collect()
+    assert len(kvstorage._RETIRED) == 1
+    other = KVStorage(1, 256, 2)  # releases the retired region first
+    assert not kvstorage._RETIRED
+    assert other.layer(0).abs().sum().item() == 0  # a fresh region reads zeros
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    assert x.tolist() == [2.0] * 8
+
+
 def test_bf16_rejects_bad_inputs(gpu):
     k = torch.zeros((1, 4, 64, 128), dtype=torch.float16, device="cuda")
     q = torch.zeros((1, 32, 1, 128), dtype=torch.bfloat16, device="cuda")
