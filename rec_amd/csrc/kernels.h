@@ -160,12 +160,15 @@ hipError_t launch_stream_read(const void* p, int64_t n16, int workgroups, uint32
 hipError_t launch_decode_partial(int kb, int vb, const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both kernels when a.S > 1
-// A few queries over the int8 or affine cache (at most this many (query, head) rows
-// per KV head, more than 32 only over long caches; no window): the streaming
-// kernel of prefill_few.hip, whose partials share the tiled kernel's
-// workspace layout and merge
+// A few queries over a quantized cache, no window and no mask array: the
+// streaming kernel of prefill_few.hip, whose partials share the tiled
+// kernel's workspace layout and merge.  Up to 32 (query, head) rows per KV
+// head over any cache, up to PREFILL_FEW_ROWS over 16,384 keys or more, and
+// up to PREFILL_BLOCK_ROWS over 16,384-131,071 keys in row groups (one
+// workgroup each; prefill_few_groups of them, 1 up to PREFILL_FEW_ROWS rows)
 constexpr int PREFILL_FEW_ROWS = 64;
 bool prefill_few_fits(const PrefillArgs& a);
+int prefill_few_groups(const PrefillArgs& a);
 hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream);
 hipError_t launch_decode_bf16(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stream);

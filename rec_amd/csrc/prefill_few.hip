@@ -10,8 +10,10 @@
 // kernel spends each 128-token tile's conversion, LDS staging and barriers on
 // 16-row tiles that are mostly empty; here, as in the decode, every wave
 // streams its 32-token chunks from HBM into registers and the tile is never
-// staged.  The L·G <= 16·NT (query, head) rows of one KV head (NT <= 4),
-// numbered query·G + head as in prefill.hip, fill NT column tiles of 16:
+// staged.  The (query, head) rows of one KV head, numbered query·G + head as
+// in prefill.hip, fill NT column tiles of 16 (NT <= 4) per workgroup; more
+// rows than one workgroup's 16·NT are split into row groups, one workgroup
+// each (below):
 //   * Q·Kᵀ on 16x16x32 bf16 (fp16 for fp16 queries) MFMAs: A = 16 tokens x 32
 //     dims of the int8 K block converted in registers (exact), B = the rows'
 //     query elements of the same dims (a lane holds dims 64m + 16kg + 8h ..
@@ -30,11 +32,16 @@
 // likewise, and P' = p.  Under fp16 queries P·V is the fp16
 // product as above; under bf16 queries the bf16 V value enters a bf16 MFMA
 // as it is, with P split into bf16 high and low parts.
-// Work decomposition: grid (splits, Hkv, B) with the prefill's split plan
-// (128-token aligned ranges), 4 waves taking 32-token chunks in turn, a
-// 2-deep ring of loads.  Each workgroup merges its waves in LDS and writes
-// the normalised output (one split) or its unnormalised partial in the
-// prefill workspace layout, which prefill_merge_kernel combines.
+// Work decomposition: one workgroup per (key split, KV head, row group) and
+// batch row, with the prefill's split plan (128-token aligned ranges); 4
+// waves take 32-token chunks in turn from a 2-deep ring of loads.  The row
+// groups of one (split, KV head) read the same K/V bytes, so their
+// workgroups are numbered 8 apart: workgroup i runs on XCD i % 8, and the
+// groups run there at about the same time, all but the first finding the
+// bytes in that XCD's L2 (20 queries x 8 heads over 32K keys, int8: 36.4 ->
+// 32.0 us against the tiled kernel).  Each workgroup merges its waves in LDS
+// and writes the normalised output (one split) or its unnormalised partial
+// in the prefill workspace layout, which prefill_merge_kernel combines.
 #include "kernels.h"
 
 namespace rec {
@@ -198,9 +205,18 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   __shared__ float pstat[FW][NC][2];
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, kg = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // workgroup 8 (n_rg u + r) + x is row group r of unit 8u + x, a unit being
+  // a (split, KV head) pair (units past the last one: idle workgroups of
+  // the grid's rounding)
+  const int n_rg = (a.L * a.G + NC - 1) / NC;
+  const int q8 = (int)blockIdx.x >> 3;
+  const int rg = __builtin_amdgcn_readfirstlane(q8 % n_rg);
+  const int unit = __builtin_amdgcn_readfirstlane(8 * (q8 / n_rg) + ((int)blockIdx.x & 7));
+  if (unit >= a.S * a.Hkv) return;
+  const int split = unit % a.S, h = unit / a.S, b = blockIdx.y;
   const int64_t bh = (int64_t)b * a.Hkv + h;
-  const int rows = a.L * a.G;  // valid columns
+  const int p_base = rg * NC;                     // the group's first row
+  const int rows = min(NC, a.L * a.G - p_base);  // and its row count (valid columns)
   const int P = (int)(a.T - a.L);
   const int64_t s_lo = a.split_lo + (int64_t)split * a.split_len;
   const int lo = __builtin_amdgcn_readfirstlane((int)s_lo);
@@ -211,8 +227,8 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
   int qpos[NT];  // last visible token of the lane's column (causal), or past every token
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int p = 16 * t + c;
-    const bool valid = p < rows;
+    const bool valid = 16 * t + c < rows;
+    const int p = p_base + 16 * t + c;
     const int qi = valid ? p / a.G : 0, hq = h * a.G + (valid ? p - qi * a.G : 0);
     qpos[t] = (valid && a.causal) ? P + qi : INT32_MAX;
     const uint16_t* row = (const uint16_t*)a.q + (int64_t)b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)qi * a.q_st;
@@ -512,7 +528,8 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
       o += f * *(const v4f*)&part[w][p][d0];
       l += f * pstat[w][p][1];
     }
-    const int qi = p / a.G, hq = h * a.G + (p - qi * a.G);
+    const int pg = p_base + p;  // the row in the KV head's numbering
+    const int qi = pg / a.G, hq = h * a.G + (pg - qi * a.G);
     if (a.S == 1) {
       if (a.sinks != nullptr) {
         const float sink = a.sinks[hq] * LOG2E;
@@ -525,7 +542,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
       store_out4(a.out, (((int64_t)b * a.Hq + hq) * a.L + qi) * HEAD_DIM + d0, r, a.out_dtype);
     } else {
       // no visible key in this split: (-inf, 0, 0), as the tiled kernel writes
-      const int64_t row = (((int64_t)bh * a.S + split) * a.nqb) * PREFILL_BLOCK_ROWS + p;
+      const int64_t row = (((int64_t)bh * a.S + split) * a.nqb) * PREFILL_BLOCK_ROWS + pg;
       *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = o;
       if (d0 == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){l > 0.f ? M : NEG_INF, l};
     }
@@ -551,23 +568,45 @@ static void launch_fm(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipSt
   }
 }
 
+// Column tiles per workgroup for `rows` (query, head) rows: all of them up to
+// PREFILL_FEW_ROWS, else row groups of three tiles, or of four from 193 rows on.
+int few_tiles(int rows) { return rows <= PREFILL_FEW_ROWS ? (rows + 15) / 16 : rows <= 192 ? 3 : 4; }
+
 }  // namespace
 
 // Up to 32 rows (two column tiles) the streaming kernel is the faster one at
 // every cache length measured; three or four tiles (one wave per SIMD, the
 // accumulators partly in AGPRs) only over long caches: 8 queries x 8 heads
-// over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.
+// over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.  Row
+// groups (more than 64 rows) from 16,384 to 131,071 keys; 32 q / 4 kv heads,
+// tiled -> row groups: int8 12 queries over 32K 28.4 -> 22.0 us, 20 over 16K
+// 26.6 -> 21.3, over 32K 36.4 -> 32.0, over 65,536 52.5 -> 49.4, 32 over 32K
+// 41.8 -> 38.6 (20 over 131,072 keys 83.7 -> 86.7, hence the bound); uint4 K
+// / int8 V 20 over 32K 36.4 -> 32.8, 12 over 65,536 43.5 -> 33.4.  A 4-bit V
+// (uint4 or affine, its values formed in registers: the instruction-bound
+// variants) gains only on small chunks and loses on larger ones (uint4 12
+// over 32K 30.2 -> 27.5, 20 over 16K 28.6 -> 26.9, but 20 over 32K 37.4 ->
+// 41.2 and over 65,536 57.3 -> 69.5; affine alike), hence its bound of
+// 100 x 32,768 (row, key) pairs per KV head.
 bool prefill_few_fits(const PrefillArgs& a) {
   const int rows = a.L * a.G;
   const bool fmt = ((a.k_fmt == 8 || a.k_fmt == 4) && (a.v_fmt == 8 || a.v_fmt == 4)) ||
                    (a.k_fmt == FMT_A8 && a.v_fmt == FMT_A4) || (a.k_fmt == FMT_A8H && a.v_fmt == FMT_A4H);
+  const bool groups = rows <= PREFILL_BLOCK_ROWS && a.T >= 16384 && a.T < 131072 &&
+                      (a.v_fmt == 8 || (int64_t)rows * a.T <= 100 * 32768);
   return fmt && a.window == 0 && a.bias.p == nullptr &&
-         (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384));
+         (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384) || groups);
+}
+
+int prefill_few_groups(const PrefillArgs& a) {
+  const int rows = a.L * a.G, nc = 16 * few_tiles(rows);
+  return (rows + nc - 1) / nc;
 }
 
 hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)a.S, a.Hkv, a.B);
-  const int nt = (a.L * a.G + 15) / 16;
+  const int nt = few_tiles(a.L * a.G);
+  const int units = a.S * a.Hkv;
+  const dim3 grid((unsigned)(8 * prefill_few_groups(a) * ((units + 7) / 8)), a.B);
   // the first query sees the fewest keys; from EXACT_PV_BELOW on, P' in one fp16 part
   const bool exact = (a.causal ? a.T - a.L + 1 : a.T) < EXACT_PV_BELOW;
   if (a.k_fmt == FMT_A8) launch_fm<FEW_AF>(a, nt, exact, grid, stream);

@@ -229,3 +229,44 @@ def test_4bit_few_query_prefill_matches_oracle(gpu, case, bits):
     kh, vh = prefill_side(oracle_xhat(kq), kq, dtype), prefill_side(oracle_xhat(vq), vq, dtype)
     ref = O.attention(f32(q), kh, vh, SCALE, q_sinks(sinks, q.dtype), mask)
     assert_close(f32(out), ref, f"case {case}")
+
+
+ROW_GROUP_CASES = [
+    # B, Hq, Hkv, P, L, causal, sinks, dtype, splits (0 = automatic)
+    (1, 32, 4, 16400, 20, True, True, torch.bfloat16, 0),   # 160 rows: four groups of three column tiles
+    (1, 32, 4, 20000, 12, True, True, torch.float16, 0),    # 96 rows: two groups
+    (1, 28, 4, 17000, 30, True, False, torch.bfloat16, 5),  # 210 rows in groups of 64: boundaries inside queries
+                                                            # (a 4-bit V takes the tiled kernel here)
+    (2, 16, 2, 16384, 10, False, True, torch.bfloat16, 1),  # unsplit, full attention: every group writes its rows
+]
+ROW_GROUP_FORMATS = {"k8v8": (8, 8), "k4v4": (4, 4), "k8v4": (8, 4), "k4v8": (4, 8), "affine": None}
+
+
+@pytest.mark.parametrize("fmt", list(ROW_GROUP_FORMATS))
+@pytest.mark.parametrize("case", ROW_GROUP_CASES,
+                         ids=lambda c: "B{}_Hq{}_Hkv{}_P{}_L{}_causal{}_s{}_{}_sp{}".format(*c[:7], str(c[7])[6:], c[8]))
+def test_row_group_prefill_matches_oracle(gpu, case, fmt):
+    """A chunk of 65-256 (query, head) rows per KV head over 16K-128K keys
+    streams through the few-query kernel in row groups, one workgroup each
+    (the groups of one split and KV head placed on one XCD); every format's
+    output equals the oracle over the cache's stored values."""
+    from rec_amd import MixedQuantizedKVCache
+    from tests.gpu_util import oracle_xhat, prefill_side
+
+    B, Hq, Hkv, P, L, causal, with_sinks, dtype, splits = case
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 61 + L, kind="outliers", frac=0.01)
+    v = synthetic.kv((B, Hkv, T, 128), 62 + L, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, L, 63 + L, dtype=dtype)
+    sinks = torch.randn(Hq, device="cuda") if with_sinks else None
+    bits = ROW_GROUP_FORMATS[fmt]
+    cache = MixedQuantizedKVCache(max_tokens=T) if bits is None else QuantizedKVCache(32, *bits, max_tokens=T)
+    cache.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    mask = "causal" if causal else None
+    out = attend(q, k[:, :, P:], v[:, :, P:], cache, SCALE, mask, sinks, out_dtype=torch.float32,
+                 splits=splits or None)
+    torch.cuda.synchronize()
+    kq, vq = cache.keys_and_values()
+    kh, vh = prefill_side(oracle_xhat(kq), kq, dtype), prefill_side(oracle_xhat(vq), vq, dtype)
+    ref = O.attention(f32(q), kh, vh, SCALE, q_sinks(sinks, q.dtype), mask)
+    assert_close(f32(out), ref, f"case {case} {fmt}")
