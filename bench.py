@@ -964,7 +964,9 @@ def main(argv=None):
     rpf_fmt = {}
     if not args.no_prefill:
         rpf = run_prefill(65536, 2048, args.prefill_steps, 2, args.seed + 51)
-        # a short chunk over a long cache (a new chat turn): the keys are split
+        # a short chunk over a long cache (a new chat turn), the keys split: 160
+        # (query, head) rows per KV head stream in row groups over the int8
+        # cache; the uint4 one keeps the tiled kernel
         rpf_short = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 53)
         rpf_short_u4 = run_prefill(32768, 20, max(10, args.steps // 20), 2, args.seed + 56, "uint4")
         # four draft tokens over a long cache: the streaming few-query kernel
