@@ -25,7 +25,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .cache import _DTYPES, HEAD_DIM
+from .cache import _DTYPES, HEAD_DIM, MixedQuantizedKVCache
 
 BLOCK_TOKENS = 65536
 MAX_BLOCKS = 4
@@ -468,3 +468,26 @@ class FixedSlidingKVCache:
             self.window_size, self.device, self.offset, self.capacity)
         other.keys, other.values = self.keys.clone(), self.values.clone()
         return other
+
+
+def make_cache(layer_types, *, kv_group_size: int = 64, kv_key_bits: int = 8, kv_value_bits: int = 4,
+               sliding_window: int = LOCAL_TOKENS, num_kv_heads: int = 4, max_tokens: Optional[int] = None,
+               batch: int = 1, device=None) -> list:
+    """One cache per layer, as ``Model.make_cache`` builds them
+    (engine/src/rec_mlx/model.py:347-360, defaults from its ModelArgs,
+    model.py:30-37): a ``MixedQuantizedKVCache(kv_group_size, kv_key_bits,
+    kv_value_bits)`` per ``"full_attention"`` layer (``max_tokens`` allocates
+    its whole context at the first append), and per other layer a sliding
+    window of ``sliding_window`` tokens -- the bf16 ring
+    ``FixedSlidingKVCache`` (the engine's sliding cache, cache.py:153-258)
+    where the reference's model takes mlx-lm's ``RotatingKVCache(max_size=
+    sliding_window, keep=0)``; its ring is allocated here, on ``device``."""
+    caches = []
+    for kind in layer_types:
+        if kind == "full_attention":
+            caches.append(MixedQuantizedKVCache(kv_group_size, kv_key_bits, kv_value_bits, max_tokens=max_tokens))
+        else:
+            caches.append(FixedSlidingKVCache(max_sequence_tokens=max_tokens or sliding_window,
+                                              num_kv_heads=num_kv_heads, head_dim=HEAD_DIM,
+                                              window_size=sliding_window, batch=batch, device=device))
+    return caches

@@ -255,3 +255,22 @@ def test_mask_trim_state():
     assert d.keys[0] is c.keys[0]
     assert d.meta_state == ("256", "6", "32", "8", "8")
     assert c.nbytes == 256 * 128 * 2 + 256 * 2 * 2
+
+
+def test_make_cache_full_attention_layers():
+    """make_cache builds what Model.make_cache does for full-attention layers
+    (model.py:347-360): MixedQuantizedKVCache(kv_group_size, kv_key_bits,
+    kv_value_bits), the reference's defaults 64 / 8 / 4 (model.py:35-37)."""
+    from rec_amd import make_cache
+
+    caches = make_cache(["full_attention"] * 3, max_tokens=4096)
+    assert len(caches) == 3 and len({id(c) for c in caches}) == 3
+    for c in caches:
+        assert type(c) is MixedQuantizedKVCache
+        assert (c.group_size, c.key_bits, c.value_bits) == (64, 8, 4)
+        assert c.offset == 0
+    c = make_cache(["full_attention"], kv_group_size=32, kv_key_bits=8, kv_value_bits=4)[0]
+    assert (c.group_size, c.key_bits, c.value_bits) == (32, 8, 4)
+    with pytest.raises(NotImplementedError):  # the affine format is 8-bit keys with 4-bit values
+        make_cache(["full_attention"], kv_key_bits=4)
+    assert make_cache([]) == []

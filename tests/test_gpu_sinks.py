@@ -181,3 +181,35 @@ def test_ring_decode_refuses_a_window_mask(gpu):
     assert cache.offset == 19
     out = attend(q, k[:, :, 19:], k[:, :, 19:], cache, SCALE, "causal", out_dtype=torch.float32)
     assert cache.offset == 20 and torch.isfinite(out).all()
+
+
+def test_make_cache_mixed_layers(gpu):
+    """make_cache over a mixed layer list (model.py:347-360): a 513-token bf16
+    ring per sliding layer and the affine quantized cache per full-attention
+    layer; a 600-token chunk and a decode step through attend() on each, the
+    sliding layer's step equal to the oracle over the last 513 tokens and the
+    full layer's to a cache built by hand."""
+    from rec_amd import MixedQuantizedKVCache, make_cache
+
+    kinds = ["sliding_attention", "full_attention", "sliding_attention"]
+    caches = make_cache(kinds, max_tokens=2048)
+    assert [type(c) for c in caches] == [FixedSlidingKVCache, MixedQuantizedKVCache, FixedSlidingKVCache]
+    assert caches[0].window_size == 513 and caches[0].capacity == 513 and caches[0] is not caches[2]
+    B, Hq, Hkv, P = 1, 32, 4, 600
+    k = synthetic.kv((B, Hkv, P + 1, 128), 581, kind="outliers", frac=0.02, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, P + 1, 128), 582, kind="outliers", frac=0.02, dtype=torch.bfloat16)
+    qc = synthetic.query(B, Hq, P, 583, dtype=torch.bfloat16)
+    qd = synthetic.query(B, Hq, 1, 584, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    by_hand = MixedQuantizedKVCache(max_tokens=2048)
+    outs = []
+    for c in caches + [by_hand]:
+        attend(qc, k[:, :, :P], v[:, :, :P], c, SCALE, "causal", sinks)
+        outs.append(attend(qd, k[:, :, P:], v[:, :, P:], c, SCALE, None, sinks, out_dtype=torch.float32))
+        assert c.offset == P + 1
+    torch.cuda.synchronize()
+    lo = P + 1 - 513
+    ref = O.attention(f32(qd), bf16_np(k[:, :, lo:]), bf16_np(v[:, :, lo:]), SCALE, q_sinks(sinks, qd.dtype))
+    assert_close(f32(outs[0]), ref, "sliding layer")
+    assert torch.equal(outs[0], outs[2])
+    assert torch.equal(outs[1], outs[3])
