@@ -449,7 +449,7 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
 static int plan_prefill_splits(PrefillArgs& a, int splits, void* workspace, size_t workspace_bytes) {
   if (splits > PREFILL_MAX_SPLITS) return fail(REC_EINVAL, "splits %d exceeds %d", splits, PREFILL_MAX_SPLITS);
   PrefillPlan p = prefill_plan(a, splits);
-  size_t need = prefill_ws_bytes(a.B, a.Hkv, p.nqb, p.S);
+  size_t need = prefill_ws_bytes(a.B, a.Hkv, (int64_t)p.nqb * p.block_rows, p.S);
   if (need > 0 && (!workspace || workspace_bytes < need)) {
     if (splits > 1)
       return fail(REC_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu that %d splits need",
@@ -460,10 +460,11 @@ static int plan_prefill_splits(PrefillArgs& a, int splits, void* workspace, size
   if (need > 0 && !aligned16(workspace)) return fail(REC_EALIGN, "workspace must be 16-byte aligned");
   a.S = p.S;
   a.nqb = p.nqb;
+  a.block_rows = p.block_rows;
   a.split_lo = p.split_lo;
   a.split_len = p.split_len;
   if (p.S > 1) {
-    const size_t rows = (size_t)a.B * a.Hkv * p.S * p.nqb * PREFILL_BLOCK_ROWS;
+    const size_t rows = (size_t)a.B * a.Hkv * p.S * p.nqb * p.block_rows;
     a.ws_acc = (float*)workspace;
     a.ws_stat = (float*)((char*)workspace + rows * HEAD_DIM * 4);
   }
@@ -478,7 +479,8 @@ size_t rec_prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int splits) {
     const int64_t nwg = (int64_t)nqb * Hkv * B;
     S = nwg >= 128 ? 1 : (int)std::min<int64_t>(PREFILL_MAX_SPLITS, (256 + nwg - 1) / nwg);
   }
-  return prefill_ws_bytes(B, Hkv, nqb, std::min(S, PREFILL_MAX_SPLITS));
+  // (blocks of 256 rows: the most any plan needs; smaller blocks take fewer splits)
+  return prefill_ws_bytes(B, Hkv, (int64_t)nqb * PREFILL_BLOCK_ROWS, std::min(S, PREFILL_MAX_SPLITS));
 }
 
 int rec_prefill_attn(const void* q, int q_dtype, int64_t q_sb, int64_t q_sh, int64_t q_st, int k_bits,

@@ -95,27 +95,30 @@ struct PrefillArgs {
   // split-K over the keys (S > 1): workgroup (qb, s) scans keys
   // [split_lo + s * split_len, + split_len) of its query block's range and
   // writes an unnormalised partial; prefill_merge_kernel combines them
-  int S, nqb;                  // splits, row blocks (PREFILL_BLOCK_ROWS (query, head) rows each)
+  int S, nqb, block_rows;      // splits, query blocks of block_rows (query, head) rows
   int64_t split_lo, split_len;
   BiasArgs bias;               // additive score bias (a mask array), or none
-  float* ws_acc;               // [B*Hkv][S][nqb][256][128]
-  float* ws_stat;              // [B*Hkv][S][nqb][256] x (max, sum)
+  float* ws_acc;               // [B*Hkv][S][nqb][block_rows][128]
+  float* ws_stat;              // [B*Hkv][S][nqb][block_rows] x (max, sum)
 };
 
 // Prefill split plan: how many key splits a launch uses and where they lie.
 constexpr int PREFILL_MAX_SPLITS = 64;
 // (query, head) rows per prefill workgroup: a KV head's rows are numbered
-// query * G + head, and workgroup qb takes rows [256 qb, 256 qb + 256)
+// query * G + head, and workgroup qb takes rows [R qb, R qb + R), R =
+// PREFILL_BLOCK_ROWS (an automatic plan for a windowed launch may take 128
+// or 64)
 constexpr int PREFILL_BLOCK_ROWS = 256;
 struct PrefillPlan {
-  int S, nqb;
+  int S, nqb, block_rows;
   int64_t split_lo, split_len;
 };
 // requested <= 0: automatic (splits only when the query blocks x KV heads x
 // batch grid is too small to fill the chip); else at most `requested`
 PrefillPlan prefill_plan(const PrefillArgs& a, int requested);
-// workspace bytes for S splits (0 when S == 1); accumulators then statistics
-size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S);
+// workspace bytes for S splits of head_rows (= nqb x block_rows) rows per KV
+// head (0 when S == 1); accumulators then statistics
+size_t prefill_ws_bytes(int B, int Hkv, int64_t head_rows, int S);
 
 // Cache rows [0, T) dequantized to bf16 (B, Hkv, T, 128) tensors.
 struct DequantArgs {

@@ -631,8 +631,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   const int qb = __builtin_amdgcn_readfirstlane((int)blockIdx.x - split * a.nqb);
   const int h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * a.Hkv + h;
-  const int p0 = qb * PF_ROWS;                       // the block's first row
-  const int n_p = min(PF_ROWS, a.L * a.G - p0);      // and its row count
+  const int p0 = qb * a.block_rows;                     // the block's first row
+  const int n_p = min(a.block_rows, a.L * a.G - p0);    // and its row count
   const int q_lo = __builtin_amdgcn_readfirstlane(p0 / a.G);  // its first and last query
   const int q_hi = __builtin_amdgcn_readfirstlane((p0 + n_p - 1) / a.G);
   const int P = (int)(a.T - a.L);  // cached tokens before the new ones
@@ -799,7 +799,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
           const float l = sum_xor32(sum_xor16(l_run[rt]));
           const float M = thr[rt] == NEG_INF ? NEG_INF : m_use[rt];  // -inf: no visible key in this split
           if (prow[rt] < n_p) {
-            const int64_t row = (((int64_t)bh * a.S + split) * a.nqb + qb) * PF_ROWS + prow[rt];
+            const int64_t row = (((int64_t)bh * a.S + split) * a.nqb + qb) * a.block_rows + prow[rt];
             float* o = a.ws_acc + row * HEAD_DIM + 4 * g;
 #pragma unroll
             for (int n = 0; n < 8; ++n) *(v4f*)(o + 16 * n) = acc[n][rt];
@@ -846,15 +846,15 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
   static_assert(16 * NR <= PREFILL_MAX_SPLITS && PREFILL_MAX_SPLITS <= 64, "one split per lane");
   const int i = blockIdx.x, hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
   const int h = hq / a.G, p = i * a.G + (hq - h * a.G);  // the (query, head) row
-  const int qb = p / PF_ROWS, r = p - qb * PF_ROWS;
+  const int qb = p / a.block_rows, r = p - qb * a.block_rows;
   const int64_t bh = (int64_t)b * a.Hkv + h;
-  const auto row = [&](int sp) { return ((bh * a.S + sp) * a.nqb + qb) * PF_ROWS + r; };
+  const auto row = [&](int sp) { return ((bh * a.S + sp) * a.nqb + qb) * a.block_rows + r; };
   // every load first -- the splits' partial rows and their statistics -- so
   // that the merge waits for memory once (slots past the last split read its
   // row again and weigh it 0).  The rows of one (query, head) are a fixed
   // stride apart: each load takes its split's offset as a scalar, so the 64
   // addresses cost no vector instructions.
-  const uint32_t step_b = (uint32_t)a.nqb * PF_ROWS * HEAD_DIM * 4;  // bytes between consecutive splits' rows
+  const uint32_t step_b = (uint32_t)a.nqb * a.block_rows * HEAD_DIM * 4;  // bytes between consecutive splits' rows
   const uint32_t last_b = (uint32_t)(a.S - 1) * step_b;              // below 2^31 (prefill_plan)
   const __amdgpu_buffer_rsrc_t racc = make_rsrc(a.ws_acc + row(0) * HEAD_DIM, (int64_t)last_b + HEAD_DIM * 4);
   v2f x[16 * NR];
@@ -883,7 +883,19 @@ __global__ __launch_bounds__(64) void prefill_merge_kernel(const PrefillArgs a) 
 
 PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
   PrefillPlan p{};
-  p.nqb = (a.L * a.G + PF_ROWS - 1) / PF_ROWS;
+  const int rows = a.L * a.G;
+  // A windowed launch's query blocks each scan at most window + block keys,
+  // so a grid too small to fill the chip takes smaller blocks (128 or 64
+  // rows; automatic or unsplit plans) before key splits, whose partials
+  // (S x rows x 512 B) outweigh the window's K/V (bf16, 32 q / 4 kv heads:
+  // a 512-token chunk over a 513-token window 36.7 -> 20.8 us with 64-row
+  // blocks, a 1024-token chunk over a 4096-token window 178 -> 138 us with
+  // 128-row blocks)
+  p.block_rows = PF_ROWS;
+  if (requested <= 1 && a.window > 0 && !prefill_few_fits(a))
+    while (p.block_rows > 64 && (int64_t)((rows + p.block_rows - 1) / p.block_rows) * a.Hkv * a.B < 256)
+      p.block_rows /= 2;
+  p.nqb = (rows + p.block_rows - 1) / p.block_rows;
   const int kt = a.kv_bf16 ? PfGeom<FMT_BF, FMT_BF>::KT : PfGeom<8, 8>::KT;
   // keys any query block scans: from the first block's window start to T
   const int64_t P = a.T - a.L;
@@ -908,8 +920,8 @@ PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
   S = std::max(1, std::min(S, PREFILL_MAX_SPLITS));
   S = (int)std::min<int64_t>(S, std::max<int64_t>(1, tiles));
   // the merge addresses one row's partials with 32-bit offsets from its first
-  // split: (S - 1) strides of nqb * 256 rows of 512 bytes stay below 2^31
-  const int64_t stride_b = (int64_t)p.nqb * PF_ROWS * HEAD_DIM * 4;
+  // split: (S - 1) strides of nqb * block_rows rows of 512 bytes stay below 2^31
+  const int64_t stride_b = (int64_t)p.nqb * p.block_rows * HEAD_DIM * 4;
   S = (int)std::min<int64_t>(S, 1 + (((int64_t)1 << 31) - 1 - HEAD_DIM * 4) / stride_b);
   const int64_t per = (tiles + S - 1) / S;  // tiles per split
   p.S = (int)((tiles + per - 1) / per);
@@ -922,9 +934,9 @@ PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
   return p;
 }
 
-size_t prefill_ws_bytes(int B, int Hkv, int nqb, int S) {
+size_t prefill_ws_bytes(int B, int Hkv, int64_t head_rows, int S) {
   if (S <= 1) return 0;
-  const size_t rows = (size_t)B * Hkv * S * nqb * PF_ROWS;
+  const size_t rows = (size_t)B * Hkv * S * head_rows;
   return rows * HEAD_DIM * 4 + rows * 2 * 4;
 }
 

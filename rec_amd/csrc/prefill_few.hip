@@ -542,7 +542,7 @@ __global__ __launch_bounds__(64 * FW) void prefill_few_kernel(const PrefillArgs 
       store_out4(a.out, (((int64_t)b * a.Hq + hq) * a.L + qi) * HEAD_DIM + d0, r, a.out_dtype);
     } else {
       // no visible key in this split: (-inf, 0, 0), as the tiled kernel writes
-      const int64_t row = (((int64_t)bh * a.S + split) * a.nqb) * PREFILL_BLOCK_ROWS + pg;
+      const int64_t row = (((int64_t)bh * a.S + split) * a.nqb) * a.block_rows + pg;
       *(v4f*)(a.ws_acc + row * HEAD_DIM + d0) = o;
       if (d0 == 0) *(v2f*)(a.ws_stat + row * 2) = (v2f){l > 0.f ? M : NEG_INF, l};
     }
