@@ -907,6 +907,31 @@ PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
     // at least two tiles per split
     const int64_t nwg = (int64_t)p.nqb * a.Hkv * a.B;
     S = nwg >= 128 ? 1 : (int)std::min<int64_t>(PREFILL_MAX_SPLITS, (256 + nwg - 1) / nwg);
+    if (!prefill_few_fits(a) && a.window == 0) {
+      if (nwg >= 128 && nwg < 192) {
+        // half to three quarters of the chip: a short prefix takes 128-row
+        // blocks, a long one two key splits (int8, 32 q / 4 kv heads,
+        // 1,024-token chunks after 0 / 1,024 / 2,048 / 4,096 / 8,192 tokens:
+        // unsplit 55.0 / 99.7 / 141.7 / 224.8 / 312.9 us, two splits 59.7 /
+        // 83.3 / 104.3 / 151.3 / 201.2, 128-row blocks 37.2 / 71.3 / 100.8 /
+        // 161.2 / 240.0)
+        if (P <= 2 * (int64_t)a.L) {
+          p.block_rows = PF_ROWS / 2;
+          p.nqb = (rows + p.block_rows - 1) / p.block_rows;
+        } else {
+          S = 2;
+        }
+      } else if (nwg < 128) {
+        // splits of at least two tiles cannot fill the chip: smaller blocks
+        // as well (128 queries after 1,024 tokens: 4 splits 31.5 us, 4 splits
+        // of 64-row blocks 20.9)
+        const int64_t s_max = std::max<int64_t>(1, std::min<int64_t>(S, tiles / 2));
+        while (p.block_rows > 64 && (int64_t)p.nqb * a.Hkv * a.B * s_max < 192) {
+          p.block_rows /= 2;
+          p.nqb = (rows + p.block_rows - 1) / p.block_rows;
+        }
+      }
+    }
     // the streaming kernel's row groups are workgroups of their own: as many
     // splits as fill the chip once, so that every workgroup runs beside its
     // unit's other row groups (20 queries x 8 heads over 32K keys: 16 splits

@@ -143,6 +143,9 @@ SPLIT_CASES = [
     (3, 12, 4, 1500, 9, True, True, torch.bfloat16, 1),     # explicitly unsplit
     (1, 12, 4, 3000, 100, True, True, torch.bfloat16, 0),   # 300 rows: the second block starts inside query 85
     (1, 28, 4, 4000, 45, True, True, torch.float16, 0),     # seven per KV head: 315 rows over two blocks
+    (4, 32, 4, 300, 256, True, True, torch.bfloat16, 0),    # half the chip's grid, short prefix: 128-row blocks
+    (4, 32, 4, 1200, 256, True, False, torch.float16, 0),   # half the chip's grid, long prefix: two key splits
+    (1, 32, 4, 1000, 128, True, True, torch.bfloat16, 0),   # splits capped at two tiles each: 64-row blocks too
 ]
 
 
