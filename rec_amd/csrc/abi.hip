@@ -475,9 +475,9 @@ size_t rec_prefill_workspace_bytes(int B, int Hq, int Hkv, int L, int splits) {
   if (B < 1 || Hkv < 1 || L < 1 || Hq < Hkv || Hq % Hkv != 0) return 0;
   const int nqb = (int)(((int64_t)L * (Hq / Hkv) + PREFILL_BLOCK_ROWS - 1) / PREFILL_BLOCK_ROWS);
   int S = splits;
-  if (S <= 0) {
+  if (S <= 0) {  // the automatic plan's most (prefill_plan): two splits from half the chip to three quarters
     const int64_t nwg = (int64_t)nqb * Hkv * B;
-    S = nwg >= 128 ? 1 : (int)std::min<int64_t>(PREFILL_MAX_SPLITS, (256 + nwg - 1) / nwg);
+    S = nwg >= 192 ? 1 : nwg >= 128 ? 2 : (int)std::min<int64_t>(PREFILL_MAX_SPLITS, (256 + nwg - 1) / nwg);
   }
   // (blocks of 256 rows: the most any plan needs; smaller blocks take fewer splits)
   return prefill_ws_bytes(B, Hkv, (int64_t)nqb * PREFILL_BLOCK_ROWS, std::min(S, PREFILL_MAX_SPLITS));

@@ -923,10 +923,13 @@ PrefillPlan prefill_plan(const PrefillArgs& a, int requested) {
         }
       } else if (nwg < 128) {
         // splits of at least two tiles cannot fill the chip: smaller blocks
-        // as well (128 queries after 1,024 tokens: 4 splits 31.5 us, 4 splits
-        // of 64-row blocks 20.9)
+        // as well, while the grid stays one round (128 queries after 1,024
+        // tokens, int8: 4 splits 31.5 us, 4 splits of 64-row blocks 20.9;
+        // a bf16 cache's 9 splits of 128-row blocks, 288 workgroups, were
+        // slower than 144)
         const int64_t s_max = std::max<int64_t>(1, std::min<int64_t>(S, tiles / 2));
-        while (p.block_rows > 64 && (int64_t)p.nqb * a.Hkv * a.B * s_max < 192) {
+        while (p.block_rows > 64 && (int64_t)p.nqb * a.Hkv * a.B * s_max < 192 &&
+               (int64_t)((rows + p.block_rows / 2 - 1) / (p.block_rows / 2)) * a.Hkv * a.B * s_max <= 256) {
           p.block_rows /= 2;
           p.nqb = (rows + p.block_rows - 1) / p.block_rows;
         }
