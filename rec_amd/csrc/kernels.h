@@ -167,8 +167,8 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both ke
 // streaming kernel of prefill_few.hip, whose partials share the tiled
 // kernel's workspace layout and merge.  Up to 32 (query, head) rows per KV
 // head over any cache, up to PREFILL_FEW_ROWS over 16,384 keys or more, and
-// up to PREFILL_BLOCK_ROWS over 16,384-131,071 keys in row groups (one
-// workgroup each; prefill_few_groups of them, 1 up to PREFILL_FEW_ROWS rows)
+// up to PREFILL_BLOCK_ROWS over 16,384-131,071 keys, in row groups of one
+// workgroup each (prefill_few_groups of them: 1 up to 32 rows)
 constexpr int PREFILL_FEW_ROWS = 64;
 bool prefill_few_fits(const PrefillArgs& a);
 int prefill_few_groups(const PrefillArgs& a);

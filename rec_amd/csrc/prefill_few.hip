@@ -568,9 +568,20 @@ static void launch_fm(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipSt
   }
 }
 
-// Column tiles per workgroup for `rows` (query, head) rows: all of them up to
-// PREFILL_FEW_ROWS, else row groups of three tiles, or of four from 193 rows on.
-int few_tiles(int rows) { return rows <= PREFILL_FEW_ROWS ? (rows + 15) / 16 : rows <= 192 ? 3 : 4; }
+// Column tiles per workgroup: all of a launch's rows up to 32, then row
+// groups of two tiles below 65,536 keys (33-64 rows) or all the rows from
+// there on, and groups of three tiles, or of four from 193 rows on, above
+// PREFILL_FEW_ROWS.  Two groups of two tiles against one of four, 8 queries
+// x 8 heads (32 q / 4 kv heads): int8 over 16K / 32K / 64K / 128K keys 16.8
+// / 21.3 / 27.2 / 39.1 -> 13.3 / 18.3 / 25.8 / 40.7 us, uint4 over 32K /
+// 64K / 128K 24.1 / 33.4 / 50.5 -> 21.8 / 33.4 / 56.1, affine over 32K /
+// 64K 23.7 / 32.3 -> 21.2 / 31.8 (6 queries over 64K: 26.4 -> 31.4).
+int few_tiles(const PrefillArgs& a) {
+  const int rows = a.L * a.G;
+  if (rows <= 32) return (rows + 15) / 16;
+  if (rows <= PREFILL_FEW_ROWS) return a.T < 65536 ? 2 : (rows + 15) / 16;
+  return rows <= 192 ? 3 : 4;
+}
 
 }  // namespace
 
@@ -599,12 +610,12 @@ bool prefill_few_fits(const PrefillArgs& a) {
 }
 
 int prefill_few_groups(const PrefillArgs& a) {
-  const int rows = a.L * a.G, nc = 16 * few_tiles(rows);
+  const int rows = a.L * a.G, nc = 16 * few_tiles(a);
   return (rows + nc - 1) / nc;
 }
 
 hipError_t launch_prefill_few(const PrefillArgs& a, hipStream_t stream) {
-  const int nt = few_tiles(a.L * a.G);
+  const int nt = few_tiles(a);
   const int units = a.S * a.Hkv;
   const dim3 grid((unsigned)(8 * prefill_few_groups(a) * ((units + 7) / 8)), a.B);
   // the first query sees the fewest keys; from EXACT_PV_BELOW on, P' in one fp16 part
