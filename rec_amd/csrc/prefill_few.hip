@@ -568,17 +568,21 @@ static void launch_fm(const PrefillArgs& a, int nt, bool exact, dim3 grid, hipSt
   }
 }
 
-// Column tiles per workgroup: all of a launch's rows up to 32, then row
-// groups of two tiles below 65,536 keys (33-64 rows) or all the rows from
-// there on, and groups of three tiles, or of four from 193 rows on, above
-// PREFILL_FEW_ROWS.  Two groups of two tiles against one of four, 8 queries
-// x 8 heads (32 q / 4 kv heads): int8 over 16K / 32K / 64K / 128K keys 16.8
-// / 21.3 / 27.2 / 39.1 -> 13.3 / 18.3 / 25.8 / 40.7 us, uint4 over 32K /
-// 64K / 128K 24.1 / 33.4 / 50.5 -> 21.8 / 33.4 / 56.1, affine over 32K /
-// 64K 23.7 / 32.3 -> 21.2 / 31.8 (6 queries over 64K: 26.4 -> 31.4).
+// Column tiles per workgroup: up to 32 of a launch's rows, row groups of one
+// tile below 32,768 keys, else all the rows; 33-64 rows, groups of two tiles
+// below 65,536 keys, else all the rows; above PREFILL_FEW_ROWS, groups of
+// three tiles, or of four from 193 rows on.  32 q / 4 kv heads: two groups of
+// one tile against one of two, 4 queries over 1K / 4K / 8K / 16K / 32K / 64K
+// int8 keys 10.0 / 10.2 / 10.5 / 11.7 / 14.5 / 19.3 -> 8.1 / 8.3 / 8.9 / 10.5
+// / 14.1 / 20.0 us, uint4 over 4K / 8K / 16K / 32K / 64K 11.5 / 12.1 / 13.2 /
+// 16.6 / 22.6 -> 9.6 / 10.3 / 12.9 / 17.5 / 26.7 (affine alike); two groups
+// of two tiles against one of four, 8 queries over 16K / 32K / 64K / 128K
+// int8 keys 16.8 / 21.3 / 27.2 / 39.1 -> 13.3 / 18.3 / 25.8 / 40.7 us, uint4
+// over 32K / 64K / 128K 24.1 / 33.4 / 50.5 -> 21.8 / 33.4 / 56.1, affine over
+// 32K / 64K 23.7 / 32.3 -> 21.2 / 31.8 (6 queries over 64K: 26.4 -> 31.4).
 int few_tiles(const PrefillArgs& a) {
   const int rows = a.L * a.G;
-  if (rows <= 32) return (rows + 15) / 16;
+  if (rows <= 32) return rows > 16 && a.T < 32768 ? 1 : (rows + 15) / 16;
   if (rows <= PREFILL_FEW_ROWS) return a.T < 65536 ? 2 : (rows + 15) / 16;
   return rows <= 192 ? 3 : 4;
 }
