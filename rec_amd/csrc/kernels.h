@@ -165,10 +165,10 @@ hipError_t launch_decode_merge(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream);  // both kernels when a.S > 1
 // A few queries over a quantized cache, no window and no mask array: the
 // streaming kernel of prefill_few.hip, whose partials share the tiled
-// kernel's workspace layout and merge.  Up to 32 (query, head) rows per KV
-// head over any cache, up to PREFILL_FEW_ROWS over 16,384 keys or more, and
-// up to PREFILL_BLOCK_ROWS over 16,384-131,071 keys, in row groups of one
-// workgroup each (prefill_few_groups of them: 1 up to 32 rows)
+// kernel's workspace layout and merge.  Up to PREFILL_FEW_ROWS (query, head)
+// rows per KV head over any cache, and up to PREFILL_BLOCK_ROWS over
+// 16,384-131,071 keys, in row groups of one workgroup each
+// (prefill_few_groups of them)
 constexpr int PREFILL_FEW_ROWS = 64;
 bool prefill_few_fits(const PrefillArgs& a);
 int prefill_few_groups(const PrefillArgs& a);

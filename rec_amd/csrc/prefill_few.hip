@@ -589,10 +589,11 @@ int few_tiles(const PrefillArgs& a) {
 
 }  // namespace
 
-// Up to 32 rows (two column tiles) the streaming kernel is the faster one at
-// every cache length measured; three or four tiles (one wave per SIMD, the
-// accumulators partly in AGPRs) only over long caches: 8 queries x 8 heads
-// over 65,536 keys 31.7 -> 27.7 us, over 8,192 keys 13.7 -> 14.9 us.  Row
+// Up to PREFILL_FEW_ROWS rows the streaming kernel is the faster one at every
+// cache length measured (33-64 rows below 65,536 keys in two row groups:
+// 8 queries x 8 heads over 512 / 2K / 8K / 12K int8 keys, tiled -> streaming
+// 14.2 / 14.3 / 14.6 / 14.3 -> 10.0 / 10.2 / 11.3 / 12.1 us; uint4 and affine
+// over 4K 16.9 / 17.3 -> 11.7 / 11.4).  Row
 // groups (more than 64 rows) from 16,384 to 131,071 keys; 32 q / 4 kv heads,
 // tiled -> row groups: int8 12 queries over 32K 28.4 -> 22.0 us, 20 over 16K
 // 26.6 -> 21.3, over 32K 36.4 -> 32.0, over 65,536 52.5 -> 49.4, 32 over 32K
@@ -610,7 +611,7 @@ bool prefill_few_fits(const PrefillArgs& a) {
   const bool groups = rows <= PREFILL_BLOCK_ROWS && a.T >= 16384 && a.T < 131072 &&
                       (a.v_fmt == 8 || (int64_t)rows * a.T <= 100 * 32768);
   return fmt && a.window == 0 && a.bias.p == nullptr &&
-         (rows <= 32 || (rows <= PREFILL_FEW_ROWS && a.T >= 16384) || groups);
+         (rows <= PREFILL_FEW_ROWS || groups);
 }
 
 int prefill_few_groups(const PrefillArgs& a) {

@@ -202,6 +202,8 @@ U4_FEW_CASES = [
     (2, 16, 2, 500, 3, True, False, torch.bfloat16, 1),    # unsplit, 24 rows
     (1, 4, 4, 700, 32, True, True, torch.float16, 3),      # one query head per KV head: 32 rows
     (1, 8, 1, 9000, 2, False, True, torch.bfloat16, 0),    # full attention, past the exact-P·V length
+    (1, 32, 4, 4096, 8, True, True, torch.bfloat16, 0),    # 64 rows over 4K keys: two row groups
+    (1, 16, 2, 900, 3, True, False, torch.float16, 2),     # 48 rows over a short cache, explicit splits
 ]
 
 

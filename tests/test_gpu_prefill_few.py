@@ -1,8 +1,8 @@
 """Parity of the few-query prefill path (prefill_few.hip) with the CPU oracle.
 
-Chunks of at most 32 (query, head) rows per KV head over an int8 or affine
-cache (64 over long caches) run on the streaming kernel instead of the tiled
-one; the outputs must lie within
+Chunks of at most 64 (query, head) rows per KV head over an int8 or affine
+cache run on the streaming kernel instead of the tiled one (33-64 rows below
+65,536 keys as two row groups); the outputs must lie within
 2e-3 absolute + 1e-3 relative of the oracle, as the tiled kernel's do, for
 causal and full masks, sinks, GQA ratios 1 to 8, bf16 and fp16 queries, key
 splits (automatic, explicit, one) and ranges whose last chunk lies wholly past
@@ -35,6 +35,11 @@ CASES = [
     (1, 16, 2, 16384, 6, True, False, torch.float16, 5),    # 48 rows, explicit splits
     (2, 24, 8, 17000, 14, True, True, torch.bfloat16, 0),   # 42 rows, G = 3, two sequences
     (1, 8, 1, 16400, 7, False, True, torch.bfloat16, 1),    # 56 rows, full attention, unsplit
+    # 33-64 rows over short caches: two row groups
+    (1, 32, 4, 4096, 8, True, True, torch.bfloat16, 0),     # 64 rows over 4K keys
+    (1, 32, 4, 500, 5, True, True, torch.float16, 0),       # 40 rows, a 32-row and an 8-row group
+    (2, 16, 2, 12000, 6, False, False, torch.bfloat16, 3),  # 48 rows, full attention, explicit splits
+    (1, 8, 1, 40, 8, True, True, torch.bfloat16, 1),        # 64 rows, unsplit, chunk past early limits
 ]
 
 
@@ -86,6 +91,8 @@ AFFINE_CASES = [
     (1, 8, 1, 62, 2, True, True, torch.bfloat16, 1),        # 16 rows: one column tile, unsplit
     (1, 32, 4, 20000, 8, True, True, torch.bfloat16, 0),    # 64 rows: four column tiles
     (1, 24, 8, 16384, 14, True, False, torch.float16, 3),   # 42 rows, G = 3
+    (1, 32, 4, 4096, 8, True, True, torch.bfloat16, 0),     # 64 rows over 4K keys: two row groups
+    (1, 16, 2, 700, 3, True, False, torch.float16, 0),      # 48 rows over a short cache
 ]
 
 
