@@ -263,7 +263,8 @@ def quantized_attention_with_sinks(
     (bf16/f16 queries, the newest ``L`` cached tokens) the chunked prefill
     kernel, which reads every cache format directly (4-bit and affine values
     rounded to the query dtype, as the reference dequantizes, int8 codes
-    exactly) and applies a sliding-window pattern itself.  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
+    exactly) and applies a sliding-window pattern itself; float32 queries
+    take one decode per query row (:func:`_rows_as_decodes`).  Returns ``(B, n_q, L, 128)`` in ``out_dtype``
     (default: the query dtype, as the reference returns, model.py:132-139).
     The sinks enter as float32 values at every ``L``, the cast this function
     makes in the reference (model.py:129); ``sink_dtype`` (bf16/f16) rounds
@@ -297,9 +298,12 @@ def quantized_attention_with_sinks(
         out, want = _new_out((B, Hq, D), out_dtype, queries)
         _decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype, bias=bias)
         out = out.view(B, Hq, 1, D)
+    elif queries.dtype == torch.float32:
+        return _rows_as_decodes(
+            queries, T, Hkv, causal, win, bias, out_dtype,
+            lambda q, t, o, b: _decode_launch(q, keys, values, scale, sinks, splits, o, T=t, sink_dtype=sink_dtype,
+                                              bias=b))
     else:
-        if queries.dtype not in (torch.bfloat16, torch.float16):
-            raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
         out, want = _new_out((B, Hq, L, D), out_dtype, queries)
         _prefill_launch(queries, keys, values, scale, sinks, causal, out, splits or 0, win, sink_dtype, bias)
     return _finish(out, want)
@@ -485,6 +489,37 @@ def _bias_args(bias, decode):
     return (t.data_ptr(), sb, skv, sg, ext) if decode else (t.data_ptr(), sb, skv, sg, sl, ext)
 
 
+def _rows_as_decodes(queries, T, Hkv, causal, window, bias, out_dtype, decode_one):
+    """A chunk of float32 queries, each query row as one decode.
+
+    The matrix-core prefill takes bf16 / fp16 operands; the reference's SDPA
+    also takes float32 queries (model.py:196-203, 211), the cache then
+    dequantized to float32.  The decode kernels attend with float32 queries
+    over the exact dequantized values, so query ``i`` of the ``L`` runs as a
+    decode over the keys it sees: the first ``T - L + i + 1`` under a causal
+    mask, a sliding window or a mask array as that query's bias row.
+    ``decode_one(q_i, T_i, out_i, bias_i)`` launches one of them; ``L``
+    launch pairs instead of one launch, for float32 models, not for speed.
+    """
+    B, Hq, L, D = queries.shape
+    dev = queries.device
+    if window:  # the causal window as a bias: query p keeps keys (p - window, p]
+        qp = torch.arange(T - L, T, device=dev)[:, None]
+        kp = torch.arange(T, device=dev)[None]
+        bias = _mask_bias((qp >= kp) & (qp < kp + window), B, Hkv, Hq // Hkv, L, T, dev)
+    out, want = _new_out((L, B, Hq, D), out_dtype, queries)
+    flat = None
+    if bias is not None:
+        t, (sb, skv, sg, sl, ext) = bias
+        flat = t.view(-1)
+    for i in range(L):
+        bias_i = None
+        if flat is not None:  # row i of the bias: 16-byte aligned (sl is a multiple of 4 elements)
+            bias_i = (flat[i * sl:], (sb, skv, sg, sl, ext - i * sl))
+        decode_one(queries[:, :, i:i + 1], T - L + i + 1 if causal else T, out[i], bias_i)
+    return _finish(out.permute(1, 2, 0, 3).contiguous(), want)
+
+
 def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=None, *, out_dtype=None,
                                  splits=None, window=None, sink_dtype=None):
     """Attention of ``queries`` ``(B, n_q, L, 128)`` over bf16 ``keys``/``values``
@@ -522,6 +557,11 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
         out, want = _new_out((B, Hq, D), out_dtype, queries)
         _bf16_decode_launch(queries, keys, values, scale, sinks, splits, out, sink_dtype=sink_dtype, bias=bias)
         out = out.view(B, Hq, 1, D)
+    elif queries.dtype == torch.float32:
+        return _rows_as_decodes(
+            queries, T, Hkv, causal, win, bias, out_dtype,
+            lambda q, t, o, b: _bf16_decode_launch(q, keys[:, :, :t], values[:, :, :t], scale, sinks, splits, o,
+                                                   sink_dtype=sink_dtype, bias=b))
     else:
         out, want = _new_out((B, Hq, L, D), out_dtype, queries)
         _bf16_prefill_launch(queries, keys, values, scale, sinks, causal, win, out, splits or 0, sink_dtype, bias)
@@ -559,10 +599,6 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
     if L == 1:
         plan1 = _mask_plan(mask, 1, min(cache.offset + 1, cache.capacity) if ring else cache.offset + 1)
     keeps_all = mask is None or (plan1 is not None and plan1[1] == 0)
-    if queries.dtype not in (torch.bfloat16, torch.float16) and L > 1:
-        # chunks run on the matrix cores: refused here, before the append
-        # changes the cache
-        raise NotImplementedError("prefill queries must be bf16 or f16 (the matrix-core input type)")
     if ring:
         # a new token goes to its ring slot and decode attends over the valid
         # slots (order-free); a chunk attends over the ring in order plus

@@ -155,9 +155,6 @@ def test_affine_rejections(gpu):
     q = synthetic.query(1, 32, 1, 92, dtype=torch.bfloat16)
     with pytest.raises(ValueError):  # group size of the call disagrees with the cache
         quantized_attention_with_sinks(q, kv_k, kv_v, SCALE, None, None, 32, 8, 4)
-    q8 = synthetic.query(1, 32, 8, 93, dtype=torch.float32)
-    with pytest.raises(NotImplementedError):  # prefill queries must be a matrix-core input type
-        quantized_attention_with_sinks(q8, kv_k, kv_v, SCALE, "causal", None, 64, 8, 4)
 
 
 F16_CASES = [
