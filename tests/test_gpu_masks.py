@@ -147,25 +147,28 @@ def test_attend_one_query_window(gpu):
     assert_close(f32(out), ref, "attend window")
 
 
-def test_attend_refuses_f32_matrix_core_queries_before_append(gpu):
-    """A float32 chunk is refused before the new tokens touch the cache; one
-    float32 query under a window decodes (the window a bias)."""
+def test_attend_f32_queries_under_masks(gpu):
+    """A float32 chunk under a window pattern (a decode per query, the window
+    its bias row), then one float32 query under a window (the window a bias)
+    and a plain float32 decode step."""
     cache = QuantizedKVCache(32, 8, 8)
-    k = synthetic.kv((1, 2, 103, 128), 61)
-    v = synthetic.kv((1, 2, 103, 128), 62)
+    k = synthetic.kv((1, 2, 105, 128), 61)
+    v = synthetic.kv((1, 2, 105, 128), 62)
     cache.update_and_fetch(k[:, :, :100], v[:, :, :100])
     q3 = synthetic.query(1, 16, 3, 63, dtype=torch.float32)
-    with pytest.raises(NotImplementedError):
-        attend(q3, k[:, :, 100:], v[:, :, 100:], cache, SCALE, "causal")
-    assert cache.offset == 100
+    keep3 = keep_pattern(3, 103, 20)
+    out = attend(q3, k[:, :, 100:103], v[:, :, 100:103], cache, SCALE, keep3)
+    assert cache.offset == 103 and out.dtype == torch.float32
+    kq, vq = cache.keys_and_values()
+    assert_close(f32(out), O.attention(f32(q3), oracle_xhat(kq), oracle_xhat(vq), SCALE, None, keep3), "f32 chunk")
     q1 = synthetic.query(1, 16, 1, 64, dtype=torch.float32)
-    keep = keep_pattern(1, 101, 50)
-    out = attend(q1, k[:, :, 100:101], v[:, :, 100:101], cache, SCALE, keep, out_dtype=torch.float32)
-    assert cache.offset == 101
+    keep = keep_pattern(1, 104, 50)
+    out = attend(q1, k[:, :, 103:104], v[:, :, 103:104], cache, SCALE, keep, out_dtype=torch.float32)
+    assert cache.offset == 104
     kq, vq = cache.keys_and_values()
     assert_close(f32(out), O.attention(f32(q1), oracle_xhat(kq), oracle_xhat(vq), SCALE, None, keep), "f32 window")
-    out = attend(q1, k[:, :, 101:102], v[:, :, 101:102], cache, SCALE, "causal", out_dtype=torch.float32)
-    assert cache.offset == 102 and torch.isfinite(out).all()
+    out = attend(q1, k[:, :, 104:105], v[:, :, 104:105], cache, SCALE, "causal", out_dtype=torch.float32)
+    assert cache.offset == 105 and torch.isfinite(out).all()
 
 
 def test_bf16_decode_window_mask(gpu):

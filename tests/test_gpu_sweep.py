@@ -1,6 +1,7 @@
 """A seeded sweep of shapes through every decode and prefill format against
 the oracle: batch sizes, GQA ratios, ragged token counts, split counts, query
-dtypes and sinks drawn from a fixed generator (the same 40 cases every run;
+dtypes (float32 chunks included) and sinks drawn from a fixed generator (the
+same 40 cases every run;
 REC_SWEEP_CASES=n draws n, the first 40 being these; two cases of the
 400-case draw always run as regressions).
 Outputs within 2e-3 abs + 1e-3 rel of the float64 oracle over the cache read
@@ -35,9 +36,7 @@ def draw(n=int(os.environ.get("REC_SWEEP_CASES", "40")), seed=2024):
         L = int(rng.choice([1, 1, 1, 7, 40]))  # mostly decode
         L = min(L, T)
         fmt = FORMATS[i % len(FORMATS)]
-        dt = DTYPES[int(rng.integers(0, 3))]
-        if L > 1 and dt == torch.float32:
-            dt = torch.bfloat16  # prefill queries are bf16 / fp16
+        dt = DTYPES[int(rng.integers(0, 3))]  # float32 chunks run a decode per query
         splits = int(rng.choice([0, 0, 1, 3, 17, 64]))
         sinks = bool(rng.integers(0, 2))
         cases.append((fmt, B, G * Hkv, Hkv, T, L, dt, splits, sinks, 5000 + 7 * i))  # last: the data seed
