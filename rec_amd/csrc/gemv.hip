@@ -26,7 +26,7 @@ namespace rec {
 
 namespace {
 
-constexpr int GV_WAVES = 4;
+constexpr int GV_WAVES = 4;        // waves per workgroup (more for matrices of few tiles)
 constexpr int GV_SPAN = 128;         // elements per span
 constexpr int GV_REC = 1024 + 128;   // bytes per (tile, span) record
 constexpr int GV_ZERO = 256;         // zero bytes read by B lanes without data
@@ -81,13 +81,15 @@ __host__ __device__ size_t q4_gemv_red_offset(int M, int64_t K) {
   return ((size_t)M * K * 2 + GV_ZERO + (size_t)M * (K / 64) * 4 + 15) & ~(size_t)15;
 }
 
-size_t q4_gemv_lds_bytes(int M, int64_t K) { return q4_gemv_red_offset(M, K) + GV_WAVES * 64 * 16; }
+static size_t lds_bytes_nw(int M, int64_t K, int nw) { return q4_gemv_red_offset(M, K) + (size_t)nw * 64 * 16; }
+
+size_t q4_gemv_lds_bytes(int M, int64_t K) { return lds_bytes_nw(M, K, GV_WAVES); }
 
 // WPT waves share one 16-row tile, wave p taking spans p, p + WPT, ...: small
 // matrices (the attention projections, the experts) then still spread over
-// every SIMD.  A workgroup covers GV_WAVES / WPT tiles.
-template <int WPT>
-__global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs a) {
+// every SIMD.  A workgroup of NW waves covers NW / WPT tiles.
+template <int WPT, int NW>
+__global__ __launch_bounds__(64 * NW) void q4_gemv_kernel(const Q4GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs
   float* xs = (float*)(zero + GV_ZERO);
   v4f* red = (v4f*)(smem + q4_gemv_red_offset(M, a.K));
 
-  const int tile = blockIdx.x * (GV_WAVES / WPT) + wave / WPT, part = wave % WPT;
+  const int tile = blockIdx.x * (NW / WPT) + wave / WPT, part = wave % WPT;
   const bool live = tile * 16 < a.N;  // wave-uniform
   const int n_w = live && part < S ? (S - part + WPT - 1) / WPT : 0;  // spans of this wave
 
@@ -130,9 +132,9 @@ __global__ __launch_bounds__(64 * GV_WAVES) void q4_gemv_kernel(const Q4GemvArgs
   // ---- stage x: records of 8 elements in the MFMA's k order, and group sums ----
   // Thread order (m, span, gs, slab, kq & 1) puts the 8 records of one group
   // on 8 consecutive lanes.
-  for (int t = tid; t < GV_ZERO / 4; t += 64 * GV_WAVES) ((uint32_t*)zero)[t] = 0;
+  for (int t = tid; t < GV_ZERO / 4; t += 64 * NW) ((uint32_t*)zero)[t] = 0;
   const int nrec = M * S * 16;
-  for (int t0 = 0; t0 < nrec; t0 += 64 * GV_WAVES) {
+  for (int t0 = 0; t0 < nrec; t0 += 64 * NW) {
     const int t = t0 + tid;
     float sum = 0.f;
     if (t < nrec) {
@@ -240,26 +242,33 @@ hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int WPT>
-hipError_t launch_q4_gemv_wpt(const Q4GemvArgs& a, int64_t tiles, size_t lds, hipStream_t stream) {
-  constexpr int TPG = GV_WAVES / WPT;  // tiles per workgroup
+template <int WPT, int NW = GV_WAVES>
+hipError_t launch_q4_gemv_wpt(const Q4GemvArgs& a, int64_t tiles, hipStream_t stream) {
+  constexpr int TPG = NW / WPT;  // tiles per workgroup
+  const size_t lds = lds_bytes_nw(a.M, a.K, NW);
   if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute((const void*)q4_gemv_kernel<WPT>,
+    const hipError_t e = hipFuncSetAttribute((const void*)q4_gemv_kernel<WPT, NW>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(q4_gemv_kernel<WPT>, dim3((unsigned)((tiles + TPG - 1) / TPG)), dim3(64 * GV_WAVES), lds, stream,
-                     a);
+  hipLaunchKernelGGL((q4_gemv_kernel<WPT, NW>), dim3((unsigned)((tiles + TPG - 1) / TPG)), dim3(64 * NW), lds,
+                     stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream) {
-  const int64_t tiles = (a.N + 15) / 16;
-  const size_t lds = q4_gemv_lds_bytes(a.M, a.K);
+  const int64_t tiles = (a.N + 15) / 16, S = a.K / GV_SPAN;
   // fewest waves per tile that still give every SIMD (1024) two waves
-  if (tiles >= 2048) return launch_q4_gemv_wpt<1>(a, tiles, lds, stream);
-  if (tiles >= 1024) return launch_q4_gemv_wpt<2>(a, tiles, lds, stream);
-  return launch_q4_gemv_wpt<4>(a, tiles, lds, stream);
+  if (tiles >= 2048) return launch_q4_gemv_wpt<1>(a, tiles, stream);
+  if (tiles >= 1024) return launch_q4_gemv_wpt<2>(a, tiles, stream);
+  // Fewer tiles than CUs (o_proj 2048 x 4096, down_proj 2048 x 6144: 128
+  // tiles): one tile per workgroup of 8 or 16 waves, so that each wave's
+  // spans fit its ring of NB and are all in flight at once
+  if (tiles < 256 && S > 4 * 4) {
+    if (S <= 8 * 4 && lds_bytes_nw(a.M, a.K, 8) <= 160 * 1024) return launch_q4_gemv_wpt<8, 8>(a, tiles, stream);
+    if (lds_bytes_nw(a.M, a.K, 16) <= 160 * 1024) return launch_q4_gemv_wpt<16, 16>(a, tiles, stream);
+  }
+  return launch_q4_gemv_wpt<4>(a, tiles, stream);
 }
 
 }  // namespace rec

@@ -48,8 +48,10 @@ CASES = [
     # M, N, K
     (1, 4096, 2048),   # q_proj
     (1, 512, 2048),    # k_proj / v_proj
-    (1, 2048, 4096),   # o_proj
-    (1, 2048, 6144),   # dense MLP down
+    (1, 2048, 4096),   # o_proj: 128 row tiles, 8 waves per tile
+    (1, 2048, 6144),   # dense MLP down: 16 waves per tile
+    (4, 300, 8192),    # 19 row tiles of 64 spans: 16 waves per tile, four vectors
+    (2, 200, 3072),    # 24 spans: 8 waves per tile, a ragged last tile
     (1, 6144, 2048),   # dense MLP gate / up
     (3, 1000, 512),    # ragged rows, expert down (K = 512)
     (8, 100, 2048),
