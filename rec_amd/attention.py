@@ -503,20 +503,33 @@ def _rows_as_decodes(queries, T, Hkv, causal, window, bias, out_dtype, decode_on
     """
     B, Hq, L, D = queries.shape
     dev = queries.device
-    if window:  # the causal window as a bias: query p keeps keys (p - window, p]
-        qp = torch.arange(T - L, T, device=dev)[:, None]
-        kp = torch.arange(T, device=dev)[None]
-        bias = _mask_bias((qp >= kp) & (qp < kp + window), B, Hkv, Hq // Hkv, L, T, dev)
     out, want = _new_out((L, B, Hq, D), out_dtype, queries)
-    flat = None
-    if bias is not None:
+    if window:
+        # The causal window (always with the causal limit) as a bias, without
+        # an (L, T) array: query i sees d = L - 1 - i keys fewer than the last
+        # one and keeps key t iff t + d >= T - window, so its row is base[d:]
+        # with base[j] = 0 from j = T - window on, else -inf.  Four copies of
+        # base shifted by 0-3 keep every row start 16-byte aligned (row i is
+        # copy d % 4 from element 4 (d // 4) on).
+        Tp = (T + 3) // 4 * 4
+        j = torch.arange(Tp, device=dev)[None] + torch.arange(4, device=dev)[:, None]
+        flat = torch.where(j >= T - window, 0.0, float("-inf")).to(torch.float32).reshape(-1).contiguous()
+
+        def row(i):
+            d = L - 1 - i
+            off = (d % 4) * Tp + d // 4 * 4
+            return flat[off:], (0, 0, 0, 0, 4 * Tp - off)
+    elif bias is not None:
         t, (sb, skv, sg, sl, ext) = bias
         flat = t.view(-1)
+
+        def row(i):  # row i of the bias: 16-byte aligned (sl is a multiple of 4 elements)
+            return flat[i * sl:], (sb, skv, sg, sl, ext - i * sl)
+    else:
+        def row(i):
+            return None
     for i in range(L):
-        bias_i = None
-        if flat is not None:  # row i of the bias: 16-byte aligned (sl is a multiple of 4 elements)
-            bias_i = (flat[i * sl:], (sb, skv, sg, sl, ext - i * sl))
-        decode_one(queries[:, :, i:i + 1], T - L + i + 1 if causal else T, out[i], bias_i)
+        decode_one(queries[:, :, i:i + 1], T - L + i + 1 if causal else T, out[i], row(i))
     return _finish(out.permute(1, 2, 0, 3).contiguous(), want)
 
 
