@@ -627,9 +627,24 @@ __global__ __launch_bounds__(512) void prefill_kernel(const PrefillArgs a) {
   // uniform, kept in scalar registers (the compiler would otherwise treat
   // them, and everything derived from them, as varying across the lanes)
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int split = __builtin_amdgcn_readfirstlane((int)blockIdx.x / a.nqb);
-  const int qb = __builtin_amdgcn_readfirstlane((int)blockIdx.x - split * a.nqb);
-  const int h = blockIdx.y, b = blockIdx.z;
+  // Workgroup i of a launch runs on XCD i % 8.  When several query blocks
+  // read the same K/V (one split of one KV head) and the (query block x
+  // split, KV head) grid is a multiple of 8, logical block l = x + gx·y is
+  // placed at i with l = (i % 8)·(n / 8) + i / 8, so that each XCD holds a
+  // run of consecutive blocks -- the query blocks of one or two KV heads --
+  // whose K/V tiles its L2 then serves to the rest of the run.
+  int bx = blockIdx.x, by = blockIdx.y;
+  {
+    const int gx = gridDim.x, n = gx * gridDim.y;
+    if (a.nqb > 1 && (n & 7) == 0) {
+      const int i = bx + gx * by, l = (i & 7) * (n >> 3) + (i >> 3);
+      by = l / gx;
+      bx = l - by * gx;
+    }
+  }
+  const int split = __builtin_amdgcn_readfirstlane(bx / a.nqb);
+  const int qb = __builtin_amdgcn_readfirstlane(bx - split * a.nqb);
+  const int h = __builtin_amdgcn_readfirstlane(by), b = blockIdx.z;
   const int64_t bh = (int64_t)b * a.Hkv + h;
   const int p0 = qb * a.block_rows;                     // the block's first row
   const int n_p = min(a.block_rows, a.L * a.G - p0);    // and its row count
