@@ -416,6 +416,7 @@ Q4_SHAPES = [
     (4096, 2048, "q_proj"),
     (2048, 4096, "o_proj"),
     (512, 2048, "k_proj"),
+    (5120, 2048, "qkv_proj"),  # q, k and v stacked (Q4Matrix.stack): one launch for the three
 ]
 
 

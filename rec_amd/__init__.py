@@ -13,7 +13,7 @@ kernels through the C ABI in ``include/rec_amd.h``.
 from ._lib import RecError, load as library  # noqa: F401
 from .attention import attend, dequantize_kv, quantized_attention_with_sinks, scaled_dot_product_attention  # noqa: F401
 from .cache import MixedQuantizedKVCache, QuantizedKV, QuantizedKVCache, to_logical  # noqa: F401
-from .gemv import Q4Matrix, q4_gemv, quantized_matmul  # noqa: F401
+from .gemv import Q4Matrix, q4_gemv, q4_gemv_parts, quantized_matmul  # noqa: F401
 from .kvstorage import FixedKVCache, FixedSlidingKVCache, KVStorage, make_cache  # noqa: F401
 
 __version__ = "0.1.0"

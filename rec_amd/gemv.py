@@ -5,7 +5,9 @@ biases: engine/src/rec_mlx/quantized.py:27-36) and multiplies them by the
 bf16 activations with ``q4`` / ``dot16`` (engine/src/rec_mlx/kernels/
 megakernel.py:161-232) after packing its weight banks once
 (megakernel.py:1017-1040).  Here a :class:`Q4Matrix` packs an MLX-layout
-matrix once (``rec_q4_pack``) and :func:`q4_gemv` runs ``rec_q4_gemv``.
+matrix once (``rec_q4_pack``) and :func:`q4_gemv` runs ``rec_q4_gemv``;
+:meth:`Q4Matrix.stack` packs several matrices of one K (a layer's q, k and v
+projections) as one, so a single launch computes them all.
 :func:`quantized_matmul` keeps the call shape of ``mx.quantized_matmul`` for
 the one configuration the reference uses (``transpose=True``, group 64, 4 bits).
 """
@@ -58,6 +60,25 @@ class Q4Matrix:
             torch.cuda.current_stream(w.device).cuda_stream,
         )
         _lib.check(rc, "rec_q4_pack")
+        self.parts = (N,)
+
+    @classmethod
+    def stack(cls, mats) -> "Q4Matrix":
+        """One matrix of the rows of several ``(w, scales, biases)`` triples of
+        one K, in order: a single launch of :func:`q4_gemv` then computes all
+        of their outputs from the same x, as the reference's decoder computes
+        the 32 query, 4 key and 4 value heads of a layer in one pass over its
+        normalised input (engine/src/rec_mlx/kernels/megakernel.py:871-886).
+        :func:`q4_gemv_parts` splits the result back into the parts."""
+        mats = list(mats)
+        if not mats:
+            raise ValueError("stack() needs at least one matrix")
+        ws, ss, bs = zip(*mats)
+        if len({int(w.shape[-1]) for w in ws}) != 1:
+            raise ValueError(f"stacked matrices need one K, got {[int(w.shape[-1]) * 8 for w in ws]}")
+        m = cls(torch.cat([_words(w) for w in ws]), torch.cat(ss), torch.cat(bs))
+        m.parts = tuple(int(w.shape[0]) for w in ws)
+        return m
 
     @property
     def shape(self):
@@ -97,6 +118,13 @@ def q4_gemv(x: torch.Tensor, m: Q4Matrix, out_dtype=None) -> torch.Tensor:
         )
         _lib.check(rc, "rec_q4_gemv")
     return out.reshape(*lead, m.N)
+
+
+def q4_gemv_parts(x: torch.Tensor, m: Q4Matrix, out_dtype=None):
+    """:func:`q4_gemv` over a :meth:`Q4Matrix.stack` matrix, returned as one
+    ``(..., N_i)`` view per stacked part (one launch for all of them)."""
+    y = q4_gemv(x, m, out_dtype)
+    return tuple(torch.split(y, list(m.parts), dim=-1))
 
 
 def quantized_matmul(x, w, scales, biases, transpose=True, group_size=GROUP, bits=4, mode="affine"):

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle as O
-from rec_amd import Q4Matrix, q4_gemv, quantized_matmul
+from rec_amd import Q4Matrix, q4_gemv, q4_gemv_parts, quantized_matmul
 
 pytestmark = pytest.mark.gpu
 
@@ -137,3 +137,26 @@ def test_q4_gemv_in_hip_graph(gpu):
         g.replay()
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, rtol=0, atol=0, msg=f"replay {rep}")
+
+
+@pytest.mark.parametrize("parts,M", [((4096, 512, 512), 1), ((100, 33, 1000), 3)], ids=["qkv", "ragged"])
+def test_stacked_matrices_one_launch(gpu, parts, M):
+    """Q4Matrix.stack packs several matrices of one K as one (a layer's q, k
+    and v projections, megakernel.py:871-886): q4_gemv_parts returns each
+    part's output from one launch, equal to the oracle for that part, also
+    where the parts share 16-row tiles (ragged row counts)."""
+    K = 2048
+    probs = [problem(M, N, K, seed=31 + i) for i, N in enumerate(parts)]
+    x = probs[0][0]
+    m = Q4Matrix.stack([(w, s, b) for _, w, s, b in probs])
+    assert m.shape == (sum(parts), K) and m.parts == parts
+    ys = q4_gemv_parts(x, m, out_dtype=torch.float32)
+    y16 = q4_gemv_parts(x, m)
+    torch.cuda.synchronize()
+    assert [y.shape for y in ys] == [(M, N) for N in parts]
+    for i, (_, w, s, b) in enumerate(probs):
+        ref, mag = oracle_rows(x, w, s, b)
+        check(ys[i], ref, mag, f"part {i}")
+        assert torch.equal(y16[i].view(torch.int16), ys[i].to(torch.bfloat16).view(torch.int16))
+    with pytest.raises(ValueError):  # parts of different K
+        Q4Matrix.stack([probs[0][1:], problem(1, 16, 1024, seed=3)[1:]])
