@@ -197,7 +197,9 @@ int rec_decode_merge(const float* sinks, int B, int Hq, int Hkv, int64_t T, int 
 /*
  * Chunked prefill: the last L of the T cached tokens are new (already
  * quantize-appended with rec_kv_append); their queries q (B, Hq, L, D), element
- * strides (q_sb, q_sh, q_st), bf16 or f16, attend over all T tokens — with
+ * strides (q_sb, q_sh, q_st), bf16 or f16 (float32 queries: one
+ * rec_decode_attn per query row i over the first T-L+i+1 tokens under a
+ * causal mask, as the Python layer does), attend over all T tokens — with
  * causal != 0, query i sees tokens [0, T-L+i]; window > 0 further limits
  * query position p to keys > p - window (a sliding-window mask array of
  * model.py:122-128; window 0 = none) — with optional sink logits.
@@ -395,7 +397,10 @@ int rec_region_destroy(void* handle);
  * rec_q4_gemv: M (1..8) bf16 vectors x (row stride x_stride elements, a
  * multiple of 8; 16-byte aligned) to out (out_dtype REC_BF16, rounded to
  * nearest even as the reference stores bfloat16_t, or REC_F32; row stride
- * out_stride elements).
+ * out_stride elements).  Matrices of one K stacked row-wise (their words,
+ * scales and biases concatenated) pack as one, and one launch computes every
+ * part, as the reference computes a layer's q, k and v heads in one pass
+ * (megakernel.py:871-886).
  * Replaces q4 / dot16 (and q4_local) of
  * engine/src/rec_mlx/kernels/megakernel.py:161-232, the projections of
  * model.py:151-154 quantized by quantized.py:27-36 (group 64, 4 bits, affine).
