@@ -275,3 +275,50 @@ def test_row_group_prefill_matches_oracle(gpu, case, fmt):
     kh, vh = prefill_side(oracle_xhat(kq), kq, dtype), prefill_side(oracle_xhat(vq), vq, dtype)
     ref = O.attention(f32(q), kh, vh, SCALE, q_sinks(sinks, q.dtype), mask)
     assert_close(f32(out), ref, f"case {case} {fmt}")
+
+
+GRAPH_CASES = [
+    # name, B, Hq, Hkv, P, L, cache format (key bits, value bits) or "affine", mask
+    ("tiled", 1, 32, 4, 2000, 300, (8, 8), "causal"),           # 256-row blocks, unsplit
+    ("few_split_merge", 1, 32, 4, 20000, 4, (4, 4), "causal"),  # streaming kernel, key splits + merge
+    ("row_groups", 1, 32, 4, 20000, 20, "affine", "causal"),    # row groups of the streaming kernel
+    ("bias", 2, 16, 2, 700, 40, (8, 4), "bias"),                # a device mask array: the tiled kernel's bias
+]
+
+
+@pytest.mark.parametrize("case", GRAPH_CASES, ids=lambda c: c[0])
+def test_prefill_in_hip_graph(gpu, case):
+    """Chunked prefill (every kernel path: tiled, few-query with key splits
+    and its merge, row groups, a mask array as a bias) captured in a HIP
+    graph and replayed several times, with eager work between the replays,
+    equals the eager call bit for bit every time (the launches record no
+    memset and allocate nothing at replay)."""
+    from rec_amd import MixedQuantizedKVCache
+
+    name, B, Hq, Hkv, P, L, fmt, mask = case
+    T = P + L
+    k = synthetic.kv((B, Hkv, T, 128), 41 + L, kind="outliers", frac=0.01)
+    v = synthetic.kv((B, Hkv, T, 128), 42 + L, kind="outliers", frac=0.01)
+    q = synthetic.query(B, Hq, L, 43 + L, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    cache = MixedQuantizedKVCache(max_tokens=T) if fmt == "affine" else QuantizedKVCache(32, *fmt, max_tokens=T)
+    kq, vq = cache.update_and_fetch(k, v)
+    group, bits = (64, (8, 4)) if fmt == "affine" else (32, fmt)
+    m = "causal"
+    if mask == "bias":
+        keep = torch.rand((B, 1, L, T), device="cuda") < 0.7
+        keep[..., 0] = True
+        m = keep
+    eager = quantized_attention_with_sinks(q, kq, vq, SCALE, m, sinks, group, *bits, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    out = torch.empty_like(eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out.copy_(quantized_attention_with_sinks(q, kq, vq, SCALE, m, sinks, group, *bits, out_dtype=torch.float32))
+    for rep in range(3):
+        out.fill_(float("nan"))
+        _ = quantized_attention_with_sinks(q[:, :, :1], kq, vq, SCALE, None, None, group, *bits)  # eager work between
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, rtol=0, atol=0, msg=f"{name}: replay {rep}")
