@@ -244,6 +244,33 @@ def dequantize_kv(keys: QuantizedKV, values: QuantizedKV):
     return k, v
 
 
+MAX_GROUP = 8  # query heads per KV head that one launch holds (the MFMA columns)
+
+
+def _head_groups(queries, sinks, mask, Hkv, call):
+    """A GQA ratio G above MAX_GROUP: the G query heads of every KV head in
+    groups of at most MAX_GROUP, one call each, outputs put back in head
+    order.  ``call(q, sinks, mask)`` attends for one group (its queries
+    ``(B, Hkv * g, L, D)``).  A mask broadcasts over the group's heads
+    (model.py:126-127 gives a four-dimensional one a group axis); a
+    three-dimensional one whose first extent is G is the per-head mask of the
+    group and is sliced with it."""
+    B, Hq, L, D = queries.shape
+    G = Hq // Hkv
+    qv = queries.reshape(B, Hkv, G, L, D)
+    sv = None if sinks is None else torch.as_tensor(sinks, device=queries.device).reshape(Hkv, G)
+    per_head = not isinstance(mask, str) and mask is not None and torch.as_tensor(mask).dim() == 3 \
+        and torch.as_tensor(mask).shape[0] == G
+    outs = []
+    for g0 in range(0, G, MAX_GROUP):
+        g1 = min(G, g0 + MAX_GROUP)
+        q = qv[:, :, g0:g1].reshape(B, Hkv * (g1 - g0), L, D)
+        sk = None if sv is None else sv[:, g0:g1].reshape(-1)
+        m = mask[g0:g1] if per_head else mask
+        outs.append(call(q, sk, m).reshape(B, Hkv, g1 - g0, L, D))
+    return torch.cat(outs, dim=2).reshape(B, Hq, L, D)
+
+
 def quantized_attention_with_sinks(
     queries, keys, values, scale, mask, sinks, group_size, key_bits, value_bits, *, out_dtype=None, splits=None,
     sink_dtype=None,
@@ -285,6 +312,10 @@ def quantized_attention_with_sinks(
     if L > keys.length:  # the L queries are the newest L cached tokens (model.py:122-125)
         raise ValueError(f"{L} queries but only {keys.length} cached tokens")
     Hkv = keys.n_kv_heads
+    if Hq // Hkv > MAX_GROUP:
+        return _head_groups(queries, sinks, mask, Hkv, lambda q, sk, m: quantized_attention_with_sinks(
+            q, keys, values, scale, m, sk, group_size, key_bits, value_bits, out_dtype=out_dtype, splits=splits,
+            sink_dtype=sink_dtype))
     T = int(keys.length)
     causal, win, bias = _resolve_mask(mask, B, Hkv, Hq // Hkv, L, T, queries.device)
     if L == 1 and win:
@@ -560,6 +591,9 @@ def scaled_dot_product_attention(queries, keys, values, scale, mask=None, sinks=
     Hkv = keys.shape[1]
     if Hq % Hkv:
         raise ValueError(f"{Hq} query heads is not a multiple of {Hkv} KV heads")
+    if Hq // Hkv > MAX_GROUP:
+        return _head_groups(queries, sinks, mask, Hkv, lambda q, sk, m: scaled_dot_product_attention(
+            q, keys, values, scale, m, sk, out_dtype=out_dtype, splits=splits, window=window, sink_dtype=sink_dtype))
     if window is not None:
         causal, win, bias = True, (0 if window >= T else int(window)), None
     else:
@@ -605,6 +639,8 @@ def attend(queries, keys, values, cache, scale, mask=None, sinks=None, *, out_dt
     B, Hq, L, D = queries.shape
     qdt = queries.dtype
     ring = isinstance(cache, FixedSlidingKVCache)
+    if keys.dim() == 4 and keys.shape[1] > 0 and Hq // keys.shape[1] > MAX_GROUP:
+        fused = False  # the query heads of a KV head take several launches (_head_groups)
     # one query's host-checked pattern over the cache after the append (None:
     # a device array, or another pattern: a bias); for one query "causal"
     # keeps every key (window 0)
