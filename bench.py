@@ -420,6 +420,51 @@ Q4_SHAPES = [
 ]
 
 
+def run_q4_gemm(steps, seed, M=2048):
+    """The int4 matrix for a prefill chunk's M tokens (rec_q4_gemm: the same
+    packed matrix as the GEMV, one GEMM), at the q projection and the dense
+    gate/up shapes; beside it PyTorch's bf16 matmul over an already
+    dequantized matrix of the same shape (the library's GEMM, a yardstick:
+    4x the weight bytes and no dequantization)."""
+    import torch
+
+    import rec_amd
+
+    res = {}
+    for N, K, name in ((4096, 2048, "q_proj"), (6144, 2048, "dense_gate_up")):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed + N)
+        w = torch.randint(-(2**31), 2**31 - 1, (N, K // 8), dtype=torch.int32, device="cuda", generator=g)
+        s = (torch.rand((N, K // 64), device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+        b = (torch.rand((N, K // 64), device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+        m = rec_amd.Q4Matrix(w, s, b)
+        x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+        out = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        dense = torch.randn((N, K), device="cuda", generator=g).to(torch.bfloat16)
+        times = {}
+        for what, fn in (("q4", lambda: out.copy_(rec_amd.q4_gemv(x, m))), ("bf16", lambda: torch.matmul(x, dense.T))):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for _ in range(steps):
+                    fn()
+            times[what] = _median_timed(torch, gr, steps)
+            del gr
+        fl = 2.0 * M * N * K
+        tf = fl / (times["q4"] * 1e-3) / 1e12
+        log(f"q4 gemm {name} {M}x{N}x{K}: {times['q4'] * 1e3:.1f} us, {tf:.0f} TFLOP/s "
+            f"(bf16 matmul over dense weights {times['bf16'] * 1e3:.1f} us)")
+        res[name] = dict(M=M, N=N, K=K, us=round(times["q4"] * 1e3, 2), tflops=round(tf, 1),
+                         frac_of_mfma_peak=round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                         library_yardstick=dict(us=round(times["bf16"] * 1e3, 2),
+                                                what="torch.matmul over a dense bf16 matrix of the same shape"))
+        del m, w, s, b, dense
+        torch.cuda.empty_cache()
+    return res
+
+
 def run_q4_gemv(steps, seed):
     """int4 group-64 GEMV (one bf16 vector) at the decoder's projection
     shapes; each launch reads a different copy of the packed matrix (about
@@ -960,6 +1005,7 @@ def main(argv=None):
     rq4 = None
     if not args.no_gemv:
         rq4 = run_q4_gemv(max(16, args.steps // 16), args.seed + 41)
+        rq4m = run_q4_gemm(10, args.seed + 43)
 
     rpf = rpf_short = rpf_short_u4 = rpf_few = rpf_few_affine = rpf_few_u4 = None
     rpf_fmt = {}
@@ -1164,6 +1210,11 @@ def main(argv=None):
             format="MLX affine 4-bit, group 64, bf16 scales and biases; one bf16 vector, bf16 out",
             shapes=rq4,
             kernel="rec::q4_gemv_kernel (bf16 MFMA 16x16x32)",
+        )
+        result["q4_gemm_prefill"] = dict(
+            format="the same packed matrix, 2,048 bf16 rows of x (a prefill chunk's projection), bf16 out",
+            shapes=rq4m,
+            kernel="rec::q4_xsum_kernel + rec::q4_gemm_kernel (bf16 MFMA 16x16x32)",
         )
     if rpf is not None:
         result["prefill_65536_plus_2048"] = rpf

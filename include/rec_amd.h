@@ -411,6 +411,20 @@ int rec_q4_pack(const uint32_t* w, const uint16_t* scales, const uint16_t* biase
 int rec_q4_gemv(const void* packed, int64_t N, int64_t K, const uint16_t* x, int64_t x_stride, int M,
                 void* out, int out_dtype, int64_t out_stride, void* stream);
 
+/*
+ * Many vectors (a prefill chunk's projections: the reference's
+ * mx.quantized_matmul over L tokens, model.py:151-154, or q4 per token):
+ * y[m] = x[m] · Wᵀ for M >= 1 bf16 vectors over the same packed matrix, as a
+ * GEMM on matrix cores with rec_q4_gemv's arithmetic (codes and products
+ * exact, sums in fp32).  x, x_stride, out, out_dtype and out_stride as
+ * rec_q4_gemv; the workspace (16-byte aligned, at least
+ * rec_q4_gemm_workspace_bytes(M, K)) receives x's group sums first.
+ */
+size_t rec_q4_gemm_workspace_bytes(int M, int64_t K);
+int rec_q4_gemm(const void* packed, int64_t N, int64_t K, const uint16_t* x, int64_t x_stride, int M,
+                void* out, int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,6 +112,8 @@ SIGNATURES["rec_prefill_bf16"] = (
 SIGNATURES["rec_q4_packed_bytes"] = (_sz, [_i64, _i64])
 SIGNATURES["rec_q4_pack"] = (_i, [_p, _p, _p, _i64, _i64, _p, _sz, _p])
 SIGNATURES["rec_q4_gemv"] = (_i, [_p, _i64, _i64, _p, _i64, _i, _p, _i, _i64, _p])
+SIGNATURES["rec_q4_gemm_workspace_bytes"] = (_sz, [_i, _i64])
+SIGNATURES["rec_q4_gemm"] = (_i, [_p, _i64, _i64, _p, _i64, _i, _p, _i, _i64, _p, _sz, _p])
 
 _lock = threading.Lock()
 _lib = None

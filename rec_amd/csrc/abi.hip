@@ -852,6 +852,46 @@ int rec_q4_gemv(const void* packed, int64_t N, int64_t K, const uint16_t* x, int
   return launched(launch_q4_gemv(a, (hipStream_t)stream), "q4 gemv launch");
 }
 
+size_t rec_q4_gemm_workspace_bytes(int M, int64_t K) {
+  if (M < 1 || K < 128 || K % 128 != 0) return 0;
+  return ((size_t)M * (size_t)(K / 64) * 4 + 15) & ~(size_t)15;
+}
+
+int rec_q4_gemm(const void* packed, int64_t N, int64_t K, const uint16_t* x, int64_t x_stride, int M, void* out,
+                int out_dtype, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  if (rec_q4_packed_bytes(N, K) == 0)
+    return fail(REC_EINVAL, "q4 matrix must have N >= 1 and K a positive multiple of 128 (N=%lld K=%lld)",
+                (long long)N, (long long)K);
+  if (M < 1 || M > (1 << 22)) return fail(REC_EINVAL, "q4 gemm: M=%d vectors, 1..%d supported", M, 1 << 22);
+  if (!packed || !x || !out || !workspace) return fail(REC_EINVAL, "q4 gemm: null pointer");
+  if (out_dtype != REC_BF16 && out_dtype != REC_F32) return fail(REC_EINVAL, "q4 gemm: out dtype must be bf16 or f32");
+  if (M > 1 && (x_stride < K || out_stride < N))
+    return fail(REC_EINVAL, "q4 gemm: row strides (%lld, %lld) shorter than rows (%lld, %lld)", (long long)x_stride,
+                (long long)out_stride, (long long)K, (long long)N);
+  if (!aligned16(packed) || !aligned16(x) || !aligned16(workspace) || (M > 1 && x_stride % 8 != 0))
+    return fail(REC_EALIGN, "q4 gemm: packed, x and workspace must be 16-byte aligned, x_stride a multiple of 8");
+  // a workgroup's 64 rows of x and the packed rows of one tile are addressed
+  // through 32-bit buffer offsets
+  if ((64 * (M > 1 ? x_stride : K) + K) * 2 >= ((int64_t)1 << 31) || (K / 128) * 1152 >= ((int64_t)1 << 31))
+    return fail(REC_EUNSUPPORTED, "q4 gemm: K=%lld, x_stride=%lld exceed the 2 GiB buffer range", (long long)K,
+                (long long)x_stride);
+  const size_t need = rec_q4_gemm_workspace_bytes(M, K);
+  if (workspace_bytes < need)
+    return fail(REC_EWORKSPACE, "q4 gemm: workspace of %zu bytes is too small (%zu needed)", workspace_bytes, need);
+  Q4GemmArgs a;
+  a.packed = (const uint8_t*)packed;
+  a.N = N;
+  a.K = K;
+  a.x = x;
+  a.x_stride = M > 1 ? x_stride : K;
+  a.M = M;
+  a.xsum = (float*)workspace;
+  a.out = out;
+  a.out_dtype = out_dtype == REC_F32 ? DT_F32 : DT_BF16;
+  a.out_stride = out_stride;
+  return launched(launch_q4_gemm(a, (hipStream_t)stream), "q4 gemm launch");
+}
+
 }  // extern "C"
 
 // ------------------------------------------------------------------------

@@ -271,4 +271,166 @@ hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream) {
   return launch_q4_gemv_wpt<4>(a, tiles, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Many vectors: the projections of a prefill chunk (M rows of x), over the
+// same packed records.  A GEMM on bf16 MFMA 16x16x32 with the GEMV's exact
+// arithmetic: codes enter as 128 + q, x as bf16, and each 64-element group's
+// sums D = Σ(128 + q)x take y += s·D + (b − 128 s)·X with X = Σx over the
+// group (q4_xsum_kernel, a pass of its own).  Here a k-step covers 32
+// consecutive elements of one group -- lane (r, kq) takes word 4t + kq of row
+// r, dword kq of record lane r + 16t -- so x enters in its own order and the
+// two groups of a span accumulate apart.
+
+// Group sums X[m][g] = Σ x[m][64g .. 64g+63] in fp32, one thread per (m, g).
+__global__ __launch_bounds__(256) void q4_xsum_kernel(const Q4GemmArgs a) {
+  const int64_t G = a.K / 64;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)a.M * G) return;
+  const int64_t m = i / G, g = i - m * G;
+  const v4i* p = (const v4i*)(a.x + m * a.x_stride + g * 64);  // 16-byte aligned rows, K % 128 == 0
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const v4i v = p[j];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t d = (uint32_t)v[e];
+      s += bf16_lo(d) + bf16_hi(d);
+    }
+  }
+  a.xsum[i] = s;
+}
+
+// Eight 4-bit codes of one word as eight bf16 values 128 + q, in element
+// order: even codes (bytes of w & 0x0f0f0f0f) and odd ones paired per byte.
+__device__ __forceinline__ v8bf unpack_codes(uint32_t w) {
+  const uint32_t u = w & 0x0f0f0f0fu, v = (w >> 4) & 0x0f0f0f0fu;
+  v4i o;
+  o[0] = (int)(__builtin_amdgcn_perm(v, u, 0x0c040c00u) | 0x43004300u);
+  o[1] = (int)(__builtin_amdgcn_perm(v, u, 0x0c050c01u) | 0x43004300u);
+  o[2] = (int)(__builtin_amdgcn_perm(v, u, 0x0c060c02u) | 0x43004300u);
+  o[3] = (int)(__builtin_amdgcn_perm(v, u, 0x0c070c03u) | 0x43004300u);
+  return __builtin_bit_cast(v8bf, o);
+}
+
+constexpr int GM_VECS = 64;  // vectors per workgroup: four 16-column tiles
+
+// Workgroup (x, y): four waves, wave w the row tile 4x + w (16 rows) against
+// vectors 64y .. 64y+63.  Lane (r, kq) of a D tile holds rows 4kq .. 4kq+3 of
+// vector column r, whose scales and biases are the record's 16-byte block kq
+// of each group.
+__global__ __launch_bounds__(256) void q4_gemm_kernel(const Q4GemmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t tiles = (a.N + 15) / 16;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile >= tiles) return;  // wave-uniform; the kernel has no barrier
+  const int S = (int)(a.K / GV_SPAN), G = (int)(a.K / 64);
+  const int r = lane & 15, kq = lane >> 4;
+  const int m0 = (int)blockIdx.y * GM_VECS;
+  const int rows = min(GM_VECS, a.M - m0);  // vectors of this workgroup (>= 1)
+  const __amdgpu_buffer_rsrc_t R = make_rsrc(a.packed + tile * S * GV_REC, (int64_t)S * GV_REC);
+  // x and its group sums: vectors past M lie past the resources' ends and read zero
+  const __amdgpu_buffer_rsrc_t RX =
+      make_rsrc(a.x + (int64_t)m0 * a.x_stride, ((int64_t)(rows - 1) * a.x_stride + a.K) * 2);
+  const __amdgpu_buffer_rsrc_t RS = make_rsrc(a.xsum + (int64_t)m0 * G, (int64_t)rows * G * 4);
+  const uint32_t wl = 16 * r + 4 * kq, sl = 1024 + 32 * kq;
+  uint32_t xrow[4], srow[4];
+#pragma unroll
+  for (int vt = 0; vt < 4; ++vt) {
+    xrow[vt] = (uint32_t)(((int64_t)(16 * vt + r) * a.x_stride + 8 * kq) * 2);
+    srow[vt] = (uint32_t)((16 * vt + r) * G * 4);
+  }
+
+  v4f y[4];
+#pragma unroll
+  for (int vt = 0; vt < 4; ++vt) y[vt] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < S; ++sp) {
+    const uint32_t rec = (uint32_t)sp * GV_REC;
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) w[t] = ld32<0>(R, wl + 256 * t, rec);
+    const v4i sb0 = ld128<0>(R, sl, rec), sb1 = ld128<0>(R, sl + 16, rec);
+    v4i xb[4][4];
+    v2i xs[4];
+#pragma unroll
+    for (int vt = 0; vt < 4; ++vt) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xb[vt][t] = ld128<0>(RX, xrow[vt] + (uint32_t)(256 * sp + 64 * t), 0);
+      xs[vt] = ld64<0>(RS, srow[vt] + (uint32_t)(8 * sp), 0);
+    }
+    v8bf av[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) av[t] = unpack_codes(w[t]);
+    // per group: scales s and the X coefficients b - 128 s of the lane's rows
+    float sc[2][4], cb[2][4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const v4i sb = g ? sb1 : sb0;
+      const uint32_t s01 = (uint32_t)sb[0], s23 = (uint32_t)sb[1], b01 = (uint32_t)sb[2], b23 = (uint32_t)sb[3];
+      const float s4[4] = {bf16_lo(s01), bf16_hi(s01), bf16_lo(s23), bf16_hi(s23)};
+      const float b4[4] = {bf16_lo(b01), bf16_hi(b01), bf16_lo(b23), bf16_hi(b23)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[g][i] = s4[i];
+        cb[g][i] = fmaf(-128.f, s4[i], b4[i]);
+      }
+    }
+#pragma unroll
+    for (int vt = 0; vt < 4; ++vt) {
+      const v4f z = {0.f, 0.f, 0.f, 0.f};
+      v4f d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], __builtin_bit_cast(v8bf, xb[vt][0]), z, 0, 0, 0);
+      d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], __builtin_bit_cast(v8bf, xb[vt][1]), d0, 0, 0, 0);
+      v4f d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2], __builtin_bit_cast(v8bf, xb[vt][2]), z, 0, 0, 0);
+      d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[3], __builtin_bit_cast(v8bf, xb[vt][3]), d1, 0, 0, 0);
+      const int x0 = xs[vt][0], x1 = xs[vt][1];  // copies: a bit_cast of a vector subscript reads element 0
+      const float X0 = __builtin_bit_cast(float, x0), X1 = __builtin_bit_cast(float, x1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float acc = y[vt][i];
+        acc = fmaf(cb[0][i], X0, fmaf(sc[0][i], d0[i], acc));
+        acc = fmaf(cb[1][i], X1, fmaf(sc[1][i], d1[i], acc));
+        y[vt][i] = acc;
+      }
+    }
+  }
+
+  const int64_t n0 = tile * 16 + 4 * kq;
+#pragma unroll
+  for (int vt = 0; vt < 4; ++vt) {
+    const int m = m0 + 16 * vt + r;
+    if (m >= a.M) continue;
+    if (a.out_dtype == DT_F32) {
+      float* o = (float*)a.out + (int64_t)m * a.out_stride + n0;
+      if (n0 + 3 < a.N) {
+        *(v4f*)o = y[vt];
+      } else {
+        for (int i = 0; i < 4; ++i)
+          if (n0 + i < a.N) o[i] = y[vt][i];
+      }
+    } else {
+      uint16_t* o = (uint16_t*)a.out + (int64_t)m * a.out_stride + n0;
+      const uint16_t h[4] = {f32_to_bf16(y[vt][0]), f32_to_bf16(y[vt][1]), f32_to_bf16(y[vt][2]),
+                             f32_to_bf16(y[vt][3])};
+      if (n0 + 3 < a.N) {
+        *(v2i*)o = (v2i){(int)(h[0] | ((uint32_t)h[1] << 16)), (int)(h[2] | ((uint32_t)h[3] << 16))};
+      } else {
+        for (int i = 0; i < 4; ++i)
+          if (n0 + i < a.N) o[i] = h[i];
+      }
+    }
+  }
+}
+
+hipError_t launch_q4_gemm(const Q4GemmArgs& a, hipStream_t stream) {
+  const int64_t sums = (int64_t)a.M * (a.K / 64);
+  hipLaunchKernelGGL(q4_xsum_kernel, dim3((unsigned)((sums + 255) / 256)), dim3(256), 0, stream, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t tiles = (a.N + 15) / 16;
+  hipLaunchKernelGGL(q4_gemm_kernel, dim3((unsigned)((tiles + 3) / 4), (unsigned)((a.M + GM_VECS - 1) / GM_VECS)),
+                     dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
 }  // namespace rec

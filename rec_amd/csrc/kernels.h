@@ -154,6 +154,20 @@ struct Q4GemvArgs {
   int64_t out_stride;
 };
 
+// Many vectors (a prefill chunk's projections): the same packed matrix as a
+// GEMM.  xsum: [M][K/64] fp32 group sums of x (workspace, written first).
+struct Q4GemmArgs {
+  const uint8_t* packed;
+  int64_t N, K;
+  const uint16_t* x;        // [M][x_stride] bf16
+  int64_t x_stride;
+  int M;
+  float* xsum;              // [M][K/64]
+  void* out;                // [M][out_stride] bf16 or fp32
+  int out_dtype;            // DT_BF16 or DT_F32
+  int64_t out_stride;
+};
+
 constexpr int DECODE_MAX_SPLITS = 256;
 constexpr int Q4_MAX_M = 8;
 
@@ -178,6 +192,7 @@ hipError_t launch_dequant(int kb, int vb, const DequantArgs& a, hipStream_t stre
 hipError_t launch_q4_pack(const Q4PackArgs& a, hipStream_t stream);
 hipError_t launch_q4_gemv(const Q4GemvArgs& a, hipStream_t stream);
 size_t q4_gemv_lds_bytes(int M, int64_t K);
+hipError_t launch_q4_gemm(const Q4GemmArgs& a, hipStream_t stream);
 hipError_t launch_ring_join_bf16(const AppendArgs& a, void* rk, void* rv, int64_t rk_sb, int64_t rk_sh,
                                  int64_t rv_sb, int64_t rv_sh, int64_t head, int64_t n, int64_t keep_from, bool place,
                                  void* ok, void* ov, hipStream_t stream);

@@ -92,7 +92,9 @@ class Q4Matrix:
 def q4_gemv(x: torch.Tensor, m: Q4Matrix, out_dtype=None) -> torch.Tensor:
     """``x @ Wᵀ`` for bf16 ``x`` of shape ``(..., K)``; returns ``(..., N)``
     in bfloat16 (rounded to nearest even, as the reference stores it) or in
-    ``out_dtype=torch.float32``."""
+    ``out_dtype=torch.float32``.  Up to 8 rows of x run the GEMV
+    (``rec_q4_gemv``), more (a prefill chunk's tokens) one GEMM on matrix
+    cores with the same arithmetic (``rec_q4_gemm``)."""
     if x.shape[-1] != m.K:
         raise ValueError(f"x has {x.shape[-1]} features, the matrix {m.K}")
     if x.dtype != torch.bfloat16:
@@ -109,6 +111,16 @@ def q4_gemv(x: torch.Tensor, m: Q4Matrix, out_dtype=None) -> torch.Tensor:
     lib = _lib.load()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     code = _lib.REC_F32 if out_dtype == torch.float32 else _lib.REC_BF16
+    if rows > MAX_VECTORS:
+        # a prefill chunk's rows: one GEMM over the packed matrix (x's group
+        # sums in a workspace first)
+        ws = torch.empty(lib.rec_q4_gemm_workspace_bytes(rows, m.K), dtype=torch.uint8, device=x.device)
+        rc = lib.rec_q4_gemm(
+            m.packed.data_ptr(), m.N, m.K, xs.data_ptr(), xs.stride(0), rows, out.data_ptr(), code, out.stride(0),
+            ws.data_ptr(), ws.numel(), stream,
+        )
+        _lib.check(rc, "rec_q4_gemm")
+        return out.reshape(*lead, m.N)
     for r0 in range(0, rows, MAX_VECTORS):
         M = min(MAX_VECTORS, rows - r0)
         xr, orow = xs[r0 : r0 + M], out[r0 : r0 + M]

@@ -160,3 +160,74 @@ def test_stacked_matrices_one_launch(gpu, parts, M):
         assert torch.equal(y16[i].view(torch.int16), ys[i].to(torch.bfloat16).view(torch.int16))
     with pytest.raises(ValueError):  # parts of different K
         Q4Matrix.stack([probs[0][1:], problem(1, 16, 1024, seed=3)[1:]])
+
+
+GEMM_CASES = [
+    # M, N, K: more than 8 vectors run rec_q4_gemm (x's group sums, then a GEMM in 64-vector tiles)
+    (9, 300, 512),
+    (64, 1000, 1024),      # one full 64-vector tile, a ragged last row tile
+    (130, 257, 384),       # three vector tiles, the last of 2
+    (200, 48, 2048),
+    (77, 4096, 128),       # one span
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: f"M{c[0]}_N{c[1]}_K{c[2]}")
+def test_q4_gemm_matches_oracle(gpu, case):
+    """Prefill-sized x (more than 8 rows): fp32 output within 1e-5·(|x|·|W|ᵀ)
+    of the float64 oracle, bf16 output the RNE of the fp32 one."""
+    M, N, K = case
+    x, w, s, b = problem(M, N, K, seed=7 * M + N + K)
+    m = Q4Matrix(w, s, b)
+    y32 = q4_gemv(x, m, out_dtype=torch.float32)
+    y16 = q4_gemv(x, m)
+    torch.cuda.synchronize()
+    ref, mag = oracle_rows(x, w, s, b)
+    check(y32, ref, mag, f"gemm {case}")
+    assert torch.equal(y16.view(torch.int16), y32.to(torch.bfloat16).view(torch.int16)), "bf16 output is not RNE(fp32)"
+
+
+def test_q4_gemm_c_abi_small_m_and_strides(gpu):
+    """rec_q4_gemm through the C ABI at M = 3 and M = 1 (a partial vector
+    tile), x rows with a stride longer than K, out rows with a stride longer
+    than N; equal to the GEMV within the bound; a short workspace refused."""
+    import ctypes
+
+    from rec_amd import _lib
+
+    lib = _lib.load()
+    N, K = 200, 1024
+    _, w, s, b = problem(1, N, K, seed=21)
+    m = Q4Matrix(w, s, b)
+    big = torch.randn((3, K + 64), device="cuda").to(torch.bfloat16)
+    x = big[:, :K]
+    for M in (3, 1):
+        out = torch.full((M, N + 8), float("nan"), device="cuda")
+        ws = torch.empty(lib.rec_q4_gemm_workspace_bytes(M, K), dtype=torch.uint8, device="cuda")
+        rc = lib.rec_q4_gemm(m.packed.data_ptr(), N, K, x.data_ptr(), K + 64, M, out.data_ptr(), _lib.REC_F32,
+                             N + 8, ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "rec_q4_gemm")
+        torch.cuda.synchronize()
+        ref, mag = oracle_rows(x[:M], w, s, b)
+        check(out[:, :N], ref, mag, f"c-abi M={M}")
+        assert bool(torch.isnan(out[:, N:]).all()), "wrote past N"
+        gv = q4_gemv(x[:M], m, out_dtype=torch.float32)
+        torch.testing.assert_close(out[:, :N], gv, rtol=1e-5, atol=1e-4)
+    rc = lib.rec_q4_gemm(m.packed.data_ptr(), N, K, x.data_ptr(), K + 64, 3, out.data_ptr(), _lib.REC_F32, N + 8,
+                         ws.data_ptr(), 4, torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.REC_EWORKSPACE
+
+
+def test_q4_gemm_prefill_projection_size(gpu):
+    """A 2,048-token chunk through the q projection (4096 x 2048): every
+    output against a float32 torch reference of the dequantized matrix."""
+    M, N, K = 2048, 4096, 2048
+    x, w, s, b = problem(M, N, K, seed=23)
+    y = q4_gemv(x, Q4Matrix(w, s, b), out_dtype=torch.float32)
+    shifts = torch.arange(0, 32, 4, device="cuda", dtype=torch.int32)
+    q = ((w.unsqueeze(-1) >> shifts) & 15).reshape(N, K).float()
+    deq = q * s.float().repeat_interleave(64, 1) + b.float().repeat_interleave(64, 1)
+    full = (x.float() @ deq.T).double()
+    mag = (x.float().abs() @ deq.abs().T).double()
+    err = (y.double() - full).abs()
+    assert bool((err <= 2e-5 * mag + 1e-5).all()), f"max err {err.max().item():.3e}"
