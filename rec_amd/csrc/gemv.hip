@@ -313,110 +313,164 @@ __device__ __forceinline__ v8bf unpack_codes(uint32_t w) {
   return __builtin_bit_cast(v8bf, o);
 }
 
-constexpr int GM_VECS = 64;  // vectors per workgroup: four 16-column tiles
+constexpr int GM_VECS = 64;    // vectors per workgroup: four 16-column tiles
+constexpr int GM_ROWS = 128;   // rows per workgroup: eight 16-row tiles, two per wave
+constexpr int GM_PITCH = 272;  // LDS bytes per staged vector row of a span (256 + 16: rows on distinct banks)
 
-// Workgroup (x, y): four waves, wave w the row tile 4x + w (16 rows) against
-// vectors 64y .. 64y+63.  Lane (r, kq) of a D tile holds rows 4kq .. 4kq+3 of
-// vector column r, whose scales and biases are the record's 16-byte block kq
-// of each group.
+// Workgroup (x, y): rows 128x .. 128x+127 against vectors 64y .. 64y+63; wave w
+// takes the row tiles 8x + 2w and 8x + 2w + 1.  Each span's x (64 vectors x
+// 128 elements, 16 KB) and its group sums are staged once in LDS, the next
+// span's fetched into registers while this one is computed (two buffers, one
+// barrier per span); every x operand read from LDS feeds both row tiles.
+// Lane (r, kq) of a D tile holds rows 4kq .. 4kq+3 of vector column r, whose
+// scales and biases are the record's 16-byte block kq of each group.
 __global__ __launch_bounds__(256) void q4_gemm_kernel(const Q4GemmArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  __shared__ __attribute__((aligned(16))) char xl[2][GM_VECS * GM_PITCH];
+  __shared__ __attribute__((aligned(16))) float xsl[2][GM_VECS * 2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t tiles = (a.N + 15) / 16;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
-  if (tile >= tiles) return;  // wave-uniform; the kernel has no barrier
   const int S = (int)(a.K / GV_SPAN), G = (int)(a.K / 64);
   const int r = lane & 15, kq = lane >> 4;
   const int m0 = (int)blockIdx.y * GM_VECS;
   const int rows = min(GM_VECS, a.M - m0);  // vectors of this workgroup (>= 1)
-  const __amdgpu_buffer_rsrc_t R = make_rsrc(a.packed + tile * S * GV_REC, (int64_t)S * GV_REC);
+  // the wave's two row tiles (tiles past the matrix read zeros, store nothing)
+  __amdgpu_buffer_rsrc_t R[2];
+  int64_t tile[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    tile[rt] = (int64_t)blockIdx.x * 8 + 2 * wave + rt;
+    const bool live = tile[rt] < tiles;
+    R[rt] = make_rsrc(a.packed + (live ? tile[rt] * S * GV_REC : 0), live ? (int64_t)S * GV_REC : 0);
+  }
   // x and its group sums: vectors past M lie past the resources' ends and read zero
   const __amdgpu_buffer_rsrc_t RX =
       make_rsrc(a.x + (int64_t)m0 * a.x_stride, ((int64_t)(rows - 1) * a.x_stride + a.K) * 2);
   const __amdgpu_buffer_rsrc_t RS = make_rsrc(a.xsum + (int64_t)m0 * G, (int64_t)rows * G * 4);
+  // staging: thread tid carries 16-byte pieces tid + 256 j (vector piece / 16,
+  // piece % 16 of its 256-byte span row); threads 0-63 also the vector's two sums
+  uint32_t xoff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int pc = tid + 256 * j;
+    xoff[j] = (uint32_t)(((int64_t)(pc >> 4) * a.x_stride + 8 * (pc & 15)) * 2);
+  }
+  const uint32_t soff = (uint32_t)(tid & 63) * (uint32_t)G * 4;
   const uint32_t wl = 16 * r + 4 * kq, sl = 1024 + 32 * kq;
-  uint32_t xrow[4], srow[4];
-#pragma unroll
-  for (int vt = 0; vt < 4; ++vt) {
-    xrow[vt] = (uint32_t)(((int64_t)(16 * vt + r) * a.x_stride + 8 * kq) * 2);
-    srow[vt] = (uint32_t)((16 * vt + r) * G * 4);
-  }
 
-  v4f y[4];
+  v4i xr[4];
+  v2i sr;
+  uint32_t wr[2][4];
+  v4i sbr[2][2];
+  const auto fetch = [&](int sp) {
 #pragma unroll
-  for (int vt = 0; vt < 4; ++vt) y[vt] = (v4f){0.f, 0.f, 0.f, 0.f};
-  for (int sp = 0; sp < S; ++sp) {
+    for (int j = 0; j < 4; ++j) xr[j] = ld128<0>(RX, xoff[j] + (uint32_t)(256 * sp), 0);
+    sr = ld64<0>(RS, soff + (uint32_t)(8 * sp), 0);
     const uint32_t rec = (uint32_t)sp * GV_REC;
-    uint32_t w[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) w[t] = ld32<0>(R, wl + 256 * t, rec);
-    const v4i sb0 = ld128<0>(R, sl, rec), sb1 = ld128<0>(R, sl + 16, rec);
-    v4i xb[4][4];
-    v2i xs[4];
+    for (int rt = 0; rt < 2; ++rt) {
 #pragma unroll
-    for (int vt = 0; vt < 4; ++vt) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) xb[vt][t] = ld128<0>(RX, xrow[vt] + (uint32_t)(256 * sp + 64 * t), 0);
-      xs[vt] = ld64<0>(RS, srow[vt] + (uint32_t)(8 * sp), 0);
+      for (int t = 0; t < 4; ++t) wr[rt][t] = ld32<0>(R[rt], wl + 256 * t, rec);
+      sbr[rt][0] = ld128<0>(R[rt], sl, rec);
+      sbr[rt][1] = ld128<0>(R[rt], sl + 16, rec);
     }
-    v8bf av[4];
+  };
+  const auto stage = [&](int buf) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) av[t] = unpack_codes(w[t]);
-    // per group: scales s and the X coefficients b - 128 s of the lane's rows
-    float sc[2][4], cb[2][4];
+    for (int j = 0; j < 4; ++j) {
+      const int pc = tid + 256 * j;
+      *(v4i*)(xl[buf] + (pc >> 4) * GM_PITCH + 16 * (pc & 15)) = xr[j];
+    }
+    if (tid < 64) *(v2i*)(xsl[buf] + 2 * tid) = sr;
+  };
+
+  v4f y[2][4];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const v4i sb = g ? sb1 : sb0;
-      const uint32_t s01 = (uint32_t)sb[0], s23 = (uint32_t)sb[1], b01 = (uint32_t)sb[2], b23 = (uint32_t)sb[3];
-      const float s4[4] = {bf16_lo(s01), bf16_hi(s01), bf16_lo(s23), bf16_hi(s23)};
-      const float b4[4] = {bf16_lo(b01), bf16_hi(b01), bf16_lo(b23), bf16_hi(b23)};
+  for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[g][i] = s4[i];
-        cb[g][i] = fmaf(-128.f, s4[i], b4[i]);
+    for (int vt = 0; vt < 4; ++vt) y[rt][vt] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int sp = 0; sp < S; ++sp) {
+    const int buf = sp & 1;
+    // this span's weights (fetched with the span's x) into operands and
+    // per-group coefficients, before the next span's loads reuse the registers
+    v8bf av[2][4];
+    float sc[2][2][4], cb[2][2][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) av[rt][t] = unpack_codes(wr[rt][t]);
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const v4i sb = sbr[rt][g];
+        const uint32_t s01 = (uint32_t)sb[0], s23 = (uint32_t)sb[1], b01 = (uint32_t)sb[2], b23 = (uint32_t)sb[3];
+        const float s4[4] = {bf16_lo(s01), bf16_hi(s01), bf16_lo(s23), bf16_hi(s23)};
+        const float b4[4] = {bf16_lo(b01), bf16_hi(b01), bf16_lo(b23), bf16_hi(b23)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[rt][g][i] = s4[i];
+          cb[rt][g][i] = fmaf(-128.f, s4[i], b4[i]);
+        }
       }
     }
+    if (sp + 1 < S) fetch(sp + 1);
 #pragma unroll
     for (int vt = 0; vt < 4; ++vt) {
-      const v4f z = {0.f, 0.f, 0.f, 0.f};
-      v4f d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[0], __builtin_bit_cast(v8bf, xb[vt][0]), z, 0, 0, 0);
-      d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[1], __builtin_bit_cast(v8bf, xb[vt][1]), d0, 0, 0, 0);
-      v4f d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[2], __builtin_bit_cast(v8bf, xb[vt][2]), z, 0, 0, 0);
-      d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[3], __builtin_bit_cast(v8bf, xb[vt][3]), d1, 0, 0, 0);
-      const int x0 = xs[vt][0], x1 = xs[vt][1];  // copies: a bit_cast of a vector subscript reads element 0
-      const float X0 = __builtin_bit_cast(float, x0), X1 = __builtin_bit_cast(float, x1);
+      const char* xp = xl[buf] + (16 * vt + r) * GM_PITCH + 16 * kq;
+      v8bf bx[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float acc = y[vt][i];
-        acc = fmaf(cb[0][i], X0, fmaf(sc[0][i], d0[i], acc));
-        acc = fmaf(cb[1][i], X1, fmaf(sc[1][i], d1[i], acc));
-        y[vt][i] = acc;
+      for (int t = 0; t < 4; ++t) bx[t] = *(const v8bf*)(xp + 64 * t);
+      const v2f xsum = *(const v2f*)(xsl[buf] + 2 * (16 * vt + r));
+      const float X0 = xsum.x, X1 = xsum.y;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const v4f z = {0.f, 0.f, 0.f, 0.f};
+        v4f d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rt][0], bx[0], z, 0, 0, 0);
+        d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rt][1], bx[1], d0, 0, 0, 0);
+        v4f d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rt][2], bx[2], z, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rt][3], bx[3], d1, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float acc = y[rt][vt][i];
+          acc = fmaf(cb[rt][0][i], X0, fmaf(sc[rt][0][i], d0[i], acc));
+          acc = fmaf(cb[rt][1][i], X1, fmaf(sc[rt][1][i], d1[i], acc));
+          y[rt][vt][i] = acc;
+        }
       }
     }
+    if (sp + 1 < S) stage(buf ^ 1);
+    __syncthreads();
   }
 
-  const int64_t n0 = tile * 16 + 4 * kq;
 #pragma unroll
-  for (int vt = 0; vt < 4; ++vt) {
-    const int m = m0 + 16 * vt + r;
-    if (m >= a.M) continue;
-    if (a.out_dtype == DT_F32) {
-      float* o = (float*)a.out + (int64_t)m * a.out_stride + n0;
-      if (n0 + 3 < a.N) {
-        *(v4f*)o = y[vt];
+  for (int rt = 0; rt < 2; ++rt) {
+    if (tile[rt] >= tiles) continue;
+    const int64_t n0 = tile[rt] * 16 + 4 * kq;
+#pragma unroll
+    for (int vt = 0; vt < 4; ++vt) {
+      const int m = m0 + 16 * vt + r;
+      if (m >= a.M) continue;
+      const v4f v = y[rt][vt];
+      if (a.out_dtype == DT_F32) {
+        float* o = (float*)a.out + (int64_t)m * a.out_stride + n0;
+        if (n0 + 3 < a.N) {
+          *(v4f*)o = v;
+        } else {
+          for (int i = 0; i < 4; ++i)
+            if (n0 + i < a.N) o[i] = v[i];
+        }
       } else {
-        for (int i = 0; i < 4; ++i)
-          if (n0 + i < a.N) o[i] = y[vt][i];
-      }
-    } else {
-      uint16_t* o = (uint16_t*)a.out + (int64_t)m * a.out_stride + n0;
-      const uint16_t h[4] = {f32_to_bf16(y[vt][0]), f32_to_bf16(y[vt][1]), f32_to_bf16(y[vt][2]),
-                             f32_to_bf16(y[vt][3])};
-      if (n0 + 3 < a.N) {
-        *(v2i*)o = (v2i){(int)(h[0] | ((uint32_t)h[1] << 16)), (int)(h[2] | ((uint32_t)h[3] << 16))};
-      } else {
-        for (int i = 0; i < 4; ++i)
-          if (n0 + i < a.N) o[i] = h[i];
+        uint16_t* o = (uint16_t*)a.out + (int64_t)m * a.out_stride + n0;
+        const uint16_t h[4] = {f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3])};
+        if (n0 + 3 < a.N) {
+          *(v2i*)o = (v2i){(int)(h[0] | ((uint32_t)h[1] << 16)), (int)(h[2] | ((uint32_t)h[3] << 16))};
+        } else {
+          for (int i = 0; i < 4; ++i)
+            if (n0 + i < a.N) o[i] = h[i];
+        }
       }
     }
   }
@@ -428,7 +482,7 @@ hipError_t launch_q4_gemm(const Q4GemmArgs& a, hipStream_t stream) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t tiles = (a.N + 15) / 16;
-  hipLaunchKernelGGL(q4_gemm_kernel, dim3((unsigned)((tiles + 3) / 4), (unsigned)((a.M + GM_VECS - 1) / GM_VECS)),
+  hipLaunchKernelGGL(q4_gemm_kernel, dim3((unsigned)((tiles + 7) / 8), (unsigned)((a.M + GM_VECS - 1) / GM_VECS)),
                      dim3(256), 0, stream, a);
   return hipGetLastError();
 }
