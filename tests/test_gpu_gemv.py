@@ -119,11 +119,13 @@ def test_strided_rows_and_many_vectors(gpu):
         q4_gemv(x.float(), m)
 
 
-def test_q4_gemv_in_hip_graph(gpu):
-    """Captured launches replayed several times, with eager work between the
-    replays, match the eager result every time."""
+@pytest.mark.parametrize("M", [2, 100], ids=["gemv", "gemm"])
+def test_q4_gemv_in_hip_graph(gpu, M):
+    """Captured launches (the GEMV, or the group sums and GEMM for more than 8
+    rows) replayed several times, with eager work between the replays, match
+    the eager result every time."""
     N, K = 2048, 4096
-    x, w, s, b = problem(2, N, K, seed=13)
+    x, w, s, b = problem(M, N, K, seed=13)
     m = Q4Matrix(w, s, b)
     eager = q4_gemv(x, m, out_dtype=torch.float32)
     torch.cuda.synchronize()
@@ -133,6 +135,7 @@ def test_q4_gemv_in_hip_graph(gpu):
         out.copy_(q4_gemv(x, m, out_dtype=torch.float32))
     for rep in range(3):
         out.fill_(float("nan"))
+        _ = q4_gemv(x[:1], m)  # eager work between the replays
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
