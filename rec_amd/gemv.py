@@ -19,7 +19,16 @@ import torch
 from . import _lib
 
 GROUP = 64
-MAX_VECTORS = 8  # rows of x per launch
+MAX_VECTORS = 8  # rows of x per GEMV launch
+
+
+def gemm_min_rows(K: int) -> int:
+    """Rows of x from which one ``rec_q4_gemm`` beats GEMV launches of 8 rows:
+    the GEMM takes ≈27.5 µs per 2,048 of K at any M up to a few hundred (it
+    waits on one 128-element span's loads per step), a GEMV launch ≈6-7 µs.
+    Measured crossings: between 32 (24.7 against 28.2 µs) and 48 rows (36.8
+    against 28.6 µs) at K = 2048, between 48 and 64 rows at K = 4096."""
+    return 24 + 8 * (K // 1024)
 
 
 def _words(w: torch.Tensor) -> torch.Tensor:
@@ -92,9 +101,10 @@ class Q4Matrix:
 def q4_gemv(x: torch.Tensor, m: Q4Matrix, out_dtype=None) -> torch.Tensor:
     """``x @ Wᵀ`` for bf16 ``x`` of shape ``(..., K)``; returns ``(..., N)``
     in bfloat16 (rounded to nearest even, as the reference stores it) or in
-    ``out_dtype=torch.float32``.  Up to 8 rows of x run the GEMV
-    (``rec_q4_gemv``), more (a prefill chunk's tokens) one GEMM on matrix
-    cores with the same arithmetic (``rec_q4_gemm``)."""
+    ``out_dtype=torch.float32``.  A few rows of x run the GEMV
+    (``rec_q4_gemv``, 8 per launch), from :func:`gemm_min_rows` on (a prefill
+    chunk's tokens) one GEMM on matrix cores with the same arithmetic
+    (``rec_q4_gemm``)."""
     if x.shape[-1] != m.K:
         raise ValueError(f"x has {x.shape[-1]} features, the matrix {m.K}")
     if x.dtype != torch.bfloat16:
@@ -111,9 +121,9 @@ def q4_gemv(x: torch.Tensor, m: Q4Matrix, out_dtype=None) -> torch.Tensor:
     lib = _lib.load()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     code = _lib.REC_F32 if out_dtype == torch.float32 else _lib.REC_BF16
-    if rows > MAX_VECTORS:
+    if rows >= gemm_min_rows(m.K):
         # a prefill chunk's rows: one GEMM over the packed matrix (x's group
-        # sums in a workspace first)
+        # sums in a workspace first); fewer rows take GEMV launches of 8
         ws = torch.empty(lib.rec_q4_gemm_workspace_bytes(rows, m.K), dtype=torch.uint8, device=x.device)
         rc = lib.rec_q4_gemm(
             m.packed.data_ptr(), m.N, m.K, xs.data_ptr(), xs.stride(0), rows, out.data_ptr(), code, out.stride(0),

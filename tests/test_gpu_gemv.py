@@ -60,6 +60,7 @@ CASES = [
     (2, 33, 384),
     (1, 24000, 256),   # 1500 row tiles: two waves per tile
     (2, 40000, 128),   # 2500 row tiles: one wave per tile
+    (39, 512, 2048),   # one row short of gemm_min_rows(2048): five GEMV launches
 ]
 
 
@@ -121,8 +122,8 @@ def test_strided_rows_and_many_vectors(gpu):
 
 @pytest.mark.parametrize("M", [2, 100], ids=["gemv", "gemm"])
 def test_q4_gemv_in_hip_graph(gpu, M):
-    """Captured launches (the GEMV, or the group sums and GEMM for more than 8
-    rows) replayed several times, with eager work between the replays, match
+    """Captured launches (the GEMV, or the group sums and GEMM for a prefill
+    chunk's rows) replayed several times, with eager work between the replays, match
     the eager result every time."""
     N, K = 2048, 4096
     x, w, s, b = problem(M, N, K, seed=13)
@@ -166,18 +167,19 @@ def test_stacked_matrices_one_launch(gpu, parts, M):
 
 
 GEMM_CASES = [
-    # M, N, K: more than 8 vectors run rec_q4_gemm (x's group sums, then a GEMM in 64-vector tiles)
-    (9, 300, 512),
+    # M, N, K: from gemm_min_rows(K) vectors on, rec_q4_gemm (x's group sums, then a GEMM in 64-vector tiles)
+    (28, 300, 512),
     (64, 1000, 1024),      # one full 64-vector tile, a ragged last row tile
     (130, 257, 384),       # three vector tiles, the last of 2
     (200, 48, 2048),
+    (40, 512, 2048),       # exactly gemm_min_rows(2048)
     (77, 4096, 128),       # one span
 ]
 
 
 @pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: f"M{c[0]}_N{c[1]}_K{c[2]}")
 def test_q4_gemm_matches_oracle(gpu, case):
-    """Prefill-sized x (more than 8 rows): fp32 output within 1e-5·(|x|·|W|ᵀ)
+    """Prefill-sized x (from gemm_min_rows(K) rows on): fp32 output within 1e-5·(|x|·|W|ᵀ)
     of the float64 oracle, bf16 output the RNE of the fp32 one."""
     M, N, K = case
     x, w, s, b = problem(M, N, K, seed=7 * M + N + K)
