@@ -268,6 +268,44 @@ def test_sliding_window_ring_decode(gpu):
     assert m.shape == (3, W + 3) and bool(m[0, 0]) is False and bool(m[2, -1]) is True
 
 
+@pytest.mark.parametrize("P", [1000, 1276], ids=["slot487_wraps", "slot250_middle"])
+@pytest.mark.parametrize("splits", [None, 1, 8], ids=["auto", "s1", "s8"])
+def test_ring_decode_513_fused_vs_unfused(gpu, P, splits):
+    """The 513-token window layer (B = 2, 32 query / 4 KV heads): fused steps
+    (the new token written into its slot by the split that reads it) against
+    a twin ring stepped unfused (update_and_fetch, then attention).  Each
+    step's output matches the oracle over the last 513 tokens, and the two
+    rings' slots are bit-equal after every step.  After 1,000 tokens the
+    write slot starts at 487 and wraps past 512 within the steps; after
+    1,276 it starts at 250, inside a middle split."""
+    from rec_amd import FixedSlidingKVCache
+
+    B, Hq, Hkv, W, steps = 2, 32, 4, 513, 30
+    n = P + steps
+    k = synthetic.kv((B, Hkv, n, 128), 201 + P, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    v = synthetic.kv((B, Hkv, n, 128), 202 + P, kind="outliers", frac=0.01, dtype=torch.bfloat16)
+    sinks = torch.randn(Hq, device="cuda")
+    fused = FixedSlidingKVCache(max_sequence_tokens=4096, num_kv_heads=Hkv, head_dim=128, window_size=W, batch=B)
+    twin = FixedSlidingKVCache(max_sequence_tokens=4096, num_kv_heads=Hkv, head_dim=128, window_size=W, batch=B)
+    assert fused.capacity == W
+    fused.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    twin.update_and_fetch(k[:, :, :P], v[:, :, :P])
+    for step in range(steps):
+        pos = P + step
+        q = synthetic.query(B, Hq, 1, 300 + step, dtype=torch.bfloat16)
+        a = attend(q, k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], fused, SCALE, None, sinks,
+                   out_dtype=torch.float32, splits=splits)
+        b = attend(q, k[:, :, pos:pos + 1], v[:, :, pos:pos + 1], twin, SCALE, None, sinks,
+                   out_dtype=torch.float32, splits=splits, fused=False)
+        torch.cuda.synchronize()
+        assert fused.offset == twin.offset == pos + 1
+        assert torch.equal(fused.keys, twin.keys) and torch.equal(fused.values, twin.values), f"ring slots, step {step}"
+        ref = O.attention(f32(q), bf16_np(k[:, :, pos + 1 - W:pos + 1]), bf16_np(v[:, :, pos + 1 - W:pos + 1]), SCALE,
+                          sinks=q_sinks(sinks, q.dtype))
+        assert_close(f32(a), ref, f"fused step {step} (slot {pos % W})")
+        assert_close(f32(b), ref, f"unfused step {step}")
+
+
 # ---------------------------------------------------------------------------
 # prefill over the bf16 cache (L > 1 queries, the newest L of the T cached tokens)
 
