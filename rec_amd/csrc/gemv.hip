@@ -301,15 +301,15 @@ __global__ __launch_bounds__(256) void q4_xsum_kernel(const Q4GemmArgs a) {
   a.xsum[i] = s;
 }
 
-// Eight 4-bit codes of one word as eight bf16 values 128 + q, in element
-// order: even codes (bytes of w & 0x0f0f0f0f) and odd ones paired per byte.
+// Eight 4-bit codes of one word as eight bf16 values 128 + q, one and-or
+// per pair: codes d and d + 4 (element order 0, 4, 1, 5, 2, 6, 3, 7, the
+// order x is staged in, as the GEMV's).
 __device__ __forceinline__ v8bf unpack_codes(uint32_t w) {
-  const uint32_t u = w & 0x0f0f0f0fu, v = (w >> 4) & 0x0f0f0f0fu;
   v4i o;
-  o[0] = (int)(__builtin_amdgcn_perm(v, u, 0x0c040c00u) | 0x43004300u);
-  o[1] = (int)(__builtin_amdgcn_perm(v, u, 0x0c050c01u) | 0x43004300u);
-  o[2] = (int)(__builtin_amdgcn_perm(v, u, 0x0c060c02u) | 0x43004300u);
-  o[3] = (int)(__builtin_amdgcn_perm(v, u, 0x0c070c03u) | 0x43004300u);
+  o[0] = (int)and_or(w, 0x000f000fu, 0x43004300u);
+  o[1] = (int)and_or(w >> 4, 0x000f000fu, 0x43004300u);
+  o[2] = (int)and_or(w >> 8, 0x000f000fu, 0x43004300u);
+  o[3] = (int)and_or(w >> 12, 0x000f000fu, 0x43004300u);
   return __builtin_bit_cast(v8bf, o);
 }
 
@@ -378,8 +378,15 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(const Q4GemmArgs a) {
   const auto stage = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      // each 8-element piece in the unpack's element order 0, 4, 1, 5, 2, 6, 3, 7
       const int pc = tid + 256 * j;
-      *(v4i*)(xl[buf] + (pc >> 4) * GM_PITCH + 16 * (pc & 15)) = xr[j];
+      const uint32_t d0 = xr[j][0], d1 = xr[j][1], d2 = xr[j][2], d3 = xr[j][3];
+      v4i o;
+      o[0] = (int)__builtin_amdgcn_perm(d2, d0, 0x05040100u);
+      o[1] = (int)__builtin_amdgcn_perm(d2, d0, 0x07060302u);
+      o[2] = (int)__builtin_amdgcn_perm(d3, d1, 0x05040100u);
+      o[3] = (int)__builtin_amdgcn_perm(d3, d1, 0x07060302u);
+      *(v4i*)(xl[buf] + (pc >> 4) * GM_PITCH + 16 * (pc & 15)) = o;
     }
     if (tid < 64) *(v2i*)(xsl[buf] + 2 * tid) = sr;
   };
