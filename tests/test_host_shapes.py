@@ -197,3 +197,39 @@ def test_storage_metadata_rows_follow_the_reference():
     assert out[49] == rows[49] and rows[0][61] == 0  # row 50 untouched, the input not modified
     with pytest.raises(ValueError):
         _metadata_rows([[0] * 10])
+
+
+def test_q4_routing_follows_the_measured_crossing(monkeypatch):
+    """q4_gemv runs GEMV launches of 8 rows below gemm_min_rows(K) rows of x
+    and one GEMM from there (the crossing measured on MI355X: between 32 and
+    48 rows at K = 2048, between 48 and 64 at K = 4096).  The library is
+    replaced by a recorder: no kernel runs."""
+    from rec_amd import _lib, gemv
+
+    assert [gemv.gemm_min_rows(K) for K in (512, 1024, 2048, 4096, 6144)] == [24, 32, 40, 56, 72]
+    calls = []
+
+    class Recorder:
+        def rec_q4_gemm_workspace_bytes(self, M, K):
+            return 16
+
+        def rec_q4_gemm(self, *args):
+            calls.append(("gemm", args[5]))
+            return 0
+
+        def rec_q4_gemv(self, *args):
+            calls.append(("gemv", args[5]))
+            return 0
+
+    class Stream:
+        cuda_stream = 0
+
+    monkeypatch.setattr(_lib, "load", lambda: Recorder())
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: Stream())
+    m = object.__new__(gemv.Q4Matrix)
+    m.N, m.K, m.parts = 8, 2048, (8,)
+    m.packed = torch.zeros(16, dtype=torch.uint8)
+    for rows, want in ((1, [("gemv", 1)]), (39, [("gemv", 8)] * 4 + [("gemv", 7)]), (40, [("gemm", 40)])):
+        calls.clear()
+        y = gemv.q4_gemv(torch.zeros(rows, 2048, dtype=torch.bfloat16), m)
+        assert y.shape == (rows, 8) and calls == want, (rows, calls)
